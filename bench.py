@@ -1,0 +1,360 @@
+"""Benchmark of the MI355X tensor hot path (liboxide_hip.so) -- one JSON line on stdout.
+
+Headline workload: BatchNorm2d training forward + backward, fp32
+NCHW [64, 128, 56, 56].  One step = statistics with running update, apply, affine backward
+(sum g, sum g*x_hat once) and input backward, launched through the C ABI on one stream.
+Algorithmic bytes per step: forward 3T + backward 5T, T = 102 760 448 B (x read by the
+statistics; x read + y written by apply; g, x read by the affine reduction; g, x read + dx
+written by the input backward).  ``value`` = 8T / step time in GB/s, inputs resident in HBM.
+
+MALL (256 MB last-level cache) is defeated for the headline: steps rotate over 4 independent
+input/output sets (1.6 GB), so each step's x and g were last touched three steps (1.2 GB of
+traffic) earlier.  Kernel durations come from HIP events recorded between the launches on the
+launch stream inside the timed region.
+
+The other configs (elementwise chain + JIT-plan replay, cross entropy, AdamW) are measured
+after the headline and reported under "extra" in the same line.  ``cpu_baseline`` times the
+oracle (a single-threaded C restatement of the reference CPU path) on one BN step.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+for p in (REPO / "oxide-beta_amd", REPO / "oracle"):
+    if str(p) not in sys.path:
+        sys.path.insert(0, str(p))
+
+PEAK_HBM_GBS = 8000.0
+T_BN = 64 * 128 * 56 * 56 * 4
+
+
+def _events(n):
+    import torch
+
+    return [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+
+
+def _read_traffic(kernel: str):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if one exists."""
+    path = REPO / "profiles" / "traffic.json"
+    if not path.exists():
+        return None
+    try:
+        data = json.loads(path.read_text())
+        return data.get(kernel, {}).get("hbm_bytes_per_launch")
+    except (ValueError, OSError):
+        return None
+
+
+def bench_batch_norm(m, steps: int, warmup: int, sets: int = 4):
+    import numpy as np
+    import torch
+
+    dev = torch.device("cuda:0")
+    n, c, h, w = 64, 128, 56, 56
+    r = np.random.default_rng(0x6F78696400000002)
+    gamma = torch.from_numpy(r.uniform(0.5, 1.5, c).astype(np.float32)).to(dev)
+    beta = torch.from_numpy(r.uniform(-0.1, 0.1, c).astype(np.float32)).to(dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0x6F78696400000002)
+    xs = [torch.randn((n, c, h, w), generator=gen, device=dev) for _ in range(sets)]
+    gs = [torch.randn((n, c, h, w), generator=gen, device=dev) for _ in range(sets)]
+    ys = [torch.empty_like(xs[0]) for _ in range(sets)]
+    dxs = [torch.empty_like(xs[0]) for _ in range(sets)]
+    rm, rv = torch.zeros(c, device=dev), torch.ones(c, device=dev)
+    mean, inv = torch.empty(c, device=dev), torch.empty(c, device=dev)
+    dw, db = torch.empty(c, device=dev), torch.empty(c, device=dev)
+    s = torch.cuda.Stream()
+    torch.cuda.synchronize()
+
+    names = ["bn_statistics_running", "bn_apply", "bn_affine_backward", "bn_input_backward"]
+    bytes_per = {"bn_statistics_running": T_BN, "bn_apply": 2 * T_BN,
+                 "bn_affine_backward": 2 * T_BN, "bn_input_backward": 3 * T_BN}
+
+    def step(i, ev=None):
+        k = i % sets
+        x, g, y, dx = xs[k], gs[k], ys[k], dxs[k]
+        if ev:
+            ev[0].record(s)
+        m.batch_norm_statistics_running(x, rm, rv, mean, inv, 0.1, 1e-5, stream=s)
+        if ev:
+            ev[1].record(s)
+        m.batch_norm_apply(c, h * w, x, gamma, beta, mean, inv, y, stream=s)
+        if ev:
+            ev[2].record(s)
+        m.batch_norm_affine_backward(n, c, h * w, g, x, mean, inv, dw, db, stream=s)
+        if ev:
+            ev[3].record(s)
+        m.batch_norm_input_backward(c, h * w, n * h * w, True, g, x, gamma, mean, inv, dw, db,
+                                    dx, stream=s)
+        if ev:
+            ev[4].record(s)
+
+    for i in range(warmup):
+        step(i)
+    s.synchronize()
+    evs = [_events(5) for _ in range(steps)]
+    start, stop = _events(2)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record(s)
+    for i in range(steps):
+        step(warmup + i, evs[i])
+    stop.record(s)
+    s.synchronize()
+    wall = time.perf_counter() - t0
+    total_ms = start.elapsed_time(stop)
+    per_kernel = {nm: [] for nm in names}
+    for ev in evs:
+        for j, nm in enumerate(names):
+            per_kernel[nm].append(ev[j].elapsed_time(ev[j + 1]))
+    kernels = {}
+    for nm in names:
+        avg_ms = sum(per_kernel[nm]) / len(per_kernel[nm])
+        kernels[nm] = {"avg_us": round(avg_ms * 1e3, 2),
+                       "alg_bytes": bytes_per[nm],
+                       "gbs": round(bytes_per[nm] / (avg_ms * 1e-3) / 1e9, 1)}
+    ms_per_step = total_ms / steps
+    # hot-cache reference: the same step repeated on one input set (x, g fit in the MALL)
+    hot_start, hot_stop = _events(2)
+    hot_start.record(s)
+    for i in range(steps):
+        step(0)
+    hot_stop.record(s)
+    s.synchronize()
+    hot_ms = hot_start.elapsed_time(hot_stop) / steps
+    host_inputs = None
+    return dict(ms_per_step=ms_per_step, wall_ms_per_step=wall * 1e3 / steps, kernels=kernels,
+                hot_ms_per_step=hot_ms, host_inputs=host_inputs, sets=sets)
+
+
+def bench_elementwise(m, reps: int = 20):
+    import numpy as np
+    import torch
+
+    import oxide_hip as ox
+
+    dev = torch.device("cuda:0")
+    n = 4096 * 4096
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0x6F78696400000001)
+    sets = 2
+    abc = [[torch.rand(n, generator=gen, device=dev) * 2 - 1 for _ in range(3)]
+           for _ in range(sets)]
+    y = [torch.empty(n, device=dev) for _ in range(sets)]
+    d = [[torch.empty(n, device=dev) for _ in range(3)] for _ in range(sets)]
+    s = torch.cuda.Stream()
+    torch.cuda.synchronize()
+
+    def timed(fn):
+        for i in range(3):
+            fn(i)
+        e0, e1 = _events(2)
+        e0.record(s)
+        for i in range(reps):
+            fn(i)
+        e1.record(s)
+        s.synchronize()
+        return e0.elapsed_time(e1) / reps * 1e3  # us
+
+    fwd = timed(lambda i: m.elementwise_chain_forward(*abc[i % sets], y[i % sets], stream=s))
+    bwd = timed(lambda i: m.elementwise_chain_backward(*abc[i % sets], None, *d[i % sets],
+                                                       stream=s))
+    # the reference's JIT plan: add -> mul -> relu, three workspaces, captured into a graph
+    module = ox.compile(lambda a, b, c: ((a + b) * c).relu())
+    rr = np.random.default_rng(0x6F78696400000001)
+    host = [rr.uniform(-1, 1, (4096, 4096)).astype(np.float32) for _ in range(3)]
+    module.run(*host)
+    plan = module.plan_for(((4096, 4096),) * 3)
+    pstream = plan.stream()
+    for _ in range(3):
+        plan.replay()
+    ox.check(ox.lib().oxh_stream_synchronize(pstream))
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        plan.replay()
+    ox.check(ox.lib().oxh_stream_synchronize(pstream))
+    replay_us = (time.perf_counter() - t0) / reps * 1e6
+    t0 = time.perf_counter()
+    for _ in range(3):
+        module.run(*host)
+    run_us = (time.perf_counter() - t0) / 3 * 1e6
+    plan.close()
+    return {
+        "config": "relu((a+b)*c) fp32 3x[4096,4096]",
+        "fused_fwd_us": round(fwd, 2), "fused_fwd_gbs": round(4 * n * 4 / fwd / 1e3, 1),
+        "fused_bwd_us": round(bwd, 2), "fused_bwd_gbs": round(6 * n * 4 / bwd / 1e3, 1),
+        "plan_replay_us": round(replay_us, 2),
+        "plan_replay_gbs": round(8 * n * 4 / replay_us / 1e3, 1),
+        "plan_run_with_copies_us": round(run_us, 1),
+    }
+
+
+def bench_cross_entropy(m, reps: int = 10):
+    import torch
+
+    dev = torch.device("cuda:0")
+    b, k = 8192, 32768
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0x6F78696400000003)
+    logits = torch.randn((b, k), generator=gen, device=dev) * 2.0
+    targets = torch.randint(0, k, (b,), generator=gen, device=dev).float()
+    grad = torch.empty_like(logits)
+    loss = torch.empty(1, device=dev)
+    outer = torch.ones(1, device=dev)
+    s = torch.cuda.Stream()
+    torch.cuda.synchronize()
+
+    def timed(fn):
+        for _ in range(2):
+            fn()
+        e0, e1 = _events(2)
+        e0.record(s)
+        for _ in range(reps):
+            fn()
+        e1.record(s)
+        s.synchronize()
+        return e0.elapsed_time(e1) / reps * 1e3
+
+    fused = timed(lambda: m.cross_entropy_forward_backward(b, k, logits, targets, outer, loss,
+                                                           grad, stream=s))
+    fwd = timed(lambda: m.cross_entropy_forward(b, k, logits, targets, loss, stream=s))
+    L = b * k * 4
+    return {"config": "CE fp32 [8192,32768]", "fused_fwd_bwd_us": round(fused, 1),
+            "fused_fwd_bwd_gbs": round(2 * L / fused / 1e3, 1), "fwd_us": round(fwd, 1),
+            "fwd_gbs": round(L / fwd / 1e3, 1)}
+
+
+def bench_adamw(m, reps: int = 10):
+    import torch
+
+    import oxide_hip as ox
+
+    dev = torch.device("cuda:0")
+    n = 64 << 20
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0x6F78696400000004)
+    p = torch.randn(n, generator=gen, device=dev) * 0.02
+    g = torch.randn(n, generator=gen, device=dev) * 1e-3
+    gp = torch.randn(n, generator=gen, device=dev) * 1e-3
+    mom = gp * 0.1
+    vel = gp * gp * 0.001
+    c1, c2 = ox.adamw_corrections(0.9, 0.999, 10)
+    s = torch.cuda.Stream()
+    torch.cuda.synchronize()
+
+    def fn():
+        m.adamw(1e-3, 0.01, 0.9, 0.999, c1, c2, 1e-8, p, g, mom, vel, p, mom, vel, stream=s)
+
+    for _ in range(2):
+        fn()
+    e0, e1 = _events(2)
+    e0.record(s)
+    for _ in range(reps):
+        fn()
+    e1.record(s)
+    s.synchronize()
+    us = e0.elapsed_time(e1) / reps * 1e3
+    return {"config": "AdamW fp32 64Mi elements t=10", "us": round(us, 1),
+            "gbs": round(7 * n * 4 / us / 1e3, 1),
+            "frac_of_peak": round(7 * n * 4 / us / 1e3 / PEAK_HBM_GBS, 3)}
+
+
+def cpu_baseline(budget_s: float = 12.0):
+    """The oracle (single-threaded C restatement of the reference CPU path) on one full BN
+    step at config 2: forward (statistics, running update, apply) + backward."""
+    import numpy as np
+
+    import oracle
+
+    r = np.random.default_rng(0x6F78696400000002)
+    shape = (64, 128, 56, 56)
+    x = r.standard_normal(shape, dtype=np.float32)
+    g = r.standard_normal(shape, dtype=np.float32)
+    gamma = r.uniform(0.5, 1.5, 128).astype(np.float32)
+    beta = r.uniform(-0.1, 0.1, 128).astype(np.float32)
+    rm, rv = np.zeros(128, np.float32), np.ones(128, np.float32)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 2 or (time.perf_counter() < t_end and len(times) < 20):
+        t0 = time.perf_counter()
+        y, mean, inv, rm, rv = oracle.bn_forward(x, gamma, beta, rm, rv)
+        oracle.bn_backward(g, x, gamma, mean, inv, True)
+        times.append(time.perf_counter() - t0)
+    best = sorted(times)[len(times) // 2]
+    return {"value": round(8 * T_BN / best / 1e9, 2), "unit": "GB/s", "cores": 1,
+            "kind": "port",
+            "sample": f"{len(times)} full config-2 BN fwd+bwd steps (median {best * 1e3:.0f} ms "
+                      f"per step) of oracle/oxide_oracle.c, single thread"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-extra", action="store_true", help="headline BN config only")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only (the hot path has no multi-GPU "
+              "component); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import oxide_hip as ox
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    m = ox.load_kernels(0)
+    bn = bench_batch_norm(m, args.steps, args.warmup)
+    dominant = max(bn["kernels"], key=lambda k: bn["kernels"][k]["avg_us"])
+    dk = bn["kernels"][dominant]
+    achieved = dk["alg_bytes"] / (dk["avg_us"] * 1e-6) / 1e9
+    value = 8 * T_BN / (bn["ms_per_step"] * 1e-3) / 1e9
+    extra = {"bn_kernels": bn["kernels"],
+             "bn_hot_cache_gbs": round(8 * T_BN / (bn["hot_ms_per_step"] * 1e-3) / 1e9, 1),
+             "bn_frac_of_peak": round(value / PEAK_HBM_GBS, 3),
+             "bn_wall_ms_per_step": round(bn["wall_ms_per_step"], 4)}
+    if not args.no_extra:
+        extra["elementwise"] = bench_elementwise(m)
+        extra["cross_entropy"] = bench_cross_entropy(m)
+        extra["adamw"] = bench_adamw(m)
+    out = {
+        "metric": "BatchNorm2d train fwd+bwd achieved HBM bandwidth (algorithmic bytes)",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(bn["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (x, g ~ N(0,1) seeded; gamma ~ U(0.5,1.5), beta ~ U(-0.1,0.1))",
+        "config": {"workload": "BatchNorm2d train fwd+bwd NCHW [64,128,56,56] fp32, momentum "
+                               "0.1, eps 1e-5, 4 rotating input sets (MALL-flushed)",
+                   "algorithmic_bytes_per_step": 8 * T_BN},
+        "roofline": {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1),
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_HBM_GBS, 3),
+                     "traffic": _read_traffic(dominant)},
+        "cpu_baseline": None if args.no_cpu else cpu_baseline(),
+        "extra": extra,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

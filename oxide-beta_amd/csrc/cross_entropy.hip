@@ -1,0 +1,291 @@
+// cross_entropy.hip -- row log-softmax cross entropy: mean NLL loss and/or the gradient with
+// respect to the logits, from one read of each row.
+//
+// Reference kernels: cross_entropy_forward (kernel_module.rs:966-1009) runs the whole batch in
+// one thread; cross_entropy_backward (1011-1050) re-scans the full row (max and sum of exp) for
+// every logit, O(B * C^2).  CPU semantics: evaluation.rs:599-636, autograd.rs:529-554.
+//
+// Design (gfx950): one workgroup per row.  On the register path (classes % 4 == 0, aligned,
+// classes <= 65536) the row is loaded once with 128-bit loads into VGPRs (up to 16 float4 per
+// lane at 1024 lanes), the max and the sum of exp(x - max) are block reductions (wave64
+// shuffles, then LDS across waves), and the gradient is written from the same registers, so a
+// fused loss+gradient moves exactly one read and one write of the logits.  The per-row losses
+// go to an fp64 workspace vector; the last workgroup to finish (device-scope counter) sums them
+// in row order and writes the mean.  Other shapes take a three-pass strided path (max, sum,
+// gradient) whose re-reads of a row hit L2.
+//
+// Per element the fp32 operations follow the CPU path: e = exp(x - max);
+// p = e / normalizer; grad = (outer / batch) * (p - onehot); row loss = (ln(normalizer) + max)
+// - x[target].  expf / logf are ROCm's device math library (a few ulp from glibc's).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <string>
+
+#include "common.h"
+
+namespace {
+
+struct CeArgs {
+  const float *logits, *targets, *outer;  // outer: device scalar (may be null when no grad)
+  float *loss;                            // may be null (no loss)
+  float *grad;                            // may be null (no gradient)
+  uint32_t *error_flag;                   // may be null
+  double *row_loss;                       // workspace [batch]
+  uint32_t *counter;                      // workspace, 1 counter
+  uint64_t batch, classes;
+};
+
+// evaluation.rs:622-636: finite, non-negative, integral and below `classes`.
+__device__ __forceinline__ bool target_index(float t, uint64_t classes, uint64_t &index) {
+  if (!isfinite(t) || t < 0.0f || t - truncf(t) != 0.0f) return false;
+  if (t >= 18446744073709551616.0f) return false;
+  const uint64_t i = static_cast<uint64_t>(t);
+  if (i >= classes) return false;
+  index = i;
+  return true;
+}
+
+template <int BLOCK>
+__device__ __forceinline__ float block_max(float v, float *lds) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  constexpr int W = BLOCK / 64;
+  const int wave = threadIdx.x / 64;
+  if (threadIdx.x % 64 == 0) lds[wave] = v;
+  __syncthreads();
+  float r = lds[0];
+#pragma unroll
+  for (int w = 1; w < W; ++w) r = fmaxf(r, lds[w]);
+  __syncthreads();
+  return r;
+}
+
+template <int BLOCK>
+__device__ __forceinline__ double block_sum(double v, double *lds) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  constexpr int W = BLOCK / 64;
+  const int wave = threadIdx.x / 64;
+  if (threadIdx.x % 64 == 0) lds[wave] = v;
+  __syncthreads();
+  double r = 0.0;
+#pragma unroll
+  for (int w = 0; w < W; ++w) r += lds[w];
+  __syncthreads();
+  return r;
+}
+
+// Row finished: record its loss, and let the last row's block write the batch mean.
+template <int BLOCK>
+__device__ __forceinline__ void finish_row(const CeArgs &a, uint64_t row, float row_loss,
+                                           double *lds) {
+  if (a.loss == nullptr) return;
+  __shared__ bool is_last;
+  if (threadIdx.x == 0) {
+    a.row_loss[row] = static_cast<double>(row_loss);
+    __threadfence();
+    const uint32_t prev =
+        __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    is_last = prev + 1 == static_cast<uint32_t>(a.batch);
+    if (is_last) {
+      __threadfence();
+      __hip_atomic_store(a.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  __syncthreads();
+  if (!is_last) return;
+  // Fixed-order sum: thread t adds rows t, t + BLOCK, ...; then a fixed-shape tree.
+  double s = 0.0;
+  for (uint64_t r = threadIdx.x; r < a.batch; r += BLOCK) s += a.row_loss[r];
+  s = block_sum<BLOCK>(s, lds);
+  if (threadIdx.x == 0)
+    *a.loss = static_cast<float>(s) / static_cast<float>(a.batch);  // evaluation.rs:616-619
+}
+
+// Register path: BLOCK lanes x V float4 hold one row of `classes` (= 4 * c4) logits.
+template <int BLOCK, int V>
+__global__ __launch_bounds__(BLOCK) void ce_row_kernel(CeArgs a) {
+  __shared__ float lds_f[BLOCK / 64];
+  __shared__ double lds_d[BLOCK / 64];
+  const uint64_t row = blockIdx.x;
+  const uint64_t c4 = a.classes / 4;
+  const float4 *x4 = reinterpret_cast<const float4 *>(a.logits + row * a.classes);
+  float4 v[V];
+  float m = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    const uint64_t i = threadIdx.x + static_cast<uint64_t>(k) * BLOCK;
+    if (i < c4) {
+      v[k] = x4[i];
+      m = fmaxf(m, fmaxf(fmaxf(v[k].x, v[k].y), fmaxf(v[k].z, v[k].w)));
+    }
+  }
+  const float maximum = block_max<BLOCK>(m, lds_f);
+  double s = 0.0;
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    const uint64_t i = threadIdx.x + static_cast<uint64_t>(k) * BLOCK;
+    if (i < c4) {
+      v[k].x = expf(v[k].x - maximum);
+      v[k].y = expf(v[k].y - maximum);
+      v[k].z = expf(v[k].z - maximum);
+      v[k].w = expf(v[k].w - maximum);
+      s += static_cast<double>(v[k].x + v[k].y) + static_cast<double>(v[k].z + v[k].w);
+    }
+  }
+  const float normalizer = static_cast<float>(block_sum<BLOCK>(s, lds_d));
+  uint64_t target = 0;
+  const bool valid = target_index(a.targets[row], a.classes, target);
+  if (!valid && threadIdx.x == 0 && a.error_flag) *a.error_flag = 1u;
+  if (a.grad) {
+    const float scale = *a.outer / static_cast<float>(a.batch);  // autograd.rs:540-541
+    float4 *g4 = reinterpret_cast<float4 *>(a.grad + row * a.classes);
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      const uint64_t i = threadIdx.x + static_cast<uint64_t>(k) * BLOCK;
+      if (i < c4) {
+        float4 r;
+        if (valid) {
+          const uint64_t e = 4 * i;
+          r.x = scale * (v[k].x / normalizer - (e + 0 == target ? 1.0f : 0.0f));
+          r.y = scale * (v[k].y / normalizer - (e + 1 == target ? 1.0f : 0.0f));
+          r.z = scale * (v[k].z / normalizer - (e + 2 == target ? 1.0f : 0.0f));
+          r.w = scale * (v[k].w / normalizer - (e + 3 == target ? 1.0f : 0.0f));
+        } else {
+          r = make_float4(NAN, NAN, NAN, NAN);
+        }
+        g4[i] = r;
+      }
+    }
+  }
+  const float row_loss =
+      valid ? logf(normalizer) + maximum - a.logits[row * a.classes + target] : NAN;
+  finish_row<BLOCK>(a, row, row_loss, lds_d);
+}
+
+// General path: any classes, any alignment; three strided passes over the row.
+constexpr int kGenBlock = 256;
+
+__global__ __launch_bounds__(kGenBlock) void ce_row_general_kernel(CeArgs a) {
+  __shared__ float lds_f[kGenBlock / 64];
+  __shared__ double lds_d[kGenBlock / 64];
+  const uint64_t row = blockIdx.x;
+  const float *x = a.logits + row * a.classes;
+  float m = -INFINITY;
+  for (uint64_t i = threadIdx.x; i < a.classes; i += kGenBlock) m = fmaxf(m, x[i]);
+  const float maximum = block_max<kGenBlock>(m, lds_f);
+  double s = 0.0;
+  for (uint64_t i = threadIdx.x; i < a.classes; i += kGenBlock)
+    s += static_cast<double>(expf(x[i] - maximum));
+  const float normalizer = static_cast<float>(block_sum<kGenBlock>(s, lds_d));
+  uint64_t target = 0;
+  const bool valid = target_index(a.targets[row], a.classes, target);
+  if (!valid && threadIdx.x == 0 && a.error_flag) *a.error_flag = 1u;
+  if (a.grad) {
+    const float scale = *a.outer / static_cast<float>(a.batch);
+    float *g = a.grad + row * a.classes;
+    for (uint64_t i = threadIdx.x; i < a.classes; i += kGenBlock) {
+      const float p = expf(x[i] - maximum) / normalizer;
+      g[i] = valid ? scale * (p - (i == target ? 1.0f : 0.0f)) : NAN;
+    }
+  }
+  const float row_loss = valid ? logf(normalizer) + maximum - x[target] : NAN;
+  finish_row<kGenBlock>(a, row, row_loss, lds_d);
+}
+
+uint64_t ce_workspace_bytes(uint64_t batch) { return (batch * 8 + 4 + 255) / 256 * 256; }
+
+oxh_status launch_ce(const char *name, oxh_stream stream, CeArgs a, void *workspace,
+                     uint64_t workspace_bytes) {
+  OXH_REQUIRE(a.batch > 0 && a.classes > 0, OXH_INVALID_SHAPE,
+              std::string(name) + ": empty logits");
+  OXH_REQUIRE(a.batch < (1ull << 31) && a.classes < (1ull << 40) &&
+                  a.batch * a.classes < (1ull << 42),
+              OXH_INVALID_SHAPE, std::string(name) + ": logits too large");
+  OXH_REQUIRE(a.logits && a.targets, OXH_INVALID_SHAPE, std::string(name) + ": null input");
+  OXH_REQUIRE(!a.grad || a.outer, OXH_INVALID_SHAPE,
+              std::string(name) + ": the gradient needs the upstream gradient scalar");
+  const uint64_t bytes = a.batch * a.classes * 4;
+  if (a.grad)
+    OXH_REQUIRE(!oxh::any_overlap(a.grad, bytes, a.logits, bytes), OXH_INVALID_SHAPE,
+                std::string(name) + ": gradient overlaps the logits");
+  if (a.loss) {
+    const uint64_t need = ce_workspace_bytes(a.batch);
+    OXH_REQUIRE(workspace != nullptr && workspace_bytes >= need, OXH_INVALID_SHAPE,
+                std::string(name) + ": workspace of " + std::to_string(need) +
+                    " bytes required (oxh_cross_entropy_workspace_size)");
+    OXH_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 7u) == 0, OXH_INVALID_SHAPE,
+                std::string(name) + ": workspace must be 8-byte aligned");
+    a.row_loss = static_cast<double *>(workspace);
+    a.counter = reinterpret_cast<uint32_t *>(static_cast<char *>(workspace) + a.batch * 8);
+  }
+  hipStream_t s = oxh::as_stream(stream);
+  const dim3 grid(static_cast<uint32_t>(a.batch));
+  const bool vec = a.classes % 4 == 0 && oxh::aligned16(a.logits) &&
+                   (!a.grad || oxh::aligned16(a.grad));
+  const uint64_t c4 = a.classes / 4;
+  if (vec && c4 <= 256) {
+    hipLaunchKernelGGL((ce_row_kernel<256, 1>), grid, dim3(256), 0, s, a);
+  } else if (vec && c4 <= 256 * 4) {
+    hipLaunchKernelGGL((ce_row_kernel<256, 4>), grid, dim3(256), 0, s, a);
+  } else if (vec && c4 <= 1024 * 2) {
+    hipLaunchKernelGGL((ce_row_kernel<1024, 2>), grid, dim3(1024), 0, s, a);
+  } else if (vec && c4 <= 1024 * 4) {
+    hipLaunchKernelGGL((ce_row_kernel<1024, 4>), grid, dim3(1024), 0, s, a);
+  } else if (vec && c4 <= 1024 * 8) {
+    hipLaunchKernelGGL((ce_row_kernel<1024, 8>), grid, dim3(1024), 0, s, a);
+  } else if (vec && c4 <= 1024 * 16) {
+    hipLaunchKernelGGL((ce_row_kernel<1024, 16>), grid, dim3(1024), 0, s, a);
+  } else {
+    hipLaunchKernelGGL(ce_row_general_kernel, grid, dim3(kGenBlock), 0, s, a);
+  }
+  return oxh::launched(name);
+}
+
+}  // namespace
+
+extern "C" {
+
+oxh_status oxh_cross_entropy_workspace_size(uint64_t batch, uint64_t classes, uint64_t *bytes) {
+  OXH_REQUIRE(bytes != nullptr, OXH_INVALID_SHAPE, "bytes is null");
+  OXH_REQUIRE(batch > 0 && classes > 0, OXH_INVALID_SHAPE, "empty logits");
+  *bytes = ce_workspace_bytes(batch);
+  return oxh::ok();
+}
+
+oxh_status oxh_cross_entropy_forward(oxh_stream stream, uint64_t batch, uint64_t classes,
+                                     const float *logits, const float *targets, float *loss,
+                                     uint32_t *error_flag, void *workspace,
+                                     uint64_t workspace_bytes) {
+  OXH_REQUIRE(loss != nullptr, OXH_INVALID_SHAPE, "oxh_cross_entropy_forward: null loss");
+  CeArgs a{logits, targets, nullptr, loss, nullptr, error_flag, nullptr, nullptr, batch,
+           classes};
+  return launch_ce("oxh_cross_entropy_forward", stream, a, workspace, workspace_bytes);
+}
+
+oxh_status oxh_cross_entropy_backward(oxh_stream stream, uint64_t batch, uint64_t classes,
+                                      const float *logits, const float *targets,
+                                      const float *outer_gradient, float *grad,
+                                      uint32_t *error_flag) {
+  OXH_REQUIRE(grad != nullptr, OXH_INVALID_SHAPE, "oxh_cross_entropy_backward: null grad");
+  CeArgs a{logits, targets, outer_gradient, nullptr, grad, error_flag, nullptr, nullptr, batch,
+           classes};
+  return launch_ce("oxh_cross_entropy_backward", stream, a, nullptr, 0);
+}
+
+oxh_status oxh_cross_entropy_forward_backward(oxh_stream stream, uint64_t batch,
+                                              uint64_t classes, const float *logits,
+                                              const float *targets,
+                                              const float *outer_gradient, float *loss,
+                                              float *grad, uint32_t *error_flag,
+                                              void *workspace, uint64_t workspace_bytes) {
+  OXH_REQUIRE(loss != nullptr && grad != nullptr, OXH_INVALID_SHAPE,
+              "oxh_cross_entropy_forward_backward: null output");
+  CeArgs a{logits, targets, outer_gradient, loss, grad, error_flag, nullptr, nullptr, batch,
+           classes};
+  return launch_ce("oxh_cross_entropy_forward_backward", stream, a, workspace,
+                   workspace_bytes);
+}
+
+}  // extern "C"

@@ -1,0 +1,186 @@
+// runtime.hip -- device selection, streams, buffers, errors and graph capture/replay.
+//
+// Mirrors the cuda-core calls the reference adapter makes (runtime.rs:46-105,
+// cuda/jit.rs:25-99) and the CudaGraphExec wrapper (cuda_graph.rs:47-179), on HIP directly:
+// the gfx950 code object is linked into this library, so "loading kernels" is selecting the
+// device.
+#include <hip/hip_runtime.h>
+
+#include <string>
+
+#include "common.h"
+
+namespace oxh {
+
+namespace {
+thread_local std::string g_last_error;
+}
+
+oxh_status fail(oxh_status status, const std::string &message) {
+  g_last_error = message;
+  return status;
+}
+
+oxh_status ok() {
+  g_last_error.clear();
+  return OXH_OK;
+}
+
+}  // namespace oxh
+
+struct oxh_graph {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+};
+
+extern "C" {
+
+const char *oxh_last_error(void) { return oxh::g_last_error.c_str(); }
+
+const char *oxh_version(void) { return "oxide-hip 0.1.0 (gfx950)"; }
+
+oxh_status oxh_device_count(int *count) {
+  OXH_REQUIRE(count != nullptr, OXH_INVALID_SHAPE, "count is null");
+  OXH_HIP_CHECK(hipGetDeviceCount(count));
+  return oxh::ok();
+}
+
+oxh_status oxh_init(int device) {
+  int count = 0;
+  OXH_HIP_CHECK(hipGetDeviceCount(&count));
+  OXH_REQUIRE(device >= 0 && device < count, OXH_INVALID_SHAPE,
+              "device " + std::to_string(device) + " is outside 0.." + std::to_string(count));
+  OXH_HIP_CHECK(hipSetDevice(device));
+  hipDeviceProp_t prop;
+  OXH_HIP_CHECK(hipGetDeviceProperties(&prop, device));
+  std::string arch = prop.gcnArchName;
+  OXH_REQUIRE(arch.rfind("gfx950", 0) == 0, OXH_EXECUTION,
+              "liboxide_hip is built for gfx950, device reports " + arch);
+  return oxh::ok();
+}
+
+oxh_status oxh_stream_create(oxh_stream *stream) {
+  OXH_REQUIRE(stream != nullptr, OXH_INVALID_SHAPE, "stream is null");
+  hipStream_t s = nullptr;
+  // Default priority, non-blocking with respect to the null stream: capturable.
+  OXH_HIP_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  *stream = s;
+  return oxh::ok();
+}
+
+oxh_status oxh_stream_destroy(oxh_stream stream) {
+  if (stream == nullptr) return oxh::ok();
+  OXH_HIP_CHECK(hipStreamDestroy(oxh::as_stream(stream)));
+  return oxh::ok();
+}
+
+oxh_status oxh_stream_synchronize(oxh_stream stream) {
+  OXH_HIP_CHECK(hipStreamSynchronize(oxh::as_stream(stream)));
+  return oxh::ok();
+}
+
+oxh_status oxh_alloc(void **ptr, uint64_t bytes) {
+  OXH_REQUIRE(ptr != nullptr, OXH_INVALID_SHAPE, "ptr is null");
+  *ptr = nullptr;
+  if (bytes == 0) return oxh::ok();
+  OXH_HIP_CHECK(hipMalloc(ptr, bytes));
+  return oxh::ok();
+}
+
+oxh_status oxh_free(void *ptr) {
+  if (ptr == nullptr) return oxh::ok();
+  OXH_HIP_CHECK(hipFree(ptr));
+  return oxh::ok();
+}
+
+oxh_status oxh_memset0_async(void *ptr, uint64_t bytes, oxh_stream stream) {
+  if (bytes == 0) return oxh::ok();
+  OXH_REQUIRE(ptr != nullptr, OXH_INVALID_SHAPE, "ptr is null");
+  OXH_HIP_CHECK(hipMemsetAsync(ptr, 0, bytes, oxh::as_stream(stream)));
+  return oxh::ok();
+}
+
+oxh_status oxh_memcpy_h2d_async(void *dst, const void *src, uint64_t bytes, oxh_stream stream) {
+  if (bytes == 0) return oxh::ok();
+  OXH_REQUIRE(dst != nullptr && src != nullptr, OXH_INVALID_SHAPE, "null pointer");
+  OXH_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, oxh::as_stream(stream)));
+  return oxh::ok();
+}
+
+oxh_status oxh_memcpy_d2h(void *dst, const void *src, uint64_t bytes, oxh_stream stream) {
+  if (bytes == 0) return oxh::ok();
+  OXH_REQUIRE(dst != nullptr && src != nullptr, OXH_INVALID_SHAPE, "null pointer");
+  OXH_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, oxh::as_stream(stream)));
+  OXH_HIP_CHECK(hipStreamSynchronize(oxh::as_stream(stream)));
+  return oxh::ok();
+}
+
+oxh_status oxh_memcpy_d2d_async(void *dst, const void *src, uint64_t bytes, oxh_stream stream) {
+  if (bytes == 0) return oxh::ok();
+  OXH_REQUIRE(dst != nullptr && src != nullptr, OXH_INVALID_SHAPE, "null pointer");
+  OXH_HIP_CHECK(
+      hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, oxh::as_stream(stream)));
+  return oxh::ok();
+}
+
+// ---------------------------------------------------------------- graphs
+
+oxh_status oxh_graph_begin(oxh_stream stream) {
+  OXH_REQUIRE(stream != nullptr, OXH_INVALID_SHAPE,
+              "the null stream cannot be captured; use oxh_stream_create");
+  // cuda_graph.rs:77 synchronizes before capture so earlier work is not part of the graph.
+  OXH_HIP_CHECK(hipStreamSynchronize(oxh::as_stream(stream)));
+  OXH_HIP_CHECK(hipStreamBeginCapture(oxh::as_stream(stream), hipStreamCaptureModeThreadLocal));
+  return oxh::ok();
+}
+
+oxh_status oxh_graph_abort(oxh_stream stream) {
+  // cuda_graph.rs:84-97: end capture even on a recording error and destroy what was recorded,
+  // so the stream stays usable.
+  hipGraph_t discarded = nullptr;
+  hipError_t err = hipStreamEndCapture(oxh::as_stream(stream), &discarded);
+  if (discarded != nullptr) (void)hipGraphDestroy(discarded);
+  (void)hipGetLastError();
+  if (err != hipSuccess && err != hipErrorStreamCaptureInvalidated)
+    return oxh::hip_status(err, "hipStreamEndCapture");
+  return oxh::ok();
+}
+
+oxh_status oxh_graph_end(oxh_stream stream, oxh_graph **out) {
+  OXH_REQUIRE(out != nullptr, OXH_INVALID_SHAPE, "graph out-pointer is null");
+  *out = nullptr;
+  hipGraph_t graph = nullptr;
+  hipError_t err = hipStreamEndCapture(oxh::as_stream(stream), &graph);
+  if (err != hipSuccess) {
+    if (graph != nullptr) (void)hipGraphDestroy(graph);
+    return oxh::hip_status(err, "hipStreamEndCapture");
+  }
+  OXH_REQUIRE(graph != nullptr, OXH_EXECUTION, "capture returned a null graph");
+  hipGraphExec_t exec = nullptr;
+  err = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  if (err != hipSuccess) {
+    (void)hipGraphDestroy(graph);
+    return oxh::hip_status(err, "hipGraphInstantiate");
+  }
+  *out = new oxh_graph{graph, exec};
+  return oxh::ok();
+}
+
+oxh_status oxh_graph_launch(const oxh_graph *graph, oxh_stream stream) {
+  OXH_REQUIRE(graph != nullptr, OXH_INVALID_SHAPE, "graph is null");
+  OXH_HIP_CHECK(hipGraphLaunch(graph->exec, oxh::as_stream(stream)));
+  return oxh::ok();
+}
+
+oxh_status oxh_graph_destroy(oxh_graph *graph) {
+  if (graph == nullptr) return oxh::ok();
+  // cuda_graph.rs:167-179: executable first, then its source graph.
+  hipError_t e1 = graph->exec ? hipGraphExecDestroy(graph->exec) : hipSuccess;
+  hipError_t e2 = graph->graph ? hipGraphDestroy(graph->graph) : hipSuccess;
+  delete graph;
+  OXH_HIP_CHECK(e1);
+  OXH_HIP_CHECK(e2);
+  return oxh::ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,700 @@
+"""Python front end of liboxide_hip.so (the MI355X backend of oxide-torch's tensor hot path).
+
+The C ABI (include/oxide_hip.h) is the product boundary; this module binds it with ctypes and
+mirrors the reference's backend surface on this path so tests and benchmarks read like the
+reference's own code:
+
+* ``LoadedModule``: the kernel launchers of ``oxide_torch_cuda::load_kernels``
+  (crates/oxide-torch-cuda/src/lib.rs:19-30, launchers from kernel_module.rs) -- ``add``,
+  ``mul``, ``relu``, ``mul_backward``, ``relu_backward``, ``accumulate``,
+  ``batch_norm_statistics``, ``batch_norm_update_running``, ``batch_norm_running_inverse_std``,
+  ``batch_norm_apply``, ``batch_norm_affine_backward``, ``batch_norm_input_backward``,
+  ``cross_entropy_forward``, ``cross_entropy_backward``, ``adamw`` -- plus the fused entry
+  points.  Arguments are device tensors (torch is only the allocator and stream provider).
+* ``HipGraphExec``: ``CudaGraphExec::{capture, launch}`` (cuda_graph.rs:47-165).
+* ``GraphPlan`` / ``HipJitPlan``: the fixed-buffer plan of jit.rs:24-56 and ``CudaJitPlan``
+  (cuda/jit.rs:10-99); ``trace`` / ``compile`` / ``JitModule`` mirror jit.rs:89-176 for the
+  elementwise operations the reference plans support.
+
+Errors raise ``OxideError`` whose ``kind`` names the reference's Error variant
+(crates/oxide-torch/src/error.rs): ``InvalidShape``, ``Execution``, ``Hip`` (for ``Cuda``),
+``Trace``.  There is no CPU fallback: if the library is missing every call fails.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+from dataclasses import dataclass, field
+from pathlib import Path
+from typing import Callable, Sequence
+
+_HERE = Path(__file__).resolve().parent
+LIB_PATH = _HERE / "liboxide_hip.so"
+HEADER_PATH = _HERE.parent / "include" / "oxide_hip.h"
+
+OK, INVALID_SHAPE, EXECUTION, HIP_ERROR, TRACE = 0, 1, 2, 3, 4
+_KINDS = {INVALID_SHAPE: "InvalidShape", EXECUTION: "Execution", HIP_ERROR: "Hip",
+          TRACE: "Trace"}
+
+PLAN_ADD, PLAN_MUL, PLAN_RELU = 1, 2, 3
+PLAN_RELU_BACKWARD, PLAN_MUL_BACKWARD, PLAN_ACCUMULATE = 4, 5, 6
+
+
+class OxideError(RuntimeError):
+    """A failed C-ABI call; ``kind`` is the reference Error variant it maps to."""
+
+    def __init__(self, status: int, message: str):
+        self.status = status
+        self.kind = _KINDS.get(status, f"status {status}")
+        super().__init__(f"{self.kind}: {message}")
+
+
+_vp = ctypes.c_void_p
+_u64 = ctypes.c_uint64
+_u32 = ctypes.c_uint32
+_i32 = ctypes.c_int32
+_int = ctypes.c_int
+_f32 = ctypes.c_float
+_st = ctypes.c_int
+
+
+class AdamWTensor(ctypes.Structure):
+    _fields_ = [("parameter", _vp), ("gradient", _vp), ("first_moment", _vp),
+                ("second_moment", _vp), ("n", _u64)]
+
+
+_SIGNATURES = {
+    "oxh_last_error": (ctypes.c_char_p, []),
+    "oxh_version": (ctypes.c_char_p, []),
+    "oxh_init": (_st, [_int]),
+    "oxh_device_count": (_st, [ctypes.POINTER(_int)]),
+    "oxh_stream_create": (_st, [ctypes.POINTER(_vp)]),
+    "oxh_stream_destroy": (_st, [_vp]),
+    "oxh_stream_synchronize": (_st, [_vp]),
+    "oxh_alloc": (_st, [ctypes.POINTER(_vp), _u64]),
+    "oxh_free": (_st, [_vp]),
+    "oxh_memset0_async": (_st, [_vp, _u64, _vp]),
+    "oxh_memcpy_h2d_async": (_st, [_vp, _vp, _u64, _vp]),
+    "oxh_memcpy_d2h": (_st, [_vp, _vp, _u64, _vp]),
+    "oxh_memcpy_d2d_async": (_st, [_vp, _vp, _u64, _vp]),
+    "oxh_add": (_st, [_vp, _vp, _vp, _vp, _u64]),
+    "oxh_mul": (_st, [_vp, _vp, _vp, _vp, _u64]),
+    "oxh_relu": (_st, [_vp, _vp, _vp, _u64]),
+    "oxh_mul_backward": (_st, [_vp, _vp, _vp, _vp, _u64]),
+    "oxh_relu_backward": (_st, [_vp, _vp, _vp, _vp, _u64]),
+    "oxh_accumulate": (_st, [_vp, _vp, _vp, _vp, _u64]),
+    "oxh_elementwise_chain_forward": (_st, [_vp, _vp, _vp, _vp, _vp, _u64]),
+    "oxh_elementwise_chain_backward": (_st, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u64]),
+    "oxh_batch_norm_workspace_size": (_st, [_u64, _u64, _u64, ctypes.POINTER(_u64)]),
+    "oxh_batch_norm_statistics": (_st, [_vp, _u64, _u64, _u64, _f32, _vp, _vp, _vp, _vp, _vp,
+                                        _u64]),
+    "oxh_batch_norm_update_running": (_st, [_vp, _u64, _f32, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "oxh_batch_norm_running_inverse_std": (_st, [_vp, _u64, _f32, _vp, _vp]),
+    "oxh_batch_norm_apply": (_st, [_vp, _u64, _u64, _u64, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "oxh_batch_norm_affine_backward": (_st, [_vp, _u64, _u64, _u64, _vp, _vp, _vp, _vp, _vp,
+                                             _vp, _vp, _u64]),
+    "oxh_batch_norm_input_backward": (_st, [_vp, _u64, _u64, _u64, _int, _vp, _vp, _vp, _vp,
+                                            _vp, _vp, _vp, _vp]),
+    "oxh_batch_norm_statistics_running": (_st, [_vp, _u64, _u64, _u64, _f32, _f32, _vp, _vp,
+                                                _vp, _vp, _vp, _vp, _u64]),
+    "oxh_batch_norm_forward_train": (_st, [_vp, _u64, _u64, _u64, _f32, _f32, _vp, _vp, _vp,
+                                           _vp, _vp, _vp, _vp, _vp, _vp, _u64]),
+    "oxh_batch_norm_backward_train": (_st, [_vp, _u64, _u64, _u64, _vp, _vp, _vp, _vp, _vp,
+                                            _vp, _vp, _vp, _vp, _u64]),
+    "oxh_cross_entropy_workspace_size": (_st, [_u64, _u64, ctypes.POINTER(_u64)]),
+    "oxh_cross_entropy_forward": (_st, [_vp, _u64, _u64, _vp, _vp, _vp, _vp, _vp, _u64]),
+    "oxh_cross_entropy_backward": (_st, [_vp, _u64, _u64, _vp, _vp, _vp, _vp, _vp]),
+    "oxh_cross_entropy_forward_backward": (_st, [_vp, _u64, _u64, _vp, _vp, _vp, _vp, _vp, _vp,
+                                                 _vp, _u64]),
+    "oxh_adamw": (_st, [_vp, _f32, _f32, _f32, _f32, _f32, _f32, _f32, _vp, _vp, _vp, _vp, _vp,
+                        _vp, _vp, _u64]),
+    "oxh_adamw_corrections": (_st, [_f32, _f32, _i32, ctypes.POINTER(_f32),
+                                    ctypes.POINTER(_f32)]),
+    "oxh_adamw_multi_tensor": (_st, [_vp, _f32, _f32, _f32, _f32, _f32, _f32, _f32,
+                                     ctypes.POINTER(AdamWTensor), _u32]),
+    "oxh_argmax_rows": (_st, [_vp, _u64, _u64, _vp, _vp]),
+    "oxh_graph_begin": (_st, [_vp]),
+    "oxh_graph_end": (_st, [_vp, ctypes.POINTER(_vp)]),
+    "oxh_graph_abort": (_st, [_vp]),
+    "oxh_graph_launch": (_st, [_vp, _vp]),
+    "oxh_graph_destroy": (_st, [_vp]),
+    "oxh_plan_create": (_st, [_int, ctypes.POINTER(_vp)]),
+    "oxh_plan_add_input": (_st, [_vp, _u64, ctypes.POINTER(_u32)]),
+    "oxh_plan_add_constant": (_st, [_vp, _vp, _u64, ctypes.POINTER(_u32)]),
+    "oxh_plan_add_workspace": (_st, [_vp, _u64, ctypes.POINTER(_u32)]),
+    "oxh_plan_add_operation": (_st, [_vp, _u32, ctypes.POINTER(_u32), _u32, _u32]),
+    "oxh_plan_set_output": (_st, [_vp, _u32]),
+    "oxh_plan_compile": (_st, [_vp]),
+    "oxh_plan_run": (_st, [_vp, ctypes.POINTER(_vp), _u32, _vp, _u64]),
+    "oxh_plan_replay": (_st, [_vp]),
+    "oxh_plan_stream": (_st, [_vp, ctypes.POINTER(_vp)]),
+    "oxh_plan_buffer": (_st, [_vp, _u32, ctypes.POINTER(_vp), ctypes.POINTER(_u64)]),
+    "oxh_plan_destroy": (_st, [_vp]),
+}
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Loads liboxide_hip.so (built by ``__graft_entry__.build()`` / ``make``)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise OxideError(HIP_ERROR, f"{LIB_PATH} is not built; run __graft_entry__.build()")
+        handle = ctypes.CDLL(os.fspath(LIB_PATH))
+        for name, (restype, argtypes) in _SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _lib = handle
+    return _lib
+
+
+def header_symbols() -> list[str]:
+    """Every function the C ABI header declares."""
+    text = HEADER_PATH.read_text()
+    return sorted(set(re.findall(r"\b(oxh_[a-z0-9_]+)\s*\(", text)))
+
+
+def check(status: int) -> None:
+    if status != OK:
+        raise OxideError(status, lib().oxh_last_error().decode())
+
+
+# ----------------------------------------------------------------------------- plumbing
+
+def _ptr(t) -> int | None:
+    """Device address of a torch tensor (or an int address, or None)."""
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    if not t.is_contiguous():
+        raise OxideError(INVALID_SHAPE, "tensors must be contiguous")
+    return t.data_ptr()
+
+
+def _f32_tensor(t, name: str):
+    import torch
+
+    if t.dtype != torch.float32 or not t.is_cuda:
+        raise OxideError(INVALID_SHAPE, f"{name} must be a float32 device tensor")
+    return t
+
+
+def current_stream() -> int:
+    import torch
+
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _stream(stream) -> int | None:
+    if stream is None:
+        return current_stream()
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream  # torch.cuda.Stream
+
+
+class Workspace:
+    """Zero-filled device scratch reused across calls (kernels leave it zeroed)."""
+
+    def __init__(self):
+        self._buf = None
+
+    def get(self, nbytes: int):
+        import torch
+
+        if self._buf is None or self._buf.numel() < nbytes:
+            self._buf = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device="cuda")
+            # the zero fill runs on torch's stream; kernels may use another stream
+            torch.cuda.synchronize()
+        return self._buf
+
+    def ptr_bytes(self, nbytes: int) -> tuple[int, int]:
+        b = self.get(nbytes)
+        return b.data_ptr(), b.numel()
+
+
+def batch_norm_workspace_size(batch: int, channels: int, spatial: int) -> int:
+    out = _u64()
+    check(lib().oxh_batch_norm_workspace_size(batch, channels, spatial, ctypes.byref(out)))
+    return out.value
+
+
+def cross_entropy_workspace_size(batch: int, classes: int) -> int:
+    out = _u64()
+    check(lib().oxh_cross_entropy_workspace_size(batch, classes, ctypes.byref(out)))
+    return out.value
+
+
+def adamw_corrections(beta1: float, beta2: float, step: int) -> tuple[float, float]:
+    c1, c2 = _f32(), _f32()
+    check(lib().oxh_adamw_corrections(beta1, beta2, step, ctypes.byref(c1), ctypes.byref(c2)))
+    return c1.value, c2.value
+
+
+def init(device: int = 0) -> None:
+    check(lib().oxh_init(device))
+
+
+# ----------------------------------------------------------------------------- launchers
+
+class LoadedModule:
+    """Launchers with the reference kernel names (kernel_module.rs) over device tensors.
+
+    Each call enqueues on ``stream`` (default: torch's current stream) and returns at once.
+    Reductions use a workspace owned by this object, so calls through one module must be
+    ordered on one stream.
+    """
+
+    def __init__(self, device: int = 0):
+        init(device)
+        self._bn_ws = Workspace()
+        self._ce_ws = Workspace()
+
+    # -- elementwise (kernel_module.rs:8-34, 492-508, 1052-1059)
+    def add(self, a, b, out, stream=None):
+        check(lib().oxh_add(_stream(stream), _ptr(a), _ptr(b), _ptr(out), out.numel()))
+
+    def mul(self, a, b, out, stream=None):
+        check(lib().oxh_mul(_stream(stream), _ptr(a), _ptr(b), _ptr(out), out.numel()))
+
+    def relu(self, x, out, stream=None):
+        check(lib().oxh_relu(_stream(stream), _ptr(x), _ptr(out), out.numel()))
+
+    def mul_backward(self, gradient, other, out, stream=None):
+        check(lib().oxh_mul_backward(_stream(stream), _ptr(gradient), _ptr(other), _ptr(out),
+                                     out.numel()))
+
+    def relu_backward(self, gradient, x, out, stream=None):
+        check(lib().oxh_relu_backward(_stream(stream), _ptr(gradient), _ptr(x), _ptr(out),
+                                      out.numel()))
+
+    def accumulate(self, a, b, out, stream=None):
+        check(lib().oxh_accumulate(_stream(stream), _ptr(a), _ptr(b), _ptr(out), out.numel()))
+
+    def elementwise_chain_forward(self, a, b, c, y, stream=None):
+        check(lib().oxh_elementwise_chain_forward(_stream(stream), _ptr(a), _ptr(b), _ptr(c),
+                                                  _ptr(y), y.numel()))
+
+    def elementwise_chain_backward(self, a, b, c, gradient, da, db, dc, stream=None):
+        check(lib().oxh_elementwise_chain_backward(_stream(stream), _ptr(a), _ptr(b), _ptr(c),
+                                                   _ptr(gradient), _ptr(da), _ptr(db), _ptr(dc),
+                                                   da.numel()))
+
+    # -- batch norm (kernel_module.rs:827-964, 1061-1092)
+    def _bn_ws_args(self, n, c, s):
+        return self._bn_ws.ptr_bytes(batch_norm_workspace_size(n, c, s))
+
+    def batch_norm_statistics(self, batch, channels, spatial, epsilon, x, mean, inverse_std,
+                              unbiased_variance, stream=None):
+        ws, wsb = self._bn_ws_args(batch, channels, spatial)
+        check(lib().oxh_batch_norm_statistics(_stream(stream), batch, channels, spatial, epsilon,
+                                              _ptr(x), _ptr(mean), _ptr(inverse_std),
+                                              _ptr(unbiased_variance), ws, wsb))
+
+    def batch_norm_update_running(self, momentum, batch_mean, batch_variance, old_mean,
+                                  old_variance, new_mean, new_variance, stream=None):
+        check(lib().oxh_batch_norm_update_running(_stream(stream), new_mean.numel(), momentum,
+                                                  _ptr(batch_mean), _ptr(batch_variance),
+                                                  _ptr(old_mean), _ptr(old_variance),
+                                                  _ptr(new_mean), _ptr(new_variance)))
+
+    def batch_norm_running_inverse_std(self, epsilon, variance, inverse_std, stream=None):
+        check(lib().oxh_batch_norm_running_inverse_std(_stream(stream), variance.numel(),
+                                                       epsilon, _ptr(variance),
+                                                       _ptr(inverse_std)))
+
+    def batch_norm_apply(self, channels, spatial, x, weight, bias, mean, inverse_std, out,
+                         stream=None):
+        batch = x.numel() // (channels * spatial)
+        check(lib().oxh_batch_norm_apply(_stream(stream), batch, channels, spatial, _ptr(x),
+                                         _ptr(weight), _ptr(bias), _ptr(mean),
+                                         _ptr(inverse_std), _ptr(out)))
+
+    def batch_norm_affine_backward(self, batch, channels, spatial, gradient, x, mean,
+                                   inverse_std, weight_gradient, bias_gradient, stream=None):
+        ws, wsb = self._bn_ws_args(batch, channels, spatial)
+        check(lib().oxh_batch_norm_affine_backward(_stream(stream), batch, channels, spatial,
+                                                   _ptr(gradient), _ptr(x), _ptr(mean),
+                                                   _ptr(inverse_std), _ptr(weight_gradient),
+                                                   _ptr(bias_gradient), ws, wsb))
+
+    def batch_norm_input_backward(self, channels, spatial, samples, training, gradient, x,
+                                  weight, mean, inverse_std, weight_gradient, bias_gradient,
+                                  out, stream=None):
+        batch = samples // spatial
+        check(lib().oxh_batch_norm_input_backward(_stream(stream), batch, channels, spatial,
+                                                  int(bool(training)), _ptr(gradient), _ptr(x),
+                                                  _ptr(weight), _ptr(mean), _ptr(inverse_std),
+                                                  _ptr(weight_gradient), _ptr(bias_gradient),
+                                                  _ptr(out)))
+
+    def batch_norm_statistics_running(self, x, running_mean, running_variance, saved_mean,
+                                      saved_inverse_std, momentum=0.1, epsilon=1e-5,
+                                      stream=None):
+        n, c, h, w = x.shape
+        ws, wsb = self._bn_ws_args(n, c, h * w)
+        check(lib().oxh_batch_norm_statistics_running(_stream(stream), n, c, h * w, momentum,
+                                                      epsilon, _ptr(x), _ptr(running_mean),
+                                                      _ptr(running_variance), _ptr(saved_mean),
+                                                      _ptr(saved_inverse_std), ws, wsb))
+
+    def batch_norm_forward_train(self, x, weight, bias, running_mean, running_variance,
+                                 saved_mean, saved_inverse_std, out, momentum=0.1, epsilon=1e-5,
+                                 stream=None):
+        n, c, h, w = x.shape
+        ws, wsb = self._bn_ws_args(n, c, h * w)
+        check(lib().oxh_batch_norm_forward_train(_stream(stream), n, c, h * w, momentum, epsilon,
+                                                 _ptr(x), _ptr(weight), _ptr(bias),
+                                                 _ptr(running_mean), _ptr(running_variance),
+                                                 _ptr(saved_mean), _ptr(saved_inverse_std),
+                                                 _ptr(out), ws, wsb))
+
+    def batch_norm_backward_train(self, gradient, x, weight, saved_mean, saved_inverse_std,
+                                  input_gradient, weight_gradient, bias_gradient, stream=None):
+        n, c, h, w = x.shape
+        ws, wsb = self._bn_ws_args(n, c, h * w)
+        check(lib().oxh_batch_norm_backward_train(_stream(stream), n, c, h * w, _ptr(gradient),
+                                                  _ptr(x), _ptr(weight), _ptr(saved_mean),
+                                                  _ptr(saved_inverse_std), _ptr(input_gradient),
+                                                  _ptr(weight_gradient), _ptr(bias_gradient),
+                                                  ws, wsb))
+
+    # -- cross entropy (kernel_module.rs:966-1050)
+    def cross_entropy_forward(self, batch, classes, logits, targets, loss, error_flag=None,
+                              stream=None):
+        ws, wsb = self._ce_ws.ptr_bytes(cross_entropy_workspace_size(batch, classes))
+        check(lib().oxh_cross_entropy_forward(_stream(stream), batch, classes, _ptr(logits),
+                                              _ptr(targets), _ptr(loss), _ptr(error_flag), ws,
+                                              wsb))
+
+    def cross_entropy_backward(self, batch, classes, logits, targets, outer_gradient, grad,
+                               error_flag=None, stream=None):
+        check(lib().oxh_cross_entropy_backward(_stream(stream), batch, classes, _ptr(logits),
+                                               _ptr(targets), _ptr(outer_gradient), _ptr(grad),
+                                               _ptr(error_flag)))
+
+    def cross_entropy_forward_backward(self, batch, classes, logits, targets, outer_gradient,
+                                       loss, grad, error_flag=None, stream=None):
+        ws, wsb = self._ce_ws.ptr_bytes(cross_entropy_workspace_size(batch, classes))
+        check(lib().oxh_cross_entropy_forward_backward(_stream(stream), batch, classes,
+                                                       _ptr(logits), _ptr(targets),
+                                                       _ptr(outer_gradient), _ptr(loss),
+                                                       _ptr(grad), _ptr(error_flag), ws, wsb))
+
+    # -- AdamW (kernel_module.rs:1094-1127)
+    def adamw(self, learning_rate, weight_decay, beta1, beta2, first_correction,
+              second_correction, epsilon, parameter, gradient, first_moment, second_moment,
+              new_parameter, new_first_moment, new_second_moment, stream=None):
+        check(lib().oxh_adamw(_stream(stream), learning_rate, weight_decay, beta1, beta2,
+                              first_correction, second_correction, epsilon, _ptr(parameter),
+                              _ptr(gradient), _ptr(first_moment), _ptr(second_moment),
+                              _ptr(new_parameter), _ptr(new_first_moment),
+                              _ptr(new_second_moment), parameter.numel()))
+
+    def adamw_multi_tensor(self, learning_rate, weight_decay, beta1, beta2, first_correction,
+                           second_correction, epsilon, tensors, stream=None):
+        """``tensors``: sequence of (parameter, gradient, first_moment, second_moment)."""
+        table = (AdamWTensor * len(tensors))()
+        for i, (p, g, m, v) in enumerate(tensors):
+            table[i] = AdamWTensor(_ptr(p), _ptr(g), _ptr(m), _ptr(v), p.numel())
+        check(lib().oxh_adamw_multi_tensor(_stream(stream), learning_rate, weight_decay, beta1,
+                                           beta2, first_correction, second_correction, epsilon,
+                                           table, len(tensors)))
+
+    def argmax_rows(self, logits, indices, stream=None):
+        rows, classes = logits.shape
+        check(lib().oxh_argmax_rows(_stream(stream), rows, classes, _ptr(logits),
+                                    _ptr(indices)))
+
+
+def load_kernels(device: int = 0) -> LoadedModule:
+    """``oxide_torch_cuda::load_kernels`` (lib.rs:19-30): the module for ``device``."""
+    return LoadedModule(device)
+
+
+# ----------------------------------------------------------------------------- graphs
+
+class HipGraphExec:
+    """``CudaGraphExec`` (cuda_graph.rs:30-179): capture once, launch many times."""
+
+    def __init__(self, handle: int):
+        self._handle = handle
+
+    @classmethod
+    def capture(cls, stream, record: Callable[[], None]) -> "HipGraphExec":
+        s = _stream(stream)
+        check(lib().oxh_graph_begin(s))
+        try:
+            record()
+        except Exception as exc:
+            # cuda_graph.rs:84-97: end and discard the capture, keep the stream usable.
+            lib().oxh_graph_abort(s)
+            if isinstance(exc, OxideError):
+                raise OxideError(EXECUTION, f"graph recording failed: {exc}") from exc
+            raise OxideError(EXECUTION, f"graph recording failed: {exc}") from exc
+        handle = _vp()
+        check(lib().oxh_graph_end(s, ctypes.byref(handle)))
+        return cls(handle.value)
+
+    def launch(self, stream) -> None:
+        check(lib().oxh_graph_launch(self._handle, _stream(stream)))
+
+    def __del__(self):
+        if getattr(self, "_handle", None) and _lib is not None:
+            _lib.oxh_graph_destroy(self._handle)
+            self._handle = None
+
+
+# ----------------------------------------------------------------------------- plans
+
+@dataclass
+class Input:
+    elements: int
+
+
+@dataclass
+class Constant:
+    values: Sequence[float]
+
+
+@dataclass
+class WorkspaceBuffer:
+    elements: int
+
+
+@dataclass
+class Operation:
+    op: int
+    inputs: tuple[int, ...]
+    output: int
+
+
+@dataclass
+class GraphPlan:
+    """jit.rs:24-56: buffers, operations, input slots, output slot."""
+
+    buffers: list = field(default_factory=list)
+    operations: list[Operation] = field(default_factory=list)
+    inputs: list[int] = field(default_factory=list)
+    output: int = -1
+
+
+class HipJitPlan:
+    """``CudaJitPlan`` (cuda/jit.rs:10-99) on liboxide_hip's plan runtime."""
+
+    def __init__(self, plan: GraphPlan, device: int = 0):
+        import numpy as np
+
+        handle = _vp()
+        check(lib().oxh_plan_create(device, ctypes.byref(handle)))
+        self._handle = handle.value
+        self._slots: list[int] = []
+        self._input_slots: list[int] = []
+        try:
+            for buf in plan.buffers:
+                slot = _u32()
+                if isinstance(buf, Input):
+                    check(lib().oxh_plan_add_input(self._handle, buf.elements,
+                                                   ctypes.byref(slot)))
+                    self._input_slots.append(len(self._slots))
+                elif isinstance(buf, Constant):
+                    arr = np.ascontiguousarray(buf.values, dtype=np.float32)
+                    check(lib().oxh_plan_add_constant(self._handle, arr.ctypes.data, arr.size,
+                                                      ctypes.byref(slot)))
+                else:
+                    check(lib().oxh_plan_add_workspace(self._handle, buf.elements,
+                                                       ctypes.byref(slot)))
+                self._slots.append(slot.value)
+            if [self._input_slots[i] for i in range(len(self._input_slots))] != list(
+                    plan.inputs):
+                raise OxideError(TRACE, "plan inputs must be the Input buffers in order")
+            for op in plan.operations:
+                ins = (_u32 * len(op.inputs))(*[self._slots[i] for i in op.inputs])
+                check(lib().oxh_plan_add_operation(self._handle, op.op, ins, len(op.inputs),
+                                                   self._slots[op.output]))
+            check(lib().oxh_plan_set_output(self._handle, self._slots[plan.output]))
+            check(lib().oxh_plan_compile(self._handle))
+        except Exception:
+            lib().oxh_plan_destroy(self._handle)
+            self._handle = None
+            raise
+        elements = _u64()
+        ptr = _vp()
+        check(lib().oxh_plan_buffer(self._handle, self._slots[plan.output], ctypes.byref(ptr),
+                                    ctypes.byref(elements)))
+        self.output_elements = elements.value
+        self.plan = plan
+
+    def run(self, inputs: Sequence) -> "np.ndarray":  # noqa: F821
+        """H2D inputs, one replay, synchronous D2H of the output (cuda/jit.rs:70-99)."""
+        import numpy as np
+
+        arrays = [np.ascontiguousarray(x, dtype=np.float32) for x in inputs]
+        ptrs = (_vp * len(arrays))(*[a.ctypes.data for a in arrays])
+        out = np.empty(self.output_elements, dtype=np.float32)
+        check(lib().oxh_plan_run(self._handle, ptrs, len(arrays), out.ctypes.data, out.size))
+        return out
+
+    def replay(self) -> None:
+        check(lib().oxh_plan_replay(self._handle))
+
+    def stream(self) -> int:
+        s = _vp()
+        check(lib().oxh_plan_stream(self._handle, ctypes.byref(s)))
+        return s.value or 0
+
+    def buffer(self, index: int) -> tuple[int, int]:
+        """(device address, elements) of the plan's buffer ``index``."""
+        ptr, n = _vp(), _u64()
+        check(lib().oxh_plan_buffer(self._handle, self._slots[index], ctypes.byref(ptr),
+                                    ctypes.byref(n)))
+        return ptr.value, n.value
+
+    def close(self) -> None:
+        if self._handle is not None:
+            check(lib().oxh_plan_destroy(self._handle))
+            self._handle = None
+
+    def __del__(self):
+        if getattr(self, "_handle", None) is not None and _lib is not None:
+            _lib.oxh_plan_destroy(self._handle)
+            self._handle = None
+
+
+# ----------------------------------------------------------------------------- trace / compile
+
+class Placeholder:
+    """A traced value: a placeholder input, a constant or an elementwise op of traced values.
+
+    Mirrors the lazy ``Tensor`` builders the reference plans lower (tensor/mod.rs:103-122:
+    equal shapes, no broadcasting)."""
+
+    _next_id = 0
+
+    def __init__(self, shape, kind, args=(), value=None):
+        self.shape = tuple(int(s) for s in shape)
+        self.kind = kind  # "input", "constant", "add", "mul", "relu"
+        self.args = args
+        self.value = value
+        Placeholder._next_id += 1
+        self.id = Placeholder._next_id
+
+    def numel(self) -> int:
+        n = 1
+        for s in self.shape:
+            n *= s
+        return n
+
+    def _binary(self, other, kind):
+        if not isinstance(other, Placeholder):
+            other = constant(other, self.shape)
+        if other.shape != self.shape:
+            raise OxideError(INVALID_SHAPE, f"shape mismatch {self.shape} vs {other.shape}")
+        return Placeholder(self.shape, kind, (self, other))
+
+    def add(self, other):
+        return self._binary(other, "add")
+
+    def mul(self, other):
+        return self._binary(other, "mul")
+
+    def relu(self):
+        return Placeholder(self.shape, "relu", (self,))
+
+    __add__ = add
+    __mul__ = mul
+
+
+def constant(values, shape=None) -> Placeholder:
+    import numpy as np
+
+    arr = np.ascontiguousarray(values, dtype=np.float32)
+    if shape is not None:
+        arr = np.broadcast_to(arr, shape).astype(np.float32)
+    return Placeholder(arr.shape, "constant", value=arr.ravel())
+
+
+def lower(output: Placeholder, inputs: Sequence[Placeholder]) -> GraphPlan:
+    """``PlanBuilder::lower`` (jit.rs:276-412): post-order, one buffer per node, memoised."""
+    plan = GraphPlan()
+    slots: dict[int, int] = {}
+    input_slot = {p.id: None for p in inputs}
+    opcode = {"add": PLAN_ADD, "mul": PLAN_MUL, "relu": PLAN_RELU}
+
+    # Inputs become the first buffers so their slots follow the argument order.
+    for p in inputs:
+        slots[p.id] = len(plan.buffers)
+        plan.buffers.append(Input(p.numel()))
+        input_slot[p.id] = slots[p.id]
+
+    def visit(node: Placeholder) -> int:
+        if node.id in slots:
+            return slots[node.id]
+        if node.kind == "input":
+            raise OxideError(TRACE, "traced graph reads a placeholder that is not an input")
+        if node.kind == "constant":
+            slots[node.id] = len(plan.buffers)
+            plan.buffers.append(Constant(node.value))
+            return slots[node.id]
+        args = tuple(visit(a) for a in node.args)
+        slot = len(plan.buffers)
+        plan.buffers.append(WorkspaceBuffer(node.numel()))
+        plan.operations.append(Operation(opcode[node.kind], args, slot))
+        slots[node.id] = slot
+        return slot
+
+    plan.output = visit(output)
+    used = set()
+    for op in plan.operations:
+        used.update(op.inputs)
+    used.add(plan.output)
+    for i, p in enumerate(inputs):
+        if slots[p.id] not in used:
+            raise OxideError(TRACE, f"traced input {i} is unused")  # jit.rs:259-266
+    plan.inputs = [slots[p.id] for p in inputs]
+    return plan
+
+
+class JitModule:
+    """``jit::trace`` / ``jit::compile`` result (jit.rs:14-176): one compiled plan per input
+    shape signature, created on first use and replayed afterwards."""
+
+    def __init__(self, fn: Callable, device: int = 0):
+        self.fn = fn
+        self.device = device
+        self._plans: dict[tuple, HipJitPlan] = {}
+
+    def cached_specializations(self) -> int:
+        return len(self._plans)
+
+    def plan_for(self, shapes: tuple) -> HipJitPlan:
+        if shapes not in self._plans:
+            holders = [Placeholder(s, "input") for s in shapes]
+            out = self.fn(*holders)
+            self._plans[shapes] = HipJitPlan(lower(out, holders), self.device)
+        return self._plans[shapes]
+
+    def run(self, *inputs):
+        import numpy as np
+
+        arrays = [np.ascontiguousarray(x, dtype=np.float32) for x in inputs]
+        shapes = tuple(a.shape for a in arrays)
+        plan = self.plan_for(shapes)
+        out_shape = self._out_shape(shapes)
+        return plan.run(arrays).reshape(out_shape)
+
+    def _out_shape(self, shapes):
+        holders = [Placeholder(s, "input") for s in shapes]
+        return self.fn(*holders).shape
+
+
+def compile(fn: Callable, device: int = 0) -> JitModule:  # noqa: A001 - mirrors jit::compile
+    return JitModule(fn, device)
+
+
+trace = compile

@@ -1,0 +1,154 @@
+"""CPU-side checks of the C ABI: the library loads and exports every declared symbol, and the
+host logic (argument validation, workspace sizing, AdamW corrections, plan building, trace
+lowering) behaves like the reference.  No call here reaches a GPU: every failing call is
+rejected on the host before any launch."""
+
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle
+import oxide_hip as ox
+
+
+def test_library_exports_every_header_symbol():
+    lib = ox.lib()
+    symbols = ox.header_symbols()
+    assert len(symbols) >= 50
+    missing = [s for s in symbols if not hasattr(lib, s)]
+    assert not missing, missing
+    # every declared function also has a ctypes signature in the front end
+    assert set(symbols) <= set(ox._SIGNATURES), set(symbols) - set(ox._SIGNATURES)
+    assert ox.lib().oxh_version().decode().startswith("oxide-hip")
+
+
+def _status(call):
+    return call
+
+
+def test_elementwise_rejects_null_and_partial_overlap():
+    lib = ox.lib()
+    assert lib.oxh_add(None, None, 16, 32, 4) == ox.INVALID_SHAPE
+    assert b"null" in lib.oxh_last_error()
+    # output overlapping an input by a partial offset is refused (exact aliasing is allowed)
+    base = 1 << 20
+    assert lib.oxh_add(None, base, base + 4096, base + 4, 100) == ox.INVALID_SHAPE
+    assert b"overlap" in lib.oxh_last_error()
+    # n == 0 is a no-op that touches nothing
+    assert lib.oxh_add(None, None, None, None, 0) == ox.OK
+    # chain backward outputs must be distinct
+    assert lib.oxh_elementwise_chain_backward(None, 16, 32, 48, None, 1 << 20, 1 << 20,
+                                              1 << 21, 8) == ox.INVALID_SHAPE
+
+
+def test_batch_norm_rejects_single_sample_like_reference():
+    """evaluation.rs:498-502 / runtime.rs:543-547: Error::Execution."""
+    lib = ox.lib()
+    ws = ctypes.c_uint64()
+    assert lib.oxh_batch_norm_workspace_size(1, 2, 1, ctypes.byref(ws)) == ox.OK
+    st = lib.oxh_batch_norm_statistics(None, 1, 2, 1, 1e-5, 256, 512, 768, 1024, 4096,
+                                       ws.value)
+    assert st == ox.EXECUTION
+    assert b"more than one value per channel" in lib.oxh_last_error()
+    with pytest.raises(oracle.OracleError) as err:
+        oracle.bn_forward(np.ones((1, 2, 1, 1), np.float32), np.ones(2, np.float32),
+                          np.zeros(2, np.float32), np.zeros(2, np.float32),
+                          np.ones(2, np.float32))
+    assert err.value.kind == "Execution"
+
+
+def test_batch_norm_workspace_checks():
+    lib = ox.lib()
+    size = ox.batch_norm_workspace_size(64, 128, 3136)
+    assert size % 256 == 0 and size >= 128 * 16
+    # too small a workspace is refused before launch
+    st = lib.oxh_batch_norm_statistics(None, 64, 128, 3136, 1e-5, 256, 512, 768, 1024, 4096,
+                                       size - 256)
+    assert st == ox.INVALID_SHAPE and b"workspace" in lib.oxh_last_error()
+    assert ox.batch_norm_workspace_size(1, 1, 2) >= 16
+    with pytest.raises(ox.OxideError) as err:
+        ox.batch_norm_workspace_size(0, 3, 3)
+    assert err.value.kind == "InvalidShape"
+
+
+def test_cross_entropy_argument_checks():
+    lib = ox.lib()
+    assert ox.cross_entropy_workspace_size(8192, 32768) >= 8192 * 8 + 4
+    # the gradient needs the upstream scalar
+    st = lib.oxh_cross_entropy_backward(None, 2, 3, 256, 512, None, 4096, None)
+    assert st == ox.INVALID_SHAPE
+    # empty logits
+    assert lib.oxh_cross_entropy_backward(None, 0, 3, 256, 512, 768, 4096, None) == \
+        ox.INVALID_SHAPE
+
+
+@pytest.mark.parametrize("step", [1, 2, 3, 7, 10, 100, 1000, 65537])
+def test_adamw_corrections_match_reference_powi(step):
+    """optim.rs:91-92 / 113-114: 1 - beta.powi(step) with compiler-rt's __powisf2."""
+    c1, c2 = ox.adamw_corrections(0.9, 0.999, step)
+    assert np.float32(c1) == np.float32(1.0) - np.float32(oracle.powi(0.9, step))
+    assert np.float32(c2) == np.float32(1.0) - np.float32(oracle.powi(0.999, step))
+
+
+def test_adamw_rejects_non_finite_hyper_parameters():
+    lib = ox.lib()
+    st = lib.oxh_adamw(None, float("nan"), 0.01, 0.9, 0.999, 0.5, 0.5, 1e-8, 256, 512, 768,
+                       1024, 256, 768, 1024, 4)
+    assert st == ox.INVALID_SHAPE
+
+
+def test_plan_builder_validation():
+    lib = ox.lib()
+    h = ctypes.c_void_p()
+    assert lib.oxh_plan_create(0, ctypes.byref(h)) == ox.OK
+    a, b, w = ctypes.c_uint32(), ctypes.c_uint32(), ctypes.c_uint32()
+    assert lib.oxh_plan_add_input(h, 4, ctypes.byref(a)) == ox.OK
+    assert lib.oxh_plan_add_input(h, 4, ctypes.byref(b)) == ox.OK
+    assert lib.oxh_plan_add_workspace(h, 4, ctypes.byref(w)) == ox.OK
+    ins = (ctypes.c_uint32 * 2)(a.value, b.value)
+    # wrong arity, unknown op, writing an input, reading own output, size mismatch
+    assert lib.oxh_plan_add_operation(h, ox.PLAN_RELU, ins, 2, w.value) == ox.TRACE
+    assert lib.oxh_plan_add_operation(h, 99, ins, 2, w.value) == ox.TRACE
+    assert lib.oxh_plan_add_operation(h, ox.PLAN_ADD, ins, 2, a.value) == ox.TRACE
+    self_read = (ctypes.c_uint32 * 2)(a.value, w.value)
+    assert lib.oxh_plan_add_operation(h, ox.PLAN_ADD, self_read, 2, w.value) == ox.TRACE
+    big = ctypes.c_uint32()
+    assert lib.oxh_plan_add_input(h, 8, ctypes.byref(big)) == ox.OK
+    mism = (ctypes.c_uint32 * 2)(a.value, big.value)
+    assert lib.oxh_plan_add_operation(h, ox.PLAN_ADD, mism, 2, w.value) == ox.INVALID_SHAPE
+    assert lib.oxh_plan_add_operation(h, ox.PLAN_ADD, ins, 2, w.value) == ox.OK
+    # running an uncompiled plan is a Trace error
+    out = np.empty(4, np.float32)
+    assert lib.oxh_plan_run(h, None, 0, out.ctypes.data, 4) == ox.TRACE
+    assert lib.oxh_plan_replay(h) == ox.TRACE
+    assert lib.oxh_plan_destroy(h) == ox.OK
+
+
+def test_trace_lowering_matches_reference_plan_shape():
+    """PlanBuilder::lower (jit.rs:276-412): relu((a + b) * c) -> 3 inputs, 3 workspaces."""
+    a, b, c = (ox.Placeholder((4096, 4096), "input") for _ in range(3))
+    plan = ox.lower(((a + b) * c).relu(), [a, b, c])
+    kinds = [type(x).__name__ for x in plan.buffers]
+    assert kinds == ["Input"] * 3 + ["WorkspaceBuffer"] * 3
+    assert [o.op for o in plan.operations] == [ox.PLAN_ADD, ox.PLAN_MUL, ox.PLAN_RELU]
+    assert plan.operations[0].inputs == (0, 1) and plan.operations[1].inputs == (3, 2)
+    assert plan.output == 5 and plan.inputs == [0, 1, 2]
+
+
+def test_trace_rejects_unused_input_and_shape_mismatch():
+    """jit.rs:259-266 (unused traced input) and tensor/mod.rs:536-552 (equal shapes)."""
+    a, b = ox.Placeholder((2,), "input"), ox.Placeholder((2,), "input")
+    with pytest.raises(ox.OxideError) as err:
+        ox.lower(a.relu(), [a, b])
+    assert err.value.kind == "Trace"
+    with pytest.raises(ox.OxideError) as err:
+        ox.Placeholder((2,), "input") + ox.Placeholder((3,), "input")
+    assert err.value.kind == "InvalidShape"
+
+
+def test_trace_constants_become_constant_buffers():
+    x = ox.Placeholder((2,), "input")
+    plan = ox.lower((x + ox.constant([1.0, 1.0])).relu(), [x])
+    assert [type(b).__name__ for b in plan.buffers] == ["Input", "Constant", "WorkspaceBuffer",
+                                                       "WorkspaceBuffer"]

@@ -1,0 +1,204 @@
+"""BatchNorm2d training forward (statistics, running update, apply) and input / weight / bias
+backward on the GPU against the oracle (evaluation.rs:448-597, autograd.rs:315-383), from
+tiny shapes with vector and scalar paths up to config 2's [64, 128, 56, 56].
+
+Tolerances (north star: max rel err 1e-5, abs 1e-6 near zero):
+  * per-element outputs (y, mean, inverse std, running stats, dx) must meet
+    |gpu - cpu| <= max(1e-5 |cpu|, 1e-6), or, where the value is a cancelling sum, the
+    conditioning bound |gpu - cpu| <= 1e-5 * (sum of the magnitudes of its terms);
+  * channel sums (dweight, dbias) of up to 200 704 terms: the oracle's sequential fp32 sum
+    carries rounding error ~1e-3 absolute, so they are checked against the conditioning bound
+    1e-5 * sum|terms| versus the oracle, and 1e-6 * sum|terms| versus an fp64 sum of the same
+    fp32 terms (the GPU accumulates in fp64).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import assert_close, assert_within, host, strict_ok, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(r, shape, scale=1.0, offset=0.0):
+    n, c, h, w = shape
+    x = (r.standard_normal(shape) * scale + offset).astype(np.float32)
+    gamma = r.uniform(0.5, 1.5, c).astype(np.float32)
+    beta = r.uniform(-0.1, 0.1, c).astype(np.float32)
+    g = r.standard_normal(shape).astype(np.float32)
+    return x, gamma, beta, g
+
+
+def _run(module, dev, x, gamma, beta, g, rm, rv, momentum=0.1, eps=1e-5):
+    c = x.shape[1]
+    dx_, dw_, db_, dg_ = to_dev(x, dev), to_dev(gamma, dev), to_dev(beta, dev), to_dev(g, dev)
+    drm, drv = to_dev(rm, dev), to_dev(rv, dev)
+    y = torch.empty_like(dx_)
+    mean, inv = torch.empty(c, device=dev), torch.empty(c, device=dev)
+    module.batch_norm_forward_train(dx_, dw_, db_, drm, drv, mean, inv, y, momentum, eps)
+    gx = torch.empty_like(dx_)
+    gw, gb = torch.empty(c, device=dev), torch.empty(c, device=dev)
+    module.batch_norm_backward_train(dg_, dx_, dw_, mean, inv, gx, gw, gb)
+    torch.cuda.synchronize()
+    return {k: host(v) for k, v in dict(y=y, mean=mean, inv=inv, rm=drm, rv=drv, dx=gx, dw=gw,
+                                        db=gb).items()}
+
+
+def _check(out, x, gamma, beta, g, rm, rv, momentum=0.1, eps=1e-5):
+    y, mean, inv, rm1, rv1 = oracle.bn_forward(x, gamma, beta, rm, rv, True, momentum, eps)
+    dx, dw, db = oracle.bn_backward(g, x, gamma, mean, inv, True)
+    n, c, h, w = x.shape
+    assert_close(out["mean"], mean, what="mean")
+    assert_close(out["inv"], inv, what="inverse std")
+    assert_close(out["rm"], rm1, what="running mean")
+    assert_close(out["rv"], rv1, what="running var")
+    cb = lambda v: v.reshape(1, c, 1, 1)  # noqa: E731
+    # y = ((x - mean) * inv) * w + b: bound by the magnitudes of its two terms
+    y_terms = np.abs((x - cb(mean)) * cb(inv) * cb(gamma)) + np.abs(cb(beta))
+    ok = strict_ok(out["y"], y)
+    if not ok.all():
+        assert_within(out["y"], y, np.maximum(1e-5 * y_terms, 1e-6), "y")
+    # dx terms: (w*inv/M) * (M*g, sum g, x_hat * sum g x_hat)
+    m_ = n * h * w
+    xhat = (x - cb(mean)) * cb(inv)
+    coef = np.abs(cb(gamma * inv / np.float32(m_)))
+    dx_terms = coef * (m_ * np.abs(g) + np.abs(cb(db)) + np.abs(xhat * cb(dw)))
+    ok = strict_ok(out["dx"], dx)
+    if not ok.all():
+        assert_within(out["dx"], dx, np.maximum(1e-5 * dx_terms, 1e-6), "dx")
+    # channel sums: conditioning bound vs the oracle and a tight bound vs fp64 of the same terms
+    sum_abs_g = np.abs(g.astype(np.float64)).sum(axis=(0, 2, 3))
+    gx32 = (g * ((x - cb(out["mean"])) * cb(out["inv"]))).astype(np.float32)
+    sum_abs_gx = np.abs(gx32.astype(np.float64)).sum(axis=(0, 2, 3))
+    assert_within(out["db"], db, 1e-5 * sum_abs_g + 1e-6, "dbias vs oracle")
+    assert_within(out["dw"], dw, 1e-5 * sum_abs_gx + 1e-6, "dweight vs oracle")
+    assert_within(out["db"], g.astype(np.float64).sum(axis=(0, 2, 3)),
+                  1e-6 * sum_abs_g + 1e-7, "dbias vs fp64")
+    assert_within(out["dw"], gx32.astype(np.float64).sum(axis=(0, 2, 3)),
+                  1e-6 * sum_abs_gx + 1e-7, "dweight vs fp64")
+    return dict(y=strict_ok(out["y"], y).mean(), dx=strict_ok(out["dx"], dx).mean(),
+                dw=strict_ok(out["dw"], dw).mean(), db=strict_ok(out["db"], db).mean())
+
+
+SHAPES = [
+    (2, 3, 4, 4),      # vector path, tiny
+    (5, 4, 7, 7),      # spatial 49: scalar path
+    (3, 2, 1, 1),      # reference KAT shape
+    (1, 3, 1, 9),      # batch 1
+    (7, 16, 14, 14),   # spatial 196
+    (128, 32, 14, 14), # config 5's largest BN tensor
+    (4, 300, 3, 5),    # many channels, odd spatial
+    (2, 1, 256, 256),  # one channel, many slices
+]
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+def test_batch_norm_train_matches_oracle(module, dev, shape):
+    r = np.random.default_rng(hash(shape) & 0xFFFFFFFF)
+    x, gamma, beta, g = _case(r, shape, 1.7, 0.3)
+    c = shape[1]
+    rm = r.uniform(-0.5, 0.5, c).astype(np.float32)
+    rv = r.uniform(0.5, 2.0, c).astype(np.float32)
+    out = _run(module, dev, x, gamma, beta, g, rm, rv)
+    _check(out, x, gamma, beta, g, rm, rv)
+
+
+def test_batch_norm_large_mean_small_std(module, dev):
+    """|mean| >> std: the shifted fp64 accumulation keeps the variance accurate."""
+    r = np.random.default_rng(7)
+    x, gamma, beta, g = _case(r, (8, 4, 16, 16), scale=0.01, offset=100.0)
+    rm, rv = np.zeros(4, np.float32), np.ones(4, np.float32)
+    out = _run(module, dev, x, gamma, beta, g, rm, rv)
+    _check(out, x, gamma, beta, g, rm, rv)
+
+
+def test_batch_norm_config2_full_shape(module, dev):
+    """Config 2: [64, 128, 56, 56], x ~ N(0,1), gamma ~ U(0.5,1.5), beta ~ U(-0.1,0.1),
+    g ~ N(0,1), running (0, 1), momentum 0.1, eps 1e-5."""
+    r = np.random.default_rng(0x6F78696400000002)
+    shape = (64, 128, 56, 56)
+    x, gamma, beta, g = _case(r, shape)
+    rm, rv = np.zeros(128, np.float32), np.ones(128, np.float32)
+    out = _run(module, dev, x, gamma, beta, g, rm, rv)
+    frac = _check(out, x, gamma, beta, g, rm, rv)
+    print("config 2 strict-criterion pass fractions:", frac)
+    assert frac["y"] > 0.999 and frac["dx"] > 0.999
+
+
+def test_batch_norm_reference_kats(module, dev):
+    """nn.rs:761-790: running mean [0.4, 0.5] after one step, output channel mean ~0."""
+    x = np.array([1, 3, 2, 4, 5, 7, 6, 8], np.float32).reshape(2, 2, 1, 2)
+    ones, zeros = np.ones(2, np.float32), np.zeros(2, np.float32)
+    out = _run(module, dev, x, ones, zeros, np.ones_like(x), zeros, ones)
+    assert np.all(np.abs(out["rm"] - [0.4, 0.5]) < 1e-5)
+    assert out["rv"][0] > 1.0
+    for ch in range(2):
+        assert abs(out["y"][:, ch].mean()) < 1e-5
+    # jit.rs:763-782: batch statistics are recomputed on every run
+    for run in ([1.0, 3.0], [10.0, 20.0]):
+        x1 = np.array(run, np.float32).reshape(1, 1, 1, 2)
+        o = _run(module, dev, x1, np.ones(1, np.float32), np.zeros(1, np.float32),
+                 np.ones_like(x1), np.zeros(1, np.float32), np.ones(1, np.float32))
+        assert np.all(np.abs(o["y"].ravel() - [-1.0, 1.0]) < 1e-4)
+
+
+def test_batch_norm_single_entry_points(module, dev):
+    """The reference's separate kernels: statistics, update_running, running_inverse_std,
+    apply, affine_backward and input_backward (train and eval)."""
+    r = np.random.default_rng(11)
+    shape = (6, 5, 8, 8)
+    n, c, h, w = shape
+    x, gamma, beta, g = _case(r, shape, 2.0, -0.5)
+    dx_, dgam, dbet, dg_ = (to_dev(a, dev) for a in (x, gamma, beta, g))
+    mean, inv, unb = (torch.empty(c, device=dev) for _ in range(3))
+    module.batch_norm_statistics(n, c, h * w, 1e-5, dx_, mean, inv, unb)
+    rm0 = to_dev(r.uniform(-1, 1, c).astype(np.float32), dev)
+    rv0 = to_dev(r.uniform(0.5, 2, c).astype(np.float32), dev)
+    rm1, rv1 = torch.empty_like(rm0), torch.empty_like(rv0)
+    module.batch_norm_update_running(0.1, mean, unb, rm0, rv0, rm1, rv1)
+    y = torch.empty_like(dx_)
+    module.batch_norm_apply(c, h * w, dx_, dgam, dbet, mean, inv, y)
+    gw, gb = torch.empty(c, device=dev), torch.empty(c, device=dev)
+    module.batch_norm_affine_backward(n, c, h * w, dg_, dx_, mean, inv, gw, gb)
+    gx = torch.empty_like(dx_)
+    module.batch_norm_input_backward(c, h * w, n * h * w, True, dg_, dx_, dgam, mean, inv, gw,
+                                     gb, gx)
+    torch.cuda.synchronize()
+    m_ref, inv_ref = oracle.bn_batch_statistics(x, 1e-5)
+    assert_close(host(mean), m_ref, what="mean")
+    assert_close(host(inv), inv_ref, what="inv")
+    _, _, _, rm_ref, rv_ref = oracle.bn_forward(x, gamma, beta, host(rm0), host(rv0))
+    assert_close(host(rm1), rm_ref, what="running mean")
+    assert_close(host(rv1), rv_ref, what="running var")
+    # unbiased variance: biased * M / (M - 1)
+    var64 = x.astype(np.float64).var(axis=(0, 2, 3))
+    np.testing.assert_allclose(host(unb), var64 * (n * h * w) / (n * h * w - 1), rtol=1e-5)
+    y_ref, *_ = oracle.bn_forward(x, gamma, beta, host(rm0), host(rv0))
+    assert_close(host(y), y_ref, atol=1e-5, what="apply")
+    dx_ref, dw_ref, db_ref = oracle.bn_backward(g, x, gamma, m_ref, inv_ref, True)
+    assert_close(host(gx), dx_ref, rtol=1e-4, atol=1e-5, what="input backward")
+    assert_close(host(gw), dw_ref, rtol=1e-4, atol=1e-4, what="weight grad")
+    assert_close(host(gb), db_ref, rtol=1e-4, atol=1e-4, what="bias grad")
+    # eval mode: running inverse std, apply with running stats, dx = g * w * inv
+    rinv = torch.empty(c, device=dev)
+    module.batch_norm_running_inverse_std(1e-5, rv0, rinv)
+    module.batch_norm_input_backward(c, h * w, n * h * w, False, dg_, dx_, dgam, rm0, rinv, gw,
+                                     gb, gx)
+    torch.cuda.synchronize()
+    assert_close(host(rinv), 1.0 / np.sqrt(host(rv0) + np.float32(1e-5)), what="running inv")
+    dx_eval, _, _ = oracle.bn_backward(g, x, gamma, host(rm0), host(rinv), False)
+    assert_close(host(gx), dx_eval, what="eval input backward")
+
+
+def test_batch_norm_workspace_reuse_and_repeat(module, dev):
+    """The reduction counters reset themselves: repeated calls give identical results."""
+    r = np.random.default_rng(3)
+    x, gamma, beta, g = _case(r, (16, 24, 10, 12))
+    rm, rv = np.zeros(24, np.float32), np.ones(24, np.float32)
+    first = _run(module, dev, x, gamma, beta, g, rm, rv)
+    for _ in range(3):
+        again = _run(module, dev, x, gamma, beta, g, rm, rv)
+        for k in first:
+            assert np.array_equal(first[k], again[k]), k

@@ -1,0 +1,100 @@
+"""Cross entropy (row log-softmax, mean NLL) forward / backward / fused on the GPU against the
+oracle (evaluation.rs:599-636, autograd.rs:529-554), from the reference KAT to config 3's
+[8192, 32768].
+
+Tolerance: the north star's max rel err 1e-5 (abs 1e-6 near zero).  Gradient entries are at
+most 1/B in magnitude, so an absolute floor of 1e-6 would be vacuous; the floor used here is
+1e-6 of the largest gradient magnitude (|outer| / B), far tighter."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import assert_close, host, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(module, dev, logits, targets, outer=1.0, mode="fused"):
+    b, k = logits.shape
+    dl, dt = to_dev(logits, dev), to_dev(targets, dev)
+    douter = torch.full((1,), outer, device=dev)
+    loss = torch.full((1,), np.nan, device=dev)
+    grad = torch.full_like(dl, np.nan)
+    flag = torch.zeros(1, dtype=torch.int32, device=dev)
+    if mode == "fused":
+        module.cross_entropy_forward_backward(b, k, dl, dt, douter, loss, grad, flag)
+    else:
+        module.cross_entropy_forward(b, k, dl, dt, loss, flag)
+        module.cross_entropy_backward(b, k, dl, dt, douter, grad, flag)
+    torch.cuda.synchronize()
+    return float(host(loss)[0]), host(grad), int(host(flag)[0])
+
+
+def _check(loss, grad, logits, targets, outer=1.0):
+    b = logits.shape[0]
+    loss_ref = oracle.ce_forward(logits, targets)
+    grad_ref = oracle.ce_backward(logits, targets, outer)
+    assert_close(np.float32(loss), np.float32(loss_ref), what="loss")
+    assert_close(grad, grad_ref, rtol=1e-5, atol=1e-6 * abs(outer) / b, what="grad")
+
+
+@pytest.mark.parametrize("shape", [(2, 2), (4, 7), (3, 1000), (2, 1), (128, 10), (5, 4096),
+                                   (3, 8192), (2, 32768), (2, 65536), (2, 70000), (1, 4),
+                                   (300, 260)])
+@pytest.mark.parametrize("mode", ["fused", "separate"])
+def test_cross_entropy_matches_oracle(module, dev, shape, mode):
+    r = np.random.default_rng(shape[0] * 100003 + shape[1])
+    logits = (r.standard_normal(shape) * 2).astype(np.float32)
+    targets = r.integers(0, shape[1], shape[0]).astype(np.float32)
+    loss, grad, flag = _run(module, dev, logits, targets, 0.75, mode)
+    assert flag == 0
+    _check(loss, grad, logits, targets, 0.75)
+
+
+def test_cross_entropy_reference_kat(module, dev):
+    """tensor/mod.rs:616-625: zero logits [2, 2], targets [0, 1] -> loss ln 2, grad exact."""
+    logits = np.zeros((2, 2), np.float32)
+    loss, grad, flag = _run(module, dev, logits, np.array([0, 1], np.float32))
+    assert abs(loss - np.log(2.0)) < 1e-6 and flag == 0
+    assert grad.ravel().tolist() == [-0.25, 0.25, 0.25, -0.25]
+
+
+def test_cross_entropy_zero_logits_closed_form(module, dev):
+    b, k = 6, 1000
+    targets = np.array([0, 999, 5, 5, 17, 3], np.float32)
+    loss, grad, _ = _run(module, dev, np.zeros((b, k), np.float32), targets)
+    assert abs(loss - np.log(k)) < 1e-5
+    expect = np.full((b, k), (1 / k) / b)
+    expect[np.arange(b), targets.astype(int)] -= 1 / b
+    np.testing.assert_allclose(grad, expect, rtol=1e-5, atol=1e-9)
+    np.testing.assert_allclose(grad.astype(np.float64).sum(axis=1), 0, atol=1e-7)
+
+
+@pytest.mark.parametrize("bad", [1.5, -1.0, np.nan, np.inf, 5.0, 1e30])
+def test_cross_entropy_invalid_target(module, dev, bad):
+    """CPU: Error::InvalidShape (evaluation.rs:622-636).  GPU: NaN loss / NaN row (as the
+    reference kernels write) and the error flag raised so the host can report it."""
+    logits = np.zeros((3, 5), np.float32)
+    targets = np.array([0, bad, 2], np.float32)
+    with pytest.raises(oracle.OracleError):
+        oracle.ce_forward(logits, targets)
+    for mode in ("fused", "separate"):
+        loss, grad, flag = _run(module, dev, logits, targets, mode=mode)
+        assert flag == 1 and np.isnan(loss)
+        assert np.isnan(grad[1]).all() and not np.isnan(grad[[0, 2]]).any()
+
+
+def test_cross_entropy_config3_full_shape(module, dev):
+    """Config 3: logits ~ N(0, 2) [8192, 32768], targets uniform in [0, 32768)."""
+    r = np.random.default_rng(0x6F78696400000003)
+    b, k = 8192, 32768
+    logits = (r.standard_normal((b, k), dtype=np.float32) * np.float32(2.0))
+    targets = r.integers(0, k, b).astype(np.float32)
+    loss, grad, flag = _run(module, dev, logits, targets)
+    assert flag == 0
+    _check(loss, grad, logits, targets)
+    # size-independent property: every gradient row sums to zero (softmax - onehot)
+    rows = grad.astype(np.float64).sum(axis=1)
+    assert np.abs(rows).max() < 1e-9
