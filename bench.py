@@ -1,8 +1,10 @@
 """Benchmark of the MI355X tensor hot path (liboxide_hip.so) -- one JSON line on stdout.
 
 Headline workload: BatchNorm2d training forward + backward, fp32
-NCHW [64, 128, 56, 56].  One step = statistics with running update, apply, affine backward
-(sum g, sum g*x_hat once) and input backward, launched through the C ABI on one stream.
+NCHW [64, 128, 56, 56].  One step = forward reduce (partial channel sums of x), forward apply (finalize
+mean / inverse std / running update + y), backward reduce (partial sums of g and g * x_hat,
+formed once) and backward input (finalize dweight / dbias + dx), launched through the C ABI on
+one stream.
 Algorithmic bytes per step: forward 3T + backward 5T, T = 102 760 448 B (x read by the
 statistics; x read + y written by apply; g, x read by the affine reduction; g, x read + dx
 written by the input backward).  ``value`` = 8T / step time in GB/s, inputs resident in HBM.
@@ -75,26 +77,25 @@ def bench_batch_norm(m, steps: int, warmup: int, sets: int = 4):
     s = torch.cuda.Stream()
     torch.cuda.synchronize()
 
-    names = ["bn_statistics_running", "bn_apply", "bn_affine_backward", "bn_input_backward"]
-    bytes_per = {"bn_statistics_running": T_BN, "bn_apply": 2 * T_BN,
-                 "bn_affine_backward": 2 * T_BN, "bn_input_backward": 3 * T_BN}
+    names = ["bn_forward_reduce", "bn_forward_apply", "bn_backward_reduce", "bn_backward_input"]
+    bytes_per = {"bn_forward_reduce": T_BN, "bn_forward_apply": 2 * T_BN,
+                 "bn_backward_reduce": 2 * T_BN, "bn_backward_input": 3 * T_BN}
 
     def step(i, ev=None):
         k = i % sets
         x, g, y, dx = xs[k], gs[k], ys[k], dxs[k]
         if ev:
             ev[0].record(s)
-        m.batch_norm_statistics_running(x, rm, rv, mean, inv, 0.1, 1e-5, stream=s)
+        m.batch_norm_forward_reduce(x, stream=s)
         if ev:
             ev[1].record(s)
-        m.batch_norm_apply(c, h * w, x, gamma, beta, mean, inv, y, stream=s)
+        m.batch_norm_forward_apply(x, gamma, beta, rm, rv, mean, inv, y, 0.1, 1e-5, stream=s)
         if ev:
             ev[2].record(s)
-        m.batch_norm_affine_backward(n, c, h * w, g, x, mean, inv, dw, db, stream=s)
+        m.batch_norm_backward_reduce(g, x, mean, inv, stream=s)
         if ev:
             ev[3].record(s)
-        m.batch_norm_input_backward(c, h * w, n * h * w, True, g, x, gamma, mean, inv, dw, db,
-                                    dx, stream=s)
+        m.batch_norm_backward_input(g, x, gamma, mean, inv, dx, dw, db, stream=s)
         if ev:
             ev[4].record(s)
 

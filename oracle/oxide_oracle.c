@@ -229,7 +229,8 @@ void oro_bn_backward(const float *grad, const float *x, uint64_t batch, uint64_t
 int oro_class_index(float value, uint64_t classes, uint64_t *index) {
   if (!isfinite(value) || value < 0.0f || (value - truncf(value)) != 0.0f)
     return ORO_INVALID_SHAPE;
-  uint64_t i = (uint64_t)value;
+  /* `value as usize` saturates: values at or above 2^64 become usize::MAX */
+  uint64_t i = value >= 18446744073709551616.0f ? UINT64_MAX : (uint64_t)value;
   if (i >= classes) return ORO_INVALID_SHAPE;
   *index = i;
   return ORO_OK;

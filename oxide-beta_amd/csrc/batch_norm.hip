@@ -7,19 +7,23 @@
 // 897-927 are one thread per element.  CPU semantics: evaluation.rs:490-597,
 // autograd.rs:315-383.
 //
-// Design (gfx950):
-//   * Reductions: grid (S slices, C channels).  Block (s, c) walks a contiguous slice of channel
-//     c's N*H*W values as 128-bit loads (the N planes of a channel lie C*H*W floats apart; the
+// Design (gfx950), two launches per direction, no inter-block synchronization:
+//   * Reduce: grid (S slices, C channels).  Block (s, c) walks a contiguous slice of channel
+//     c's N*H*W values with 128-bit loads (the N planes of a channel lie C*H*W floats apart; the
 //     float4 index within the channel is split into plane / offset with a multiply-high
-//     division), accumulates in fp64, reduces the block with wave64 shuffles and LDS, and writes
-//     one fp64 partial pair.  The last block of a channel to finish (device-scope counter) sums
-//     the S partials in fixed order and writes the per-channel results -- for the forward also
-//     the running-stat update -- then resets the counter, so the workspace stays zeroed.
-//   * Apply / input-backward: one streaming pass with 128-bit loads; per-channel values are
-//     gathered from L1-resident [C] vectors.
+//     division), accumulates in fp64, reduces the block with wave64 shuffles and LDS, and stores
+//     one fp64 partial pair to the workspace.  Forward partials are sums of (x - K) and
+//     (x - K)^2 with K = x[0, c, 0]; backward partials are sums of g and g * x_hat.
+//   * Map: every block of the streaming pass (apply or dx) first finalizes the statistics of
+//     the channels its planes belong to, summing that channel's S partials in a fixed order, so
+//     all blocks derive bit-identical values; the block holding plane (n = 0, c) also writes the
+//     per-channel outputs (saved mean / inverse std and the running update, or dweight /
+//     dbias).  Then it streams its planes with 128-bit loads, channel values from LDS.
+//     A kernel boundary separates reduce and map, so no fence or atomic is needed (on gfx950 an
+//     agent-scope release writes back the XCD's L2, far too costly per block).
 //   * Per-element arithmetic follows the CPU path's fp32 operation order exactly
 //     (-ffp-contract=off): y = ((x - mean) * inv) * w + b, x_hat = (x - mean) * inv,
-//     dx = ((w * inv) / M) * ((M * g - sum_g) - x_hat * sum_g_xhat).
+//     dx = ((w * inv) / M) * ((M * g - sum_g) - x_hat * sum_g_xhat), eval dx = (g * w) * inv.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -31,21 +35,20 @@ namespace {
 
 constexpr int kRedBlock = 256;  // 4 waves
 constexpr int kRedWaves = kRedBlock / 64;
+constexpr int kMapBlock = 256;
+constexpr uint32_t kMapElems = 4096;  // elements per map block (16 KiB per stream)
+constexpr uint32_t kMaxPlanes = 256;  // planes per map block (small spatial sizes)
+
+// ---------------------------------------------------------------- geometry
 
 struct Geometry {
   uint32_t batch, channels, spatial;
-  uint64_t samples;      // batch * spatial (values per channel)
-  uint32_t slices;       // S
-  uint64_t slice_len;    // values per slice (multiple of 4 on the vector path)
-  bool vec;              // spatial % 4 == 0 and pointers aligned
-  oxh::FastDiv spatial_div;   // divides a channel-relative index by spatial (or spatial / 4)
+  uint64_t samples;          // batch * spatial (values per channel)
+  uint32_t slices;           // S
+  uint64_t slice_len;        // values per slice (always a multiple of 4)
+  bool vec;                  // spatial % 4 == 0 and pointers aligned
+  oxh::FastDiv spatial_div;  // divides a channel-relative index by spatial (or spatial / 4)
 };
-
-// Workspace layout: double2 partial[C][S], then uint32 counter[C].
-inline uint64_t partial_bytes(uint64_t c, uint64_t s) { return c * s * 16; }
-inline uint64_t workspace_bytes_for(uint64_t c, uint64_t s) {
-  return ((partial_bytes(c, s) + c * 4) + 255) / 256 * 256;
-}
 
 uint32_t choose_slices(uint64_t channels, uint64_t samples) {
   // Aim for ~8 blocks per CU in total, but keep >= 4096 values per block.
@@ -56,6 +59,67 @@ uint32_t choose_slices(uint64_t channels, uint64_t samples) {
   if (s > 1024) s = 1024;
   if (s < 1) s = 1;
   return static_cast<uint32_t>(s);
+}
+
+// The slicing depends only on the shape (never on alignment), so the reduce and map kernels of
+// one operation always agree on S.
+Geometry make_geometry(uint64_t batch, uint64_t channels, uint64_t spatial, bool aligned) {
+  Geometry g{};
+  g.batch = static_cast<uint32_t>(batch);
+  g.channels = static_cast<uint32_t>(channels);
+  g.spatial = static_cast<uint32_t>(spatial);
+  g.samples = batch * spatial;
+  g.vec = aligned && spatial % 4 == 0;
+  const uint32_t s = choose_slices(channels, g.samples);
+  uint64_t len = (g.samples + s - 1) / s;
+  len = (len + 3) / 4 * 4;
+  g.slice_len = len;
+  g.slices = static_cast<uint32_t>((g.samples + len - 1) / len);  // drop empty slices
+  g.spatial_div = oxh::make_fastdiv(static_cast<uint32_t>(g.vec ? spatial / 4 : spatial));
+  return g;
+}
+
+uint64_t workspace_bytes_for(const Geometry &g) {
+  return (static_cast<uint64_t>(g.channels) * g.slices * 16 + 255) / 256 * 256;
+}
+
+// Map blocks: either a chunk of one plane (spatial >= kMapElems) or up to kMaxPlanes whole
+// planes (smaller spatial sizes).
+struct PlaneMap {
+  uint32_t channels, spatial;
+  uint64_t planes;            // batch * channels
+  uint32_t chunks;            // chunks per plane (> 0: chunk mode)
+  uint32_t chunk_len;         // elements per chunk (multiple of 4)
+  uint32_t planes_per_block;  // plane mode
+  bool vec;
+  oxh::FastDiv spatial_div;   // divides a block-relative element offset by spatial
+  uint64_t blocks;
+};
+
+PlaneMap make_plane_map(uint64_t batch, uint64_t channels, uint64_t spatial, bool aligned) {
+  PlaneMap m{};
+  m.channels = static_cast<uint32_t>(channels);
+  m.spatial = static_cast<uint32_t>(spatial);
+  m.planes = batch * channels;
+  m.vec = aligned && spatial % 4 == 0;
+  if (spatial >= kMapElems) {
+    uint32_t chunks = static_cast<uint32_t>((spatial + kMapElems - 1) / kMapElems);
+    uint64_t len = (spatial + chunks - 1) / chunks;
+    len = (len + 3) / 4 * 4;
+    m.chunk_len = static_cast<uint32_t>(len);
+    m.chunks = static_cast<uint32_t>((spatial + len - 1) / len);
+    m.planes_per_block = 1;
+    m.blocks = m.planes * m.chunks;
+  } else {
+    m.chunks = 0;
+    uint32_t ppb = static_cast<uint32_t>(kMapElems / spatial);
+    if (ppb > kMaxPlanes) ppb = kMaxPlanes;
+    if (ppb < 1) ppb = 1;
+    m.planes_per_block = ppb;
+    m.blocks = (m.planes + ppb - 1) / ppb;
+  }
+  m.spatial_div = oxh::make_fastdiv(m.spatial);
+  return m;
 }
 
 __device__ __forceinline__ double wave_sum(double v) {
@@ -85,72 +149,43 @@ __device__ __forceinline__ void block_sum2(double &a, double &b, double (*lds)[k
   }
 }
 
-// Called by thread 0 of every block after its partial is stored: returns true in exactly one
-// block per channel (the last to arrive), after which that block may read all partials.
-__device__ __forceinline__ bool arrive_last(uint32_t *counter, uint32_t expected) {
-  __threadfence();
-  const uint32_t prev =
-      __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-  const bool last = prev + 1 == expected;
-  if (last) {
-    __threadfence();
-    __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  return last;
-}
-
-// Address (in floats) of channel-relative value j of channel c.
+// Address (in floats or float4) of channel-relative value j of channel c.
 __device__ __forceinline__ uint64_t nchw_index(const Geometry &g, uint32_t c, uint32_t j) {
   const uint32_t n = oxh::fast_div(j, g.spatial_div);
   const uint32_t i = j - n * g.spatial_div.d;
   return (static_cast<uint64_t>(n) * g.channels + c) * g.spatial_div.d + i;
 }
 
-// ---------------------------------------------------------------- forward statistics
+// ---------------------------------------------------------------- reductions
 
-struct StatsOut {
-  float *mean, *inverse_std, *unbiased_variance;  // unbiased_variance may be null
-  float *running_mean, *running_variance;         // null: no running update
-  float momentum, epsilon;
-};
-
-__global__ __launch_bounds__(kRedBlock) void bn_stats_kernel(Geometry g, const float *__restrict__ x,
-                                                           StatsOut out, double2 *partial,
-                                                           uint32_t *counter) {
+// Forward partials: (sum (x - K), sum (x - K)^2), K = x[0, c, 0].
+__global__ __launch_bounds__(kRedBlock) void bn_reduce_x_kernel(Geometry g,
+                                                                const float *__restrict__ x,
+                                                                double2 *__restrict__ partial) {
   __shared__ double lds[2][kRedWaves];
-  __shared__ bool is_last;
   const uint32_t s = blockIdx.x, c = blockIdx.y;
-  // Shift by the channel's first value: sums of (x - K) and (x - K)^2 in fp64 keep the
-  // variance free of cancellation even when |mean| >> std.
-  const float shift = x[static_cast<uint64_t>(c) * g.spatial];
-  const double k = shift;
+  const double k = static_cast<double>(x[static_cast<uint64_t>(c) * g.spatial]);
   double sum = 0.0, sq = 0.0;
   const uint64_t begin = static_cast<uint64_t>(s) * g.slice_len;
-  uint64_t end = begin + g.slice_len;
-  if (end > g.samples) end = g.samples;
+  const uint64_t end = begin + g.slice_len < g.samples ? begin + g.slice_len : g.samples;
   if (g.vec) {
     const float4 *x4 = reinterpret_cast<const float4 *>(x);
-    const uint32_t b4 = static_cast<uint32_t>(begin / 4), e4 = static_cast<uint32_t>(end / 4);
-    uint32_t j = b4 + threadIdx.x;
+    const uint32_t e4 = static_cast<uint32_t>(end / 4);
+    uint32_t j = static_cast<uint32_t>(begin / 4) + threadIdx.x;
+    auto add4 = [&](const float4 &v) {
+      const double d0 = static_cast<double>(v.x) - k, d1 = static_cast<double>(v.y) - k;
+      const double d2 = static_cast<double>(v.z) - k, d3 = static_cast<double>(v.w) - k;
+      sum += (d0 + d1) + (d2 + d3);
+      sq += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+    };
     for (; j + 3 * kRedBlock < e4; j += 4 * kRedBlock) {
       float4 v[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) v[u] = x4[nchw_index(g, c, j + u * kRedBlock)];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const double d0 = static_cast<double>(v[u].x) - k, d1 = static_cast<double>(v[u].y) - k;
-        const double d2 = static_cast<double>(v[u].z) - k, d3 = static_cast<double>(v[u].w) - k;
-        sum += (d0 + d1) + (d2 + d3);
-        sq += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
-      }
+      for (int u = 0; u < 4; ++u) add4(v[u]);
     }
-    for (; j < e4; j += kRedBlock) {
-      const float4 v = x4[nchw_index(g, c, j)];
-      const double d0 = static_cast<double>(v.x) - k, d1 = static_cast<double>(v.y) - k;
-      const double d2 = static_cast<double>(v.z) - k, d3 = static_cast<double>(v.w) - k;
-      sum += (d0 + d1) + (d2 + d3);
-      sq += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
-    }
+    for (; j < e4; j += kRedBlock) add4(x4[nchw_index(g, c, j)]);
   } else {
     for (uint64_t j = begin + threadIdx.x; j < end; j += kRedBlock) {
       const double d = static_cast<double>(x[nchw_index(g, c, static_cast<uint32_t>(j))]) - k;
@@ -159,69 +194,27 @@ __global__ __launch_bounds__(kRedBlock) void bn_stats_kernel(Geometry g, const f
     }
   }
   block_sum2(sum, sq, lds);
-  if (threadIdx.x == 0) {
-    partial[static_cast<uint64_t>(c) * g.slices + s] = make_double2(sum, sq);
-    is_last = arrive_last(&counter[c], g.slices);
-  }
-  __syncthreads();
-  if (!is_last || threadIdx.x != 0) return;
-  // Last block of channel c: combine the slices in fixed order.
-  double total = 0.0, total_sq = 0.0;
-  for (uint32_t t = 0; t < g.slices; ++t) {
-    const double2 p = partial[static_cast<uint64_t>(c) * g.slices + t];
-    total += p.x;
-    total_sq += p.y;
-  }
-  const double m = static_cast<double>(g.samples);
-  const double mean_shifted = total / m;
-  double var = total_sq / m - mean_shifted * mean_shifted;
-  if (var < 0.0) var = 0.0;
-  const float mean_f = static_cast<float>(k + mean_shifted);
-  const float var_f = static_cast<float>(var);
-  // evaluation.rs:531-534: (variance + epsilon).sqrt().recip()
-  out.mean[c] = mean_f;
-  out.inverse_std[c] = 1.0f / sqrtf(var_f + out.epsilon);
-  // evaluation.rs:537-558: the running update recomputes the statistics with epsilon 0 and
-  // recovers the biased variance as inv_std.powi(-2) (== 1 / (inv * inv)), then applies the
-  // unbiased correction M / (M - 1) in fp32.
-  const float inv0 = 1.0f / sqrtf(var_f);
-  const float biased = 1.0f / (inv0 * inv0);
-  const float correction =
-      static_cast<float>(g.samples) / static_cast<float>(g.samples - 1);
-  if (out.unbiased_variance) out.unbiased_variance[c] = biased * correction;
-  if (out.running_mean) {
-    const float mom = out.momentum;
-    out.running_mean[c] = (1.0f - mom) * out.running_mean[c] + mom * mean_f;
-    out.running_variance[c] =
-        (1.0f - mom) * out.running_variance[c] + mom * biased * correction;
-  }
+  if (threadIdx.x == 0) partial[static_cast<uint64_t>(c) * g.slices + s] = make_double2(sum, sq);
 }
 
-// ---------------------------------------------------------------- backward affine reduction
-
-struct AffineOut {
-  float *weight_gradient, *bias_gradient;
-};
-
-__global__ __launch_bounds__(kRedBlock) void bn_affine_kernel(
+// Backward partials: (sum g, sum g * x_hat) with x_hat = (x - mean) * inv in fp32 and the
+// product g * x_hat rounded to fp32 as the CPU path forms it (autograd.rs:353-362).
+__global__ __launch_bounds__(kRedBlock) void bn_reduce_gx_kernel(
     Geometry g, const float *__restrict__ grad, const float *__restrict__ x,
-    const float *__restrict__ mean, const float *__restrict__ inverse_std, AffineOut out,
-    double2 *partial, uint32_t *counter) {
+    const float *__restrict__ mean, const float *__restrict__ inverse_std,
+    double2 *__restrict__ partial) {
   __shared__ double lds[2][kRedWaves];
-  __shared__ bool is_last;
   const uint32_t s = blockIdx.x, c = blockIdx.y;
   const float mu = mean[c], inv = inverse_std[c];
   double sg = 0.0, sgx = 0.0;
   const uint64_t begin = static_cast<uint64_t>(s) * g.slice_len;
-  uint64_t end = begin + g.slice_len;
-  if (end > g.samples) end = g.samples;
-  // autograd.rs:353-362: normalized = (x - mean) * inv (fp32); terms g and g * normalized.
+  const uint64_t end = begin + g.slice_len < g.samples ? begin + g.slice_len : g.samples;
   if (g.vec) {
     const float4 *x4 = reinterpret_cast<const float4 *>(x);
     const float4 *g4 = reinterpret_cast<const float4 *>(grad);
-    const uint32_t b4 = static_cast<uint32_t>(begin / 4), e4 = static_cast<uint32_t>(end / 4);
-    uint32_t j = b4 + threadIdx.x;
-    auto accumulate = [&](const float4 &xv, const float4 &gv) {
+    const uint32_t e4 = static_cast<uint32_t>(end / 4);
+    uint32_t j = static_cast<uint32_t>(begin / 4) + threadIdx.x;
+    auto add4 = [&](const float4 &xv, const float4 &gv) {
       const float n0 = (xv.x - mu) * inv, n1 = (xv.y - mu) * inv;
       const float n2 = (xv.z - mu) * inv, n3 = (xv.w - mu) * inv;
       sg += (static_cast<double>(gv.x) + static_cast<double>(gv.y)) +
@@ -238,11 +231,11 @@ __global__ __launch_bounds__(kRedBlock) void bn_affine_kernel(
         gv[u] = g4[idx];
       }
 #pragma unroll
-      for (int u = 0; u < 4; ++u) accumulate(xv[u], gv[u]);
+      for (int u = 0; u < 4; ++u) add4(xv[u], gv[u]);
     }
     for (; j < e4; j += kRedBlock) {
       const uint64_t idx = nchw_index(g, c, j);
-      accumulate(x4[idx], g4[idx]);
+      add4(x4[idx], g4[idx]);
     }
   } else {
     for (uint64_t j = begin + threadIdx.x; j < end; j += kRedBlock) {
@@ -254,155 +247,283 @@ __global__ __launch_bounds__(kRedBlock) void bn_affine_kernel(
     }
   }
   block_sum2(sg, sgx, lds);
-  if (threadIdx.x == 0) {
-    partial[static_cast<uint64_t>(c) * g.slices + s] = make_double2(sg, sgx);
-    is_last = arrive_last(&counter[c], g.slices);
+  if (threadIdx.x == 0) partial[static_cast<uint64_t>(c) * g.slices + s] = make_double2(sg, sgx);
+}
+
+// ---------------------------------------------------------------- finalization
+
+struct Moments {
+  float mean, inv, biased, correction;
+};
+
+// Channel statistics from its S forward partials, summed in slice order.
+__device__ __forceinline__ Moments forward_moments(const double2 *partial, uint32_t slices,
+                                                   uint32_t c, float shift, uint64_t samples,
+                                                   float epsilon) {
+  double total = 0.0, total_sq = 0.0;
+  for (uint32_t t = 0; t < slices; ++t) {
+    const double2 p = partial[static_cast<uint64_t>(c) * slices + t];
+    total += p.x;
+    total_sq += p.y;
+  }
+  const double m = static_cast<double>(samples);
+  const double mean_shifted = total / m;
+  double var = total_sq / m - mean_shifted * mean_shifted;
+  if (var < 0.0) var = 0.0;
+  Moments r;
+  r.mean = static_cast<float>(static_cast<double>(shift) + mean_shifted);
+  const float var_f = static_cast<float>(var);
+  // evaluation.rs:531-534: (variance + epsilon).sqrt().recip()
+  r.inv = 1.0f / sqrtf(var_f + epsilon);
+  // evaluation.rs:537-558: the running update recomputes the statistics with epsilon 0 and
+  // recovers the biased variance as inv_std.powi(-2) (== 1 / (inv * inv)); the unbiased
+  // correction M / (M - 1) is formed in fp32.
+  const float inv0 = 1.0f / sqrtf(var_f);
+  r.biased = 1.0f / (inv0 * inv0);
+  r.correction = static_cast<float>(samples) / static_cast<float>(samples - 1);
+  return r;
+}
+
+__device__ __forceinline__ void backward_sums(const double2 *partial, uint32_t slices,
+                                              uint32_t c, float &sum_g, float &sum_gx) {
+  double a = 0.0, b = 0.0;
+  for (uint32_t t = 0; t < slices; ++t) {
+    const double2 p = partial[static_cast<uint64_t>(c) * slices + t];
+    a += p.x;
+    b += p.y;
+  }
+  sum_g = static_cast<float>(a);
+  sum_gx = static_cast<float>(b);
+}
+
+struct StatsOut {
+  float *mean, *inverse_std, *unbiased_variance;  // unbiased_variance may be null
+  float *running_mean, *running_variance;         // null: no running update
+  float momentum, epsilon;
+};
+
+__device__ __forceinline__ void write_forward_outputs(const StatsOut &o, uint32_t c,
+                                                      const Moments &r) {
+  o.mean[c] = r.mean;
+  o.inverse_std[c] = r.inv;
+  if (o.unbiased_variance) o.unbiased_variance[c] = r.biased * r.correction;
+  if (o.running_mean) {
+    const float mom = o.momentum;
+    o.running_mean[c] = (1.0f - mom) * o.running_mean[c] + mom * r.mean;
+    o.running_variance[c] = (1.0f - mom) * o.running_variance[c] + mom * r.biased * r.correction;
+  }
+}
+
+// One thread per channel: the reference's separate statistics output (no consumer kernel).
+__global__ void bn_finalize_forward_kernel(Geometry g, const float *__restrict__ x,
+                                           const double2 *__restrict__ partial, StatsOut out) {
+  const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= g.channels) return;
+  const float shift = x[static_cast<uint64_t>(c) * g.spatial];
+  write_forward_outputs(out, c,
+                        forward_moments(partial, g.slices, c, shift, g.samples, out.epsilon));
+}
+
+__global__ void bn_finalize_affine_kernel(Geometry g, const double2 *__restrict__ partial,
+                                          float *weight_gradient, float *bias_gradient) {
+  const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= g.channels) return;
+  float sg, sgx;
+  backward_sums(partial, g.slices, c, sg, sgx);
+  weight_gradient[c] = sgx;
+  bias_gradient[c] = sg;
+}
+
+// ---------------------------------------------------------------- map passes
+
+// Per-plane channel values cached in LDS (V floats per plane).
+template <int V>
+struct Cache {
+  float v[V][kMaxPlanes];
+};
+
+// Forward apply.  Channel values: mean, inv, w, b.  Statistics come from the partials
+// (finalize + apply) or from mean / inverse_std arrays (the reference's separate apply).
+struct ApplyPhase {
+  static constexpr int V = 4, NI = 1;
+  struct Args {
+    const float *x, *weight, *bias;
+    const float *mean, *inverse_std;  // used when partial == null
+    const double2 *partial;
+    uint32_t slices;
+    uint64_t samples;
+    StatsOut out;  // written by the block holding plane (0, c) when partial != null
+    float *y;
+  };
+  __device__ static void channel(const Args &a, const PlaneMap &m, uint32_t c, bool designated,
+                                 Cache<V> &cache, uint32_t k) {
+    float mu, inv;
+    if (a.partial) {
+      const float shift = a.x[static_cast<uint64_t>(c) * m.spatial];
+      const Moments r =
+          forward_moments(a.partial, a.slices, c, shift, a.samples, a.out.epsilon);
+      if (designated) write_forward_outputs(a.out, c, r);
+      mu = r.mean;
+      inv = r.inv;
+    } else {
+      mu = a.mean[c];
+      inv = a.inverse_std[c];
+    }
+    cache.v[0][k] = mu;
+    cache.v[1][k] = inv;
+    cache.v[2][k] = a.weight[c];
+    cache.v[3][k] = a.bias[c];
+  }
+  __device__ static const float *input(const Args &a, int) { return a.x; }
+  __device__ static float *output(const Args &a) { return a.y; }
+  __device__ static float element(const Args &, const Cache<V> &cache, uint32_t k,
+                                  const float (&in)[NI]) {
+    // evaluation.rs:590-595
+    return (in[0] - cache.v[0][k]) * cache.v[1][k] * cache.v[2][k] + cache.v[3][k];
+  }
+};
+
+// Training input backward.  Channel values: mean, inv, (w * inv) / M, sum g, sum g * x_hat.
+struct DxTrainPhase {
+  static constexpr int V = 5, NI = 2;  // in[0] = g, in[1] = x
+  struct Args {
+    const float *grad, *x, *weight, *mean, *inverse_std;
+    const float *weight_gradient, *bias_gradient;  // used when partial == null
+    const double2 *partial;
+    uint32_t slices;
+    float samples;                                   // M in fp32 (autograd.rs:344-345)
+    float *out_weight_gradient, *out_bias_gradient;  // written when partial != null
+    float *dx;
+  };
+  __device__ static void channel(const Args &a, const PlaneMap &, uint32_t c, bool designated,
+                                 Cache<V> &cache, uint32_t k) {
+    float sg, sgx;
+    if (a.partial) {
+      backward_sums(a.partial, a.slices, c, sg, sgx);
+      if (designated) {
+        a.out_weight_gradient[c] = sgx;
+        a.out_bias_gradient[c] = sg;
+      }
+    } else {
+      sg = a.bias_gradient[c];
+      sgx = a.weight_gradient[c];
+    }
+    const float inv = a.inverse_std[c];
+    cache.v[0][k] = a.mean[c];
+    cache.v[1][k] = inv;
+    cache.v[2][k] = a.weight[c] * inv / a.samples;
+    cache.v[3][k] = sg;
+    cache.v[4][k] = sgx;
+  }
+  __device__ static const float *input(const Args &a, int i) { return i == 0 ? a.grad : a.x; }
+  __device__ static float *output(const Args &a) { return a.dx; }
+  __device__ static float element(const Args &a, const Cache<V> &cache, uint32_t k,
+                                  const float (&in)[NI]) {
+    // autograd.rs:367-373
+    const float normalized = (in[1] - cache.v[0][k]) * cache.v[1][k];
+    return cache.v[2][k] * (a.samples * in[0] - cache.v[3][k] - normalized * cache.v[4][k]);
+  }
+};
+
+// Eval input backward: dx = (g * w) * inv (autograd.rs:374-378).
+struct DxEvalPhase {
+  static constexpr int V = 2, NI = 1;
+  struct Args {
+    const float *grad, *weight, *inverse_std;
+    float *dx;
+  };
+  __device__ static void channel(const Args &a, const PlaneMap &, uint32_t c, bool,
+                                 Cache<V> &cache, uint32_t k) {
+    cache.v[0][k] = a.weight[c];
+    cache.v[1][k] = a.inverse_std[c];
+  }
+  __device__ static const float *input(const Args &a, int) { return a.grad; }
+  __device__ static float *output(const Args &a) { return a.dx; }
+  __device__ static float element(const Args &, const Cache<V> &cache, uint32_t k,
+                                  const float (&in)[NI]) {
+    return in[0] * cache.v[0][k] * cache.v[1][k];
+  }
+};
+
+template <class P>
+__global__ __launch_bounds__(kMapBlock) void bn_map_kernel(PlaneMap m, typename P::Args a) {
+  __shared__ Cache<P::V> cache;
+  const uint64_t b = blockIdx.x;
+  uint64_t plane0, e0, e1;
+  uint32_t nplanes;
+  bool first_chunk;
+  if (m.chunks > 0) {
+    plane0 = b / m.chunks;
+    const uint32_t chunk = static_cast<uint32_t>(b - plane0 * m.chunks);
+    e0 = plane0 * m.spatial + static_cast<uint64_t>(chunk) * m.chunk_len;
+    const uint64_t plane_end = (plane0 + 1) * m.spatial;
+    e1 = e0 + m.chunk_len < plane_end ? e0 + m.chunk_len : plane_end;
+    nplanes = 1;
+    first_chunk = chunk == 0;
+  } else {
+    plane0 = b * m.planes_per_block;
+    const uint64_t last =
+        plane0 + m.planes_per_block < m.planes ? plane0 + m.planes_per_block : m.planes;
+    nplanes = static_cast<uint32_t>(last - plane0);
+    e0 = plane0 * m.spatial;
+    e1 = last * m.spatial;
+    first_chunk = true;
+  }
+  for (uint32_t k = threadIdx.x; k < nplanes; k += kMapBlock) {
+    const uint64_t plane = plane0 + k;
+    const uint32_t c = static_cast<uint32_t>(plane % m.channels);
+    P::channel(a, m, c, first_chunk && plane < m.channels, cache, k);
   }
   __syncthreads();
-  if (!is_last || threadIdx.x != 0) return;
-  double total_g = 0.0, total_gx = 0.0;
-  for (uint32_t t = 0; t < g.slices; ++t) {
-    const double2 p = partial[static_cast<uint64_t>(c) * g.slices + t];
-    total_g += p.x;
-    total_gx += p.y;
-  }
-  out.weight_gradient[c] = static_cast<float>(total_gx);
-  out.bias_gradient[c] = static_cast<float>(total_g);
-}
-
-// ---------------------------------------------------------------- elementwise passes
-
-struct ChannelMap {
-  uint64_t total;        // batch * channels * spatial
-  oxh::FastDiv plane;    // divides an element (or float4) index by spatial (or spatial / 4)
-  oxh::FastDiv channel;  // divides a plane index by channels
-  bool vec;
-};
-
-__device__ __forceinline__ uint32_t channel_of(const ChannelMap &m, uint32_t idx) {
-  const uint32_t p = oxh::fast_div(idx, m.plane);
-  return p - oxh::fast_div(p, m.channel) * m.channel.d;
-}
-
-// 64-bit element indices: the plane index of element e is e / spatial; only the plane index is
-// taken through the 32-bit divider, so totals up to 2^31 planes are supported.
-__device__ __forceinline__ uint32_t channel_of64(const ChannelMap &m, uint64_t idx) {
-  const uint64_t p = idx / m.plane.d;
-  return static_cast<uint32_t>(p % m.channel.d);
-}
-
-struct ApplyArgs {
-  const float *x, *weight, *bias, *mean, *inverse_std;
-  float *y;
-};
-
-__device__ __forceinline__ float bn_apply1(float v, float mu, float inv, float w, float b) {
-  return (v - mu) * inv * w + b;
-}
-
-constexpr int kMapUnroll = 4;
-
-__global__ __launch_bounds__(oxh::kBlock) void bn_apply_kernel(ChannelMap m, ApplyArgs a) {
-  const uint64_t tile = static_cast<uint64_t>(oxh::kBlock) * kMapUnroll;
+  float *out = P::output(a);
   if (m.vec) {
-    const uint64_t n4 = m.total / 4;
-    const float4 *x4 = reinterpret_cast<const float4 *>(a.x);
-    float4 *y4 = reinterpret_cast<float4 *>(a.y);
-    for (uint64_t base = static_cast<uint64_t>(blockIdx.x) * tile; base < n4;
-         base += static_cast<uint64_t>(gridDim.x) * tile) {
-      float4 v[kMapUnroll];
-      uint32_t ch[kMapUnroll];
+    // e0 and e1 are multiples of 4: spatial % 4 == 0 and chunk_len % 4 == 0.
+    const uint32_t n4 = static_cast<uint32_t>((e1 - e0) / 4);
+    const float4 *in4[P::NI];
 #pragma unroll
-      for (int u = 0; u < kMapUnroll; ++u) {
-        const uint64_t q = base + threadIdx.x + u * oxh::kBlock;
+    for (int i = 0; i < P::NI; ++i)
+      in4[i] = reinterpret_cast<const float4 *>(P::input(a, i) + e0);
+    float4 *out4 = reinterpret_cast<float4 *>(out + e0);
+    for (uint32_t base = 0; base < n4; base += 4 * kMapBlock) {
+      float4 v[4][P::NI];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t q = base + threadIdx.x + u * kMapBlock;
         if (q < n4) {
-          v[u] = x4[q];
-          ch[u] = channel_of(m, static_cast<uint32_t>(q));
+#pragma unroll
+          for (int i = 0; i < P::NI; ++i) v[u][i] = in4[i][q];
         }
       }
 #pragma unroll
-      for (int u = 0; u < kMapUnroll; ++u) {
-        const uint64_t q = base + threadIdx.x + u * oxh::kBlock;
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t q = base + threadIdx.x + u * kMapBlock;
         if (q < n4) {
-          const uint32_t c = ch[u];
-          const float mu = a.mean[c], inv = a.inverse_std[c], w = a.weight[c], b = a.bias[c];
+          const uint32_t k = m.chunks > 0 ? 0u : oxh::fast_div(q * 4, m.spatial_div);
+          float x0[P::NI], x1[P::NI], x2[P::NI], x3[P::NI];
+#pragma unroll
+          for (int i = 0; i < P::NI; ++i) {
+            x0[i] = v[u][i].x;
+            x1[i] = v[u][i].y;
+            x2[i] = v[u][i].z;
+            x3[i] = v[u][i].w;
+          }
           float4 r;
-          r.x = bn_apply1(v[u].x, mu, inv, w, b);
-          r.y = bn_apply1(v[u].y, mu, inv, w, b);
-          r.z = bn_apply1(v[u].z, mu, inv, w, b);
-          r.w = bn_apply1(v[u].w, mu, inv, w, b);
-          y4[q] = r;
+          r.x = P::element(a, cache, k, x0);
+          r.y = P::element(a, cache, k, x1);
+          r.z = P::element(a, cache, k, x2);
+          r.w = P::element(a, cache, k, x3);
+          out4[q] = r;
         }
       }
     }
   } else {
-    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
-    for (uint64_t e = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < m.total;
-         e += stride) {
-      const uint32_t c = channel_of64(m, e);
-      a.y[e] = bn_apply1(a.x[e], a.mean[c], a.inverse_std[c], a.weight[c], a.bias[c]);
-    }
-  }
-}
-
-struct InputBackwardArgs {
-  const float *grad, *x, *weight, *mean, *inverse_std, *weight_gradient, *bias_gradient;
-  float *dx;
-  float samples;  // M as fp32 (autograd.rs:344-345)
-  bool training;
-};
-
-__device__ __forceinline__ float bn_dx1(const InputBackwardArgs &a, uint32_t c, float g,
-                                        float v) {
-  const float w = a.weight[c], inv = a.inverse_std[c];
-  if (!a.training) return g * w * inv;  // autograd.rs:374-378
-  const float normalized = (v - a.mean[c]) * inv;
-  // autograd.rs:367-373
-  return w * inv / a.samples *
-         (a.samples * g - a.bias_gradient[c] - normalized * a.weight_gradient[c]);
-}
-
-__global__ __launch_bounds__(oxh::kBlock) void bn_input_backward_kernel(ChannelMap m,
-                                                                        InputBackwardArgs a) {
-  const uint64_t tile = static_cast<uint64_t>(oxh::kBlock) * kMapUnroll;
-  if (m.vec) {
-    const uint64_t n4 = m.total / 4;
-    const float4 *x4 = reinterpret_cast<const float4 *>(a.x);
-    const float4 *g4 = reinterpret_cast<const float4 *>(a.grad);
-    float4 *d4 = reinterpret_cast<float4 *>(a.dx);
-    for (uint64_t base = static_cast<uint64_t>(blockIdx.x) * tile; base < n4;
-         base += static_cast<uint64_t>(gridDim.x) * tile) {
-      float4 xv[kMapUnroll], gv[kMapUnroll];
-      uint32_t ch[kMapUnroll];
+    const uint32_t n = static_cast<uint32_t>(e1 - e0);
+    for (uint32_t q = threadIdx.x; q < n; q += kMapBlock) {
+      const uint32_t k = m.chunks > 0 ? 0u : oxh::fast_div(q, m.spatial_div);
+      float x[P::NI];
 #pragma unroll
-      for (int u = 0; u < kMapUnroll; ++u) {
-        const uint64_t q = base + threadIdx.x + u * oxh::kBlock;
-        if (q < n4) {
-          gv[u] = g4[q];
-          if (a.training) xv[u] = x4[q];
-          ch[u] = channel_of(m, static_cast<uint32_t>(q));
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < kMapUnroll; ++u) {
-        const uint64_t q = base + threadIdx.x + u * oxh::kBlock;
-        if (q < n4) {
-          const uint32_t c = ch[u];
-          float4 r;
-          r.x = bn_dx1(a, c, gv[u].x, xv[u].x);
-          r.y = bn_dx1(a, c, gv[u].y, xv[u].y);
-          r.z = bn_dx1(a, c, gv[u].z, xv[u].z);
-          r.w = bn_dx1(a, c, gv[u].w, xv[u].w);
-          d4[q] = r;
-        }
-      }
-    }
-  } else {
-    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
-    for (uint64_t e = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < m.total;
-         e += stride) {
-      const uint32_t c = channel_of64(m, e);
-      a.dx[e] = bn_dx1(a, c, a.grad[e], a.training ? a.x[e] : 0.0f);
+      for (int i = 0; i < P::NI; ++i) x[i] = P::input(a, i)[e0 + q];
+      out[e0 + q] = P::element(a, cache, k, x);
     }
   }
 }
@@ -431,52 +552,21 @@ oxh_status check_shape(const char *name, uint64_t batch, uint64_t channels, uint
   OXH_REQUIRE(batch > 0 && channels > 0 && spatial > 0, OXH_INVALID_SHAPE,
               std::string(name) + ": empty NCHW shape");
   OXH_REQUIRE(batch < (1ull << 31) && channels <= 65535 && spatial < (1ull << 31),
-              OXH_INVALID_SHAPE, std::string(name) + ": dimension too large (channels <= 65535)");
+              OXH_INVALID_SHAPE,
+              std::string(name) + ": dimension too large (channels <= 65535)");
   OXH_REQUIRE(batch * spatial < (1ull << 31), OXH_INVALID_SHAPE,
               std::string(name) + ": more than 2^31 values per channel");
   OXH_REQUIRE(batch * channels * spatial < (1ull << 40), OXH_INVALID_SHAPE,
               std::string(name) + ": tensor too large");
+  const PlaneMap m = make_plane_map(batch, channels, spatial, false);
+  OXH_REQUIRE(m.blocks < (1ull << 31), OXH_INVALID_SHAPE,
+              std::string(name) + ": too many planes");
   return oxh::ok();
 }
 
-Geometry make_geometry(uint64_t batch, uint64_t channels, uint64_t spatial, bool aligned) {
-  Geometry g{};
-  g.batch = static_cast<uint32_t>(batch);
-  g.channels = static_cast<uint32_t>(channels);
-  g.spatial = static_cast<uint32_t>(spatial);
-  g.samples = batch * spatial;
-  g.vec = aligned && spatial % 4 == 0;
-  g.slices = choose_slices(channels, g.samples);
-  uint64_t len = (g.samples + g.slices - 1) / g.slices;
-  if (g.vec) len = (len + 3) / 4 * 4;
-  g.slice_len = len;
-  // Slices that would start past the end are dropped.
-  g.slices = static_cast<uint32_t>((g.samples + len - 1) / len);
-  g.spatial_div = oxh::make_fastdiv(static_cast<uint32_t>(g.vec ? spatial / 4 : spatial));
-  return g;
-}
-
-ChannelMap make_channel_map(uint64_t batch, uint64_t channels, uint64_t spatial, bool aligned) {
-  ChannelMap m{};
-  m.total = batch * channels * spatial;
-  m.vec = aligned && spatial % 4 == 0 && m.total / 4 < (1ull << 31);
-  m.plane = oxh::make_fastdiv(static_cast<uint32_t>(m.vec ? spatial / 4 : spatial));
-  m.channel = oxh::make_fastdiv(static_cast<uint32_t>(channels));
-  return m;
-}
-
-uint32_t map_grid(const ChannelMap &m) {
-  const uint64_t units = m.vec ? m.total / 4 : m.total;
-  const uint64_t per_block = static_cast<uint64_t>(oxh::kBlock) * (m.vec ? kMapUnroll : 1);
-  uint64_t grid = (units + per_block - 1) / per_block;
-  if (grid < 1) grid = 1;
-  if (grid > (1u << 20)) grid = 1u << 20;
-  return static_cast<uint32_t>(grid);
-}
-
-oxh_status check_workspace(const char *name, const Geometry &g, void *workspace,
+oxh_status check_workspace(const char *name, const Geometry &g, const void *workspace,
                            uint64_t bytes) {
-  const uint64_t need = workspace_bytes_for(g.channels, g.slices);
+  const uint64_t need = workspace_bytes_for(g);
   OXH_REQUIRE(workspace != nullptr && bytes >= need, OXH_INVALID_SHAPE,
               std::string(name) + ": workspace of " + std::to_string(need) +
                   " bytes required (oxh_batch_norm_workspace_size)");
@@ -485,78 +575,63 @@ oxh_status check_workspace(const char *name, const Geometry &g, void *workspace,
   return oxh::ok();
 }
 
-oxh_status launch_stats(const char *name, oxh_stream stream, uint64_t batch, uint64_t channels,
-                        uint64_t spatial, const float *input, const StatsOut &out,
-                        void *workspace, uint64_t workspace_bytes) {
+oxh_status no_overlap(const char *name, const void *out, uint64_t out_bytes,
+                      std::initializer_list<const void *> ins, uint64_t in_bytes) {
+  for (const void *in : ins)
+    if (in) OXH_REQUIRE(!oxh::any_overlap(out, out_bytes, in, in_bytes), OXH_INVALID_SHAPE,
+                        std::string(name) + ": output overlaps an input");
+  return oxh::ok();
+}
+
+oxh_status launch_reduce_x(const char *name, oxh_stream stream, uint64_t batch,
+                           uint64_t channels, uint64_t spatial, const float *input,
+                           void *workspace, uint64_t workspace_bytes, Geometry *geometry) {
   oxh_status st = check_shape(name, batch, channels, spatial);
   if (st != OXH_OK) return st;
   OXH_REQUIRE(batch * spatial > 1, OXH_EXECUTION,
               "BatchNorm training requires more than one value per channel");
-  OXH_REQUIRE(input && out.mean && out.inverse_std, OXH_INVALID_SHAPE,
-              std::string(name) + ": null pointer");
+  OXH_REQUIRE(input != nullptr, OXH_INVALID_SHAPE, std::string(name) + ": null input");
   const Geometry g = make_geometry(batch, channels, spatial, oxh::aligned16(input));
   st = check_workspace(name, g, workspace, workspace_bytes);
   if (st != OXH_OK) return st;
-  auto *partial = static_cast<double2 *>(workspace);
-  auto *counter = reinterpret_cast<uint32_t *>(static_cast<char *>(workspace) +
-                                               partial_bytes(g.channels, g.slices));
-  hipLaunchKernelGGL(bn_stats_kernel, dim3(g.slices, g.channels), dim3(kRedBlock), 0,
-                     oxh::as_stream(stream), g, input, out, partial, counter);
+  OXH_REQUIRE(!oxh::any_overlap(workspace, workspace_bytes_for(g), input,
+                                batch * channels * spatial * 4),
+              OXH_INVALID_SHAPE, std::string(name) + ": workspace overlaps the input");
+  hipLaunchKernelGGL(bn_reduce_x_kernel, dim3(g.slices, g.channels), dim3(kRedBlock), 0,
+                     oxh::as_stream(stream), g, input, static_cast<double2 *>(workspace));
+  if (geometry) *geometry = g;
   return oxh::launched(name);
 }
 
-oxh_status launch_affine(const char *name, oxh_stream stream, uint64_t batch, uint64_t channels,
-                         uint64_t spatial, const float *gradient, const float *input,
-                         const float *mean, const float *inverse_std, float *weight_gradient,
-                         float *bias_gradient, void *workspace, uint64_t workspace_bytes) {
+oxh_status launch_reduce_gx(const char *name, oxh_stream stream, uint64_t batch,
+                            uint64_t channels, uint64_t spatial, const float *gradient,
+                            const float *input, const float *mean, const float *inverse_std,
+                            void *workspace, uint64_t workspace_bytes, Geometry *geometry) {
   oxh_status st = check_shape(name, batch, channels, spatial);
   if (st != OXH_OK) return st;
-  OXH_REQUIRE(gradient && input && mean && inverse_std && weight_gradient && bias_gradient,
-              OXH_INVALID_SHAPE, std::string(name) + ": null pointer");
+  OXH_REQUIRE(gradient && input && mean && inverse_std, OXH_INVALID_SHAPE,
+              std::string(name) + ": null pointer");
   const Geometry g = make_geometry(batch, channels, spatial,
                                    oxh::aligned16(input) && oxh::aligned16(gradient));
   st = check_workspace(name, g, workspace, workspace_bytes);
   if (st != OXH_OK) return st;
-  auto *partial = static_cast<double2 *>(workspace);
-  auto *counter = reinterpret_cast<uint32_t *>(static_cast<char *>(workspace) +
-                                               partial_bytes(g.channels, g.slices));
-  hipLaunchKernelGGL(bn_affine_kernel, dim3(g.slices, g.channels), dim3(kRedBlock), 0,
+  hipLaunchKernelGGL(bn_reduce_gx_kernel, dim3(g.slices, g.channels), dim3(kRedBlock), 0,
                      oxh::as_stream(stream), g, gradient, input, mean, inverse_std,
-                     AffineOut{weight_gradient, bias_gradient}, partial, counter);
+                     static_cast<double2 *>(workspace));
+  if (geometry) *geometry = g;
   return oxh::launched(name);
 }
 
-oxh_status launch_apply(const char *name, oxh_stream stream, uint64_t batch, uint64_t channels,
-                        uint64_t spatial, const ApplyArgs &a) {
-  oxh_status st = check_shape(name, batch, channels, spatial);
-  if (st != OXH_OK) return st;
-  OXH_REQUIRE(a.x && a.weight && a.bias && a.mean && a.inverse_std && a.y, OXH_INVALID_SHAPE,
-              std::string(name) + ": null pointer");
-  const uint64_t bytes = batch * channels * spatial * 4;
-  OXH_REQUIRE(!oxh::any_overlap(a.x, bytes, a.y, bytes) || a.x == a.y, OXH_INVALID_SHAPE,
-              std::string(name) + ": output partially overlaps the input");
-  const ChannelMap m = make_channel_map(batch, channels, spatial,
-                                        oxh::aligned16(a.x) && oxh::aligned16(a.y));
-  hipLaunchKernelGGL(bn_apply_kernel, dim3(map_grid(m)), dim3(oxh::kBlock), 0,
-                     oxh::as_stream(stream), m, a);
+template <class P>
+oxh_status launch_map(const char *name, oxh_stream stream, uint64_t batch, uint64_t channels,
+                      uint64_t spatial, bool aligned, const typename P::Args &a) {
+  const PlaneMap m = make_plane_map(batch, channels, spatial, aligned);
+  hipLaunchKernelGGL(bn_map_kernel<P>, dim3(static_cast<uint32_t>(m.blocks)), dim3(kMapBlock),
+                     0, oxh::as_stream(stream), m, a);
   return oxh::launched(name);
 }
 
-oxh_status launch_input_backward(const char *name, oxh_stream stream, uint64_t batch,
-                                 uint64_t channels, uint64_t spatial, const InputBackwardArgs &a) {
-  oxh_status st = check_shape(name, batch, channels, spatial);
-  if (st != OXH_OK) return st;
-  OXH_REQUIRE(a.grad && a.weight && a.inverse_std && a.dx, OXH_INVALID_SHAPE,
-              std::string(name) + ": null pointer");
-  OXH_REQUIRE(!a.training || (a.x && a.mean && a.weight_gradient && a.bias_gradient),
-              OXH_INVALID_SHAPE, std::string(name) + ": null pointer");
-  const bool aligned = oxh::aligned16(a.grad) && oxh::aligned16(a.dx) &&
-                       (!a.training || oxh::aligned16(a.x));
-  const ChannelMap m = make_channel_map(batch, channels, spatial, aligned);
-  hipLaunchKernelGGL(bn_input_backward_kernel, dim3(map_grid(m)), dim3(oxh::kBlock), 0,
-                     oxh::as_stream(stream), m, a);
-  return oxh::launched(name);
-}
+uint32_t channel_grid(uint64_t channels) { return static_cast<uint32_t>((channels + 255) / 256); }
 
 }  // namespace
 
@@ -567,12 +642,7 @@ oxh_status oxh_batch_norm_workspace_size(uint64_t batch, uint64_t channels, uint
   OXH_REQUIRE(bytes != nullptr, OXH_INVALID_SHAPE, "bytes is null");
   oxh_status st = check_shape("oxh_batch_norm_workspace_size", batch, channels, spatial);
   if (st != OXH_OK) return st;
-  // The slice count does not depend on alignment, so either geometry gives the same size.
-  const Geometry g = make_geometry(batch, channels, spatial, true);
-  const Geometry h = make_geometry(batch, channels, spatial, false);
-  const uint64_t a = workspace_bytes_for(g.channels, g.slices);
-  const uint64_t b = workspace_bytes_for(h.channels, h.slices);
-  *bytes = a > b ? a : b;
+  *bytes = workspace_bytes_for(make_geometry(batch, channels, spatial, true));
   return oxh::ok();
 }
 
@@ -580,9 +650,17 @@ oxh_status oxh_batch_norm_statistics(oxh_stream stream, uint64_t batch, uint64_t
                                      uint64_t spatial, float epsilon, const float *input,
                                      float *mean, float *inverse_std, float *unbiased_variance,
                                      void *workspace, uint64_t workspace_bytes) {
+  const char *name = "oxh_batch_norm_statistics";
+  OXH_REQUIRE(mean && inverse_std, OXH_INVALID_SHAPE, std::string(name) + ": null output");
+  Geometry g;
+  oxh_status st = launch_reduce_x(name, stream, batch, channels, spatial, input, workspace,
+                                  workspace_bytes, &g);
+  if (st != OXH_OK) return st;
   StatsOut out{mean, inverse_std, unbiased_variance, nullptr, nullptr, 0.0f, epsilon};
-  return launch_stats("oxh_batch_norm_statistics", stream, batch, channels, spatial, input, out,
-                      workspace, workspace_bytes);
+  hipLaunchKernelGGL(bn_finalize_forward_kernel, dim3(channel_grid(channels)), dim3(256), 0,
+                     oxh::as_stream(stream), g, input,
+                     static_cast<const double2 *>(workspace), out);
+  return oxh::launched(name);
 }
 
 oxh_status oxh_batch_norm_update_running(oxh_stream stream, uint64_t channels, float momentum,
@@ -590,14 +668,14 @@ oxh_status oxh_batch_norm_update_running(oxh_stream stream, uint64_t channels, f
                                          const float *old_mean, const float *old_variance,
                                          float *new_mean, float *new_variance) {
   if (channels == 0) return oxh::ok();
-  OXH_REQUIRE(channels < (1ull << 31), OXH_INVALID_SHAPE, "too many channels");
+  OXH_REQUIRE(channels <= 65535, OXH_INVALID_SHAPE, "too many channels");
   OXH_REQUIRE(batch_mean && batch_variance && old_mean && old_variance && new_mean &&
                   new_variance,
               OXH_INVALID_SHAPE, "oxh_batch_norm_update_running: null pointer");
-  const uint32_t grid = static_cast<uint32_t>((channels + 255) / 256);
-  hipLaunchKernelGGL(bn_update_running_kernel, dim3(grid), dim3(256), 0, oxh::as_stream(stream),
-                     static_cast<uint32_t>(channels), momentum, batch_mean, batch_variance,
-                     old_mean, old_variance, new_mean, new_variance);
+  hipLaunchKernelGGL(bn_update_running_kernel, dim3(channel_grid(channels)), dim3(256), 0,
+                     oxh::as_stream(stream), static_cast<uint32_t>(channels), momentum,
+                     batch_mean, batch_variance, old_mean, old_variance, new_mean,
+                     new_variance);
   return oxh::launched("oxh_batch_norm_update_running");
 }
 
@@ -605,11 +683,10 @@ oxh_status oxh_batch_norm_running_inverse_std(oxh_stream stream, uint64_t channe
                                               float epsilon, const float *variance,
                                               float *inverse_std) {
   if (channels == 0) return oxh::ok();
-  OXH_REQUIRE(channels < (1ull << 31), OXH_INVALID_SHAPE, "too many channels");
+  OXH_REQUIRE(channels <= 65535, OXH_INVALID_SHAPE, "too many channels");
   OXH_REQUIRE(variance && inverse_std, OXH_INVALID_SHAPE,
               "oxh_batch_norm_running_inverse_std: null pointer");
-  const uint32_t grid = static_cast<uint32_t>((channels + 255) / 256);
-  hipLaunchKernelGGL(bn_running_inverse_std_kernel, dim3(grid), dim3(256), 0,
+  hipLaunchKernelGGL(bn_running_inverse_std_kernel, dim3(channel_grid(channels)), dim3(256), 0,
                      oxh::as_stream(stream), static_cast<uint32_t>(channels), epsilon, variance,
                      inverse_std);
   return oxh::launched("oxh_batch_norm_running_inverse_std");
@@ -619,8 +696,17 @@ oxh_status oxh_batch_norm_apply(oxh_stream stream, uint64_t batch, uint64_t chan
                                 uint64_t spatial, const float *input, const float *weight,
                                 const float *bias, const float *mean, const float *inverse_std,
                                 float *output) {
-  return launch_apply("oxh_batch_norm_apply", stream, batch, channels, spatial,
-                      ApplyArgs{input, weight, bias, mean, inverse_std, output});
+  const char *name = "oxh_batch_norm_apply";
+  oxh_status st = check_shape(name, batch, channels, spatial);
+  if (st != OXH_OK) return st;
+  OXH_REQUIRE(input && weight && bias && mean && inverse_std && output, OXH_INVALID_SHAPE,
+              std::string(name) + ": null pointer");
+  const uint64_t bytes = batch * channels * spatial * 4;
+  OXH_REQUIRE(input == output || !oxh::any_overlap(input, bytes, output, bytes),
+              OXH_INVALID_SHAPE, std::string(name) + ": output partially overlaps the input");
+  ApplyPhase::Args a{input, weight, bias, mean, inverse_std, nullptr, 0, 0, StatsOut{}, output};
+  return launch_map<ApplyPhase>(name, stream, batch, channels, spatial,
+                                oxh::aligned16(input) && oxh::aligned16(output), a);
 }
 
 oxh_status oxh_batch_norm_affine_backward(oxh_stream stream, uint64_t batch, uint64_t channels,
@@ -629,9 +715,17 @@ oxh_status oxh_batch_norm_affine_backward(oxh_stream stream, uint64_t batch, uin
                                           const float *inverse_std, float *weight_gradient,
                                           float *bias_gradient, void *workspace,
                                           uint64_t workspace_bytes) {
-  return launch_affine("oxh_batch_norm_affine_backward", stream, batch, channels, spatial,
-                       gradient, input, mean, inverse_std, weight_gradient, bias_gradient,
-                       workspace, workspace_bytes);
+  const char *name = "oxh_batch_norm_affine_backward";
+  OXH_REQUIRE(weight_gradient && bias_gradient, OXH_INVALID_SHAPE,
+              std::string(name) + ": null output");
+  Geometry g;
+  oxh_status st = launch_reduce_gx(name, stream, batch, channels, spatial, gradient, input, mean,
+                                   inverse_std, workspace, workspace_bytes, &g);
+  if (st != OXH_OK) return st;
+  hipLaunchKernelGGL(bn_finalize_affine_kernel, dim3(channel_grid(channels)), dim3(256), 0,
+                     oxh::as_stream(stream), g, static_cast<const double2 *>(workspace),
+                     weight_gradient, bias_gradient);
+  return oxh::launched(name);
 }
 
 oxh_status oxh_batch_norm_input_backward(oxh_stream stream, uint64_t batch, uint64_t channels,
@@ -640,27 +734,106 @@ oxh_status oxh_batch_norm_input_backward(oxh_stream stream, uint64_t batch, uint
                                          const float *mean, const float *inverse_std,
                                          const float *weight_gradient,
                                          const float *bias_gradient, float *output) {
-  InputBackwardArgs a{gradient, input, weight, mean, inverse_std, weight_gradient,
-                      bias_gradient, output, static_cast<float>(batch * spatial),
-                      training != 0};
-  return launch_input_backward("oxh_batch_norm_input_backward", stream, batch, channels,
-                               spatial, a);
+  const char *name = "oxh_batch_norm_input_backward";
+  oxh_status st = check_shape(name, batch, channels, spatial);
+  if (st != OXH_OK) return st;
+  OXH_REQUIRE(gradient && weight && inverse_std && output, OXH_INVALID_SHAPE,
+              std::string(name) + ": null pointer");
+  const uint64_t bytes = batch * channels * spatial * 4;
+  if (!training) {
+    OXH_REQUIRE(gradient == output || !oxh::any_overlap(gradient, bytes, output, bytes),
+                OXH_INVALID_SHAPE, std::string(name) + ": output partially overlaps gradient");
+    DxEvalPhase::Args a{gradient, weight, inverse_std, output};
+    return launch_map<DxEvalPhase>(name, stream, batch, channels, spatial,
+                                   oxh::aligned16(gradient) && oxh::aligned16(output), a);
+  }
+  OXH_REQUIRE(input && mean && weight_gradient && bias_gradient, OXH_INVALID_SHAPE,
+              std::string(name) + ": null pointer");
+  st = no_overlap(name, output, bytes, {input, gradient}, bytes);
+  if (st != OXH_OK) return st;
+  DxTrainPhase::Args a{gradient, input, weight, mean, inverse_std, weight_gradient,
+                       bias_gradient, nullptr, 0, static_cast<float>(batch * spatial),
+                       nullptr, nullptr, output};
+  return launch_map<DxTrainPhase>(
+      name, stream, batch, channels, spatial,
+      oxh::aligned16(gradient) && oxh::aligned16(input) && oxh::aligned16(output), a);
 }
 
-oxh_status oxh_batch_norm_statistics_running(oxh_stream stream, uint64_t batch,
-                                             uint64_t channels, uint64_t spatial, float momentum,
-                                             float epsilon, const float *input,
-                                             float *running_mean, float *running_variance,
-                                             float *saved_mean, float *saved_inverse_std,
-                                             void *workspace, uint64_t workspace_bytes) {
+oxh_status oxh_batch_norm_forward_reduce(oxh_stream stream, uint64_t batch, uint64_t channels,
+                                         uint64_t spatial, const float *input, void *workspace,
+                                         uint64_t workspace_bytes) {
+  return launch_reduce_x("oxh_batch_norm_forward_reduce", stream, batch, channels, spatial,
+                         input, workspace, workspace_bytes, nullptr);
+}
+
+oxh_status oxh_batch_norm_forward_apply(oxh_stream stream, uint64_t batch, uint64_t channels,
+                                        uint64_t spatial, float momentum, float epsilon,
+                                        const float *input, const float *weight,
+                                        const float *bias, float *running_mean,
+                                        float *running_variance, float *saved_mean,
+                                        float *saved_inverse_std, float *output,
+                                        const void *workspace, uint64_t workspace_bytes) {
+  const char *name = "oxh_batch_norm_forward_apply";
   OXH_REQUIRE(std::isfinite(momentum) && std::isfinite(epsilon) && epsilon >= 0.0f,
-              OXH_INVALID_SHAPE, "oxh_batch_norm_statistics_running: bad momentum or epsilon");
-  OXH_REQUIRE(running_mean && running_variance, OXH_INVALID_SHAPE,
-              "oxh_batch_norm_statistics_running: null running statistics");
-  StatsOut out{saved_mean, saved_inverse_std, nullptr, running_mean, running_variance, momentum,
-               epsilon};
-  return launch_stats("oxh_batch_norm_statistics_running", stream, batch, channels, spatial,
-                      input, out, workspace, workspace_bytes);
+              OXH_INVALID_SHAPE, std::string(name) + ": bad momentum or epsilon");
+  oxh_status st = check_shape(name, batch, channels, spatial);
+  if (st != OXH_OK) return st;
+  OXH_REQUIRE(batch * spatial > 1, OXH_EXECUTION,
+              "BatchNorm training requires more than one value per channel");
+  OXH_REQUIRE(input && weight && bias && running_mean && running_variance && saved_mean &&
+                  saved_inverse_std && output,
+              OXH_INVALID_SHAPE, std::string(name) + ": null pointer");
+  const Geometry g = make_geometry(batch, channels, spatial, false);
+  st = check_workspace(name, g, workspace, workspace_bytes);
+  if (st != OXH_OK) return st;
+  const uint64_t bytes = batch * channels * spatial * 4;
+  st = no_overlap(name, output, bytes, {input}, bytes);
+  if (st != OXH_OK) return st;
+  ApplyPhase::Args a{input, weight, bias, nullptr, nullptr,
+                     static_cast<const double2 *>(workspace), g.slices, g.samples,
+                     StatsOut{saved_mean, saved_inverse_std, nullptr, running_mean,
+                              running_variance, momentum, epsilon},
+                     output};
+  return launch_map<ApplyPhase>(name, stream, batch, channels, spatial,
+                                oxh::aligned16(input) && oxh::aligned16(output), a);
+}
+
+oxh_status oxh_batch_norm_backward_reduce(oxh_stream stream, uint64_t batch, uint64_t channels,
+                                          uint64_t spatial, const float *gradient,
+                                          const float *input, const float *saved_mean,
+                                          const float *saved_inverse_std, void *workspace,
+                                          uint64_t workspace_bytes) {
+  return launch_reduce_gx("oxh_batch_norm_backward_reduce", stream, batch, channels, spatial,
+                          gradient, input, saved_mean, saved_inverse_std, workspace,
+                          workspace_bytes, nullptr);
+}
+
+oxh_status oxh_batch_norm_backward_input(oxh_stream stream, uint64_t batch, uint64_t channels,
+                                         uint64_t spatial, const float *gradient,
+                                         const float *input, const float *weight,
+                                         const float *saved_mean,
+                                         const float *saved_inverse_std, float *input_gradient,
+                                         float *weight_gradient, float *bias_gradient,
+                                         const void *workspace, uint64_t workspace_bytes) {
+  const char *name = "oxh_batch_norm_backward_input";
+  oxh_status st = check_shape(name, batch, channels, spatial);
+  if (st != OXH_OK) return st;
+  OXH_REQUIRE(gradient && input && weight && saved_mean && saved_inverse_std &&
+                  input_gradient && weight_gradient && bias_gradient,
+              OXH_INVALID_SHAPE, std::string(name) + ": null pointer");
+  const Geometry g = make_geometry(batch, channels, spatial, false);
+  st = check_workspace(name, g, workspace, workspace_bytes);
+  if (st != OXH_OK) return st;
+  const uint64_t bytes = batch * channels * spatial * 4;
+  st = no_overlap(name, input_gradient, bytes, {input, gradient}, bytes);
+  if (st != OXH_OK) return st;
+  DxTrainPhase::Args a{gradient, input, weight, saved_mean, saved_inverse_std, nullptr, nullptr,
+                       static_cast<const double2 *>(workspace), g.slices,
+                       static_cast<float>(batch * spatial), weight_gradient, bias_gradient,
+                       input_gradient};
+  return launch_map<DxTrainPhase>(
+      name, stream, batch, channels, spatial,
+      oxh::aligned16(gradient) && oxh::aligned16(input) && oxh::aligned16(input_gradient), a);
 }
 
 oxh_status oxh_batch_norm_forward_train(oxh_stream stream, uint64_t batch, uint64_t channels,
@@ -670,14 +843,14 @@ oxh_status oxh_batch_norm_forward_train(oxh_stream stream, uint64_t batch, uint6
                                         float *running_variance, float *saved_mean,
                                         float *saved_inverse_std, float *output, void *workspace,
                                         uint64_t workspace_bytes) {
-  oxh_status st = oxh_batch_norm_statistics_running(stream, batch, channels, spatial, momentum,
-                                                    epsilon, input, running_mean,
-                                                    running_variance, saved_mean,
-                                                    saved_inverse_std, workspace,
-                                                    workspace_bytes);
+  OXH_REQUIRE(std::isfinite(momentum) && std::isfinite(epsilon) && epsilon >= 0.0f,
+              OXH_INVALID_SHAPE, "oxh_batch_norm_forward_train: bad momentum or epsilon");
+  oxh_status st = oxh_batch_norm_forward_reduce(stream, batch, channels, spatial, input,
+                                                workspace, workspace_bytes);
   if (st != OXH_OK) return st;
-  return launch_apply("oxh_batch_norm_forward_train", stream, batch, channels, spatial,
-                      ApplyArgs{input, weight, bias, saved_mean, saved_inverse_std, output});
+  return oxh_batch_norm_forward_apply(stream, batch, channels, spatial, momentum, epsilon, input,
+                                      weight, bias, running_mean, running_variance, saved_mean,
+                                      saved_inverse_std, output, workspace, workspace_bytes);
 }
 
 oxh_status oxh_batch_norm_backward_train(oxh_stream stream, uint64_t batch, uint64_t channels,
@@ -687,14 +860,14 @@ oxh_status oxh_batch_norm_backward_train(oxh_stream stream, uint64_t batch, uint
                                          const float *saved_inverse_std, float *input_gradient,
                                          float *weight_gradient, float *bias_gradient,
                                          void *workspace, uint64_t workspace_bytes) {
-  oxh_status st = launch_affine("oxh_batch_norm_backward_train", stream, batch, channels,
-                                spatial, gradient, input, saved_mean, saved_inverse_std,
-                                weight_gradient, bias_gradient, workspace, workspace_bytes);
+  oxh_status st = oxh_batch_norm_backward_reduce(stream, batch, channels, spatial, gradient,
+                                                 input, saved_mean, saved_inverse_std,
+                                                 workspace, workspace_bytes);
   if (st != OXH_OK) return st;
-  InputBackwardArgs a{gradient, input, weight, saved_mean, saved_inverse_std, weight_gradient,
-                      bias_gradient, input_gradient, static_cast<float>(batch * spatial), true};
-  return launch_input_backward("oxh_batch_norm_backward_train", stream, batch, channels, spatial,
-                               a);
+  return oxh_batch_norm_backward_input(stream, batch, channels, spatial, gradient, input, weight,
+                                       saved_mean, saved_inverse_std, input_gradient,
+                                       weight_gradient, bias_gradient, workspace,
+                                       workspace_bytes);
 }
 
 }  // extern "C"

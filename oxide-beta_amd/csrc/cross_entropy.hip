@@ -10,9 +10,10 @@
 // lane at 1024 lanes), the max and the sum of exp(x - max) are block reductions (wave64
 // shuffles, then LDS across waves), and the gradient is written from the same registers, so a
 // fused loss+gradient moves exactly one read and one write of the logits.  The per-row losses
-// go to an fp64 workspace vector; the last workgroup to finish (device-scope counter) sums them
-// in row order and writes the mean.  Other shapes take a three-pass strided path (max, sum,
-// gradient) whose re-reads of a row hit L2.
+// go to an fp64 workspace vector and a one-block kernel sums them in row order for the mean (no
+// inter-block synchronization: on gfx950 an agent-scope release per block would write back the
+// XCD's L2).  Other shapes take a three-pass strided path (max, sum, gradient) whose re-reads of
+// a row hit L2.
 //
 // Per element the fp32 operations follow the CPU path: e = exp(x - max);
 // p = e / normalizer; grad = (outer / batch) * (p - onehot); row loss = (ln(normalizer) + max)
@@ -32,7 +33,6 @@ struct CeArgs {
   float *grad;                            // may be null (no gradient)
   uint32_t *error_flag;                   // may be null
   double *row_loss;                       // workspace [batch]
-  uint32_t *counter;                      // workspace, 1 counter
   uint64_t batch, classes;
 };
 
@@ -76,31 +76,23 @@ __device__ __forceinline__ double block_sum(double v, double *lds) {
   return r;
 }
 
-// Row finished: record its loss, and let the last row's block write the batch mean.
-template <int BLOCK>
-__device__ __forceinline__ void finish_row(const CeArgs &a, uint64_t row, float row_loss,
-                                           double *lds) {
-  if (a.loss == nullptr) return;
-  __shared__ bool is_last;
-  if (threadIdx.x == 0) {
-    a.row_loss[row] = static_cast<double>(row_loss);
-    __threadfence();
-    const uint32_t prev =
-        __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    is_last = prev + 1 == static_cast<uint32_t>(a.batch);
-    if (is_last) {
-      __threadfence();
-      __hip_atomic_store(a.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
-  __syncthreads();
-  if (!is_last) return;
-  // Fixed-order sum: thread t adds rows t, t + BLOCK, ...; then a fixed-shape tree.
+// Row finished: record its loss for the batch mean.
+__device__ __forceinline__ void finish_row(const CeArgs &a, uint64_t row, float row_loss) {
+  if (a.loss != nullptr && threadIdx.x == 0) a.row_loss[row] = static_cast<double>(row_loss);
+}
+
+// Batch mean of the row losses (one block): thread t adds rows t, t + 1024, ... in order, then a
+// fixed-shape tree, so the result is deterministic.  evaluation.rs:616-619 divides the summed
+// loss by the batch size in fp32.
+constexpr int kMeanBlock = 1024;
+
+__global__ __launch_bounds__(kMeanBlock) void ce_mean_kernel(const double *__restrict__ row_loss,
+                                                             uint64_t batch, float *loss) {
+  __shared__ double lds[kMeanBlock / 64];
   double s = 0.0;
-  for (uint64_t r = threadIdx.x; r < a.batch; r += BLOCK) s += a.row_loss[r];
-  s = block_sum<BLOCK>(s, lds);
-  if (threadIdx.x == 0)
-    *a.loss = static_cast<float>(s) / static_cast<float>(a.batch);  // evaluation.rs:616-619
+  for (uint64_t r = threadIdx.x; r < batch; r += kMeanBlock) s += row_loss[r];
+  s = block_sum<kMeanBlock>(s, lds);
+  if (threadIdx.x == 0) *loss = static_cast<float>(s) / static_cast<float>(batch);
 }
 
 // Register path: BLOCK lanes x V float4 hold one row of `classes` (= 4 * c4) logits.
@@ -161,7 +153,7 @@ __global__ __launch_bounds__(BLOCK) void ce_row_kernel(CeArgs a) {
   }
   const float row_loss =
       valid ? logf(normalizer) + maximum - a.logits[row * a.classes + target] : NAN;
-  finish_row<BLOCK>(a, row, row_loss, lds_d);
+  finish_row(a, row, row_loss);
 }
 
 // General path: any classes, any alignment; three strided passes over the row.
@@ -191,10 +183,10 @@ __global__ __launch_bounds__(kGenBlock) void ce_row_general_kernel(CeArgs a) {
     }
   }
   const float row_loss = valid ? logf(normalizer) + maximum - x[target] : NAN;
-  finish_row<kGenBlock>(a, row, row_loss, lds_d);
+  finish_row(a, row, row_loss);
 }
 
-uint64_t ce_workspace_bytes(uint64_t batch) { return (batch * 8 + 4 + 255) / 256 * 256; }
+uint64_t ce_workspace_bytes(uint64_t batch) { return (batch * 8 + 255) / 256 * 256; }
 
 oxh_status launch_ce(const char *name, oxh_stream stream, CeArgs a, void *workspace,
                      uint64_t workspace_bytes) {
@@ -218,7 +210,9 @@ oxh_status launch_ce(const char *name, oxh_stream stream, CeArgs a, void *worksp
     OXH_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 7u) == 0, OXH_INVALID_SHAPE,
                 std::string(name) + ": workspace must be 8-byte aligned");
     a.row_loss = static_cast<double *>(workspace);
-    a.counter = reinterpret_cast<uint32_t *>(static_cast<char *>(workspace) + a.batch * 8);
+    OXH_REQUIRE(!oxh::any_overlap(workspace, need, a.logits, bytes) &&
+                    (!a.grad || !oxh::any_overlap(workspace, need, a.grad, bytes)),
+                OXH_INVALID_SHAPE, std::string(name) + ": workspace overlaps the logits or grad");
   }
   hipStream_t s = oxh::as_stream(stream);
   const dim3 grid(static_cast<uint32_t>(a.batch));
@@ -240,6 +234,10 @@ oxh_status launch_ce(const char *name, oxh_stream stream, CeArgs a, void *worksp
   } else {
     hipLaunchKernelGGL(ce_row_general_kernel, grid, dim3(kGenBlock), 0, s, a);
   }
+  oxh_status st = oxh::launched(name);
+  if (st != OXH_OK || a.loss == nullptr) return st;
+  hipLaunchKernelGGL(ce_mean_kernel, dim3(1), dim3(kMeanBlock), 0, s, a.row_loss, a.batch,
+                     a.loss);
   return oxh::launched(name);
 }
 
@@ -259,8 +257,7 @@ oxh_status oxh_cross_entropy_forward(oxh_stream stream, uint64_t batch, uint64_t
                                      uint32_t *error_flag, void *workspace,
                                      uint64_t workspace_bytes) {
   OXH_REQUIRE(loss != nullptr, OXH_INVALID_SHAPE, "oxh_cross_entropy_forward: null loss");
-  CeArgs a{logits, targets, nullptr, loss, nullptr, error_flag, nullptr, nullptr, batch,
-           classes};
+  CeArgs a{logits, targets, nullptr, loss, nullptr, error_flag, nullptr, batch, classes};
   return launch_ce("oxh_cross_entropy_forward", stream, a, workspace, workspace_bytes);
 }
 
@@ -269,8 +266,7 @@ oxh_status oxh_cross_entropy_backward(oxh_stream stream, uint64_t batch, uint64_
                                       const float *outer_gradient, float *grad,
                                       uint32_t *error_flag) {
   OXH_REQUIRE(grad != nullptr, OXH_INVALID_SHAPE, "oxh_cross_entropy_backward: null grad");
-  CeArgs a{logits, targets, outer_gradient, nullptr, grad, error_flag, nullptr, nullptr, batch,
-           classes};
+  CeArgs a{logits, targets, outer_gradient, nullptr, grad, error_flag, nullptr, batch, classes};
   return launch_ce("oxh_cross_entropy_backward", stream, a, nullptr, 0);
 }
 
@@ -282,8 +278,7 @@ oxh_status oxh_cross_entropy_forward_backward(oxh_stream stream, uint64_t batch,
                                               void *workspace, uint64_t workspace_bytes) {
   OXH_REQUIRE(loss != nullptr && grad != nullptr, OXH_INVALID_SHAPE,
               "oxh_cross_entropy_forward_backward: null output");
-  CeArgs a{logits, targets, outer_gradient, loss, grad, error_flag, nullptr, nullptr, batch,
-           classes};
+  CeArgs a{logits, targets, outer_gradient, loss, grad, error_flag, nullptr, batch, classes};
   return launch_ce("oxh_cross_entropy_forward_backward", stream, a, workspace,
                    workspace_bytes);
 }

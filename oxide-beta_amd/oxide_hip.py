@@ -97,8 +97,13 @@ _SIGNATURES = {
                                              _vp, _vp, _u64]),
     "oxh_batch_norm_input_backward": (_st, [_vp, _u64, _u64, _u64, _int, _vp, _vp, _vp, _vp,
                                             _vp, _vp, _vp, _vp]),
-    "oxh_batch_norm_statistics_running": (_st, [_vp, _u64, _u64, _u64, _f32, _f32, _vp, _vp,
-                                                _vp, _vp, _vp, _vp, _u64]),
+    "oxh_batch_norm_forward_reduce": (_st, [_vp, _u64, _u64, _u64, _vp, _vp, _u64]),
+    "oxh_batch_norm_forward_apply": (_st, [_vp, _u64, _u64, _u64, _f32, _f32, _vp, _vp, _vp,
+                                           _vp, _vp, _vp, _vp, _vp, _vp, _u64]),
+    "oxh_batch_norm_backward_reduce": (_st, [_vp, _u64, _u64, _u64, _vp, _vp, _vp, _vp, _vp,
+                                             _u64]),
+    "oxh_batch_norm_backward_input": (_st, [_vp, _u64, _u64, _u64, _vp, _vp, _vp, _vp, _vp,
+                                            _vp, _vp, _vp, _vp, _u64]),
     "oxh_batch_norm_forward_train": (_st, [_vp, _u64, _u64, _u64, _f32, _f32, _vp, _vp, _vp,
                                            _vp, _vp, _vp, _vp, _vp, _vp, _u64]),
     "oxh_batch_norm_backward_train": (_st, [_vp, _u64, _u64, _u64, _vp, _vp, _vp, _vp, _vp,
@@ -199,7 +204,7 @@ def _stream(stream) -> int | None:
 
 
 class Workspace:
-    """Zero-filled device scratch reused across calls (kernels leave it zeroed)."""
+    """Device scratch for the reductions' partial sums, grown on demand."""
 
     def __init__(self):
         self._buf = None
@@ -208,8 +213,9 @@ class Workspace:
         import torch
 
         if self._buf is None or self._buf.numel() < nbytes:
-            self._buf = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device="cuda")
-            # the zero fill runs on torch's stream; kernels may use another stream
+            # allocated on torch's stream; kernels may run on another stream
+            torch.cuda.synchronize()
+            self._buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device="cuda")
             torch.cuda.synchronize()
         return self._buf
 
@@ -333,15 +339,40 @@ class LoadedModule:
                                                   _ptr(weight_gradient), _ptr(bias_gradient),
                                                   _ptr(out)))
 
-    def batch_norm_statistics_running(self, x, running_mean, running_variance, saved_mean,
-                                      saved_inverse_std, momentum=0.1, epsilon=1e-5,
-                                      stream=None):
+    def batch_norm_forward_reduce(self, x, stream=None):
         n, c, h, w = x.shape
         ws, wsb = self._bn_ws_args(n, c, h * w)
-        check(lib().oxh_batch_norm_statistics_running(_stream(stream), n, c, h * w, momentum,
-                                                      epsilon, _ptr(x), _ptr(running_mean),
-                                                      _ptr(running_variance), _ptr(saved_mean),
-                                                      _ptr(saved_inverse_std), ws, wsb))
+        check(lib().oxh_batch_norm_forward_reduce(_stream(stream), n, c, h * w, _ptr(x), ws,
+                                                  wsb))
+
+    def batch_norm_forward_apply(self, x, weight, bias, running_mean, running_variance,
+                                 saved_mean, saved_inverse_std, out, momentum=0.1,
+                                 epsilon=1e-5, stream=None):
+        n, c, h, w = x.shape
+        ws, wsb = self._bn_ws_args(n, c, h * w)
+        check(lib().oxh_batch_norm_forward_apply(_stream(stream), n, c, h * w, momentum, epsilon,
+                                                 _ptr(x), _ptr(weight), _ptr(bias),
+                                                 _ptr(running_mean), _ptr(running_variance),
+                                                 _ptr(saved_mean), _ptr(saved_inverse_std),
+                                                 _ptr(out), ws, wsb))
+
+    def batch_norm_backward_reduce(self, gradient, x, saved_mean, saved_inverse_std,
+                                   stream=None):
+        n, c, h, w = x.shape
+        ws, wsb = self._bn_ws_args(n, c, h * w)
+        check(lib().oxh_batch_norm_backward_reduce(_stream(stream), n, c, h * w, _ptr(gradient),
+                                                   _ptr(x), _ptr(saved_mean),
+                                                   _ptr(saved_inverse_std), ws, wsb))
+
+    def batch_norm_backward_input(self, gradient, x, weight, saved_mean, saved_inverse_std,
+                                  input_gradient, weight_gradient, bias_gradient, stream=None):
+        n, c, h, w = x.shape
+        ws, wsb = self._bn_ws_args(n, c, h * w)
+        check(lib().oxh_batch_norm_backward_input(_stream(stream), n, c, h * w, _ptr(gradient),
+                                                  _ptr(x), _ptr(weight), _ptr(saved_mean),
+                                                  _ptr(saved_inverse_std), _ptr(input_gradient),
+                                                  _ptr(weight_gradient), _ptr(bias_gradient),
+                                                  ws, wsb))
 
     def batch_norm_forward_train(self, x, weight, bias, running_mean, running_variance,
                                  saved_mean, saved_inverse_std, out, momentum=0.1, epsilon=1e-5,

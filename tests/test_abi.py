@@ -74,7 +74,7 @@ def test_batch_norm_workspace_checks():
 
 def test_cross_entropy_argument_checks():
     lib = ox.lib()
-    assert ox.cross_entropy_workspace_size(8192, 32768) >= 8192 * 8 + 4
+    assert ox.cross_entropy_workspace_size(8192, 32768) >= 8192 * 8
     # the gradient needs the upstream scalar
     st = lib.oxh_cross_entropy_backward(None, 2, 3, 256, 512, None, 4096, None)
     assert st == ox.INVALID_SHAPE

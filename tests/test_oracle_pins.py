@@ -255,7 +255,8 @@ def test_cross_entropy_zero_logits_closed_form():
 
 @pytest.mark.parametrize("value,ok", [(3.0, True), (0.0, True), (-0.0, True), (1.5, False),
                                       (-1.0, False), (float("nan"), False), (float("inf"), False),
-                                      (5.0, False)])
+                                      (5.0, False), (1e30, False), (2.0 ** 64, False),
+                                      (2.0 ** 63, False)])
 def test_class_index_rules(value, ok):
     if ok:
         assert oracle.class_index(value, 5) == int(abs(value))
