@@ -19,6 +19,11 @@
 
 namespace {
 
+#ifndef OXH_ADAMW_UNROLL
+#define OXH_ADAMW_UNROLL 2  // float4 per thread per stream (overridable for tuning sweeps)
+#endif
+constexpr int kUnroll = OXH_ADAMW_UNROLL;
+
 struct Hyper {
   float lr, wd, b1, b2, c1, c2, eps;
 };
@@ -61,17 +66,17 @@ __device__ __forceinline__ void adamw_range(const Hyper &h, const Streams &s, ui
     float4 *mo4 = reinterpret_cast<float4 *>(s.mo);
     float4 *vo4 = reinterpret_cast<float4 *>(s.vo);
     uint64_t i = b4 + threadIdx.x;
-    for (; i + (oxh::kUnroll - 1) * oxh::kBlock < e4; i += oxh::kUnroll * oxh::kBlock) {
-      float4 p[oxh::kUnroll], g[oxh::kUnroll], m[oxh::kUnroll], v[oxh::kUnroll];
+    for (; i + (kUnroll - 1) * oxh::kBlock < e4; i += kUnroll * oxh::kBlock) {
+      float4 p[kUnroll], g[kUnroll], m[kUnroll], v[kUnroll];
 #pragma unroll
-      for (int u = 0; u < oxh::kUnroll; ++u) {
+      for (int u = 0; u < kUnroll; ++u) {
         p[u] = p4[i + u * oxh::kBlock];
         g[u] = g4[i + u * oxh::kBlock];
         m[u] = m4[i + u * oxh::kBlock];
         v[u] = v4[i + u * oxh::kBlock];
       }
 #pragma unroll
-      for (int u = 0; u < oxh::kUnroll; ++u) {
+      for (int u = 0; u < kUnroll; ++u) {
         float4 po, mo, vo;
         adamw_vec(h, p[u], g[u], m[u], v[u], po, mo, vo);
         po4[i + u * oxh::kBlock] = po;
@@ -97,8 +102,9 @@ __device__ __forceinline__ void adamw_range(const Hyper &h, const Streams &s, ui
   }
 }
 
-// Elements per block: kBlock threads x kUnroll float4 x 4 passes.
-constexpr uint64_t kChunk = static_cast<uint64_t>(oxh::kBlock) * oxh::kUnroll * 4 * 4;
+// Elements per block: kBlock threads x kUnroll float4 (one pass; many short blocks stream
+// faster on MI355X than long per-lane loops).
+constexpr uint64_t kChunk = static_cast<uint64_t>(oxh::kBlock) * kUnroll * 4;
 
 __global__ __launch_bounds__(oxh::kBlock) void adamw_kernel(Hyper h, Streams s, uint64_t n,
                                                             bool vec) {
@@ -193,7 +199,7 @@ oxh_status oxh_adamw(oxh_stream stream, float learning_rate, float weight_decay,
   const Streams s{parameter, gradient, first_moment, second_moment,
                   new_parameter, new_first_moment, new_second_moment};
   uint64_t grid = (n + kChunk - 1) / kChunk;
-  if (grid > (1u << 20)) grid = 1u << 20;
+  if (grid > 0x7FFFFFFFull) grid = 0x7FFFFFFFull;
   hipLaunchKernelGGL(adamw_kernel, dim3(static_cast<uint32_t>(grid)), dim3(oxh::kBlock), 0,
                      oxh::as_stream(stream), h, s, n, vec);
   return oxh::launched("oxh_adamw");

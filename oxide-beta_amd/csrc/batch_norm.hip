@@ -14,11 +14,14 @@
 //     division), accumulates in fp64, reduces the block with wave64 shuffles and LDS, and stores
 //     one fp64 partial pair to the workspace.  Forward partials are sums of (x - K) and
 //     (x - K)^2 with K = x[0, c, 0]; backward partials are sums of g and g * x_hat.
-//   * Map: every block of the streaming pass (apply or dx) first finalizes the statistics of
-//     the channels its planes belong to, summing that channel's S partials in a fixed order, so
-//     all blocks derive bit-identical values; the block holding plane (n = 0, c) also writes the
-//     per-channel outputs (saved mean / inverse std and the running update, or dweight /
-//     dbias).  Then it streams its planes with 128-bit loads, channel values from LDS.
+//   * Map: each block of the streaming pass (apply or dx) covers a flat range of 1024 elements
+//     (one float4 per lane per stream: on MI355X short blocks stream faster than long per-lane
+//     loops, and they re-read what the reduce just read while it is still in the 256 MB MALL).
+//     It issues its loads, then finalizes the statistics of the <= kMaxPlanes channels its
+//     planes belong to, summing that channel's S partials in a fixed order, so all blocks
+//     derive bit-identical values; the block holding the first element of plane (n = 0, c)
+//     also writes the per-channel outputs (saved mean / inverse std and the running update, or
+//     dweight / dbias).  Channel values are read back from LDS.
 //     A kernel boundary separates reduce and map, so no fence or atomic is needed (on gfx950 an
 //     agent-scope release writes back the XCD's L2, far too costly per block).
 //   * Per-element arithmetic follows the CPU path's fp32 operation order exactly
@@ -33,11 +36,25 @@
 
 namespace {
 
+// Launch-shape constants (overridable at build time for tuning sweeps).
+#ifndef OXH_BN_RED_BLOCKS_PER_CU
+#define OXH_BN_RED_BLOCKS_PER_CU 8  // reduce grid: target blocks per CU over all channels
+#endif
+#ifndef OXH_BN_RED_UNROLL
+#define OXH_BN_RED_UNROLL 4  // float4 loads in flight per thread per stream in a reduce pass
+#endif
+#ifndef OXH_BN_MAP_VEC
+#define OXH_BN_MAP_VEC 2  // float4 per thread per stream in a map block
+#endif
+
 constexpr int kRedBlock = 256;  // 4 waves
 constexpr int kRedWaves = kRedBlock / 64;
+constexpr int kRedUnroll = OXH_BN_RED_UNROLL;
+constexpr uint32_t kMaxSlices = 64;  // partials per channel (summed by every map block)
 constexpr int kMapBlock = 256;
-constexpr uint32_t kMapElems = 4096;  // elements per map block (16 KiB per stream)
-constexpr uint32_t kMaxPlanes = 256;  // planes per map block (small spatial sizes)
+constexpr int kMapVec = OXH_BN_MAP_VEC;
+constexpr uint32_t kMapElems = kMapBlock * 4 * kMapVec;  // elements per map block
+constexpr uint32_t kMaxPlanes = 256;  // planes one map block may touch
 
 // ---------------------------------------------------------------- geometry
 
@@ -51,12 +68,15 @@ struct Geometry {
 };
 
 uint32_t choose_slices(uint64_t channels, uint64_t samples) {
-  // Aim for ~8 blocks per CU in total, but keep >= 4096 values per block.
-  uint64_t target = (8ull * oxh::kComputeUnits + channels - 1) / channels;
+  // Aim for OXH_BN_RED_BLOCKS_PER_CU blocks per CU in total, but keep >= 4096 values per
+  // block and at most kMaxSlices partials per channel.
+  uint64_t target =
+      (static_cast<uint64_t>(OXH_BN_RED_BLOCKS_PER_CU) * oxh::kComputeUnits + channels - 1) /
+      channels;
   uint64_t max_by_work = samples / 4096;
   if (max_by_work < 1) max_by_work = 1;
   uint64_t s = target < max_by_work ? target : max_by_work;
-  if (s > 1024) s = 1024;
+  if (s > kMaxSlices) s = kMaxSlices;
   if (s < 1) s = 1;
   return static_cast<uint32_t>(s);
 }
@@ -83,16 +103,14 @@ uint64_t workspace_bytes_for(const Geometry &g) {
   return (static_cast<uint64_t>(g.channels) * g.slices * 16 + 255) / 256 * 256;
 }
 
-// Map blocks: either a chunk of one plane (spatial >= kMapElems) or up to kMaxPlanes whole
-// planes (smaller spatial sizes).
+// Map blocks: block b covers the flattened elements [b * E, (b + 1) * E) of the NCHW tensor,
+// which touch at most kMaxPlanes (n, c) planes.  E = kMapElems, reduced for tiny planes.
 struct PlaneMap {
   uint32_t channels, spatial;
-  uint64_t planes;            // batch * channels
-  uint32_t chunks;            // chunks per plane (> 0: chunk mode)
-  uint32_t chunk_len;         // elements per chunk (multiple of 4)
-  uint32_t planes_per_block;  // plane mode
+  uint64_t total;        // batch * channels * spatial
+  uint32_t block_elems;  // E (a multiple of 4 on the vector path)
   bool vec;
-  oxh::FastDiv spatial_div;   // divides a block-relative element offset by spatial
+  oxh::FastDiv spatial_div;
   uint64_t blocks;
 };
 
@@ -100,24 +118,14 @@ PlaneMap make_plane_map(uint64_t batch, uint64_t channels, uint64_t spatial, boo
   PlaneMap m{};
   m.channels = static_cast<uint32_t>(channels);
   m.spatial = static_cast<uint32_t>(spatial);
-  m.planes = batch * channels;
+  m.total = batch * channels * spatial;
   m.vec = aligned && spatial % 4 == 0;
-  if (spatial >= kMapElems) {
-    uint32_t chunks = static_cast<uint32_t>((spatial + kMapElems - 1) / kMapElems);
-    uint64_t len = (spatial + chunks - 1) / chunks;
-    len = (len + 3) / 4 * 4;
-    m.chunk_len = static_cast<uint32_t>(len);
-    m.chunks = static_cast<uint32_t>((spatial + len - 1) / len);
-    m.planes_per_block = 1;
-    m.blocks = m.planes * m.chunks;
-  } else {
-    m.chunks = 0;
-    uint32_t ppb = static_cast<uint32_t>(kMapElems / spatial);
-    if (ppb > kMaxPlanes) ppb = kMaxPlanes;
-    if (ppb < 1) ppb = 1;
-    m.planes_per_block = ppb;
-    m.blocks = (m.planes + ppb - 1) / ppb;
-  }
+  uint64_t e = kMapElems;
+  const uint64_t cap = static_cast<uint64_t>(kMaxPlanes - 1) * spatial;  // <= kMaxPlanes planes
+  if (e > cap) e = cap;
+  if (m.vec) e = e / 4 * 4;  // spatial % 4 == 0 keeps cap >= 4
+  m.block_elems = static_cast<uint32_t>(e);
+  m.blocks = (m.total + e - 1) / e;
   m.spatial_div = oxh::make_fastdiv(m.spatial);
   return m;
 }
@@ -178,12 +186,12 @@ __global__ __launch_bounds__(kRedBlock) void bn_reduce_x_kernel(Geometry g,
       sum += (d0 + d1) + (d2 + d3);
       sq += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
     };
-    for (; j + 3 * kRedBlock < e4; j += 4 * kRedBlock) {
-      float4 v[4];
+    for (; j + (kRedUnroll - 1) * kRedBlock < e4; j += kRedUnroll * kRedBlock) {
+      float4 v[kRedUnroll];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) v[u] = x4[nchw_index(g, c, j + u * kRedBlock)];
+      for (int u = 0; u < kRedUnroll; ++u) v[u] = x4[nchw_index(g, c, j + u * kRedBlock)];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) add4(v[u]);
+      for (int u = 0; u < kRedUnroll; ++u) add4(v[u]);
     }
     for (; j < e4; j += kRedBlock) add4(x4[nchw_index(g, c, j)]);
   } else {
@@ -222,16 +230,16 @@ __global__ __launch_bounds__(kRedBlock) void bn_reduce_gx_kernel(
       sgx += (static_cast<double>(gv.x * n0) + static_cast<double>(gv.y * n1)) +
              (static_cast<double>(gv.z * n2) + static_cast<double>(gv.w * n3));
     };
-    for (; j + 3 * kRedBlock < e4; j += 4 * kRedBlock) {
-      float4 xv[4], gv[4];
+    for (; j + (kRedUnroll - 1) * kRedBlock < e4; j += kRedUnroll * kRedBlock) {
+      float4 xv[kRedUnroll], gv[kRedUnroll];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < kRedUnroll; ++u) {
         const uint64_t idx = nchw_index(g, c, j + u * kRedBlock);
         xv[u] = x4[idx];
         gv[u] = g4[idx];
       }
 #pragma unroll
-      for (int u = 0; u < 4; ++u) add4(xv[u], gv[u]);
+      for (int u = 0; u < kRedUnroll; ++u) add4(xv[u], gv[u]);
     }
     for (; j < e4; j += kRedBlock) {
       const uint64_t idx = nchw_index(g, c, j);
@@ -256,19 +264,12 @@ struct Moments {
   float mean, inv, biased, correction;
 };
 
-// Channel statistics from its S forward partials, summed in slice order.
-__device__ __forceinline__ Moments forward_moments(const double2 *partial, uint32_t slices,
-                                                   uint32_t c, float shift, uint64_t samples,
+// Channel statistics from the sums of (x - shift) and (x - shift)^2 over its M values.
+__device__ __forceinline__ Moments forward_moments(double2 sums, float shift, uint64_t samples,
                                                    float epsilon) {
-  double total = 0.0, total_sq = 0.0;
-  for (uint32_t t = 0; t < slices; ++t) {
-    const double2 p = partial[static_cast<uint64_t>(c) * slices + t];
-    total += p.x;
-    total_sq += p.y;
-  }
   const double m = static_cast<double>(samples);
-  const double mean_shifted = total / m;
-  double var = total_sq / m - mean_shifted * mean_shifted;
+  const double mean_shifted = sums.x / m;
+  double var = sums.y / m - mean_shifted * mean_shifted;
   if (var < 0.0) var = 0.0;
   Moments r;
   r.mean = static_cast<float>(static_cast<double>(shift) + mean_shifted);
@@ -284,17 +285,25 @@ __device__ __forceinline__ Moments forward_moments(const double2 *partial, uint3
   return r;
 }
 
-__device__ __forceinline__ void backward_sums(const double2 *partial, uint32_t slices,
-                                              uint32_t c, float &sum_g, float &sum_gx) {
-  double a = 0.0, b = 0.0;
-  for (uint32_t t = 0; t < slices; ++t) {
-    const double2 p = partial[static_cast<uint64_t>(c) * slices + t];
-    a += p.x;
-    b += p.y;
-  }
-  sum_g = static_cast<float>(a);
-  sum_gx = static_cast<float>(b);
+__device__ __forceinline__ bool lane0() { return threadIdx.x % 64 == 0; }
+
+// Per-lane share of a channel's partials: lane l holds partial l (S <= kMaxSlices = 64, so one
+// load per lane); loading only -- the sums are formed later, after the block's data loads have
+// been issued, so the two load latencies overlap.
+__device__ __forceinline__ double2 load_lane_partial(const double2 *partial, uint32_t slices,
+                                                     uint32_t c) {
+  const uint32_t lane = threadIdx.x % 64;
+  return lane < slices ? partial[static_cast<uint64_t>(c) * slices + lane]
+                       : make_double2(0.0, 0.0);
 }
+
+// Fixed butterfly over the wave; every lane returns lane 0's sums (bit-identical in all
+// blocks and in the finalize kernels, which use the same reduction).
+__device__ __forceinline__ double2 wave_sums_lane0(double2 v) {
+  const double a = wave_sum(v.x), b = wave_sum(v.y);
+  return make_double2(__shfl(a, 0, 64), __shfl(b, 0, 64));
+}
+
 
 struct StatsOut {
   float *mean, *inverse_std, *unbiased_variance;  // unbiased_variance may be null
@@ -314,24 +323,27 @@ __device__ __forceinline__ void write_forward_outputs(const StatsOut &o, uint32_
   }
 }
 
-// One thread per channel: the reference's separate statistics output (no consumer kernel).
-__global__ void bn_finalize_forward_kernel(Geometry g, const float *__restrict__ x,
-                                           const double2 *__restrict__ partial, StatsOut out) {
-  const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
+// One wave per channel: the reference's separate statistics output (no consumer kernel).
+__global__ __launch_bounds__(256) void bn_finalize_forward_kernel(
+    Geometry g, const float *__restrict__ x, const double2 *__restrict__ partial, StatsOut out) {
+  const uint32_t c = blockIdx.x * 4 + threadIdx.x / 64;
   if (c >= g.channels) return;
   const float shift = x[static_cast<uint64_t>(c) * g.spatial];
-  write_forward_outputs(out, c,
-                        forward_moments(partial, g.slices, c, shift, g.samples, out.epsilon));
+  const Moments r = forward_moments(wave_sums_lane0(load_lane_partial(partial, g.slices, c)),
+                                    shift, g.samples, out.epsilon);
+  if (lane0()) write_forward_outputs(out, c, r);
 }
 
-__global__ void bn_finalize_affine_kernel(Geometry g, const double2 *__restrict__ partial,
-                                          float *weight_gradient, float *bias_gradient) {
-  const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
+__global__ __launch_bounds__(256) void bn_finalize_affine_kernel(
+    Geometry g, const double2 *__restrict__ partial, float *weight_gradient,
+    float *bias_gradient) {
+  const uint32_t c = blockIdx.x * 4 + threadIdx.x / 64;
   if (c >= g.channels) return;
-  float sg, sgx;
-  backward_sums(partial, g.slices, c, sg, sgx);
-  weight_gradient[c] = sgx;
-  bias_gradient[c] = sg;
+  const double2 sums = wave_sums_lane0(load_lane_partial(partial, g.slices, c));
+  if (lane0()) {
+    weight_gradient[c] = static_cast<float>(sums.y);
+    bias_gradient[c] = static_cast<float>(sums.x);
+  }
 }
 
 // ---------------------------------------------------------------- map passes
@@ -341,6 +353,10 @@ template <int V>
 struct Cache {
   float v[V][kMaxPlanes];
 };
+
+// Map phases.  load() (all lanes of a wave, for channel c) only issues the channel's loads;
+// finish() forms the channel values and lane 0 stores them in the LDS cache and, in the block
+// holding the first element of plane (0, c), the per-channel outputs.
 
 // Forward apply.  Channel values: mean, inv, w, b.  Statistics come from the partials
 // (finalize + apply) or from mean / inverse_std arrays (the reference's separate apply).
@@ -352,27 +368,42 @@ struct ApplyPhase {
     const double2 *partial;
     uint32_t slices;
     uint64_t samples;
-    StatsOut out;  // written by the block holding plane (0, c) when partial != null
+    StatsOut out;  // written by the designated block when partial != null
     float *y;
   };
-  __device__ static void channel(const Args &a, const PlaneMap &m, uint32_t c, bool designated,
-                                 Cache<V> &cache, uint32_t k) {
-    float mu, inv;
+  struct Pre {
+    double2 part;
+    float shift, mu, inv, w, b;
+  };
+  __device__ static Pre load(const Args &a, const PlaneMap &m, uint32_t c) {
+    Pre p;
     if (a.partial) {
-      const float shift = a.x[static_cast<uint64_t>(c) * m.spatial];
-      const Moments r =
-          forward_moments(a.partial, a.slices, c, shift, a.samples, a.out.epsilon);
-      if (designated) write_forward_outputs(a.out, c, r);
+      p.part = load_lane_partial(a.partial, a.slices, c);
+      p.shift = a.x[static_cast<uint64_t>(c) * m.spatial];
+    } else {
+      p.mu = a.mean[c];
+      p.inv = a.inverse_std[c];
+    }
+    p.w = a.weight[c];
+    p.b = a.bias[c];
+    return p;
+  }
+  __device__ static void finish(const Args &a, uint32_t c, const Pre &p, bool designated,
+                                Cache<V> &cache, uint32_t k) {
+    float mu = p.mu, inv = p.inv;
+    if (a.partial) {
+      const Moments r = forward_moments(wave_sums_lane0(p.part), p.shift, a.samples,
+                                        a.out.epsilon);
+      if (designated && lane0()) write_forward_outputs(a.out, c, r);
       mu = r.mean;
       inv = r.inv;
-    } else {
-      mu = a.mean[c];
-      inv = a.inverse_std[c];
     }
-    cache.v[0][k] = mu;
-    cache.v[1][k] = inv;
-    cache.v[2][k] = a.weight[c];
-    cache.v[3][k] = a.bias[c];
+    if (lane0()) {
+      cache.v[0][k] = mu;
+      cache.v[1][k] = inv;
+      cache.v[2][k] = p.w;
+      cache.v[3][k] = p.b;
+    }
   }
   __device__ static const float *input(const Args &a, int) { return a.x; }
   __device__ static float *output(const Args &a) { return a.y; }
@@ -395,25 +426,42 @@ struct DxTrainPhase {
     float *out_weight_gradient, *out_bias_gradient;  // written when partial != null
     float *dx;
   };
-  __device__ static void channel(const Args &a, const PlaneMap &, uint32_t c, bool designated,
-                                 Cache<V> &cache, uint32_t k) {
-    float sg, sgx;
+  struct Pre {
+    double2 part;
+    float sg, sgx, mu, inv, w;
+  };
+  __device__ static Pre load(const Args &a, const PlaneMap &, uint32_t c) {
+    Pre p;
     if (a.partial) {
-      backward_sums(a.partial, a.slices, c, sg, sgx);
-      if (designated) {
+      p.part = load_lane_partial(a.partial, a.slices, c);
+    } else {
+      p.sg = a.bias_gradient[c];
+      p.sgx = a.weight_gradient[c];
+    }
+    p.mu = a.mean[c];
+    p.inv = a.inverse_std[c];
+    p.w = a.weight[c];
+    return p;
+  }
+  __device__ static void finish(const Args &a, uint32_t c, const Pre &p, bool designated,
+                                Cache<V> &cache, uint32_t k) {
+    float sg = p.sg, sgx = p.sgx;
+    if (a.partial) {
+      const double2 sums = wave_sums_lane0(p.part);
+      sg = static_cast<float>(sums.x);
+      sgx = static_cast<float>(sums.y);
+      if (designated && lane0()) {
         a.out_weight_gradient[c] = sgx;
         a.out_bias_gradient[c] = sg;
       }
-    } else {
-      sg = a.bias_gradient[c];
-      sgx = a.weight_gradient[c];
     }
-    const float inv = a.inverse_std[c];
-    cache.v[0][k] = a.mean[c];
-    cache.v[1][k] = inv;
-    cache.v[2][k] = a.weight[c] * inv / a.samples;
-    cache.v[3][k] = sg;
-    cache.v[4][k] = sgx;
+    if (lane0()) {
+      cache.v[0][k] = p.mu;
+      cache.v[1][k] = p.inv;
+      cache.v[2][k] = p.w * p.inv / a.samples;
+      cache.v[3][k] = sg;
+      cache.v[4][k] = sgx;
+    }
   }
   __device__ static const float *input(const Args &a, int i) { return i == 0 ? a.grad : a.x; }
   __device__ static float *output(const Args &a) { return a.dx; }
@@ -432,10 +480,18 @@ struct DxEvalPhase {
     const float *grad, *weight, *inverse_std;
     float *dx;
   };
-  __device__ static void channel(const Args &a, const PlaneMap &, uint32_t c, bool,
-                                 Cache<V> &cache, uint32_t k) {
-    cache.v[0][k] = a.weight[c];
-    cache.v[1][k] = a.inverse_std[c];
+  struct Pre {
+    float w, inv;
+  };
+  __device__ static Pre load(const Args &a, const PlaneMap &, uint32_t c) {
+    return Pre{a.weight[c], a.inverse_std[c]};
+  }
+  __device__ static void finish(const Args &, uint32_t, const Pre &p, bool, Cache<V> &cache,
+                                uint32_t k) {
+    if (lane0()) {
+      cache.v[0][k] = p.w;
+      cache.v[1][k] = p.inv;
+    }
   }
   __device__ static const float *input(const Args &a, int) { return a.grad; }
   __device__ static float *output(const Args &a) { return a.dx; }
@@ -445,81 +501,79 @@ struct DxEvalPhase {
   }
 };
 
+// Channel finalize for planes k = wave, wave + 4, ... of the block (wave-uniform loop).  The
+// first plane's loads may already be in flight (pre / have_pre).
+template <class P>
+__device__ __forceinline__ void finish_planes(const PlaneMap &m, const typename P::Args &a,
+                                              uint64_t plane0, uint32_t r0, uint32_t nplanes,
+                                              const typename P::Pre &pre, bool have_pre,
+                                              Cache<P::V> &cache) {
+  for (uint32_t k = threadIdx.x / 64; k < nplanes; k += kMapBlock / 64) {
+    const uint64_t plane = plane0 + k;
+    const uint32_t c = static_cast<uint32_t>(plane % m.channels);
+    const bool designated = plane < m.channels && (k > 0 || r0 == 0);
+    const bool first = k == threadIdx.x / 64;
+    P::finish(a, c, first && have_pre ? pre : P::load(a, m, c), designated, cache, k);
+  }
+}
+
 template <class P>
 __global__ __launch_bounds__(kMapBlock) void bn_map_kernel(PlaneMap m, typename P::Args a) {
   __shared__ Cache<P::V> cache;
-  const uint64_t b = blockIdx.x;
-  uint64_t plane0, e0, e1;
-  uint32_t nplanes;
-  bool first_chunk;
-  if (m.chunks > 0) {
-    plane0 = b / m.chunks;
-    const uint32_t chunk = static_cast<uint32_t>(b - plane0 * m.chunks);
-    e0 = plane0 * m.spatial + static_cast<uint64_t>(chunk) * m.chunk_len;
-    const uint64_t plane_end = (plane0 + 1) * m.spatial;
-    e1 = e0 + m.chunk_len < plane_end ? e0 + m.chunk_len : plane_end;
-    nplanes = 1;
-    first_chunk = chunk == 0;
-  } else {
-    plane0 = b * m.planes_per_block;
-    const uint64_t last =
-        plane0 + m.planes_per_block < m.planes ? plane0 + m.planes_per_block : m.planes;
-    nplanes = static_cast<uint32_t>(last - plane0);
-    e0 = plane0 * m.spatial;
-    e1 = last * m.spatial;
-    first_chunk = true;
-  }
-  for (uint32_t k = threadIdx.x; k < nplanes; k += kMapBlock) {
-    const uint64_t plane = plane0 + k;
-    const uint32_t c = static_cast<uint32_t>(plane % m.channels);
-    P::channel(a, m, c, first_chunk && plane < m.channels, cache, k);
-  }
-  __syncthreads();
+  const uint64_t e0 = static_cast<uint64_t>(blockIdx.x) * m.block_elems;
+  const uint64_t e1 = e0 + m.block_elems < m.total ? e0 + m.block_elems : m.total;
+  const uint64_t plane0 = e0 / m.spatial;
+  const uint32_t r0 = static_cast<uint32_t>(e0 - plane0 * m.spatial);  // offset in plane0
+  const uint32_t nplanes = static_cast<uint32_t>((e1 - 1) / m.spatial - plane0 + 1);
+  const uint32_t n = static_cast<uint32_t>(e1 - e0);
   float *out = P::output(a);
+  // 1) the channel loads of this wave's first plane, 2) the block's data loads, 3) the channel
+  // finalize (its loads return first), 4) the elementwise pass.
+  const uint32_t wave = threadIdx.x / 64;
+  typename P::Pre pre{};
+  const bool have_pre = wave < nplanes;
+  if (have_pre) pre = P::load(a, m, static_cast<uint32_t>((plane0 + wave) % m.channels));
   if (m.vec) {
-    // e0 and e1 are multiples of 4: spatial % 4 == 0 and chunk_len % 4 == 0.
-    const uint32_t n4 = static_cast<uint32_t>((e1 - e0) / 4);
-    const float4 *in4[P::NI];
+    // e0 and r0 are multiples of 4 (spatial % 4 == 0, block_elems % 4 == 0).
+    const uint32_t n4 = n / 4;
+    float4 v[kMapVec][P::NI];
 #pragma unroll
-    for (int i = 0; i < P::NI; ++i)
-      in4[i] = reinterpret_cast<const float4 *>(P::input(a, i) + e0);
-    float4 *out4 = reinterpret_cast<float4 *>(out + e0);
-    for (uint32_t base = 0; base < n4; base += 4 * kMapBlock) {
-      float4 v[4][P::NI];
+    for (int u = 0; u < kMapVec; ++u) {
+      const uint32_t q = threadIdx.x + u * kMapBlock;
+      if (q < n4) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const uint32_t q = base + threadIdx.x + u * kMapBlock;
-        if (q < n4) {
-#pragma unroll
-          for (int i = 0; i < P::NI; ++i) v[u][i] = in4[i][q];
-        }
+        for (int i = 0; i < P::NI; ++i)
+          v[u][i] = reinterpret_cast<const float4 *>(P::input(a, i) + e0)[q];
       }
+    }
+    finish_planes<P>(m, a, plane0, r0, nplanes, pre, have_pre, cache);
+    __syncthreads();
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const uint32_t q = base + threadIdx.x + u * kMapBlock;
-        if (q < n4) {
-          const uint32_t k = m.chunks > 0 ? 0u : oxh::fast_div(q * 4, m.spatial_div);
-          float x0[P::NI], x1[P::NI], x2[P::NI], x3[P::NI];
+    for (int u = 0; u < kMapVec; ++u) {
+      const uint32_t q = threadIdx.x + u * kMapBlock;
+      if (q < n4) {
+        const uint32_t k = oxh::fast_div(r0 + q * 4, m.spatial_div);
+        float x0[P::NI], x1[P::NI], x2[P::NI], x3[P::NI];
 #pragma unroll
-          for (int i = 0; i < P::NI; ++i) {
-            x0[i] = v[u][i].x;
-            x1[i] = v[u][i].y;
-            x2[i] = v[u][i].z;
-            x3[i] = v[u][i].w;
-          }
-          float4 r;
-          r.x = P::element(a, cache, k, x0);
-          r.y = P::element(a, cache, k, x1);
-          r.z = P::element(a, cache, k, x2);
-          r.w = P::element(a, cache, k, x3);
-          out4[q] = r;
+        for (int i = 0; i < P::NI; ++i) {
+          x0[i] = v[u][i].x;
+          x1[i] = v[u][i].y;
+          x2[i] = v[u][i].z;
+          x3[i] = v[u][i].w;
         }
+        float4 r;
+        r.x = P::element(a, cache, k, x0);
+        r.y = P::element(a, cache, k, x1);
+        r.z = P::element(a, cache, k, x2);
+        r.w = P::element(a, cache, k, x3);
+        reinterpret_cast<float4 *>(out + e0)[q] = r;
       }
     }
   } else {
-    const uint32_t n = static_cast<uint32_t>(e1 - e0);
+    finish_planes<P>(m, a, plane0, r0, nplanes, pre, have_pre, cache);
+    __syncthreads();
     for (uint32_t q = threadIdx.x; q < n; q += kMapBlock) {
-      const uint32_t k = m.chunks > 0 ? 0u : oxh::fast_div(q, m.spatial_div);
+      const uint32_t k = oxh::fast_div(r0 + q, m.spatial_div);
       float x[P::NI];
 #pragma unroll
       for (int i = 0; i < P::NI; ++i) x[i] = P::input(a, i)[e0 + q];
@@ -657,7 +711,7 @@ oxh_status oxh_batch_norm_statistics(oxh_stream stream, uint64_t batch, uint64_t
                                   workspace_bytes, &g);
   if (st != OXH_OK) return st;
   StatsOut out{mean, inverse_std, unbiased_variance, nullptr, nullptr, 0.0f, epsilon};
-  hipLaunchKernelGGL(bn_finalize_forward_kernel, dim3(channel_grid(channels)), dim3(256), 0,
+  hipLaunchKernelGGL(bn_finalize_forward_kernel, dim3((channels + 3) / 4), dim3(256), 0,
                      oxh::as_stream(stream), g, input,
                      static_cast<const double2 *>(workspace), out);
   return oxh::launched(name);
@@ -722,7 +776,7 @@ oxh_status oxh_batch_norm_affine_backward(oxh_stream stream, uint64_t batch, uin
   oxh_status st = launch_reduce_gx(name, stream, batch, channels, spatial, gradient, input, mean,
                                    inverse_std, workspace, workspace_bytes, &g);
   if (st != OXH_OK) return st;
-  hipLaunchKernelGGL(bn_finalize_affine_kernel, dim3(channel_grid(channels)), dim3(256), 0,
+  hipLaunchKernelGGL(bn_finalize_affine_kernel, dim3((channels + 3) / 4), dim3(256), 0,
                      oxh::as_stream(stream), g, static_cast<const double2 *>(workspace),
                      weight_gradient, bias_gradient);
   return oxh::launched(name);

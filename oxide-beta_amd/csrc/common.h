@@ -33,10 +33,8 @@ inline hipStream_t as_stream(oxh_stream s) { return reinterpret_cast<hipStream_t
 
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Streaming kernels: 256 threads (4 waves) per block; each thread handles kUnroll float4 per
-// pass, so a block covers 256 * kUnroll * 4 floats.
+// Streaming kernels: 256 threads (4 waves) per block.
 constexpr int kBlock = 256;
-constexpr int kUnroll = 4;
 
 // Number of compute units on gfx950 (MI355X); used to size reductions so that every CU gets
 // several workgroups.

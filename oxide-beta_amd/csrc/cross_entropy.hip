@@ -6,8 +6,8 @@
 // every logit, O(B * C^2).  CPU semantics: evaluation.rs:599-636, autograd.rs:529-554.
 //
 // Design (gfx950): one workgroup per row.  On the register path (classes % 4 == 0, aligned,
-// classes <= 65536) the row is loaded once with 128-bit loads into VGPRs (up to 16 float4 per
-// lane at 1024 lanes), the max and the sum of exp(x - max) are block reductions (wave64
+// classes <= 16 * 4 * OXH_CE_BLOCK) the row is loaded once with 128-bit loads into VGPRs (up to
+// 16 float4 per lane), the max and the sum of exp(x - max) are block reductions (wave64
 // shuffles, then LDS across waves), and the gradient is written from the same registers, so a
 // fused loss+gradient moves exactly one read and one write of the logits.  The per-row losses
 // go to an fp64 workspace vector and a one-block kernel sums them in row order for the mean (no
@@ -26,6 +26,15 @@
 #include "common.h"
 
 namespace {
+
+// Row block shape for wide rows (overridable at build time for tuning sweeps): lanes per row
+// and the minimum waves per SIMD the register budget must allow.
+#ifndef OXH_CE_BLOCK
+#define OXH_CE_BLOCK 512
+#endif
+#ifndef OXH_CE_MINW
+#define OXH_CE_MINW 4
+#endif
 
 struct CeArgs {
   const float *logits, *targets, *outer;  // outer: device scalar (may be null when no grad)
@@ -95,9 +104,11 @@ __global__ __launch_bounds__(kMeanBlock) void ce_mean_kernel(const double *__res
   if (threadIdx.x == 0) *loss = static_cast<float>(s) / static_cast<float>(batch);
 }
 
-// Register path: BLOCK lanes x V float4 hold one row of `classes` (= 4 * c4) logits.
-template <int BLOCK, int V>
-__global__ __launch_bounds__(BLOCK) void ce_row_kernel(CeArgs a) {
+// Register path: BLOCK lanes x V float4 hold one row of `classes` (= 4 * c4) logits.  MINW
+// (waves per SIMD the compiler must allow) bounds the VGPRs so several rows share a CU and one
+// row's memory phase overlaps another's exp / reduction phase.
+template <int BLOCK, int V, int MINW>
+__global__ __launch_bounds__(BLOCK, MINW) void ce_row_kernel(CeArgs a) {
   __shared__ float lds_f[BLOCK / 64];
   __shared__ double lds_d[BLOCK / 64];
   const uint64_t row = blockIdx.x;
@@ -132,6 +143,10 @@ __global__ __launch_bounds__(BLOCK) void ce_row_kernel(CeArgs a) {
   if (!valid && threadIdx.x == 0 && a.error_flag) *a.error_flag = 1u;
   if (a.grad) {
     const float scale = *a.outer / static_cast<float>(a.batch);  // autograd.rs:540-541
+    // p = e / normalizer (autograd.rs:548) as e * (1 / normalizer): within 1.5 ulp of the
+    // correctly rounded quotient, one division per row instead of one per logit.  The target
+    // logit keeps the exact quotient because p - 1 cancels.
+    const float rinv = 1.0f / normalizer;
     float4 *g4 = reinterpret_cast<float4 *>(a.grad + row * a.classes);
 #pragma unroll
     for (int k = 0; k < V; ++k) {
@@ -139,11 +154,20 @@ __global__ __launch_bounds__(BLOCK) void ce_row_kernel(CeArgs a) {
       if (i < c4) {
         float4 r;
         if (valid) {
+          r.x = scale * (v[k].x * rinv);
+          r.y = scale * (v[k].y * rinv);
+          r.z = scale * (v[k].z * rinv);
+          r.w = scale * (v[k].w * rinv);
           const uint64_t e = 4 * i;
-          r.x = scale * (v[k].x / normalizer - (e + 0 == target ? 1.0f : 0.0f));
-          r.y = scale * (v[k].y / normalizer - (e + 1 == target ? 1.0f : 0.0f));
-          r.z = scale * (v[k].z / normalizer - (e + 2 == target ? 1.0f : 0.0f));
-          r.w = scale * (v[k].w / normalizer - (e + 3 == target ? 1.0f : 0.0f));
+          if (target >= e && target < e + 4) {
+            const int t = static_cast<int>(target - e);
+            const float et = t == 0 ? v[k].x : t == 1 ? v[k].y : t == 2 ? v[k].z : v[k].w;
+            const float gt = scale * (et / normalizer - 1.0f);
+            if (t == 0) r.x = gt;
+            else if (t == 1) r.y = gt;
+            else if (t == 2) r.z = gt;
+            else r.w = gt;
+          }
         } else {
           r = make_float4(NAN, NAN, NAN, NAN);
         }
@@ -219,18 +243,22 @@ oxh_status launch_ce(const char *name, oxh_stream stream, CeArgs a, void *worksp
   const bool vec = a.classes % 4 == 0 && oxh::aligned16(a.logits) &&
                    (!a.grad || oxh::aligned16(a.grad));
   const uint64_t c4 = a.classes / 4;
+  constexpr int B = OXH_CE_BLOCK, W = OXH_CE_MINW;
   if (vec && c4 <= 256) {
-    hipLaunchKernelGGL((ce_row_kernel<256, 1>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((ce_row_kernel<256, 1, 2>), grid, dim3(256), 0, s, a);
   } else if (vec && c4 <= 256 * 4) {
-    hipLaunchKernelGGL((ce_row_kernel<256, 4>), grid, dim3(256), 0, s, a);
-  } else if (vec && c4 <= 1024 * 2) {
-    hipLaunchKernelGGL((ce_row_kernel<1024, 2>), grid, dim3(1024), 0, s, a);
-  } else if (vec && c4 <= 1024 * 4) {
-    hipLaunchKernelGGL((ce_row_kernel<1024, 4>), grid, dim3(1024), 0, s, a);
-  } else if (vec && c4 <= 1024 * 8) {
-    hipLaunchKernelGGL((ce_row_kernel<1024, 8>), grid, dim3(1024), 0, s, a);
-  } else if (vec && c4 <= 1024 * 16) {
-    hipLaunchKernelGGL((ce_row_kernel<1024, 16>), grid, dim3(1024), 0, s, a);
+    hipLaunchKernelGGL((ce_row_kernel<256, 4, 2>), grid, dim3(256), 0, s, a);
+  } else if (vec && c4 <= B * 2) {
+    hipLaunchKernelGGL((ce_row_kernel<B, 2, W>), grid, dim3(B), 0, s, a);
+  } else if (vec && c4 <= B * 4) {
+    hipLaunchKernelGGL((ce_row_kernel<B, 4, W>), grid, dim3(B), 0, s, a);
+  } else if (vec && c4 <= B * 8) {
+    hipLaunchKernelGGL((ce_row_kernel<B, 8, W>), grid, dim3(B), 0, s, a);
+  } else if (vec && c4 <= B * 16) {
+    hipLaunchKernelGGL((ce_row_kernel<B, 16, (W > 4 ? 4 : W)>), grid, dim3(B), 0, s, a);
+  } else if (vec && B <= 256 && c4 <= B * 32) {
+    if constexpr (B <= 256)
+      hipLaunchKernelGGL((ce_row_kernel<B, 32, (W > 2 ? 2 : W)>), grid, dim3(B), 0, s, a);
   } else {
     hipLaunchKernelGGL(ce_row_general_kernel, grid, dim3(kGenBlock), 0, s, a);
   }

@@ -3,8 +3,9 @@
 //
 // Reference kernels: kernel_module.rs:8-34 (add, mul, relu), 492-508 (mul_backward,
 // relu_backward), 1052-1059 (accumulate).  The reference launches one thread per element with
-// scalar 4-byte loads; here every thread moves kUnroll 128-bit vectors per input per pass, so
-// each wave issues 1 KiB-wide fully coalesced loads and keeps several in flight.  Every
+// scalar 4-byte loads; here every thread moves kUnroll 128-bit vectors per stream, so each wave
+// issues 1 KiB-wide fully coalesced loads.  On MI355X many short blocks (one float4 per lane)
+// stream faster than fewer blocks with long per-lane loops (measured best: 2).  Every
 // operation is a single IEEE fp32 add, multiply or compare per element (no contraction), so the
 // results are bit-identical to the reference's CPU path (evaluation.rs:21-34,
 // autograd.rs:94-147).
@@ -13,6 +14,11 @@
 #include "common.h"
 
 namespace {
+
+#ifndef OXH_EW_UNROLL
+#define OXH_EW_UNROLL 2  // float4 per thread per stream (overridable for tuning sweeps)
+#endif
+constexpr int kUnroll = OXH_EW_UNROLL;
 
 template <int NI, int NO>
 struct MapArgs {
@@ -92,19 +98,19 @@ template <class Op>
 __global__ __launch_bounds__(oxh::kBlock) void map_vec4_kernel(
     MapArgs<Op::NI, Op::NO> args, uint64_t n4, uint64_t n) {
   constexpr int NI = Op::NI, NO = Op::NO;
-  const uint64_t tile = static_cast<uint64_t>(oxh::kBlock) * oxh::kUnroll;
+  const uint64_t tile = static_cast<uint64_t>(oxh::kBlock) * kUnroll;
   const uint64_t tiles = (n4 + tile - 1) / tile;
   for (uint64_t t = blockIdx.x; t < tiles; t += gridDim.x) {
     const uint64_t base = t * tile + threadIdx.x;
-    float4 in[oxh::kUnroll][NI];
-    if (base + (oxh::kUnroll - 1) * oxh::kBlock < n4) {
+    float4 in[kUnroll][NI];
+    if (base + (kUnroll - 1) * oxh::kBlock < n4) {
 #pragma unroll
-      for (int u = 0; u < oxh::kUnroll; ++u)
+      for (int u = 0; u < kUnroll; ++u)
 #pragma unroll
         for (int i = 0; i < NI; ++i)
           in[u][i] = reinterpret_cast<const float4 *>(args.in[i])[base + u * oxh::kBlock];
 #pragma unroll
-      for (int u = 0; u < oxh::kUnroll; ++u) {
+      for (int u = 0; u < kUnroll; ++u) {
         float4 out[NO];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -120,7 +126,7 @@ __global__ __launch_bounds__(oxh::kBlock) void map_vec4_kernel(
           reinterpret_cast<float4 *>(args.out[o])[base + u * oxh::kBlock] = out[o];
       }
     } else {
-      for (int u = 0; u < oxh::kUnroll; ++u) {
+      for (int u = 0; u < kUnroll; ++u) {
         const uint64_t idx = base + u * oxh::kBlock;
         if (idx >= n4) break;
         float4 v[NI], out[NO];
@@ -170,7 +176,7 @@ __global__ __launch_bounds__(oxh::kBlock) void map_scalar_kernel(
   }
 }
 
-constexpr uint64_t kMaxGrid = 1u << 20;
+constexpr uint64_t kMaxGrid = 1u << 24;
 
 template <class Op>
 oxh_status launch_map(const char *name, oxh_stream stream, const MapArgs<Op::NI, Op::NO> &args,
@@ -195,7 +201,7 @@ oxh_status launch_map(const char *name, oxh_stream stream, const MapArgs<Op::NI,
   hipStream_t s = oxh::as_stream(stream);
   if (vec) {
     const uint64_t n4 = n / 4;
-    const uint64_t tile = static_cast<uint64_t>(oxh::kBlock) * oxh::kUnroll;
+    const uint64_t tile = static_cast<uint64_t>(oxh::kBlock) * kUnroll;
     uint64_t grid = (n4 + tile - 1) / tile;
     if (grid == 0) grid = 1;
     if (grid > kMaxGrid) grid = kMaxGrid;

@@ -146,6 +146,13 @@ def lib() -> ctypes.CDLL:
     """Loads liboxide_hip.so (built by ``__graft_entry__.build()`` / ``make``)."""
     global _lib
     if _lib is None:
+        # Tensors and streams handed to the C ABI come from torch, so the library must bind to
+        # the HIP runtime torch loaded (same SONAME): import torch first.  Loading the library
+        # first would bring in a second HIP runtime that torch then fails to initialise.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         if not LIB_PATH.exists():
             raise OxideError(HIP_ERROR, f"{LIB_PATH} is not built; run __graft_entry__.build()")
         handle = ctypes.CDLL(os.fspath(LIB_PATH))
