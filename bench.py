@@ -12,9 +12,10 @@ written by the input backward).  ``value`` = 8T / step time in GB/s, inputs resi
 MALL (256 MB last-level cache) is defeated for the headline: steps rotate over 4 independent
 input/output sets (1.6 GB), so each step's x and g were last touched three steps (1.2 GB of
 traffic) earlier.  The headline step time is a hipGraph replay (the four steps captured once,
-as a fixed plan is deployed); per-kernel durations for the roofline come from HIP events
-recorded between eager launches on the launch stream inside a second timed region, and the
-eager time without those events is reported beside it.
+as a fixed plan is deployed).  Per-kernel durations for the roofline come from HIP events
+that each dispatch records at its own start and end (oxh_time_next_launch, i.e.
+hipExtLaunchKernelGGL) inside a second, eager timed region; the eager step time is reported
+beside the graph one.
 
 The other configs (elementwise chain + JIT-plan replay, cross entropy, AdamW) are measured
 after the headline and reported under "extra" in the same line.  ``cpu_baseline`` times the
@@ -83,42 +84,43 @@ def bench_batch_norm(m, steps: int, warmup: int, sets: int = 4):
     bytes_per = {"bn_forward_reduce": T_BN, "bn_forward_apply": 2 * T_BN,
                  "bn_backward_reduce": 2 * T_BN, "bn_backward_input": 3 * T_BN}
 
-    def step(i, ev=None):
+    def step(i, timers=None):
         k = i % sets
         x, g, y, dx = xs[k], gs[k], ys[k], dxs[k]
-        if ev:
-            ev[0].record(s)
+        if timers:
+            timers[0].arm()
         m.batch_norm_forward_reduce(x, stream=s)
-        if ev:
-            ev[1].record(s)
+        if timers:
+            timers[1].arm()
         m.batch_norm_forward_apply(x, gamma, beta, rm, rv, mean, inv, y, 0.1, 1e-5, stream=s)
-        if ev:
-            ev[2].record(s)
+        if timers:
+            timers[2].arm()
         m.batch_norm_backward_reduce(g, x, mean, inv, stream=s)
-        if ev:
-            ev[3].record(s)
+        if timers:
+            timers[3].arm()
         m.batch_norm_backward_input(g, x, gamma, mean, inv, dx, dw, db, stream=s)
-        if ev:
-            ev[4].record(s)
+
+    import oxide_hip as ox
 
     for i in range(warmup):
         step(i)
     s.synchronize()
-    evs = [_events(5) for _ in range(steps)]
+    # per-kernel durations: each dispatch records its own start / stop events
+    timers = [[ox.KernelTimer() for _ in names] for _ in range(steps)]
     start, stop = _events(2)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     start.record(s)
     for i in range(steps):
-        step(warmup + i, evs[i])
+        step(warmup + i, timers[i])
     stop.record(s)
     s.synchronize()
     wall = time.perf_counter() - t0
     total_ms = start.elapsed_time(stop)
     per_kernel = {nm: [] for nm in names}
-    for ev in evs:
+    for tm in timers:
         for j, nm in enumerate(names):
-            per_kernel[nm].append(ev[j].elapsed_time(ev[j + 1]))
+            per_kernel[nm].append(tm[j].elapsed_ms())
     kernels = {}
     for nm in names:
         avg_ms = sum(per_kernel[nm]) / len(per_kernel[nm])
@@ -135,8 +137,6 @@ def bench_batch_norm(m, steps: int, warmup: int, sets: int = 4):
     s.synchronize()
     eager_ms = e_start.elapsed_time(e_stop) / steps
     # headline: the step captured once per input set into one hipGraph and replayed
-    import oxide_hip as ox
-
     graph = ox.HipGraphExec.capture(s, lambda: [step(k) for k in range(sets)])
     replays = max(1, steps // sets)
     graph.launch(s)
@@ -295,6 +295,21 @@ def bench_adamw(m, reps: int = 10):
             "frac_of_peak": round(7 * n * 4 / us / 1e3 / PEAK_HBM_GBS, 3)}
 
 
+def copy_calibration():
+    """Three 1 GiB device-to-device copies (hipMemcpyAsync's blit kernel): a plain copy of
+    known traffic (1 GiB read + 1 GiB written per launch) for scaling HBM counters."""
+    import torch
+
+    import oxide_hip as ox
+
+    src = torch.zeros(1 << 28, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        ox.check(ox.lib().oxh_memcpy_d2d_async(dst.data_ptr(), src.data_ptr(), 1 << 30, 0))
+    torch.cuda.synchronize()
+
+
 def cpu_baseline(budget_s: float = 12.0):
     """The oracle (single-threaded C restatement of the reference CPU path) on one full BN
     step at config 2: forward (statistics, running update, apply) + backward."""
@@ -330,6 +345,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-extra", action="store_true", help="headline BN config only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a 1 GiB device-to-device copy (3 launches) whose known "
+                         "traffic calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the hot path has no multi-GPU "
@@ -384,6 +402,8 @@ def main():
         "cpu_baseline": None if args.no_cpu else cpu_baseline(),
         "extra": extra,
     }
+    if args.copy_calibration:
+        copy_calibration()
     print(json.dumps(out), flush=True)
 
 

@@ -200,7 +200,7 @@ oxh_status oxh_adamw(oxh_stream stream, float learning_rate, float weight_decay,
                   new_parameter, new_first_moment, new_second_moment};
   uint64_t grid = (n + kChunk - 1) / kChunk;
   if (grid > 0x7FFFFFFFull) grid = 0x7FFFFFFFull;
-  hipLaunchKernelGGL(adamw_kernel, dim3(static_cast<uint32_t>(grid)), dim3(oxh::kBlock), 0,
+  oxh::launch(adamw_kernel, dim3(static_cast<uint32_t>(grid)), dim3(oxh::kBlock), 0,
                      oxh::as_stream(stream), h, s, n, vec);
   return oxh::launched("oxh_adamw");
 }
@@ -257,7 +257,7 @@ oxh_status oxh_adamw_multi_tensor(oxh_stream stream, float learning_rate, float 
     if (k == 0) continue;
     table.count = k;
     table.first_chunk[k] = static_cast<uint32_t>(chunks);
-    hipLaunchKernelGGL(adamw_multi_kernel, dim3(static_cast<uint32_t>(chunks)),
+    oxh::launch(adamw_multi_kernel, dim3(static_cast<uint32_t>(chunks)),
                        dim3(oxh::kBlock), 0, oxh::as_stream(stream), h, table);
     oxh_status st = oxh::launched("oxh_adamw_multi_tensor");
     if (st != OXH_OK) return st;

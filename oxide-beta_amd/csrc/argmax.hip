@@ -70,7 +70,7 @@ extern "C" oxh_status oxh_argmax_rows(oxh_stream stream, uint64_t rows, uint64_t
   OXH_REQUIRE(logits && indices, OXH_INVALID_SHAPE, "oxh_argmax_rows: null pointer");
   OXH_REQUIRE(rows < (1ull << 33), OXH_INVALID_SHAPE, "oxh_argmax_rows: too many rows");
   const uint64_t grid = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
-  hipLaunchKernelGGL(argmax_kernel, dim3(static_cast<uint32_t>(grid)), dim3(64 * kRowsPerBlock),
+  oxh::launch(argmax_kernel, dim3(static_cast<uint32_t>(grid)), dim3(64 * kRowsPerBlock),
                      0, oxh::as_stream(stream), rows, classes, logits, indices);
   return oxh::launched("oxh_argmax_rows");
 }

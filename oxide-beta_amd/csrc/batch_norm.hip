@@ -651,7 +651,7 @@ oxh_status launch_reduce_x(const char *name, oxh_stream stream, uint64_t batch,
   OXH_REQUIRE(!oxh::any_overlap(workspace, workspace_bytes_for(g), input,
                                 batch * channels * spatial * 4),
               OXH_INVALID_SHAPE, std::string(name) + ": workspace overlaps the input");
-  hipLaunchKernelGGL(bn_reduce_x_kernel, dim3(g.slices, g.channels), dim3(kRedBlock), 0,
+  oxh::launch(bn_reduce_x_kernel, dim3(g.slices, g.channels), dim3(kRedBlock), 0,
                      oxh::as_stream(stream), g, input, static_cast<double2 *>(workspace));
   if (geometry) *geometry = g;
   return oxh::launched(name);
@@ -669,7 +669,7 @@ oxh_status launch_reduce_gx(const char *name, oxh_stream stream, uint64_t batch,
                                    oxh::aligned16(input) && oxh::aligned16(gradient));
   st = check_workspace(name, g, workspace, workspace_bytes);
   if (st != OXH_OK) return st;
-  hipLaunchKernelGGL(bn_reduce_gx_kernel, dim3(g.slices, g.channels), dim3(kRedBlock), 0,
+  oxh::launch(bn_reduce_gx_kernel, dim3(g.slices, g.channels), dim3(kRedBlock), 0,
                      oxh::as_stream(stream), g, gradient, input, mean, inverse_std,
                      static_cast<double2 *>(workspace));
   if (geometry) *geometry = g;
@@ -680,7 +680,7 @@ template <class P>
 oxh_status launch_map(const char *name, oxh_stream stream, uint64_t batch, uint64_t channels,
                       uint64_t spatial, bool aligned, const typename P::Args &a) {
   const PlaneMap m = make_plane_map(batch, channels, spatial, aligned);
-  hipLaunchKernelGGL(bn_map_kernel<P>, dim3(static_cast<uint32_t>(m.blocks)), dim3(kMapBlock),
+  oxh::launch(bn_map_kernel<P>, dim3(static_cast<uint32_t>(m.blocks)), dim3(kMapBlock),
                      0, oxh::as_stream(stream), m, a);
   return oxh::launched(name);
 }
@@ -711,7 +711,7 @@ oxh_status oxh_batch_norm_statistics(oxh_stream stream, uint64_t batch, uint64_t
                                   workspace_bytes, &g);
   if (st != OXH_OK) return st;
   StatsOut out{mean, inverse_std, unbiased_variance, nullptr, nullptr, 0.0f, epsilon};
-  hipLaunchKernelGGL(bn_finalize_forward_kernel, dim3((channels + 3) / 4), dim3(256), 0,
+  oxh::launch(bn_finalize_forward_kernel, dim3((channels + 3) / 4), dim3(256), 0,
                      oxh::as_stream(stream), g, input,
                      static_cast<const double2 *>(workspace), out);
   return oxh::launched(name);
@@ -726,7 +726,7 @@ oxh_status oxh_batch_norm_update_running(oxh_stream stream, uint64_t channels, f
   OXH_REQUIRE(batch_mean && batch_variance && old_mean && old_variance && new_mean &&
                   new_variance,
               OXH_INVALID_SHAPE, "oxh_batch_norm_update_running: null pointer");
-  hipLaunchKernelGGL(bn_update_running_kernel, dim3(channel_grid(channels)), dim3(256), 0,
+  oxh::launch(bn_update_running_kernel, dim3(channel_grid(channels)), dim3(256), 0,
                      oxh::as_stream(stream), static_cast<uint32_t>(channels), momentum,
                      batch_mean, batch_variance, old_mean, old_variance, new_mean,
                      new_variance);
@@ -740,7 +740,7 @@ oxh_status oxh_batch_norm_running_inverse_std(oxh_stream stream, uint64_t channe
   OXH_REQUIRE(channels <= 65535, OXH_INVALID_SHAPE, "too many channels");
   OXH_REQUIRE(variance && inverse_std, OXH_INVALID_SHAPE,
               "oxh_batch_norm_running_inverse_std: null pointer");
-  hipLaunchKernelGGL(bn_running_inverse_std_kernel, dim3(channel_grid(channels)), dim3(256), 0,
+  oxh::launch(bn_running_inverse_std_kernel, dim3(channel_grid(channels)), dim3(256), 0,
                      oxh::as_stream(stream), static_cast<uint32_t>(channels), epsilon, variance,
                      inverse_std);
   return oxh::launched("oxh_batch_norm_running_inverse_std");
@@ -776,7 +776,7 @@ oxh_status oxh_batch_norm_affine_backward(oxh_stream stream, uint64_t batch, uin
   oxh_status st = launch_reduce_gx(name, stream, batch, channels, spatial, gradient, input, mean,
                                    inverse_std, workspace, workspace_bytes, &g);
   if (st != OXH_OK) return st;
-  hipLaunchKernelGGL(bn_finalize_affine_kernel, dim3((channels + 3) / 4), dim3(256), 0,
+  oxh::launch(bn_finalize_affine_kernel, dim3((channels + 3) / 4), dim3(256), 0,
                      oxh::as_stream(stream), g, static_cast<const double2 *>(workspace),
                      weight_gradient, bias_gradient);
   return oxh::launched(name);

@@ -4,6 +4,7 @@
 // geometry used by the streaming kernels.  gfx950 only: wave64, 256 CUs in 8 XCDs.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -70,6 +71,28 @@ inline FastDiv make_fastdiv(uint32_t d) {
 
 __device__ __forceinline__ uint32_t fast_div(uint32_t n, const FastDiv &f) {
   return (__umulhi(n, f.mul) + n) >> f.shift;
+}
+
+// Kernel timing hook: oxh_time_next_launch arms the calling thread's next kernel launch to
+// record a start / stop event pair around the dispatch itself (hipExtLaunchKernelGGL), the
+// same interval a kernel-trace profiler reports.
+struct LaunchEvents {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+LaunchEvents &armed_launch_events();
+
+template <typename Kernel, typename... Args>
+inline void launch(Kernel kernel, dim3 grid, dim3 block, uint32_t shared_bytes,
+                   hipStream_t stream, Args... args) {
+  LaunchEvents &armed = armed_launch_events();
+  if (armed.start != nullptr || armed.stop != nullptr) {
+    const LaunchEvents ev = armed;
+    armed = LaunchEvents{};
+    hipExtLaunchKernelGGL(kernel, grid, block, shared_bytes, stream, ev.start, ev.stop, 0u,
+                          args...);
+  } else {
+    hipLaunchKernelGGL(kernel, grid, block, shared_bytes, stream, args...);
+  }
 }
 
 }  // namespace oxh

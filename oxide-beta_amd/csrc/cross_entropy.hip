@@ -245,26 +245,26 @@ oxh_status launch_ce(const char *name, oxh_stream stream, CeArgs a, void *worksp
   const uint64_t c4 = a.classes / 4;
   constexpr int B = OXH_CE_BLOCK, W = OXH_CE_MINW;
   if (vec && c4 <= 256) {
-    hipLaunchKernelGGL((ce_row_kernel<256, 1, 2>), grid, dim3(256), 0, s, a);
+    oxh::launch((ce_row_kernel<256, 1, 2>), grid, dim3(256), 0, s, a);
   } else if (vec && c4 <= 256 * 4) {
-    hipLaunchKernelGGL((ce_row_kernel<256, 4, 2>), grid, dim3(256), 0, s, a);
+    oxh::launch((ce_row_kernel<256, 4, 2>), grid, dim3(256), 0, s, a);
   } else if (vec && c4 <= B * 2) {
-    hipLaunchKernelGGL((ce_row_kernel<B, 2, W>), grid, dim3(B), 0, s, a);
+    oxh::launch((ce_row_kernel<B, 2, W>), grid, dim3(B), 0, s, a);
   } else if (vec && c4 <= B * 4) {
-    hipLaunchKernelGGL((ce_row_kernel<B, 4, W>), grid, dim3(B), 0, s, a);
+    oxh::launch((ce_row_kernel<B, 4, W>), grid, dim3(B), 0, s, a);
   } else if (vec && c4 <= B * 8) {
-    hipLaunchKernelGGL((ce_row_kernel<B, 8, W>), grid, dim3(B), 0, s, a);
+    oxh::launch((ce_row_kernel<B, 8, W>), grid, dim3(B), 0, s, a);
   } else if (vec && c4 <= B * 16) {
-    hipLaunchKernelGGL((ce_row_kernel<B, 16, (W > 4 ? 4 : W)>), grid, dim3(B), 0, s, a);
+    oxh::launch((ce_row_kernel<B, 16, (W > 4 ? 4 : W)>), grid, dim3(B), 0, s, a);
   } else if (vec && B <= 256 && c4 <= B * 32) {
     if constexpr (B <= 256)
-      hipLaunchKernelGGL((ce_row_kernel<B, 32, (W > 2 ? 2 : W)>), grid, dim3(B), 0, s, a);
+      oxh::launch((ce_row_kernel<B, 32, (W > 2 ? 2 : W)>), grid, dim3(B), 0, s, a);
   } else {
-    hipLaunchKernelGGL(ce_row_general_kernel, grid, dim3(kGenBlock), 0, s, a);
+    oxh::launch(ce_row_general_kernel, grid, dim3(kGenBlock), 0, s, a);
   }
   oxh_status st = oxh::launched(name);
   if (st != OXH_OK || a.loss == nullptr) return st;
-  hipLaunchKernelGGL(ce_mean_kernel, dim3(1), dim3(kMeanBlock), 0, s, a.row_loss, a.batch,
+  oxh::launch(ce_mean_kernel, dim3(1), dim3(kMeanBlock), 0, s, a.row_loss, a.batch,
                      a.loss);
   return oxh::launched(name);
 }

@@ -205,12 +205,12 @@ oxh_status launch_map(const char *name, oxh_stream stream, const MapArgs<Op::NI,
     uint64_t grid = (n4 + tile - 1) / tile;
     if (grid == 0) grid = 1;
     if (grid > kMaxGrid) grid = kMaxGrid;
-    hipLaunchKernelGGL(map_vec4_kernel<Op>, dim3(static_cast<uint32_t>(grid)), dim3(oxh::kBlock),
+    oxh::launch(map_vec4_kernel<Op>, dim3(static_cast<uint32_t>(grid)), dim3(oxh::kBlock),
                        0, s, args, n4, n);
   } else {
     uint64_t grid = (n + oxh::kBlock - 1) / oxh::kBlock;
     if (grid > kMaxGrid) grid = kMaxGrid;
-    hipLaunchKernelGGL(map_scalar_kernel<Op>, dim3(static_cast<uint32_t>(grid)),
+    oxh::launch(map_scalar_kernel<Op>, dim3(static_cast<uint32_t>(grid)),
                        dim3(oxh::kBlock), 0, s, args, n);
   }
   return oxh::launched(name);

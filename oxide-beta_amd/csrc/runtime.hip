@@ -26,6 +26,11 @@ oxh_status ok() {
   return OXH_OK;
 }
 
+LaunchEvents &armed_launch_events() {
+  thread_local LaunchEvents armed;
+  return armed;
+}
+
 }  // namespace oxh
 
 struct oxh_graph {
@@ -120,6 +125,37 @@ oxh_status oxh_memcpy_d2d_async(void *dst, const void *src, uint64_t bytes, oxh_
   OXH_REQUIRE(dst != nullptr && src != nullptr, OXH_INVALID_SHAPE, "null pointer");
   OXH_HIP_CHECK(
       hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, oxh::as_stream(stream)));
+  return oxh::ok();
+}
+
+// ---------------------------------------------------------------- kernel timing
+
+oxh_status oxh_event_create(oxh_event *event) {
+  OXH_REQUIRE(event != nullptr, OXH_INVALID_SHAPE, "event is null");
+  hipEvent_t e = nullptr;
+  OXH_HIP_CHECK(hipEventCreate(&e));
+  *event = e;
+  return oxh::ok();
+}
+
+oxh_status oxh_event_destroy(oxh_event event) {
+  if (event == nullptr) return oxh::ok();
+  OXH_HIP_CHECK(hipEventDestroy(static_cast<hipEvent_t>(event)));
+  return oxh::ok();
+}
+
+oxh_status oxh_event_elapsed_ms(oxh_event start, oxh_event stop, float *ms) {
+  OXH_REQUIRE(start && stop && ms, OXH_INVALID_SHAPE, "null argument");
+  OXH_HIP_CHECK(hipEventSynchronize(static_cast<hipEvent_t>(stop)));
+  OXH_HIP_CHECK(
+      hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)));
+  return oxh::ok();
+}
+
+oxh_status oxh_time_next_launch(oxh_event start, oxh_event stop) {
+  OXH_REQUIRE(start != nullptr || stop != nullptr, OXH_INVALID_SHAPE, "no event given");
+  oxh::armed_launch_events() =
+      oxh::LaunchEvents{static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)};
   return oxh::ok();
 }
 

@@ -79,6 +79,10 @@ _SIGNATURES = {
     "oxh_memcpy_h2d_async": (_st, [_vp, _vp, _u64, _vp]),
     "oxh_memcpy_d2h": (_st, [_vp, _vp, _u64, _vp]),
     "oxh_memcpy_d2d_async": (_st, [_vp, _vp, _u64, _vp]),
+    "oxh_event_create": (_st, [ctypes.POINTER(_vp)]),
+    "oxh_event_destroy": (_st, [_vp]),
+    "oxh_event_elapsed_ms": (_st, [_vp, _vp, ctypes.POINTER(_f32)]),
+    "oxh_time_next_launch": (_st, [_vp, _vp]),
     "oxh_add": (_st, [_vp, _vp, _vp, _vp, _u64]),
     "oxh_mul": (_st, [_vp, _vp, _vp, _vp, _u64]),
     "oxh_relu": (_st, [_vp, _vp, _vp, _u64]),
@@ -247,6 +251,29 @@ def adamw_corrections(beta1: float, beta2: float, step: int) -> tuple[float, flo
     c1, c2 = _f32(), _f32()
     check(lib().oxh_adamw_corrections(beta1, beta2, step, ctypes.byref(c1), ctypes.byref(c2)))
     return c1.value, c2.value
+
+
+class KernelTimer:
+    """Start / stop events around single kernel dispatches (``oxh_time_next_launch``)."""
+
+    def __init__(self):
+        self.start, self.stop = _vp(), _vp()
+        check(lib().oxh_event_create(ctypes.byref(self.start)))
+        check(lib().oxh_event_create(ctypes.byref(self.stop)))
+
+    def arm(self) -> None:
+        """The calling thread's next kernel launch records this timer's events."""
+        check(lib().oxh_time_next_launch(self.start, self.stop))
+
+    def elapsed_ms(self) -> float:
+        ms = _f32()
+        check(lib().oxh_event_elapsed_ms(self.start, self.stop, ctypes.byref(ms)))
+        return ms.value
+
+    def __del__(self):
+        if _lib is not None:
+            _lib.oxh_event_destroy(self.start)
+            _lib.oxh_event_destroy(self.stop)
 
 
 def init(device: int = 0) -> None:

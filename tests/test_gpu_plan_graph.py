@@ -128,3 +128,20 @@ def test_graph_replay_of_training_ops_matches_eager(module, dev):
         _ = torch.randn(1000, device=dev).sum().item()  # unrelated eager work between replays
         for k in eager:
             assert torch.equal(eager[k], graphed[k]), (replay, k)
+
+
+def test_kernel_timer_brackets_one_dispatch(module, dev):
+    """oxh_time_next_launch: the armed launch records its own start / stop events; the next
+    launch is not timed."""
+    x = torch.randn(1 << 24, device=dev)
+    y = torch.empty_like(x)
+    torch.cuda.synchronize()
+    t = ox.KernelTimer()
+    t.arm()
+    module.relu(x, y)
+    ms = t.elapsed_ms()
+    assert 0.0 < ms < 50.0
+    module.relu(x, y)  # not armed: the timer keeps its first interval
+    torch.cuda.synchronize()
+    assert t.elapsed_ms() == ms
+    assert torch.equal(y, torch.relu(x))
