@@ -9,7 +9,8 @@
 //   p'     = p - lr*((first/c1) / (sqrt(second/c2) + eps) + wd*p)
 // built with -ffp-contract=off and IEEE (correctly rounded) division and square root, so the
 // result is bit-identical to the CPU path.  Traffic: 4 reads + 3 writes of 4 bytes per element,
-// all as 128-bit accesses.
+// all as 128-bit accesses with the non-temporal hint (every byte is touched once per step;
+// measured on MI355X: 5.93 TB/s with the hint on loads and stores, 5.40 TB/s without).
 #include <hip/hip_runtime.h>
 
 #include <cstring>
@@ -22,7 +23,19 @@ namespace {
 #ifndef OXH_ADAMW_UNROLL
 #define OXH_ADAMW_UNROLL 2  // float4 per thread per stream (overridable for tuning sweeps)
 #endif
+#ifndef OXH_ADAMW_NT
+#define OXH_ADAMW_NT 3  // 1: non-temporal loads, 2: non-temporal stores, 3: both
+#endif
 constexpr int kUnroll = OXH_ADAMW_UNROLL;
+
+__device__ __forceinline__ float4 ld(const float4 *p) {
+  if constexpr ((OXH_ADAMW_NT & 1) != 0) return oxh::load_nt(p);
+  else return *p;
+}
+__device__ __forceinline__ void st(float4 *p, const float4 &v) {
+  if constexpr ((OXH_ADAMW_NT & 2) != 0) oxh::store_nt(p, v);
+  else *p = v;
+}
 
 struct Hyper {
   float lr, wd, b1, b2, c1, c2, eps;
@@ -70,26 +83,26 @@ __device__ __forceinline__ void adamw_range(const Hyper &h, const Streams &s, ui
       float4 p[kUnroll], g[kUnroll], m[kUnroll], v[kUnroll];
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
-        p[u] = p4[i + u * oxh::kBlock];
-        g[u] = g4[i + u * oxh::kBlock];
-        m[u] = m4[i + u * oxh::kBlock];
-        v[u] = v4[i + u * oxh::kBlock];
+        p[u] = ld(&p4[i + u * oxh::kBlock]);
+        g[u] = ld(&g4[i + u * oxh::kBlock]);
+        m[u] = ld(&m4[i + u * oxh::kBlock]);
+        v[u] = ld(&v4[i + u * oxh::kBlock]);
       }
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
         float4 po, mo, vo;
         adamw_vec(h, p[u], g[u], m[u], v[u], po, mo, vo);
-        po4[i + u * oxh::kBlock] = po;
-        mo4[i + u * oxh::kBlock] = mo;
-        vo4[i + u * oxh::kBlock] = vo;
+        st(&po4[i + u * oxh::kBlock], po);
+        st(&mo4[i + u * oxh::kBlock], mo);
+        st(&vo4[i + u * oxh::kBlock], vo);
       }
     }
     for (; i < e4; i += oxh::kBlock) {
       float4 po, mo, vo;
-      adamw_vec(h, p4[i], g4[i], m4[i], v4[i], po, mo, vo);
-      po4[i] = po;
-      mo4[i] = mo;
-      vo4[i] = vo;
+      adamw_vec(h, ld(&p4[i]), ld(&g4[i]), ld(&m4[i]), ld(&v4[i]), po, mo, vo);
+      st(&po4[i], po);
+      st(&mo4[i], mo);
+      st(&vo4[i], vo);
     }
     begin = e4 * 4;
   }

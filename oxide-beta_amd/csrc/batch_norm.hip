@@ -43,6 +43,9 @@ namespace {
 #ifndef OXH_BN_RED_UNROLL
 #define OXH_BN_RED_UNROLL 4  // float4 loads in flight per thread per stream in a reduce pass
 #endif
+#ifndef OXH_BN_NT_STORE
+#define OXH_BN_NT_STORE 3  // non-temporal stores: 1 = apply's y, 2 = input backward's dx
+#endif
 #ifndef OXH_BN_MAP_VEC
 #define OXH_BN_MAP_VEC 2  // float4 per thread per stream in a map block
 #endif
@@ -361,7 +364,7 @@ struct Cache {
 // Forward apply.  Channel values: mean, inv, w, b.  Statistics come from the partials
 // (finalize + apply) or from mean / inverse_std arrays (the reference's separate apply).
 struct ApplyPhase {
-  static constexpr int V = 4, NI = 1;
+  static constexpr int V = 4, NI = 1, kNtStoreBit = 1;
   struct Args {
     const float *x, *weight, *bias;
     const float *mean, *inverse_std;  // used when partial == null
@@ -416,7 +419,7 @@ struct ApplyPhase {
 
 // Training input backward.  Channel values: mean, inv, (w * inv) / M, sum g, sum g * x_hat.
 struct DxTrainPhase {
-  static constexpr int V = 5, NI = 2;  // in[0] = g, in[1] = x
+  static constexpr int V = 5, NI = 2, kNtStoreBit = 2;  // in[0] = g, in[1] = x
   struct Args {
     const float *grad, *x, *weight, *mean, *inverse_std;
     const float *weight_gradient, *bias_gradient;  // used when partial == null
@@ -475,7 +478,7 @@ struct DxTrainPhase {
 
 // Eval input backward: dx = (g * w) * inv (autograd.rs:374-378).
 struct DxEvalPhase {
-  static constexpr int V = 2, NI = 1;
+  static constexpr int V = 2, NI = 1, kNtStoreBit = 2;
   struct Args {
     const float *grad, *weight, *inverse_std;
     float *dx;
@@ -566,7 +569,10 @@ __global__ __launch_bounds__(kMapBlock) void bn_map_kernel(PlaneMap m, typename 
         r.y = P::element(a, cache, k, x1);
         r.z = P::element(a, cache, k, x2);
         r.w = P::element(a, cache, k, x3);
-        reinterpret_cast<float4 *>(out + e0)[q] = r;
+        if constexpr ((OXH_BN_NT_STORE & P::kNtStoreBit) != 0)
+          oxh::store_nt(reinterpret_cast<float4 *>(out + e0) + q, r);
+        else
+          reinterpret_cast<float4 *>(out + e0)[q] = r;
       }
     }
   } else {

@@ -73,6 +73,17 @@ __device__ __forceinline__ uint32_t fast_div(uint32_t n, const FastDiv &f) {
   return (__umulhi(n, f.mul) + n) >> f.shift;
 }
 
+// 128-bit loads / stores with the non-temporal hint (streamed once: do not keep in cache).
+typedef float vf4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 load_nt(const float4 *p) {
+  const vf4_t v = __builtin_nontemporal_load(reinterpret_cast<const vf4_t *>(p));
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void store_nt(float4 *p, const float4 &v) {
+  const vf4_t x = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(x, reinterpret_cast<vf4_t *>(p));
+}
+
 // Kernel timing hook: oxh_time_next_launch arms the calling thread's next kernel launch to
 // record a start / stop event pair around the dispatch itself (hipExtLaunchKernelGGL), the
 // same interval a kernel-trace profiler reports.

@@ -32,6 +32,9 @@ namespace {
 #ifndef OXH_CE_BLOCK
 #define OXH_CE_BLOCK 512
 #endif
+#ifndef OXH_CE_NT
+#define OXH_CE_NT 3  // 1: non-temporal logit loads, 2: non-temporal gradient stores, 3: both
+#endif
 #ifndef OXH_CE_MINW
 #define OXH_CE_MINW 4
 #endif
@@ -104,74 +107,97 @@ __global__ __launch_bounds__(kMeanBlock) void ce_mean_kernel(const double *__res
   if (threadIdx.x == 0) *loss = static_cast<float>(s) / static_cast<float>(batch);
 }
 
+// exp(d) for d = x - rowmax <= 0, within ~1.5 ulp: 2^(d * log2 e) with the product carried as
+// hi + lo (an exact fma residual plus d times the tail of log2 e), the hardware 2^x (v_exp_f32,
+// 1 ulp) on the fraction |f| <= 0.5 + 2^-24, and the integer part applied by ldexp.  NaN
+// propagates; d below -200 (including -inf) gives 0, as expf does.
+__device__ __forceinline__ float exp_nonpos(float d) {
+  constexpr float kLog2eHi = 1.44269502162933349609375f;  // nearest float to log2(e)
+  constexpr float kLog2eLo = 1.925963033500011e-08f;      // log2(e) - kLog2eHi
+  d = d < -200.0f ? -200.0f : d;
+  const float hi = d * kLog2eHi;
+  const float lo = fmaf(d, kLog2eLo, fmaf(d, kLog2eHi, -hi));
+  const float n = rintf(hi);
+  const float f = (hi - n) + lo;  // hi - n is exact
+  return ldexpf(__builtin_amdgcn_exp2f(f), static_cast<int>(n));
+}
+
+__device__ __forceinline__ float4 exp4_nonpos(const float4 &x, float m) {
+  return make_float4(exp_nonpos(x.x - m), exp_nonpos(x.y - m), exp_nonpos(x.z - m),
+                     exp_nonpos(x.w - m));
+}
+
 // Register path: BLOCK lanes x V float4 hold one row of `classes` (= 4 * c4) logits.  MINW
 // (waves per SIMD the compiler must allow) bounds the VGPRs so several rows share a CU and one
-// row's memory phase overlaps another's exp / reduction phase.
-template <int BLOCK, int V, int MINW>
+// row's memory phase overlaps another's exp / reduction phase.  FULL: c4 == BLOCK * V, so no
+// lane needs a bounds check.
+template <int BLOCK, int V, int MINW, bool FULL>
 __global__ __launch_bounds__(BLOCK, MINW) void ce_row_kernel(CeArgs a) {
   __shared__ float lds_f[BLOCK / 64];
   __shared__ double lds_d[BLOCK / 64];
   const uint64_t row = blockIdx.x;
-  const uint64_t c4 = a.classes / 4;
+  const uint32_t c4 = static_cast<uint32_t>(a.classes / 4);
   const float4 *x4 = reinterpret_cast<const float4 *>(a.logits + row * a.classes);
+  auto in_row = [&](int k) { return FULL || threadIdx.x + static_cast<uint32_t>(k) * BLOCK < c4; };
   float4 v[V];
+#pragma unroll
+  for (int k = 0; k < V; ++k)
+    v[k] = !in_row(k) ? make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY)
+           : (OXH_CE_NT & 1) != 0 ? oxh::load_nt(x4 + threadIdx.x + k * BLOCK)
+                                  : x4[threadIdx.x + k * BLOCK];
+  // row max: fold(-inf, f32::max) in any order gives the same value (evaluation.rs:609)
   float m = -INFINITY;
 #pragma unroll
-  for (int k = 0; k < V; ++k) {
-    const uint64_t i = threadIdx.x + static_cast<uint64_t>(k) * BLOCK;
-    if (i < c4) {
-      v[k] = x4[i];
-      m = fmaxf(m, fmaxf(fmaxf(v[k].x, v[k].y), fmaxf(v[k].z, v[k].w)));
-    }
-  }
+  for (int k = 0; k < V; ++k) m = fmaxf(m, fmaxf(fmaxf(v[k].x, v[k].y), fmaxf(v[k].z, v[k].w)));
   const float maximum = block_max<BLOCK>(m, lds_f);
-  double s = 0.0;
+  // e = exp(x - max) kept in place; per-lane pairwise fp32 sums, fp64 across lanes
+  float part[V];
 #pragma unroll
   for (int k = 0; k < V; ++k) {
-    const uint64_t i = threadIdx.x + static_cast<uint64_t>(k) * BLOCK;
-    if (i < c4) {
-      v[k].x = expf(v[k].x - maximum);
-      v[k].y = expf(v[k].y - maximum);
-      v[k].z = expf(v[k].z - maximum);
-      v[k].w = expf(v[k].w - maximum);
-      s += static_cast<double>(v[k].x + v[k].y) + static_cast<double>(v[k].z + v[k].w);
+    if (in_row(k)) {
+      v[k] = exp4_nonpos(v[k], maximum);
+      part[k] = (v[k].x + v[k].y) + (v[k].z + v[k].w);
+    } else {
+      part[k] = 0.0f;
     }
   }
-  const float normalizer = static_cast<float>(block_sum<BLOCK>(s, lds_d));
+#pragma unroll
+  for (int w = 1; w < V; w *= 2)
+#pragma unroll
+    for (int k = 0; k + w < V; k += 2 * w) part[k] += part[k + w];
+  const float normalizer = static_cast<float>(block_sum<BLOCK>(static_cast<double>(part[0]), lds_d));
   uint64_t target = 0;
   const bool valid = target_index(a.targets[row], a.classes, target);
   if (!valid && threadIdx.x == 0 && a.error_flag) *a.error_flag = 1u;
   if (a.grad) {
-    const float scale = *a.outer / static_cast<float>(a.batch);  // autograd.rs:540-541
-    // p = e / normalizer (autograd.rs:548) as e * (1 / normalizer): within 1.5 ulp of the
-    // correctly rounded quotient, one division per row instead of one per logit.  The target
-    // logit keeps the exact quotient because p - 1 cancels.
-    const float rinv = 1.0f / normalizer;
     float4 *g4 = reinterpret_cast<float4 *>(a.grad + row * a.classes);
+    if (!valid) {
 #pragma unroll
-    for (int k = 0; k < V; ++k) {
-      const uint64_t i = threadIdx.x + static_cast<uint64_t>(k) * BLOCK;
-      if (i < c4) {
-        float4 r;
-        if (valid) {
-          r.x = scale * (v[k].x * rinv);
-          r.y = scale * (v[k].y * rinv);
-          r.z = scale * (v[k].z * rinv);
-          r.w = scale * (v[k].w * rinv);
-          const uint64_t e = 4 * i;
-          if (target >= e && target < e + 4) {
-            const int t = static_cast<int>(target - e);
-            const float et = t == 0 ? v[k].x : t == 1 ? v[k].y : t == 2 ? v[k].z : v[k].w;
-            const float gt = scale * (et / normalizer - 1.0f);
-            if (t == 0) r.x = gt;
-            else if (t == 1) r.y = gt;
-            else if (t == 2) r.z = gt;
-            else r.w = gt;
-          }
-        } else {
-          r = make_float4(NAN, NAN, NAN, NAN);
+      for (int k = 0; k < V; ++k)
+        if (in_row(k)) g4[threadIdx.x + k * BLOCK] = make_float4(NAN, NAN, NAN, NAN);
+    } else {
+      // grad = (outer / B) * (e / normalizer - onehot) (autograd.rs:540-551).  Off-target:
+      // e * ((outer / B) / normalizer), within 2.5 ulp of the CPU's scale * (e / normalizer),
+      // one multiply per logit.  The target logit keeps scale * (e / normalizer - 1) exactly,
+      // since the subtraction cancels.
+      const float scale = *a.outer / static_cast<float>(a.batch);
+      const float sr = scale / normalizer;
+      const uint32_t t4 = static_cast<uint32_t>(target / 4);
+      const uint32_t owner = t4 % BLOCK, kt = t4 / BLOCK, ct = static_cast<uint32_t>(target % 4);
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+        if (!in_row(k)) continue;
+        float4 r = make_float4(v[k].x * sr, v[k].y * sr, v[k].z * sr, v[k].w * sr);
+        if (static_cast<uint32_t>(k) == kt && threadIdx.x == owner) {
+          const float et = ct == 0 ? v[k].x : ct == 1 ? v[k].y : ct == 2 ? v[k].z : v[k].w;
+          const float gt = scale * (et / normalizer - 1.0f);
+          if (ct == 0) r.x = gt;
+          else if (ct == 1) r.y = gt;
+          else if (ct == 2) r.z = gt;
+          else r.w = gt;
         }
-        g4[i] = r;
+        if constexpr ((OXH_CE_NT & 2) != 0) oxh::store_nt(g4 + threadIdx.x + k * BLOCK, r);
+        else g4[threadIdx.x + k * BLOCK] = r;
       }
     }
   }
@@ -244,21 +270,31 @@ oxh_status launch_ce(const char *name, oxh_stream stream, CeArgs a, void *worksp
                    (!a.grad || oxh::aligned16(a.grad));
   const uint64_t c4 = a.classes / 4;
   constexpr int B = OXH_CE_BLOCK, W = OXH_CE_MINW;
-  if (vec && c4 <= 256) {
-    oxh::launch((ce_row_kernel<256, 1, 2>), grid, dim3(256), 0, s, a);
+  auto row = [&](auto kernel, int block) {
+    oxh::launch(kernel, grid, dim3(block), 0, s, a);
+  };
+  if (vec && c4 == 256) {
+    row(ce_row_kernel<256, 1, 2, true>, 256);
+  } else if (vec && c4 <= 256) {
+    row(ce_row_kernel<256, 1, 2, false>, 256);
+  } else if (vec && c4 == 256 * 4) {
+    row(ce_row_kernel<256, 4, 2, true>, 256);
   } else if (vec && c4 <= 256 * 4) {
-    oxh::launch((ce_row_kernel<256, 4, 2>), grid, dim3(256), 0, s, a);
+    row(ce_row_kernel<256, 4, 2, false>, 256);
   } else if (vec && c4 <= B * 2) {
-    oxh::launch((ce_row_kernel<B, 2, W>), grid, dim3(B), 0, s, a);
+    row(ce_row_kernel<B, 2, W, false>, B);
   } else if (vec && c4 <= B * 4) {
-    oxh::launch((ce_row_kernel<B, 4, W>), grid, dim3(B), 0, s, a);
+    row(ce_row_kernel<B, 4, W, false>, B);
+  } else if (vec && c4 == B * 8) {
+    row(ce_row_kernel<B, 8, W, true>, B);
   } else if (vec && c4 <= B * 8) {
-    oxh::launch((ce_row_kernel<B, 8, W>), grid, dim3(B), 0, s, a);
+    row(ce_row_kernel<B, 8, W, false>, B);
+  } else if (vec && c4 == B * 16) {
+    row(ce_row_kernel<B, 16, (W > 4 ? 4 : W), true>, B);
   } else if (vec && c4 <= B * 16) {
-    oxh::launch((ce_row_kernel<B, 16, (W > 4 ? 4 : W)>), grid, dim3(B), 0, s, a);
-  } else if (vec && B <= 256 && c4 <= B * 32) {
-    if constexpr (B <= 256)
-      oxh::launch((ce_row_kernel<B, 32, (W > 2 ? 2 : W)>), grid, dim3(B), 0, s, a);
+    row(ce_row_kernel<B, 16, (W > 4 ? 4 : W), false>, B);
+  } else if (vec && B <= 256 && c4 == B * 32) {
+    if constexpr (B <= 256) row(ce_row_kernel<B, 32, (W > 2 ? 2 : W), true>, B);
   } else {
     oxh::launch(ce_row_general_kernel, grid, dim3(kGenBlock), 0, s, a);
   }

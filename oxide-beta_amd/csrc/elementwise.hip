@@ -18,7 +18,27 @@ namespace {
 #ifndef OXH_EW_UNROLL
 #define OXH_EW_UNROLL 2  // float4 per thread per stream (overridable for tuning sweeps)
 #endif
+// Non-temporal hints (bit 1: loads, bit 2: stores), measured per kind of operation: the single
+// reference ops stream faster with non-temporal loads, the fused chain (three outputs in the
+// backward) with both.
+#ifndef OXH_EW_NT_OP
+#define OXH_EW_NT_OP 1
+#endif
+#ifndef OXH_EW_NT_CHAIN
+#define OXH_EW_NT_CHAIN 3
+#endif
 constexpr int kUnroll = OXH_EW_UNROLL;
+
+template <int NT>
+__device__ __forceinline__ float4 ld(const float4 *p) {
+  if constexpr ((NT & 1) != 0) return oxh::load_nt(p);
+  else return *p;
+}
+template <int NT>
+__device__ __forceinline__ void st(float4 *p, const float4 &v) {
+  if constexpr ((NT & 2) != 0) oxh::store_nt(p, v);
+  else *p = v;
+}
 
 template <int NI, int NO>
 struct MapArgs {
@@ -28,26 +48,31 @@ struct MapArgs {
 
 // Operations: scalar functors applied lane-wise.
 struct AddOp {
+  static constexpr int NT = OXH_EW_NT_OP;
   static constexpr int NI = 2, NO = 1;
   __device__ static void apply(const float (&x)[NI], float (&y)[NO]) { y[0] = x[0] + x[1]; }
 };
 struct MulOp {
+  static constexpr int NT = OXH_EW_NT_OP;
   static constexpr int NI = 2, NO = 1;
   __device__ static void apply(const float (&x)[NI], float (&y)[NO]) { y[0] = x[0] * x[1]; }
 };
 struct ReluOp {  // kernel_module.rs:26-34: x > 0 ? x : 0 (NaN and -0 give +0)
+  static constexpr int NT = OXH_EW_NT_OP;
   static constexpr int NI = 1, NO = 1;
   __device__ static void apply(const float (&x)[NI], float (&y)[NO]) {
     y[0] = x[0] > 0.0f ? x[0] : 0.0f;
   }
 };
 struct ReluBackwardOp {  // in0 = gradient, in1 = forward input
+  static constexpr int NT = OXH_EW_NT_OP;
   static constexpr int NI = 2, NO = 1;
   __device__ static void apply(const float (&x)[NI], float (&y)[NO]) {
     y[0] = x[1] > 0.0f ? x[0] : 0.0f;
   }
 };
 struct ChainForwardOp {  // relu((a + b) * c)
+  static constexpr int NT = OXH_EW_NT_CHAIN;
   static constexpr int NI = 3, NO = 1;
   __device__ static void apply(const float (&x)[NI], float (&y)[NO]) {
     float s = x[0] + x[1];
@@ -58,6 +83,7 @@ struct ChainForwardOp {  // relu((a + b) * c)
 // Backward of relu((a + b) * c) through the reference VJPs: relu (autograd.rs:139-147), mul
 // (123-138: left grad = g * right, right grad = g * left), add (119-122: both get g).
 struct ChainBackwardOnesOp {
+  static constexpr int NT = OXH_EW_NT_CHAIN;
   static constexpr int NI = 3, NO = 3;
   __device__ static void apply(const float (&x)[NI], float (&y)[NO]) {
     float s = x[0] + x[1];
@@ -70,6 +96,7 @@ struct ChainBackwardOnesOp {
   }
 };
 struct ChainBackwardOp {  // in3 = upstream gradient
+  static constexpr int NT = OXH_EW_NT_CHAIN;
   static constexpr int NI = 4, NO = 3;
   __device__ static void apply(const float (&x)[NI], float (&y)[NO]) {
     float s = x[0] + x[1];
@@ -108,7 +135,7 @@ __global__ __launch_bounds__(oxh::kBlock) void map_vec4_kernel(
       for (int u = 0; u < kUnroll; ++u)
 #pragma unroll
         for (int i = 0; i < NI; ++i)
-          in[u][i] = reinterpret_cast<const float4 *>(args.in[i])[base + u * oxh::kBlock];
+          in[u][i] = ld<Op::NT>(reinterpret_cast<const float4 *>(args.in[i]) + base + u * oxh::kBlock);
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
         float4 out[NO];
@@ -123,7 +150,7 @@ __global__ __launch_bounds__(oxh::kBlock) void map_vec4_kernel(
         }
 #pragma unroll
         for (int o = 0; o < NO; ++o)
-          reinterpret_cast<float4 *>(args.out[o])[base + u * oxh::kBlock] = out[o];
+          st<Op::NT>(reinterpret_cast<float4 *>(args.out[o]) + base + u * oxh::kBlock, out[o]);
       }
     } else {
       for (int u = 0; u < kUnroll; ++u) {
@@ -131,7 +158,7 @@ __global__ __launch_bounds__(oxh::kBlock) void map_vec4_kernel(
         if (idx >= n4) break;
         float4 v[NI], out[NO];
 #pragma unroll
-        for (int i = 0; i < NI; ++i) v[i] = reinterpret_cast<const float4 *>(args.in[i])[idx];
+        for (int i = 0; i < NI; ++i) v[i] = ld<Op::NT>(reinterpret_cast<const float4 *>(args.in[i]) + idx);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           float x[NI], y[NO];
@@ -142,7 +169,7 @@ __global__ __launch_bounds__(oxh::kBlock) void map_vec4_kernel(
           for (int o = 0; o < NO; ++o) set_lane(out[o], k, y[o]);
         }
 #pragma unroll
-        for (int o = 0; o < NO; ++o) reinterpret_cast<float4 *>(args.out[o])[idx] = out[o];
+        for (int o = 0; o < NO; ++o) st<Op::NT>(reinterpret_cast<float4 *>(args.out[o]) + idx, out[o]);
       }
     }
   }

@@ -98,3 +98,24 @@ def test_cross_entropy_config3_full_shape(module, dev):
     # size-independent property: every gradient row sums to zero (softmax - onehot)
     rows = grad.astype(np.float64).sum(axis=1)
     assert np.abs(rows).max() < 1e-9
+
+
+def test_cross_entropy_exp_accuracy_within_rows(module, dev):
+    """Pins the device exp to a few ulp independently of the oracle's normalizer: within one
+    row every off-target gradient is e * (scale / normalizer) with e = exp(d), d = x - max in
+    fp32, so gpu / (scale * exp64(d)) is one constant per row up to the rounding of the device
+    exp and of one multiply.  Its spread must stay below 5e-7 (about 4 ulp); dropping the
+    log2(e) tail or a 2^x with worse than a few ulp of error exceeds that for d near -30."""
+    r = np.random.default_rng(99)
+    b, k = 16, 32768
+    logits = (r.standard_normal((b, k)) * 4).astype(np.float32)
+    targets = r.integers(0, k, b).astype(np.float32)
+    _, grad, _ = _run(module, dev, logits, targets)
+    d = (logits - logits.max(axis=1, keepdims=True)).astype(np.float32)
+    e64 = np.exp(d.astype(np.float64))
+    mask = e64 > 1e-30
+    mask[np.arange(b), targets.astype(int)] = False
+    for row in range(b):
+        ratio = grad[row][mask[row]].astype(np.float64) / e64[row][mask[row]]
+        spread = (ratio.max() - ratio.min()) / ratio.mean()
+        assert spread < 5e-7, (row, spread)
