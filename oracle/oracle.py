@@ -59,6 +59,10 @@ _SIGNATURES = {
     "oro_ce_backward": (_int, [_F, _F, _u64, _u64, _f32, _F]),
     "oro_powi": (_f32, [_f32, _i32]),
     "oro_adamw_update": (None, [_F, _F, _F, _F, _u64, _f32, _f32, _f32, _f32, _f32, _i32]),
+    "oro_conv2d_forward": (None, [_F, _F, _F] + [_u64] * 10 + [_F]),
+    "oro_conv2d_backward": (None, [_F, _F, _F] + [_u64] * 10 + [_F, _F, _F]),
+    "oro_avg_pool2d_forward": (None, [_F] + [_u64] * 8 + [_F]),
+    "oro_avg_pool2d_backward": (None, [_F] + [_u64] * 8 + [_F]),
     "oro_initialized_weights": (None, [_U64P, _u64, _F]),
     "oro_argmax_rows": (None, [_F, _u64, _u64, _U64P]),
 }
@@ -233,6 +237,51 @@ def adamw_update(param, grad, m, v, step, lr=1e-3, weight_decay=0.01, beta1=0.9,
     lib().oro_adamw_update(_f(p), _f(g), _f(m), _f(v), p.size, lr, weight_decay, beta1, beta2,
                            epsilon, step)
     return p, m, v
+
+
+# ---------------------------------------------------------------- conv2d / avg_pool2d
+
+def conv2d_forward(x, weight, bias, stride, padding, groups):
+    x, weight, bias = _c(x), _c(weight), _c(bias)
+    n, cin, h, w = x.shape
+    cout, _, kh, kw = weight.shape
+    oh, ow = (h + 2 * padding - kh) // stride + 1, (w + 2 * padding - kw) // stride + 1
+    out = np.empty((n, cout, oh, ow), np.float32)
+    lib().oro_conv2d_forward(_f(x), _f(weight), _f(bias), n, cin, h, w, cout, kh, kw, stride,
+                             padding, groups, _f(out))
+    return out
+
+
+def conv2d_backward(grad, x, weight, stride, padding, groups):
+    """Returns (dinput, dweight, dbias)."""
+    grad, x, weight = _c(grad), _c(x), _c(weight)
+    n, cin, h, w = x.shape
+    cout, _, kh, kw = weight.shape
+    dx = np.empty_like(x)
+    dw = np.empty_like(weight)
+    db = np.empty(cout, np.float32)
+    lib().oro_conv2d_backward(_f(grad), _f(x), _f(weight), n, cin, h, w, cout, kh, kw, stride,
+                              padding, groups, _f(dx), _f(dw), _f(db))
+    return dx, dw, db
+
+
+def avg_pool2d_forward(x, kernel, stride):
+    x = _c(x)
+    n, c, h, w = x.shape
+    oh, ow = (h - kernel[0]) // stride[0] + 1, (w - kernel[1]) // stride[1] + 1
+    out = np.empty((n, c, oh, ow), np.float32)
+    lib().oro_avg_pool2d_forward(_f(x), n, c, h, w, kernel[0], kernel[1], stride[0], stride[1],
+                                 _f(out))
+    return out
+
+
+def avg_pool2d_backward(grad, input_shape, kernel, stride):
+    grad = _c(grad)
+    n, c, h, w = input_shape
+    dx = np.empty(input_shape, np.float32)
+    lib().oro_avg_pool2d_backward(_f(grad), n, c, h, w, kernel[0], kernel[1], stride[0],
+                                  stride[1], _f(dx))
+    return dx
 
 
 # ---------------------------------------------------------------- model helpers

@@ -302,6 +302,121 @@ void oro_adamw_update(float *param, const float *grad, float *first_moment, floa
   }
 }
 
+/* ------------------------------------------------------------------ conv2d / avg_pool2d */
+
+/* evaluation.rs:334-397 */
+void oro_conv2d_forward(const float *input, const float *weight, const float *bias,
+                        uint64_t batch, uint64_t in_channels, uint64_t height, uint64_t width,
+                        uint64_t out_channels, uint64_t kernel_h, uint64_t kernel_w,
+                        uint64_t stride, uint64_t padding, uint64_t groups, float *output) {
+  uint64_t out_h = (height + 2 * padding - kernel_h) / stride + 1;
+  uint64_t out_w = (width + 2 * padding - kernel_w) / stride + 1;
+  uint64_t in_per_group = in_channels / groups, out_per_group = out_channels / groups;
+  for (uint64_t n = 0; n < batch; ++n)
+    for (uint64_t oc = 0; oc < out_channels; ++oc) {
+      uint64_t group = oc / out_per_group;
+      for (uint64_t oy = 0; oy < out_h; ++oy)
+        for (uint64_t ox = 0; ox < out_w; ++ox) {
+          float sum = bias[oc];
+          for (uint64_t lc = 0; lc < in_per_group; ++lc) {
+            uint64_t ic = group * in_per_group + lc;
+            for (uint64_t ky = 0; ky < kernel_h; ++ky) {
+              uint64_t py = oy * stride + ky;
+              if (py < padding || py - padding >= height) continue;
+              uint64_t iy = py - padding;
+              for (uint64_t kx = 0; kx < kernel_w; ++kx) {
+                uint64_t px = ox * stride + kx;
+                if (px < padding || px - padding >= width) continue;
+                uint64_t ix = px - padding;
+                sum += input[((n * in_channels + ic) * height + iy) * width + ix] *
+                       weight[((oc * in_per_group + lc) * kernel_h + ky) * kernel_w + kx];
+              }
+            }
+          }
+          output[((n * out_channels + oc) * out_h + oy) * out_w + ox] = sum;
+        }
+    }
+}
+
+/* autograd.rs:412-483 */
+void oro_conv2d_backward(const float *grad, const float *input, const float *weight,
+                         uint64_t batch, uint64_t in_channels, uint64_t height, uint64_t width,
+                         uint64_t out_channels, uint64_t kernel_h, uint64_t kernel_w,
+                         uint64_t stride, uint64_t padding, uint64_t groups, float *dinput,
+                         float *dweight, float *dbias) {
+  uint64_t out_h = (height + 2 * padding - kernel_h) / stride + 1;
+  uint64_t out_w = (width + 2 * padding - kernel_w) / stride + 1;
+  uint64_t in_per_group = in_channels / groups, out_per_group = out_channels / groups;
+  memset(dinput, 0, batch * in_channels * height * width * sizeof(float));
+  memset(dweight, 0, out_channels * in_per_group * kernel_h * kernel_w * sizeof(float));
+  memset(dbias, 0, out_channels * sizeof(float));
+  for (uint64_t n = 0; n < batch; ++n)
+    for (uint64_t oc = 0; oc < out_channels; ++oc) {
+      uint64_t group = oc / out_per_group;
+      for (uint64_t oy = 0; oy < out_h; ++oy)
+        for (uint64_t ox = 0; ox < out_w; ++ox) {
+          float g = grad[((n * out_channels + oc) * out_h + oy) * out_w + ox];
+          dbias[oc] += g;
+          for (uint64_t lc = 0; lc < in_per_group; ++lc) {
+            uint64_t ic = group * in_per_group + lc;
+            for (uint64_t ky = 0; ky < kernel_h; ++ky) {
+              uint64_t py = oy * stride + ky;
+              if (py < padding || py - padding >= height) continue;
+              uint64_t iy = py - padding;
+              for (uint64_t kx = 0; kx < kernel_w; ++kx) {
+                uint64_t px = ox * stride + kx;
+                if (px < padding || px - padding >= width) continue;
+                uint64_t ix = px - padding;
+                uint64_t ii = ((n * in_channels + ic) * height + iy) * width + ix;
+                uint64_t wi = ((oc * in_per_group + lc) * kernel_h + ky) * kernel_w + kx;
+                dinput[ii] += g * weight[wi];
+                dweight[wi] += g * input[ii];
+              }
+            }
+          }
+        }
+    }
+}
+
+/* evaluation.rs:399-445 */
+void oro_avg_pool2d_forward(const float *input, uint64_t batch, uint64_t channels,
+                            uint64_t height, uint64_t width, uint64_t kernel_h, uint64_t kernel_w,
+                            uint64_t stride_h, uint64_t stride_w, float *output) {
+  uint64_t out_h = (height - kernel_h) / stride_h + 1, out_w = (width - kernel_w) / stride_w + 1;
+  float denominator = (float)(kernel_h * kernel_w);
+  for (uint64_t n = 0; n < batch; ++n)
+    for (uint64_t c = 0; c < channels; ++c)
+      for (uint64_t oy = 0; oy < out_h; ++oy)
+        for (uint64_t ox = 0; ox < out_w; ++ox) {
+          float sum = 0.0f;
+          for (uint64_t ky = 0; ky < kernel_h; ++ky)
+            for (uint64_t kx = 0; kx < kernel_w; ++kx)
+              sum += input[((n * channels + c) * height + oy * stride_h + ky) * width +
+                           ox * stride_w + kx];
+          output[((n * channels + c) * out_h + oy) * out_w + ox] = sum / denominator;
+        }
+}
+
+/* autograd.rs:485-527 */
+void oro_avg_pool2d_backward(const float *grad, uint64_t batch, uint64_t channels,
+                             uint64_t height, uint64_t width, uint64_t kernel_h,
+                             uint64_t kernel_w, uint64_t stride_h, uint64_t stride_w,
+                             float *dinput) {
+  uint64_t out_h = (height - kernel_h) / stride_h + 1, out_w = (width - kernel_w) / stride_w + 1;
+  float denominator = (float)(kernel_h * kernel_w);
+  memset(dinput, 0, batch * channels * height * width * sizeof(float));
+  for (uint64_t n = 0; n < batch; ++n)
+    for (uint64_t c = 0; c < channels; ++c)
+      for (uint64_t oy = 0; oy < out_h; ++oy)
+        for (uint64_t ox = 0; ox < out_w; ++ox) {
+          float contribution = grad[((n * channels + c) * out_h + oy) * out_w + ox] / denominator;
+          for (uint64_t ky = 0; ky < kernel_h; ++ky)
+            for (uint64_t kx = 0; kx < kernel_w; ++kx)
+              dinput[((n * channels + c) * height + oy * stride_h + ky) * width + ox * stride_w +
+                     kx] += contribution;
+        }
+}
+
 /* ------------------------------------------------------------------ model helpers */
 
 /* nn.rs:657-674 */

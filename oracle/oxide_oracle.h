@@ -21,6 +21,8 @@
  *   adamw                              torch.optim.AdamW in fp64; t=1 sign(g) closed form;
  *                                      optim.rs:168-208 loss-decrease property
  *   argmax (last index wins ties)      hand cases incl. ties, -0/+0 and NaN ordering
+ *   conv2d fwd/bwd, avg_pool2d fwd/bwd KAT tensor/mod.rs:586-614 (exact); torch fp64 conv2d /
+ *                                      avg_pool2d + autograd, grouped and strided cases
  *   initialized_weights                parity unpinned beyond range/determinism properties
  */
 #ifndef OXIDE_ORACLE_H
@@ -96,6 +98,28 @@ float oro_powi(float a, int32_t b);
 void oro_adamw_update(float *param, const float *grad, float *first_moment, float *second_moment,
                       uint64_t n, float learning_rate, float weight_decay, float beta1,
                       float beta2, float epsilon, int32_t step);
+
+/* ---- conv2d / avg_pool2d (NCHW, OIHW weights) ---- */
+/* evaluation.rs:334-397: out[n,oc,oy,ox] = bias[oc] + sum over (local channel, ky, kx). */
+void oro_conv2d_forward(const float *input, const float *weight, const float *bias,
+                        uint64_t batch, uint64_t in_channels, uint64_t height, uint64_t width,
+                        uint64_t out_channels, uint64_t kernel_h, uint64_t kernel_w,
+                        uint64_t stride, uint64_t padding, uint64_t groups, float *output);
+/* autograd.rs:412-483: scatter-accumulated input, weight and bias gradients. */
+void oro_conv2d_backward(const float *grad, const float *input, const float *weight,
+                         uint64_t batch, uint64_t in_channels, uint64_t height, uint64_t width,
+                         uint64_t out_channels, uint64_t kernel_h, uint64_t kernel_w,
+                         uint64_t stride, uint64_t padding, uint64_t groups, float *dinput,
+                         float *dweight, float *dbias);
+/* evaluation.rs:399-445 */
+void oro_avg_pool2d_forward(const float *input, uint64_t batch, uint64_t channels,
+                            uint64_t height, uint64_t width, uint64_t kernel_h, uint64_t kernel_w,
+                            uint64_t stride_h, uint64_t stride_w, float *output);
+/* autograd.rs:485-527 */
+void oro_avg_pool2d_backward(const float *grad, uint64_t batch, uint64_t channels,
+                             uint64_t height, uint64_t width, uint64_t kernel_h,
+                             uint64_t kernel_w, uint64_t stride_h, uint64_t stride_w,
+                             float *dinput);
 
 /* ---- models / driver helpers ---- */
 /* nn.rs:657-674: deterministic variance-scaled init of an OIHW conv weight. */

@@ -141,7 +141,30 @@ struct TensorTable {
   uint32_t vec_mask_lo, vec_mask_hi;
 };
 
-__global__ __launch_bounds__(oxh::kBlock) void adamw_multi_kernel(Hyper h, TensorTable table) {
+// Rust's f32::powi(i32) as compiler-rt's __powisf2: square-and-multiply over |b|, then one
+// reciprocal when b < 0 (host and device use this same sequence of fp32 operations).
+__host__ __device__ inline float powi_f32(float a, int32_t b) {
+  const bool recip = b < 0;
+  float r = 1.0f;
+  for (;;) {
+    if (b & 1) r *= a;
+    b /= 2;
+    if (b == 0) break;
+    a *= a;
+  }
+  return recip ? 1.0f / r : r;
+}
+
+__global__ void increment_step_kernel(int32_t *step) { *step += 1; }
+
+// step != null: the bias corrections come from the device step counter (optim.rs:113-114).
+__global__ __launch_bounds__(oxh::kBlock) void adamw_multi_kernel(Hyper h, TensorTable table,
+                                                                  const int32_t *step) {
+  if (step != nullptr) {
+    const int32_t t = *step;
+    h.c1 = 1.0f - powi_f32(h.b1, t);
+    h.c2 = 1.0f - powi_f32(h.b2, t);
+  }
   const uint32_t b = blockIdx.x;
   uint32_t t = 0;
   while (t + 1 < table.count && table.first_chunk[t + 1] <= b) ++t;
@@ -166,21 +189,8 @@ oxh_status oxh_adamw_corrections(float beta1, float beta2, int32_t step, float *
                                  float *second_correction) {
   OXH_REQUIRE(first_correction != nullptr && second_correction != nullptr, OXH_INVALID_SHAPE,
               "oxh_adamw_corrections: null output");
-  // Rust's f32::powi(i32) lowers to compiler-rt's __powisf2: square-and-multiply over |b|,
-  // then one reciprocal when b < 0.
-  auto powi = [](float a, int32_t b) {
-    const bool recip = b < 0;
-    float r = 1.0f;
-    for (;;) {
-      if (b & 1) r *= a;
-      b /= 2;
-      if (b == 0) break;
-      a *= a;
-    }
-    return recip ? 1.0f / r : r;
-  };
-  *first_correction = 1.0f - powi(beta1, step);
-  *second_correction = 1.0f - powi(beta2, step);
+  *first_correction = 1.0f - powi_f32(beta1, step);
+  *second_correction = 1.0f - powi_f32(beta2, step);
   return oxh::ok();
 }
 
@@ -218,16 +228,42 @@ oxh_status oxh_adamw(oxh_stream stream, float learning_rate, float weight_decay,
   return oxh::launched("oxh_adamw");
 }
 
+namespace {
+oxh_status adamw_multi(const char *name, oxh_stream stream, const Hyper &h, const int32_t *step,
+                       const oxh_adamw_tensor *tensors, uint32_t count);
+}
+
 oxh_status oxh_adamw_multi_tensor(oxh_stream stream, float learning_rate, float weight_decay,
                                   float beta1, float beta2, float first_correction,
                                   float second_correction, float epsilon,
                                   const oxh_adamw_tensor *tensors, uint32_t count) {
-  if (count == 0) return oxh::ok();
-  OXH_REQUIRE(tensors != nullptr, OXH_INVALID_SHAPE, "oxh_adamw_multi_tensor: null table");
   const Hyper h{learning_rate, weight_decay, beta1, beta2, first_correction, second_correction,
                 epsilon};
+  return adamw_multi("oxh_adamw_multi_tensor", stream, h, nullptr, tensors, count);
+}
+
+oxh_status oxh_adamw_multi_tensor_step(oxh_stream stream, float learning_rate,
+                                       float weight_decay, float beta1, float beta2,
+                                       float epsilon, int32_t *step,
+                                       const oxh_adamw_tensor *tensors, uint32_t count) {
+  OXH_REQUIRE(step != nullptr, OXH_INVALID_SHAPE,
+              "oxh_adamw_multi_tensor_step: null step counter");
+  const Hyper h{learning_rate, weight_decay, beta1, beta2, 1.0f, 1.0f, epsilon};
+  oxh::launch(increment_step_kernel, dim3(1), dim3(1), 0, oxh::as_stream(stream), step);
+  oxh_status st = oxh::launched("oxh_adamw_multi_tensor_step");
+  if (st != OXH_OK) return st;
+  return adamw_multi("oxh_adamw_multi_tensor_step", stream, h, step, tensors, count);
+}
+
+}  // extern "C"
+
+namespace {
+oxh_status adamw_multi(const char *name, oxh_stream stream, const Hyper &h, const int32_t *step,
+                       const oxh_adamw_tensor *tensors, uint32_t count) {
+  if (count == 0) return oxh::ok();
+  OXH_REQUIRE(tensors != nullptr, OXH_INVALID_SHAPE, std::string(name) + ": null table");
   OXH_REQUIRE(finite_hyper(h), OXH_INVALID_SHAPE,
-              "oxh_adamw_multi_tensor: non-finite hyper-parameter");
+              std::string(name) + ": non-finite hyper-parameter");
   for (uint32_t i = 0; i < count; ++i) {
     const oxh_adamw_tensor &t = tensors[i];
     if (t.n == 0) continue;
@@ -270,12 +306,12 @@ oxh_status oxh_adamw_multi_tensor(oxh_stream stream, float learning_rate, float 
     if (k == 0) continue;
     table.count = k;
     table.first_chunk[k] = static_cast<uint32_t>(chunks);
-    oxh::launch(adamw_multi_kernel, dim3(static_cast<uint32_t>(chunks)),
-                       dim3(oxh::kBlock), 0, oxh::as_stream(stream), h, table);
-    oxh_status st = oxh::launched("oxh_adamw_multi_tensor");
+    oxh::launch(adamw_multi_kernel, dim3(static_cast<uint32_t>(chunks)), dim3(oxh::kBlock), 0,
+                oxh::as_stream(stream), h, table, step);
+    oxh_status st = oxh::launched(name);
     if (st != OXH_OK) return st;
   }
   return oxh::ok();
 }
 
-}  // extern "C"
+}  // namespace

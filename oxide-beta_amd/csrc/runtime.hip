@@ -6,6 +6,7 @@
 // device.
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <string>
 
 #include "common.h"
@@ -125,6 +126,34 @@ oxh_status oxh_memcpy_d2d_async(void *dst, const void *src, uint64_t bytes, oxh_
   OXH_REQUIRE(dst != nullptr && src != nullptr, OXH_INVALID_SHAPE, "null pointer");
   OXH_HIP_CHECK(
       hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, oxh::as_stream(stream)));
+  return oxh::ok();
+}
+
+// ---------------------------------------------------------------- model initialization
+
+oxh_status oxh_initialized_weights(const uint64_t shape[4], uint64_t input_channels_per_group,
+                                   float *out) {
+  OXH_REQUIRE(shape != nullptr && out != nullptr, OXH_INVALID_SHAPE, "null argument");
+  OXH_REQUIRE(input_channels_per_group > 0 && shape[2] * shape[3] > 0, OXH_INVALID_SHAPE,
+              "oxh_initialized_weights: empty kernel or channel group");
+  // nn.rs:657-674: fan_in = in_per_group * kh * kw as f32; scale = sqrt(2 / fan_in); the state
+  // starts at 0x9E3779B9, xors every dimension times 0xBF58476D1CE4E5B9, is forced odd, then
+  // advances by xorshift64 (<< 13, >> 7, << 17) once per element; the top 24 bits give a
+  // uniform in [0, 1) mapped to [-scale, scale).
+  const float fan_in = static_cast<float>(input_channels_per_group * shape[2] * shape[3]);
+  const float scale = std::sqrt(2.0f / fan_in);
+  uint64_t state = 0x9E3779B9ull;
+  for (int d = 0; d < 4; ++d) state ^= shape[d] * 0xBF58476D1CE4E5B9ull;
+  state |= 1;
+  const uint64_t total = shape[0] * shape[1] * shape[2] * shape[3];
+  for (uint64_t i = 0; i < total; ++i) {
+    state ^= state << 13;
+    state ^= state >> 7;
+    state ^= state << 17;
+    const float unit = static_cast<float>(static_cast<uint32_t>(state >> 40)) /
+                       static_cast<float>(1u << 24);
+    out[i] = (unit * 2.0f - 1.0f) * scale;
+  }
   return oxh::ok();
 }
 

@@ -65,6 +65,20 @@ class AdamWTensor(ctypes.Structure):
                 ("second_moment", _vp), ("n", _u64)]
 
 
+class Conv2dShape(ctypes.Structure):
+    _fields_ = [(f, ctypes.c_uint64) for f in (
+        "batch", "in_channels", "height", "width", "out_channels", "kernel_h", "kernel_w",
+        "stride", "padding", "groups")]
+
+
+class Pool2dShape(ctypes.Structure):
+    _fields_ = [(f, ctypes.c_uint64) for f in (
+        "batch", "channels", "height", "width", "kernel_h", "kernel_w", "stride_h", "stride_w")]
+
+
+_CS = ctypes.POINTER(Conv2dShape)
+_PS = ctypes.POINTER(Pool2dShape)
+
 _SIGNATURES = {
     "oxh_last_error": (ctypes.c_char_p, []),
     "oxh_version": (ctypes.c_char_p, []),
@@ -123,6 +137,17 @@ _SIGNATURES = {
                                     ctypes.POINTER(_f32)]),
     "oxh_adamw_multi_tensor": (_st, [_vp, _f32, _f32, _f32, _f32, _f32, _f32, _f32,
                                      ctypes.POINTER(AdamWTensor), _u32]),
+    "oxh_adamw_multi_tensor_step": (_st, [_vp, _f32, _f32, _f32, _f32, _f32, _vp,
+                                          ctypes.POINTER(AdamWTensor), _u32]),
+    "oxh_conv2d_output_size": (_st, [_CS, ctypes.POINTER(_u64), ctypes.POINTER(_u64)]),
+    "oxh_conv2d_forward": (_st, [_vp, _CS, _vp, _vp, _vp, _vp]),
+    "oxh_conv2d_input_backward": (_st, [_vp, _CS, _vp, _vp, _vp]),
+    "oxh_conv2d_weight_backward_workspace_size": (_st, [_CS, ctypes.POINTER(_u64)]),
+    "oxh_conv2d_weight_backward": (_st, [_vp, _CS, _vp, _vp, _vp, _vp, _u64]),
+    "oxh_conv2d_bias_backward": (_st, [_vp, _CS, _vp, _vp, _vp, _u64]),
+    "oxh_avg_pool2d_forward": (_st, [_vp, _PS, _vp, _vp]),
+    "oxh_avg_pool2d_backward": (_st, [_vp, _PS, _vp, _vp]),
+    "oxh_initialized_weights": (_st, [ctypes.POINTER(_u64), _u64, ctypes.POINTER(_f32)]),
     "oxh_argmax_rows": (_st, [_vp, _u64, _u64, _vp, _vp]),
     "oxh_graph_begin": (_st, [_vp]),
     "oxh_graph_end": (_st, [_vp, ctypes.POINTER(_vp)]),
@@ -276,6 +301,36 @@ class KernelTimer:
             _lib.oxh_event_destroy(self.stop)
 
 
+def initialized_weights(shape, input_channels_per_group):
+    """nn.rs:657-674 deterministic OIHW init (host memory), via the library."""
+    import numpy as np
+
+    dims = (_u64 * 4)(*[int(d) for d in shape])
+    out = np.empty(int(np.prod(shape)), dtype=np.float32)
+    check(lib().oxh_initialized_weights(dims, int(input_channels_per_group),
+                                        out.ctypes.data_as(ctypes.POINTER(_f32))))
+    return out.reshape(shape)
+
+
+def conv2d_shape(batch, in_channels, height, width, out_channels, kernel, stride, padding,
+                 groups) -> Conv2dShape:
+    return Conv2dShape(batch, in_channels, height, width, out_channels, kernel, kernel, stride,
+                       padding, groups)
+
+
+def conv2d_output_size(shape: Conv2dShape) -> tuple[int, int]:
+    oh, ow = _u64(), _u64()
+    check(lib().oxh_conv2d_output_size(ctypes.byref(shape), ctypes.byref(oh), ctypes.byref(ow)))
+    return oh.value, ow.value
+
+
+def conv2d_workspace_size(shape: Conv2dShape) -> int:
+    out = _u64()
+    check(lib().oxh_conv2d_weight_backward_workspace_size(ctypes.byref(shape),
+                                                          ctypes.byref(out)))
+    return out.value
+
+
 def init(device: int = 0) -> None:
     check(lib().oxh_init(device))
 
@@ -294,6 +349,7 @@ class LoadedModule:
         init(device)
         self._bn_ws = Workspace()
         self._ce_ws = Workspace()
+        self._conv_ws = Workspace()
 
     # -- elementwise (kernel_module.rs:8-34, 492-508, 1052-1059)
     def add(self, a, b, out, stream=None):
@@ -470,6 +526,46 @@ class LoadedModule:
         check(lib().oxh_adamw_multi_tensor(_stream(stream), learning_rate, weight_decay, beta1,
                                            beta2, first_correction, second_correction, epsilon,
                                            table, len(tensors)))
+
+    def adamw_multi_tensor_step(self, learning_rate, weight_decay, beta1, beta2, epsilon,
+                                step_counter, tensors, stream=None):
+        """``tensors``: sequence of (parameter, gradient, first_moment, second_moment);
+        ``step_counter``: device int32 incremented before the update."""
+        table = (AdamWTensor * len(tensors))()
+        for i, (p, g, m, v) in enumerate(tensors):
+            table[i] = AdamWTensor(_ptr(p), _ptr(g), _ptr(m), _ptr(v), p.numel())
+        check(lib().oxh_adamw_multi_tensor_step(_stream(stream), learning_rate, weight_decay,
+                                                beta1, beta2, epsilon, _ptr(step_counter),
+                                                table, len(tensors)))
+
+    # -- conv2d / avg_pool2d (kernel_module.rs:359-490, 558-825)
+    def conv2d_forward(self, shape, x, weight, bias, out, stream=None):
+        check(lib().oxh_conv2d_forward(_stream(stream), ctypes.byref(shape), _ptr(x),
+                                       _ptr(weight), _ptr(bias), _ptr(out)))
+
+    def conv2d_input_backward(self, shape, gradient, weight, input_gradient, stream=None):
+        check(lib().oxh_conv2d_input_backward(_stream(stream), ctypes.byref(shape),
+                                              _ptr(gradient), _ptr(weight),
+                                              _ptr(input_gradient)))
+
+    def conv2d_weight_backward(self, shape, gradient, x, weight_gradient, stream=None):
+        ws, wsb = self._conv_ws.ptr_bytes(conv2d_workspace_size(shape))
+        check(lib().oxh_conv2d_weight_backward(_stream(stream), ctypes.byref(shape),
+                                               _ptr(gradient), _ptr(x), _ptr(weight_gradient),
+                                               ws, wsb))
+
+    def conv2d_bias_backward(self, shape, gradient, bias_gradient, stream=None):
+        ws, wsb = self._conv_ws.ptr_bytes(conv2d_workspace_size(shape))
+        check(lib().oxh_conv2d_bias_backward(_stream(stream), ctypes.byref(shape),
+                                             _ptr(gradient), _ptr(bias_gradient), ws, wsb))
+
+    def avg_pool2d_forward(self, shape, x, out, stream=None):
+        check(lib().oxh_avg_pool2d_forward(_stream(stream), ctypes.byref(shape), _ptr(x),
+                                           _ptr(out)))
+
+    def avg_pool2d_backward(self, shape, gradient, input_gradient, stream=None):
+        check(lib().oxh_avg_pool2d_backward(_stream(stream), ctypes.byref(shape),
+                                            _ptr(gradient), _ptr(input_gradient)))
 
     def argmax_rows(self, logits, indices, stream=None):
         rows, classes = logits.shape

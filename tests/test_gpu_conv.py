@@ -1,0 +1,113 @@
+"""conv2d forward / input / weight / bias backward and avg_pool2d on the GPU against the oracle
+(evaluation.rs:334-445, autograd.rs:412-527) on every MobileNetV4-Conv-S layer kind.
+
+Forward, input gradient and pooling sum their terms in the CPU path's order: bit-exact.  Weight
+and bias gradients reduce batch chunks in a fixed order: |gpu - cpu| <= 1e-5 * sum|terms|."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import oxide_hip as ox
+from helpers import assert_bitexact, assert_within, host, to_dev
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    (2, 1, 28, 28, 32, 3, 2, 1),
+    (128, 1, 28, 28, 32, 3, 2, 1),     # config 5 stem at full batch
+    (3, 32, 7, 7, 32, 3, 2, 1),
+    (2, 64, 4, 4, 64, 5, 1, 64),
+    (2, 192, 4, 4, 192, 5, 2, 192),
+    (4, 96, 2, 2, 192, 1, 1, 1),
+    (3, 12, 6, 5, 8, 3, 1, 4),
+    (5, 20, 1, 1, 30, 1, 1, 1),
+    (128, 960, 1, 1, 1280, 1, 1, 1),   # config 5's largest layer
+]
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_conv2d_matches_oracle(module, dev, case):
+    n, cin, h, w, cout, k, s, groups = case
+    pad = k // 2
+    r = np.random.default_rng(hash(case) & 0xFFFFFFFF)
+    x = r.standard_normal((n, cin, h, w)).astype(np.float32)
+    wt = (r.standard_normal((cout, cin // groups, k, k)) * 0.3).astype(np.float32)
+    b = r.standard_normal(cout).astype(np.float32)
+    shape = ox.conv2d_shape(n, cin, h, w, cout, k, s, pad, groups)
+    oh, ow = ox.conv2d_output_size(shape)
+    g = r.standard_normal((n, cout, oh, ow)).astype(np.float32)
+    dx_, dw_, db_, dg_ = to_dev(x, dev), to_dev(wt, dev), to_dev(b, dev), to_dev(g, dev)
+    y = torch.empty((n, cout, oh, ow), device=dev)
+    gx, gw, gb = torch.empty_like(dx_), torch.empty_like(dw_), torch.empty_like(db_)
+    module.conv2d_forward(shape, dx_, dw_, db_, y)
+    module.conv2d_input_backward(shape, dg_, dw_, gx)
+    module.conv2d_weight_backward(shape, dg_, dx_, gw)
+    module.conv2d_bias_backward(shape, dg_, gb)
+    torch.cuda.synchronize()
+    assert_bitexact(host(y), oracle.conv2d_forward(x, wt, b, s, pad, groups), "forward")
+    rdx, rdw, rdb = oracle.conv2d_backward(g, x, wt, s, pad, groups)
+    assert_bitexact(host(gx), rdx, "input gradient")
+    # weight / bias gradient conditioning bounds from the magnitudes of their terms
+    abs_dw = oracle.conv2d_backward(np.abs(g), np.abs(x), np.abs(wt), s, pad, groups)[1]
+    assert_within(host(gw), rdw, 1e-5 * abs_dw.astype(np.float64) + 1e-7, "weight gradient")
+    assert_within(host(gb), rdb, 1e-5 * np.abs(g).astype(np.float64).sum(axis=(0, 2, 3)) + 1e-7,
+                  "bias gradient")
+
+
+@pytest.mark.parametrize("shape,kernel,stride", [((2, 3, 4, 4), (2, 2), (2, 2)),
+                                                 ((128, 960, 1, 1), (1, 1), (1, 1)),
+                                                 ((2, 5, 7, 7), (7, 7), (7, 7)),
+                                                 ((1, 2, 5, 6), (3, 2), (1, 2))])
+def test_avg_pool2d_matches_oracle(module, dev, shape, kernel, stride):
+    r = np.random.default_rng(3)
+    x = r.standard_normal(shape).astype(np.float32)
+    ps = ox.Pool2dShape(*shape, kernel[0], kernel[1], stride[0], stride[1])
+    ref = oracle.avg_pool2d_forward(x, kernel, stride)
+    y = torch.empty(ref.shape, device=dev)
+    module.avg_pool2d_forward(ps, to_dev(x, dev), y)
+    g = r.standard_normal(ref.shape).astype(np.float32)
+    dx = torch.empty(shape, device=dev)
+    module.avg_pool2d_backward(ps, to_dev(g, dev), dx)
+    torch.cuda.synchronize()
+    assert_bitexact(host(y), ref, "pool forward")
+    assert_bitexact(host(dx), oracle.avg_pool2d_backward(g, shape, kernel, stride),
+                    "pool backward")
+
+
+def test_conv_reference_kat(module, dev):
+    """tensor/mod.rs:586-614 on the GPU."""
+    x = np.arange(1, 10, dtype=np.float32).reshape(1, 1, 3, 3)
+    shape = ox.conv2d_shape(1, 1, 3, 3, 1, 2, 1, 0, 1)
+    y = torch.empty((1, 1, 2, 2), device=dev)
+    module.conv2d_forward(shape, to_dev(x, dev), torch.ones((1, 1, 2, 2), device=dev),
+                          torch.zeros(1, device=dev), y)
+    dwx = np.arange(1, 9, dtype=np.float32).reshape(1, 2, 2, 2)
+    dshape = ox.conv2d_shape(1, 2, 2, 2, 2, 1, 1, 0, 2)
+    dy = torch.empty((1, 2, 2, 2), device=dev)
+    module.conv2d_forward(dshape, to_dev(dwx, dev), to_dev(np.array([2.0, 3.0], np.float32)
+                                                          .reshape(2, 1, 1, 1), dev),
+                          torch.zeros(2, device=dev), dy)
+    torch.cuda.synchronize()
+    assert host(y).ravel().tolist() == [12.0, 16.0, 24.0, 28.0]
+    assert host(dy).ravel().tolist() == [2, 4, 6, 8, 15, 18, 21, 24]
+
+
+def test_adamw_step_counter_matches_host_corrections(module, dev, rng):
+    """oxh_adamw_multi_tensor_step: the device step counter gives the same bit-exact update as
+    host-computed corrections, on consecutive steps."""
+    n = 3000
+    p = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    g = (rng.standard_normal(n) * 1e-3).astype(np.float32)
+    dp, dg = to_dev(p, dev), to_dev(g, dev)
+    dm, dv = torch.zeros_like(dp), torch.zeros_like(dp)
+    step = torch.zeros(1, dtype=torch.int32, device=dev)
+    pr, mr, vr = p, np.zeros_like(p), np.zeros_like(p)
+    for t in range(1, 4):
+        module.adamw_multi_tensor_step(1e-3, 1e-4, 0.9, 0.999, 1e-8, step, [(dp, dg, dm, dv)])
+        pr, mr, vr = oracle.adamw_update(pr, g, mr, vr, t, 1e-3, 1e-4)
+        torch.cuda.synchronize()
+        assert int(host(step)[0]) == t
+        assert_bitexact(host(dp), pr, f"param step {t}")
+        assert_bitexact(host(dv), vr, f"v step {t}")
