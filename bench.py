@@ -295,6 +295,44 @@ def bench_adamw(m, reps: int = 10):
             "frac_of_peak": round(7 * n * 4 / us / 1e3 / PEAK_HBM_GBS, 3)}
 
 
+def bench_mnist_step(steps: int = 20, batch: int = 128):
+    """Config 5: the MobileNetV4-Conv-S MNIST training step (forward, cross entropy,
+    backward, AdamW) as one hipGraph replay; synthetic batch (pixels k / 255, labels 0-9)."""
+    import numpy as np
+    import torch
+
+    import training as T
+
+    step = T.TrainingStep(T.MobileNetV4ConvSmall.mnist(), batch)
+    r = np.random.default_rng(0x6F78696400000005)
+    step.set_batch((r.integers(0, 256, (batch, 1, 28, 28)) / 255.0).astype(np.float32),
+                   r.integers(0, 10, batch).astype(np.float32))
+
+    def timed(fn, reps):
+        e0, e1 = _events(2)
+        e0.record(step.stream)
+        for _ in range(reps):
+            fn()
+        e1.record(step.stream)
+        step.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    step.run_eager()
+    eager_ms = timed(step.run_eager, 3)
+    step.capture()
+    for _ in range(3):
+        step.replay()
+    graph_ms = timed(step.replay, steps)
+    loss = step.loss_value()
+    nbytes = step.kernel_bytes()
+    return {"config": f"MobileNetV4-Conv-S MNIST train step, batch {batch}, fp32",
+            "graph_ms_per_step": round(graph_ms, 4), "eager_ms_per_step": round(eager_ms, 3),
+            "images_per_s": round(batch / (graph_ms * 1e-3), 1),
+            "launch_groups_per_step": len(step.ops), "steps_timed": steps,
+            "parameters": step.model.parameter_count(),
+            "loss_after": round(loss, 5), "alg_bytes_per_step": nbytes}
+
+
 def copy_calibration():
     """Three 1 GiB device-to-device copies (hipMemcpyAsync's blit kernel): a plain copy of
     known traffic (1 GiB read + 1 GiB written per launch) for scaling HBM counters."""
@@ -378,6 +416,7 @@ def main():
         extra["elementwise"] = bench_elementwise(m)
         extra["cross_entropy"] = bench_cross_entropy(m)
         extra["adamw"] = bench_adamw(m)
+        extra["mnist_step"] = bench_mnist_step()
     out = {
         "metric": "BatchNorm2d train fwd+bwd achieved HBM bandwidth (algorithmic bytes)",
         "value": round(value, 1),

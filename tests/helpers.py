@@ -53,3 +53,56 @@ def assert_within(got, ref, bound, what=""):
         worst = bad[np.argmax((d.ravel() / np.maximum(bound.ravel(), 1e-300))[bad])]
         raise AssertionError(f"{what}: {bad.size} of {ok.size} outside the bound; worst at "
                              f"{worst}: |d|={d.ravel()[worst]!r} bound={bound.ravel()[worst]!r}")
+
+
+def check_batch_norm_forward(out, x, gamma, beta, rm, rv, momentum=0.1, eps=1e-5):
+    """out: dict with y, mean, inv, rm, rv from the device for inputs x, gamma, beta and running
+    statistics rm, rv (before the update).  Returns the oracle's (mean, inv) and the fraction of
+    y within the strict criterion."""
+    import oracle
+
+    y, mean, inv, rm1, rv1 = oracle.bn_forward(x, gamma, beta, rm, rv, True, momentum, eps)
+    c = x.shape[1]
+    assert_close(out["mean"], mean, what="mean")
+    assert_close(out["inv"], inv, what="inverse std")
+    assert_close(out["rm"], rm1, what="running mean")
+    assert_close(out["rv"], rv1, what="running var")
+    cb = lambda v: v.reshape(1, c, 1, 1)  # noqa: E731
+    # y = ((x - mean) * inv) * w + b: x - mean cancels, so the terms are x * inv * w,
+    # mean * inv * w and b (one ulp of the mean moves y by |mean| * inv * |w| * 2^-24)
+    y_terms = ((np.abs(x) + np.abs(cb(mean))) * cb(inv) * np.abs(cb(gamma))
+               + np.abs(cb(beta)))
+    ok = strict_ok(out["y"], y)
+    if not ok.all():
+        assert_within(out["y"], y, np.maximum(1e-5 * y_terms, 1e-6), "y")
+    return ok.mean()
+
+
+def check_batch_norm_backward(out, g, x, gamma, mean, inv):
+    """out: dict with dx, dw, db from the device for upstream gradient g and the saved batch
+    statistics (mean, inv) the device used.  Returns the strict-criterion fractions."""
+    import oracle
+
+    dx, dw, db = oracle.bn_backward(g, x, gamma, mean, inv, True)
+    n, c, h, w = x.shape
+    cb = lambda v: v.reshape(1, c, 1, 1)  # noqa: E731
+    # dx terms: (w*inv/M) * (M*g, sum g, x_hat * sum g x_hat)
+    m_ = n * h * w
+    xhat = (x - cb(mean)) * cb(inv)
+    coef = np.abs(cb(gamma * inv / np.float32(m_)))
+    dx_terms = coef * (m_ * np.abs(g) + np.abs(cb(db)) + np.abs(xhat * cb(dw)))
+    ok = strict_ok(out["dx"], dx)
+    if not ok.all():
+        assert_within(out["dx"], dx, np.maximum(1e-5 * dx_terms, 1e-6), "dx")
+    # channel sums: conditioning bound vs the oracle and a tight bound vs fp64 of the same terms
+    sum_abs_g = np.abs(g.astype(np.float64)).sum(axis=(0, 2, 3))
+    gx32 = (g * ((x - cb(mean)) * cb(inv))).astype(np.float32)
+    sum_abs_gx = np.abs(gx32.astype(np.float64)).sum(axis=(0, 2, 3))
+    assert_within(out["db"], db, 1e-5 * sum_abs_g + 1e-6, "dbias vs oracle")
+    assert_within(out["dw"], dw, 1e-5 * sum_abs_gx + 1e-6, "dweight vs oracle")
+    assert_within(out["db"], g.astype(np.float64).sum(axis=(0, 2, 3)),
+                  1e-6 * sum_abs_g + 1e-7, "dbias vs fp64")
+    assert_within(out["dw"], gx32.astype(np.float64).sum(axis=(0, 2, 3)),
+                  1e-6 * sum_abs_gx + 1e-7, "dweight vs fp64")
+    return dict(dx=ok.mean(), dw=strict_ok(out["dw"], dw).mean(),
+                db=strict_ok(out["db"], db).mean())
