@@ -382,6 +382,9 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-extra", action="store_true", help="headline BN config only")
+    ap.add_argument("--only", choices=["elementwise", "cross_entropy", "adamw", "mnist_step"],
+                    help="run one secondary workload alone and print its result (for "
+                         "profiling that workload's kernels)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 1 GiB device-to-device copy (3 launches) whose known "
@@ -400,6 +403,13 @@ def main():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
     m = ox.load_kernels(0)
+    if args.only:
+        runners = {"elementwise": lambda: bench_elementwise(m),
+                   "cross_entropy": lambda: bench_cross_entropy(m),
+                   "adamw": lambda: bench_adamw(m),
+                   "mnist_step": lambda: bench_mnist_step(args.steps)}
+        print(json.dumps({"workload": args.only, **runners[args.only]()}), flush=True)
+        return
     bn = bench_batch_norm(m, args.steps, args.warmup)
     dominant = max(bn["kernels"], key=lambda k: bn["kernels"][k]["avg_us"])
     dk = bn["kernels"][dominant]

@@ -24,6 +24,11 @@
 //     dweight / dbias).  Channel values are read back from LDS.
 //     A kernel boundary separates reduce and map, so no fence or atomic is needed (on gfx950 an
 //     agent-scope release writes back the XCD's L2, far too costly per block).
+//   * Small planes (H*W < OXH_BN_FLAT_SPATIAL, e.g. the 7x7 ... 1x1 layers of a MobileNet at
+//     MNIST resolution): a map block would span hundreds of planes and finalize each, so one
+//     wave per channel finalizes into the per-channel outputs (saved mean / inverse std and the
+//     running update, or dweight / dbias) and a flat pass reads them per element: three
+//     launches per direction, each channel finalized once, same arithmetic.
 //   * Per-element arithmetic follows the CPU path's fp32 operation order exactly
 //     (-ffp-contract=off): y = ((x - mean) * inv) * w + b, x_hat = (x - mean) * inv,
 //     dx = ((w * inv) / M) * ((M * g - sum_g) - x_hat * sum_g_xhat), eval dx = (g * w) * inv.
@@ -49,6 +54,9 @@ namespace {
 #ifndef OXH_BN_MAP_VEC
 #define OXH_BN_MAP_VEC 2  // float4 per thread per stream in a map block
 #endif
+#ifndef OXH_BN_FLAT_SPATIAL
+#define OXH_BN_FLAT_SPATIAL 64  // planes smaller than this use finalize + flat map
+#endif
 
 constexpr int kRedBlock = 256;  // 4 waves
 constexpr int kRedWaves = kRedBlock / 64;
@@ -58,6 +66,7 @@ constexpr int kMapBlock = 256;
 constexpr int kMapVec = OXH_BN_MAP_VEC;
 constexpr uint32_t kMapElems = kMapBlock * 4 * kMapVec;  // elements per map block
 constexpr uint32_t kMaxPlanes = 256;  // planes one map block may touch
+constexpr uint64_t kFlatSpatial = OXH_BN_FLAT_SPATIAL;
 
 // ---------------------------------------------------------------- geometry
 
@@ -408,12 +417,18 @@ struct ApplyPhase {
       cache.v[3][k] = p.b;
     }
   }
+  // Channel values read from the per-channel arrays (partial == null).
+  __device__ static void direct(const Args &a, uint32_t c, float (&cv)[V]) {
+    cv[0] = a.mean[c];
+    cv[1] = a.inverse_std[c];
+    cv[2] = a.weight[c];
+    cv[3] = a.bias[c];
+  }
   __device__ static const float *input(const Args &a, int) { return a.x; }
   __device__ static float *output(const Args &a) { return a.y; }
-  __device__ static float element(const Args &, const Cache<V> &cache, uint32_t k,
-                                  const float (&in)[NI]) {
+  __device__ static float element(const Args &, const float (&cv)[V], const float (&in)[NI]) {
     // evaluation.rs:590-595
-    return (in[0] - cache.v[0][k]) * cache.v[1][k] * cache.v[2][k] + cache.v[3][k];
+    return (in[0] - cv[0]) * cv[1] * cv[2] + cv[3];
   }
 };
 
@@ -466,13 +481,19 @@ struct DxTrainPhase {
       cache.v[4][k] = sgx;
     }
   }
+  __device__ static void direct(const Args &a, uint32_t c, float (&cv)[V]) {
+    cv[0] = a.mean[c];
+    cv[1] = a.inverse_std[c];
+    cv[2] = a.weight[c] * cv[1] / a.samples;
+    cv[3] = a.bias_gradient[c];
+    cv[4] = a.weight_gradient[c];
+  }
   __device__ static const float *input(const Args &a, int i) { return i == 0 ? a.grad : a.x; }
   __device__ static float *output(const Args &a) { return a.dx; }
-  __device__ static float element(const Args &a, const Cache<V> &cache, uint32_t k,
-                                  const float (&in)[NI]) {
+  __device__ static float element(const Args &a, const float (&cv)[V], const float (&in)[NI]) {
     // autograd.rs:367-373
-    const float normalized = (in[1] - cache.v[0][k]) * cache.v[1][k];
-    return cache.v[2][k] * (a.samples * in[0] - cache.v[3][k] - normalized * cache.v[4][k]);
+    const float normalized = (in[1] - cv[0]) * cv[1];
+    return cv[2] * (a.samples * in[0] - cv[3] - normalized * cv[4]);
   }
 };
 
@@ -496,11 +517,14 @@ struct DxEvalPhase {
       cache.v[1][k] = p.inv;
     }
   }
+  __device__ static void direct(const Args &a, uint32_t c, float (&cv)[V]) {
+    cv[0] = a.weight[c];
+    cv[1] = a.inverse_std[c];
+  }
   __device__ static const float *input(const Args &a, int) { return a.grad; }
   __device__ static float *output(const Args &a) { return a.dx; }
-  __device__ static float element(const Args &, const Cache<V> &cache, uint32_t k,
-                                  const float (&in)[NI]) {
-    return in[0] * cache.v[0][k] * cache.v[1][k];
+  __device__ static float element(const Args &, const float (&cv)[V], const float (&in)[NI]) {
+    return in[0] * cv[0] * cv[1];
   }
 };
 
@@ -556,6 +580,9 @@ __global__ __launch_bounds__(kMapBlock) void bn_map_kernel(PlaneMap m, typename 
       const uint32_t q = threadIdx.x + u * kMapBlock;
       if (q < n4) {
         const uint32_t k = oxh::fast_div(r0 + q * 4, m.spatial_div);
+        float cv[P::V];
+#pragma unroll
+        for (int j = 0; j < P::V; ++j) cv[j] = cache.v[j][k];
         float x0[P::NI], x1[P::NI], x2[P::NI], x3[P::NI];
 #pragma unroll
         for (int i = 0; i < P::NI; ++i) {
@@ -565,10 +592,10 @@ __global__ __launch_bounds__(kMapBlock) void bn_map_kernel(PlaneMap m, typename 
           x3[i] = v[u][i].w;
         }
         float4 r;
-        r.x = P::element(a, cache, k, x0);
-        r.y = P::element(a, cache, k, x1);
-        r.z = P::element(a, cache, k, x2);
-        r.w = P::element(a, cache, k, x3);
+        r.x = P::element(a, cv, x0);
+        r.y = P::element(a, cv, x1);
+        r.z = P::element(a, cv, x2);
+        r.w = P::element(a, cv, x3);
         if constexpr ((OXH_BN_NT_STORE & P::kNtStoreBit) != 0)
           oxh::store_nt(reinterpret_cast<float4 *>(out + e0) + q, r);
         else
@@ -580,10 +607,61 @@ __global__ __launch_bounds__(kMapBlock) void bn_map_kernel(PlaneMap m, typename 
     __syncthreads();
     for (uint32_t q = threadIdx.x; q < n; q += kMapBlock) {
       const uint32_t k = oxh::fast_div(r0 + q, m.spatial_div);
+      float cv[P::V];
+#pragma unroll
+      for (int j = 0; j < P::V; ++j) cv[j] = cache.v[j][k];
       float x[P::NI];
 #pragma unroll
       for (int i = 0; i < P::NI; ++i) x[i] = P::input(a, i)[e0 + q];
-      out[e0 + q] = P::element(a, cache, k, x);
+      out[e0 + q] = P::element(a, cv, x);
+    }
+  }
+}
+
+// Small planes: a map block of kMapElems elements would span hundreds of (n, c) planes and
+// finalize each of them, so for spatial < kFlatSpatial the statistics are finalized once per
+// channel by the finalize kernels above (into the per-channel output arrays), and this flat pass
+// reads each element's channel values from those arrays (cached: C * V floats).
+struct FlatMap {
+  uint32_t channels;
+  uint32_t units;  // float4 units (vec) or elements
+  bool vec;        // spatial % 4 == 0 and pointers aligned: a float4 lies in one plane
+  oxh::FastDiv spatial_div, channel_div;
+};
+
+template <class P>
+__global__ __launch_bounds__(kMapBlock) void bn_flat_map_kernel(FlatMap m, typename P::Args a) {
+  float *out = P::output(a);
+  const uint32_t stride = gridDim.x * kMapBlock;
+  for (uint32_t q = blockIdx.x * kMapBlock + threadIdx.x; q < m.units; q += stride) {
+    const uint32_t e = m.vec ? q * 4 : q;  // < 2^31 (checked on the host)
+    const uint32_t plane = oxh::fast_div(e, m.spatial_div);
+    const uint32_t c = plane - oxh::fast_div(plane, m.channel_div) * m.channels;
+    float cv[P::V];
+    P::direct(a, c, cv);
+    if (m.vec) {
+      float4 v[P::NI];
+#pragma unroll
+      for (int i = 0; i < P::NI; ++i) v[i] = reinterpret_cast<const float4 *>(P::input(a, i))[q];
+      float x0[P::NI], x1[P::NI], x2[P::NI], x3[P::NI];
+#pragma unroll
+      for (int i = 0; i < P::NI; ++i) {
+        x0[i] = v[i].x;
+        x1[i] = v[i].y;
+        x2[i] = v[i].z;
+        x3[i] = v[i].w;
+      }
+      float4 r;
+      r.x = P::element(a, cv, x0);
+      r.y = P::element(a, cv, x1);
+      r.z = P::element(a, cv, x2);
+      r.w = P::element(a, cv, x3);
+      reinterpret_cast<float4 *>(out)[q] = r;
+    } else {
+      float x[P::NI];
+#pragma unroll
+      for (int i = 0; i < P::NI; ++i) x[i] = P::input(a, i)[q];
+      out[q] = P::element(a, cv, x);
     }
   }
 }
@@ -682,9 +760,35 @@ oxh_status launch_reduce_gx(const char *name, oxh_stream stream, uint64_t batch,
   return oxh::launched(name);
 }
 
+bool a_is_direct(const ApplyPhase::Args &a) { return a.partial == nullptr; }
+bool a_is_direct(const DxTrainPhase::Args &a) { return a.partial == nullptr; }
+bool a_is_direct(const DxEvalPhase::Args &) { return true; }
+
+// The flat pass serves planes smaller than kFlatSpatial values (tensors under 2^31 elements).
+bool use_flat(uint64_t batch, uint64_t channels, uint64_t spatial) {
+  return spatial < kFlatSpatial && batch * channels * spatial < (1ull << 31);
+}
+
+// Per-element pass.  With a.partial set, the block-finalizing map kernel is the only option
+// (the flat pass reads finalized per-channel arrays; the entry points finalize first).
 template <class P>
 oxh_status launch_map(const char *name, oxh_stream stream, uint64_t batch, uint64_t channels,
                       uint64_t spatial, bool aligned, const typename P::Args &a) {
+  if (a_is_direct(a) && use_flat(batch, channels, spatial)) {
+    FlatMap f{};
+    const uint64_t total = batch * channels * spatial;
+    f.channels = static_cast<uint32_t>(channels);
+    f.vec = aligned && spatial % 4 == 0;
+    f.units = static_cast<uint32_t>(f.vec ? total / 4 : total);
+    f.spatial_div = oxh::make_fastdiv(static_cast<uint32_t>(spatial));
+    f.channel_div = oxh::make_fastdiv(static_cast<uint32_t>(channels));
+    uint64_t blocks = (f.units + kMapBlock - 1) / kMapBlock;
+    const uint64_t cap = 8ull * oxh::kComputeUnits;
+    if (blocks > cap) blocks = cap;
+    oxh::launch(bn_flat_map_kernel<P>, dim3(static_cast<uint32_t>(blocks)), dim3(kMapBlock), 0,
+                oxh::as_stream(stream), f, a);
+    return oxh::launched(name);
+  }
   const PlaneMap m = make_plane_map(batch, channels, spatial, aligned);
   oxh::launch(bn_map_kernel<P>, dim3(static_cast<uint32_t>(m.blocks)), dim3(kMapBlock),
                      0, oxh::as_stream(stream), m, a);
@@ -849,13 +953,22 @@ oxh_status oxh_batch_norm_forward_apply(oxh_stream stream, uint64_t batch, uint6
   const uint64_t bytes = batch * channels * spatial * 4;
   st = no_overlap(name, output, bytes, {input}, bytes);
   if (st != OXH_OK) return st;
+  const StatsOut stats{saved_mean, saved_inverse_std, nullptr, running_mean, running_variance,
+                       momentum, epsilon};
+  const bool aligned = oxh::aligned16(input) && oxh::aligned16(output);
+  if (use_flat(batch, channels, spatial)) {
+    oxh::launch(bn_finalize_forward_kernel, dim3((channels + 3) / 4), dim3(256), 0,
+                oxh::as_stream(stream), g, input, static_cast<const double2 *>(workspace),
+                stats);
+    st = oxh::launched(name);
+    if (st != OXH_OK) return st;
+    ApplyPhase::Args a{input, weight, bias, saved_mean, saved_inverse_std, nullptr, 0, 0,
+                       StatsOut{}, output};
+    return launch_map<ApplyPhase>(name, stream, batch, channels, spatial, aligned, a);
+  }
   ApplyPhase::Args a{input, weight, bias, nullptr, nullptr,
-                     static_cast<const double2 *>(workspace), g.slices, g.samples,
-                     StatsOut{saved_mean, saved_inverse_std, nullptr, running_mean,
-                              running_variance, momentum, epsilon},
-                     output};
-  return launch_map<ApplyPhase>(name, stream, batch, channels, spatial,
-                                oxh::aligned16(input) && oxh::aligned16(output), a);
+                     static_cast<const double2 *>(workspace), g.slices, g.samples, stats, output};
+  return launch_map<ApplyPhase>(name, stream, batch, channels, spatial, aligned, a);
 }
 
 oxh_status oxh_batch_norm_backward_reduce(oxh_stream stream, uint64_t batch, uint64_t channels,
@@ -887,13 +1000,23 @@ oxh_status oxh_batch_norm_backward_input(oxh_stream stream, uint64_t batch, uint
   const uint64_t bytes = batch * channels * spatial * 4;
   st = no_overlap(name, input_gradient, bytes, {input, gradient}, bytes);
   if (st != OXH_OK) return st;
+  const bool aligned =
+      oxh::aligned16(gradient) && oxh::aligned16(input) && oxh::aligned16(input_gradient);
+  const float samples = static_cast<float>(batch * spatial);
+  if (use_flat(batch, channels, spatial)) {
+    oxh::launch(bn_finalize_affine_kernel, dim3((channels + 3) / 4), dim3(256), 0,
+                oxh::as_stream(stream), g, static_cast<const double2 *>(workspace),
+                weight_gradient, bias_gradient);
+    st = oxh::launched(name);
+    if (st != OXH_OK) return st;
+    DxTrainPhase::Args a{gradient, input, weight, saved_mean, saved_inverse_std, weight_gradient,
+                         bias_gradient, nullptr, 0, samples, nullptr, nullptr, input_gradient};
+    return launch_map<DxTrainPhase>(name, stream, batch, channels, spatial, aligned, a);
+  }
   DxTrainPhase::Args a{gradient, input, weight, saved_mean, saved_inverse_std, nullptr, nullptr,
-                       static_cast<const double2 *>(workspace), g.slices,
-                       static_cast<float>(batch * spatial), weight_gradient, bias_gradient,
-                       input_gradient};
-  return launch_map<DxTrainPhase>(
-      name, stream, batch, channels, spatial,
-      oxh::aligned16(gradient) && oxh::aligned16(input) && oxh::aligned16(input_gradient), a);
+                       static_cast<const double2 *>(workspace), g.slices, samples,
+                       weight_gradient, bias_gradient, input_gradient};
+  return launch_map<DxTrainPhase>(name, stream, batch, channels, spatial, aligned, a);
 }
 
 oxh_status oxh_batch_norm_forward_train(oxh_stream stream, uint64_t batch, uint64_t channels,

@@ -13,8 +13,23 @@
 // window order.  These are the CPU path's exact fp32 operation sequences (-ffp-contract=off),
 // so the results are bit-identical.  Weight and bias gradients reduce over batch * oh * ow
 // terms; one thread per weight element would serialize thousands of dependent adds, so they are
-// split into batch chunks (each chunk in the CPU order) whose partial sums a second launch adds
-// in chunk order: deterministic, within fp32 rounding of the CPU's single running sum.
+// split into chunks of that range (each chunk in the CPU order) whose partial sums a second
+// launch adds in chunk order: deterministic, within fp32 rounding of the CPU's single running
+// sum.
+//
+// Kernels (gfx950).  Index arithmetic is 32-bit with multiply-high division (tensors below 2^31
+// elements), and the valid kernel taps / output positions of each element are computed in
+// closed form, so the inner loops carry no bounds tests.
+//   * Pointwise convolutions (1x1, stride 1, no padding, one group) are matrix products
+//     Y[oc, (n,p)] = b[oc] + sum_ic W[oc, ic] X[ic, (n,p)], and likewise the input and weight
+//     gradients.  They run as an LDS-tiled product: 32 x 32 outputs per 256-thread block, 2 x 2
+//     per thread, k-slabs of 128 staged through LDS with the next slab's loads in flight during
+//     the current slab's arithmetic.  Each output is still one serial sum in ascending k from
+//     its initial value -- the CPU order -- so forward and input gradient stay bit-identical;
+//     the weight gradient splits k into fixed chunks.  No MFMA: a matrix-core instruction
+//     reorders the additions inside each tile.
+//   * Other convolutions (depthwise, and the strided 3 x 3 full convolutions) run one output
+//     (or input, or weight-chunk) element per thread.
 #include <hip/hip_runtime.h>
 
 #include <string>
@@ -23,37 +38,57 @@
 
 namespace {
 
+constexpr uint64_t kMaxElems = 1ull << 31;  // 32-bit index arithmetic
+
 struct ConvGeom {
   uint32_t batch, in_c, h, w, out_c, kh, kw, stride, pad, groups;
   uint32_t oh, ow, in_per_group, out_per_group;
+  oxh::FastDiv ow_div, oh_div, oc_div, w_div, h_div, ic_div, s_div, ipg_div, opg_div, kw_div,
+      kh_div;
 };
 
-__global__ __launch_bounds__(256) void conv2d_forward_kernel(ConvGeom g,
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, const oxh::FastDiv &d) {
+  return oxh::fast_div(n, d);
+}
+
+// Largest q with q * s <= a for a >= 0; -1 for a < 0.
+__device__ __forceinline__ int floor_div(int a, const oxh::FastDiv &s) {
+  return a < 0 ? -1 : static_cast<int>(fdiv(static_cast<uint32_t>(a), s));
+}
+// Smallest q >= 0 with q * s >= a.
+__device__ __forceinline__ int ceil_div0(int a, const oxh::FastDiv &s) {
+  return a <= 0 ? 0 : static_cast<int>(fdiv(static_cast<uint32_t>(a) + s.d - 1, s));
+}
+
+// ---------------------------------------------------------------- direct kernels
+
+__global__ __launch_bounds__(256) void conv2d_forward_kernel(ConvGeom g, uint32_t total,
                                                              const float *__restrict__ x,
                                                              const float *__restrict__ wt,
                                                              const float *__restrict__ bias,
                                                              float *__restrict__ y) {
-  const uint64_t total = static_cast<uint64_t>(g.batch) * g.out_c * g.oh * g.ow;
-  for (uint64_t o = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; o < total;
-       o += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
-    const uint32_t ox = static_cast<uint32_t>(o % g.ow);
-    const uint32_t oy = static_cast<uint32_t>((o / g.ow) % g.oh);
-    const uint32_t oc = static_cast<uint32_t>((o / (static_cast<uint64_t>(g.ow) * g.oh)) % g.out_c);
-    const uint64_t n = o / (static_cast<uint64_t>(g.ow) * g.oh * g.out_c);
-    const uint32_t group = oc / g.out_per_group;
+  for (uint32_t o = blockIdx.x * 256 + threadIdx.x; o < total; o += gridDim.x * 256) {
+    const uint32_t t0 = fdiv(o, g.ow_div), ox = o - t0 * g.ow;
+    const uint32_t t1 = fdiv(t0, g.oh_div), oy = t0 - t1 * g.oh;
+    const uint32_t n = fdiv(t1, g.oc_div), oc = t1 - n * g.out_c;
+    const uint32_t group = fdiv(oc, g.opg_div);
+    const int by = static_cast<int>(oy * g.stride) - static_cast<int>(g.pad);
+    const int bx = static_cast<int>(ox * g.stride) - static_cast<int>(g.pad);
+    // taps with 0 <= by + ky < h and 0 <= bx + kx < w
+    const int ky0 = by < 0 ? -by : 0, kx0 = bx < 0 ? -bx : 0;
+    const int ky1 = min(static_cast<int>(g.kh), static_cast<int>(g.h) - by);
+    const int kx1 = min(static_cast<int>(g.kw), static_cast<int>(g.w) - bx);
+    const uint32_t plane = g.h * g.w, taps = g.kh * g.kw;
+    const float *xn = x + (n * g.in_c + group * g.in_per_group) * plane;
+    const float *wo = wt + oc * g.in_per_group * taps;
     float sum = bias[oc];
     for (uint32_t lc = 0; lc < g.in_per_group; ++lc) {
-      const uint32_t ic = group * g.in_per_group + lc;
-      const float *xp = x + (n * g.in_c + ic) * g.h * g.w;
-      const float *wp = wt + (static_cast<uint64_t>(oc) * g.in_per_group + lc) * g.kh * g.kw;
-      for (uint32_t ky = 0; ky < g.kh; ++ky) {
-        const int iy = static_cast<int>(oy * g.stride + ky) - static_cast<int>(g.pad);
-        if (iy < 0 || iy >= static_cast<int>(g.h)) continue;
-        for (uint32_t kx = 0; kx < g.kw; ++kx) {
-          const int ix = static_cast<int>(ox * g.stride + kx) - static_cast<int>(g.pad);
-          if (ix < 0 || ix >= static_cast<int>(g.w)) continue;
-          sum += xp[iy * g.w + ix] * wp[ky * g.kw + kx];
-        }
+      const float *xp = xn + lc * plane;
+      const float *wp = wo + lc * taps;
+      for (int ky = ky0; ky < ky1; ++ky) {
+        const float *xr = xp + (by + ky) * static_cast<int>(g.w) + bx;
+        const float *wr = wp + ky * static_cast<int>(g.kw);
+        for (int kx = kx0; kx < kx1; ++kx) sum += xr[kx] * wr[kx];
       }
     }
     y[o] = sum;
@@ -62,160 +97,303 @@ __global__ __launch_bounds__(256) void conv2d_forward_kernel(ConvGeom g,
 
 // One thread per input element; contributions in (oc, oy, ox) ascending order.
 __global__ __launch_bounds__(256) void conv2d_input_backward_kernel(
-    ConvGeom g, const float *__restrict__ grad, const float *__restrict__ wt,
+    ConvGeom g, uint32_t total, const float *__restrict__ grad, const float *__restrict__ wt,
     float *__restrict__ dx) {
-  const uint64_t total = static_cast<uint64_t>(g.batch) * g.in_c * g.h * g.w;
-  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
-       i += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
-    const uint32_t ix = static_cast<uint32_t>(i % g.w);
-    const uint32_t iy = static_cast<uint32_t>((i / g.w) % g.h);
-    const uint32_t ic = static_cast<uint32_t>((i / (static_cast<uint64_t>(g.w) * g.h)) % g.in_c);
-    const uint64_t n = i / (static_cast<uint64_t>(g.w) * g.h * g.in_c);
-    const uint32_t group = ic / g.in_per_group, lc = ic % g.in_per_group;
+  for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < total; i += gridDim.x * 256) {
+    const uint32_t t0 = fdiv(i, g.w_div), ix = i - t0 * g.w;
+    const uint32_t t1 = fdiv(t0, g.h_div), iy = t0 - t1 * g.h;
+    const uint32_t n = fdiv(t1, g.ic_div), ic = t1 - n * g.in_c;
+    const uint32_t group = fdiv(ic, g.ipg_div), lc = ic - group * g.in_per_group;
+    // outputs with 0 <= ty - oy * s < kh, ty = iy + pad (and likewise in x)
+    const int ty = static_cast<int>(iy + g.pad), tx = static_cast<int>(ix + g.pad);
+    const int oy0 = ceil_div0(ty - static_cast<int>(g.kh) + 1, g.s_div);
+    const int ox0 = ceil_div0(tx - static_cast<int>(g.kw) + 1, g.s_div);
+    const int oy1 = min(floor_div(ty, g.s_div), static_cast<int>(g.oh) - 1);
+    const int ox1 = min(floor_div(tx, g.s_div), static_cast<int>(g.ow) - 1);
+    const uint32_t oplane = g.oh * g.ow, taps = g.kh * g.kw;
+    const int s = static_cast<int>(g.stride);
     float acc = 0.0f;
     for (uint32_t j = 0; j < g.out_per_group; ++j) {
       const uint32_t oc = group * g.out_per_group + j;
-      const float *gp = grad + (n * g.out_c + oc) * g.oh * g.ow;
-      const float *wp = wt + (static_cast<uint64_t>(oc) * g.in_per_group + lc) * g.kh * g.kw;
-      // oy = (iy + pad - ky) / stride ascends as ky descends
-      for (int ky = static_cast<int>(g.kh) - 1; ky >= 0; --ky) {
-        const int ty = static_cast<int>(iy + g.pad) - ky;
-        if (ty < 0 || ty % static_cast<int>(g.stride) != 0) continue;
-        const int oy = ty / static_cast<int>(g.stride);
-        if (oy >= static_cast<int>(g.oh)) continue;
-        for (int kx = static_cast<int>(g.kw) - 1; kx >= 0; --kx) {
-          const int tx = static_cast<int>(ix + g.pad) - kx;
-          if (tx < 0 || tx % static_cast<int>(g.stride) != 0) continue;
-          const int ox = tx / static_cast<int>(g.stride);
-          if (ox >= static_cast<int>(g.ow)) continue;
-          acc += gp[oy * g.ow + ox] * wp[ky * g.kw + kx];
-        }
+      const float *gp = grad + (n * g.out_c + oc) * oplane;
+      const float *wp = wt + (oc * g.in_per_group + lc) * taps;
+      for (int oy = oy0; oy <= oy1; ++oy) {
+        const float *gr = gp + oy * static_cast<int>(g.ow);
+        // kx = tx - ox * s
+        const float *wr = wp + (ty - oy * s) * static_cast<int>(g.kw) + tx;
+        for (int ox = ox0; ox <= ox1; ++ox) acc += gr[ox] * wr[-ox * s];
       }
     }
     dx[i] = acc;
   }
 }
 
-// Weight gradient, phase 1: chunk c of the batch for weight element e (grid-stride over
+// Weight gradient, phase 1: batch chunk c for weight element e (grid-stride over
 // chunks * weights), terms in (n, oy, ox) order.
 __global__ __launch_bounds__(256) void conv2d_weight_partial_kernel(
-    ConvGeom g, uint32_t chunks, const float *__restrict__ grad, const float *__restrict__ x,
-    float *__restrict__ partial) {
-  const uint64_t weights = static_cast<uint64_t>(g.out_c) * g.in_per_group * g.kh * g.kw;
-  const uint64_t total = weights * chunks;
+    ConvGeom g, uint32_t weights, oxh::FastDiv weights_div, uint32_t chunks,
+    const float *__restrict__ grad, const float *__restrict__ x, float *__restrict__ partial) {
+  const uint32_t total = weights * chunks;
   const uint32_t per = (g.batch + chunks - 1) / chunks;
-  for (uint64_t t = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < total;
-       t += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
-    const uint64_t e = t % weights;
-    const uint32_t chunk = static_cast<uint32_t>(t / weights);
-    const uint32_t kx = static_cast<uint32_t>(e % g.kw);
-    const uint32_t ky = static_cast<uint32_t>((e / g.kw) % g.kh);
-    const uint32_t lc = static_cast<uint32_t>((e / (static_cast<uint64_t>(g.kw) * g.kh)) % g.in_per_group);
-    const uint32_t oc = static_cast<uint32_t>(e / (static_cast<uint64_t>(g.kw) * g.kh * g.in_per_group));
-    const uint32_t ic = (oc / g.out_per_group) * g.in_per_group + lc;
-    const uint32_t n0 = chunk * per, n1 = n0 + per < g.batch ? n0 + per : g.batch;
+  const uint32_t plane = g.h * g.w, oplane = g.oh * g.ow;
+  const int s = static_cast<int>(g.stride);
+  for (uint32_t t = blockIdx.x * 256 + threadIdx.x; t < total; t += gridDim.x * 256) {
+    const uint32_t chunk = fdiv(t, weights_div), e = t - chunk * weights;
+    const uint32_t t0 = fdiv(e, g.kw_div), kx = e - t0 * g.kw;
+    const uint32_t t1 = fdiv(t0, g.kh_div), ky = t0 - t1 * g.kh;
+    const uint32_t oc = fdiv(t1, g.ipg_div), lc = t1 - oc * g.in_per_group;
+    const uint32_t ic = fdiv(oc, g.opg_div) * g.in_per_group + lc;
+    // outputs with 0 <= oy * s + dy < h, dy = ky - pad (and likewise in x)
+    const int dy = static_cast<int>(ky) - static_cast<int>(g.pad);
+    const int dx = static_cast<int>(kx) - static_cast<int>(g.pad);
+    const int oy0 = ceil_div0(-dy, g.s_div), ox0 = ceil_div0(-dx, g.s_div);
+    const int oy1 = min(floor_div(static_cast<int>(g.h) - 1 - dy, g.s_div),
+                        static_cast<int>(g.oh) - 1);
+    const int ox1 = min(floor_div(static_cast<int>(g.w) - 1 - dx, g.s_div),
+                        static_cast<int>(g.ow) - 1);
+    const uint32_t n0 = chunk * per, n1 = min(n0 + per, g.batch);
     float acc = 0.0f;
     for (uint32_t n = n0; n < n1; ++n) {
-      const float *gp = grad + (static_cast<uint64_t>(n) * g.out_c + oc) * g.oh * g.ow;
-      const float *xp = x + (static_cast<uint64_t>(n) * g.in_c + ic) * g.h * g.w;
-      for (uint32_t oy = 0; oy < g.oh; ++oy) {
-        const int iy = static_cast<int>(oy * g.stride + ky) - static_cast<int>(g.pad);
-        if (iy < 0 || iy >= static_cast<int>(g.h)) continue;
-        for (uint32_t ox = 0; ox < g.ow; ++ox) {
-          const int ix = static_cast<int>(ox * g.stride + kx) - static_cast<int>(g.pad);
-          if (ix < 0 || ix >= static_cast<int>(g.w)) continue;
-          acc += gp[oy * g.ow + ox] * xp[iy * g.w + ix];
-        }
+      const float *gp = grad + (n * g.out_c + oc) * oplane;
+      const float *xp = x + (n * g.in_c + ic) * plane;
+      for (int oy = oy0; oy <= oy1; ++oy) {
+        const float *gr = gp + oy * static_cast<int>(g.ow);
+        const float *xr = xp + (oy * s + dy) * static_cast<int>(g.w) + dx;
+        for (int ox = ox0; ox <= ox1; ++ox) acc += gr[ox] * xr[ox * s];
       }
     }
     partial[t] = acc;
   }
 }
 
-// Bias gradient, phase 1: chunk c of the batch for output channel oc, terms in (n, oy, ox).
+// Bias gradient, phase 1: batch chunk c for output channel oc, terms in (n, oy, ox).
 __global__ __launch_bounds__(256) void conv2d_bias_partial_kernel(
-    uint32_t batch, uint32_t out_c, uint32_t plane, uint32_t chunks,
+    uint32_t batch, uint32_t out_c, oxh::FastDiv out_c_div, uint32_t plane, uint32_t chunks,
     const float *__restrict__ grad, float *__restrict__ partial) {
-  const uint64_t total = static_cast<uint64_t>(out_c) * chunks;
+  const uint32_t total = out_c * chunks;
   const uint32_t per = (batch + chunks - 1) / chunks;
-  for (uint64_t t = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < total;
-       t += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
-    const uint32_t oc = static_cast<uint32_t>(t % out_c);
-    const uint32_t chunk = static_cast<uint32_t>(t / out_c);
-    const uint32_t n0 = chunk * per, n1 = n0 + per < batch ? n0 + per : batch;
+  for (uint32_t t = blockIdx.x * 256 + threadIdx.x; t < total; t += gridDim.x * 256) {
+    const uint32_t chunk = fdiv(t, out_c_div), oc = t - chunk * out_c;
+    const uint32_t n0 = chunk * per, n1 = min(n0 + per, batch);
     float acc = 0.0f;
     for (uint32_t n = n0; n < n1; ++n) {
-      const float *gp = grad + (static_cast<uint64_t>(n) * out_c + oc) * plane;
+      const float *gp = grad + (n * out_c + oc) * plane;
       for (uint32_t i = 0; i < plane; ++i) acc += gp[i];
     }
     partial[t] = acc;
   }
 }
 
-// Phase 2 of both: out[e] = sum over chunks of partial[chunk][e], in chunk order.
-__global__ __launch_bounds__(256) void sum_chunks_kernel(uint64_t count, uint32_t chunks,
+// Phase 2 of both: out[e] = sum over chunks of partial[chunk][e], in chunk order (loads issued
+// in groups of 8 ahead of the serial adds).
+__global__ __launch_bounds__(256) void sum_chunks_kernel(uint32_t count, uint32_t chunks,
                                                          const float *__restrict__ partial,
                                                          float *__restrict__ out) {
-  for (uint64_t e = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < count;
-       e += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
+  for (uint32_t e = blockIdx.x * 256 + threadIdx.x; e < count; e += gridDim.x * 256) {
     float acc = 0.0f;
-    for (uint32_t c = 0; c < chunks; ++c) acc += partial[c * count + e];
+    uint32_t c = 0;
+    for (; c + 8 <= chunks; c += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = partial[static_cast<uint64_t>(c + u) * count + e];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc += v[u];
+    }
+    for (; c < chunks; ++c) acc += partial[static_cast<uint64_t>(c) * count + e];
     out[e] = acc;
   }
 }
 
+// ---------------------------------------------------------------- pointwise product
+
+// Offset of index i along one operand axis: (i / p) * outer + (i % p) * inner.
+struct Axis {
+  oxh::FastDiv p;
+  uint32_t outer, inner;
+};
+
+__device__ __forceinline__ uint32_t axis_offset(const Axis &a, uint32_t i) {
+  const uint32_t q = fdiv(i, a.p);
+  return q * a.outer + (i - q * a.p.d) * a.inner;
+}
+
+// Element (r, k) of an operand lies at ptr[offset(row, r) + offset(k, k)].  k_fast: consecutive
+// threads load consecutive k (the operand is contiguous along k), else consecutive rows.
+struct Operand {
+  const float *ptr;
+  Axis row, k;
+  bool k_fast;
+};
+
+struct ProductArgs {
+  Operand a, b;       // a: (m, k); b: (n, k)
+  float *c;           // c[chunk * c_chunk + offset(cm, m) + offset(cn, n)]
+  Axis cm, cn;
+  uint32_t c_chunk;
+  const float *init;  // initial value per m (the bias), or null for 0
+  uint32_t M, N, K, k_chunk;
+};
+
+constexpr int kTile = 32, kMicro = 2, kSlab = 128;
+constexpr int kTileLoads = kTile * kSlab / 256;  // per thread, per operand, per slab
+
+__device__ __forceinline__ void tile_coords(bool k_fast, int e, int &r, int &kk) {
+  if (k_fast) {
+    kk = e % kSlab;
+    r = e / kSlab;
+  } else {
+    r = e % kTile;
+    kk = e / kTile;
+  }
+}
+
+__device__ __forceinline__ void fetch_slab(const Operand &o, uint32_t r0, uint32_t rows,
+                                           uint32_t k0, uint32_t kc, float (&v)[kTileLoads]) {
+#pragma unroll
+  for (int u = 0; u < kTileLoads; ++u) {
+    int r, kk;
+    tile_coords(o.k_fast, threadIdx.x + u * 256, r, kk);
+    const uint32_t row = r0 + r;
+    v[u] = (row < rows && static_cast<uint32_t>(kk) < kc)
+               ? o.ptr[axis_offset(o.row, row) + axis_offset(o.k, k0 + kk)]
+               : 0.0f;
+  }
+}
+
+// LDS rows padded to kTile + 1 floats: k-fast stores hit distinct banks.
+__device__ __forceinline__ void stage_slab(bool k_fast, const float (&v)[kTileLoads],
+                                           float (*s)[kTile + 1]) {
+#pragma unroll
+  for (int u = 0; u < kTileLoads; ++u) {
+    int r, kk;
+    tile_coords(k_fast, threadIdx.x + u * 256, r, kk);
+    s[kk][r] = v[u];
+  }
+}
+
+// C[m, n] = init[m] + sum_{k in chunk, ascending} A[m, k] * B[n, k]: one serial fp32 sum per
+// output (each product rounded, then added: -ffp-contract=off).
+__global__ __launch_bounds__(256) void pointwise_product_kernel(ProductArgs g) {
+  __shared__ float as[kSlab][kTile + 1];
+  __shared__ float bs[kSlab][kTile + 1];
+  const uint32_t m0 = blockIdx.y * kTile, n0 = blockIdx.x * kTile;
+  const uint32_t kb = blockIdx.z * g.k_chunk;
+  const uint32_t ke = min(kb + g.k_chunk, g.K);
+  constexpr int kCols = kTile / kMicro;  // 16 x 16 threads
+  const int tx = threadIdx.x % kCols, ty = threadIdx.x / kCols;
+  float acc[kMicro][kMicro];
+#pragma unroll
+  for (int i = 0; i < kMicro; ++i) {
+    const uint32_t m = m0 + ty * kMicro + i;
+    const float v = (g.init != nullptr && m < g.M) ? g.init[m] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < kMicro; ++j) acc[i][j] = v;
+  }
+  float va[kTileLoads], vb[kTileLoads];
+  if (kb < ke) {
+    const uint32_t kc = min(ke - kb, static_cast<uint32_t>(kSlab));
+    fetch_slab(g.a, m0, g.M, kb, kc, va);
+    fetch_slab(g.b, n0, g.N, kb, kc, vb);
+  }
+  for (uint32_t k0 = kb; k0 < ke; k0 += kSlab) {
+    const uint32_t kc = min(ke - k0, static_cast<uint32_t>(kSlab));
+    stage_slab(g.a.k_fast, va, as);
+    stage_slab(g.b.k_fast, vb, bs);
+    __syncthreads();
+    const uint32_t k1 = k0 + kSlab;
+    if (k1 < ke) {  // the next slab's loads overlap this slab's arithmetic
+      const uint32_t kc1 = min(ke - k1, static_cast<uint32_t>(kSlab));
+      fetch_slab(g.a, m0, g.M, k1, kc1, va);
+      fetch_slab(g.b, n0, g.N, k1, kc1, vb);
+    }
+    for (uint32_t kk = 0; kk < kc; ++kk) {
+      float av[kMicro], bv[kMicro];
+#pragma unroll
+      for (int i = 0; i < kMicro; ++i) av[i] = as[kk][ty * kMicro + i];
+#pragma unroll
+      for (int j = 0; j < kMicro; ++j) bv[j] = bs[kk][tx * kMicro + j];
+#pragma unroll
+      for (int i = 0; i < kMicro; ++i)
+#pragma unroll
+        for (int j = 0; j < kMicro; ++j) acc[i][j] += av[i] * bv[j];
+    }
+    __syncthreads();
+  }
+  float *c = g.c + static_cast<uint64_t>(blockIdx.z) * g.c_chunk;
+#pragma unroll
+  for (int i = 0; i < kMicro; ++i) {
+    const uint32_t m = m0 + ty * kMicro + i;
+    if (m >= g.M) continue;
+#pragma unroll
+    for (int j = 0; j < kMicro; ++j) {
+      const uint32_t n = n0 + tx * kMicro + j;
+      if (n < g.N) c[axis_offset(g.cm, m) + axis_offset(g.cn, n)] = acc[i][j];
+    }
+  }
+}
+
+// ---------------------------------------------------------------- pooling
+
 struct PoolGeom {
   uint32_t batch, channels, h, w, kh, kw, sh, sw, oh, ow;
+  oxh::FastDiv ow_div, oh_div, w_div, h_div, sh_div, sw_div;
   float denominator;
 };
 
 // evaluation.rs:414-444: window sum in (ky, kx) order divided by the window area.
-__global__ __launch_bounds__(256) void avg_pool2d_forward_kernel(PoolGeom g,
+__global__ __launch_bounds__(256) void avg_pool2d_forward_kernel(PoolGeom g, uint32_t total,
                                                                  const float *__restrict__ x,
                                                                  float *__restrict__ y) {
-  const uint64_t total = static_cast<uint64_t>(g.batch) * g.channels * g.oh * g.ow;
-  for (uint64_t o = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; o < total;
-       o += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
-    const uint32_t ox = static_cast<uint32_t>(o % g.ow);
-    const uint32_t oy = static_cast<uint32_t>((o / g.ow) % g.oh);
-    const uint64_t plane = o / (static_cast<uint64_t>(g.ow) * g.oh);
-    const float *xp = x + plane * g.h * g.w;
+  for (uint32_t o = blockIdx.x * 256 + threadIdx.x; o < total; o += gridDim.x * 256) {
+    const uint32_t t0 = fdiv(o, g.ow_div), ox = o - t0 * g.ow;
+    const uint32_t plane = fdiv(t0, g.oh_div), oy = t0 - plane * g.oh;
+    const float *xp = x + plane * g.h * g.w + oy * g.sh * g.w + ox * g.sw;
     float sum = 0.0f;
     for (uint32_t ky = 0; ky < g.kh; ++ky)
-      for (uint32_t kx = 0; kx < g.kw; ++kx)
-        sum += xp[(oy * g.sh + ky) * g.w + ox * g.sw + kx];
+      for (uint32_t kx = 0; kx < g.kw; ++kx) sum += xp[ky * g.w + kx];
     y[o] = sum / g.denominator;
   }
 }
 
 // autograd.rs:501-525: each output adds g / area to every input of its window; gathered here per
 // input element in (oy, ox) ascending order.
-__global__ __launch_bounds__(256) void avg_pool2d_backward_kernel(PoolGeom g,
+__global__ __launch_bounds__(256) void avg_pool2d_backward_kernel(PoolGeom g, uint32_t total,
                                                                   const float *__restrict__ grad,
                                                                   float *__restrict__ dx) {
-  const uint64_t total = static_cast<uint64_t>(g.batch) * g.channels * g.h * g.w;
-  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
-       i += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
-    const uint32_t ix = static_cast<uint32_t>(i % g.w);
-    const uint32_t iy = static_cast<uint32_t>((i / g.w) % g.h);
-    const uint64_t plane = i / (static_cast<uint64_t>(g.w) * g.h);
+  for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < total; i += gridDim.x * 256) {
+    const uint32_t t0 = fdiv(i, g.w_div), ix = i - t0 * g.w;
+    const uint32_t plane = fdiv(t0, g.h_div), iy = t0 - plane * g.h;
     const float *gp = grad + plane * g.oh * g.ow;
     // outputs oy with oy * sh <= iy < oy * sh + kh
-    const uint32_t oy_lo = iy + 1 > g.kh ? (iy + 1 - g.kh + g.sh - 1) / g.sh : 0;
-    const uint32_t ox_lo = ix + 1 > g.kw ? (ix + 1 - g.kw + g.sw - 1) / g.sw : 0;
+    const int oy0 = ceil_div0(static_cast<int>(iy) - static_cast<int>(g.kh) + 1, g.sh_div);
+    const int ox0 = ceil_div0(static_cast<int>(ix) - static_cast<int>(g.kw) + 1, g.sw_div);
+    const int oy1 = min(floor_div(static_cast<int>(iy), g.sh_div), static_cast<int>(g.oh) - 1);
+    const int ox1 = min(floor_div(static_cast<int>(ix), g.sw_div), static_cast<int>(g.ow) - 1);
     float acc = 0.0f;
-    for (uint32_t oy = oy_lo; oy < g.oh && oy * g.sh <= iy; ++oy)
-      for (uint32_t ox = ox_lo; ox < g.ow && ox * g.sw <= ix; ++ox)
-        acc += gp[oy * g.ow + ox] / g.denominator;
+    for (int oy = oy0; oy <= oy1; ++oy)
+      for (int ox = ox0; ox <= ox1; ++ox)
+        acc += gp[oy * static_cast<int>(g.ow) + ox] / g.denominator;
     dx[i] = acc;
   }
 }
+
+// ---------------------------------------------------------------- host side
 
 uint32_t grid_for(uint64_t items) {
   uint64_t g = (items + 255) / 256;
   if (g < 1) g = 1;
   if (g > (1u << 20)) g = 1u << 20;
   return static_cast<uint32_t>(g);
+}
+
+uint64_t input_elems(const ConvGeom &g) {
+  return static_cast<uint64_t>(g.batch) * g.in_c * g.h * g.w;
+}
+uint64_t output_elems(const ConvGeom &g) {
+  return static_cast<uint64_t>(g.batch) * g.out_c * g.oh * g.ow;
+}
+uint64_t weight_elems(const ConvGeom &g) {
+  return static_cast<uint64_t>(g.out_c) * g.in_per_group * g.kh * g.kw;
 }
 
 oxh_status make_conv_geom(const char *name, const oxh_conv2d_shape *s, ConvGeom &g) {
@@ -233,6 +411,18 @@ oxh_status make_conv_geom(const char *name, const oxh_conv2d_shape *s, ConvGeom 
   OXH_REQUIRE(s->height + 2 * s->padding >= s->kernel_h &&
                   s->width + 2 * s->padding >= s->kernel_w,
               OXH_INVALID_SHAPE, std::string(name) + ": kernel larger than the padded input");
+  // every tensor, and the index ranges the kernels form, below 2^31
+  const uint64_t in_n = s->batch * s->in_channels * s->height * s->width;
+  const uint64_t oh = (s->height + 2 * s->padding - s->kernel_h) / s->stride + 1;
+  const uint64_t ow = (s->width + 2 * s->padding - s->kernel_w) / s->stride + 1;
+  const uint64_t out_n = s->batch * s->out_channels * oh * ow;
+  const uint64_t w_n = s->out_channels * (s->in_channels / s->groups) * s->kernel_h * s->kernel_w;
+  const uint64_t sizes[] = {s->batch * s->in_channels, s->batch * s->out_channels, in_n, out_n,
+                            w_n, s->height + s->padding + s->kernel_h,
+                            s->width + s->padding + s->kernel_w};
+  for (uint64_t n : sizes)
+    OXH_REQUIRE(n < kMaxElems, OXH_INVALID_SHAPE,
+                std::string(name) + ": tensors are limited to 2^31 elements");
   g.batch = static_cast<uint32_t>(s->batch);
   g.in_c = static_cast<uint32_t>(s->in_channels);
   g.h = static_cast<uint32_t>(s->height);
@@ -243,32 +433,91 @@ oxh_status make_conv_geom(const char *name, const oxh_conv2d_shape *s, ConvGeom 
   g.stride = static_cast<uint32_t>(s->stride);
   g.pad = static_cast<uint32_t>(s->padding);
   g.groups = static_cast<uint32_t>(s->groups);
-  g.oh = (g.h + 2 * g.pad - g.kh) / g.stride + 1;
-  g.ow = (g.w + 2 * g.pad - g.kw) / g.stride + 1;
+  g.oh = static_cast<uint32_t>(oh);
+  g.ow = static_cast<uint32_t>(ow);
   g.in_per_group = g.in_c / g.groups;
   g.out_per_group = g.out_c / g.groups;
-  const uint64_t sizes[] = {static_cast<uint64_t>(g.batch) * g.in_c * g.h * g.w,
-                            static_cast<uint64_t>(g.batch) * g.out_c * g.oh * g.ow,
-                            static_cast<uint64_t>(g.out_c) * g.in_per_group * g.kh * g.kw};
-  for (uint64_t n : sizes)
-    OXH_REQUIRE(n < (1ull << 40), OXH_INVALID_SHAPE, std::string(name) + ": tensor too large");
+  g.ow_div = oxh::make_fastdiv(g.ow);
+  g.oh_div = oxh::make_fastdiv(g.oh);
+  g.oc_div = oxh::make_fastdiv(g.out_c);
+  g.w_div = oxh::make_fastdiv(g.w);
+  g.h_div = oxh::make_fastdiv(g.h);
+  g.ic_div = oxh::make_fastdiv(g.in_c);
+  g.s_div = oxh::make_fastdiv(g.stride);
+  g.ipg_div = oxh::make_fastdiv(g.in_per_group);
+  g.opg_div = oxh::make_fastdiv(g.out_per_group);
+  g.kw_div = oxh::make_fastdiv(g.kw);
+  g.kh_div = oxh::make_fastdiv(g.kh);
   return oxh::ok();
 }
 
-// Batch chunks for the weight / bias reductions: enough threads to fill the GPU (~64K), at most
-// one chunk per batch element.
+// 1x1, stride 1, no padding, one group: the convolution is a matrix product over channels.
+bool pointwise(const ConvGeom &g) {
+  return g.kh == 1 && g.kw == 1 && g.stride == 1 && g.pad == 0 && g.groups == 1 &&
+         (g.out_c + kTile - 1) / kTile <= 65535 && (g.in_c + kTile - 1) / kTile <= 65535;
+}
+
+Axis linear(uint32_t stride) { return Axis{oxh::make_fastdiv(1), stride, 0}; }
+// (n, p) flattened with p < plane: offset n * (channels * plane) + p.
+Axis batch_plane(uint32_t plane, uint32_t channels) {
+  return Axis{oxh::make_fastdiv(plane), channels * plane, 1};
+}
+uint32_t unit_stride(const Axis &a) { return a.p.d == 1 ? a.outer : a.inner; }
+Operand operand(const float *ptr, Axis row, Axis k) {
+  return Operand{ptr, row, k, unit_stride(k) <= unit_stride(row)};
+}
+
+// k chunks of the pointwise weight gradient: about 512 blocks in total, at least 64 k per
+// chunk, every chunk non-empty.
+struct KSplit {
+  uint32_t chunks, per;
+};
+KSplit product_split(const ConvGeom &g) {
+  const uint64_t tiles = static_cast<uint64_t>((g.out_c + kTile - 1) / kTile) *
+                         ((g.in_c + kTile - 1) / kTile);
+  const uint64_t k = static_cast<uint64_t>(g.batch) * g.h * g.w;
+  const uint64_t weights = static_cast<uint64_t>(g.out_c) * g.in_c;
+  uint64_t c = (512 + tiles - 1) / tiles;
+  const uint64_t by_work = k / 64 > 0 ? k / 64 : 1;
+  if (c > by_work) c = by_work;
+  if (c > 1024) c = 1024;
+  while (c > 1 && c * weights >= kMaxElems) --c;
+  if (c < 1) c = 1;
+  const uint64_t per = (k + c - 1) / c;
+  return KSplit{static_cast<uint32_t>((k + per - 1) / per), static_cast<uint32_t>(per)};
+}
+
+oxh_status launch_product(const char *name, hipStream_t s, const ProductArgs &a,
+                          uint32_t chunks) {
+  const dim3 grid((a.N + kTile - 1) / kTile, (a.M + kTile - 1) / kTile, chunks);
+  oxh::launch(pointwise_product_kernel, grid, dim3(256), 0, s, a);
+  return oxh::launched(name);
+}
+
+// Batch chunks for the direct weight / bias reductions: enough threads to fill the GPU, at
+// most one chunk per batch element.
 uint32_t weight_chunks(const ConvGeom &g) {
-  const uint64_t weights = static_cast<uint64_t>(g.out_c) * g.in_per_group * g.kh * g.kw;
+  const uint64_t weights = weight_elems(g);
   uint64_t c = (65536 + weights - 1) / weights;
   if (c > g.batch) c = g.batch;
+  while (c > 1 && weights * c >= kMaxElems) --c;
   if (c < 1) c = 1;
   return static_cast<uint32_t>(c);
 }
 uint32_t bias_chunks(uint64_t batch, uint64_t out_c) {
-  uint64_t c = (65536 + out_c - 1) / out_c;
+  uint64_t c = (16384 + out_c - 1) / out_c;
   if (c > batch) c = batch;
+  while (c > 1 && out_c * c >= kMaxElems) --c;
   if (c < 1) c = 1;
   return static_cast<uint32_t>(c);
+}
+
+uint64_t weight_partial_bytes(const ConvGeom &g) {
+  if (pointwise(g)) {
+    const KSplit k = product_split(g);
+    return k.chunks > 1 ? static_cast<uint64_t>(k.chunks) * g.out_c * g.in_c * 4 : 0;
+  }
+  return weight_elems(g) * weight_chunks(g) * 4;
 }
 
 oxh_status make_pool_geom(const char *name, const oxh_pool2d_shape *s, PoolGeom &g) {
@@ -281,6 +530,9 @@ oxh_status make_pool_geom(const char *name, const oxh_pool2d_shape *s, PoolGeom 
   // tensor/mod.rs:236-250: the window must fit
   OXH_REQUIRE(s->kernel_h <= s->height && s->kernel_w <= s->width, OXH_INVALID_SHAPE,
               std::string(name) + ": avg_pool2d window exceeds the input");
+  OXH_REQUIRE(s->batch * s->channels * s->height * s->width < kMaxElems &&
+                  s->batch * s->channels < kMaxElems,
+              OXH_INVALID_SHAPE, std::string(name) + ": tensors are limited to 2^31 elements");
   g.batch = static_cast<uint32_t>(s->batch);
   g.channels = static_cast<uint32_t>(s->channels);
   g.h = static_cast<uint32_t>(s->height);
@@ -292,8 +544,12 @@ oxh_status make_pool_geom(const char *name, const oxh_pool2d_shape *s, PoolGeom 
   g.oh = (g.h - g.kh) / g.sh + 1;
   g.ow = (g.w - g.kw) / g.sw + 1;
   g.denominator = static_cast<float>(static_cast<uint64_t>(g.kh) * g.kw);
-  OXH_REQUIRE(static_cast<uint64_t>(g.batch) * g.channels * g.h * g.w < (1ull << 40),
-              OXH_INVALID_SHAPE, std::string(name) + ": tensor too large");
+  g.ow_div = oxh::make_fastdiv(g.ow);
+  g.oh_div = oxh::make_fastdiv(g.oh);
+  g.w_div = oxh::make_fastdiv(g.w);
+  g.h_div = oxh::make_fastdiv(g.h);
+  g.sh_div = oxh::make_fastdiv(g.sh);
+  g.sw_div = oxh::make_fastdiv(g.sw);
   return oxh::ok();
 }
 
@@ -321,12 +577,28 @@ oxh_status oxh_conv2d_forward(oxh_stream stream, const oxh_conv2d_shape *shape,
   if (st != OXH_OK) return st;
   OXH_REQUIRE(input && weight && bias && output, OXH_INVALID_SHAPE,
               std::string(name) + ": null pointer");
-  const uint64_t out_n = static_cast<uint64_t>(g.batch) * g.out_c * g.oh * g.ow;
-  const uint64_t in_n = static_cast<uint64_t>(g.batch) * g.in_c * g.h * g.w;
+  const uint64_t out_n = output_elems(g), in_n = input_elems(g);
   OXH_REQUIRE(!oxh::any_overlap(output, out_n * 4, input, in_n * 4), OXH_INVALID_SHAPE,
               std::string(name) + ": output overlaps the input");
-  oxh::launch(conv2d_forward_kernel, dim3(grid_for(out_n)), dim3(256), 0,
-              oxh::as_stream(stream), g, input, weight, bias, output);
+  hipStream_t s = oxh::as_stream(stream);
+  if (pointwise(g)) {
+    // Y[oc, (n, p)] = b[oc] + sum_ic W[oc, ic] X[(n, p), ic]
+    const uint32_t plane = g.h * g.w;
+    ProductArgs a{};
+    a.a = operand(weight, linear(g.in_c), linear(1));
+    a.b = operand(input, batch_plane(plane, g.in_c), linear(plane));
+    a.c = output;
+    a.cm = linear(plane);
+    a.cn = batch_plane(plane, g.out_c);
+    a.init = bias;
+    a.M = g.out_c;
+    a.N = g.batch * plane;
+    a.K = g.in_c;
+    a.k_chunk = a.K;
+    return launch_product(name, s, a, 1);
+  }
+  oxh::launch(conv2d_forward_kernel, dim3(grid_for(out_n)), dim3(256), 0, s, g,
+              static_cast<uint32_t>(out_n), input, weight, bias, output);
   return oxh::launched(name);
 }
 
@@ -339,9 +611,26 @@ oxh_status oxh_conv2d_input_backward(oxh_stream stream, const oxh_conv2d_shape *
   if (st != OXH_OK) return st;
   OXH_REQUIRE(gradient && weight && input_gradient, OXH_INVALID_SHAPE,
               std::string(name) + ": null pointer");
-  const uint64_t in_n = static_cast<uint64_t>(g.batch) * g.in_c * g.h * g.w;
-  oxh::launch(conv2d_input_backward_kernel, dim3(grid_for(in_n)), dim3(256), 0,
-              oxh::as_stream(stream), g, gradient, weight, input_gradient);
+  const uint64_t in_n = input_elems(g);
+  hipStream_t s = oxh::as_stream(stream);
+  if (pointwise(g)) {
+    // dX[ic, (n, p)] = 0 + sum_oc W[oc, ic] G[(n, p), oc]
+    const uint32_t plane = g.h * g.w;
+    ProductArgs a{};
+    a.a = operand(weight, linear(1), linear(g.in_c));
+    a.b = operand(gradient, batch_plane(plane, g.out_c), linear(plane));
+    a.c = input_gradient;
+    a.cm = linear(plane);
+    a.cn = batch_plane(plane, g.in_c);
+    a.init = nullptr;
+    a.M = g.in_c;
+    a.N = g.batch * plane;
+    a.K = g.out_c;
+    a.k_chunk = a.K;
+    return launch_product(name, s, a, 1);
+  }
+  oxh::launch(conv2d_input_backward_kernel, dim3(grid_for(in_n)), dim3(256), 0, s, g,
+              static_cast<uint32_t>(in_n), gradient, weight, input_gradient);
   return oxh::launched(name);
 }
 
@@ -351,10 +640,10 @@ oxh_status oxh_conv2d_weight_backward_workspace_size(const oxh_conv2d_shape *sha
   oxh_status st = make_conv_geom("oxh_conv2d_weight_backward_workspace_size", shape, g);
   if (st != OXH_OK) return st;
   OXH_REQUIRE(bytes != nullptr, OXH_INVALID_SHAPE, "bytes is null");
-  const uint64_t weights = static_cast<uint64_t>(g.out_c) * g.in_per_group * g.kh * g.kw;
-  const uint64_t wb = weights * weight_chunks(g) * 4;
+  const uint64_t wb = weight_partial_bytes(g);
   const uint64_t bb = static_cast<uint64_t>(g.out_c) * bias_chunks(g.batch, g.out_c) * 4;
-  *bytes = ((wb > bb ? wb : bb) + 255) / 256 * 256;
+  const uint64_t need = wb > bb ? wb : bb;
+  *bytes = (need + 255) / 256 * 256;
   return oxh::ok();
 }
 
@@ -368,15 +657,40 @@ oxh_status oxh_conv2d_weight_backward(oxh_stream stream, const oxh_conv2d_shape 
   if (st != OXH_OK) return st;
   OXH_REQUIRE(gradient && input && weight_gradient, OXH_INVALID_SHAPE,
               std::string(name) + ": null pointer");
-  const uint32_t chunks = weight_chunks(g);
-  const uint64_t weights = static_cast<uint64_t>(g.out_c) * g.in_per_group * g.kh * g.kw;
-  OXH_REQUIRE(workspace != nullptr && workspace_bytes >= weights * chunks * 4,
-              OXH_INVALID_SHAPE,
-              std::string(name) + ": workspace too small (oxh_conv2d_weight_backward_workspace_size)");
+  const uint64_t need = weight_partial_bytes(g);
+  OXH_REQUIRE(need == 0 || (workspace != nullptr && workspace_bytes >= need), OXH_INVALID_SHAPE,
+              std::string(name) +
+                  ": workspace too small (oxh_conv2d_weight_backward_workspace_size)");
   float *partial = static_cast<float *>(workspace);
   hipStream_t s = oxh::as_stream(stream);
-  oxh::launch(conv2d_weight_partial_kernel, dim3(grid_for(weights * chunks)), dim3(256), 0, s,
-              g, chunks, gradient, input, partial);
+  if (pointwise(g)) {
+    // dW[oc, ic] = sum_{(n, p)} G[oc, (n, p)] X[ic, (n, p)], k = (n, p) in chunks
+    const uint32_t plane = g.h * g.w;
+    const KSplit split = product_split(g);
+    ProductArgs a{};
+    a.a = operand(gradient, linear(plane), batch_plane(plane, g.out_c));
+    a.b = operand(input, linear(plane), batch_plane(plane, g.in_c));
+    a.c = split.chunks > 1 ? partial : weight_gradient;
+    a.cm = linear(g.in_c);
+    a.cn = linear(1);
+    a.c_chunk = g.out_c * g.in_c;
+    a.init = nullptr;
+    a.M = g.out_c;
+    a.N = g.in_c;
+    a.K = g.batch * plane;
+    a.k_chunk = split.per;
+    st = launch_product(name, s, a, split.chunks);
+    if (st != OXH_OK || split.chunks == 1) return st;
+    const uint32_t count = g.out_c * g.in_c;
+    oxh::launch(sum_chunks_kernel, dim3(grid_for(count)), dim3(256), 0, s, count, split.chunks,
+                static_cast<const float *>(partial), weight_gradient);
+    return oxh::launched(name);
+  }
+  const uint32_t chunks = weight_chunks(g);
+  const uint32_t weights = static_cast<uint32_t>(weight_elems(g));
+  oxh::launch(conv2d_weight_partial_kernel,
+              dim3(grid_for(static_cast<uint64_t>(weights) * chunks)), dim3(256), 0, s, g,
+              weights, oxh::make_fastdiv(weights), chunks, gradient, input, partial);
   st = oxh::launched(name);
   if (st != OXH_OK) return st;
   oxh::launch(sum_chunks_kernel, dim3(grid_for(weights)), dim3(256), 0, s, weights, chunks,
@@ -396,17 +710,18 @@ oxh_status oxh_conv2d_bias_backward(oxh_stream stream, const oxh_conv2d_shape *s
   OXH_REQUIRE(workspace != nullptr &&
                   workspace_bytes >= static_cast<uint64_t>(g.out_c) * chunks * 4,
               OXH_INVALID_SHAPE,
-              std::string(name) + ": workspace too small (oxh_conv2d_weight_backward_workspace_size)");
+              std::string(name) +
+                  ": workspace too small (oxh_conv2d_weight_backward_workspace_size)");
   float *partial = static_cast<float *>(workspace);
   hipStream_t s = oxh::as_stream(stream);
   oxh::launch(conv2d_bias_partial_kernel,
-              dim3(grid_for(static_cast<uint64_t>(g.out_c) * chunks)), dim3(256), 0, s, g.batch,
-              g.out_c, g.oh * g.ow, chunks, gradient, partial);
+              dim3(grid_for(static_cast<uint64_t>(g.out_c) * chunks)), dim3(256), 0, s,
+              g.batch, g.out_c, oxh::make_fastdiv(g.out_c), g.oh * g.ow, chunks, gradient,
+              partial);
   st = oxh::launched(name);
   if (st != OXH_OK) return st;
-  oxh::launch(sum_chunks_kernel, dim3(grid_for(g.out_c)), dim3(256), 0, s,
-              static_cast<uint64_t>(g.out_c), chunks, static_cast<const float *>(partial),
-              bias_gradient);
+  oxh::launch(sum_chunks_kernel, dim3(grid_for(g.out_c)), dim3(256), 0, s, g.out_c, chunks,
+              static_cast<const float *>(partial), bias_gradient);
   return oxh::launched(name);
 }
 
@@ -419,7 +734,7 @@ oxh_status oxh_avg_pool2d_forward(oxh_stream stream, const oxh_pool2d_shape *sha
   OXH_REQUIRE(input && output, OXH_INVALID_SHAPE, std::string(name) + ": null pointer");
   const uint64_t out_n = static_cast<uint64_t>(g.batch) * g.channels * g.oh * g.ow;
   oxh::launch(avg_pool2d_forward_kernel, dim3(grid_for(out_n)), dim3(256), 0,
-              oxh::as_stream(stream), g, input, output);
+              oxh::as_stream(stream), g, static_cast<uint32_t>(out_n), input, output);
   return oxh::launched(name);
 }
 
@@ -433,7 +748,7 @@ oxh_status oxh_avg_pool2d_backward(oxh_stream stream, const oxh_pool2d_shape *sh
               std::string(name) + ": null pointer");
   const uint64_t in_n = static_cast<uint64_t>(g.batch) * g.channels * g.h * g.w;
   oxh::launch(avg_pool2d_backward_kernel, dim3(grid_for(in_n)), dim3(256), 0,
-              oxh::as_stream(stream), g, gradient, input_gradient);
+              oxh::as_stream(stream), g, static_cast<uint32_t>(in_n), gradient, input_gradient);
   return oxh::launched(name);
 }
 

@@ -24,6 +24,14 @@ CASES = [
     (3, 12, 6, 5, 8, 3, 1, 4),
     (5, 20, 1, 1, 30, 1, 1, 1),
     (128, 960, 1, 1, 1280, 1, 1, 1),   # config 5's largest layer
+    # pointwise (1x1, stride 1) product path: k over several 128-slabs, partial 32-tiles,
+    # the weight gradient split over (n, p) chunks, plane 1 and plane > 1
+    (3, 300, 3, 3, 40, 1, 1, 1),
+    (2, 40, 5, 5, 300, 1, 1, 1),
+    (64, 16, 8, 8, 24, 1, 1, 1),
+    (1, 7, 1, 1, 3, 1, 1, 1),
+    (128, 1280, 1, 1, 10, 1, 1, 1),    # config 5's classifier
+    (2, 6, 7, 7, 4, 1, 2, 1),          # 1x1 with stride 2: direct path
 ]
 
 
