@@ -12,10 +12,11 @@
 // path's scatter loop adds them (oy ascending is ky descending); the pooling kernels follow the
 // window order.  These are the CPU path's exact fp32 operation sequences (-ffp-contract=off),
 // so the results are bit-identical.  Weight and bias gradients reduce over batch * oh * ow
-// terms; one thread per weight element would serialize thousands of dependent adds, so they are
-// split into chunks of that range (each chunk in the CPU order) whose partial sums a second
-// launch adds in chunk order: deterministic, within fp32 rounding of the CPU's single running
-// sum.
+// terms; one thread per weight element would serialize thousands of dependent adds, so the
+// weight gradient splits that range into chunks (each in the CPU order) whose partial sums a
+// second launch adds in chunk order, and the bias gradient gives each channel one wave whose
+// lane sums a fixed butterfly combines: deterministic, within fp32 rounding of the CPU's single
+// running sum.
 //
 // Kernels (gfx950).  Index arithmetic is 32-bit with multiply-high division (tensors below 2^31
 // elements), and the valid kernel taps / output positions of each element are computed in
@@ -166,26 +167,29 @@ __global__ __launch_bounds__(256) void conv2d_weight_partial_kernel(
   }
 }
 
-// Bias gradient, phase 1: batch chunk c for output channel oc, terms in (n, oy, ox).
-__global__ __launch_bounds__(256) void conv2d_bias_partial_kernel(
-    uint32_t batch, uint32_t out_c, oxh::FastDiv out_c_div, uint32_t plane, uint32_t chunks,
-    const float *__restrict__ grad, float *__restrict__ partial) {
-  const uint32_t total = out_c * chunks;
-  const uint32_t per = (batch + chunks - 1) / chunks;
-  for (uint32_t t = blockIdx.x * 256 + threadIdx.x; t < total; t += gridDim.x * 256) {
-    const uint32_t chunk = fdiv(t, out_c_div), oc = t - chunk * out_c;
-    const uint32_t n0 = chunk * per, n1 = min(n0 + per, batch);
-    float acc = 0.0f;
-    for (uint32_t n = n0; n < n1; ++n) {
-      const float *gp = grad + (n * out_c + oc) * plane;
-      for (uint32_t i = 0; i < plane; ++i) acc += gp[i];
-    }
-    partial[t] = acc;
+// Bias gradient: one wave per output channel.  Lane l adds the channel's terms l, l + 64, ...
+// of the (n, oy, ox) order in fp32; a fixed xor butterfly combines the 64 lane sums
+// (deterministic; within fp32 rounding of the CPU's single running sum).
+__global__ __launch_bounds__(256) void conv2d_bias_kernel(uint32_t batch, uint32_t out_c,
+                                                          uint32_t plane, oxh::FastDiv plane_div,
+                                                          const float *__restrict__ grad,
+                                                          float *__restrict__ out) {
+  const uint32_t oc = blockIdx.x * 4 + threadIdx.x / 64;
+  if (oc >= out_c) return;  // wave-uniform
+  const uint32_t lane = threadIdx.x % 64, total = batch * plane;
+  float acc = 0.0f;
+#pragma unroll 4
+  for (uint32_t j = lane; j < total; j += 64) {
+    const uint32_t n = fdiv(j, plane_div), p = j - n * plane;
+    acc += grad[(n * out_c + oc) * plane + p];
   }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  if (lane == 0) out[oc] = acc;
 }
 
-// Phase 2 of both: out[e] = sum over chunks of partial[chunk][e], in chunk order (loads issued
-// in groups of 8 ahead of the serial adds).
+// Weight gradient, phase 2: out[e] = sum over chunks of partial[chunk][e], in chunk order
+// (loads issued in groups of 8 ahead of the serial adds).
 __global__ __launch_bounds__(256) void sum_chunks_kernel(uint32_t count, uint32_t chunks,
                                                          const float *__restrict__ partial,
                                                          float *__restrict__ out) {
@@ -234,7 +238,7 @@ struct ProductArgs {
   uint32_t M, N, K, k_chunk;
 };
 
-constexpr int kTile = 32, kMicro = 2, kSlab = 128;
+constexpr int kTile = 32, kMicro = 2, kSlab = 128, kUnrollK = 8;
 constexpr int kTileLoads = kTile * kSlab / 256;  // per thread, per operand, per slab
 
 __device__ __forceinline__ void tile_coords(bool k_fast, int e, int &r, int &kk) {
@@ -306,7 +310,26 @@ __global__ __launch_bounds__(256) void pointwise_product_kernel(ProductArgs g) {
       fetch_slab(g.a, m0, g.M, k1, kc1, va);
       fetch_slab(g.b, n0, g.N, k1, kc1, vb);
     }
-    for (uint32_t kk = 0; kk < kc; ++kk) {
+    // groups of kUnrollK steps: the LDS reads of a group are issued together, then each
+    // accumulator takes its products in ascending k
+    uint32_t kk = 0;
+    for (; kk + kUnrollK <= kc; kk += kUnrollK) {
+      float av[kUnrollK][kMicro], bv[kUnrollK][kMicro];
+#pragma unroll
+      for (int u = 0; u < kUnrollK; ++u) {
+#pragma unroll
+        for (int i = 0; i < kMicro; ++i) av[u][i] = as[kk + u][ty * kMicro + i];
+#pragma unroll
+        for (int j = 0; j < kMicro; ++j) bv[u][j] = bs[kk + u][tx * kMicro + j];
+      }
+#pragma unroll
+      for (int u = 0; u < kUnrollK; ++u)
+#pragma unroll
+        for (int i = 0; i < kMicro; ++i)
+#pragma unroll
+          for (int j = 0; j < kMicro; ++j) acc[i][j] += av[u][i] * bv[u][j];
+    }
+    for (; kk < kc; ++kk) {
       float av[kMicro], bv[kMicro];
 #pragma unroll
       for (int i = 0; i < kMicro; ++i) av[i] = as[kk][ty * kMicro + i];
@@ -494,24 +517,16 @@ oxh_status launch_product(const char *name, hipStream_t s, const ProductArgs &a,
   return oxh::launched(name);
 }
 
-// Batch chunks for the direct weight / bias reductions: enough threads to fill the GPU, at
+// Batch chunks for the direct weight reduction: about 2^20 threads (short serial chains), at
 // most one chunk per batch element.
 uint32_t weight_chunks(const ConvGeom &g) {
   const uint64_t weights = weight_elems(g);
-  uint64_t c = (65536 + weights - 1) / weights;
+  uint64_t c = ((1ull << 20) + weights - 1) / weights;
   if (c > g.batch) c = g.batch;
   while (c > 1 && weights * c >= kMaxElems) --c;
   if (c < 1) c = 1;
   return static_cast<uint32_t>(c);
 }
-uint32_t bias_chunks(uint64_t batch, uint64_t out_c) {
-  uint64_t c = (16384 + out_c - 1) / out_c;
-  if (c > batch) c = batch;
-  while (c > 1 && out_c * c >= kMaxElems) --c;
-  if (c < 1) c = 1;
-  return static_cast<uint32_t>(c);
-}
-
 uint64_t weight_partial_bytes(const ConvGeom &g) {
   if (pointwise(g)) {
     const KSplit k = product_split(g);
@@ -640,10 +655,7 @@ oxh_status oxh_conv2d_weight_backward_workspace_size(const oxh_conv2d_shape *sha
   oxh_status st = make_conv_geom("oxh_conv2d_weight_backward_workspace_size", shape, g);
   if (st != OXH_OK) return st;
   OXH_REQUIRE(bytes != nullptr, OXH_INVALID_SHAPE, "bytes is null");
-  const uint64_t wb = weight_partial_bytes(g);
-  const uint64_t bb = static_cast<uint64_t>(g.out_c) * bias_chunks(g.batch, g.out_c) * 4;
-  const uint64_t need = wb > bb ? wb : bb;
-  *bytes = (need + 255) / 256 * 256;
+  *bytes = (weight_partial_bytes(g) + 255) / 256 * 256;
   return oxh::ok();
 }
 
@@ -706,22 +718,11 @@ oxh_status oxh_conv2d_bias_backward(oxh_stream stream, const oxh_conv2d_shape *s
   oxh_status st = make_conv_geom(name, shape, g);
   if (st != OXH_OK) return st;
   OXH_REQUIRE(gradient && bias_gradient, OXH_INVALID_SHAPE, std::string(name) + ": null pointer");
-  const uint32_t chunks = bias_chunks(g.batch, g.out_c);
-  OXH_REQUIRE(workspace != nullptr &&
-                  workspace_bytes >= static_cast<uint64_t>(g.out_c) * chunks * 4,
-              OXH_INVALID_SHAPE,
-              std::string(name) +
-                  ": workspace too small (oxh_conv2d_weight_backward_workspace_size)");
-  float *partial = static_cast<float *>(workspace);
-  hipStream_t s = oxh::as_stream(stream);
-  oxh::launch(conv2d_bias_partial_kernel,
-              dim3(grid_for(static_cast<uint64_t>(g.out_c) * chunks)), dim3(256), 0, s,
-              g.batch, g.out_c, oxh::make_fastdiv(g.out_c), g.oh * g.ow, chunks, gradient,
-              partial);
-  st = oxh::launched(name);
-  if (st != OXH_OK) return st;
-  oxh::launch(sum_chunks_kernel, dim3(grid_for(g.out_c)), dim3(256), 0, s, g.out_c, chunks,
-              static_cast<const float *>(partial), bias_gradient);
+  (void)workspace;  // the single-pass reduction needs none
+  (void)workspace_bytes;
+  oxh::launch(conv2d_bias_kernel, dim3((g.out_c + 3) / 4), dim3(256), 0, oxh::as_stream(stream),
+              g.batch, g.out_c, g.oh * g.ow, oxh::make_fastdiv(g.oh * g.ow), gradient,
+              bias_gradient);
   return oxh::launched(name);
 }
 
