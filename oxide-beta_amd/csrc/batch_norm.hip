@@ -217,12 +217,18 @@ __global__ __launch_bounds__(kRedBlock) void bn_reduce_x_kernel(Geometry g,
   if (threadIdx.x == 0) partial[static_cast<uint64_t>(c) * g.slices + s] = make_double2(sum, sq);
 }
 
+// ReLU backward applied to the incoming gradient (kernel_module.rs:501-508): g where the ReLU's
+// output r (hence its input) is positive, else 0.
+__device__ __forceinline__ float relu_masked(float g, float r) { return r > 0.0f ? g : 0.0f; }
+
 // Backward partials: (sum g, sum g * x_hat) with x_hat = (x - mean) * inv in fp32 and the
-// product g * x_hat rounded to fp32 as the CPU path forms it (autograd.rs:353-362).
+// product g * x_hat rounded to fp32 as the CPU path forms it (autograd.rs:353-362).  With
+// Relu, g is first masked by the following ReLU's output (relu_out).
+template <bool Relu>
 __global__ __launch_bounds__(kRedBlock) void bn_reduce_gx_kernel(
-    Geometry g, const float *__restrict__ grad, const float *__restrict__ x,
-    const float *__restrict__ mean, const float *__restrict__ inverse_std,
-    double2 *__restrict__ partial) {
+    Geometry g, const float *__restrict__ grad, const float *__restrict__ relu_out,
+    const float *__restrict__ x, const float *__restrict__ mean,
+    const float *__restrict__ inverse_std, double2 *__restrict__ partial) {
   __shared__ double lds[2][kRedWaves];
   const uint32_t s = blockIdx.x, c = blockIdx.y;
   const float mu = mean[c], inv = inverse_std[c];
@@ -232,8 +238,18 @@ __global__ __launch_bounds__(kRedBlock) void bn_reduce_gx_kernel(
   if (g.vec) {
     const float4 *x4 = reinterpret_cast<const float4 *>(x);
     const float4 *g4 = reinterpret_cast<const float4 *>(grad);
+    const float4 *r4 = reinterpret_cast<const float4 *>(relu_out);
     const uint32_t e4 = static_cast<uint32_t>(end / 4);
     uint32_t j = static_cast<uint32_t>(begin / 4) + threadIdx.x;
+    auto load_g = [&](uint64_t idx) {
+      float4 v = g4[idx];
+      if constexpr (Relu) {
+        const float4 r = r4[idx];
+        v = make_float4(relu_masked(v.x, r.x), relu_masked(v.y, r.y), relu_masked(v.z, r.z),
+                        relu_masked(v.w, r.w));
+      }
+      return v;
+    };
     auto add4 = [&](const float4 &xv, const float4 &gv) {
       const float n0 = (xv.x - mu) * inv, n1 = (xv.y - mu) * inv;
       const float n2 = (xv.z - mu) * inv, n3 = (xv.w - mu) * inv;
@@ -248,19 +264,20 @@ __global__ __launch_bounds__(kRedBlock) void bn_reduce_gx_kernel(
       for (int u = 0; u < kRedUnroll; ++u) {
         const uint64_t idx = nchw_index(g, c, j + u * kRedBlock);
         xv[u] = x4[idx];
-        gv[u] = g4[idx];
+        gv[u] = load_g(idx);
       }
 #pragma unroll
       for (int u = 0; u < kRedUnroll; ++u) add4(xv[u], gv[u]);
     }
     for (; j < e4; j += kRedBlock) {
       const uint64_t idx = nchw_index(g, c, j);
-      add4(x4[idx], g4[idx]);
+      add4(x4[idx], load_g(idx));
     }
   } else {
     for (uint64_t j = begin + threadIdx.x; j < end; j += kRedBlock) {
       const uint64_t idx = nchw_index(g, c, static_cast<uint32_t>(j));
-      const float gv = grad[idx];
+      float gv = grad[idx];
+      if constexpr (Relu) gv = relu_masked(gv, relu_out[idx]);
       const float nv = (x[idx] - mu) * inv;
       sg += static_cast<double>(gv);
       sgx += static_cast<double>(gv * nv);
@@ -382,6 +399,7 @@ struct ApplyPhase {
     uint64_t samples;
     StatsOut out;  // written by the designated block when partial != null
     float *y;
+    bool relu;     // y = relu(batch norm) (ConvNormAct, nn.rs:376-385)
   };
   struct Pre {
     double2 part;
@@ -426,15 +444,18 @@ struct ApplyPhase {
   }
   __device__ static const float *input(const Args &a, int) { return a.x; }
   __device__ static float *output(const Args &a) { return a.y; }
-  __device__ static float element(const Args &, const float (&cv)[V], const float (&in)[NI]) {
-    // evaluation.rs:590-595
-    return (in[0] - cv[0]) * cv[1] * cv[2] + cv[3];
+  __device__ static float element(const Args &a, const float (&cv)[V], const float (&in)[NI]) {
+    // evaluation.rs:590-595, then kernel_module.rs:26-34 (x > 0 ? x : 0)
+    const float y = (in[0] - cv[0]) * cv[1] * cv[2] + cv[3];
+    return a.relu ? (y > 0.0f ? y : 0.0f) : y;
   }
 };
 
 // Training input backward.  Channel values: mean, inv, (w * inv) / M, sum g, sum g * x_hat.
-struct DxTrainPhase {
-  static constexpr int V = 5, NI = 2, kNtStoreBit = 2;  // in[0] = g, in[1] = x
+// With Relu the incoming gradient is masked by the following ReLU's output (in[2]).
+template <bool Relu>
+struct DxTrainPhaseT {
+  static constexpr int V = 5, NI = Relu ? 3 : 2, kNtStoreBit = 2;  // in: g, x, relu output
   struct Args {
     const float *grad, *x, *weight, *mean, *inverse_std;
     const float *weight_gradient, *bias_gradient;  // used when partial == null
@@ -443,6 +464,7 @@ struct DxTrainPhase {
     float samples;                                   // M in fp32 (autograd.rs:344-345)
     float *out_weight_gradient, *out_bias_gradient;  // written when partial != null
     float *dx;
+    const float *relu_out;                           // read when Relu
   };
   struct Pre {
     double2 part;
@@ -488,14 +510,19 @@ struct DxTrainPhase {
     cv[3] = a.bias_gradient[c];
     cv[4] = a.weight_gradient[c];
   }
-  __device__ static const float *input(const Args &a, int i) { return i == 0 ? a.grad : a.x; }
+  __device__ static const float *input(const Args &a, int i) {
+    return i == 0 ? a.grad : (i == 1 ? a.x : a.relu_out);
+  }
   __device__ static float *output(const Args &a) { return a.dx; }
   __device__ static float element(const Args &a, const float (&cv)[V], const float (&in)[NI]) {
     // autograd.rs:367-373
+    float g = in[0];
+    if constexpr (Relu) g = relu_masked(g, in[NI - 1]);
     const float normalized = (in[1] - cv[0]) * cv[1];
-    return cv[2] * (a.samples * in[0] - cv[3] - normalized * cv[4]);
+    return cv[2] * (a.samples * g - cv[3] - normalized * cv[4]);
   }
 };
+using DxTrainPhase = DxTrainPhaseT<false>;
 
 // Eval input backward: dx = (g * w) * inv (autograd.rs:374-378).
 struct DxEvalPhase {
@@ -666,6 +693,92 @@ __global__ __launch_bounds__(kMapBlock) void bn_flat_map_kernel(FlatMap m, typen
   }
 }
 
+// Small planes with few values per channel: one block per channel performs the whole
+// operation -- the channel sums, their finalization, and the elementwise pass (whose second
+// read of the channel is served by L2) -- in a single launch.
+constexpr uint64_t kChannelMaxSamples = 65536;
+
+struct ChannelGeom {
+  uint32_t channels, spatial, samples;  // samples = batch * spatial
+  oxh::FastDiv spatial_div;
+};
+
+__device__ __forceinline__ uint32_t channel_index(const ChannelGeom &g, uint32_t c, uint32_t j) {
+  const uint32_t n = oxh::fast_div(j, g.spatial_div);
+  return (n * g.channels + c) * g.spatial + (j - n * g.spatial);
+}
+
+template <bool Relu>
+__global__ __launch_bounds__(kRedBlock) void bn_channel_forward_kernel(
+    ChannelGeom g, const float *__restrict__ x, const float *__restrict__ weight,
+    const float *__restrict__ bias, StatsOut out, float *__restrict__ y) {
+  __shared__ double lds[2][kRedWaves];
+  __shared__ float stats[2];
+  const uint32_t c = blockIdx.x;
+  const float shift = x[static_cast<uint64_t>(c) * g.spatial];  // x[0, c, 0]
+  const double k = static_cast<double>(shift);
+  double sum = 0.0, sq = 0.0;
+  for (uint32_t j = threadIdx.x; j < g.samples; j += kRedBlock) {
+    const double d = static_cast<double>(x[channel_index(g, c, j)]) - k;
+    sum += d;
+    sq += d * d;
+  }
+  block_sum2(sum, sq, lds);
+  if (threadIdx.x == 0) {
+    const Moments r = forward_moments(make_double2(sum, sq), shift, g.samples, out.epsilon);
+    write_forward_outputs(out, c, r);
+    stats[0] = r.mean;
+    stats[1] = r.inv;
+  }
+  __syncthreads();
+  const float mu = stats[0], inv = stats[1], w = weight[c], b = bias[c];
+  for (uint32_t j = threadIdx.x; j < g.samples; j += kRedBlock) {
+    const uint32_t idx = channel_index(g, c, j);
+    float v = (x[idx] - mu) * inv * w + b;  // evaluation.rs:590-595
+    if constexpr (Relu) v = v > 0.0f ? v : 0.0f;
+    y[idx] = v;
+  }
+}
+
+template <bool Relu>
+__global__ __launch_bounds__(kRedBlock) void bn_channel_backward_kernel(
+    ChannelGeom g, const float *__restrict__ grad, const float *__restrict__ relu_out,
+    const float *__restrict__ x, const float *__restrict__ weight, const float *__restrict__ mean,
+    const float *__restrict__ inverse_std, float *__restrict__ dx, float *__restrict__ dweight,
+    float *__restrict__ dbias) {
+  __shared__ double lds[2][kRedWaves];
+  __shared__ float sums[2];
+  const uint32_t c = blockIdx.x;
+  const float mu = mean[c], inv = inverse_std[c];
+  double sg = 0.0, sgx = 0.0;
+  for (uint32_t j = threadIdx.x; j < g.samples; j += kRedBlock) {
+    const uint32_t idx = channel_index(g, c, j);
+    float gv = grad[idx];
+    if constexpr (Relu) gv = relu_masked(gv, relu_out[idx]);
+    const float nv = (x[idx] - mu) * inv;
+    sg += static_cast<double>(gv);
+    sgx += static_cast<double>(gv * nv);
+  }
+  block_sum2(sg, sgx, lds);
+  if (threadIdx.x == 0) {
+    sums[0] = static_cast<float>(sg);
+    sums[1] = static_cast<float>(sgx);
+    dbias[c] = sums[0];
+    dweight[c] = sums[1];
+  }
+  __syncthreads();
+  // autograd.rs:344-373: ((w * inv) / M) * ((M * g - sum_g) - x_hat * sum_g_xhat)
+  const float samples = static_cast<float>(g.samples);
+  const float coef = weight[c] * inv / samples, sgf = sums[0], sgxf = sums[1];
+  for (uint32_t j = threadIdx.x; j < g.samples; j += kRedBlock) {
+    const uint32_t idx = channel_index(g, c, j);
+    float gv = grad[idx];
+    if constexpr (Relu) gv = relu_masked(gv, relu_out[idx]);
+    const float normalized = (x[idx] - mu) * inv;
+    dx[idx] = coef * (samples * gv - sgf - normalized * sgxf);
+  }
+}
+
 __global__ void bn_update_running_kernel(uint32_t channels, float momentum,
                                          const float *batch_mean, const float *batch_variance,
                                          const float *old_mean, const float *old_variance,
@@ -743,25 +856,33 @@ oxh_status launch_reduce_x(const char *name, oxh_stream stream, uint64_t batch,
 
 oxh_status launch_reduce_gx(const char *name, oxh_stream stream, uint64_t batch,
                             uint64_t channels, uint64_t spatial, const float *gradient,
-                            const float *input, const float *mean, const float *inverse_std,
-                            void *workspace, uint64_t workspace_bytes, Geometry *geometry) {
+                            const float *relu_out, const float *input, const float *mean,
+                            const float *inverse_std, void *workspace, uint64_t workspace_bytes,
+                            Geometry *geometry) {
   oxh_status st = check_shape(name, batch, channels, spatial);
   if (st != OXH_OK) return st;
   OXH_REQUIRE(gradient && input && mean && inverse_std, OXH_INVALID_SHAPE,
               std::string(name) + ": null pointer");
-  const Geometry g = make_geometry(batch, channels, spatial,
-                                   oxh::aligned16(input) && oxh::aligned16(gradient));
+  const Geometry g = make_geometry(
+      batch, channels, spatial,
+      oxh::aligned16(input) && oxh::aligned16(gradient) && oxh::aligned16(relu_out));
   st = check_workspace(name, g, workspace, workspace_bytes);
   if (st != OXH_OK) return st;
-  oxh::launch(bn_reduce_gx_kernel, dim3(g.slices, g.channels), dim3(kRedBlock), 0,
-                     oxh::as_stream(stream), g, gradient, input, mean, inverse_std,
-                     static_cast<double2 *>(workspace));
+  const dim3 grid(g.slices, g.channels);
+  auto *partial = static_cast<double2 *>(workspace);
+  if (relu_out)
+    oxh::launch(bn_reduce_gx_kernel<true>, grid, dim3(kRedBlock), 0, oxh::as_stream(stream), g,
+                gradient, relu_out, input, mean, inverse_std, partial);
+  else
+    oxh::launch(bn_reduce_gx_kernel<false>, grid, dim3(kRedBlock), 0, oxh::as_stream(stream), g,
+                gradient, relu_out, input, mean, inverse_std, partial);
   if (geometry) *geometry = g;
   return oxh::launched(name);
 }
 
 bool a_is_direct(const ApplyPhase::Args &a) { return a.partial == nullptr; }
-bool a_is_direct(const DxTrainPhase::Args &a) { return a.partial == nullptr; }
+bool a_is_direct(const DxTrainPhaseT<false>::Args &a) { return a.partial == nullptr; }
+bool a_is_direct(const DxTrainPhaseT<true>::Args &a) { return a.partial == nullptr; }
 bool a_is_direct(const DxEvalPhase::Args &) { return true; }
 
 // The flat pass serves planes smaller than kFlatSpatial values (tensors under 2^31 elements).
@@ -796,6 +917,189 @@ oxh_status launch_map(const char *name, oxh_stream stream, uint64_t batch, uint6
 }
 
 uint32_t channel_grid(uint64_t channels) { return static_cast<uint32_t>((channels + 255) / 256); }
+
+bool use_channel(uint64_t batch, uint64_t channels, uint64_t spatial) {
+  return spatial < kFlatSpatial && batch * spatial <= kChannelMaxSamples &&
+         batch * channels * spatial < (1ull << 31);
+}
+
+ChannelGeom make_channel_geom(uint64_t batch, uint64_t channels, uint64_t spatial) {
+  ChannelGeom g{};
+  g.channels = static_cast<uint32_t>(channels);
+  g.spatial = static_cast<uint32_t>(spatial);
+  g.samples = static_cast<uint32_t>(batch * spatial);
+  g.spatial_div = oxh::make_fastdiv(g.spatial);
+  return g;
+}
+
+// forward_apply after forward_reduce; relu: y = relu(batch norm).
+oxh_status forward_apply_impl(const char *name, oxh_stream stream, uint64_t batch,
+                              uint64_t channels, uint64_t spatial, float momentum,
+                              float epsilon, const float *input, const float *weight,
+                              const float *bias, float *running_mean, float *running_variance,
+                              float *saved_mean, float *saved_inverse_std, float *output,
+                              const void *workspace, uint64_t workspace_bytes, bool relu) {
+  OXH_REQUIRE(std::isfinite(momentum) && std::isfinite(epsilon) && epsilon >= 0.0f,
+              OXH_INVALID_SHAPE, std::string(name) + ": bad momentum or epsilon");
+  oxh_status st = check_shape(name, batch, channels, spatial);
+  if (st != OXH_OK) return st;
+  OXH_REQUIRE(batch * spatial > 1, OXH_EXECUTION,
+              "BatchNorm training requires more than one value per channel");
+  OXH_REQUIRE(input && weight && bias && running_mean && running_variance && saved_mean &&
+                  saved_inverse_std && output,
+              OXH_INVALID_SHAPE, std::string(name) + ": null pointer");
+  const Geometry g = make_geometry(batch, channels, spatial, false);
+  st = check_workspace(name, g, workspace, workspace_bytes);
+  if (st != OXH_OK) return st;
+  const uint64_t bytes = batch * channels * spatial * 4;
+  st = no_overlap(name, output, bytes, {input}, bytes);
+  if (st != OXH_OK) return st;
+  const StatsOut stats{saved_mean, saved_inverse_std, nullptr, running_mean, running_variance,
+                       momentum, epsilon};
+  const bool aligned = oxh::aligned16(input) && oxh::aligned16(output);
+  if (use_flat(batch, channels, spatial)) {
+    oxh::launch(bn_finalize_forward_kernel, dim3((channels + 3) / 4), dim3(256), 0,
+                oxh::as_stream(stream), g, input, static_cast<const double2 *>(workspace),
+                stats);
+    st = oxh::launched(name);
+    if (st != OXH_OK) return st;
+    ApplyPhase::Args a{input, weight, bias, saved_mean, saved_inverse_std, nullptr, 0, 0,
+                       StatsOut{}, output, relu};
+    return launch_map<ApplyPhase>(name, stream, batch, channels, spatial, aligned, a);
+  }
+  ApplyPhase::Args a{input,    weight,    bias,  nullptr, nullptr,
+                     static_cast<const double2 *>(workspace), g.slices, g.samples, stats, output,
+                     relu};
+  return launch_map<ApplyPhase>(name, stream, batch, channels, spatial, aligned, a);
+}
+
+// backward_input after backward_reduce; relu_out (nullable): the following ReLU's output,
+// whose sign masks the incoming gradient.
+oxh_status backward_input_impl(const char *name, oxh_stream stream, uint64_t batch,
+                               uint64_t channels, uint64_t spatial, const float *gradient,
+                               const float *relu_out, const float *input, const float *weight,
+                               const float *saved_mean, const float *saved_inverse_std,
+                               float *input_gradient, float *weight_gradient,
+                               float *bias_gradient, const void *workspace,
+                               uint64_t workspace_bytes) {
+  oxh_status st = check_shape(name, batch, channels, spatial);
+  if (st != OXH_OK) return st;
+  OXH_REQUIRE(gradient && input && weight && saved_mean && saved_inverse_std &&
+                  input_gradient && weight_gradient && bias_gradient,
+              OXH_INVALID_SHAPE, std::string(name) + ": null pointer");
+  const Geometry g = make_geometry(batch, channels, spatial, false);
+  st = check_workspace(name, g, workspace, workspace_bytes);
+  if (st != OXH_OK) return st;
+  const uint64_t bytes = batch * channels * spatial * 4;
+  st = no_overlap(name, input_gradient, bytes, {input, gradient, relu_out}, bytes);
+  if (st != OXH_OK) return st;
+  const bool aligned = oxh::aligned16(gradient) && oxh::aligned16(input) &&
+                       oxh::aligned16(input_gradient) && oxh::aligned16(relu_out);
+  const float samples = static_cast<float>(batch * spatial);
+  const double2 *partial = static_cast<const double2 *>(workspace);
+  const bool flat = use_flat(batch, channels, spatial);
+  if (flat) {
+    oxh::launch(bn_finalize_affine_kernel, dim3((channels + 3) / 4), dim3(256), 0,
+                oxh::as_stream(stream), g, partial, weight_gradient, bias_gradient);
+    st = oxh::launched(name);
+    if (st != OXH_OK) return st;
+  }
+  const float *wg_in = flat ? weight_gradient : nullptr;
+  const float *bg_in = flat ? bias_gradient : nullptr;
+  const double2 *part = flat ? nullptr : partial;
+  float *wg_out = flat ? nullptr : weight_gradient;
+  float *bg_out = flat ? nullptr : bias_gradient;
+  if (relu_out) {
+    DxTrainPhaseT<true>::Args a{gradient, input,  weight, saved_mean, saved_inverse_std,
+                                wg_in,    bg_in,  part,   g.slices,   samples,
+                                wg_out,   bg_out, input_gradient, relu_out};
+    return launch_map<DxTrainPhaseT<true>>(name, stream, batch, channels, spatial, aligned, a);
+  }
+  DxTrainPhase::Args a{gradient, input,  weight, saved_mean, saved_inverse_std,
+                       wg_in,    bg_in,  part,   g.slices,   samples,
+                       wg_out,   bg_out, input_gradient, nullptr};
+  return launch_map<DxTrainPhase>(name, stream, batch, channels, spatial, aligned, a);
+}
+
+oxh_status forward_train_impl(const char *name, oxh_stream stream, uint64_t batch,
+                              uint64_t channels, uint64_t spatial, float momentum,
+                              float epsilon, const float *input, const float *weight,
+                              const float *bias, float *running_mean, float *running_variance,
+                              float *saved_mean, float *saved_inverse_std, float *output,
+                              void *workspace, uint64_t workspace_bytes, bool relu) {
+  if (!use_channel(batch, channels, spatial)) {
+    oxh_status st = launch_reduce_x(name, stream, batch, channels, spatial, input, workspace,
+                                    workspace_bytes, nullptr);
+    if (st != OXH_OK) return st;
+    return forward_apply_impl(name, stream, batch, channels, spatial, momentum, epsilon, input,
+                              weight, bias, running_mean, running_variance, saved_mean,
+                              saved_inverse_std, output, workspace, workspace_bytes, relu);
+  }
+  OXH_REQUIRE(std::isfinite(momentum) && std::isfinite(epsilon) && epsilon >= 0.0f,
+              OXH_INVALID_SHAPE, std::string(name) + ": bad momentum or epsilon");
+  oxh_status st = check_shape(name, batch, channels, spatial);
+  if (st != OXH_OK) return st;
+  OXH_REQUIRE(batch * spatial > 1, OXH_EXECUTION,
+              "BatchNorm training requires more than one value per channel");
+  OXH_REQUIRE(input && weight && bias && running_mean && running_variance && saved_mean &&
+                  saved_inverse_std && output,
+              OXH_INVALID_SHAPE, std::string(name) + ": null pointer");
+  st = check_workspace(name, make_geometry(batch, channels, spatial, false), workspace,
+                       workspace_bytes);
+  if (st != OXH_OK) return st;
+  const uint64_t bytes = batch * channels * spatial * 4;
+  st = no_overlap(name, output, bytes, {input}, bytes);
+  if (st != OXH_OK) return st;
+  const StatsOut stats{saved_mean, saved_inverse_std, nullptr, running_mean, running_variance,
+                       momentum, epsilon};
+  const ChannelGeom cg = make_channel_geom(batch, channels, spatial);
+  if (relu)
+    oxh::launch(bn_channel_forward_kernel<true>, dim3(cg.channels), dim3(kRedBlock), 0,
+                oxh::as_stream(stream), cg, input, weight, bias, stats, output);
+  else
+    oxh::launch(bn_channel_forward_kernel<false>, dim3(cg.channels), dim3(kRedBlock), 0,
+                oxh::as_stream(stream), cg, input, weight, bias, stats, output);
+  return oxh::launched(name);
+}
+
+oxh_status backward_train_impl(const char *name, oxh_stream stream, uint64_t batch,
+                               uint64_t channels, uint64_t spatial, const float *gradient,
+                               const float *relu_out, const float *input, const float *weight,
+                               const float *saved_mean, const float *saved_inverse_std,
+                               float *input_gradient, float *weight_gradient,
+                               float *bias_gradient, void *workspace,
+                               uint64_t workspace_bytes) {
+  if (!use_channel(batch, channels, spatial)) {
+    oxh_status st = launch_reduce_gx(name, stream, batch, channels, spatial, gradient, relu_out,
+                                     input, saved_mean, saved_inverse_std, workspace,
+                                     workspace_bytes, nullptr);
+    if (st != OXH_OK) return st;
+    return backward_input_impl(name, stream, batch, channels, spatial, gradient, relu_out, input,
+                               weight, saved_mean, saved_inverse_std, input_gradient,
+                               weight_gradient, bias_gradient, workspace, workspace_bytes);
+  }
+  oxh_status st = check_shape(name, batch, channels, spatial);
+  if (st != OXH_OK) return st;
+  OXH_REQUIRE(gradient && input && weight && saved_mean && saved_inverse_std &&
+                  input_gradient && weight_gradient && bias_gradient,
+              OXH_INVALID_SHAPE, std::string(name) + ": null pointer");
+  st = check_workspace(name, make_geometry(batch, channels, spatial, false), workspace,
+                       workspace_bytes);
+  if (st != OXH_OK) return st;
+  const uint64_t bytes = batch * channels * spatial * 4;
+  st = no_overlap(name, input_gradient, bytes, {input, gradient, relu_out}, bytes);
+  if (st != OXH_OK) return st;
+  const ChannelGeom cg = make_channel_geom(batch, channels, spatial);
+  if (relu_out)
+    oxh::launch(bn_channel_backward_kernel<true>, dim3(cg.channels), dim3(kRedBlock), 0,
+                oxh::as_stream(stream), cg, gradient, relu_out, input, weight, saved_mean,
+                saved_inverse_std, input_gradient, weight_gradient, bias_gradient);
+  else
+    oxh::launch(bn_channel_backward_kernel<false>, dim3(cg.channels), dim3(kRedBlock), 0,
+                oxh::as_stream(stream), cg, gradient, relu_out, input, weight, saved_mean,
+                saved_inverse_std, input_gradient, weight_gradient, bias_gradient);
+  return oxh::launched(name);
+}
 
 }  // namespace
 
@@ -868,7 +1172,8 @@ oxh_status oxh_batch_norm_apply(oxh_stream stream, uint64_t batch, uint64_t chan
   const uint64_t bytes = batch * channels * spatial * 4;
   OXH_REQUIRE(input == output || !oxh::any_overlap(input, bytes, output, bytes),
               OXH_INVALID_SHAPE, std::string(name) + ": output partially overlaps the input");
-  ApplyPhase::Args a{input, weight, bias, mean, inverse_std, nullptr, 0, 0, StatsOut{}, output};
+  ApplyPhase::Args a{input,  weight, bias, mean, inverse_std, nullptr, 0, 0, StatsOut{}, output,
+                     false};
   return launch_map<ApplyPhase>(name, stream, batch, channels, spatial,
                                 oxh::aligned16(input) && oxh::aligned16(output), a);
 }
@@ -883,8 +1188,8 @@ oxh_status oxh_batch_norm_affine_backward(oxh_stream stream, uint64_t batch, uin
   OXH_REQUIRE(weight_gradient && bias_gradient, OXH_INVALID_SHAPE,
               std::string(name) + ": null output");
   Geometry g;
-  oxh_status st = launch_reduce_gx(name, stream, batch, channels, spatial, gradient, input, mean,
-                                   inverse_std, workspace, workspace_bytes, &g);
+  oxh_status st = launch_reduce_gx(name, stream, batch, channels, spatial, gradient, nullptr,
+                                   input, mean, inverse_std, workspace, workspace_bytes, &g);
   if (st != OXH_OK) return st;
   oxh::launch(bn_finalize_affine_kernel, dim3((channels + 3) / 4), dim3(256), 0,
                      oxh::as_stream(stream), g, static_cast<const double2 *>(workspace),
@@ -917,7 +1222,7 @@ oxh_status oxh_batch_norm_input_backward(oxh_stream stream, uint64_t batch, uint
   if (st != OXH_OK) return st;
   DxTrainPhase::Args a{gradient, input, weight, mean, inverse_std, weight_gradient,
                        bias_gradient, nullptr, 0, static_cast<float>(batch * spatial),
-                       nullptr, nullptr, output};
+                       nullptr, nullptr, output, nullptr};
   return launch_map<DxTrainPhase>(
       name, stream, batch, channels, spatial,
       oxh::aligned16(gradient) && oxh::aligned16(input) && oxh::aligned16(output), a);
@@ -937,38 +1242,10 @@ oxh_status oxh_batch_norm_forward_apply(oxh_stream stream, uint64_t batch, uint6
                                         float *running_variance, float *saved_mean,
                                         float *saved_inverse_std, float *output,
                                         const void *workspace, uint64_t workspace_bytes) {
-  const char *name = "oxh_batch_norm_forward_apply";
-  OXH_REQUIRE(std::isfinite(momentum) && std::isfinite(epsilon) && epsilon >= 0.0f,
-              OXH_INVALID_SHAPE, std::string(name) + ": bad momentum or epsilon");
-  oxh_status st = check_shape(name, batch, channels, spatial);
-  if (st != OXH_OK) return st;
-  OXH_REQUIRE(batch * spatial > 1, OXH_EXECUTION,
-              "BatchNorm training requires more than one value per channel");
-  OXH_REQUIRE(input && weight && bias && running_mean && running_variance && saved_mean &&
-                  saved_inverse_std && output,
-              OXH_INVALID_SHAPE, std::string(name) + ": null pointer");
-  const Geometry g = make_geometry(batch, channels, spatial, false);
-  st = check_workspace(name, g, workspace, workspace_bytes);
-  if (st != OXH_OK) return st;
-  const uint64_t bytes = batch * channels * spatial * 4;
-  st = no_overlap(name, output, bytes, {input}, bytes);
-  if (st != OXH_OK) return st;
-  const StatsOut stats{saved_mean, saved_inverse_std, nullptr, running_mean, running_variance,
-                       momentum, epsilon};
-  const bool aligned = oxh::aligned16(input) && oxh::aligned16(output);
-  if (use_flat(batch, channels, spatial)) {
-    oxh::launch(bn_finalize_forward_kernel, dim3((channels + 3) / 4), dim3(256), 0,
-                oxh::as_stream(stream), g, input, static_cast<const double2 *>(workspace),
-                stats);
-    st = oxh::launched(name);
-    if (st != OXH_OK) return st;
-    ApplyPhase::Args a{input, weight, bias, saved_mean, saved_inverse_std, nullptr, 0, 0,
-                       StatsOut{}, output};
-    return launch_map<ApplyPhase>(name, stream, batch, channels, spatial, aligned, a);
-  }
-  ApplyPhase::Args a{input, weight, bias, nullptr, nullptr,
-                     static_cast<const double2 *>(workspace), g.slices, g.samples, stats, output};
-  return launch_map<ApplyPhase>(name, stream, batch, channels, spatial, aligned, a);
+  return forward_apply_impl("oxh_batch_norm_forward_apply", stream, batch, channels, spatial,
+                            momentum, epsilon, input, weight, bias, running_mean,
+                            running_variance, saved_mean, saved_inverse_std, output, workspace,
+                            workspace_bytes, false);
 }
 
 oxh_status oxh_batch_norm_backward_reduce(oxh_stream stream, uint64_t batch, uint64_t channels,
@@ -977,7 +1254,7 @@ oxh_status oxh_batch_norm_backward_reduce(oxh_stream stream, uint64_t batch, uin
                                           const float *saved_inverse_std, void *workspace,
                                           uint64_t workspace_bytes) {
   return launch_reduce_gx("oxh_batch_norm_backward_reduce", stream, batch, channels, spatial,
-                          gradient, input, saved_mean, saved_inverse_std, workspace,
+                          gradient, nullptr, input, saved_mean, saved_inverse_std, workspace,
                           workspace_bytes, nullptr);
 }
 
@@ -988,35 +1265,10 @@ oxh_status oxh_batch_norm_backward_input(oxh_stream stream, uint64_t batch, uint
                                          const float *saved_inverse_std, float *input_gradient,
                                          float *weight_gradient, float *bias_gradient,
                                          const void *workspace, uint64_t workspace_bytes) {
-  const char *name = "oxh_batch_norm_backward_input";
-  oxh_status st = check_shape(name, batch, channels, spatial);
-  if (st != OXH_OK) return st;
-  OXH_REQUIRE(gradient && input && weight && saved_mean && saved_inverse_std &&
-                  input_gradient && weight_gradient && bias_gradient,
-              OXH_INVALID_SHAPE, std::string(name) + ": null pointer");
-  const Geometry g = make_geometry(batch, channels, spatial, false);
-  st = check_workspace(name, g, workspace, workspace_bytes);
-  if (st != OXH_OK) return st;
-  const uint64_t bytes = batch * channels * spatial * 4;
-  st = no_overlap(name, input_gradient, bytes, {input, gradient}, bytes);
-  if (st != OXH_OK) return st;
-  const bool aligned =
-      oxh::aligned16(gradient) && oxh::aligned16(input) && oxh::aligned16(input_gradient);
-  const float samples = static_cast<float>(batch * spatial);
-  if (use_flat(batch, channels, spatial)) {
-    oxh::launch(bn_finalize_affine_kernel, dim3((channels + 3) / 4), dim3(256), 0,
-                oxh::as_stream(stream), g, static_cast<const double2 *>(workspace),
-                weight_gradient, bias_gradient);
-    st = oxh::launched(name);
-    if (st != OXH_OK) return st;
-    DxTrainPhase::Args a{gradient, input, weight, saved_mean, saved_inverse_std, weight_gradient,
-                         bias_gradient, nullptr, 0, samples, nullptr, nullptr, input_gradient};
-    return launch_map<DxTrainPhase>(name, stream, batch, channels, spatial, aligned, a);
-  }
-  DxTrainPhase::Args a{gradient, input, weight, saved_mean, saved_inverse_std, nullptr, nullptr,
-                       static_cast<const double2 *>(workspace), g.slices, samples,
-                       weight_gradient, bias_gradient, input_gradient};
-  return launch_map<DxTrainPhase>(name, stream, batch, channels, spatial, aligned, a);
+  return backward_input_impl("oxh_batch_norm_backward_input", stream, batch, channels, spatial,
+                             gradient, nullptr, input, weight, saved_mean, saved_inverse_std,
+                             input_gradient, weight_gradient, bias_gradient, workspace,
+                             workspace_bytes);
 }
 
 oxh_status oxh_batch_norm_forward_train(oxh_stream stream, uint64_t batch, uint64_t channels,
@@ -1026,14 +1278,10 @@ oxh_status oxh_batch_norm_forward_train(oxh_stream stream, uint64_t batch, uint6
                                         float *running_variance, float *saved_mean,
                                         float *saved_inverse_std, float *output, void *workspace,
                                         uint64_t workspace_bytes) {
-  OXH_REQUIRE(std::isfinite(momentum) && std::isfinite(epsilon) && epsilon >= 0.0f,
-              OXH_INVALID_SHAPE, "oxh_batch_norm_forward_train: bad momentum or epsilon");
-  oxh_status st = oxh_batch_norm_forward_reduce(stream, batch, channels, spatial, input,
-                                                workspace, workspace_bytes);
-  if (st != OXH_OK) return st;
-  return oxh_batch_norm_forward_apply(stream, batch, channels, spatial, momentum, epsilon, input,
-                                      weight, bias, running_mean, running_variance, saved_mean,
-                                      saved_inverse_std, output, workspace, workspace_bytes);
+  return forward_train_impl("oxh_batch_norm_forward_train", stream, batch, channels, spatial,
+                            momentum, epsilon, input, weight, bias, running_mean,
+                            running_variance, saved_mean, saved_inverse_std, output, workspace,
+                            workspace_bytes, false);
 }
 
 oxh_status oxh_batch_norm_backward_train(oxh_stream stream, uint64_t batch, uint64_t channels,
@@ -1043,14 +1291,41 @@ oxh_status oxh_batch_norm_backward_train(oxh_stream stream, uint64_t batch, uint
                                          const float *saved_inverse_std, float *input_gradient,
                                          float *weight_gradient, float *bias_gradient,
                                          void *workspace, uint64_t workspace_bytes) {
-  oxh_status st = oxh_batch_norm_backward_reduce(stream, batch, channels, spatial, gradient,
-                                                 input, saved_mean, saved_inverse_std,
-                                                 workspace, workspace_bytes);
-  if (st != OXH_OK) return st;
-  return oxh_batch_norm_backward_input(stream, batch, channels, spatial, gradient, input, weight,
-                                       saved_mean, saved_inverse_std, input_gradient,
-                                       weight_gradient, bias_gradient, workspace,
-                                       workspace_bytes);
+  return backward_train_impl("oxh_batch_norm_backward_train", stream, batch, channels, spatial,
+                             gradient, nullptr, input, weight, saved_mean, saved_inverse_std,
+                             input_gradient, weight_gradient, bias_gradient, workspace,
+                             workspace_bytes);
+}
+
+oxh_status oxh_batch_norm_relu_forward_train(oxh_stream stream, uint64_t batch,
+                                             uint64_t channels, uint64_t spatial, float momentum,
+                                             float epsilon, const float *input,
+                                             const float *weight, const float *bias,
+                                             float *running_mean, float *running_variance,
+                                             float *saved_mean, float *saved_inverse_std,
+                                             float *output, void *workspace,
+                                             uint64_t workspace_bytes) {
+  return forward_train_impl("oxh_batch_norm_relu_forward_train", stream, batch, channels,
+                            spatial, momentum, epsilon, input, weight, bias, running_mean,
+                            running_variance, saved_mean, saved_inverse_std, output, workspace,
+                            workspace_bytes, true);
+}
+
+oxh_status oxh_batch_norm_relu_backward_train(oxh_stream stream, uint64_t batch,
+                                              uint64_t channels, uint64_t spatial,
+                                              const float *gradient, const float *output,
+                                              const float *input, const float *weight,
+                                              const float *saved_mean,
+                                              const float *saved_inverse_std,
+                                              float *input_gradient, float *weight_gradient,
+                                              float *bias_gradient, void *workspace,
+                                              uint64_t workspace_bytes) {
+  OXH_REQUIRE(output != nullptr, OXH_INVALID_SHAPE,
+              "oxh_batch_norm_relu_backward_train: null output");
+  return backward_train_impl("oxh_batch_norm_relu_backward_train", stream, batch, channels,
+                             spatial, gradient, output, input, weight, saved_mean,
+                             saved_inverse_std, input_gradient, weight_gradient, bias_gradient,
+                             workspace, workspace_bytes);
 }
 
 }  // extern "C"

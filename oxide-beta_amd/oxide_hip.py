@@ -126,6 +126,10 @@ _SIGNATURES = {
                                            _vp, _vp, _vp, _vp, _vp, _vp, _u64]),
     "oxh_batch_norm_backward_train": (_st, [_vp, _u64, _u64, _u64, _vp, _vp, _vp, _vp, _vp,
                                             _vp, _vp, _vp, _vp, _u64]),
+    "oxh_batch_norm_relu_forward_train": (_st, [_vp, _u64, _u64, _u64, _f32, _f32, _vp, _vp,
+                                                _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u64]),
+    "oxh_batch_norm_relu_backward_train": (_st, [_vp, _u64, _u64, _u64, _vp, _vp, _vp, _vp, _vp,
+                                                 _vp, _vp, _vp, _vp, _vp, _u64]),
     "oxh_cross_entropy_workspace_size": (_st, [_u64, _u64, ctypes.POINTER(_u64)]),
     "oxh_cross_entropy_forward": (_st, [_vp, _u64, _u64, _vp, _vp, _vp, _vp, _vp, _u64]),
     "oxh_cross_entropy_backward": (_st, [_vp, _u64, _u64, _vp, _vp, _vp, _vp, _vp]),
@@ -484,6 +488,29 @@ class LoadedModule:
                                                   _ptr(saved_inverse_std), _ptr(input_gradient),
                                                   _ptr(weight_gradient), _ptr(bias_gradient),
                                                   ws, wsb))
+
+    def batch_norm_relu_forward_train(self, x, weight, bias, running_mean, running_variance,
+                                      saved_mean, saved_inverse_std, out, momentum=0.1,
+                                      epsilon=1e-5, stream=None):
+        """out = relu(batch_norm(x)) (ConvNormAct with activation, nn.rs:376-385)."""
+        n, c, h, w = x.shape
+        ws, wsb = self._bn_ws_args(n, c, h * w)
+        check(lib().oxh_batch_norm_relu_forward_train(
+            _stream(stream), n, c, h * w, momentum, epsilon, _ptr(x), _ptr(weight), _ptr(bias),
+            _ptr(running_mean), _ptr(running_variance), _ptr(saved_mean),
+            _ptr(saved_inverse_std), _ptr(out), ws, wsb))
+
+    def batch_norm_relu_backward_train(self, gradient, out, x, weight, saved_mean,
+                                       saved_inverse_std, input_gradient, weight_gradient,
+                                       bias_gradient, stream=None):
+        """Backward of batch_norm_relu_forward_train; ``gradient`` is w.r.t. its output
+        ``out``."""
+        n, c, h, w = x.shape
+        ws, wsb = self._bn_ws_args(n, c, h * w)
+        check(lib().oxh_batch_norm_relu_backward_train(
+            _stream(stream), n, c, h * w, _ptr(gradient), _ptr(out), _ptr(x), _ptr(weight),
+            _ptr(saved_mean), _ptr(saved_inverse_std), _ptr(input_gradient),
+            _ptr(weight_gradient), _ptr(bias_gradient), ws, wsb))
 
     # -- cross entropy (kernel_module.rs:966-1050)
     def cross_entropy_forward(self, batch, classes, logits, targets, loss, error_flag=None,

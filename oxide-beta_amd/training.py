@@ -19,6 +19,12 @@ first-write-then-accumulate gradients (runtime.rs:671-692), and one multi-tensor
 advances a device step counter -- and that list is captured into one hipGraph, so a step is one
 graph launch. Each scheduled ``Op`` records the tensors it reads and writes so a checker can
 recompute it independently.
+
+Two rewrites keep the launch count down without changing any value: a BatchNorm whose only
+consumer is a ReLU (ConvNormAct with activation) runs as one fused BN + ReLU launch group each
+way (the ReLU backward's mask is read from the ReLU output, which is positive exactly where its
+input is), and the gradient of a residual add's first operand, when the add is that operand's
+only consumer, is the add's own gradient buffer (the add's backward is the identity).
 """
 
 from __future__ import annotations
@@ -355,6 +361,17 @@ class TrainingStep:
         self.logits_node = model.forward(self.input_node)
         self.loss_node = self.logits_node.cross_entropy(self.target_node)
         self.order = _topological(self.loss_node)
+        self.consumers: dict[int, list[Node]] = {}
+        for n in self.order:
+            for i in n.inputs:
+                self.consumers.setdefault(i.id, []).append(n)
+        # relu node id -> the batch norm it absorbs
+        self.fused_relu: dict[int, Node] = {}
+        for n in self.order:
+            if n.op == "relu" and n.inputs[0].op == "batch_norm2d" and \
+                    len(self.consumers[n.inputs[0].id]) == 1:
+                self.fused_relu[n.id] = n.inputs[0]
+        self.fused_bn = {bn.id for bn in self.fused_relu.values()}
         self.params = model.parameters()
         self.value: dict[int, object] = {}
         self.grad: dict[int, object] = {}
@@ -385,7 +402,8 @@ class TrainingStep:
             if n.op == "reshape":
                 self.value[n.id] = self.value[n.inputs[0].id].view(n.shape)
                 continue
-            self.value[n.id] = self._empty(n.shape)
+            if n.id not in self.fused_bn:  # a fused BN's output is never stored
+                self.value[n.id] = self._empty(n.shape)
             if n.op == "batch_norm2d":
                 bn = n.attrs["bn"]
                 bn.device_running_mean = torch.from_numpy(bn.running_mean.copy()).to(self.dev)
@@ -393,13 +411,22 @@ class TrainingStep:
                     bn.running_variance.copy()).to(self.dev)
                 n.attrs["saved_mean"] = self._empty((bn.channels,))
                 n.attrs["saved_inverse_std"] = self._empty((bn.channels,))
-        for n in self.order:  # activation gradients; a reshape shares its input's buffer
-            if n.op in ("param", "input", "targets", "cross_entropy"):
+        # activation gradients, consumers before producers: a reshape shares its input's
+        # buffer; an add's first operand, consumed only by the add, shares the add's
+        self.aliased: set[int] = set()
+        for n in reversed(self.order):
+            if n.op in ("param", "input", "targets", "cross_entropy") or n.id in self.fused_bn:
                 continue
-            if n.op == "reshape":
-                self.grad[n.id] = self.grad[n.inputs[0].id].view(n.shape)
-            else:
+            if n.id not in self.grad:
                 self.grad[n.id] = self._empty(n.shape)
+            if n.op == "reshape":
+                self.grad[n.inputs[0].id] = self.grad[n.id].view(n.inputs[0].shape)
+            elif n.op == "add":
+                first = n.inputs[0]
+                if len(self.consumers[first.id]) == 1 and first.id not in self.grad and \
+                        first.op not in ("param", "input"):
+                    self.grad[first.id] = self.grad[n.id]
+                    self.aliased.add(first.id)
         self.outer_gradient = torch.ones(1, device=self.dev)
         self.error_flag = torch.zeros(1, dtype=torch.int32, device=self.dev)
         self.step_counter = torch.zeros(1, dtype=torch.int32, device=self.dev)
@@ -455,8 +482,26 @@ class TrainingStep:
         for n in self.order:
             if n.op in ("param", "input", "targets", "reshape"):
                 continue
+            if n.id in self.fused_bn:
+                continue  # scheduled with its ReLU
             out = V[n.id]
-            if n.op == "conv2d":
+            if n.op == "relu" and n.id in self.fused_relu:
+                bn_node = self.fused_relu[n.id]
+                x, gamma, beta = (V[i.id] for i in bn_node.inputs)
+                bn = bn_node.attrs["bn"]
+                sm, si = bn_node.attrs["saved_mean"], bn_node.attrs["saved_inverse_std"]
+                rm, rv = bn.device_running_mean, bn.device_running_variance
+                self._emit(Op(f"bn{bn_node.id}+relu{n.id}", "batch_norm2d_relu_forward",
+                              dict(x=x, weight=gamma, bias=beta),
+                              dict(y=out, saved_mean=sm, saved_inverse_std=si),
+                              inplace=(rm, rv),
+                              attrs=dict(momentum=BN_MOMENTUM, epsilon=BN_EPSILON,
+                                         running_mean=rm, running_variance=rv)),
+                           lambda x=x, gamma=gamma, beta=beta, rm=rm, rv=rv, sm=sm, si=si,
+                           out=out: m.batch_norm_relu_forward_train(
+                               x, gamma, beta, rm, rv, sm, si, out, BN_MOMENTUM, BN_EPSILON,
+                               stream=s))
+            elif n.op == "conv2d":
                 x, w, b = (V[i.id] for i in n.inputs)
                 shape = ox.conv2d_shape(*n.inputs[0].shape, n.shape[1], n.inputs[1].shape[2],
                                         n.attrs["stride"], n.attrs["padding"], n.attrs["groups"])
@@ -518,10 +563,30 @@ class TrainingStep:
         for n in reversed(self.order):
             if n.op in ("param", "input", "targets", "cross_entropy"):
                 continue
+            if n.id in self.fused_bn:
+                continue  # its backward ran with its ReLU's
             if n.id not in self._written:
                 raise ox.OxideError(ox.TRACE, f"{n.op} value {n.id} receives no gradient")
             g = G[n.id]
-            if n.op == "reshape":
+            if n.op == "relu" and n.id in self.fused_relu:
+                bn_node = self.fused_relu[n.id]
+                x_node, w_node, b_node = bn_node.inputs
+                x, gamma, y = V[x_node.id], V[w_node.id], V[n.id]
+                sm, si = bn_node.attrs["saved_mean"], bn_node.attrs["saved_inverse_std"]
+                dgamma, _ = self._contribution(w_node)
+                dbeta, _ = self._contribution(b_node)
+                dst, acc = self._contribution(x_node)
+                self._emit(Op(f"bn{bn_node.id}+relu{n.id}.backward",
+                              "batch_norm2d_relu_backward",
+                              dict(gradient=g, y=y, x=x, weight=gamma, saved_mean=sm,
+                                   saved_inverse_std=si),
+                              dict(contribution=dst, weight_gradient=dgamma,
+                                   bias_gradient=dbeta),
+                              accumulate_into=acc),
+                           lambda g=g, y=y, x=x, gamma=gamma, sm=sm, si=si, dst=dst,
+                           dgamma=dgamma, dbeta=dbeta: m.batch_norm_relu_backward_train(
+                               g, y, x, gamma, sm, si, dst, dgamma, dbeta, stream=s))
+            elif n.op == "reshape":
                 # the gradient buffer is the input's; its one consumer has written it
                 if n.inputs[0].id in self._written:
                     raise ox.OxideError(ox.TRACE, "a reshaped value must have one consumer")
@@ -535,6 +600,9 @@ class TrainingStep:
                            lambda g=g, x=x, dst=dst: m.relu_backward(g, x, dst, stream=s))
             elif n.op == "add":
                 for i, inp in enumerate(n.inputs):
+                    if i == 0 and inp.id in self.aliased:
+                        self._written.add(inp.id)  # the add's gradient buffer is its own
+                        continue
                     dst, acc = self._contribution(inp)
                     self._emit(Op(f"add{n.id}.backward{i}", "add_backward", dict(gradient=g),
                                   dict(contribution=dst), accumulate_into=acc),
@@ -670,10 +738,12 @@ class TrainingStep:
         launches (fp32: each element read or written once)."""
         out = {"batch_norm2d": 0, "elementwise": 0, "adamw": 0}
         for op in self.ops:
-            if op.kind == "batch_norm2d_forward":
+            if op.kind in ("batch_norm2d_forward", "batch_norm2d_relu_forward"):
                 out["batch_norm2d"] += 3 * op.reads["x"].numel() * 4
             elif op.kind == "batch_norm2d_backward":
                 out["batch_norm2d"] += 5 * op.reads["x"].numel() * 4
+            elif op.kind == "batch_norm2d_relu_backward":  # + the ReLU output, twice
+                out["batch_norm2d"] += 7 * op.reads["x"].numel() * 4
             elif op.kind in ("relu_forward", "relu_backward", "add_forward"):
                 k = 2 if op.kind == "relu_forward" else 3
                 out["elementwise"] += k * next(iter(op.reads.values())).numel() * 4

@@ -55,13 +55,16 @@ def assert_within(got, ref, bound, what=""):
                              f"{worst}: |d|={d.ravel()[worst]!r} bound={bound.ravel()[worst]!r}")
 
 
-def check_batch_norm_forward(out, x, gamma, beta, rm, rv, momentum=0.1, eps=1e-5):
+def check_batch_norm_forward(out, x, gamma, beta, rm, rv, momentum=0.1, eps=1e-5, relu=False):
     """out: dict with y, mean, inv, rm, rv from the device for inputs x, gamma, beta and running
-    statistics rm, rv (before the update).  Returns the oracle's (mean, inv) and the fraction of
-    y within the strict criterion."""
+    statistics rm, rv (before the update); relu: y is relu(batch norm) (ReLU is 1-Lipschitz, so
+    the batch-norm bound carries over).  Returns the fraction of y within the strict
+    criterion."""
     import oracle
 
     y, mean, inv, rm1, rv1 = oracle.bn_forward(x, gamma, beta, rm, rv, True, momentum, eps)
+    if relu:
+        y = oracle.relu(y)
     c = x.shape[1]
     assert_close(out["mean"], mean, what="mean")
     assert_close(out["inv"], inv, what="inverse std")

@@ -192,3 +192,53 @@ def test_batch_norm_workspace_reuse_and_repeat(module, dev):
         again = _run(module, dev, x, gamma, beta, g, rm, rv)
         for k in first:
             assert np.array_equal(first[k], again[k]), k
+
+
+@pytest.mark.parametrize("shape", [(2, 3, 4, 4), (5, 4, 7, 7), (128, 96, 2, 2), (128, 1280, 1, 1),
+                                   (64, 32, 4, 4), (7, 16, 14, 14), (128, 32, 14, 14),
+                                   (3, 5, 3, 3)])
+def test_batch_norm_relu_fused_matches_unfused(module, dev, shape):
+    """ConvNormAct's BN + ReLU in one launch per direction: the fused forward equals the ReLU
+    kernel applied to the unfused forward, and the fused backward equals the unfused backward
+    fed the ReLU backward kernel's gradient -- bit for bit (same sums, same element formulas),
+    on the one-block-per-channel path (small planes) and the reduce + map path (14 x 14);
+    the unfused BN itself is pinned to the oracle."""
+    r = np.random.default_rng(hash(shape) & 0xFFFF)
+    x, gamma, beta, g = _case(r, shape, 1.3, 0.2)
+    c = shape[1]
+    rm = r.uniform(-0.5, 0.5, c).astype(np.float32)
+    rv = r.uniform(0.5, 2.0, c).astype(np.float32)
+    dx_, dw_, db_, dg_ = to_dev(x, dev), to_dev(gamma, dev), to_dev(beta, dev), to_dev(g, dev)
+
+    def stats():
+        return (to_dev(rm, dev), to_dev(rv, dev), torch.empty(c, device=dev),
+                torch.empty(c, device=dev))
+
+    # unfused: BN forward, ReLU, ReLU backward, BN backward
+    rm1, rv1, m1, i1 = stats()
+    y_bn = torch.empty_like(dx_)
+    module.batch_norm_forward_train(dx_, dw_, db_, rm1, rv1, m1, i1, y_bn, 0.1, 1e-5)
+    y1 = torch.empty_like(dx_)
+    module.relu(y_bn, y1)
+    g_masked = torch.empty_like(dx_)
+    module.relu_backward(dg_, y_bn, g_masked)
+    gx1, gw1, gb1 = torch.empty_like(dx_), torch.empty(c, device=dev), torch.empty(c, device=dev)
+    module.batch_norm_backward_train(g_masked, dx_, dw_, m1, i1, gx1, gw1, gb1)
+    # fused
+    rm2, rv2, m2, i2 = stats()
+    y2 = torch.empty_like(dx_)
+    module.batch_norm_relu_forward_train(dx_, dw_, db_, rm2, rv2, m2, i2, y2, 0.1, 1e-5)
+    gx2, gw2, gb2 = torch.empty_like(dx_), torch.empty(c, device=dev), torch.empty(c, device=dev)
+    module.batch_norm_relu_backward_train(dg_, y2, dx_, dw_, m2, i2, gx2, gw2, gb2)
+    torch.cuda.synchronize()
+    for a, b, what in ((y2, y1, "y"), (m2, m1, "mean"), (i2, i1, "inv"), (rm2, rm1, "rm"),
+                       (rv2, rv1, "rv"), (gx2, gx1, "dx"), (gw2, gw1, "dw"), (gb2, gb1, "db")):
+        np.testing.assert_array_equal(host(a), host(b), err_msg=what)
+    assert (host(y2) >= 0).all()
+    # the unfused composition against the oracle
+    out = dict(y=host(y_bn), mean=host(m1), inv=host(i1), rm=host(rm1), rv=host(rv1))
+    check_batch_norm_forward(out, x, gamma, beta, rm, rv)
+    gm = oracle.relu_backward(g, host(y_bn))
+    np.testing.assert_array_equal(host(g_masked), gm)
+    check_batch_norm_backward(dict(dx=host(gx1), dw=host(gw1), db=host(gb1)), gm, x, gamma,
+                              host(m1), host(i1))

@@ -93,6 +93,24 @@ class OracleChecker:
         check_batch_norm_backward(out, r["gradient"], r["x"], r["weight"], r["saved_mean"],
                                   r["saved_inverse_std"])
 
+    def batch_norm2d_relu_forward(self, op, r):
+        a, w = op.attrs, op.writes
+        out = dict(y=host(w["y"]), mean=host(w["saved_mean"]), inv=host(w["saved_inverse_std"]),
+                   rm=host(a["running_mean"]), rv=host(a["running_variance"]))
+        assert (out["y"] >= 0).all()
+        check_batch_norm_forward(out, r["x"], r["weight"], r["bias"],
+                                 self.prior[id(a["running_mean"])],
+                                 self.prior[id(a["running_variance"])], a["momentum"],
+                                 a["epsilon"], relu=True)
+
+    def batch_norm2d_relu_backward(self, op, r):
+        w = op.writes
+        out = dict(dx=host(w["contribution"]), dw=host(w["weight_gradient"]),
+                   db=host(w["bias_gradient"]))
+        masked = oracle.relu_backward(r["gradient"], r["y"])
+        check_batch_norm_backward(out, masked, r["x"], r["weight"], r["saved_mean"],
+                                  r["saved_inverse_std"])
+
     def relu_forward(self, op, r):
         assert_bitexact(host(op.writes["y"]), oracle.relu(r["x"]), op.name)
 
@@ -140,11 +158,14 @@ class OracleChecker:
             assert_bitexact(host(v), rv, f"adamw second moment {i}")
 
 
+# 46 BatchNorms, 32 of them followed by a ReLU (fused); 10 residual adds, whose first operand's
+# gradient is the add's own buffer (no launch)
 EXPECTED_KINDS = {"conv2d_forward": 47, "conv2d_parameter_backward": 47,
-                  "conv2d_input_backward": 46, "batch_norm2d_forward": 46,
-                  "batch_norm2d_backward": 46, "relu_forward": 32, "relu_backward": 32,
-                  "add_forward": 10, "add_backward": 20, "avg_pool2d_forward": 1,
-                  "avg_pool2d_backward": 1, "cross_entropy": 1, "adamw": 1}
+                  "conv2d_input_backward": 46, "batch_norm2d_forward": 14,
+                  "batch_norm2d_relu_forward": 32, "batch_norm2d_backward": 14,
+                  "batch_norm2d_relu_backward": 32, "add_forward": 10, "add_backward": 10,
+                  "avg_pool2d_forward": 1, "avg_pool2d_backward": 1, "cross_entropy": 1,
+                  "adamw": 1}
 
 
 def test_config5_step_every_op_matches_oracle():
