@@ -38,6 +38,7 @@ for p in (REPO / "oxide-beta_amd", REPO / "oracle"):
         sys.path.insert(0, str(p))
 
 PEAK_HBM_GBS = 8000.0
+EXTRAS = ("elementwise", "cross_entropy", "adamw", "mnist_step")
 T_BN = 64 * 128 * 56 * 56 * 4
 
 
@@ -319,18 +320,37 @@ def bench_mnist_step(steps: int = 20, batch: int = 128):
 
     step.run_eager()
     eager_ms = timed(step.run_eager, 3)
+    # per launch group: events on the step's stream around each group (eager; the events add
+    # a small gap between groups, so shares are of the summed group times)
+    pairs = [_events(2) for _ in step.ops]
+    for op, (e0, e1) in zip(step.ops, pairs):
+        e0.record(step.stream)
+        op.launch()
+        e1.record(step.stream)
+    step.synchronize()
+    kinds = {}
+    for op, (e0, e1) in zip(step.ops, pairs):
+        category, nbytes = T.op_bytes(op)
+        k = kinds.setdefault(category, {"groups": 0, "us": 0.0, "alg_bytes": 0})
+        k["groups"] += 1
+        k["us"] += e0.elapsed_time(e1) * 1e3
+        k["alg_bytes"] += nbytes
+    total_us = sum(k["us"] for k in kinds.values())
+    for k in kinds.values():
+        k["share"] = round(k["us"] / total_us, 4)
+        k["gbs"] = round(k["alg_bytes"] / (k["us"] * 1e-6) / 1e9, 1) if k["alg_bytes"] else None
+        k["us"] = round(k["us"], 1)
     step.capture()
     for _ in range(3):
         step.replay()
     graph_ms = timed(step.replay, steps)
     loss = step.loss_value()
-    nbytes = step.kernel_bytes()
     return {"config": f"MobileNetV4-Conv-S MNIST train step, batch {batch}, fp32",
             "graph_ms_per_step": round(graph_ms, 4), "eager_ms_per_step": round(eager_ms, 3),
             "images_per_s": round(batch / (graph_ms * 1e-3), 1),
             "launch_groups_per_step": len(step.ops), "steps_timed": steps,
-            "parameters": step.model.parameter_count(),
-            "loss_after": round(loss, 5), "alg_bytes_per_step": nbytes}
+            "parameters": step.model.parameter_count(), "loss_after": round(loss, 5),
+            "per_kind": kinds}
 
 
 def copy_calibration():
@@ -382,7 +402,10 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-extra", action="store_true", help="headline BN config only")
-    ap.add_argument("--only", choices=["elementwise", "cross_entropy", "adamw", "mnist_step"],
+    ap.add_argument("--extras", default=",".join(EXTRAS),
+                    help="comma-separated secondary workloads measured after the headline "
+                         f"(default: all of {','.join(EXTRAS)})")
+    ap.add_argument("--only", choices=EXTRAS,
                     help="run one secondary workload alone and print its result (for "
                          "profiling that workload's kernels)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -422,11 +445,16 @@ def main():
              "bn_eager_gbs": round(8 * T_BN / (bn["eager_ms_per_step"] * 1e-3) / 1e9, 1),
              "bn_events_ms_per_step": round(bn["event_ms_per_step"], 4),
              "bn_graph_steps_timed": bn["graph_steps"]}
-    if not args.no_extra:
-        extra["elementwise"] = bench_elementwise(m)
-        extra["cross_entropy"] = bench_cross_entropy(m)
-        extra["adamw"] = bench_adamw(m)
-        extra["mnist_step"] = bench_mnist_step()
+    chosen = [] if args.no_extra else [e for e in args.extras.split(",") if e]
+    for name in chosen:
+        if name not in EXTRAS:
+            print(f"bench.py: unknown workload {name!r}", file=sys.stderr)
+            sys.exit(2)
+    runners = {"elementwise": lambda: bench_elementwise(m),
+               "cross_entropy": lambda: bench_cross_entropy(m),
+               "adamw": lambda: bench_adamw(m), "mnist_step": lambda: bench_mnist_step()}
+    for name in chosen:
+        extra[name] = runners[name]()
     out = {
         "metric": "BatchNorm2d train fwd+bwd achieved HBM bandwidth (algorithmic bytes)",
         "value": round(value, 1),

@@ -733,25 +733,34 @@ class TrainingStep:
         self.synchronize()
         return int(self.step_counter.item())
 
-    def kernel_bytes(self) -> dict:
-        """Algorithmic HBM bytes per step of the BatchNorm, ReLU / add / accumulate and AdamW
-        launches (fp32: each element read or written once)."""
-        out = {"batch_norm2d": 0, "elementwise": 0, "adamw": 0}
-        for op in self.ops:
-            if op.kind in ("batch_norm2d_forward", "batch_norm2d_relu_forward"):
-                out["batch_norm2d"] += 3 * op.reads["x"].numel() * 4
-            elif op.kind == "batch_norm2d_backward":
-                out["batch_norm2d"] += 5 * op.reads["x"].numel() * 4
-            elif op.kind == "batch_norm2d_relu_backward":  # + the ReLU output, twice
-                out["batch_norm2d"] += 7 * op.reads["x"].numel() * 4
-            elif op.kind in ("relu_forward", "relu_backward", "add_forward"):
-                k = 2 if op.kind == "relu_forward" else 3
-                out["elementwise"] += k * next(iter(op.reads.values())).numel() * 4
-            elif op.kind == "adamw":
-                out["adamw"] += sum(7 * t[0].numel() * 4 for t in op.attrs["tensors"])
-            if op.accumulate_into is not None:
-                out["elementwise"] += 3 * op.accumulate_into.numel() * 4
-        return out
+def op_bytes(op: Op) -> tuple[str, int]:
+    """(category, algorithmic HBM bytes) of one launch group: every tensor it must read or
+    write, once (fp32).  Categories: the hot-path kernel families (batch_norm2d, elementwise,
+    cross_entropy, adamw) and the layers around them (conv2d, avg_pool2d)."""
+    nb = lambda t: t.numel() * 4  # noqa: E731
+    acc = 3 * nb(op.accumulate_into) if op.accumulate_into is not None else 0
+    k = op.kind
+    if k in ("batch_norm2d_forward", "batch_norm2d_relu_forward"):
+        return "batch_norm2d", 2 * nb(op.reads["x"])                       # x in, y out
+    if k == "batch_norm2d_backward":
+        return "batch_norm2d", 3 * nb(op.reads["x"]) + acc                 # g, x in; dx out
+    if k == "batch_norm2d_relu_backward":
+        return "batch_norm2d", 4 * nb(op.reads["x"]) + acc                 # g, y, x in; dx out
+    if k == "add_forward":
+        return "elementwise", 3 * nb(op.reads["a"])
+    if k == "relu_forward":
+        return "elementwise", 2 * nb(op.reads["x"])
+    if k == "relu_backward":
+        return "elementwise", 3 * nb(op.reads["gradient"]) + acc           # g, x in; out
+    if k == "add_backward":
+        return "elementwise", 2 * nb(op.reads["gradient"]) + acc           # copy of g
+    if k == "cross_entropy":
+        return "cross_entropy", 2 * nb(op.reads["logits"])
+    if k == "adamw":
+        return "adamw", sum(7 * nb(t[0]) for t in op.attrs["tensors"])
+    if k.startswith("avg_pool2d"):
+        return "avg_pool2d", 0
+    return "conv2d", 0
 
 
 def _conv_attrs(n: Node) -> dict:

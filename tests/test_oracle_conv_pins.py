@@ -102,3 +102,35 @@ def test_library_init_matches_oracle_restatement():
         a = oxide_hip.initialized_weights(shape, ipg)
         b = oracle.initialized_weights(shape, ipg)
         assert np.array_equal(a, b), shape
+
+
+def test_init_statistical_and_structural_properties():
+    """nn.rs:657-674 pinned by what its construction fixes (no reference output holds concrete
+    weights): every value is (k / 2^24 * 2 - 1) * sqrt(2 / fan_in) for an integer k in
+    [0, 2^24) (24-bit uniforms), the values are uniform on [-scale, scale) (mean 0, variance
+    scale^2 / 3, extremes near +-scale), consecutive values are uncorrelated (xorshift64
+    13/7/17 stream), and the seed is an XOR fold over the dimensions, so shapes that permute
+    the same dimensions draw the same unit stream.  A wrong fan-in, shift, scale or a skipped
+    xorshift step fails one of these."""
+    shape, ipg = [64, 48, 3, 3], 48
+    w32 = oracle.initialized_weights(shape, ipg).ravel()
+    scale = np.sqrt(np.float32(2.0) / np.float32(ipg * 9)).astype(np.float32)
+    # each value is the fp32 product of some grid point (k / 2^23 - 1) and the scale
+    k0 = np.round((w32.astype(np.float64) / float(scale) + 1.0) * 2.0 ** 23)
+    on_grid = np.zeros(w32.size, bool)
+    for d in (-1, 0, 1):
+        k = k0 + d
+        v = ((k / 2.0 ** 23) - 1.0).astype(np.float32)  # exact in fp32
+        on_grid |= (v * scale == w32) & (k >= 0) & (k < 2 ** 24)
+    assert on_grid.all()
+    u = w32.astype(np.float64) / float(scale)
+    n = u.size
+    assert abs(u.mean()) < 4 * np.sqrt(1 / 3 / n)
+    assert abs(u.var() - 1 / 3) < 0.02
+    assert u.max() > 0.999 and u.min() < -0.999 and np.abs(u).max() <= 1.0
+    assert abs(np.corrcoef(u[:-1], u[1:])[0, 1]) < 4 / np.sqrt(n)
+    a = oracle.initialized_weights([6, 4, 1, 1], 4).ravel() / np.sqrt(np.float32(2 / 4))
+    b = oracle.initialized_weights([4, 6, 1, 1], 6).ravel() / np.sqrt(np.float32(2 / 6))
+    np.testing.assert_allclose(a, b, rtol=1e-6)
+    c = oracle.initialized_weights([5, 4, 1, 1], 4).ravel()[:20] / np.sqrt(np.float32(2 / 4))
+    assert not np.allclose(a[:20], c)
