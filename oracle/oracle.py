@@ -65,6 +65,8 @@ _SIGNATURES = {
     "oro_avg_pool2d_backward": (None, [_F] + [_u64] * 8 + [_F]),
     "oro_initialized_weights": (None, [_U64P, _u64, _F]),
     "oro_argmax_rows": (None, [_F, _u64, _u64, _U64P]),
+    "oro_mnist_normalize": (None, [ctypes.c_void_p, _u64, _F]),
+    "oro_mnist_shuffle": (None, [_U64P, _u64]),
 }
 
 _lib = None
@@ -300,3 +302,37 @@ def argmax_rows(logits):
     out = np.empty(rows, np.uint64)
     lib().oro_argmax_rows(_f(logits), rows, classes, out.ctypes.data_as(_U64P))
     return out
+
+
+# ---------------------------------------------------------------- MNIST data
+
+def mnist_normalize(pixels):
+    """mnist.rs:118-121 per byte, float32."""
+    pixels = np.ascontiguousarray(pixels, dtype=np.uint8)
+    out = np.empty(pixels.shape, np.float32)
+    lib().oro_mnist_normalize(pixels.ctypes.data, pixels.size, _f(out))
+    return out
+
+
+def mnist_order(count, shuffle):
+    """MnistBatches::new index order (mnist.rs:84-100,191-199)."""
+    values = np.arange(count, dtype=np.uint64)
+    if shuffle:
+        lib().oro_mnist_shuffle(values.ctypes.data_as(_U64P), count)
+    return values
+
+
+# ---------------------------------------------------------------- OXTR checkpoints
+
+def oxtr_bytes(tensors):
+    """mobilenet_v4.rs:217-264: the bytes save() writes for (shape, values) pairs."""
+    import struct
+
+    out = [b"OXTR\x01", struct.pack("<Q", len(tensors))]
+    for shape, values in tensors:
+        values = np.ascontiguousarray(values, dtype=np.float32).ravel()
+        out.append(struct.pack("<Q", len(shape)))
+        out.extend(struct.pack("<Q", int(d)) for d in shape)
+        out.append(struct.pack("<Q", values.size))
+        out.append(values.astype("<f4").tobytes())
+    return b"".join(out)

@@ -456,3 +456,24 @@ void oro_argmax_rows(const float *logits, uint64_t rows, uint64_t classes, uint6
     out[r] = best;
   }
 }
+
+/* ------------------------------------------------------------------ MNIST data */
+
+/* mnist.rs:118-121 */
+void oro_mnist_normalize(const uint8_t *pixels, uint64_t n, float *out) {
+  for (uint64_t i = 0; i < n; ++i) out[i] = ((float)pixels[i] / 255.0f - 0.1307f) / 0.3081f;
+}
+
+/* mnist.rs:191-199: for index in (1..len).rev(), swap with state % (index + 1). */
+void oro_mnist_shuffle(uint64_t *values, uint64_t n) {
+  uint64_t state = 0xD1B54A32D192ED03ull;
+  for (uint64_t index = n; index-- > 1;) {
+    state ^= state << 13;
+    state ^= state >> 7;
+    state ^= state << 17;
+    uint64_t swap_with = state % (index + 1);
+    uint64_t t = values[index];
+    values[index] = values[swap_with];
+    values[swap_with] = t;
+  }
+}

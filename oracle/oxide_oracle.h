@@ -128,6 +128,12 @@ void oro_initialized_weights(const uint64_t *shape, uint64_t input_channels_per_
 /* mnist_training.rs:201-218: argmax with total_cmp, last index wins ties. */
 void oro_argmax_rows(const float *logits, uint64_t rows, uint64_t classes, uint64_t *out);
 
+/* ---- MNIST data (crates/oxide-torch/src/data/mnist.rs) ---- */
+/* mnist.rs:118-121: (f32::from(pixel) / 255.0 - 0.1307) / 0.3081 per byte. */
+void oro_mnist_normalize(const uint8_t *pixels, uint64_t n, float *out);
+/* mnist.rs:191-199: deterministic_shuffle of `values` in place. */
+void oro_mnist_shuffle(uint64_t *values, uint64_t n);
+
 #ifdef __cplusplus
 }
 #endif

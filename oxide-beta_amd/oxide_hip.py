@@ -76,6 +76,11 @@ class Pool2dShape(ctypes.Structure):
         "batch", "channels", "height", "width", "kernel_h", "kernel_w", "stride_h", "stride_w")]
 
 
+class CheckpointTensor(ctypes.Structure):
+    _fields_ = [("rank", ctypes.c_uint64), ("shape", ctypes.POINTER(ctypes.c_uint64)),
+                ("len", ctypes.c_uint64), ("data", ctypes.POINTER(ctypes.c_float))]
+
+
 _CS = ctypes.POINTER(Conv2dShape)
 _PS = ctypes.POINTER(Pool2dShape)
 
@@ -153,6 +158,22 @@ _SIGNATURES = {
     "oxh_avg_pool2d_backward": (_st, [_vp, _PS, _vp, _vp]),
     "oxh_initialized_weights": (_st, [ctypes.POINTER(_u64), _u64, ctypes.POINTER(_f32)]),
     "oxh_argmax_rows": (_st, [_vp, _u64, _u64, _vp, _vp]),
+    "oxh_checkpoint_save": (_st, [ctypes.c_char_p, ctypes.POINTER(CheckpointTensor), _u64]),
+    "oxh_checkpoint_load": (_st, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
+    "oxh_checkpoint_count": (_st, [_vp, ctypes.POINTER(_u64)]),
+    "oxh_checkpoint_entry": (_st, [_vp, _u64, ctypes.POINTER(_u64),
+                                   ctypes.POINTER(ctypes.POINTER(_u64)), ctypes.POINTER(_u64),
+                                   ctypes.POINTER(ctypes.POINTER(_f32))]),
+    "oxh_checkpoint_free": (_st, [_vp]),
+    "oxh_idx_parse_images": (_st, [_vp, _u64, ctypes.POINTER(_u64)]),
+    "oxh_idx_parse_labels": (_st, [_vp, _u64, ctypes.POINTER(_u64)]),
+    "oxh_mnist_load": (_st, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
+    "oxh_mnist_free": (_st, [_vp]),
+    "oxh_mnist_split": (_st, [_vp, ctypes.c_int, ctypes.POINTER(_vp), ctypes.POINTER(_vp),
+                              ctypes.POINTER(_u64)]),
+    "oxh_mnist_batch_order": (_st, [_u64, ctypes.c_int, _vp]),
+    "oxh_mnist_batch_host": (_st, [_vp, _vp, _u64, _vp, _u64, _vp, _vp]),
+    "oxh_mnist_gather_batch": (_st, [_vp, _vp, _vp, _u64, _vp, _u64, _vp, _vp]),
     "oxh_graph_begin": (_st, [_vp]),
     "oxh_graph_end": (_st, [_vp, ctypes.POINTER(_vp)]),
     "oxh_graph_abort": (_st, [_vp]),
@@ -314,6 +335,47 @@ def initialized_weights(shape, input_channels_per_group):
     check(lib().oxh_initialized_weights(dims, int(input_channels_per_group),
                                         out.ctypes.data_as(ctypes.POINTER(_f32))))
     return out.reshape(shape)
+
+
+def checkpoint_save(path, tensors) -> None:
+    """Writes an OXTR checkpoint (mobilenet_v4.rs:217-264); ``tensors`` is a sequence of
+    (shape, float32 values) in order."""
+    import numpy as np
+
+    keep = []
+    table = (CheckpointTensor * len(tensors))()
+    for i, (shape, values) in enumerate(tensors):
+        dims = np.ascontiguousarray(shape, dtype=np.uint64)
+        vals = np.ascontiguousarray(values, dtype=np.float32).ravel()
+        keep += [dims, vals]
+        table[i] = CheckpointTensor(len(dims), dims.ctypes.data_as(ctypes.POINTER(_u64)),
+                                    vals.size, vals.ctypes.data_as(ctypes.POINTER(_f32)))
+    check(lib().oxh_checkpoint_save(str(path).encode(), table, len(tensors)))
+
+
+def checkpoint_load(path) -> list:
+    """Reads an OXTR checkpoint (mobilenet_v4.rs:386-428): a list of (shape tuple, float32
+    values)."""
+    import numpy as np
+
+    handle = _vp()
+    check(lib().oxh_checkpoint_load(str(path).encode(), ctypes.byref(handle)))
+    try:
+        count = _u64()
+        check(lib().oxh_checkpoint_count(handle, ctypes.byref(count)))
+        out = []
+        for i in range(count.value):
+            rank, n = _u64(), _u64()
+            shape_p, data_p = ctypes.POINTER(_u64)(), ctypes.POINTER(_f32)()
+            check(lib().oxh_checkpoint_entry(handle, i, ctypes.byref(rank), ctypes.byref(shape_p),
+                                             ctypes.byref(n), ctypes.byref(data_p)))
+            shape = tuple(shape_p[d] for d in range(rank.value))
+            values = (np.ctypeslib.as_array(data_p, (n.value,)).copy() if n.value
+                      else np.zeros(0, np.float32))
+            out.append((shape, values))
+        return out
+    finally:
+        lib().oxh_checkpoint_free(handle)
 
 
 def conv2d_shape(batch, in_channels, height, width, out_channels, kernel, stride, padding,

@@ -285,6 +285,56 @@ class MobileNetV4ConvSmall:
     def parameter_count(self) -> int:
         return sum(p.values.size for p in self.parameters())
 
+    def train(self):
+        self.training = True
+
+    def eval(self):
+        self.training = False
+
+    training = True
+
+    def save(self, path) -> None:
+        """OXTR checkpoint (mobilenet_v4.rs:217-264): every parameter in visit order, then each
+        BatchNorm's running mean and running variance.  Values come from the host copies; a
+        TrainingStep's device state is brought back first with ``TrainingStep.sync_to_model``."""
+        tensors = [(p.shape, p.values) for p in self.parameters()]
+        for bn in self.batch_norms():
+            tensors += [((bn.channels,), bn.running_mean), ((bn.channels,), bn.running_variance)]
+        ox.checkpoint_save(path, tensors)
+
+    @classmethod
+    def load_mnist(cls, path) -> "MobileNetV4ConvSmall":
+        """load_mnist (mobilenet_v4.rs:266-321): the MNIST model with the checkpoint's
+        parameters and running statistics, in inference mode.  Too few or extra tensors ->
+        Execution; a parameter or buffer of another shape -> InvalidShape."""
+        tensors = ox.checkpoint_load(path)
+        model = cls.mnist()
+        nxt = 0
+        for p in model.parameters():
+            if nxt >= len(tensors):
+                raise ox.OxideError(ox.EXECUTION, "checkpoint has too few tensors")
+            shape, values = tensors[nxt]
+            if tuple(shape) != tuple(p.shape):
+                raise ox.OxideError(ox.INVALID_SHAPE, f"checkpoint tensor {nxt} has shape "
+                                    f"{list(shape)}, expected {list(p.shape)}")
+            if values.size != p.values.size:  # Tensor::from_vec in replace_data
+                raise ox.OxideError(ox.INVALID_SHAPE, "data length does not match the shape")
+            p.values = values.reshape(p.shape).astype(np.float32)
+            nxt += 1
+        for bn in model.batch_norms():
+            for name in ("running_mean", "running_variance"):
+                if nxt >= len(tensors):
+                    raise ox.OxideError(ox.EXECUTION, "checkpoint has too few buffers")
+                shape, values = tensors[nxt]
+                if tuple(shape) != (bn.channels,) or values.size != bn.channels:
+                    raise ox.OxideError(ox.INVALID_SHAPE, f"checkpoint buffer {nxt} shape mismatch")
+                setattr(bn, name, values.astype(np.float32))
+                nxt += 1
+        if nxt != len(tensors):
+            raise ox.OxideError(ox.EXECUTION, "checkpoint has extra tensors")
+        model.eval()
+        return model
+
 
 # ----------------------------------------------------------------------------- schedule
 
@@ -732,6 +782,127 @@ class TrainingStep:
     def steps_taken(self) -> int:
         self.synchronize()
         return int(self.step_counter.item())
+
+    def sync_to_model(self) -> None:
+        """Copies the device parameters and BatchNorm running statistics back into the model's
+        host arrays (sync_batch_norm_state, runtime.rs:1268-1304), e.g. before ``save``."""
+        self.synchronize()
+        for p in self.params:
+            p.values = p.value.detach().cpu().numpy().copy()
+        for bn in self.model.batch_norms():
+            bn.running_mean = bn.device_running_mean.detach().cpu().numpy().copy()
+            bn.running_variance = bn.device_running_variance.detach().cpu().numpy().copy()
+
+class EvalForward:
+    """The inference-mode forward (``model.eval()``: BatchNorm normalizes with the running
+    statistics, evaluation.rs:448-488,560-575) of ``batch`` images, as mnist_training.rs
+    evaluates the test set, with argmax predictions.  Parameters and running statistics are the
+    device tensors of ``source`` (a TrainingStep over the same model) when given, else uploaded
+    from the model's host arrays (e.g. after ``MobileNetV4ConvSmall.load_mnist``)."""
+
+    def __init__(self, model: MobileNetV4ConvSmall, batch: int,
+                 source: TrainingStep | None = None, device: int = 0):
+        import torch
+
+        if source is not None and source.model is not model:
+            raise ox.OxideError(ox.INVALID_SHAPE, "source trains another model")
+        self.torch, self.model, self.batch = torch, model, batch
+        self.dev = torch.device(f"cuda:{device}")
+        self.m = source.m if source is not None else ox.LoadedModule(device)
+        self.stream = source.stream if source is not None else torch.cuda.Stream(device=self.dev)
+        r = model.input_resolution
+        self.input_node = Node("input", (), (batch, model.input_channels, r, r))
+        self.logits_node = model.forward(self.input_node)
+        order = _topological(self.logits_node)
+        V: dict[int, object] = {}
+        for n in order:
+            if n.op == "param":
+                p = n.attrs["param"]
+                V[n.id] = (p.value if source is not None
+                           else torch.from_numpy(p.values.copy()).to(self.dev))
+            elif n.op == "reshape":
+                V[n.id] = V[n.inputs[0].id].view(n.shape)
+            else:
+                V[n.id] = torch.empty(n.shape, device=self.dev)
+        self.input, self.logits = V[self.input_node.id], V[self.logits_node.id]
+        self.class_indices = torch.zeros(batch, dtype=torch.int32, device=self.dev)
+        self.ops: list[Op] = []
+        m, s = self.m, self.stream
+        for n in order:
+            if n.op in ("param", "input", "reshape"):
+                continue
+            out = V[n.id]
+            if n.op == "conv2d":
+                x, w, b = (V[i.id] for i in n.inputs)
+                shape = ox.conv2d_shape(*n.inputs[0].shape, n.shape[1], n.inputs[1].shape[2],
+                                        n.attrs["stride"], n.attrs["padding"], n.attrs["groups"])
+                self.ops.append(Op(f"conv{n.id}", "conv2d_forward", dict(x=x, weight=w, bias=b),
+                                   dict(y=out), attrs=_conv_attrs(n),
+                                   launch=lambda shape=shape, x=x, w=w, b=b, out=out:
+                                   m.conv2d_forward(shape, x, w, b, out, stream=s)))
+            elif n.op == "batch_norm2d":
+                x, gamma, beta = (V[i.id] for i in n.inputs)
+                bn = n.attrs["bn"]
+                if source is not None:
+                    rm, rv = bn.device_running_mean, bn.device_running_variance
+                else:
+                    rm = torch.from_numpy(bn.running_mean.copy()).to(self.dev)
+                    rv = torch.from_numpy(bn.running_variance.copy()).to(self.dev)
+                inv = torch.empty(bn.channels, device=self.dev)
+                _, c, h, w_ = n.shape
+
+                def launch(x=x, gamma=gamma, beta=beta, rm=rm, rv=rv, inv=inv, out=out, c=c,
+                           hw=h * w_):
+                    # evaluation.rs:560-575 then 577-597
+                    m.batch_norm_running_inverse_std(BN_EPSILON, rv, inv, stream=s)
+                    m.batch_norm_apply(c, hw, x, gamma, beta, rm, inv, out, stream=s)
+
+                self.ops.append(Op(f"bn{n.id}", "batch_norm2d_eval_forward",
+                                   dict(x=x, weight=gamma, bias=beta, running_mean=rm,
+                                        running_variance=rv),
+                                   dict(y=out, inverse_std=inv),
+                                   attrs=dict(epsilon=BN_EPSILON), launch=launch))
+            elif n.op == "relu":
+                x = V[n.inputs[0].id]
+                self.ops.append(Op(f"relu{n.id}", "relu_forward", dict(x=x), dict(y=out),
+                                   launch=lambda x=x, out=out: m.relu(x, out, stream=s)))
+            elif n.op == "add":
+                a, b = V[n.inputs[0].id], V[n.inputs[1].id]
+                self.ops.append(Op(f"add{n.id}", "add_forward", dict(a=a, b=b), dict(y=out),
+                                   launch=lambda a=a, b=b, out=out: m.add(a, b, out, stream=s)))
+            elif n.op == "avg_pool2d":
+                x = V[n.inputs[0].id]
+                ps = ox.Pool2dShape(*n.inputs[0].shape, *n.attrs["kernel"], *n.attrs["stride"])
+                self.ops.append(Op(f"pool{n.id}", "avg_pool2d_forward", dict(x=x), dict(y=out),
+                                   attrs=dict(kernel=n.attrs["kernel"],
+                                              stride=n.attrs["stride"]),
+                                   launch=lambda ps=ps, x=x, out=out:
+                                   m.avg_pool2d_forward(ps, x, out, stream=s)))
+            else:
+                raise ox.OxideError(ox.TRACE, f"no inference forward for {n.op}")
+        torch.cuda.synchronize()
+
+    def set_images(self, images: np.ndarray) -> None:
+        images = np.ascontiguousarray(images, np.float32).reshape(self.input.shape)
+        self.stream.synchronize()
+        self.input.copy_(self.torch.from_numpy(images))
+        self.torch.cuda.synchronize()
+
+    def run(self, before=None, after=None) -> None:
+        for op in self.ops:
+            if before is not None:
+                before(op)
+            op.launch()
+            if after is not None:
+                after(op)
+
+    def predicted_classes(self) -> np.ndarray:
+        """argmax of each row of the logits (count_correct, mnist_training.rs:201-218: ties go
+        to the last index)."""
+        self.m.argmax_rows(self.logits, self.class_indices, stream=self.stream)
+        self.stream.synchronize()
+        return self.class_indices.cpu().numpy().astype(np.int64)
+
 
 def op_bytes(op: Op) -> tuple[str, int]:
     """(category, algorithmic HBM bytes) of one launch group: every tensor it must read or
