@@ -131,9 +131,10 @@ oxh_status oxh_checkpoint_entry(const oxh_checkpoint *checkpoint, uint64_t index
   return oxh::ok();
 }
 
+// Leaves the calling thread's last error untouched (it runs on error paths too).
 oxh_status oxh_checkpoint_free(oxh_checkpoint *checkpoint) {
   delete checkpoint;
-  return oxh::ok();
+  return OXH_OK;
 }
 
 }  // extern "C"

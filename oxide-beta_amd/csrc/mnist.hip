@@ -164,8 +164,8 @@ oxh_status oxh_mnist_load(const char *directory, oxh_mnist **out) {
 }
 
 oxh_status oxh_mnist_free(oxh_mnist *mnist) {
-  delete mnist;
-  return oxh::ok();
+  delete mnist;  // the last error stays untouched
+  return OXH_OK;
 }
 
 oxh_status oxh_mnist_split(const oxh_mnist *mnist, int test, const uint8_t **images,

@@ -10,6 +10,9 @@ def to_dev(a, dev):
 
 
 def host(t):
+    """Host copy of a torch tensor or of a library-owned device view."""
+    if hasattr(t, "host"):
+        return t.host()
     return t.detach().cpu().numpy()
 
 

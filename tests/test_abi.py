@@ -18,8 +18,11 @@ def test_library_exports_every_header_symbol():
     assert len(symbols) >= 50
     missing = [s for s in symbols if not hasattr(lib, s)]
     assert not missing, missing
-    # every declared function also has a ctypes signature in the front end
-    assert set(symbols) <= set(ox._SIGNATURES), set(symbols) - set(ox._SIGNATURES)
+    # every declared function also has a ctypes signature in the front ends
+    import training
+
+    bound = set(ox._SIGNATURES) | set(training.signatures())
+    assert set(symbols) <= bound, set(symbols) - bound
     assert ox.lib().oxh_version().decode().startswith("oxide-hip")
 
 

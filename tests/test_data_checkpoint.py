@@ -10,7 +10,6 @@ import pytest
 import data as D
 import oracle
 import oxide_hip as ox
-import training as T
 
 
 def _idx_images(pixels: np.ndarray, rows=28, cols=28, magic=2051) -> bytes:
@@ -169,52 +168,3 @@ def test_checkpoint_read_errors(tmp_path):
     load(good[:9])                                           # truncated count
     load(b"OXTR\x01" + (2 ** 62).to_bytes(8, "little"))      # absurd count, no data
     load(b"OXTR\x01" + (1).to_bytes(8, "little") + (2 ** 61).to_bytes(8, "little"))
-
-
-def _model_tensors(model):
-    out = [(p.shape, p.values) for p in model.parameters()]
-    for bn in model.batch_norms():
-        out += [((bn.channels,), bn.running_mean), ((bn.channels,), bn.running_variance)]
-    return out
-
-
-def test_model_save_load_round_trip(tmp_path):
-    """save() writes parameters (visit order) then each BatchNorm's running mean / variance;
-    load_mnist restores them and switches to inference mode."""
-    model = T.MobileNetV4ConvSmall.mnist()
-    r = np.random.default_rng(3)
-    for bn in model.batch_norms():
-        bn.running_mean = r.standard_normal(bn.channels).astype(np.float32)
-        bn.running_variance = r.uniform(0.5, 2, bn.channels).astype(np.float32)
-    path = tmp_path / "mobilenetv4-mnist.oxtr"
-    model.save(path)
-    tensors = _model_tensors(model)
-    assert len(tensors) == 186 + 2 * 46
-    assert path.read_bytes() == oracle.oxtr_bytes(tensors)
-    loaded = T.MobileNetV4ConvSmall.load_mnist(path)
-    assert loaded.training is False
-    for a, b in zip(_model_tensors(loaded), tensors):
-        assert tuple(a[0]) == tuple(b[0])
-        np.testing.assert_array_equal(a[1], b[1])
-
-
-def test_model_load_errors(tmp_path):
-    model = T.MobileNetV4ConvSmall.mnist()
-    tensors = _model_tensors(model)
-    path = tmp_path / "m.oxtr"
-
-    def expect(ts, status, text):
-        ox.checkpoint_save(path, ts)
-        with pytest.raises(ox.OxideError) as e:
-            T.MobileNetV4ConvSmall.load_mnist(path)
-        assert e.value.status == status and text in str(e.value), str(e.value)
-
-    expect(tensors[:100], ox.EXECUTION, "checkpoint has too few tensors")
-    expect(tensors[:186], ox.EXECUTION, "checkpoint has too few buffers")
-    expect(tensors + [((1,), np.zeros(1, np.float32))], ox.EXECUTION, "extra tensors")
-    bad = list(tensors)
-    bad[0] = ((32, 1, 3, 2), np.zeros(192, np.float32))
-    expect(bad, ox.INVALID_SHAPE, "checkpoint tensor 0 has shape")
-    bad = list(tensors)
-    bad[186] = ((31,), np.zeros(31, np.float32))
-    expect(bad, ox.INVALID_SHAPE, "checkpoint buffer 186 shape mismatch")

@@ -115,3 +115,68 @@ def test_train_save_load_evaluate(tmp_path):
     assert_bitexact(host(fresh.logits), host(shared.logits), "logits")
     np.testing.assert_array_equal(fresh.predicted_classes(),
                                   oracle.argmax_rows(host(fresh.logits)))
+
+
+def _model_tensors(model):
+    out = [(p.shape, host(p.value)) for p in model.parameters()]
+    for bn in model.batch_norms():
+        out += [((bn.channels,), host(bn.device_running_mean)),
+                ((bn.channels,), host(bn.device_running_variance))]
+    return out
+
+
+def test_model_save_load_round_trip(tmp_path):
+    """save() writes parameters (visit order) then each BatchNorm's running mean / variance
+    (mobilenet_v4.rs:217-264), byte for byte as the oracle's writer; load_mnist restores them
+    and switches to inference mode."""
+    model = T.MobileNetV4ConvSmall.mnist()
+    r = np.random.default_rng(3)
+    for bn in model.batch_norms():
+        bn.device_running_mean.copy_from(r.standard_normal(bn.channels).astype(np.float32))
+        bn.device_running_variance.copy_from(r.uniform(0.5, 2, bn.channels).astype(np.float32))
+    path = tmp_path / "mobilenetv4-mnist.oxtr"
+    model.save(path)
+    tensors = _model_tensors(model)
+    assert len(tensors) == 186 + 2 * 46
+    assert path.read_bytes() == oracle.oxtr_bytes(tensors)
+    loaded = T.MobileNetV4ConvSmall.load_mnist(path)
+    assert loaded.training is False
+    for a, b in zip(_model_tensors(loaded), tensors):
+        assert tuple(a[0]) == tuple(b[0])
+        np.testing.assert_array_equal(a[1], b[1])
+    # the deterministic init reached the device unchanged
+    p0 = model.parameters()[0]
+    np.testing.assert_array_equal(host(p0.value), oracle.initialized_weights([32, 1, 3, 3], 1))
+
+
+def test_model_load_errors(tmp_path):
+    """load_mnist's error kinds (mobilenet_v4.rs:271-321)."""
+    tensors = _model_tensors(T.MobileNetV4ConvSmall.mnist())
+    path = tmp_path / "m.oxtr"
+
+    def expect(ts, status, text):
+        ox.checkpoint_save(path, ts)
+        with pytest.raises(ox.OxideError) as e:
+            T.MobileNetV4ConvSmall.load_mnist(path)
+        assert e.value.status == status and text in str(e.value), str(e.value)
+
+    expect(tensors[:100], ox.EXECUTION, "checkpoint has too few tensors")
+    expect(tensors[:186], ox.EXECUTION, "checkpoint has too few buffers")
+    expect(tensors + [((1,), np.zeros(1, np.float32))], ox.EXECUTION, "extra tensors")
+    bad = list(tensors)
+    bad[0] = ((32, 1, 3, 2), np.zeros(192, np.float32))
+    expect(bad, ox.INVALID_SHAPE, "checkpoint tensor 0 has a different shape")
+    bad = list(tensors)
+    bad[0] = ((32, 1, 3, 3), np.zeros(10, np.float32))
+    expect(bad, ox.INVALID_SHAPE, "data length does not match the shape")
+    bad = list(tensors)
+    bad[186] = ((31,), np.zeros(31, np.float32))
+    expect(bad, ox.INVALID_SHAPE, "checkpoint buffer 186 shape mismatch")
+    # a trainer needs a model in training mode
+    ox.checkpoint_save(path, tensors)
+    loaded = T.MobileNetV4ConvSmall.load_mnist(path)
+    with pytest.raises(ox.OxideError) as e:
+        T.TrainingStep(loaded, 4)
+    assert e.value.status == ox.EXECUTION
+    loaded.train()
+    T.TrainingStep(loaded, 4)

@@ -1,5 +1,5 @@
-"""Host-side tracing of MobileNetV4-Conv-S (no GPU): the reference's own shape tests
-(mobilenet_v4.rs:442-466) and module validation errors (nn.rs)."""
+"""Host-side description of MobileNetV4-Conv-S by the library (no GPU): the reference's own
+shape tests (mobilenet_v4.rs:442-466) and the model census."""
 
 import pytest
 
@@ -9,9 +9,8 @@ import training as T
 
 def test_conv_small_matches_supplement_table_11_shapes():
     """mobilenet_v4.rs:442-459."""
-    model = T.MobileNetV4ConvSmall.new(1000)
-    out, shapes = model.forward_with_shapes(T.Node("input", (), (1, 3, 224, 224)))
-    assert out.shape == (1, 1000)
+    d = T.MobileNetV4ConvSmall.describe(1000, 3, 224, batch=1)
+    shapes = d["block_shapes"]
     assert len(shapes) == 19
     assert shapes[0] == (1, 32, 112, 112)
     assert shapes[1] == (1, 32, 56, 56)
@@ -26,39 +25,24 @@ def test_conv_small_matches_supplement_table_11_shapes():
 
 
 def test_mnist_variant_accepts_grayscale_images():
-    """mobilenet_v4.rs:461-466."""
-    model = T.MobileNetV4ConvSmall.mnist()
-    assert model.forward(T.Node("input", (), (2, 1, 28, 28))).shape == (2, 10)
-    with pytest.raises(ox.OxideError):
-        model.forward(T.Node("input", (), (2, 3, 28, 28)))
+    """mobilenet_v4.rs:461-466: [2, 1, 28, 28] -> [2, 10]."""
+    d = T.MobileNetV4ConvSmall.describe(10, 1, 28, batch=2)
+    assert d["block_shapes"][-1] == (2, 10)
+    assert d["block_shapes"][:3] == [(2, 32, 14, 14), (2, 32, 7, 7), (2, 64, 4, 4)]
 
 
-def test_mnist_graph_census():
-    """The traced step: 47 convolutions (one per Conv2d), 46 BatchNorms, a residual add per
-    stride-1 block with equal channels, parameters in visit order (weight, bias per conv;
-    gamma, beta per BatchNorm)."""
-    model = T.MobileNetV4ConvSmall.mnist()
-    loss = model.forward(T.Node("input", (), (8, 1, 28, 28))).cross_entropy(
-        T.Node("targets", (), (8,)))
-    ops = [n.op for n in T._topological(loss)]
-    assert ops.count("conv2d") == 47 and ops.count("batch_norm2d") == 46
-    residual = sum(getattr(b, "residual", False) for b in model.blocks)
-    assert ops.count("add") == residual == 10
-    params = model.parameters()
-    assert len(params) == 2 * 47 + 2 * 46
-    assert params[0].shape == (32, 1, 3, 3) and params[1].shape == (32,)
-    assert params[-2].shape == (10, 1280, 1, 1)
-    # every parameter is reached by the traced graph exactly once
-    ids = [n.attrs["param"] for n in T._topological(loss) if n.op == "param"]
-    assert sorted(map(id, ids)) == sorted(map(id, params))
+def test_mnist_model_census():
+    """47 convolutions (weight + bias each) and 46 BatchNorms (gamma + beta each) in visit
+    order: 186 parameter tensors, 2 517 802 values."""
+    d = T.MobileNetV4ConvSmall.describe(10, 1, 28)
+    assert d["parameters"] == 2 * 47 + 2 * 46 == 186
+    assert d["batch_norms"] == 46
+    assert d["values"] == 2517802
 
 
-def test_module_validation():
+def test_invalid_configurations():
+    with pytest.raises(ox.OxideError) as e:
+        T.MobileNetV4ConvSmall.describe(0, 1, 28)
+    assert e.value.status == ox.INVALID_SHAPE and "num_classes" in str(e.value)
     with pytest.raises(ox.OxideError):
-        T.Conv2d(3, 4, 3, 1, 2)  # 3 channels do not split into 2 groups
-    with pytest.raises(ox.OxideError):
-        T.Conv2d(4, 4, 0, 1, 1)
-    with pytest.raises(ox.OxideError):
-        T.UniversalInvertedBottleneck(8, 8, 16, 3, None, 2)
-    with pytest.raises(ox.OxideError):
-        T.MobileNetV4ConvSmall(0)
+        T.MobileNetV4ConvSmall.describe(10, 1, 28, batch=0)
