@@ -167,6 +167,58 @@ __global__ __launch_bounds__(256) void conv2d_weight_partial_kernel(
   }
 }
 
+// Depthwise weight gradient (one group per channel, square kernels of size 3 or 5): one block
+// per channel.  Each thread walks the channel's output positions j, j + 256, ... and keeps one
+// partial sum per kernel tap in registers; a fixed xor butterfly per wave and a fixed-order sum
+// over the 4 waves combine them (deterministic; within fp32 rounding of the CPU's (n, oy, ox)
+// running sum).  One launch, in place of the batch-chunk partials and their sum.
+template <int K>
+__global__ __launch_bounds__(256) void conv2d_depthwise_weight_kernel(
+    ConvGeom g, oxh::FastDiv oplane_div, const float *__restrict__ grad,
+    const float *__restrict__ x, float *__restrict__ weight_gradient) {
+  constexpr int kTaps = K * K;
+  __shared__ float wave_sums[4][kTaps];
+  const uint32_t c = blockIdx.x;
+  const uint32_t oplane = g.oh * g.ow, plane = g.h * g.w;
+  const uint32_t positions = g.batch * oplane;
+  const int h = static_cast<int>(g.h), w = static_cast<int>(g.w);
+  float acc[kTaps];
+#pragma unroll
+  for (int t = 0; t < kTaps; ++t) acc[t] = 0.0f;
+  for (uint32_t j = threadIdx.x; j < positions; j += 256) {
+    const uint32_t n = fdiv(j, oplane_div), r = j - n * oplane;
+    const uint32_t oy = fdiv(r, g.ow_div), ox = r - oy * g.ow;
+    const float gv = grad[(n * g.out_c + c) * oplane + r];
+    const float *xp = x + (n * g.in_c + c) * plane;
+    const int by = static_cast<int>(oy * g.stride) - static_cast<int>(g.pad);
+    const int bx = static_cast<int>(ox * g.stride) - static_cast<int>(g.pad);
+#pragma unroll
+    for (int ky = 0; ky < K; ++ky) {
+      const int iy = by + ky;
+      if (iy < 0 || iy >= h) continue;
+#pragma unroll
+      for (int kx = 0; kx < K; ++kx) {
+        const int ix = bx + kx;
+        if (ix >= 0 && ix < w) acc[ky * K + kx] += gv * xp[iy * w + ix];
+      }
+    }
+  }
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+#pragma unroll
+  for (int t = 0; t < kTaps; ++t) {
+    float v = acc[t];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    if (lane == 0) wave_sums[wave][t] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x < kTaps) {
+    const int t = threadIdx.x;
+    weight_gradient[c * kTaps + t] =
+        ((wave_sums[0][t] + wave_sums[1][t]) + wave_sums[2][t]) + wave_sums[3][t];
+  }
+}
+
 // Bias gradient: one wave per output channel.  Lane l adds the channel's terms l, l + 64, ...
 // of the (n, oy, ox) order in fp32; a fixed xor butterfly combines the 64 lane sums
 // (deterministic; within fp32 rounding of the CPU's single running sum).
@@ -527,7 +579,15 @@ uint32_t weight_chunks(const ConvGeom &g) {
   if (c < 1) c = 1;
   return static_cast<uint32_t>(c);
 }
+// Depthwise convolutions with 3 x 3 or 5 x 5 kernels take the one-block-per-channel weight
+// gradient.
+bool depthwise_single_pass(const ConvGeom &g) {
+  return g.in_per_group == 1 && g.out_per_group == 1 && g.kh == g.kw &&
+         (g.kh == 3 || g.kh == 5) && g.out_c <= 65535 * 16;
+}
+
 uint64_t weight_partial_bytes(const ConvGeom &g) {
+  if (depthwise_single_pass(g)) return 0;
   if (pointwise(g)) {
     const KSplit k = product_split(g);
     return k.chunks > 1 ? static_cast<uint64_t>(k.chunks) * g.out_c * g.in_c * 4 : 0;
@@ -696,6 +756,16 @@ oxh_status oxh_conv2d_weight_backward(oxh_stream stream, const oxh_conv2d_shape 
     const uint32_t count = g.out_c * g.in_c;
     oxh::launch(sum_chunks_kernel, dim3(grid_for(count)), dim3(256), 0, s, count, split.chunks,
                 static_cast<const float *>(partial), weight_gradient);
+    return oxh::launched(name);
+  }
+  if (depthwise_single_pass(g)) {
+    const oxh::FastDiv oplane_div = oxh::make_fastdiv(g.oh * g.ow);
+    if (g.kh == 3)
+      oxh::launch(conv2d_depthwise_weight_kernel<3>, dim3(g.out_c), dim3(256), 0, s, g,
+                  oplane_div, gradient, input, weight_gradient);
+    else
+      oxh::launch(conv2d_depthwise_weight_kernel<5>, dim3(g.out_c), dim3(256), 0, s, g,
+                  oplane_div, gradient, input, weight_gradient);
     return oxh::launched(name);
   }
   const uint32_t chunks = weight_chunks(g);
