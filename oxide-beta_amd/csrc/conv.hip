@@ -290,52 +290,113 @@ struct ProductArgs {
   uint32_t M, N, K, k_chunk;
 };
 
-constexpr int kTile = 32, kMicro = 2, kSlab = 128, kUnrollK = 8;
-constexpr int kTileLoads = kTile * kSlab / 256;  // per thread, per operand, per slab
+// Tilings of the product, each with one serial sum per output: 32 x 32 outputs per 256-thread
+// block (2 x 2 per thread) for grids that fill the chip; for small grids, where the serial k
+// chain of each thread sets the time, 8 x 8 outputs per 64-thread block (one per thread: a
+// quarter of the chain work per thread, four times the blocks, and one wave per CU rather than
+// four sharing its LDS), or 16 x 16 per 256 threads with OXH_TINY_TILE=16.
+#ifndef OXH_SMALL_SLAB
+#define OXH_SMALL_SLAB 128  // k per LDS stage of the small-grid tilings
+#endif
+constexpr int kTile = 32, kUnrollK = 8;  // kTile: the tiling of large grids
 
-__device__ __forceinline__ void tile_coords(bool k_fast, int e, int &r, int &kk) {
-  if (k_fast) {
-    kk = e % kSlab;
-    r = e / kSlab;
-  } else {
-    r = e % kTile;
-    kk = e / kTile;
-  }
-}
+template <int Tile, int Threads>
+struct TileShape {
+  static constexpr int kCols = Threads == 256 ? 16 : 8;       // threads per tile row
+  static constexpr int kMicro = Tile / kCols;                  // outputs per thread per axis
+  static constexpr int kSlab = Tile == kTile ? 128 : OXH_SMALL_SLAB;  // k per LDS stage
+  static constexpr int kLoads = Tile * kSlab / Threads;        // per thread, per operand
+  static_assert(kCols * kCols == Threads && kMicro * kCols == Tile, "tile shape");
+  static_assert(Threads % kSlab == 0 || kSlab % Threads == 0, "slab");
+};
 
-__device__ __forceinline__ void fetch_slab(const Operand &o, uint32_t r0, uint32_t rows,
-                                           uint32_t k0, uint32_t kc, float (&v)[kTileLoads]) {
+// One operand's share of a slab load (element e = thread + u * Threads of the slab's
+// Tile x kSlab values).  k-fast operands (contiguous along k): e = r * kSlab + kk, so a thread
+// keeps kKCols k columns and visits its rows in order; row-fast ones: e = kk * Tile + r, the
+// thread's row is fixed and its k step by Threads / Tile.  Row offsets are computed once per
+// block.  A load outside the operand reads element 0 instead (no branch per load) and its value
+// is never used: the arithmetic stops at the slab's k count, and rows past M or N only feed
+// outputs that are not stored.
+template <int Tile, int Threads, bool KFast>
+struct SlabLoader {
+  using S = TileShape<Tile, Threads>;
+  static constexpr int kLoads = S::kLoads, kSlab = S::kSlab;
+  static constexpr int kKCols = KFast && kSlab > Threads ? kSlab / Threads : 1;
+  static constexpr int kRows = KFast ? kLoads / kKCols : 1;  // distinct rows per thread
+  static constexpr int kRowStep = KFast ? (kSlab > Threads ? 1 : Threads / kSlab) : 0;
+  static constexpr int kKStep = KFast ? Threads : Threads / Tile;
+  uint32_t row_off[kRows];
+  uint32_t row_ok;  // bit i: row i inside the operand
+  int r, kk;        // first (row, k) of the thread
+
+  __device__ __forceinline__ SlabLoader(const Operand &o, uint32_t r0, uint32_t rows) {
+    const int t = static_cast<int>(threadIdx.x);
+    r = KFast ? (kSlab > Threads ? 0 : t / kSlab) : t % Tile;
+    kk = KFast ? t % kSlab : t / Tile;
+    row_ok = 0;
 #pragma unroll
-  for (int u = 0; u < kTileLoads; ++u) {
-    int r, kk;
-    tile_coords(o.k_fast, threadIdx.x + u * 256, r, kk);
-    const uint32_t row = r0 + r;
-    v[u] = (row < rows && static_cast<uint32_t>(kk) < kc)
-               ? o.ptr[axis_offset(o.row, row) + axis_offset(o.k, k0 + kk)]
-               : 0.0f;
+    for (int i = 0; i < kRows; ++i) {
+      const uint32_t row = r0 + r + i * kRowStep;
+      const bool ok = row < rows;
+      row_off[i] = ok ? axis_offset(o.row, row) : 0;
+      row_ok |= ok ? (1u << i) : 0u;
+    }
   }
-}
 
-// LDS rows padded to kTile + 1 floats: k-fast stores hit distinct banks.
-__device__ __forceinline__ void stage_slab(bool k_fast, const float (&v)[kTileLoads],
-                                           float (*s)[kTile + 1]) {
+  // load u: row index u / kKCols, k column u % kKCols (k-fast); k step u (row-fast)
+  __device__ __forceinline__ void fetch(const Operand &o, uint32_t k0, uint32_t kc,
+                                        float (&v)[kLoads]) const {
+    if constexpr (KFast) {
+      uint32_t koff[kKCols];
+      bool k_ok[kKCols];
 #pragma unroll
-  for (int u = 0; u < kTileLoads; ++u) {
-    int r, kk;
-    tile_coords(k_fast, threadIdx.x + u * 256, r, kk);
-    s[kk][r] = v[u];
+      for (int j = 0; j < kKCols; ++j) {
+        const uint32_t k = static_cast<uint32_t>(kk + j * kKStep);
+        k_ok[j] = k < kc;
+        koff[j] = axis_offset(o.k, k0 + k);
+      }
+#pragma unroll
+      for (int u = 0; u < kLoads; ++u) {
+        const int i = u / kKCols, j = u % kKCols;
+        const bool ok = k_ok[j] && ((row_ok >> i) & 1u);
+        v[u] = o.ptr[ok ? row_off[i] + koff[j] : 0];
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < kLoads; ++u) {
+        const uint32_t k = static_cast<uint32_t>(kk + u * kKStep);
+        const bool ok = (row_ok & 1u) && k < kc;
+        v[u] = o.ptr[ok ? row_off[0] + axis_offset(o.k, k0 + k) : 0];
+      }
+    }
   }
-}
+
+  // LDS rows padded to Tile + 1 floats: k-fast stores hit distinct banks.
+  __device__ __forceinline__ void stage(const float (&v)[kLoads], float (*s)[Tile + 1]) const {
+#pragma unroll
+    for (int u = 0; u < kLoads; ++u) {
+      if constexpr (KFast)
+        s[kk + (u % kKCols) * kKStep][r + (u / kKCols) * kRowStep] = v[u];
+      else
+        s[kk + u * kKStep][r] = v[u];
+    }
+  }
+};
 
 // C[m, n] = init[m] + sum_{k in chunk, ascending} A[m, k] * B[n, k]: one serial fp32 sum per
-// output (each product rounded, then added: -ffp-contract=off).
-__global__ __launch_bounds__(256) void pointwise_product_kernel(ProductArgs g) {
-  __shared__ float as[kSlab][kTile + 1];
-  __shared__ float bs[kSlab][kTile + 1];
-  const uint32_t m0 = blockIdx.y * kTile, n0 = blockIdx.x * kTile;
+// output (each product rounded, then added: -ffp-contract=off).  Within a slab the LDS reads
+// of the next group of kUnrollK steps are issued before the current group's arithmetic.
+template <int Tile, int Threads, bool AKFast, bool BKFast>
+__global__ __launch_bounds__(Threads) void pointwise_product_kernel(ProductArgs g) {
+  using S = TileShape<Tile, Threads>;
+  constexpr int kMicro = S::kMicro, kLoads = S::kLoads, kSlab = S::kSlab, kCols = S::kCols;
+  constexpr int U = kUnrollK;
+  // kSlab + U rows: the read-ahead of the group after a slab's last one stays in the buffer
+  __shared__ float as[kSlab + U][Tile + 1];
+  __shared__ float bs[kSlab + U][Tile + 1];
+  const uint32_t m0 = blockIdx.y * Tile, n0 = blockIdx.x * Tile;
   const uint32_t kb = blockIdx.z * g.k_chunk;
   const uint32_t ke = min(kb + g.k_chunk, g.K);
-  constexpr int kCols = kTile / kMicro;  // 16 x 16 threads
   const int tx = threadIdx.x % kCols, ty = threadIdx.x / kCols;
   float acc[kMicro][kMicro];
 #pragma unroll
@@ -345,41 +406,56 @@ __global__ __launch_bounds__(256) void pointwise_product_kernel(ProductArgs g) {
 #pragma unroll
     for (int j = 0; j < kMicro; ++j) acc[i][j] = v;
   }
-  float va[kTileLoads], vb[kTileLoads];
+  const SlabLoader<Tile, Threads, AKFast> la(g.a, m0, g.M);
+  const SlabLoader<Tile, Threads, BKFast> lb(g.b, n0, g.N);
+  float va[kLoads], vb[kLoads];
   if (kb < ke) {
     const uint32_t kc = min(ke - kb, static_cast<uint32_t>(kSlab));
-    fetch_slab(g.a, m0, g.M, kb, kc, va);
-    fetch_slab(g.b, n0, g.N, kb, kc, vb);
+    la.fetch(g.a, kb, kc, va);
+    lb.fetch(g.b, kb, kc, vb);
   }
+  float a0[U][kMicro], b0[U][kMicro], a1[U][kMicro], b1[U][kMicro];
+  auto read_group = [&](uint32_t k, float (&av)[U][kMicro], float (&bv)[U][kMicro]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+      for (int i = 0; i < kMicro; ++i) av[u][i] = as[k + u][ty * kMicro + i];
+#pragma unroll
+      for (int j = 0; j < kMicro; ++j) bv[u][j] = bs[k + u][tx * kMicro + j];
+    }
+  };
+  auto add_group = [&](const float (&av)[U][kMicro], const float (&bv)[U][kMicro]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int i = 0; i < kMicro; ++i)
+#pragma unroll
+        for (int j = 0; j < kMicro; ++j) acc[i][j] += av[u][i] * bv[u][j];
+  };
   for (uint32_t k0 = kb; k0 < ke; k0 += kSlab) {
     const uint32_t kc = min(ke - k0, static_cast<uint32_t>(kSlab));
-    stage_slab(g.a.k_fast, va, as);
-    stage_slab(g.b.k_fast, vb, bs);
+    la.stage(va, as);
+    lb.stage(vb, bs);
     __syncthreads();
     const uint32_t k1 = k0 + kSlab;
     if (k1 < ke) {  // the next slab's loads overlap this slab's arithmetic
       const uint32_t kc1 = min(ke - k1, static_cast<uint32_t>(kSlab));
-      fetch_slab(g.a, m0, g.M, k1, kc1, va);
-      fetch_slab(g.b, n0, g.N, k1, kc1, vb);
+      la.fetch(g.a, k1, kc1, va);
+      lb.fetch(g.b, k1, kc1, vb);
     }
-    // groups of kUnrollK steps: the LDS reads of a group are issued together, then each
-    // accumulator takes its products in ascending k
+    // whole groups, two per iteration so the read-ahead alternates register sets; every
+    // group read starts at a row <= kSlab
+    const uint32_t full = kc / U * U;
     uint32_t kk = 0;
-    for (; kk + kUnrollK <= kc; kk += kUnrollK) {
-      float av[kUnrollK][kMicro], bv[kUnrollK][kMicro];
-#pragma unroll
-      for (int u = 0; u < kUnrollK; ++u) {
-#pragma unroll
-        for (int i = 0; i < kMicro; ++i) av[u][i] = as[kk + u][ty * kMicro + i];
-#pragma unroll
-        for (int j = 0; j < kMicro; ++j) bv[u][j] = bs[kk + u][tx * kMicro + j];
-      }
-#pragma unroll
-      for (int u = 0; u < kUnrollK; ++u)
-#pragma unroll
-        for (int i = 0; i < kMicro; ++i)
-#pragma unroll
-          for (int j = 0; j < kMicro; ++j) acc[i][j] += av[u][i] * bv[u][j];
+    if (full > 0) read_group(0, a0, b0);
+    while (kk < full) {
+      read_group(kk + U, a1, b1);
+      add_group(a0, b0);
+      kk += U;
+      if (kk >= full) break;
+      read_group(kk + U, a0, b0);
+      add_group(a1, b1);
+      kk += U;
     }
     for (; kk < kc; ++kk) {
       float av[kMicro], bv[kMicro];
@@ -542,6 +618,7 @@ Operand operand(const float *ptr, Axis row, Axis k) {
   return Operand{ptr, row, k, unit_stride(k) <= unit_stride(row)};
 }
 
+
 // k chunks of the pointwise weight gradient: about 512 blocks in total, at least 64 k per
 // chunk, every chunk non-empty.
 struct KSplit {
@@ -562,10 +639,38 @@ KSplit product_split(const ConvGeom &g) {
   return KSplit{static_cast<uint32_t>((k + per - 1) / per), static_cast<uint32_t>(per)};
 }
 
+#ifndef OXH_TINY_TILE
+#define OXH_TINY_TILE 8  // small-grid tiling: 8 (8 x 8, 64 threads) or 16 (16 x 16, 256)
+#endif
+#ifndef OXH_SMALL_GRID
+#define OXH_SMALL_GRID 512  // below this many 32 x 32 blocks the small-grid tiling runs
+#endif
+constexpr uint64_t kSmallGrid = OXH_SMALL_GRID;
+
+template <int Tile, int Threads>
+void launch_tiled(hipStream_t s, const ProductArgs &a, uint32_t chunks) {
+  const dim3 grid((a.N + Tile - 1) / Tile, (a.M + Tile - 1) / Tile, chunks);
+  const dim3 block(Threads);
+  if (a.a.k_fast && a.b.k_fast)
+    oxh::launch(pointwise_product_kernel<Tile, Threads, true, true>, grid, block, 0, s, a);
+  else if (a.a.k_fast)
+    oxh::launch(pointwise_product_kernel<Tile, Threads, true, false>, grid, block, 0, s, a);
+  else if (a.b.k_fast)
+    oxh::launch(pointwise_product_kernel<Tile, Threads, false, true>, grid, block, 0, s, a);
+  else
+    oxh::launch(pointwise_product_kernel<Tile, Threads, false, false>, grid, block, 0, s, a);
+}
+
 oxh_status launch_product(const char *name, hipStream_t s, const ProductArgs &a,
                           uint32_t chunks) {
-  const dim3 grid((a.N + kTile - 1) / kTile, (a.M + kTile - 1) / kTile, chunks);
-  oxh::launch(pointwise_product_kernel, grid, dim3(256), 0, s, a);
+  const uint64_t big =
+      static_cast<uint64_t>((a.N + kTile - 1) / kTile) * ((a.M + kTile - 1) / kTile) * chunks;
+  if (big >= kSmallGrid)
+    launch_tiled<kTile, 256>(s, a, chunks);
+  else if (OXH_TINY_TILE == 8)
+    launch_tiled<8, 64>(s, a, chunks);
+  else
+    launch_tiled<16, 256>(s, a, chunks);
   return oxh::launched(name);
 }
 
