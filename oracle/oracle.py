@@ -267,6 +267,16 @@ def conv2d_backward(grad, x, weight, stride, padding, groups):
     return dx, dw, db
 
 
+def conv2d_bias_backward(grad):
+    """Bias gradient of a convolution with output gradient ``grad`` [n, c, h, w]: the dbias of
+    oro_conv2d_backward (evaluation of autograd.rs:412-527's bias sum), which does not depend
+    on the input or weights -- run on a 1x1, one-input-channel geometry of the same output."""
+    grad = _c(grad)
+    n, c, h, w = grad.shape
+    return conv2d_backward(grad, np.zeros((n, 1, h, w), np.float32),
+                           np.zeros((c, 1, 1, 1), np.float32), 1, 0, 1)[2]
+
+
 def avg_pool2d_forward(x, kernel, stride):
     x = _c(x)
     n, c, h, w = x.shape

@@ -740,12 +740,15 @@ __global__ __launch_bounds__(kRedBlock) void bn_channel_forward_kernel(
   }
 }
 
-template <bool Relu>
+// With DxSum, the block also sums the dx it writes (fp64, fixed order) into dx_sum[c]: the
+// bias gradient of a convolution whose output is this BatchNorm's input (autograd.rs:412-527
+// reduces the same values over (n, y, x) in a pass of its own).
+template <bool Relu, bool DxSum>
 __global__ __launch_bounds__(kRedBlock) void bn_channel_backward_kernel(
     ChannelGeom g, const float *__restrict__ grad, const float *__restrict__ relu_out,
     const float *__restrict__ x, const float *__restrict__ weight, const float *__restrict__ mean,
     const float *__restrict__ inverse_std, float *__restrict__ dx, float *__restrict__ dweight,
-    float *__restrict__ dbias) {
+    float *__restrict__ dbias, float *__restrict__ dx_sum) {
   __shared__ double lds[2][kRedWaves];
   __shared__ float sums[2];
   const uint32_t c = blockIdx.x;
@@ -770,13 +773,40 @@ __global__ __launch_bounds__(kRedBlock) void bn_channel_backward_kernel(
   // autograd.rs:344-373: ((w * inv) / M) * ((M * g - sum_g) - x_hat * sum_g_xhat)
   const float samples = static_cast<float>(g.samples);
   const float coef = weight[c] * inv / samples, sgf = sums[0], sgxf = sums[1];
+  double total = 0.0, unused = 0.0;
   for (uint32_t j = threadIdx.x; j < g.samples; j += kRedBlock) {
     const uint32_t idx = channel_index(g, c, j);
     float gv = grad[idx];
     if constexpr (Relu) gv = relu_masked(gv, relu_out[idx]);
     const float normalized = (x[idx] - mu) * inv;
-    dx[idx] = coef * (samples * gv - sgf - normalized * sgxf);
+    const float d = coef * (samples * gv - sgf - normalized * sgxf);
+    dx[idx] = d;
+    if constexpr (DxSum) total += static_cast<double>(d);
   }
+  if constexpr (DxSum) {
+    block_sum2(total, unused, lds);  // lds is free again: sums[] was read after a barrier
+    if (threadIdx.x == 0) dx_sum[c] = static_cast<float>(total);
+  }
+}
+
+// Per-channel sum of an NCHW tensor (fp64, fixed order): one block per channel.  The dx sum of
+// the planes the one-block-per-channel backward does not take.
+__global__ __launch_bounds__(kRedBlock) void bn_channel_sum_kernel(uint32_t channels,
+                                                                   uint32_t spatial,
+                                                                   uint32_t samples,
+                                                                   oxh::FastDiv spatial_div,
+                                                                   const float *__restrict__ v,
+                                                                   float *__restrict__ out) {
+  __shared__ double lds[2][kRedWaves];
+  const uint32_t c = blockIdx.x;
+  double total = 0.0, unused = 0.0;
+  for (uint32_t j = threadIdx.x; j < samples; j += kRedBlock) {
+    const uint32_t n = oxh::fast_div(j, spatial_div);
+    total += static_cast<double>(
+        v[(static_cast<uint64_t>(n) * channels + c) * spatial + (j - n * spatial)]);
+  }
+  block_sum2(total, unused, lds);
+  if (threadIdx.x == 0) out[c] = static_cast<float>(total);
 }
 
 __global__ void bn_update_running_kernel(uint32_t channels, float momentum,
@@ -1067,16 +1097,26 @@ oxh_status backward_train_impl(const char *name, oxh_stream stream, uint64_t bat
                                const float *relu_out, const float *input, const float *weight,
                                const float *saved_mean, const float *saved_inverse_std,
                                float *input_gradient, float *weight_gradient,
-                               float *bias_gradient, void *workspace,
+                               float *bias_gradient, float *input_gradient_sum, void *workspace,
                                uint64_t workspace_bytes) {
   if (!use_channel(batch, channels, spatial)) {
     oxh_status st = launch_reduce_gx(name, stream, batch, channels, spatial, gradient, relu_out,
                                      input, saved_mean, saved_inverse_std, workspace,
                                      workspace_bytes, nullptr);
     if (st != OXH_OK) return st;
-    return backward_input_impl(name, stream, batch, channels, spatial, gradient, relu_out, input,
-                               weight, saved_mean, saved_inverse_std, input_gradient,
-                               weight_gradient, bias_gradient, workspace, workspace_bytes);
+    st = backward_input_impl(name, stream, batch, channels, spatial, gradient, relu_out, input,
+                             weight, saved_mean, saved_inverse_std, input_gradient,
+                             weight_gradient, bias_gradient, workspace, workspace_bytes);
+    if (st != OXH_OK || input_gradient_sum == nullptr) return st;
+    const uint64_t samples = batch * spatial;
+    OXH_REQUIRE(samples < (1ull << 31), OXH_INVALID_SHAPE,
+                std::string(name) + ": more than 2^31 values per channel");
+    oxh::launch(bn_channel_sum_kernel, dim3(static_cast<uint32_t>(channels)), dim3(kRedBlock), 0,
+                oxh::as_stream(stream), static_cast<uint32_t>(channels),
+                static_cast<uint32_t>(spatial), static_cast<uint32_t>(samples),
+                oxh::make_fastdiv(static_cast<uint32_t>(spatial)),
+                static_cast<const float *>(input_gradient), input_gradient_sum);
+    return oxh::launched(name);
   }
   oxh_status st = check_shape(name, batch, channels, spatial);
   if (st != OXH_OK) return st;
@@ -1090,14 +1130,13 @@ oxh_status backward_train_impl(const char *name, oxh_stream stream, uint64_t bat
   st = no_overlap(name, input_gradient, bytes, {input, gradient, relu_out}, bytes);
   if (st != OXH_OK) return st;
   const ChannelGeom cg = make_channel_geom(batch, channels, spatial);
-  if (relu_out)
-    oxh::launch(bn_channel_backward_kernel<true>, dim3(cg.channels), dim3(kRedBlock), 0,
-                oxh::as_stream(stream), cg, gradient, relu_out, input, weight, saved_mean,
-                saved_inverse_std, input_gradient, weight_gradient, bias_gradient);
-  else
-    oxh::launch(bn_channel_backward_kernel<false>, dim3(cg.channels), dim3(kRedBlock), 0,
-                oxh::as_stream(stream), cg, gradient, relu_out, input, weight, saved_mean,
-                saved_inverse_std, input_gradient, weight_gradient, bias_gradient);
+  auto kernel = relu_out ? (input_gradient_sum ? bn_channel_backward_kernel<true, true>
+                                               : bn_channel_backward_kernel<true, false>)
+                         : (input_gradient_sum ? bn_channel_backward_kernel<false, true>
+                                               : bn_channel_backward_kernel<false, false>);
+  oxh::launch(kernel, dim3(cg.channels), dim3(kRedBlock), 0, oxh::as_stream(stream), cg,
+              gradient, relu_out, input, weight, saved_mean, saved_inverse_std, input_gradient,
+              weight_gradient, bias_gradient, input_gradient_sum);
   return oxh::launched(name);
 }
 
@@ -1293,7 +1332,7 @@ oxh_status oxh_batch_norm_backward_train(oxh_stream stream, uint64_t batch, uint
                                          void *workspace, uint64_t workspace_bytes) {
   return backward_train_impl("oxh_batch_norm_backward_train", stream, batch, channels, spatial,
                              gradient, nullptr, input, weight, saved_mean, saved_inverse_std,
-                             input_gradient, weight_gradient, bias_gradient, workspace,
+                             input_gradient, weight_gradient, bias_gradient, nullptr, workspace,
                              workspace_bytes);
 }
 
@@ -1325,7 +1364,22 @@ oxh_status oxh_batch_norm_relu_backward_train(oxh_stream stream, uint64_t batch,
   return backward_train_impl("oxh_batch_norm_relu_backward_train", stream, batch, channels,
                              spatial, gradient, output, input, weight, saved_mean,
                              saved_inverse_std, input_gradient, weight_gradient, bias_gradient,
-                             workspace, workspace_bytes);
+                             nullptr, workspace, workspace_bytes);
+}
+
+oxh_status oxh_conv_batch_norm_backward_train(
+    oxh_stream stream, uint64_t batch, uint64_t channels, uint64_t spatial,
+    const float *gradient, const float *relu_output, const float *input, const float *weight,
+    const float *saved_mean, const float *saved_inverse_std, float *input_gradient,
+    float *weight_gradient, float *bias_gradient, float *conv_bias_gradient, void *workspace,
+    uint64_t workspace_bytes) {
+  const char *name = "oxh_conv_batch_norm_backward_train";
+  OXH_REQUIRE(conv_bias_gradient != nullptr, OXH_INVALID_SHAPE,
+              std::string(name) + ": null conv_bias_gradient");
+  return backward_train_impl(name, stream, batch, channels, spatial, gradient, relu_output,
+                             input, weight, saved_mean, saved_inverse_std, input_gradient,
+                             weight_gradient, bias_gradient, conv_bias_gradient, workspace,
+                             workspace_bytes);
 }
 
 }  // extern "C"

@@ -656,6 +656,7 @@ oxh_status build_trainer(oxh_trainer &t) {
   const uint64_t wsb = t.workspace_bytes;
   auto name = [](const char *p, size_t i) { return std::string(p) + std::to_string(i); };
   std::vector<char> written(n, 0);
+  std::vector<char> conv_bias_done(n, 0);  // conv nodes whose bias gradient a BN backward forms
   // Where a contribution to node x's gradient goes: its buffer (first) or the scratch buffer
   // added into it afterwards.
   auto contribution = [&](int x, float *&dst, float *&acc) {
@@ -850,6 +851,15 @@ oxh_status build_trainer(oxh_trainer &t) {
         contribution(bn.in[1], dg, unused);
         contribution(bn.in[2], db, unused);
         contribution(xin, dst, acc);
+        // a convolution whose only consumer is this BN: its output gradient is this dx, whose
+        // per-channel sum (the convolution's bias gradient) the BN backward forms in passing
+        float *conv_db = nullptr;
+        const Node &src = g.nodes[xin];
+        if (src.op == Op::Conv && consumers[xin] == 1 && acc == nullptr &&
+            !written[src.in[2]]) {
+          contribution(src.in[2], conv_db, unused);
+          conv_bias_done[xin] = 1;
+        }
         const uint64_t N = bn.shape[0], C = bn.shape[1], HW = bn.shape[2] * bn.shape[3];
         op.kind = fused ? "batch_norm2d_relu_backward" : "batch_norm2d_backward";
         op.name = (fused ? name("bn", bi) + "+" + name("relu", r) : name("bn", bi)) + ".backward";
@@ -862,7 +872,11 @@ oxh_status build_trainer(oxh_trainer &t) {
         op.tensors.push_back(ref("contribution", dst, g.nodes[xin], 1));
         op.tensors.push_back(ref_flat("weight_gradient", dg, C, 1));
         op.tensors.push_back(ref_flat("bias_gradient", db, C, 1));
+        if (conv_db) op.tensors.push_back(ref_flat("conv_bias_gradient", conv_db, C, 1));
         emit(std::move(op), acc, g.nodes[xin], [=](hipStream_t st) {
+          if (conv_db)
+            return oxh_conv_batch_norm_backward_train(st, N, C, HW, gr, y, xi, w, sm, si, dst,
+                                                      dg, db, conv_db, ws, wsb);
           return fused ? oxh_batch_norm_relu_backward_train(st, N, C, HW, gr, y, xi, w, sm, si,
                                                             dst, dg, db, ws, wsb)
                        : oxh_batch_norm_backward_train(st, N, C, HW, gr, xi, w, sm, si, dst, dg,
@@ -914,21 +928,22 @@ oxh_status build_trainer(oxh_trainer &t) {
         const oxh_conv2d_shape s = conv_shape(g, x);
         const int xin = x.in[0];
         const float *xi = t.value[xin], *w = t.value[x.in[1]];
-        float *dw, *db, *unused;
+        float *dw, *db = nullptr, *unused;
         contribution(x.in[1], dw, unused);
-        contribution(x.in[2], db, unused);
+        const bool bias_here = !conv_bias_done[r];  // else the following BN formed it
+        if (bias_here) contribution(x.in[2], db, unused);
         OpRec p;
         p.kind = "conv2d_parameter_backward";
         p.name = name("conv", r) + ".backward_parameters";
         p.tensors = {ref("gradient", const_cast<float *>(gr), x, 0),
                      ref("x", const_cast<float *>(xi), g.nodes[xin], 0),
                      ref("weight", const_cast<float *>(w), g.nodes[x.in[1]], 0),
-                     ref("weight_gradient", dw, g.nodes[x.in[1]], 1),
-                     ref("bias_gradient", db, g.nodes[x.in[2]], 1)};
+                     ref("weight_gradient", dw, g.nodes[x.in[1]], 1)};
+        if (bias_here) p.tensors.push_back(ref("bias_gradient", db, g.nodes[x.in[2]], 1));
         p.attrs = conv_attrs(x);
         p.launch = [s, gr, xi, dw, db, ws, wsb](hipStream_t st) {
           oxh_status e = oxh_conv2d_weight_backward(st, &s, gr, xi, dw, ws, wsb);
-          if (e != OXH_OK) return e;
+          if (e != OXH_OK || db == nullptr) return e;
           return oxh_conv2d_bias_backward(st, &s, gr, db, ws, wsb);
         };
         ops.push_back(std::move(p));

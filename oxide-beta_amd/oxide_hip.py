@@ -135,6 +135,8 @@ _SIGNATURES = {
                                                 _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u64]),
     "oxh_batch_norm_relu_backward_train": (_st, [_vp, _u64, _u64, _u64, _vp, _vp, _vp, _vp, _vp,
                                                  _vp, _vp, _vp, _vp, _vp, _u64]),
+    "oxh_conv_batch_norm_backward_train": (_st, [_vp, _u64, _u64, _u64, _vp, _vp, _vp, _vp, _vp,
+                                                 _vp, _vp, _vp, _vp, _vp, _vp, _u64]),
     "oxh_cross_entropy_workspace_size": (_st, [_u64, _u64, ctypes.POINTER(_u64)]),
     "oxh_cross_entropy_forward": (_st, [_vp, _u64, _u64, _vp, _vp, _vp, _vp, _vp, _u64]),
     "oxh_cross_entropy_backward": (_st, [_vp, _u64, _u64, _vp, _vp, _vp, _vp, _vp]),
@@ -573,6 +575,19 @@ class LoadedModule:
             _stream(stream), n, c, h * w, _ptr(gradient), _ptr(out), _ptr(x), _ptr(weight),
             _ptr(saved_mean), _ptr(saved_inverse_std), _ptr(input_gradient),
             _ptr(weight_gradient), _ptr(bias_gradient), ws, wsb))
+
+    def conv_batch_norm_backward_train(self, gradient, relu_out, x, weight, saved_mean,
+                                       saved_inverse_std, input_gradient, weight_gradient,
+                                       bias_gradient, conv_bias_gradient, stream=None):
+        """BatchNorm training backward (through the following ReLU when ``relu_out`` is not
+        None) that also writes the per-channel sum of ``input_gradient``: the bias gradient of
+        the convolution producing ``x``."""
+        n, c, h, w = x.shape
+        ws, wsb = self._bn_ws_args(n, c, h * w)
+        check(lib().oxh_conv_batch_norm_backward_train(
+            _stream(stream), n, c, h * w, _ptr(gradient), _ptr(relu_out), _ptr(x),
+            _ptr(weight), _ptr(saved_mean), _ptr(saved_inverse_std), _ptr(input_gradient),
+            _ptr(weight_gradient), _ptr(bias_gradient), _ptr(conv_bias_gradient), ws, wsb))
 
     # -- cross entropy (kernel_module.rs:966-1050)
     def cross_entropy_forward(self, batch, classes, logits, targets, loss, error_flag=None,

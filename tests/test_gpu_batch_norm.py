@@ -17,6 +17,7 @@ import pytest
 import torch
 
 import oracle
+import oxide_hip as ox
 from helpers import (assert_close, assert_within, check_batch_norm_backward,
                      check_batch_norm_forward, host, strict_ok, to_dev)
 
@@ -242,3 +243,42 @@ def test_batch_norm_relu_fused_matches_unfused(module, dev, shape):
     np.testing.assert_array_equal(host(g_masked), gm)
     check_batch_norm_backward(dict(dx=host(gx1), dw=host(gw1), db=host(gb1)), gm, x, gamma,
                               host(m1), host(i1))
+
+
+@pytest.mark.parametrize("shape", [(2, 3, 4, 4), (128, 96, 2, 2), (128, 1280, 1, 1),
+                                   (128, 32, 14, 14), (3, 5, 3, 3)])
+@pytest.mark.parametrize("relu", [False, True])
+def test_conv_batch_norm_backward_writes_conv_bias(module, dev, shape, relu):
+    """The BatchNorm backward that also reduces its input gradient per channel (the bias
+    gradient of the convolution feeding it): BatchNorm outputs bit-equal to the plain entry
+    point's, on the one-block-per-channel path and the reduce + map path (14 x 14); the
+    convolution bias gradient against the oracle's conv2d bias sum over that input gradient
+    (|d| <= 1e-5 * sum|terms|: fp64 block sums against the CPU's fp32 running sum)."""
+    r = np.random.default_rng(hash((shape, relu)) & 0xFFFF)
+    x, gamma, beta, g = _case(r, shape, 1.3, 0.2)
+    c = shape[1]
+    dx_, dw_, dg_ = to_dev(x, dev), to_dev(gamma, dev), to_dev(g, dev)
+    mean = to_dev(r.standard_normal(c).astype(np.float32) * 0.1, dev)
+    inv = to_dev(r.uniform(0.5, 2.0, c).astype(np.float32), dev)
+    y = to_dev(np.maximum(r.standard_normal(shape).astype(np.float32), 0), dev) if relu else None
+
+    def outs():
+        return (torch.empty_like(dx_), torch.empty(c, device=dev), torch.empty(c, device=dev))
+
+    gx1, gw1, gb1 = outs()
+    if relu:
+        module.batch_norm_relu_backward_train(dg_, y, dx_, dw_, mean, inv, gx1, gw1, gb1)
+    else:
+        module.batch_norm_backward_train(dg_, dx_, dw_, mean, inv, gx1, gw1, gb1)
+    gx2, gw2, gb2 = outs()
+    conv_bias = torch.full((c,), float("nan"), device=dev)
+    module.conv_batch_norm_backward_train(dg_, y, dx_, dw_, mean, inv, gx2, gw2, gb2, conv_bias)
+    torch.cuda.synchronize()
+    for a, b, what in ((gx2, gx1, "dx"), (gw2, gw1, "dw"), (gb2, gb1, "db")):
+        np.testing.assert_array_equal(host(a), host(b), err_msg=what)
+    dx = host(gx2)
+    assert_within(host(conv_bias), oracle.conv2d_bias_backward(dx),
+                  1e-5 * np.abs(dx).astype(np.float64).sum(axis=(0, 2, 3)) + 1e-7, "conv bias")
+    with pytest.raises(ox.OxideError) as e:
+        module.conv_batch_norm_backward_train(dg_, y, dx_, dw_, mean, inv, gx2, gw2, gb2, None)
+    assert e.value.status == ox.INVALID_SHAPE

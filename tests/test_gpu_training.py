@@ -72,9 +72,22 @@ class OracleChecker:
                                         a["padding"], a["groups"])[1]
         assert_within(host(op.writes["weight_gradient"]), rdw,
                       1e-5 * abs_dw.astype(np.float64) + 1e-7, f"{op.name} weight")
-        assert_within(host(op.writes["bias_gradient"]), rdb,
-                      1e-5 * np.abs(g).astype(np.float64).sum(axis=(0, 2, 3)) + 1e-7,
-                      f"{op.name} bias")
+        if "bias_gradient" in op.writes:  # else the following BatchNorm's backward formed it
+            assert_within(host(op.writes["bias_gradient"]), rdb,
+                          1e-5 * np.abs(g).astype(np.float64).sum(axis=(0, 2, 3)) + 1e-7,
+                          f"{op.name} bias")
+            self.counts["conv bias in parameter backward"] += 1
+
+    def _conv_bias(self, op):
+        """The bias gradient of the convolution feeding a BatchNorm, formed by the BN backward
+        from the input gradient it wrote."""
+        if "conv_bias_gradient" not in op.writes:
+            return
+        dx = host(op.writes["contribution"])
+        assert_within(host(op.writes["conv_bias_gradient"]), oracle.conv2d_bias_backward(dx),
+                      1e-5 * np.abs(dx).astype(np.float64).sum(axis=(0, 2, 3)) + 1e-7,
+                      f"{op.name} conv bias")
+        self.counts["conv bias in batch norm backward"] += 1
 
     def batch_norm2d_forward(self, op, r):
         a, w = op.attrs, op.writes
@@ -91,6 +104,7 @@ class OracleChecker:
                    db=host(w["bias_gradient"]))
         check_batch_norm_backward(out, r["gradient"], r["x"], r["weight"], r["saved_mean"],
                                   r["saved_inverse_std"])
+        self._conv_bias(op)
 
     def batch_norm2d_relu_forward(self, op, r):
         a, w = op.attrs, op.writes
@@ -109,6 +123,7 @@ class OracleChecker:
         masked = oracle.relu_backward(r["gradient"], r["y"])
         check_batch_norm_backward(out, masked, r["x"], r["weight"], r["saved_mean"],
                                   r["saved_inverse_std"])
+        self._conv_bias(op)
 
     def relu_forward(self, op, r):
         assert_bitexact(host(op.writes["y"]), oracle.relu(r["x"]), op.name)
@@ -157,14 +172,16 @@ class OracleChecker:
             assert_bitexact(host(v), rv, f"adamw second moment {i}")
 
 
-# 46 BatchNorms, 32 of them followed by a ReLU (fused); 10 residual adds, whose first operand's
-# gradient is the add's own buffer (no launch)
+# 46 BatchNorms, 32 of them followed by a ReLU (fused), each fed by a convolution whose bias
+# gradient its backward forms (the classifier's, fed by no BN, stays with its parameter
+# backward); 10 residual adds, whose first operand's gradient is the add's own buffer (no launch)
 EXPECTED_KINDS = {"conv2d_forward": 47, "conv2d_parameter_backward": 47,
                   "conv2d_input_backward": 46, "batch_norm2d_forward": 14,
                   "batch_norm2d_relu_forward": 32, "batch_norm2d_backward": 14,
                   "batch_norm2d_relu_backward": 32, "add_forward": 10, "add_backward": 10,
                   "avg_pool2d_forward": 1, "avg_pool2d_backward": 1, "cross_entropy": 1,
-                  "adamw": 1}
+                  "adamw": 1, "conv bias in parameter backward": 1,
+                  "conv bias in batch norm backward": 46}
 
 
 def test_config5_step_every_op_matches_oracle():
