@@ -97,9 +97,11 @@ __global__ __launch_bounds__(256) void conv2d_forward_kernel(ConvGeom g, uint32_
 }
 
 // One thread per input element; contributions in (oc, oy, ox) ascending order.
+// addend (may be null, may equal dx): dx = sum + addend[i], the gradient accumulation of a
+// tensor with a second consumer done in the same pass (the sum is complete before the add).
 __global__ __launch_bounds__(256) void conv2d_input_backward_kernel(
     ConvGeom g, uint32_t total, const float *__restrict__ grad, const float *__restrict__ wt,
-    float *__restrict__ dx) {
+    const float *addend, float *dx) {
   for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < total; i += gridDim.x * 256) {
     const uint32_t t0 = fdiv(i, g.w_div), ix = i - t0 * g.w;
     const uint32_t t1 = fdiv(t0, g.h_div), iy = t0 - t1 * g.h;
@@ -125,7 +127,7 @@ __global__ __launch_bounds__(256) void conv2d_input_backward_kernel(
         for (int ox = ox0; ox <= ox1; ++ox) acc += gr[ox] * wr[-ox * s];
       }
     }
-    dx[i] = acc;
+    dx[i] = addend != nullptr ? acc + addend[i] : acc;
   }
 }
 
@@ -287,6 +289,7 @@ struct ProductArgs {
   Axis cm, cn;
   uint32_t c_chunk;
   const float *init;  // initial value per m (the bias), or null for 0
+  const float *addend;  // added to each finished sum (indexed as c; one chunk only), or null
   uint32_t M, N, K, k_chunk;
 };
 
@@ -478,7 +481,9 @@ __global__ __launch_bounds__(Threads) void pointwise_product_kernel(ProductArgs 
 #pragma unroll
     for (int j = 0; j < kMicro; ++j) {
       const uint32_t n = n0 + tx * kMicro + j;
-      if (n < g.N) c[axis_offset(g.cm, m) + axis_offset(g.cn, n)] = acc[i][j];
+      if (n >= g.N) continue;
+      const uint32_t idx = axis_offset(g.cm, m) + axis_offset(g.cn, n);
+      c[idx] = g.addend != nullptr ? acc[i][j] + g.addend[idx] : acc[i][j];
     }
   }
 }
@@ -733,6 +738,39 @@ oxh_status make_pool_geom(const char *name, const oxh_pool2d_shape *s, PoolGeom 
   return oxh::ok();
 }
 
+oxh_status input_backward_impl(const char *name, oxh_stream stream,
+                               const oxh_conv2d_shape *shape, const float *gradient,
+                               const float *weight, const float *addend,
+                               float *input_gradient) {
+  ConvGeom g;
+  oxh_status st = make_conv_geom(name, shape, g);
+  if (st != OXH_OK) return st;
+  OXH_REQUIRE(gradient && weight && input_gradient, OXH_INVALID_SHAPE,
+              std::string(name) + ": null pointer");
+  const uint64_t in_n = input_elems(g);
+  hipStream_t s = oxh::as_stream(stream);
+  if (pointwise(g)) {
+    // dX[ic, (n, p)] = 0 + sum_oc W[oc, ic] G[(n, p), oc]
+    const uint32_t plane = g.h * g.w;
+    ProductArgs a{};
+    a.a = operand(weight, linear(1), linear(g.in_c));
+    a.b = operand(gradient, batch_plane(plane, g.out_c), linear(plane));
+    a.c = input_gradient;
+    a.cm = linear(plane);
+    a.cn = batch_plane(plane, g.in_c);
+    a.init = nullptr;
+    a.addend = addend;
+    a.M = g.in_c;
+    a.N = g.batch * plane;
+    a.K = g.out_c;
+    a.k_chunk = a.K;
+    return launch_product(name, s, a, 1);
+  }
+  oxh::launch(conv2d_input_backward_kernel, dim3(grid_for(in_n)), dim3(256), 0, s, g,
+              static_cast<uint32_t>(in_n), gradient, weight, addend, input_gradient);
+  return oxh::launched(name);
+}
+
 }  // namespace
 
 extern "C" {
@@ -785,33 +823,17 @@ oxh_status oxh_conv2d_forward(oxh_stream stream, const oxh_conv2d_shape *shape,
 oxh_status oxh_conv2d_input_backward(oxh_stream stream, const oxh_conv2d_shape *shape,
                                      const float *gradient, const float *weight,
                                      float *input_gradient) {
-  const char *name = "oxh_conv2d_input_backward";
-  ConvGeom g;
-  oxh_status st = make_conv_geom(name, shape, g);
-  if (st != OXH_OK) return st;
-  OXH_REQUIRE(gradient && weight && input_gradient, OXH_INVALID_SHAPE,
-              std::string(name) + ": null pointer");
-  const uint64_t in_n = input_elems(g);
-  hipStream_t s = oxh::as_stream(stream);
-  if (pointwise(g)) {
-    // dX[ic, (n, p)] = 0 + sum_oc W[oc, ic] G[(n, p), oc]
-    const uint32_t plane = g.h * g.w;
-    ProductArgs a{};
-    a.a = operand(weight, linear(1), linear(g.in_c));
-    a.b = operand(gradient, batch_plane(plane, g.out_c), linear(plane));
-    a.c = input_gradient;
-    a.cm = linear(plane);
-    a.cn = batch_plane(plane, g.in_c);
-    a.init = nullptr;
-    a.M = g.in_c;
-    a.N = g.batch * plane;
-    a.K = g.out_c;
-    a.k_chunk = a.K;
-    return launch_product(name, s, a, 1);
-  }
-  oxh::launch(conv2d_input_backward_kernel, dim3(grid_for(in_n)), dim3(256), 0, s, g,
-              static_cast<uint32_t>(in_n), gradient, weight, input_gradient);
-  return oxh::launched(name);
+  return input_backward_impl("oxh_conv2d_input_backward", stream, shape, gradient, weight,
+                             nullptr, input_gradient);
+}
+
+oxh_status oxh_conv2d_input_backward_accumulate(oxh_stream stream,
+                                                const oxh_conv2d_shape *shape,
+                                                const float *gradient, const float *weight,
+                                                const float *addend, float *input_gradient) {
+  const char *name = "oxh_conv2d_input_backward_accumulate";
+  OXH_REQUIRE(addend != nullptr, OXH_INVALID_SHAPE, std::string(name) + ": null addend");
+  return input_backward_impl(name, stream, shape, gradient, weight, addend, input_gradient);
 }
 
 oxh_status oxh_conv2d_weight_backward_workspace_size(const oxh_conv2d_shape *shape,

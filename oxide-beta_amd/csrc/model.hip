@@ -657,9 +657,37 @@ oxh_status build_trainer(oxh_trainer &t) {
   auto name = [](const char *p, size_t i) { return std::string(p) + std::to_string(i); };
   std::vector<char> written(n, 0);
   std::vector<char> conv_bias_done(n, 0);  // conv nodes whose bias gradient a BN backward forms
+  // A residual add's gradient handed to its non-aliased operand waits here and is added by
+  // that operand's next contribution in the same pass (a convolution's input backward) rather
+  // than copied into its buffer first; anything else flushes it as the copy.
+  struct Pending {
+    const float *gradient = nullptr;
+    std::string name;
+    int add = -1;
+  };
+  std::vector<Pending> pending(n);
+  auto flush = [&](int x) {
+    if (pending[x].gradient == nullptr) return;
+    const Pending p = pending[x];
+    pending[x] = Pending{};
+    written[x] = 1;
+    float *dst = t.grad[x];
+    const uint64_t bytes = node_bytes(g.nodes[x]);
+    OpRec c;
+    c.kind = "add_backward";
+    c.name = p.name;
+    c.tensors = {ref("gradient", const_cast<float *>(p.gradient), g.nodes[p.add], 0),
+                 ref("contribution", dst, g.nodes[x], 1)};
+    const float *gr = p.gradient;
+    c.launch = [dst, gr, bytes](hipStream_t st) {
+      return oxh_memcpy_d2d_async(dst, gr, bytes, st);
+    };
+    ops.push_back(std::move(c));
+  };
   // Where a contribution to node x's gradient goes: its buffer (first) or the scratch buffer
   // added into it afterwards.
   auto contribution = [&](int x, float *&dst, float *&acc) {
+    flush(x);
     if (!written[x]) {
       written[x] = 1;
       dst = t.grad[x];
@@ -813,6 +841,7 @@ oxh_status build_trainer(oxh_trainer &t) {
     if (x.op == Op::Param || x.op == Op::Input || x.op == Op::Targets ||
         x.op == Op::CrossEntropy || fused_bn[r])
       continue;
+    flush(static_cast<int>(r));  // a gradient still waiting for a second contribution
     OXH_REQUIRE(written[r], OXH_TRACE, "a traced value receives no gradient");
     const float *gr = t.grad[r];
     OpRec op;
@@ -891,12 +920,17 @@ oxh_status build_trainer(oxh_trainer &t) {
             written[inp] = 1;  // the add's gradient buffer is its own
             continue;
           }
+          const std::string cname = name("add", r) + ".backward" + std::to_string(k);
+          if (!written[inp] && pending[inp].gradient == nullptr) {
+            pending[inp] = Pending{gr, cname, static_cast<int>(r)};
+            continue;
+          }
           float *dst, *acc;
           contribution(inp, dst, acc);
           const uint64_t bytes = node_bytes(x);
           OpRec c;
           c.kind = "add_backward";
-          c.name = name("add", r) + ".backward" + std::to_string(k);
+          c.name = cname;
           c.tensors = {ref("gradient", const_cast<float *>(gr), x, 0),
                        ref("contribution", dst, g.nodes[inp], 1)};
           emit(std::move(c), acc, g.nodes[inp], [dst, gr, bytes](hipStream_t st) {
@@ -949,16 +983,28 @@ oxh_status build_trainer(oxh_trainer &t) {
         ops.push_back(std::move(p));
         if (g.nodes[xin].op == Op::Input) break;  // the network input needs no gradient
         float *dst, *acc;
-        contribution(xin, dst, acc);
+        const float *addend = nullptr;
+        if (pending[xin].gradient != nullptr && !written[xin]) {
+          addend = pending[xin].gradient;
+          op.tensors.push_back(ref("addend", const_cast<float *>(addend),
+                                   g.nodes[pending[xin].add], 0));
+          pending[xin] = Pending{};
+          written[xin] = 1;
+          dst = t.grad[xin];
+          acc = nullptr;
+        } else {
+          contribution(xin, dst, acc);
+        }
         op.kind = "conv2d_input_backward";
         op.name = name("conv", r) + ".backward_input";
-        op.tensors = {ref("gradient", const_cast<float *>(gr), x, 0),
-                      ref("x", const_cast<float *>(xi), g.nodes[xin], 0),
-                      ref("weight", const_cast<float *>(w), g.nodes[x.in[1]], 0),
-                      ref("contribution", dst, g.nodes[xin], 1)};
+        op.tensors.push_back(ref("gradient", const_cast<float *>(gr), x, 0));
+        op.tensors.push_back(ref("x", const_cast<float *>(xi), g.nodes[xin], 0));
+        op.tensors.push_back(ref("weight", const_cast<float *>(w), g.nodes[x.in[1]], 0));
+        op.tensors.push_back(ref("contribution", dst, g.nodes[xin], 1));
         op.attrs = conv_attrs(x);
-        emit(std::move(op), acc, g.nodes[xin], [s, gr, w, dst](hipStream_t st) {
-          return oxh_conv2d_input_backward(st, &s, gr, w, dst);
+        emit(std::move(op), acc, g.nodes[xin], [s, gr, w, addend, dst](hipStream_t st) {
+          return addend ? oxh_conv2d_input_backward_accumulate(st, &s, gr, w, addend, dst)
+                        : oxh_conv2d_input_backward(st, &s, gr, w, dst);
         });
         break;
       }
@@ -966,6 +1012,8 @@ oxh_status build_trainer(oxh_trainer &t) {
         return oxh::fail(OXH_TRACE, "no backward for a traced node");
     }
   }
+
+  for (size_t i = 0; i < n; ++i) flush(static_cast<int>(i));
 
   // AdamW over every parameter (visit order)
   t.adam.clear();

@@ -153,6 +153,7 @@ _SIGNATURES = {
     "oxh_conv2d_output_size": (_st, [_CS, ctypes.POINTER(_u64), ctypes.POINTER(_u64)]),
     "oxh_conv2d_forward": (_st, [_vp, _CS, _vp, _vp, _vp, _vp]),
     "oxh_conv2d_input_backward": (_st, [_vp, _CS, _vp, _vp, _vp]),
+    "oxh_conv2d_input_backward_accumulate": (_st, [_vp, _CS, _vp, _vp, _vp, _vp]),
     "oxh_conv2d_weight_backward_workspace_size": (_st, [_CS, ctypes.POINTER(_u64)]),
     "oxh_conv2d_weight_backward": (_st, [_vp, _CS, _vp, _vp, _vp, _vp, _u64]),
     "oxh_conv2d_bias_backward": (_st, [_vp, _CS, _vp, _vp, _vp, _u64]),
@@ -651,6 +652,13 @@ class LoadedModule:
         check(lib().oxh_conv2d_input_backward(_stream(stream), ctypes.byref(shape),
                                               _ptr(gradient), _ptr(weight),
                                               _ptr(input_gradient)))
+
+    def conv2d_input_backward_accumulate(self, shape, gradient, weight, addend, input_gradient,
+                                         stream=None):
+        """input_gradient = conv2d input backward + addend (gradient accumulation)."""
+        check(lib().oxh_conv2d_input_backward_accumulate(_stream(stream), ctypes.byref(shape),
+                                                         _ptr(gradient), _ptr(weight),
+                                                         _ptr(addend), _ptr(input_gradient)))
 
     def conv2d_weight_backward(self, shape, gradient, x, weight_gradient, stream=None):
         ws, wsb = self._conv_ws.ptr_bytes(conv2d_workspace_size(shape))

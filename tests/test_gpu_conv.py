@@ -65,6 +65,32 @@ def test_conv2d_matches_oracle(module, dev, case):
                   "bias gradient")
 
 
+@pytest.mark.parametrize("case", [(2, 64, 4, 4, 64, 5, 1, 64), (3, 12, 6, 5, 8, 3, 1, 4),
+                                  (4, 96, 2, 2, 192, 1, 1, 1), (128, 64, 8, 8, 256, 1, 1, 1),
+                                  (2, 6, 7, 7, 4, 1, 2, 1)])
+@pytest.mark.parametrize("in_place", [False, True])
+def test_conv2d_input_backward_accumulate(module, dev, case, in_place):
+    """Input gradient plus an addend in the same pass (a residual input's two gradient
+    contributions): bit-equal to the oracle's input gradient followed by the accumulation add,
+    on the direct and product paths, with the addend a separate buffer or the output itself."""
+    n, cin, h, w, cout, k, s, groups = case
+    pad = k // 2
+    r = np.random.default_rng(hash(case) & 0xFFFFFF)
+    shape = ox.conv2d_shape(n, cin, h, w, cout, k, s, pad, groups)
+    oh, ow = ox.conv2d_output_size(shape)
+    wt = (r.standard_normal((cout, cin // groups, k, k)) * 0.3).astype(np.float32)
+    g = r.standard_normal((n, cout, oh, ow)).astype(np.float32)
+    addend = r.standard_normal((n, cin, h, w)).astype(np.float32)
+    dw_, dg_, da_ = to_dev(wt, dev), to_dev(g, dev), to_dev(addend, dev)
+    out = da_ if in_place else torch.empty_like(da_)
+    module.conv2d_input_backward_accumulate(shape, dg_, dw_, da_, out)
+    torch.cuda.synchronize()
+    rdx = oracle.conv2d_backward(g, np.zeros((n, cin, h, w), np.float32), wt, s, pad, groups)[0]
+    assert_bitexact(host(out), oracle.accumulate(addend, rdx), "accumulated input gradient")
+    with pytest.raises(ox.OxideError):
+        module.conv2d_input_backward_accumulate(shape, dg_, dw_, None, out)
+
+
 @pytest.mark.parametrize("shape,kernel,stride", [((2, 3, 4, 4), (2, 2), (2, 2)),
                                                  ((128, 960, 1, 1), (1, 1), (1, 1)),
                                                  ((2, 5, 7, 7), (7, 7), (7, 7)),

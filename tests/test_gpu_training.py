@@ -62,6 +62,9 @@ class OracleChecker:
         a = op.attrs
         ref = oracle.conv2d_backward(r["gradient"], r["x"], r["weight"], a["stride"],
                                      a["padding"], a["groups"])[0]
+        if "addend" in r:  # a residual add's gradient accumulated in the same pass
+            ref = oracle.accumulate(r["addend"], ref)
+            self.counts["conv input backward with addend"] += 1
         assert_bitexact(host(op.writes["contribution"]), ref, op.name)
 
     def conv2d_parameter_backward(self, op, r):
@@ -174,11 +177,13 @@ class OracleChecker:
 
 # 46 BatchNorms, 32 of them followed by a ReLU (fused), each fed by a convolution whose bias
 # gradient its backward forms (the classifier's, fed by no BN, stays with its parameter
-# backward); 10 residual adds, whose first operand's gradient is the add's own buffer (no launch)
+# backward); 10 residual adds, whose first operand's gradient is the add's own buffer and whose
+# second operand's is added by that operand's convolution input backward (no add launches)
 EXPECTED_KINDS = {"conv2d_forward": 47, "conv2d_parameter_backward": 47,
                   "conv2d_input_backward": 46, "batch_norm2d_forward": 14,
                   "batch_norm2d_relu_forward": 32, "batch_norm2d_backward": 14,
-                  "batch_norm2d_relu_backward": 32, "add_forward": 10, "add_backward": 10,
+                  "batch_norm2d_relu_backward": 32, "add_forward": 10,
+                  "conv input backward with addend": 10,
                   "avg_pool2d_forward": 1, "avg_pool2d_backward": 1, "cross_entropy": 1,
                   "adamw": 1, "conv bias in parameter backward": 1,
                   "conv bias in batch norm backward": 46}
