@@ -789,24 +789,41 @@ __global__ __launch_bounds__(kRedBlock) void bn_channel_backward_kernel(
   }
 }
 
-// Per-channel sum of an NCHW tensor (fp64, fixed order): one block per channel.  The dx sum of
-// the planes the one-block-per-channel backward does not take.
-__global__ __launch_bounds__(kRedBlock) void bn_channel_sum_kernel(uint32_t channels,
-                                                                   uint32_t spatial,
-                                                                   uint32_t samples,
-                                                                   oxh::FastDiv spatial_div,
+// Per-channel sum of an NCHW tensor (fp64, fixed order) for the planes the
+// one-block-per-channel backward does not take: partial sums over the reduce slices, then one
+// thread per channel adds them in slice order.
+__global__ __launch_bounds__(kRedBlock) void bn_sum_partial_kernel(Geometry g,
                                                                    const float *__restrict__ v,
-                                                                   float *__restrict__ out) {
+                                                                   double *__restrict__ partial) {
   __shared__ double lds[2][kRedWaves];
-  const uint32_t c = blockIdx.x;
+  const uint32_t s = blockIdx.x, c = blockIdx.y;
   double total = 0.0, unused = 0.0;
-  for (uint32_t j = threadIdx.x; j < samples; j += kRedBlock) {
-    const uint32_t n = oxh::fast_div(j, spatial_div);
-    total += static_cast<double>(
-        v[(static_cast<uint64_t>(n) * channels + c) * spatial + (j - n * spatial)]);
+  const uint64_t begin = static_cast<uint64_t>(s) * g.slice_len;
+  const uint64_t end = begin + g.slice_len < g.samples ? begin + g.slice_len : g.samples;
+  if (g.vec) {
+    const float4 *v4 = reinterpret_cast<const float4 *>(v);
+    const uint32_t e4 = static_cast<uint32_t>(end / 4);
+    for (uint32_t j = static_cast<uint32_t>(begin / 4) + threadIdx.x; j < e4; j += kRedBlock) {
+      const float4 q = v4[nchw_index(g, c, j)];
+      total += (static_cast<double>(q.x) + static_cast<double>(q.y)) +
+               (static_cast<double>(q.z) + static_cast<double>(q.w));
+    }
+  } else {
+    for (uint64_t j = begin + threadIdx.x; j < end; j += kRedBlock)
+      total += static_cast<double>(v[nchw_index(g, c, static_cast<uint32_t>(j))]);
   }
   block_sum2(total, unused, lds);
-  if (threadIdx.x == 0) out[c] = static_cast<float>(total);
+  if (threadIdx.x == 0) partial[static_cast<uint64_t>(c) * g.slices + s] = total;
+}
+
+__global__ void bn_sum_finalize_kernel(uint32_t channels, uint32_t slices,
+                                       const double *__restrict__ partial,
+                                       float *__restrict__ out) {
+  const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= channels) return;
+  double total = 0.0;
+  for (uint32_t s = 0; s < slices; ++s) total += partial[static_cast<uint64_t>(c) * slices + s];
+  out[c] = static_cast<float>(total);
 }
 
 __global__ void bn_update_running_kernel(uint32_t channels, float momentum,
@@ -1108,14 +1125,17 @@ oxh_status backward_train_impl(const char *name, oxh_stream stream, uint64_t bat
                              weight, saved_mean, saved_inverse_std, input_gradient,
                              weight_gradient, bias_gradient, workspace, workspace_bytes);
     if (st != OXH_OK || input_gradient_sum == nullptr) return st;
-    const uint64_t samples = batch * spatial;
-    OXH_REQUIRE(samples < (1ull << 31), OXH_INVALID_SHAPE,
-                std::string(name) + ": more than 2^31 values per channel");
-    oxh::launch(bn_channel_sum_kernel, dim3(static_cast<uint32_t>(channels)), dim3(kRedBlock), 0,
-                oxh::as_stream(stream), static_cast<uint32_t>(channels),
-                static_cast<uint32_t>(spatial), static_cast<uint32_t>(samples),
-                oxh::make_fastdiv(static_cast<uint32_t>(spatial)),
-                static_cast<const float *>(input_gradient), input_gradient_sum);
+    // the backward's partials are consumed (stream order): the workspace holds the dx sums'
+    const Geometry g =
+        make_geometry(batch, channels, spatial, oxh::aligned16(input_gradient));
+    auto *partial = static_cast<double *>(workspace);
+    oxh::launch(bn_sum_partial_kernel, dim3(g.slices, g.channels), dim3(kRedBlock), 0,
+                oxh::as_stream(stream), g, static_cast<const float *>(input_gradient), partial);
+    st = oxh::launched(name);
+    if (st != OXH_OK) return st;
+    oxh::launch(bn_sum_finalize_kernel, dim3((g.channels + 255) / 256), dim3(256), 0,
+                oxh::as_stream(stream), g.channels, g.slices,
+                static_cast<const double *>(partial), input_gradient_sum);
     return oxh::launched(name);
   }
   oxh_status st = check_shape(name, batch, channels, spatial);
