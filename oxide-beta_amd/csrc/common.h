@@ -60,7 +60,7 @@ struct FastDiv {
   uint32_t d, mul, shift;
 };
 
-inline FastDiv make_fastdiv(uint32_t d) {
+__host__ __device__ inline FastDiv make_fastdiv(uint32_t d) {
   FastDiv f{d, 0, 0};
   uint32_t s = 0;
   while ((1ull << s) < d) ++s;

@@ -61,6 +61,14 @@ __device__ __forceinline__ int ceil_div0(int a, const oxh::FastDiv &s) {
   return a <= 0 ? 0 : static_cast<int>(fdiv(static_cast<uint32_t>(a) + s.d - 1, s));
 }
 
+// p where mask is all ones, else -0.0f (x + (-0.0f) == x for every x): the term of a tap
+// outside the input.  Bit operations rather than a select keep the tap's loads unconditional
+// (the compiler turns a select on a loaded value into a branch around the load).
+__device__ __forceinline__ float tap_term(float p, uint32_t mask) {
+  return __uint_as_float((__float_as_uint(p) & mask) | (~mask & 0x80000000u));
+}
+__device__ __forceinline__ uint32_t tap_mask(bool valid) { return valid ? 0xFFFFFFFFu : 0u; }
+
 // ---------------------------------------------------------------- direct kernels
 
 __global__ __launch_bounds__(256) void conv2d_forward_kernel(ConvGeom g, uint32_t total,
@@ -93,6 +101,372 @@ __global__ __launch_bounds__(256) void conv2d_forward_kernel(ConvGeom g, uint32_
       }
     }
     y[o] = sum;
+  }
+}
+
+// Square K x K kernels with stride S (3 or 5, 1 or 2): the taps unrolled at compile time, each
+// tap's input load issued unconditionally (an address inside the plane when the tap is outside
+// it) and its product replaced by -0.0f when outside -- x + (-0.0f) == x for every x, so the
+// sums equal those that skip the padding taps, in the same order, bit for bit, while all K * K
+// loads of a channel are in flight together.
+template <int K, int S>
+__global__ __launch_bounds__(256) void conv2d_forward_taps_kernel(ConvGeom g, uint32_t total,
+                                                                  const float *__restrict__ x,
+                                                                  const float *__restrict__ wt,
+                                                                  const float *__restrict__ bias,
+                                                                  float *__restrict__ y) {
+  for (uint32_t o = blockIdx.x * 256 + threadIdx.x; o < total; o += gridDim.x * 256) {
+    const uint32_t t0 = fdiv(o, g.ow_div), ox = o - t0 * g.ow;
+    const uint32_t t1 = fdiv(t0, g.oh_div), oy = t0 - t1 * g.oh;
+    const uint32_t n = fdiv(t1, g.oc_div), oc = t1 - n * g.out_c;
+    const uint32_t group = fdiv(oc, g.opg_div);
+    const int by = static_cast<int>(oy) * S - static_cast<int>(g.pad);
+    const int bx = static_cast<int>(ox) * S - static_cast<int>(g.pad);
+    const uint32_t plane = g.h * g.w;
+    int row[K], col[K];
+    bool vy[K], vx[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      vy[k] = static_cast<uint32_t>(by + k) < g.h;
+      vx[k] = static_cast<uint32_t>(bx + k) < g.w;
+      row[k] = vy[k] ? (by + k) * static_cast<int>(g.w) : 0;
+      col[k] = vx[k] ? bx + k : 0;
+    }
+    uint32_t mask[K * K];
+#pragma unroll
+    for (int t = 0; t < K * K; ++t) mask[t] = tap_mask(vy[t / K] && vx[t % K]);
+    const float *xn = x + (n * g.in_c + group * g.in_per_group) * plane;
+    const float *wo = wt + oc * g.in_per_group * (K * K);
+    float sum = bias[oc];
+#pragma unroll 2
+    for (uint32_t lc = 0; lc < g.in_per_group; ++lc) {
+      const float *xp = xn + lc * plane;
+      const float *wp = wo + lc * (K * K);
+      float xv[K * K], wv[K * K];
+#pragma unroll
+      for (int t = 0; t < K * K; ++t) {
+        xv[t] = xp[row[t / K] + col[t % K]];
+        wv[t] = wp[t];
+      }
+#pragma unroll
+      for (int t = 0; t < K * K; ++t) {
+        const float p = xv[t] * wv[t];
+        sum += tap_term(p, mask[t]);
+      }
+    }
+    y[o] = sum;
+  }
+}
+
+// Input gradient for square K x K kernels with stride S: the outputs an input element feeds
+// are oy = floor(ty / S) - (M - 1) + j, j < M = ceil(K / S) (ascending, as the CPU path adds
+// them), each valid when inside the output and its tap ky = ty - oy * S < K; likewise in x.
+template <int K, int S>
+__global__ __launch_bounds__(256) void conv2d_input_backward_taps_kernel(
+    ConvGeom g, uint32_t total, const float *__restrict__ grad, const float *__restrict__ wt,
+    const float *addend, float *dx) {
+  constexpr int M = (K + S - 1) / S;
+  for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < total; i += gridDim.x * 256) {
+    const uint32_t t0 = fdiv(i, g.w_div), ix = i - t0 * g.w;
+    const uint32_t t1 = fdiv(t0, g.h_div), iy = t0 - t1 * g.h;
+    const uint32_t n = fdiv(t1, g.ic_div), ic = t1 - n * g.in_c;
+    const uint32_t group = fdiv(ic, g.ipg_div), lc = ic - group * g.in_per_group;
+    const int ty = static_cast<int>(iy + g.pad), tx = static_cast<int>(ix + g.pad);
+    int grow[M], gcol[M], wrow[M], wcol[M];
+    bool vy[M], vx[M];
+#pragma unroll
+    for (int j = 0; j < M; ++j) {
+      const int oy = ty / S - (M - 1) + j, ox = tx / S - (M - 1) + j;
+      const int ky = ty - oy * S, kx = tx - ox * S;
+      vy[j] = oy >= 0 && oy < static_cast<int>(g.oh) && ky < K;
+      vx[j] = ox >= 0 && ox < static_cast<int>(g.ow) && kx < K;
+      grow[j] = vy[j] ? oy * static_cast<int>(g.ow) : 0;
+      gcol[j] = vx[j] ? ox : 0;
+      wrow[j] = vy[j] ? ky * K : 0;
+      wcol[j] = vx[j] ? kx : 0;
+    }
+    uint32_t mask[M * M];
+#pragma unroll
+    for (int t = 0; t < M * M; ++t) mask[t] = tap_mask(vy[t / M] && vx[t % M]);
+    const uint32_t oplane = g.oh * g.ow;
+    float acc = 0.0f;
+#pragma unroll 2
+    for (uint32_t j = 0; j < g.out_per_group; ++j) {
+      const uint32_t oc = group * g.out_per_group + j;
+      const float *gp = grad + (n * g.out_c + oc) * oplane;
+      const float *wp = wt + (oc * g.in_per_group + lc) * (K * K);
+      float gv[M * M], wv[M * M];
+#pragma unroll
+      for (int t = 0; t < M * M; ++t) {
+        gv[t] = gp[grow[t / M] + gcol[t % M]];
+        wv[t] = wp[wrow[t / M] + wcol[t % M]];
+      }
+#pragma unroll
+      for (int t = 0; t < M * M; ++t) {
+        const float p = gv[t] * wv[t];
+        acc += tap_term(p, mask[t]);
+      }
+    }
+    dx[i] = addend != nullptr ? acc + addend[i] : acc;
+  }
+}
+
+// Ungrouped K x K convolutions on small planes: one block per (image, channel tile) stages the
+// image's operand planes and the tile's weights in LDS with coalesced loads (the tap kernels'
+// per-lane gathers are bound by the L1 address rate); each thread then computes kLdsR
+// channels at one position, reading each staged plane value once for all of them and the
+// kLdsR weights as one float4 broadcast (weights staged channel-innermost, the tile padded to
+// a multiple of kLdsR with zeros).  Sums run in the CPU path's order with the tap kernels'
+// -0.0f padding terms (bit-exact forward and input gradient).  kLdsFloats bounds one block's
+// staging.
+constexpr uint32_t kLdsFloats = 16384;  // 64 KB
+constexpr int kLdsR = 4;
+
+__device__ __forceinline__ uint32_t round4(uint32_t v) { return (v + 3) & ~3u; }
+
+// Block-wide global -> LDS staging with kStageUnroll loads in flight per thread (a load, a
+// wait and a store per element would put one memory latency per element on the block).
+// Element i < count is src[src_index(i)], stored at dst[dst_index(i)].
+constexpr int kStageUnroll = 8;
+
+template <class SrcMap, class DstMap>
+__device__ __forceinline__ void stage(float *dst, const float *src, uint32_t count,
+                                      SrcMap src_index, DstMap dst_index) {
+  for (uint32_t b = threadIdx.x; b < count; b += 256 * kStageUnroll) {
+    float v[kStageUnroll];
+#pragma unroll
+    for (int u = 0; u < kStageUnroll; ++u) {
+      const uint32_t i = b + u * 256;
+      v[u] = src[src_index(i < count ? i : count - 1)];
+    }
+#pragma unroll
+    for (int u = 0; u < kStageUnroll; ++u) {
+      const uint32_t i = b + u * 256;
+      if (i < count) dst[dst_index(i)] = v[u];
+    }
+  }
+}
+__device__ __forceinline__ uint32_t same_index(uint32_t i) { return i; }
+__device__ __forceinline__ void stage_plain(float *dst, const float *src, uint32_t count) {
+  stage(dst, src, count, same_index, same_index);
+}
+__device__ __forceinline__ void zero_fill(float *dst, uint32_t count, uint32_t stride,
+                                          uint32_t first, uint32_t width) {
+  // dst[r * stride + first + c] = 0 for r < count, c < width
+  for (uint32_t i = threadIdx.x; i < count * width; i += 256) {
+    const uint32_t r = i / width;
+    dst[r * stride + first + (i - r * width)] = 0.0f;
+  }
+}
+
+template <int K, int S>
+__global__ __launch_bounds__(256) void conv2d_forward_lds_kernel(
+    ConvGeom g, uint32_t oc_tile, oxh::FastDiv oplane_div, oxh::FastDiv rows_div,
+    const float *__restrict__ x, const float *__restrict__ wt, const float *__restrict__ bias,
+    float *__restrict__ y) {
+  extern __shared__ float lds[];
+  constexpr int T = K * K;
+  const uint32_t n = blockIdx.y, oc0 = blockIdx.x * oc_tile;
+  const uint32_t ocn = min(oc_tile, g.out_c - oc0), ocp = round4(ocn);
+  const uint32_t plane = g.h * g.w, xs = g.in_c * plane;
+  float *xl = lds, *wl = lds + round4(xs);  // wl[(ic * T + tap) * ocp + ocl]
+  stage_plain(xl, x + static_cast<uint64_t>(n) * xs, xs);
+  const uint32_t rows = g.in_c * T;  // r = ic * T + tap
+  stage(wl, wt + static_cast<uint64_t>(oc0) * rows, ocn * rows, same_index, [&](uint32_t i) {
+    const uint32_t ocl = fdiv(i, rows_div);
+    return (i - ocl * rows) * ocp + ocl;
+  });
+  if (ocp > ocn) zero_fill(wl, rows, ocp, ocn, ocp - ocn);
+  __syncthreads();
+  const uint32_t oplane = g.oh * g.ow, items = (ocp / kLdsR) * oplane;
+  for (uint32_t it = threadIdx.x; it < items; it += 256) {
+    const uint32_t q = fdiv(it, oplane_div), pos = it - q * oplane;
+    const uint32_t oy = fdiv(pos, g.ow_div), ox = pos - oy * g.ow;
+    const int by = static_cast<int>(oy) * S - static_cast<int>(g.pad);
+    const int bx = static_cast<int>(ox) * S - static_cast<int>(g.pad);
+    int off[T];
+    uint32_t mask[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const int iy = by + t / K, ix = bx + t % K;
+      const bool v = static_cast<uint32_t>(iy) < g.h && static_cast<uint32_t>(ix) < g.w;
+      off[t] = v ? iy * static_cast<int>(g.w) + ix : 0;
+      mask[t] = tap_mask(v);
+    }
+    float acc[kLdsR];
+#pragma unroll
+    for (int r = 0; r < kLdsR; ++r) {
+      const uint32_t ocl = q * kLdsR + r;
+      acc[r] = ocl < ocn ? bias[oc0 + ocl] : 0.0f;
+    }
+    const float *wq = wl + q * kLdsR;
+    for (uint32_t ic = 0; ic < g.in_c; ++ic) {
+      const float *xp = xl + ic * plane;
+      const float *wp = wq + ic * T * ocp;
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const float xv = xp[off[t]];
+        const float4 w4 = *reinterpret_cast<const float4 *>(wp + t * ocp);
+        acc[0] += tap_term(xv * w4.x, mask[t]);
+        acc[1] += tap_term(xv * w4.y, mask[t]);
+        acc[2] += tap_term(xv * w4.z, mask[t]);
+        acc[3] += tap_term(xv * w4.w, mask[t]);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < kLdsR; ++r) {
+      const uint32_t ocl = q * kLdsR + r;
+      if (ocl < ocn) y[(static_cast<uint64_t>(n) * g.out_c + oc0 + ocl) * oplane + pos] = acc[r];
+    }
+  }
+}
+
+// Input gradient: block (input-channel tile, image) stages the image's whole output gradient
+// and the weights of the tile's input channels as wl[(oc * K * K + tap) * icp + icl].
+template <int K, int S>
+__global__ __launch_bounds__(256) void conv2d_input_backward_lds_kernel(
+    ConvGeom g, uint32_t ic_tile, oxh::FastDiv plane_div, const float *__restrict__ grad,
+    const float *__restrict__ wt, const float *addend, float *dx) {
+  extern __shared__ float lds[];
+  constexpr int T = K * K, M = (K + S - 1) / S;
+  const uint32_t n = blockIdx.y, ic0 = blockIdx.x * ic_tile;
+  const uint32_t icn = min(ic_tile, g.in_c - ic0), icp = round4(icn);
+  const uint32_t oplane = g.oh * g.ow, gs = g.out_c * oplane;
+  float *gl = lds, *wl = lds + round4(gs);
+  stage_plain(gl, grad + static_cast<uint64_t>(n) * gs, gs);
+  // element i = (oc, icl, tap): per oc the tile's icn * T contiguous weights
+  const uint32_t rows = g.out_c * T, run = icn * T;
+  const oxh::FastDiv run_div = oxh::make_fastdiv(run);
+  stage(
+      wl, wt + static_cast<uint64_t>(ic0) * T, g.out_c * run,
+      [&](uint32_t i) {
+        const uint32_t oc = fdiv(i, run_div);
+        return oc * g.in_c * T + (i - oc * run);
+      },
+      [&](uint32_t i) {
+        const uint32_t oc = fdiv(i, run_div), rem = i - oc * run, icl = rem / T;
+        return (oc * T + rem - icl * T) * icp + icl;
+      });
+  if (icp > icn) zero_fill(wl, rows, icp, icn, icp - icn);
+  __syncthreads();
+  const uint32_t plane = g.h * g.w, items = (icp / kLdsR) * plane;
+  for (uint32_t it = threadIdx.x; it < items; it += 256) {
+    const uint32_t q = fdiv(it, plane_div), pos = it - q * plane;
+    const uint32_t iy = fdiv(pos, g.w_div), ix = pos - iy * g.w;
+    const int ty = static_cast<int>(iy + g.pad), tx = static_cast<int>(ix + g.pad);
+    int goff[M * M], woff[M * M];
+    uint32_t mask[M * M];
+#pragma unroll
+    for (int t = 0; t < M * M; ++t) {
+      const int oy = ty / S - (M - 1) + t / M, ox = tx / S - (M - 1) + t % M;
+      const int ky = ty - oy * S, kx = tx - ox * S;
+      const bool v = oy >= 0 && oy < static_cast<int>(g.oh) && ky < K && ox >= 0 &&
+                     ox < static_cast<int>(g.ow) && kx < K;
+      goff[t] = v ? oy * static_cast<int>(g.ow) + ox : 0;
+      woff[t] = v ? (ky * K + kx) * static_cast<int>(icp) : 0;
+      mask[t] = tap_mask(v);
+    }
+    float acc[kLdsR] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const float *wq = wl + q * kLdsR;
+    for (uint32_t oc = 0; oc < g.out_c; ++oc) {
+      const float *gp = gl + oc * oplane;
+      const float *wp = wq + oc * T * icp;
+#pragma unroll
+      for (int t = 0; t < M * M; ++t) {
+        const float gv = gp[goff[t]];
+        const float4 w4 = *reinterpret_cast<const float4 *>(wp + woff[t]);
+        acc[0] += tap_term(gv * w4.x, mask[t]);
+        acc[1] += tap_term(gv * w4.y, mask[t]);
+        acc[2] += tap_term(gv * w4.z, mask[t]);
+        acc[3] += tap_term(gv * w4.w, mask[t]);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < kLdsR; ++r) {
+      const uint32_t icl = q * kLdsR + r;
+      if (icl >= icn) continue;
+      const uint64_t i = (static_cast<uint64_t>(n) * g.in_c + ic0 + icl) * plane + pos;
+      dx[i] = addend != nullptr ? acc[r] + addend[i] : acc[r];
+    }
+  }
+}
+
+// Weight gradient partials: block (output-channel tile of kDwOcTile, image chunk) stages each
+// image's input planes and the tile's output-gradient planes position-major
+// (gl[pos * kDwOcTile + ocl], zero past the tile); thread t owns the (ic, tap) pairs t,
+// t + 256 (<= kDwPairSlots of them) for every channel of the tile.  Partials over the chunk,
+// in position order per image (the chunk sums then run in chunk order).
+constexpr int kDwOcTile = 16, kDwPairSlots = 2;
+
+template <int K, int S>
+__global__ __launch_bounds__(256) void conv2d_weight_lds_kernel(ConvGeom g, uint32_t per_chunk,
+                                                                oxh::FastDiv oplane_div,
+                                                                const float *__restrict__ grad,
+                                                                const float *__restrict__ x,
+                                                                float *__restrict__ partial) {
+  extern __shared__ float lds[];
+  constexpr int T = K * K;
+  const uint32_t oc0 = blockIdx.x * kDwOcTile, chunk = blockIdx.y;
+  const uint32_t ocn = min(static_cast<uint32_t>(kDwOcTile), g.out_c - oc0);
+  const uint32_t plane = g.h * g.w, oplane = g.oh * g.ow, xs = g.in_c * plane;
+  const uint32_t pairs = g.in_c * T;
+  float *gl = lds, *xl = lds + kDwOcTile * oplane;
+  float acc[kDwPairSlots][kDwOcTile];
+  int base[kDwPairSlots], ky[kDwPairSlots], kx[kDwPairSlots];
+#pragma unroll
+  for (int j = 0; j < kDwPairSlots; ++j) {
+    const uint32_t pr = threadIdx.x + j * 256;
+    const uint32_t ic = pr / T, tap = pr - ic * T;
+    ky[j] = static_cast<int>(tap / K) - static_cast<int>(g.pad);
+    kx[j] = static_cast<int>(tap % K) - static_cast<int>(g.pad);
+    base[j] = pr < pairs ? static_cast<int>(ic * plane) : 0;
+#pragma unroll
+    for (int o = 0; o < kDwOcTile; ++o) acc[j][o] = 0.0f;
+  }
+  const uint32_t n0 = chunk * per_chunk, n1 = min(n0 + per_chunk, g.batch);
+  for (uint32_t n = n0; n < n1; ++n) {
+    __syncthreads();  // the previous image's planes are read
+    stage_plain(xl, x + static_cast<uint64_t>(n) * xs, xs);
+    stage(gl, grad + (static_cast<uint64_t>(n) * g.out_c + oc0) * oplane, ocn * oplane,
+          same_index, [&](uint32_t i) {
+            const uint32_t ocl = fdiv(i, oplane_div);
+            return (i - ocl * oplane) * kDwOcTile + ocl;
+          });
+    if (n == n0 && ocn < kDwOcTile) zero_fill(gl, oplane, kDwOcTile, ocn, kDwOcTile - ocn);
+    __syncthreads();
+    for (uint32_t pos = 0, oy = 0; oy < g.oh; ++oy)
+      for (uint32_t ox = 0; ox < g.ow; ++ox, ++pos) {
+        float gv[kDwOcTile];
+        const float4 *g4 = reinterpret_cast<const float4 *>(gl + pos * kDwOcTile);
+#pragma unroll
+        for (int o = 0; o < kDwOcTile / 4; ++o) {
+          const float4 v = g4[o];
+          gv[4 * o] = v.x;
+          gv[4 * o + 1] = v.y;
+          gv[4 * o + 2] = v.z;
+          gv[4 * o + 3] = v.w;
+        }
+#pragma unroll
+        for (int j = 0; j < kDwPairSlots; ++j) {
+          const int iy = static_cast<int>(oy) * S + ky[j], ix = static_cast<int>(ox) * S + kx[j];
+          const bool ok = threadIdx.x + j * 256 < pairs && static_cast<uint32_t>(iy) < g.h &&
+                          static_cast<uint32_t>(ix) < g.w;
+          const float xv = xl[ok ? base[j] + iy * static_cast<int>(g.w) + ix : 0];
+          const uint32_t m = tap_mask(ok);
+#pragma unroll
+          for (int o = 0; o < kDwOcTile; ++o) acc[j][o] += tap_term(gv[o] * xv, m);
+        }
+      }
+  }
+  const uint32_t weights = g.out_c * pairs;
+  float *out = partial + static_cast<uint64_t>(chunk) * weights;
+#pragma unroll
+  for (int j = 0; j < kDwPairSlots; ++j) {
+    const uint32_t pr = threadIdx.x + j * 256;
+    if (pr >= pairs) continue;
+#pragma unroll
+    for (int o = 0; o < kDwOcTile; ++o)
+      if (static_cast<uint32_t>(o) < ocn) out[(oc0 + o) * pairs + pr] = acc[j][o];
   }
 }
 
@@ -607,6 +981,77 @@ oxh_status make_conv_geom(const char *name, const oxh_conv2d_shape *s, ConvGeom 
   return oxh::ok();
 }
 
+// Square 3 x 3 or 5 x 5 kernels with stride 1 or 2 take the tap-unrolled direct kernels:
+// returns 10 * K + S, or 0 for the generic ones.
+int tap_kernel(const ConvGeom &g) {
+  if (g.kh != g.kw || (g.kh != 3 && g.kh != 5) || (g.stride != 1 && g.stride != 2)) return 0;
+  return static_cast<int>(10 * g.kh + g.stride);
+}
+
+// Plans of the LDS-staged per-image kernels: `tile` channels per block (0: not applicable).
+struct LdsPlan {
+  uint32_t tile = 0, tiles = 0, chunks = 1, per_chunk = 0, lds_bytes = 0;
+};
+
+bool lds_eligible(const ConvGeom &g) {
+  return g.groups == 1 && tap_kernel(g) != 0 && g.batch <= 65535;
+}
+
+// `staged` floats per block plus `per` per tile channel (tiles of kLdsR-channel groups,
+// weights padded to a multiple of kLdsR), over `channels` channels of `plane` positions: about
+// one group per thread per block.
+LdsPlan channel_tiles(uint64_t staged, uint64_t per, uint64_t channels, uint64_t plane) {
+  LdsPlan p;
+  staged = (staged + 3) / 4 * 4;
+  if (staged + kLdsR * per > kLdsFloats) return p;
+  const uint64_t fit = (kLdsFloats - staged) / per / kLdsR * kLdsR;
+  uint64_t groups = 256 / plane;
+  if (groups < 1) groups = 1;
+  uint64_t tile = groups * kLdsR;
+  const uint64_t all = (channels + kLdsR - 1) / kLdsR * kLdsR;
+  if (tile > all) tile = all;
+  if (tile > fit) tile = fit;
+  p.tile = static_cast<uint32_t>(tile);
+  p.tiles = static_cast<uint32_t>((channels + tile - 1) / tile);
+  p.lds_bytes = static_cast<uint32_t>((staged + tile * per) * 4);
+  return p;
+}
+
+LdsPlan forward_lds_plan(const ConvGeom &g) {
+  if (!lds_eligible(g)) return LdsPlan{};
+  const uint64_t taps = g.kh * g.kw;
+  return channel_tiles(static_cast<uint64_t>(g.in_c) * g.h * g.w, g.in_c * taps, g.out_c,
+                       static_cast<uint64_t>(g.oh) * g.ow);
+}
+
+LdsPlan input_backward_lds_plan(const ConvGeom &g) {
+  if (!lds_eligible(g)) return LdsPlan{};
+  const uint64_t taps = g.kh * g.kw;
+  return channel_tiles(static_cast<uint64_t>(g.out_c) * g.oh * g.ow, g.out_c * taps, g.in_c,
+                       static_cast<uint64_t>(g.h) * g.w);
+}
+
+// Weight gradient: (ic, tap) pairs within the thread slots, the image planes plus a full
+// output-channel tile within the LDS budget; image chunks for about 512 blocks.
+LdsPlan weight_lds_plan(const ConvGeom &g) {
+  LdsPlan p;
+  if (!lds_eligible(g)) return p;
+  const uint64_t pairs = static_cast<uint64_t>(g.in_c) * g.kh * g.kw;
+  const uint64_t staged = static_cast<uint64_t>(g.in_c) * g.h * g.w +
+                          static_cast<uint64_t>(kDwOcTile) * g.oh * g.ow;
+  if (pairs > 256u * kDwPairSlots || staged > kLdsFloats) return p;
+  p.tile = kDwOcTile;
+  p.tiles = (g.out_c + kDwOcTile - 1) / kDwOcTile;
+  uint32_t chunks = 512 / p.tiles;
+  if (chunks < 1) chunks = 1;
+  if (chunks > g.batch) chunks = g.batch;
+  while (chunks > 1 && static_cast<uint64_t>(chunks) * weight_elems(g) >= kMaxElems) --chunks;
+  p.per_chunk = (g.batch + chunks - 1) / chunks;
+  p.chunks = (g.batch + p.per_chunk - 1) / p.per_chunk;
+  p.lds_bytes = static_cast<uint32_t>(staged * 4);
+  return p;
+}
+
 // 1x1, stride 1, no padding, one group: the convolution is a matrix product over channels.
 bool pointwise(const ConvGeom &g) {
   return g.kh == 1 && g.kw == 1 && g.stride == 1 && g.pad == 0 && g.groups == 1 &&
@@ -698,6 +1143,8 @@ bool depthwise_single_pass(const ConvGeom &g) {
 
 uint64_t weight_partial_bytes(const ConvGeom &g) {
   if (depthwise_single_pass(g)) return 0;
+  const LdsPlan lp = weight_lds_plan(g);
+  if (lp.tile > 0) return lp.chunks > 1 ? lp.chunks * weight_elems(g) * 4 : 0;
   if (pointwise(g)) {
     const KSplit k = product_split(g);
     return k.chunks > 1 ? static_cast<uint64_t>(k.chunks) * g.out_c * g.in_c * 4 : 0;
@@ -766,8 +1213,27 @@ oxh_status input_backward_impl(const char *name, oxh_stream stream,
     a.k_chunk = a.K;
     return launch_product(name, s, a, 1);
   }
-  oxh::launch(conv2d_input_backward_kernel, dim3(grid_for(in_n)), dim3(256), 0, s, g,
-              static_cast<uint32_t>(in_n), gradient, weight, addend, input_gradient);
+  const LdsPlan lp = input_backward_lds_plan(g);
+  if (lp.tile > 0) {
+    const dim3 lgrid(lp.tiles, g.batch), lblock(256);
+    const oxh::FastDiv pd = oxh::make_fastdiv(g.h * g.w);
+    switch (tap_kernel(g)) {
+      case 31: oxh::launch(conv2d_input_backward_lds_kernel<3, 1>, lgrid, lblock, lp.lds_bytes, s, g, lp.tile, pd, gradient, weight, addend, input_gradient); break;
+      case 32: oxh::launch(conv2d_input_backward_lds_kernel<3, 2>, lgrid, lblock, lp.lds_bytes, s, g, lp.tile, pd, gradient, weight, addend, input_gradient); break;
+      case 51: oxh::launch(conv2d_input_backward_lds_kernel<5, 1>, lgrid, lblock, lp.lds_bytes, s, g, lp.tile, pd, gradient, weight, addend, input_gradient); break;
+      default: oxh::launch(conv2d_input_backward_lds_kernel<5, 2>, lgrid, lblock, lp.lds_bytes, s, g, lp.tile, pd, gradient, weight, addend, input_gradient);
+    }
+    return oxh::launched(name);
+  }
+  const dim3 grid(grid_for(in_n)), block(256);
+  const uint32_t total = static_cast<uint32_t>(in_n);
+  switch (tap_kernel(g)) {
+    case 31: oxh::launch(conv2d_input_backward_taps_kernel<3, 1>, grid, block, 0, s, g, total, gradient, weight, addend, input_gradient); break;
+    case 32: oxh::launch(conv2d_input_backward_taps_kernel<3, 2>, grid, block, 0, s, g, total, gradient, weight, addend, input_gradient); break;
+    case 51: oxh::launch(conv2d_input_backward_taps_kernel<5, 1>, grid, block, 0, s, g, total, gradient, weight, addend, input_gradient); break;
+    case 52: oxh::launch(conv2d_input_backward_taps_kernel<5, 2>, grid, block, 0, s, g, total, gradient, weight, addend, input_gradient); break;
+    default: oxh::launch(conv2d_input_backward_kernel, grid, block, 0, s, g, total, gradient, weight, addend, input_gradient);
+  }
   return oxh::launched(name);
 }
 
@@ -815,8 +1281,28 @@ oxh_status oxh_conv2d_forward(oxh_stream stream, const oxh_conv2d_shape *shape,
     a.k_chunk = a.K;
     return launch_product(name, s, a, 1);
   }
-  oxh::launch(conv2d_forward_kernel, dim3(grid_for(out_n)), dim3(256), 0, s, g,
-              static_cast<uint32_t>(out_n), input, weight, bias, output);
+  const LdsPlan lp = forward_lds_plan(g);
+  if (lp.tile > 0) {
+    const dim3 lgrid(lp.tiles, g.batch), lblock(256);
+    const oxh::FastDiv od = oxh::make_fastdiv(g.oh * g.ow);
+    const oxh::FastDiv rd = oxh::make_fastdiv(g.in_c * g.kh * g.kw);
+    switch (tap_kernel(g)) {
+      case 31: oxh::launch(conv2d_forward_lds_kernel<3, 1>, lgrid, lblock, lp.lds_bytes, s, g, lp.tile, od, rd, input, weight, bias, output); break;
+      case 32: oxh::launch(conv2d_forward_lds_kernel<3, 2>, lgrid, lblock, lp.lds_bytes, s, g, lp.tile, od, rd, input, weight, bias, output); break;
+      case 51: oxh::launch(conv2d_forward_lds_kernel<5, 1>, lgrid, lblock, lp.lds_bytes, s, g, lp.tile, od, rd, input, weight, bias, output); break;
+      default: oxh::launch(conv2d_forward_lds_kernel<5, 2>, lgrid, lblock, lp.lds_bytes, s, g, lp.tile, od, rd, input, weight, bias, output);
+    }
+    return oxh::launched(name);
+  }
+  const dim3 grid(grid_for(out_n)), block(256);
+  const uint32_t total = static_cast<uint32_t>(out_n);
+  switch (tap_kernel(g)) {
+    case 31: oxh::launch(conv2d_forward_taps_kernel<3, 1>, grid, block, 0, s, g, total, input, weight, bias, output); break;
+    case 32: oxh::launch(conv2d_forward_taps_kernel<3, 2>, grid, block, 0, s, g, total, input, weight, bias, output); break;
+    case 51: oxh::launch(conv2d_forward_taps_kernel<5, 1>, grid, block, 0, s, g, total, input, weight, bias, output); break;
+    case 52: oxh::launch(conv2d_forward_taps_kernel<5, 2>, grid, block, 0, s, g, total, input, weight, bias, output); break;
+    default: oxh::launch(conv2d_forward_kernel, grid, block, 0, s, g, total, input, weight, bias, output);
+  }
   return oxh::launched(name);
 }
 
@@ -893,6 +1379,24 @@ oxh_status oxh_conv2d_weight_backward(oxh_stream stream, const oxh_conv2d_shape 
     else
       oxh::launch(conv2d_depthwise_weight_kernel<5>, dim3(g.out_c), dim3(256), 0, s, g,
                   oplane_div, gradient, input, weight_gradient);
+    return oxh::launched(name);
+  }
+  const LdsPlan lp = weight_lds_plan(g);
+  if (lp.tile > 0) {
+    const uint32_t weights = static_cast<uint32_t>(weight_elems(g));
+    float *out = lp.chunks > 1 ? partial : weight_gradient;
+    const dim3 lgrid(lp.tiles, lp.chunks), lblock(256);
+    const oxh::FastDiv od = oxh::make_fastdiv(g.oh * g.ow);
+    switch (tap_kernel(g)) {
+      case 31: oxh::launch(conv2d_weight_lds_kernel<3, 1>, lgrid, lblock, lp.lds_bytes, s, g, lp.per_chunk, od, gradient, input, out); break;
+      case 32: oxh::launch(conv2d_weight_lds_kernel<3, 2>, lgrid, lblock, lp.lds_bytes, s, g, lp.per_chunk, od, gradient, input, out); break;
+      case 51: oxh::launch(conv2d_weight_lds_kernel<5, 1>, lgrid, lblock, lp.lds_bytes, s, g, lp.per_chunk, od, gradient, input, out); break;
+      default: oxh::launch(conv2d_weight_lds_kernel<5, 2>, lgrid, lblock, lp.lds_bytes, s, g, lp.per_chunk, od, gradient, input, out);
+    }
+    st = oxh::launched(name);
+    if (st != OXH_OK || lp.chunks == 1) return st;
+    oxh::launch(sum_chunks_kernel, dim3(grid_for(weights)), dim3(256), 0, s, weights, lp.chunks,
+                static_cast<const float *>(partial), weight_gradient);
     return oxh::launched(name);
   }
   const uint32_t chunks = weight_chunks(g);

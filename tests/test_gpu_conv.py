@@ -33,6 +33,13 @@ CASES = [
     (128, 1280, 1, 1, 10, 1, 1, 1),    # config 5's classifier
     (128, 64, 8, 8, 256, 1, 1, 1),     # grids of >= 512 32 x 32 tiles (the others take 16 x 16)
     (2, 6, 7, 7, 4, 1, 2, 1),          # 1x1 with stride 2: direct path
+    # ungrouped 3x3 / 5x5: per-image LDS staging (every K, S pair; ragged channel tiles), and a
+    # plane too large to stage (per-thread tap kernels)
+    (128, 32, 7, 7, 96, 3, 2, 1),      # config 5's second fused-IB convolution at full batch
+    (5, 24, 6, 6, 40, 3, 1, 1),
+    (4, 16, 9, 7, 24, 5, 1, 1),
+    (3, 8, 11, 10, 12, 5, 2, 1),
+    (2, 64, 20, 20, 16, 3, 1, 1),
 ]
 
 
