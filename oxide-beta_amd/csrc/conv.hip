@@ -232,16 +232,17 @@ constexpr int kStageUnroll = 8;
 template <class SrcMap, class DstMap>
 __device__ __forceinline__ void stage(float *dst, const float *src, uint32_t count,
                                       SrcMap src_index, DstMap dst_index) {
-  for (uint32_t b = threadIdx.x; b < count; b += 256 * kStageUnroll) {
+  const uint32_t nt = blockDim.x;
+  for (uint32_t b = threadIdx.x; b < count; b += nt * kStageUnroll) {
     float v[kStageUnroll];
 #pragma unroll
     for (int u = 0; u < kStageUnroll; ++u) {
-      const uint32_t i = b + u * 256;
+      const uint32_t i = b + u * nt;
       v[u] = src[src_index(i < count ? i : count - 1)];
     }
 #pragma unroll
     for (int u = 0; u < kStageUnroll; ++u) {
-      const uint32_t i = b + u * 256;
+      const uint32_t i = b + u * nt;
       if (i < count) dst[dst_index(i)] = v[u];
     }
   }
@@ -253,7 +254,7 @@ __device__ __forceinline__ void stage_plain(float *dst, const float *src, uint32
 __device__ __forceinline__ void zero_fill(float *dst, uint32_t count, uint32_t stride,
                                           uint32_t first, uint32_t width) {
   // dst[r * stride + first + c] = 0 for r < count, c < width
-  for (uint32_t i = threadIdx.x; i < count * width; i += 256) {
+  for (uint32_t i = threadIdx.x; i < count * width; i += blockDim.x) {
     const uint32_t r = i / width;
     dst[r * stride + first + (i - r * width)] = 0.0f;
   }
@@ -393,17 +394,17 @@ __global__ __launch_bounds__(256) void conv2d_input_backward_lds_kernel(
 
 // Weight gradient partials: block (output-channel tile of kDwOcTile, image chunk) stages each
 // image's input planes and the tile's output-gradient planes position-major
-// (gl[pos * kDwOcTile + ocl], zero past the tile); thread t owns the (ic, tap) pairs t,
-// t + 256 (<= kDwPairSlots of them) for every channel of the tile.  Partials over the chunk,
-// in position order per image (the chunk sums then run in chunk order).
-constexpr int kDwOcTile = 16, kDwPairSlots = 2;
+// (gl[pos * kDwOcTile + ocl], zero past the tile).  Thread t < pairs * groups owns one
+// (ic, tap) pair for every channel of the tile over one of `groups` position ranges (groups > 1
+// when there are few pairs); the ranges' sums are added in range order at the end.  Partials
+// over the chunk (the chunk sums then run in chunk order).
+constexpr int kDwOcTile = 16;
+constexpr uint32_t kDwMaxThreads = 512;
 
 template <int K, int S>
-__global__ __launch_bounds__(256) void conv2d_weight_lds_kernel(ConvGeom g, uint32_t per_chunk,
-                                                                oxh::FastDiv oplane_div,
-                                                                const float *__restrict__ grad,
-                                                                const float *__restrict__ x,
-                                                                float *__restrict__ partial) {
+__global__ __launch_bounds__(kDwMaxThreads) void conv2d_weight_lds_kernel(
+    ConvGeom g, uint32_t per_chunk, uint32_t groups, oxh::FastDiv oplane_div,
+    const float *__restrict__ grad, const float *__restrict__ x, float *__restrict__ partial) {
   extern __shared__ float lds[];
   constexpr int T = K * K;
   const uint32_t oc0 = blockIdx.x * kDwOcTile, chunk = blockIdx.y;
@@ -411,18 +412,18 @@ __global__ __launch_bounds__(256) void conv2d_weight_lds_kernel(ConvGeom g, uint
   const uint32_t plane = g.h * g.w, oplane = g.oh * g.ow, xs = g.in_c * plane;
   const uint32_t pairs = g.in_c * T;
   float *gl = lds, *xl = lds + kDwOcTile * oplane;
-  float acc[kDwPairSlots][kDwOcTile];
-  int base[kDwPairSlots], ky[kDwPairSlots], kx[kDwPairSlots];
+  const uint32_t item = threadIdx.x, grp = item / pairs, pr = item - grp * pairs;
+  const bool active = item < pairs * groups;
+  const uint32_t ic = pr / T, tap = pr - ic * T;
+  const int ky = static_cast<int>(tap / K) - static_cast<int>(g.pad);
+  const int kx = static_cast<int>(tap % K) - static_cast<int>(g.pad);
+  const int base = static_cast<int>(ic * plane);
+  const uint32_t p0 = active ? grp * oplane / groups : 0;
+  const uint32_t p1 = active ? (grp + 1) * oplane / groups : 0;
+  const uint32_t oy0 = fdiv(p0, g.ow_div), ox0 = p0 - oy0 * g.ow;
+  float acc[kDwOcTile];
 #pragma unroll
-  for (int j = 0; j < kDwPairSlots; ++j) {
-    const uint32_t pr = threadIdx.x + j * 256;
-    const uint32_t ic = pr / T, tap = pr - ic * T;
-    ky[j] = static_cast<int>(tap / K) - static_cast<int>(g.pad);
-    kx[j] = static_cast<int>(tap % K) - static_cast<int>(g.pad);
-    base[j] = pr < pairs ? static_cast<int>(ic * plane) : 0;
-#pragma unroll
-    for (int o = 0; o < kDwOcTile; ++o) acc[j][o] = 0.0f;
-  }
+  for (int o = 0; o < kDwOcTile; ++o) acc[o] = 0.0f;
   const uint32_t n0 = chunk * per_chunk, n1 = min(n0 + per_chunk, g.batch);
   for (uint32_t n = n0; n < n1; ++n) {
     __syncthreads();  // the previous image's planes are read
@@ -434,39 +435,51 @@ __global__ __launch_bounds__(256) void conv2d_weight_lds_kernel(ConvGeom g, uint
           });
     if (n == n0 && ocn < kDwOcTile) zero_fill(gl, oplane, kDwOcTile, ocn, kDwOcTile - ocn);
     __syncthreads();
-    for (uint32_t pos = 0, oy = 0; oy < g.oh; ++oy)
-      for (uint32_t ox = 0; ox < g.ow; ++ox, ++pos) {
-        float gv[kDwOcTile];
-        const float4 *g4 = reinterpret_cast<const float4 *>(gl + pos * kDwOcTile);
+    uint32_t oy = oy0, ox = ox0;
+    for (uint32_t pos = p0; pos < p1; ++pos) {
+      float gv[kDwOcTile];
+      const float4 *g4 = reinterpret_cast<const float4 *>(gl + pos * kDwOcTile);
 #pragma unroll
-        for (int o = 0; o < kDwOcTile / 4; ++o) {
-          const float4 v = g4[o];
-          gv[4 * o] = v.x;
-          gv[4 * o + 1] = v.y;
-          gv[4 * o + 2] = v.z;
-          gv[4 * o + 3] = v.w;
-        }
-#pragma unroll
-        for (int j = 0; j < kDwPairSlots; ++j) {
-          const int iy = static_cast<int>(oy) * S + ky[j], ix = static_cast<int>(ox) * S + kx[j];
-          const bool ok = threadIdx.x + j * 256 < pairs && static_cast<uint32_t>(iy) < g.h &&
-                          static_cast<uint32_t>(ix) < g.w;
-          const float xv = xl[ok ? base[j] + iy * static_cast<int>(g.w) + ix : 0];
-          const uint32_t m = tap_mask(ok);
-#pragma unroll
-          for (int o = 0; o < kDwOcTile; ++o) acc[j][o] += tap_term(gv[o] * xv, m);
-        }
+      for (int o = 0; o < kDwOcTile / 4; ++o) {
+        const float4 v = g4[o];
+        gv[4 * o] = v.x;
+        gv[4 * o + 1] = v.y;
+        gv[4 * o + 2] = v.z;
+        gv[4 * o + 3] = v.w;
       }
+      const int iy = static_cast<int>(oy) * S + ky, ix = static_cast<int>(ox) * S + kx;
+      const bool ok = static_cast<uint32_t>(iy) < g.h && static_cast<uint32_t>(ix) < g.w;
+      const float xv = xl[ok ? base + iy * static_cast<int>(g.w) + ix : 0];
+      const uint32_t m = tap_mask(ok);
+#pragma unroll
+      for (int o = 0; o < kDwOcTile; ++o) acc[o] += tap_term(gv[o] * xv, m);
+      if (++ox == g.ow) {
+        ox = 0;
+        ++oy;
+      }
+    }
   }
   const uint32_t weights = g.out_c * pairs;
   float *out = partial + static_cast<uint64_t>(chunk) * weights;
-#pragma unroll
-  for (int j = 0; j < kDwPairSlots; ++j) {
-    const uint32_t pr = threadIdx.x + j * 256;
-    if (pr >= pairs) continue;
+  if (groups == 1) {
+    if (!active) return;
 #pragma unroll
     for (int o = 0; o < kDwOcTile; ++o)
-      if (static_cast<uint32_t>(o) < ocn) out[(oc0 + o) * pairs + pr] = acc[j][o];
+      if (static_cast<uint32_t>(o) < ocn) out[(oc0 + o) * pairs + pr] = acc[o];
+    return;
+  }
+  __syncthreads();  // the staged planes are read: the block's LDS holds the range sums
+  float *red = lds;  // red[(grp * pairs + pr) * kDwOcTile + o]
+  if (active) {
+#pragma unroll
+    for (int o = 0; o < kDwOcTile; ++o) red[item * kDwOcTile + o] = acc[o];
+  }
+  __syncthreads();
+  for (uint32_t e = threadIdx.x; e < pairs * ocn; e += blockDim.x) {
+    const uint32_t o = e / pairs, q = e - o * pairs;
+    float v = 0.0f;
+    for (uint32_t r = 0; r < groups; ++r) v += red[(r * pairs + q) * kDwOcTile + o];
+    out[(oc0 + o) * pairs + q] = v;
   }
 }
 
@@ -991,6 +1004,7 @@ int tap_kernel(const ConvGeom &g) {
 // Plans of the LDS-staged per-image kernels: `tile` channels per block (0: not applicable).
 struct LdsPlan {
   uint32_t tile = 0, tiles = 0, chunks = 1, per_chunk = 0, lds_bytes = 0;
+  uint32_t groups = 1, threads = 256;  // weight gradient: position ranges, block size
 };
 
 bool lds_eligible(const ConvGeom &g) {
@@ -1031,24 +1045,33 @@ LdsPlan input_backward_lds_plan(const ConvGeom &g) {
                        static_cast<uint64_t>(g.h) * g.w);
 }
 
-// Weight gradient: (ic, tap) pairs within the thread slots, the image planes plus a full
-// output-channel tile within the LDS budget; image chunks for about 512 blocks.
+// Weight gradient: one thread per (ic, tap) pair and position range (pairs <= kDwMaxThreads;
+// ranges so that a block has about 256 threads), the image planes plus a full output-channel
+// tile (or the range sums) within the LDS budget; image chunks for about 512 blocks.
 LdsPlan weight_lds_plan(const ConvGeom &g) {
   LdsPlan p;
   if (!lds_eligible(g)) return p;
   const uint64_t pairs = static_cast<uint64_t>(g.in_c) * g.kh * g.kw;
-  const uint64_t staged = static_cast<uint64_t>(g.in_c) * g.h * g.w +
-                          static_cast<uint64_t>(kDwOcTile) * g.oh * g.ow;
-  if (pairs > 256u * kDwPairSlots || staged > kLdsFloats) return p;
+  const uint64_t oplane = static_cast<uint64_t>(g.oh) * g.ow;
+  if (pairs > kDwMaxThreads) return p;
+  uint64_t groups = 256 / pairs;
+  if (groups < 1) groups = 1;
+  if (groups > oplane) groups = oplane;
+  const uint64_t staged = static_cast<uint64_t>(g.in_c) * g.h * g.w + kDwOcTile * oplane;
+  const uint64_t reduce = groups > 1 ? pairs * groups * kDwOcTile : 0;
+  const uint64_t floats = staged > reduce ? staged : reduce;
+  if (floats > kLdsFloats) return p;
   p.tile = kDwOcTile;
   p.tiles = (g.out_c + kDwOcTile - 1) / kDwOcTile;
+  p.groups = static_cast<uint32_t>(groups);
+  p.threads = static_cast<uint32_t>((pairs * groups + 63) / 64 * 64);
   uint32_t chunks = 512 / p.tiles;
   if (chunks < 1) chunks = 1;
   if (chunks > g.batch) chunks = g.batch;
   while (chunks > 1 && static_cast<uint64_t>(chunks) * weight_elems(g) >= kMaxElems) --chunks;
   p.per_chunk = (g.batch + chunks - 1) / chunks;
   p.chunks = (g.batch + p.per_chunk - 1) / p.per_chunk;
-  p.lds_bytes = static_cast<uint32_t>(staged * 4);
+  p.lds_bytes = static_cast<uint32_t>(floats * 4);
   return p;
 }
 
@@ -1385,13 +1408,13 @@ oxh_status oxh_conv2d_weight_backward(oxh_stream stream, const oxh_conv2d_shape 
   if (lp.tile > 0) {
     const uint32_t weights = static_cast<uint32_t>(weight_elems(g));
     float *out = lp.chunks > 1 ? partial : weight_gradient;
-    const dim3 lgrid(lp.tiles, lp.chunks), lblock(256);
+    const dim3 lgrid(lp.tiles, lp.chunks), lblock(lp.threads);
     const oxh::FastDiv od = oxh::make_fastdiv(g.oh * g.ow);
     switch (tap_kernel(g)) {
-      case 31: oxh::launch(conv2d_weight_lds_kernel<3, 1>, lgrid, lblock, lp.lds_bytes, s, g, lp.per_chunk, od, gradient, input, out); break;
-      case 32: oxh::launch(conv2d_weight_lds_kernel<3, 2>, lgrid, lblock, lp.lds_bytes, s, g, lp.per_chunk, od, gradient, input, out); break;
-      case 51: oxh::launch(conv2d_weight_lds_kernel<5, 1>, lgrid, lblock, lp.lds_bytes, s, g, lp.per_chunk, od, gradient, input, out); break;
-      default: oxh::launch(conv2d_weight_lds_kernel<5, 2>, lgrid, lblock, lp.lds_bytes, s, g, lp.per_chunk, od, gradient, input, out);
+      case 31: oxh::launch(conv2d_weight_lds_kernel<3, 1>, lgrid, lblock, lp.lds_bytes, s, g, lp.per_chunk, lp.groups, od, gradient, input, out); break;
+      case 32: oxh::launch(conv2d_weight_lds_kernel<3, 2>, lgrid, lblock, lp.lds_bytes, s, g, lp.per_chunk, lp.groups, od, gradient, input, out); break;
+      case 51: oxh::launch(conv2d_weight_lds_kernel<5, 1>, lgrid, lblock, lp.lds_bytes, s, g, lp.per_chunk, lp.groups, od, gradient, input, out); break;
+      default: oxh::launch(conv2d_weight_lds_kernel<5, 2>, lgrid, lblock, lp.lds_bytes, s, g, lp.per_chunk, lp.groups, od, gradient, input, out);
     }
     st = oxh::launched(name);
     if (st != OXH_OK || lp.chunks == 1) return st;
