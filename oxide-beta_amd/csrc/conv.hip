@@ -557,40 +557,42 @@ __global__ __launch_bounds__(256) void conv2d_weight_partial_kernel(
 }
 
 // Depthwise weight gradient (one group per channel, square kernels of size 3 or 5): one block
-// per channel.  Each thread walks the channel's output positions j, j + 256, ... and keeps one
-// partial sum per kernel tap in registers; a fixed xor butterfly per wave and a fixed-order sum
-// over the 4 waves combine them (deterministic; within fp32 rounding of the CPU's (n, oy, ox)
-// running sum).  One launch, in place of the batch-chunk partials and their sum.
-template <int K>
-__global__ __launch_bounds__(256) void conv2d_depthwise_weight_kernel(
+// of Threads per channel (1024 when there are few channels).  Each thread walks the channel's
+// output positions j, j + Threads, ... and keeps one partial sum per kernel tap in registers
+// (all K * K input loads of a position issued together, taps outside the input adding -0.0f);
+// a fixed xor butterfly per wave and a fixed-order sum over the waves combine them
+// (deterministic; within fp32 rounding of the CPU's (n, oy, ox) running sum).  One launch, in
+// place of batch-chunk partials and their sum.
+template <int K, int Threads>
+__global__ __launch_bounds__(Threads) void conv2d_depthwise_weight_kernel(
     ConvGeom g, oxh::FastDiv oplane_div, const float *__restrict__ grad,
     const float *__restrict__ x, float *__restrict__ weight_gradient) {
-  constexpr int kTaps = K * K;
-  __shared__ float wave_sums[4][kTaps];
+  constexpr int kTaps = K * K, kWaves = Threads / 64;
+  __shared__ float wave_sums[kWaves][kTaps];
   const uint32_t c = blockIdx.x;
   const uint32_t oplane = g.oh * g.ow, plane = g.h * g.w;
   const uint32_t positions = g.batch * oplane;
-  const int h = static_cast<int>(g.h), w = static_cast<int>(g.w);
   float acc[kTaps];
 #pragma unroll
   for (int t = 0; t < kTaps; ++t) acc[t] = 0.0f;
-  for (uint32_t j = threadIdx.x; j < positions; j += 256) {
+  for (uint32_t j = threadIdx.x; j < positions; j += Threads) {
     const uint32_t n = fdiv(j, oplane_div), r = j - n * oplane;
     const uint32_t oy = fdiv(r, g.ow_div), ox = r - oy * g.ow;
     const float gv = grad[(n * g.out_c + c) * oplane + r];
     const float *xp = x + (n * g.in_c + c) * plane;
     const int by = static_cast<int>(oy * g.stride) - static_cast<int>(g.pad);
     const int bx = static_cast<int>(ox * g.stride) - static_cast<int>(g.pad);
+    float xv[kTaps];
+    uint32_t mask[kTaps];
 #pragma unroll
-    for (int ky = 0; ky < K; ++ky) {
-      const int iy = by + ky;
-      if (iy < 0 || iy >= h) continue;
-#pragma unroll
-      for (int kx = 0; kx < K; ++kx) {
-        const int ix = bx + kx;
-        if (ix >= 0 && ix < w) acc[ky * K + kx] += gv * xp[iy * w + ix];
-      }
+    for (int t = 0; t < kTaps; ++t) {
+      const int iy = by + t / K, ix = bx + t % K;
+      const bool v = static_cast<uint32_t>(iy) < g.h && static_cast<uint32_t>(ix) < g.w;
+      xv[t] = xp[v ? iy * static_cast<int>(g.w) + ix : 0];
+      mask[t] = tap_mask(v);
     }
+#pragma unroll
+    for (int t = 0; t < kTaps; ++t) acc[t] += tap_term(gv * xv[t], mask[t]);
   }
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
 #pragma unroll
@@ -603,8 +605,10 @@ __global__ __launch_bounds__(256) void conv2d_depthwise_weight_kernel(
   __syncthreads();
   if (threadIdx.x < kTaps) {
     const int t = threadIdx.x;
-    weight_gradient[c * kTaps + t] =
-        ((wave_sums[0][t] + wave_sums[1][t]) + wave_sums[2][t]) + wave_sums[3][t];
+    float v = wave_sums[0][t];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) v += wave_sums[w][t];
+    weight_gradient[c * kTaps + t] = v;
   }
 }
 
@@ -1396,11 +1400,18 @@ oxh_status oxh_conv2d_weight_backward(oxh_stream stream, const oxh_conv2d_shape 
   }
   if (depthwise_single_pass(g)) {
     const oxh::FastDiv oplane_div = oxh::make_fastdiv(g.oh * g.ow);
-    if (g.kh == 3)
-      oxh::launch(conv2d_depthwise_weight_kernel<3>, dim3(g.out_c), dim3(256), 0, s, g,
+    const bool wide = g.out_c <= 128;  // few channels: more threads per channel
+    if (g.kh == 3 && wide)
+      oxh::launch(conv2d_depthwise_weight_kernel<3, 1024>, dim3(g.out_c), dim3(1024), 0, s, g,
+                  oplane_div, gradient, input, weight_gradient);
+    else if (g.kh == 3)
+      oxh::launch(conv2d_depthwise_weight_kernel<3, 256>, dim3(g.out_c), dim3(256), 0, s, g,
+                  oplane_div, gradient, input, weight_gradient);
+    else if (wide)
+      oxh::launch(conv2d_depthwise_weight_kernel<5, 1024>, dim3(g.out_c), dim3(1024), 0, s, g,
                   oplane_div, gradient, input, weight_gradient);
     else
-      oxh::launch(conv2d_depthwise_weight_kernel<5>, dim3(g.out_c), dim3(256), 0, s, g,
+      oxh::launch(conv2d_depthwise_weight_kernel<5, 256>, dim3(g.out_c), dim3(256), 0, s, g,
                   oplane_div, gradient, input, weight_gradient);
     return oxh::launched(name);
   }
