@@ -11,6 +11,7 @@
 // autograd.rs:94-147).
 #include <hip/hip_runtime.h>
 
+#include "chain.h"
 #include "common.h"
 
 namespace {
@@ -243,7 +244,100 @@ oxh_status launch_map(const char *name, oxh_stream stream, const MapArgs<Op::NI,
   return oxh::launched(name);
 }
 
+// One step of a fused chain on one value (the plan operations' formulas above).
+__device__ __forceinline__ float chain_step(uint32_t op, float x0, float x1) {
+  switch (op) {
+    case OXH_PLAN_ADD:
+    case OXH_PLAN_ACCUMULATE: return x0 + x1;
+    case OXH_PLAN_MUL:
+    case OXH_PLAN_MUL_BACKWARD: return x0 * x1;
+    case OXH_PLAN_RELU: return x0 > 0.0f ? x0 : 0.0f;
+    default: return x1 > 0.0f ? x0 : 0.0f;  // OXH_PLAN_RELU_BACKWARD
+  }
+}
+
+__device__ __forceinline__ float4 chain_step4(const oxh::ChainStep &s, const float4 &acc,
+                                              const float4 &b) {
+  const float4 x0 = s.acc_second ? b : acc, x1 = s.acc_second ? acc : b;
+  return make_float4(chain_step(s.op, x0.x, x1.x), chain_step(s.op, x0.y, x1.y),
+                     chain_step(s.op, x0.z, x1.z), chain_step(s.op, x0.w, x1.w));
+}
+
+// A fused chain: per float4 of elements the steps run in order on registers, each loading its
+// other operand (non-temporal) and storing its result where the plan needs it.  The steps are
+// kernel arguments, so every branch on them is uniform; occupancy hides the per-step loads.
+__global__ __launch_bounds__(oxh::kBlock) void chain_vec4_kernel(oxh::Chain c, uint64_t n4,
+                                                                 uint64_t n) {
+  constexpr int U = kUnroll;  // float4 per thread per stream, loads of a step issued together
+  const uint64_t tile = static_cast<uint64_t>(oxh::kBlock) * U;
+  for (uint64_t base = static_cast<uint64_t>(blockIdx.x) * tile + threadIdx.x; base < n4;
+       base += static_cast<uint64_t>(gridDim.x) * tile) {
+    uint64_t idx[U];
+    bool live[U];
+    float4 acc[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      idx[u] = base + static_cast<uint64_t>(u) * oxh::kBlock;
+      live[u] = idx[u] < n4;
+      if (!live[u]) idx[u] = base;  // a repeat of element base: loaded, never stored
+      acc[u] = oxh::load_nt(reinterpret_cast<const float4 *>(c.first) + idx[u]);
+    }
+    for (uint32_t k = 0; k < c.count; ++k) {
+      const oxh::ChainStep s = c.steps[k];
+      float4 b[U];
+      if (s.other >= 0) {
+        const float4 *src = reinterpret_cast<const float4 *>(c.other[s.other]);
+#pragma unroll
+        for (int u = 0; u < U; ++u) b[u] = oxh::load_nt(src + idx[u]);
+      } else {
+#pragma unroll
+        for (int u = 0; u < U; ++u) b[u] = acc[u];
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc[u] = chain_step4(s, acc[u], b[u]);
+      if (s.store >= 0) {
+        float4 *dst = reinterpret_cast<float4 *>(c.store[s.store]);
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          if (live[u]) oxh::store_nt(dst + idx[u], acc[u]);
+      }
+    }
+  }
+  if (blockIdx.x == 0) {
+    const uint64_t i = n4 * 4 + threadIdx.x;
+    if (i < n) {
+      float acc = c.first[i];
+      for (uint32_t k = 0; k < c.count; ++k) {
+        const oxh::ChainStep s = c.steps[k];
+        const float b = s.other >= 0 ? c.other[s.other][i] : acc;
+        acc = s.acc_second ? chain_step(s.op, b, acc) : chain_step(s.op, acc, b);
+        if (s.store >= 0) c.store[s.store][i] = acc;
+      }
+    }
+  }
+}
+
 }  // namespace
+
+namespace oxh {
+
+// Plan buffers are separate hipMalloc allocations (256-byte aligned): the vector path only.
+oxh_status launch_chain(hipStream_t stream, const Chain &c, uint64_t n) {
+  if (n == 0) return ok();
+  OXH_REQUIRE(c.count >= 1 && c.count <= static_cast<uint32_t>(kChainMax) && c.first != nullptr,
+              OXH_TRACE, "malformed elementwise chain");
+  OXH_REQUIRE(aligned16(c.first), OXH_TRACE, "chain buffers must be 16-byte aligned");
+  const uint64_t n4 = n / 4;
+  const uint64_t tile = static_cast<uint64_t>(kBlock) * kUnroll;
+  uint64_t grid = (n4 + tile - 1) / tile;
+  if (grid == 0) grid = 1;
+  if (grid > kMaxGrid) grid = kMaxGrid;
+  launch(chain_vec4_kernel, dim3(static_cast<uint32_t>(grid)), dim3(kBlock), 0, stream, c, n4,
+         n);
+  return launched("elementwise chain");
+}
+
+}  // namespace oxh
 
 extern "C" {
 

@@ -8,13 +8,18 @@
 //   run:     inputs copied host-to-device into their fixed buffers, one graph replay, the
 //            output copied back synchronously (70-99);
 //   replay:  the graph alone, for callers whose inputs are already resident.
-// Plan operations are the reference's Add / Mul / Relu plus the backward elementwise kernels,
-// all launched through this library's C ABI launchers.
+// Plan operations are the reference's Add / Mul / Relu plus the backward elementwise kernels.
+// compile fuses each run of operations in which every operation consumes the previous one's
+// result (and reads no buffer an earlier operation of the run wrote) into one streaming kernel
+// (chain.h): the same fp32 operation per element and step, so the output is bit-identical to
+// the separate launches; a workspace read only inside its run is never written (it lives in
+// registers).  Single operations go through this library's C ABI launchers.
 #include <hip/hip_runtime.h>
 
 #include <string>
 #include <vector>
 
+#include "chain.h"
 #include "common.h"
 
 namespace {
@@ -79,6 +84,92 @@ oxh_status launch_operation(const oxh_plan &p, const Operation &o) {
     case OXH_PLAN_ACCUMULATE: return oxh_accumulate(s, in0, in1, out, n);
     default: return oxh::fail(OXH_TRACE, "unknown plan operation");
   }
+}
+
+// Runs of fusable operations, [begin, end) in plan order.
+struct Run {
+  size_t begin, end;
+};
+
+std::vector<Run> form_runs(const oxh_plan &p) {
+  std::vector<Run> runs;
+  const auto &ops = p.operations;
+  size_t i = 0;
+  while (i < ops.size()) {
+    size_t j = i + 1;
+    std::vector<uint32_t> written = {ops[i].output};
+    while (j < ops.size() && j - i < static_cast<size_t>(oxh::kChainMax)) {
+      const Operation &o = ops[j];
+      const uint32_t prev = ops[j - 1].output;
+      int pos = -1;
+      for (size_t q = 0; q < o.inputs.size(); ++q)
+        if (o.inputs[q] == prev) {
+          pos = static_cast<int>(q);
+          break;
+        }
+      if (pos < 0) break;
+      bool ok = true;
+      for (size_t q = 0; q < o.inputs.size(); ++q) {
+        const uint32_t in = o.inputs[q];
+        if (in == prev) continue;
+        for (uint32_t w : written) ok = ok && in != w;
+      }
+      if (!ok) break;
+      written.push_back(o.output);
+      ++j;
+    }
+    runs.push_back(Run{i, j});
+    i = j;
+  }
+  return runs;
+}
+
+// The chain of a run: step k stores its result when no later step of the run writes the
+// buffer again and the buffer is the plan output or is read from memory by any operation --
+// after the run, or before it (that read sees this replay's value in the next replay) --
+// rather than taken as the running value by step k + 1.
+oxh_status launch_run(const oxh_plan &p, const Run &r) {
+  oxh::Chain c{};
+  const auto &ops = p.operations;
+  c.first = p.buffers[ops[r.begin].inputs[0]].device;
+  c.count = static_cast<uint32_t>(r.end - r.begin);
+  uint32_t n_other = 0, n_store = 0;
+  for (size_t k = r.begin; k < r.end; ++k) {
+    const Operation &o = ops[k];
+    oxh::ChainStep &st = c.steps[k - r.begin];
+    st.op = o.op;
+    st.other = -1;
+    st.acc_second = 0;
+    st.store = -1;
+    if (k == r.begin) {
+      if (o.inputs.size() > 1) {
+        st.other = static_cast<int32_t>(n_other);
+        c.other[n_other++] = p.buffers[o.inputs[1]].device;
+      }
+    } else {
+      const uint32_t prev = ops[k - 1].output;
+      if (o.inputs.size() > 1) {
+        const bool first_is_acc = o.inputs[0] == prev;
+        const uint32_t b = first_is_acc ? o.inputs[1] : o.inputs[0];
+        st.acc_second = first_is_acc ? 0u : 1u;
+        if (b != prev) {
+          st.other = static_cast<int32_t>(n_other);
+          c.other[n_other++] = p.buffers[b].device;
+        }
+      }
+    }
+    bool needed = static_cast<int64_t>(o.output) == p.output;
+    for (size_t q = 0; q < ops.size() && !needed; ++q) {
+      if (q == k + 1 && q < r.end) continue;  // the running value, in registers
+      for (uint32_t in : ops[q].inputs) needed = needed || in == o.output;
+    }
+    for (size_t q = k + 1; q < r.end && needed; ++q) needed = ops[q].output != o.output;
+    if (needed) {
+      st.store = static_cast<int32_t>(n_store);
+      c.store[n_store++] = p.buffers[o.output].device;
+    }
+  }
+  return oxh::launch_chain(p.stream, c, p.buffers[ops[r.begin].output].elements);
 }
 
 void release(oxh_plan *p) {
@@ -196,8 +287,9 @@ oxh_status oxh_plan_compile(oxh_plan *plan) {
     release(plan);
     return st;
   }
-  for (const Operation &o : plan->operations) {
-    st = launch_operation(*plan, o);
+  for (const Run &r : form_runs(*plan)) {
+    st = r.end - r.begin == 1 ? launch_operation(*plan, plan->operations[r.begin])
+                              : launch_run(*plan, r);
     if (st != OXH_OK) {
       const std::string message = oxh_last_error();
       (void)oxh_graph_abort(plan->stream);

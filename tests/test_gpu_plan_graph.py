@@ -145,3 +145,81 @@ def test_kernel_timer_brackets_one_dispatch(module, dev):
     torch.cuda.synchronize()
     assert t.elapsed_ms() == ms
     assert torch.equal(y, torch.relu(x))
+
+
+def _host_plan(plan, inputs, state=None):
+    """The plan evaluated op by op on the host with the oracle's elementwise functions.
+    Workspaces start at zero, as the compiled plan's do, and keep their values from one run to
+    the next (``state``); returns (output, state)."""
+    bufs, k = [], 0
+    for i, b in enumerate(plan.buffers):
+        if isinstance(b, ox.Input):
+            bufs.append(np.asarray(inputs[k], np.float32).ravel())
+            k += 1
+        elif isinstance(b, ox.Constant):
+            bufs.append(np.asarray(b.values, np.float32))
+        else:
+            bufs.append(state[i] if state is not None else np.zeros(b.elements, np.float32))
+    fn = {ox.PLAN_ADD: oracle.add, ox.PLAN_MUL: oracle.mul, ox.PLAN_MUL_BACKWARD: oracle.mul,
+          ox.PLAN_ACCUMULATE: oracle.accumulate, ox.PLAN_RELU_BACKWARD: oracle.relu_backward}
+    for op in plan.operations:
+        args = [bufs[i] for i in op.inputs]
+        bufs[op.output] = (oracle.relu(args[0]) if op.op == ox.PLAN_RELU
+                           else fn[op.op](args[0], args[1]))
+    return bufs[plan.output], bufs
+
+
+def _plan(n_inputs, n_work, ops, output, elements, constant=None):
+    buffers = [ox.Input(elements) for _ in range(n_inputs)]
+    if constant is not None:
+        buffers.append(ox.Constant(constant))
+    buffers += [ox.WorkspaceBuffer(elements) for _ in range(n_work)]
+    return ox.GraphPlan(buffers=buffers, operations=[ox.Operation(*o) for o in ops],
+                        inputs=list(range(n_inputs)), output=output)
+
+
+A, M, R, RB, MB, ACC = (ox.PLAN_ADD, ox.PLAN_MUL, ox.PLAN_RELU, ox.PLAN_RELU_BACKWARD,
+                        ox.PLAN_MUL_BACKWARD, ox.PLAN_ACCUMULATE)
+
+
+@pytest.mark.parametrize("name,n_in,n_work,ops,out", [
+    # x * x (the running value as both operands), then relu
+    ("square", 1, 2, [(M, (0, 0), 1), (R, (1,), 2)], 2),
+    # the running value as the second input of a non-commutative op, in both positions
+    ("relu_backward_sides", 2, 3, [(A, (0, 1), 2), (RB, (1, 2), 3), (RB, (3, 0), 4)], 4),
+    # an intermediate read again after the run: stored, and a new run starts from it
+    ("reused_intermediate", 2, 4, [(A, (0, 1), 2), (M, (2, 1), 3), (R, (0,), 4),
+                                   (ACC, (2, 4), 5)], 5),
+    # the output written in the middle of a run
+    ("output_mid_run", 2, 3, [(A, (0, 1), 2), (M, (2, 0), 3), (R, (3,), 4)], 3),
+    # a run reading a buffer written earlier in it ends there
+    ("reads_earlier_write", 2, 3, [(A, (0, 1), 2), (M, (2, 1), 3), (A, (3, 2), 4)], 4),
+    # write-after-read inside a run: op 2 rewrites the buffer op 0 read (the next replay's op 0
+    # reads it), once as the output and once as an internal workspace
+    ("rewrite_read_buffer", 1, 4, [(A, (0, 2), 3), (MB, (3, 0), 4), (A, (4, 0), 2)], 2),
+    ("rewrite_read_internal", 1, 4, [(A, (0, 2), 3), (MB, (3, 0), 2), (A, (2, 0), 4)], 4),
+    # longer than one fused run (eight steps), with stores of a buffer written twice
+    ("long", 2, 3, [(A, (0, 1), 2), (M, (2, 1), 3), (R, (3,), 2), (A, (2, 0), 3), (M, (3, 3), 4),
+                    (ACC, (4, 1), 2), (R, (2,), 3), (A, (3, 0), 4), (M, (4, 1), 2),
+                    (RB, (0, 2), 3), (A, (3, 3), 4)], 4),
+])
+@pytest.mark.parametrize("elements", [4096 * 1024 + 3, 5])
+def test_fused_plan_runs_match_op_by_op(name, n_in, n_work, ops, out, elements):
+    """Compiled plans fuse runs of dependent operations into one kernel; the output equals the
+    op-by-op evaluation with the oracle bit for bit (ragged lengths exercise the tail)."""
+    ws = list(range(n_in, n_in + n_work))
+    plan = _plan(n_in, n_work, ops, out, elements)
+    assert all(o[2] in ws for o in ops)
+    r = np.random.default_rng(hash(name) & 0xFFFF)
+    inputs = [r.uniform(-1, 1, elements).astype(np.float32) for _ in range(n_in)]
+    inputs[0][:3] = [0.0, -0.0, np.nan]
+    hp = ox.HipJitPlan(plan)
+    state = None
+    try:
+        for _ in range(3):  # later replays start from the earlier ones' workspaces
+            got = hp.run(inputs)
+            ref, state = _host_plan(plan, inputs, state)
+            assert_bitexact(got, ref, name)
+            inputs = [x[::-1].copy() for x in inputs]
+    finally:
+        hp.close()
