@@ -692,7 +692,7 @@ struct ProductArgs {
 #ifndef OXH_SMALL_SLAB
 #define OXH_SMALL_SLAB 128  // k per LDS stage of the small-grid tilings
 #endif
-constexpr int kTile = 32, kUnrollK = 8;  // kTile: the tiling of large grids
+constexpr int kTile = 32;  // the tiling of large grids
 
 template <int Tile, int Threads>
 struct TileShape {
@@ -765,29 +765,35 @@ struct SlabLoader {
     }
   }
 
-  // LDS rows padded to Tile + 1 floats: k-fast stores hit distinct banks.
-  __device__ __forceinline__ void stage(const float (&v)[kLoads], float (*s)[Tile + 1]) const {
+  // LDS tile rows hold k contiguously (s[row][k], rows of kRow floats) so the product reads
+  // four k of a row as one 128-bit access.
+  template <int kRow>
+  __device__ __forceinline__ void stage(const float (&v)[kLoads], float (*s)[kRow]) const {
 #pragma unroll
     for (int u = 0; u < kLoads; ++u) {
       if constexpr (KFast)
-        s[kk + (u % kKCols) * kKStep][r + (u / kKCols) * kRowStep] = v[u];
+        s[r + (u / kKCols) * kRowStep][kk + (u % kKCols) * kKStep] = v[u];
       else
-        s[kk + u * kKStep][r] = v[u];
+        s[r][kk + u * kKStep] = v[u];
     }
   }
 };
 
 // C[m, n] = init[m] + sum_{k in chunk, ascending} A[m, k] * B[n, k]: one serial fp32 sum per
-// output (each product rounded, then added: -ffp-contract=off).  Within a slab the LDS reads
-// of the next group of kUnrollK steps are issued before the current group's arithmetic.
+// output (each product rounded, then added: -ffp-contract=off).  Within a slab, groups of kG4
+// float4 (4 k each) per row are read from LDS as 128-bit accesses, the next group's reads
+// issued before the current group's arithmetic.
 template <int Tile, int Threads, bool AKFast, bool BKFast>
 __global__ __launch_bounds__(Threads) void pointwise_product_kernel(ProductArgs g) {
   using S = TileShape<Tile, Threads>;
   constexpr int kMicro = S::kMicro, kLoads = S::kLoads, kSlab = S::kSlab, kCols = S::kCols;
-  constexpr int U = kUnrollK;
-  // kSlab + U rows: the read-ahead of the group after a slab's last one stays in the buffer
-  __shared__ float as[kSlab + U][Tile + 1];
-  __shared__ float bs[kSlab + U][Tile + 1];
+  constexpr int kG4 = kMicro == 1 ? 4 : 2;  // float4 per row per group (16 or 8 k)
+  constexpr int kGroupK = 4 * kG4;
+  // rows of kSlab k plus one group of read-ahead, padded by 4 floats (rows start in different
+  // banks; 16-byte alignment kept)
+  constexpr int kRow = kSlab + kGroupK + 4;
+  __shared__ __align__(16) float as[Tile][kRow];
+  __shared__ __align__(16) float bs[Tile][kRow];
   const uint32_t m0 = blockIdx.y * Tile, n0 = blockIdx.x * Tile;
   const uint32_t kb = blockIdx.z * g.k_chunk;
   const uint32_t ke = min(kb + g.k_chunk, g.K);
@@ -808,23 +814,28 @@ __global__ __launch_bounds__(Threads) void pointwise_product_kernel(ProductArgs 
     la.fetch(g.a, kb, kc, va);
     lb.fetch(g.b, kb, kc, vb);
   }
-  float a0[U][kMicro], b0[U][kMicro], a1[U][kMicro], b1[U][kMicro];
-  auto read_group = [&](uint32_t k, float (&av)[U][kMicro], float (&bv)[U][kMicro]) {
+  float4 a0[kMicro][kG4], b0[kMicro][kG4], a1[kMicro][kG4], b1[kMicro][kG4];
+  auto read_group = [&](uint32_t k, float4 (&av)[kMicro][kG4], float4 (&bv)[kMicro][kG4]) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
+    for (int i = 0; i < kMicro; ++i)
 #pragma unroll
-      for (int i = 0; i < kMicro; ++i) av[u][i] = as[k + u][ty * kMicro + i];
-#pragma unroll
-      for (int j = 0; j < kMicro; ++j) bv[u][j] = bs[k + u][tx * kMicro + j];
-    }
+      for (int q = 0; q < kG4; ++q) {
+        av[i][q] = *reinterpret_cast<const float4 *>(&as[ty * kMicro + i][k + 4 * q]);
+        bv[i][q] = *reinterpret_cast<const float4 *>(&bs[tx * kMicro + i][k + 4 * q]);
+      }
   };
-  auto add_group = [&](const float (&av)[U][kMicro], const float (&bv)[U][kMicro]) {
+  auto add_group = [&](const float4 (&av)[kMicro][kG4], const float4 (&bv)[kMicro][kG4]) {
 #pragma unroll
-    for (int u = 0; u < U; ++u)
+    for (int q = 0; q < kG4; ++q)
 #pragma unroll
       for (int i = 0; i < kMicro; ++i)
 #pragma unroll
-        for (int j = 0; j < kMicro; ++j) acc[i][j] += av[u][i] * bv[u][j];
+        for (int j = 0; j < kMicro; ++j) {
+          acc[i][j] += av[i][q].x * bv[j][q].x;
+          acc[i][j] += av[i][q].y * bv[j][q].y;
+          acc[i][j] += av[i][q].z * bv[j][q].z;
+          acc[i][j] += av[i][q].w * bv[j][q].w;
+        }
   };
   for (uint32_t k0 = kb; k0 < ke; k0 += kSlab) {
     const uint32_t kc = min(ke - k0, static_cast<uint32_t>(kSlab));
@@ -837,26 +848,26 @@ __global__ __launch_bounds__(Threads) void pointwise_product_kernel(ProductArgs 
       la.fetch(g.a, k1, kc1, va);
       lb.fetch(g.b, k1, kc1, vb);
     }
-    // whole groups, two per iteration so the read-ahead alternates register sets; every
-    // group read starts at a row <= kSlab
-    const uint32_t full = kc / U * U;
+    // whole groups, two per iteration so the read-ahead alternates register sets; a group read
+    // starts at k <= kSlab, inside the row
+    const uint32_t full = kc / kGroupK * kGroupK;
     uint32_t kk = 0;
     if (full > 0) read_group(0, a0, b0);
     while (kk < full) {
-      read_group(kk + U, a1, b1);
+      read_group(kk + kGroupK, a1, b1);
       add_group(a0, b0);
-      kk += U;
+      kk += kGroupK;
       if (kk >= full) break;
-      read_group(kk + U, a0, b0);
+      read_group(kk + kGroupK, a0, b0);
       add_group(a1, b1);
-      kk += U;
+      kk += kGroupK;
     }
     for (; kk < kc; ++kk) {
       float av[kMicro], bv[kMicro];
 #pragma unroll
-      for (int i = 0; i < kMicro; ++i) av[i] = as[kk][ty * kMicro + i];
+      for (int i = 0; i < kMicro; ++i) av[i] = as[ty * kMicro + i][kk];
 #pragma unroll
-      for (int j = 0; j < kMicro; ++j) bv[j] = bs[kk][tx * kMicro + j];
+      for (int j = 0; j < kMicro; ++j) bv[j] = bs[tx * kMicro + j][kk];
 #pragma unroll
       for (int i = 0; i < kMicro; ++i)
 #pragma unroll
