@@ -824,18 +824,27 @@ __global__ __launch_bounds__(Threads) void pointwise_product_kernel(ProductArgs 
         bv[i][q] = *reinterpret_cast<const float4 *>(&bs[tx * kMicro + i][k + 4 * q]);
       }
   };
+  // the group's products first, then each accumulator's adds in ascending k (the adds form
+  // the dependent chain; the products stay off it)
   auto add_group = [&](const float4 (&av)[kMicro][kG4], const float4 (&bv)[kMicro][kG4]) {
+    float p[kMicro][kMicro][4 * kG4];
 #pragma unroll
     for (int q = 0; q < kG4; ++q)
 #pragma unroll
       for (int i = 0; i < kMicro; ++i)
 #pragma unroll
         for (int j = 0; j < kMicro; ++j) {
-          acc[i][j] += av[i][q].x * bv[j][q].x;
-          acc[i][j] += av[i][q].y * bv[j][q].y;
-          acc[i][j] += av[i][q].z * bv[j][q].z;
-          acc[i][j] += av[i][q].w * bv[j][q].w;
+          p[i][j][4 * q] = av[i][q].x * bv[j][q].x;
+          p[i][j][4 * q + 1] = av[i][q].y * bv[j][q].y;
+          p[i][j][4 * q + 2] = av[i][q].z * bv[j][q].z;
+          p[i][j][4 * q + 3] = av[i][q].w * bv[j][q].w;
         }
+#pragma unroll
+    for (int t = 0; t < 4 * kG4; ++t)
+#pragma unroll
+      for (int i = 0; i < kMicro; ++i)
+#pragma unroll
+        for (int j = 0; j < kMicro; ++j) acc[i][j] += p[i][j][t];
   };
   for (uint32_t k0 = kb; k0 < ke; k0 += kSlab) {
     const uint32_t kc = min(ke - k0, static_cast<uint32_t>(kSlab));
