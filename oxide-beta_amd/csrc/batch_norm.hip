@@ -708,83 +708,157 @@ __device__ __forceinline__ uint32_t channel_index(const ChannelGeom &g, uint32_t
   return (n * g.channels + c) * g.spatial + (j - n * g.spatial);
 }
 
-template <bool Relu>
+// Block-wide sums of two doubles, the total in every thread: each wave's butterfly total goes
+// to LDS and every thread adds the kRedWaves wave totals in the same order (one barrier, no
+// broadcast step).  `lds` must not be in use by another sum of the same block.
+__device__ __forceinline__ void block_sum2_all(double &a, double &b, double (*lds)[kRedWaves]) {
+  a = wave_sum(a);
+  b = wave_sum(b);
+  const int wave = threadIdx.x / 64;
+  if (threadIdx.x % 64 == 0) {
+    lds[0][wave] = a;
+    lds[1][wave] = b;
+  }
+  __syncthreads();
+  a = 0.0;
+  b = 0.0;
+#pragma unroll
+  for (int w = 0; w < kRedWaves; ++w) {
+    a += lds[0][w];
+    b += lds[1][w];
+  }
+}
+
+// Up to kChannelKeep values per thread stay in registers between a channel kernel's sum pass
+// and its elementwise pass (config 5's planes hold at most 2048 values per channel); larger
+// channels read their values again (L2).
+constexpr int kChannelKeep = 8;
+
+template <bool Relu, bool Keep>
 __global__ __launch_bounds__(kRedBlock) void bn_channel_forward_kernel(
     ChannelGeom g, const float *__restrict__ x, const float *__restrict__ weight,
     const float *__restrict__ bias, StatsOut out, float *__restrict__ y) {
   __shared__ double lds[2][kRedWaves];
-  __shared__ float stats[2];
   const uint32_t c = blockIdx.x;
   const float shift = x[static_cast<uint64_t>(c) * g.spatial];  // x[0, c, 0]
   const double k = static_cast<double>(shift);
   double sum = 0.0, sq = 0.0;
-  for (uint32_t j = threadIdx.x; j < g.samples; j += kRedBlock) {
-    const double d = static_cast<double>(x[channel_index(g, c, j)]) - k;
-    sum += d;
-    sq += d * d;
+  float kept[Keep ? kChannelKeep : 1];
+  uint32_t at[Keep ? kChannelKeep : 1];
+  if constexpr (Keep) {
+#pragma unroll
+    for (int u = 0; u < kChannelKeep; ++u) {
+      const uint32_t j = threadIdx.x + u * kRedBlock;
+      at[u] = j < g.samples ? channel_index(g, c, j) : 0;
+      kept[u] = x[at[u]];
+    }
+#pragma unroll
+    for (int u = 0; u < kChannelKeep; ++u) {
+      if (threadIdx.x + u * kRedBlock >= g.samples) break;
+      const double d = static_cast<double>(kept[u]) - k;
+      sum += d;
+      sq += d * d;
+    }
+  } else {
+    for (uint32_t j = threadIdx.x; j < g.samples; j += kRedBlock) {
+      const double d = static_cast<double>(x[channel_index(g, c, j)]) - k;
+      sum += d;
+      sq += d * d;
+    }
   }
-  block_sum2(sum, sq, lds);
-  if (threadIdx.x == 0) {
-    const Moments r = forward_moments(make_double2(sum, sq), shift, g.samples, out.epsilon);
-    write_forward_outputs(out, c, r);
-    stats[0] = r.mean;
-    stats[1] = r.inv;
-  }
-  __syncthreads();
-  const float mu = stats[0], inv = stats[1], w = weight[c], b = bias[c];
-  for (uint32_t j = threadIdx.x; j < g.samples; j += kRedBlock) {
-    const uint32_t idx = channel_index(g, c, j);
-    float v = (x[idx] - mu) * inv * w + b;  // evaluation.rs:590-595
+  block_sum2_all(sum, sq, lds);
+  const Moments r = forward_moments(make_double2(sum, sq), shift, g.samples, out.epsilon);
+  if (threadIdx.x == 0) write_forward_outputs(out, c, r);
+  const float mu = r.mean, inv = r.inv, w = weight[c], b = bias[c];
+  auto apply = [&](float v) {
+    v = (v - mu) * inv * w + b;  // evaluation.rs:590-595
     if constexpr (Relu) v = v > 0.0f ? v : 0.0f;
-    y[idx] = v;
+    return v;
+  };
+  if constexpr (Keep) {
+#pragma unroll
+    for (int u = 0; u < kChannelKeep; ++u)
+      if (threadIdx.x + u * kRedBlock < g.samples) y[at[u]] = apply(kept[u]);
+  } else {
+    for (uint32_t j = threadIdx.x; j < g.samples; j += kRedBlock) {
+      const uint32_t idx = channel_index(g, c, j);
+      y[idx] = apply(x[idx]);
+    }
   }
 }
 
 // With DxSum, the block also sums the dx it writes (fp64, fixed order) into dx_sum[c]: the
 // bias gradient of a convolution whose output is this BatchNorm's input (autograd.rs:412-527
 // reduces the same values over (n, y, x) in a pass of its own).
-template <bool Relu, bool DxSum>
+template <bool Relu, bool DxSum, bool Keep>
 __global__ __launch_bounds__(kRedBlock) void bn_channel_backward_kernel(
     ChannelGeom g, const float *__restrict__ grad, const float *__restrict__ relu_out,
     const float *__restrict__ x, const float *__restrict__ weight, const float *__restrict__ mean,
     const float *__restrict__ inverse_std, float *__restrict__ dx, float *__restrict__ dweight,
     float *__restrict__ dbias, float *__restrict__ dx_sum) {
-  __shared__ double lds[2][kRedWaves];
-  __shared__ float sums[2];
+  __shared__ double lds[2][2][kRedWaves];  // one region per block sum
   const uint32_t c = blockIdx.x;
   const float mu = mean[c], inv = inverse_std[c];
   double sg = 0.0, sgx = 0.0;
-  for (uint32_t j = threadIdx.x; j < g.samples; j += kRedBlock) {
-    const uint32_t idx = channel_index(g, c, j);
-    float gv = grad[idx];
-    if constexpr (Relu) gv = relu_masked(gv, relu_out[idx]);
-    const float nv = (x[idx] - mu) * inv;
-    sg += static_cast<double>(gv);
-    sgx += static_cast<double>(gv * nv);
+  float kg[Keep ? kChannelKeep : 1], kn[Keep ? kChannelKeep : 1];
+  uint32_t at[Keep ? kChannelKeep : 1];
+  if constexpr (Keep) {
+#pragma unroll
+    for (int u = 0; u < kChannelKeep; ++u) {
+      const uint32_t j = threadIdx.x + u * kRedBlock;
+      at[u] = j < g.samples ? channel_index(g, c, j) : 0;
+      float gv = grad[at[u]];
+      if constexpr (Relu) gv = relu_masked(gv, relu_out[at[u]]);
+      kg[u] = gv;
+      kn[u] = (x[at[u]] - mu) * inv;
+    }
+#pragma unroll
+    for (int u = 0; u < kChannelKeep; ++u) {
+      if (threadIdx.x + u * kRedBlock >= g.samples) break;
+      sg += static_cast<double>(kg[u]);
+      sgx += static_cast<double>(kg[u] * kn[u]);
+    }
+  } else {
+    for (uint32_t j = threadIdx.x; j < g.samples; j += kRedBlock) {
+      const uint32_t idx = channel_index(g, c, j);
+      float gv = grad[idx];
+      if constexpr (Relu) gv = relu_masked(gv, relu_out[idx]);
+      const float nv = (x[idx] - mu) * inv;
+      sg += static_cast<double>(gv);
+      sgx += static_cast<double>(gv * nv);
+    }
   }
-  block_sum2(sg, sgx, lds);
+  block_sum2_all(sg, sgx, lds[0]);
+  const float sgf = static_cast<float>(sg), sgxf = static_cast<float>(sgx);
   if (threadIdx.x == 0) {
-    sums[0] = static_cast<float>(sg);
-    sums[1] = static_cast<float>(sgx);
-    dbias[c] = sums[0];
-    dweight[c] = sums[1];
+    dbias[c] = sgf;
+    dweight[c] = sgxf;
   }
-  __syncthreads();
   // autograd.rs:344-373: ((w * inv) / M) * ((M * g - sum_g) - x_hat * sum_g_xhat)
   const float samples = static_cast<float>(g.samples);
-  const float coef = weight[c] * inv / samples, sgf = sums[0], sgxf = sums[1];
+  const float coef = weight[c] * inv / samples;
   double total = 0.0, unused = 0.0;
-  for (uint32_t j = threadIdx.x; j < g.samples; j += kRedBlock) {
-    const uint32_t idx = channel_index(g, c, j);
-    float gv = grad[idx];
-    if constexpr (Relu) gv = relu_masked(gv, relu_out[idx]);
-    const float normalized = (x[idx] - mu) * inv;
-    const float d = coef * (samples * gv - sgf - normalized * sgxf);
-    dx[idx] = d;
-    if constexpr (DxSum) total += static_cast<double>(d);
+  if constexpr (Keep) {
+#pragma unroll
+    for (int u = 0; u < kChannelKeep; ++u) {
+      if (threadIdx.x + u * kRedBlock >= g.samples) break;
+      const float d = coef * (samples * kg[u] - sgf - kn[u] * sgxf);
+      dx[at[u]] = d;
+      if constexpr (DxSum) total += static_cast<double>(d);
+    }
+  } else {
+    for (uint32_t j = threadIdx.x; j < g.samples; j += kRedBlock) {
+      const uint32_t idx = channel_index(g, c, j);
+      float gv = grad[idx];
+      if constexpr (Relu) gv = relu_masked(gv, relu_out[idx]);
+      const float normalized = (x[idx] - mu) * inv;
+      const float d = coef * (samples * gv - sgf - normalized * sgxf);
+      dx[idx] = d;
+      if constexpr (DxSum) total += static_cast<double>(d);
+    }
   }
   if constexpr (DxSum) {
-    block_sum2(total, unused, lds);  // lds is free again: sums[] was read after a barrier
+    block_sum2_all(total, unused, lds[1]);
     if (threadIdx.x == 0) dx_sum[c] = static_cast<float>(total);
   }
 }
@@ -1100,12 +1174,13 @@ oxh_status forward_train_impl(const char *name, oxh_stream stream, uint64_t batc
   const StatsOut stats{saved_mean, saved_inverse_std, nullptr, running_mean, running_variance,
                        momentum, epsilon};
   const ChannelGeom cg = make_channel_geom(batch, channels, spatial);
-  if (relu)
-    oxh::launch(bn_channel_forward_kernel<true>, dim3(cg.channels), dim3(kRedBlock), 0,
-                oxh::as_stream(stream), cg, input, weight, bias, stats, output);
-  else
-    oxh::launch(bn_channel_forward_kernel<false>, dim3(cg.channels), dim3(kRedBlock), 0,
-                oxh::as_stream(stream), cg, input, weight, bias, stats, output);
+  const bool keep = cg.samples <= static_cast<uint32_t>(kRedBlock * kChannelKeep);
+  auto kernel = relu ? (keep ? bn_channel_forward_kernel<true, true>
+                             : bn_channel_forward_kernel<true, false>)
+                     : (keep ? bn_channel_forward_kernel<false, true>
+                             : bn_channel_forward_kernel<false, false>);
+  oxh::launch(kernel, dim3(cg.channels), dim3(kRedBlock), 0, oxh::as_stream(stream), cg, input,
+              weight, bias, stats, output);
   return oxh::launched(name);
 }
 
@@ -1150,10 +1225,18 @@ oxh_status backward_train_impl(const char *name, oxh_stream stream, uint64_t bat
   st = no_overlap(name, input_gradient, bytes, {input, gradient, relu_out}, bytes);
   if (st != OXH_OK) return st;
   const ChannelGeom cg = make_channel_geom(batch, channels, spatial);
-  auto kernel = relu_out ? (input_gradient_sum ? bn_channel_backward_kernel<true, true>
-                                               : bn_channel_backward_kernel<true, false>)
-                         : (input_gradient_sum ? bn_channel_backward_kernel<false, true>
-                                               : bn_channel_backward_kernel<false, false>);
+  const bool keep = cg.samples <= static_cast<uint32_t>(kRedBlock * kChannelKeep);
+  using K = decltype(&bn_channel_backward_kernel<true, true, true>);
+  const K kernels[2][2][2] = {
+      {{bn_channel_backward_kernel<false, false, false>,
+        bn_channel_backward_kernel<false, false, true>},
+       {bn_channel_backward_kernel<false, true, false>,
+        bn_channel_backward_kernel<false, true, true>}},
+      {{bn_channel_backward_kernel<true, false, false>,
+        bn_channel_backward_kernel<true, false, true>},
+       {bn_channel_backward_kernel<true, true, false>,
+        bn_channel_backward_kernel<true, true, true>}}};
+  const K kernel = kernels[relu_out != nullptr][input_gradient_sum != nullptr][keep];
   oxh::launch(kernel, dim3(cg.channels), dim3(kRedBlock), 0, oxh::as_stream(stream), cg,
               gradient, relu_out, input, weight, saved_mean, saved_inverse_std, input_gradient,
               weight_gradient, bias_gradient, input_gradient_sum);

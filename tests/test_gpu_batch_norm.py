@@ -64,6 +64,11 @@ SHAPES = [
     (128, 32, 14, 14), # config 5's largest BN tensor
     (4, 300, 3, 5),    # many channels, odd spatial
     (2, 1, 256, 256),  # one channel, many slices
+    # one block per channel: values kept in registers (<= 2048 per channel) or read twice
+    (128, 96, 2, 2),
+    (128, 64, 4, 4),   # exactly 2048 values per channel
+    (129, 8, 4, 4),    # 2064: read twice
+    (64, 8, 7, 7),
 ]
 
 
@@ -197,7 +202,7 @@ def test_batch_norm_workspace_reuse_and_repeat(module, dev):
 
 @pytest.mark.parametrize("shape", [(2, 3, 4, 4), (5, 4, 7, 7), (128, 96, 2, 2), (128, 1280, 1, 1),
                                    (64, 32, 4, 4), (7, 16, 14, 14), (128, 32, 14, 14),
-                                   (3, 5, 3, 3)])
+                                   (3, 5, 3, 3), (64, 8, 7, 7), (128, 4, 4, 4)])
 def test_batch_norm_relu_fused_matches_unfused(module, dev, shape):
     """ConvNormAct's BN + ReLU in one launch per direction: the fused forward equals the ReLU
     kernel applied to the unfused forward, and the fused backward equals the unfused backward
@@ -246,7 +251,7 @@ def test_batch_norm_relu_fused_matches_unfused(module, dev, shape):
 
 
 @pytest.mark.parametrize("shape", [(2, 3, 4, 4), (128, 96, 2, 2), (128, 1280, 1, 1),
-                                   (128, 32, 14, 14), (3, 5, 3, 3)])
+                                   (128, 32, 14, 14), (3, 5, 3, 3), (64, 8, 7, 7)])
 @pytest.mark.parametrize("relu", [False, True])
 def test_conv_batch_norm_backward_writes_conv_bias(module, dev, shape, relu):
     """The BatchNorm backward that also reduces its input gradient per channel (the bias
