@@ -734,10 +734,13 @@ __device__ __forceinline__ void block_sum2_all(double &a, double &b, double (*ld
 // channels read their values again (L2).
 constexpr int kChannelKeep = 8;
 
+// addend (may be null; never with Relu): y = BN(x) + addend, the residual add that follows a
+// block's last BatchNorm, in the same pass.
 template <bool Relu, bool Keep>
 __global__ __launch_bounds__(kRedBlock) void bn_channel_forward_kernel(
     ChannelGeom g, const float *__restrict__ x, const float *__restrict__ weight,
-    const float *__restrict__ bias, StatsOut out, float *__restrict__ y) {
+    const float *__restrict__ bias, StatsOut out, const float *__restrict__ addend,
+    float *__restrict__ y) {
   __shared__ double lds[2][kRedWaves];
   const uint32_t c = blockIdx.x;
   const float shift = x[static_cast<uint64_t>(c) * g.spatial];  // x[0, c, 0]
@@ -778,11 +781,15 @@ __global__ __launch_bounds__(kRedBlock) void bn_channel_forward_kernel(
   if constexpr (Keep) {
 #pragma unroll
     for (int u = 0; u < kChannelKeep; ++u)
-      if (threadIdx.x + u * kRedBlock < g.samples) y[at[u]] = apply(kept[u]);
+      if (threadIdx.x + u * kRedBlock < g.samples) {
+        const float v = apply(kept[u]);
+        y[at[u]] = addend != nullptr ? v + addend[at[u]] : v;
+      }
   } else {
     for (uint32_t j = threadIdx.x; j < g.samples; j += kRedBlock) {
       const uint32_t idx = channel_index(g, c, j);
-      y[idx] = apply(x[idx]);
+      const float v = apply(x[idx]);
+      y[idx] = addend != nullptr ? v + addend[idx] : v;
     }
   }
 }
@@ -1147,14 +1154,17 @@ oxh_status forward_train_impl(const char *name, oxh_stream stream, uint64_t batc
                               float epsilon, const float *input, const float *weight,
                               const float *bias, float *running_mean, float *running_variance,
                               float *saved_mean, float *saved_inverse_std, float *output,
-                              void *workspace, uint64_t workspace_bytes, bool relu) {
+                              void *workspace, uint64_t workspace_bytes, bool relu,
+                              const float *addend = nullptr) {
   if (!use_channel(batch, channels, spatial)) {
     oxh_status st = launch_reduce_x(name, stream, batch, channels, spatial, input, workspace,
                                     workspace_bytes, nullptr);
     if (st != OXH_OK) return st;
-    return forward_apply_impl(name, stream, batch, channels, spatial, momentum, epsilon, input,
-                              weight, bias, running_mean, running_variance, saved_mean,
-                              saved_inverse_std, output, workspace, workspace_bytes, relu);
+    st = forward_apply_impl(name, stream, batch, channels, spatial, momentum, epsilon, input,
+                            weight, bias, running_mean, running_variance, saved_mean,
+                            saved_inverse_std, output, workspace, workspace_bytes, relu);
+    if (st != OXH_OK || addend == nullptr) return st;
+    return oxh_add(stream, output, addend, output, batch * channels * spatial);
   }
   OXH_REQUIRE(std::isfinite(momentum) && std::isfinite(epsilon) && epsilon >= 0.0f,
               OXH_INVALID_SHAPE, std::string(name) + ": bad momentum or epsilon");
@@ -1180,7 +1190,7 @@ oxh_status forward_train_impl(const char *name, oxh_stream stream, uint64_t batc
                      : (keep ? bn_channel_forward_kernel<false, true>
                              : bn_channel_forward_kernel<false, false>);
   oxh::launch(kernel, dim3(cg.channels), dim3(kRedBlock), 0, oxh::as_stream(stream), cg, input,
-              weight, bias, stats, output);
+              weight, bias, stats, addend, output);
   return oxh::launched(name);
 }
 
@@ -1451,6 +1461,24 @@ oxh_status oxh_batch_norm_relu_forward_train(oxh_stream stream, uint64_t batch,
                             spatial, momentum, epsilon, input, weight, bias, running_mean,
                             running_variance, saved_mean, saved_inverse_std, output, workspace,
                             workspace_bytes, true);
+}
+
+oxh_status oxh_batch_norm_add_forward_train(oxh_stream stream, uint64_t batch, uint64_t channels,
+                                            uint64_t spatial, float momentum, float epsilon,
+                                            const float *input, const float *weight,
+                                            const float *bias, float *running_mean,
+                                            float *running_variance, float *saved_mean,
+                                            float *saved_inverse_std, const float *addend,
+                                            float *output, void *workspace,
+                                            uint64_t workspace_bytes) {
+  const char *name = "oxh_batch_norm_add_forward_train";
+  OXH_REQUIRE(addend != nullptr, OXH_INVALID_SHAPE, std::string(name) + ": null addend");
+  const uint64_t bytes = batch * channels * spatial * 4;
+  OXH_REQUIRE(!oxh::any_overlap(output, bytes, addend, bytes), OXH_INVALID_SHAPE,
+              std::string(name) + ": output overlaps the addend");
+  return forward_train_impl(name, stream, batch, channels, spatial, momentum, epsilon, input,
+                            weight, bias, running_mean, running_variance, saved_mean,
+                            saved_inverse_std, output, workspace, workspace_bytes, false, addend);
 }
 
 oxh_status oxh_batch_norm_relu_backward_train(oxh_stream stream, uint64_t batch,

@@ -566,6 +566,20 @@ oxh_status build_trainer(oxh_trainer &t) {
       fused_bn[x.in[0]] = 1;
     }
   }
+  // a BN (without ReLU) whose only consumer is a residual add, as the add's first operand:
+  // its forward writes the add's output (BN + shortcut) and the add launches nothing
+  std::vector<int64_t> bn_into_add(n, -1);
+  std::vector<char> add_absorbed(n, 0);
+  for (size_t i = 0; i < n; ++i) {
+    const Node &x = g.nodes[i];
+    if (x.op != Op::Add) continue;
+    const int first = x.in[0];
+    if (g.nodes[first].op == Op::Bn && !fused_bn[first] && consumers[first] == 1 &&
+        x.in[1] != first) {
+      bn_into_add[first] = static_cast<int64_t>(i);
+      add_absorbed[i] = 1;
+    }
+  }
   // gradient buffers, consumers before producers
   std::vector<int64_t> grad_of(n, -1);  // node whose grad buffer this node uses (-1: own)
   std::vector<char> has_grad(n, 0), aliased(n, 0);
@@ -722,7 +736,7 @@ oxh_status build_trainer(oxh_trainer &t) {
   for (size_t i = 0; i < n; ++i) {
     const Node &x = g.nodes[i];
     if (x.op == Op::Param || x.op == Op::Input || x.op == Op::Targets || x.op == Op::Reshape ||
-        fused_bn[i])
+        fused_bn[i] || add_absorbed[i])
       continue;
     float *out = t.value[i];
     OpRec op;
@@ -762,6 +776,27 @@ oxh_status build_trainer(oxh_trainer &t) {
         const float *xi = t.value[bn.in[0]], *w = t.value[bn.in[1]], *b = t.value[bn.in[2]];
         float *sm = t.saved_mean[bi], *si = t.saved_inv[bi], *rm = bs.rm, *rv = bs.rv;
         const uint64_t N = bn.shape[0], C = bn.shape[1], HW = bn.shape[2] * bn.shape[3];
+        if (!fused && bn_into_add[i] >= 0) {  // BN + residual add in one launch
+          const Node &ad = g.nodes[bn_into_add[i]];
+          const float *skip = t.value[ad.in[1]];
+          float *sum = t.value[bn_into_add[i]];
+          op.kind = "batch_norm2d_add_forward";
+          op.name = name("bn", bi) + "+" + name("add", bn_into_add[i]);
+          op.tensors = {ref("x", const_cast<float *>(xi), g.nodes[bn.in[0]], 0),
+                        ref("weight", const_cast<float *>(w), g.nodes[bn.in[1]], 0),
+                        ref("bias", const_cast<float *>(b), g.nodes[bn.in[2]], 0),
+                        ref("addend", const_cast<float *>(skip), g.nodes[ad.in[1]], 0),
+                        ref("y", sum, ad, 1), ref_flat("saved_mean", sm, C, 1),
+                        ref_flat("saved_inverse_std", si, C, 1),
+                        ref_flat("running_mean", rm, C, 2), ref_flat("running_variance", rv, C, 2)};
+          op.attrs = {{"momentum", kBnMomentum}, {"epsilon", kBnEpsilon}};
+          op.launch = [=](hipStream_t st) {
+            return oxh_batch_norm_add_forward_train(st, N, C, HW, kBnMomentum, kBnEpsilon, xi, w,
+                                                    b, rm, rv, sm, si, skip, sum, ws, wsb);
+          };
+          ops.push_back(std::move(op));
+          break;
+        }
         op.kind = fused ? "batch_norm2d_relu_forward" : "batch_norm2d_forward";
         op.name = fused ? name("bn", bi) + "+" + name("relu", i) : name("bn", bi);
         op.tensors = {ref("x", const_cast<float *>(xi), g.nodes[bn.in[0]], 0),

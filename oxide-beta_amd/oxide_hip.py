@@ -135,6 +135,8 @@ _SIGNATURES = {
                                                 _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u64]),
     "oxh_batch_norm_relu_backward_train": (_st, [_vp, _u64, _u64, _u64, _vp, _vp, _vp, _vp, _vp,
                                                  _vp, _vp, _vp, _vp, _vp, _u64]),
+    "oxh_batch_norm_add_forward_train": (_st, [_vp, _u64, _u64, _u64, _f32, _f32, _vp, _vp, _vp,
+                                               _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u64]),
     "oxh_conv_batch_norm_backward_train": (_st, [_vp, _u64, _u64, _u64, _vp, _vp, _vp, _vp, _vp,
                                                  _vp, _vp, _vp, _vp, _vp, _vp, _u64]),
     "oxh_cross_entropy_workspace_size": (_st, [_u64, _u64, ctypes.POINTER(_u64)]),
@@ -576,6 +578,17 @@ class LoadedModule:
             _stream(stream), n, c, h * w, _ptr(gradient), _ptr(out), _ptr(x), _ptr(weight),
             _ptr(saved_mean), _ptr(saved_inverse_std), _ptr(input_gradient),
             _ptr(weight_gradient), _ptr(bias_gradient), ws, wsb))
+
+    def batch_norm_add_forward_train(self, x, weight, bias, running_mean, running_variance,
+                                     saved_mean, saved_inverse_std, addend, out, momentum=0.1,
+                                     epsilon=1e-5, stream=None):
+        """BatchNorm training forward followed by the residual add: ``out`` = BN(x) + addend."""
+        n, c, h, w = x.shape
+        ws, wsb = self._bn_ws_args(n, c, h * w)
+        check(lib().oxh_batch_norm_add_forward_train(
+            _stream(stream), n, c, h * w, momentum, epsilon, _ptr(x), _ptr(weight), _ptr(bias),
+            _ptr(running_mean), _ptr(running_variance), _ptr(saved_mean),
+            _ptr(saved_inverse_std), _ptr(addend), _ptr(out), ws, wsb))
 
     def conv_batch_norm_backward_train(self, gradient, relu_out, x, weight, saved_mean,
                                        saved_inverse_std, input_gradient, weight_gradient,

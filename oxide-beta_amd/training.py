@@ -471,6 +471,8 @@ def op_bytes(op: Op) -> tuple[str, int]:
     k = op.kind
     if k in ("batch_norm2d_forward", "batch_norm2d_relu_forward"):
         return "batch_norm2d", 2 * nb(op.reads["x"])                       # x in, y out
+    if k == "batch_norm2d_add_forward":
+        return "batch_norm2d", 3 * nb(op.reads["x"])                       # x, shortcut in; y out
     if k == "batch_norm2d_backward":
         return "batch_norm2d", 3 * nb(op.reads["x"]) + acc                 # g, x in; dx out
     if k == "batch_norm2d_relu_backward":

@@ -287,3 +287,39 @@ def test_conv_batch_norm_backward_writes_conv_bias(module, dev, shape, relu):
     with pytest.raises(ox.OxideError) as e:
         module.conv_batch_norm_backward_train(dg_, y, dx_, dw_, mean, inv, gx2, gw2, gb2, None)
     assert e.value.status == ox.INVALID_SHAPE
+
+
+@pytest.mark.parametrize("shape", [(128, 96, 2, 2), (128, 128, 1, 1), (64, 8, 7, 7),
+                                   (7, 16, 14, 14), (3, 5, 3, 3)])
+def test_batch_norm_add_fused_matches_unfused(module, dev, shape):
+    """BatchNorm forward + residual add in one pass: the output equals the add kernel applied to
+    the plain forward's output bit for bit, with identical statistics, on the
+    one-block-per-channel path (values kept or read twice) and the reduce + map path."""
+    r = np.random.default_rng(hash(shape) & 0xFFFF)
+    x, gamma, beta, _ = _case(r, shape, 1.1, 0.4)
+    c = shape[1]
+    skip = r.standard_normal(shape).astype(np.float32)
+    rm = r.uniform(-0.5, 0.5, c).astype(np.float32)
+    rv = r.uniform(0.5, 2.0, c).astype(np.float32)
+    dx_, dw_, db_, ds_ = to_dev(x, dev), to_dev(gamma, dev), to_dev(beta, dev), to_dev(skip, dev)
+
+    def stats():
+        return (to_dev(rm, dev), to_dev(rv, dev), torch.empty(c, device=dev),
+                torch.empty(c, device=dev))
+
+    rm1, rv1, m1, i1 = stats()
+    y = torch.empty_like(dx_)
+    module.batch_norm_forward_train(dx_, dw_, db_, rm1, rv1, m1, i1, y, 0.1, 1e-5)
+    unfused = torch.empty_like(dx_)
+    module.add(y, ds_, unfused)
+    rm2, rv2, m2, i2 = stats()
+    fused = torch.empty_like(dx_)
+    module.batch_norm_add_forward_train(dx_, dw_, db_, rm2, rv2, m2, i2, ds_, fused)
+    torch.cuda.synchronize()
+    for a, b, what in ((fused, unfused, "y + skip"), (m2, m1, "mean"), (i2, i1, "inv"),
+                       (rm2, rm1, "running mean"), (rv2, rv1, "running variance")):
+        np.testing.assert_array_equal(host(a), host(b), err_msg=what)
+    check_batch_norm_forward(dict(y=host(y), mean=host(m1), inv=host(i1), rm=host(rm1),
+                                  rv=host(rv1)), x, gamma, beta, rm, rv)
+    with pytest.raises(ox.OxideError):
+        module.batch_norm_add_forward_train(dx_, dw_, db_, rm2, rv2, m2, i2, fused, fused)

@@ -101,6 +101,21 @@ class OracleChecker:
                                  self.prior[id(a["running_variance"])], a["momentum"],
                                  a["epsilon"])
 
+    def batch_norm2d_add_forward(self, op, r):
+        """BN forward writing BN(x) + shortcut: the statistics against the oracle, the output
+        equal to the fp32 normalization with those statistics followed by the add."""
+        a, w = op.attrs, op.writes
+        x, gamma, beta = r["x"], r["weight"], r["bias"]
+        mean, inv = host(w["saved_mean"]), host(w["saved_inverse_std"])
+        sh = (1, x.shape[1], 1, 1)
+        y_bn = ((x - mean.reshape(sh)) * inv.reshape(sh)) * gamma.reshape(sh) + beta.reshape(sh)
+        out = dict(y=y_bn, mean=mean, inv=inv, rm=host(a["running_mean"]),
+                   rv=host(a["running_variance"]))
+        check_batch_norm_forward(out, x, gamma, beta, self.prior[id(a["running_mean"])],
+                                 self.prior[id(a["running_variance"])], a["momentum"],
+                                 a["epsilon"])
+        assert_bitexact(host(w["y"]), oracle.add(y_bn, r["addend"]), op.name)
+
     def batch_norm2d_backward(self, op, r):
         w = op.writes
         out = dict(dx=host(w["contribution"]), dw=host(w["weight_gradient"]),
@@ -177,12 +192,14 @@ class OracleChecker:
 
 # 46 BatchNorms, 32 of them followed by a ReLU (fused), each fed by a convolution whose bias
 # gradient its backward forms (the classifier's, fed by no BN, stays with its parameter
-# backward); 10 residual adds, whose first operand's gradient is the add's own buffer and whose
-# second operand's is added by that operand's convolution input backward (no add launches)
+# backward); 10 residual adds, formed by the forward of the BN feeding them, whose first
+# operand's gradient is the add's own buffer and whose second operand's is added by that
+# operand's convolution input backward (no add launches in either direction)
 EXPECTED_KINDS = {"conv2d_forward": 47, "conv2d_parameter_backward": 47,
-                  "conv2d_input_backward": 46, "batch_norm2d_forward": 14,
+                  "conv2d_input_backward": 46, "batch_norm2d_forward": 4,
+                  "batch_norm2d_add_forward": 10,
                   "batch_norm2d_relu_forward": 32, "batch_norm2d_backward": 14,
-                  "batch_norm2d_relu_backward": 32, "add_forward": 10,
+                  "batch_norm2d_relu_backward": 32,
                   "conv input backward with addend": 10,
                   "avg_pool2d_forward": 1, "avg_pool2d_backward": 1, "cross_entropy": 1,
                   "adamw": 1, "conv bias in parameter backward": 1,
