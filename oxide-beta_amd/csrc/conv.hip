@@ -1116,6 +1116,10 @@ Operand operand(const float *ptr, Axis row, Axis k) {
 }
 
 
+#ifndef OXH_SINGLE_K
+#define OXH_SINGLE_K 1024  // weight gradients with at most this many k terms: one pass, no chunks
+#endif
+
 // k chunks of the pointwise weight gradient: about 512 blocks in total, at least 64 k per
 // chunk, every chunk non-empty.
 struct KSplit {
@@ -1126,6 +1130,7 @@ KSplit product_split(const ConvGeom &g) {
                          ((g.in_c + kTile - 1) / kTile);
   const uint64_t k = static_cast<uint64_t>(g.batch) * g.h * g.w;
   const uint64_t weights = static_cast<uint64_t>(g.out_c) * g.in_c;
+  if (k <= OXH_SINGLE_K) return KSplit{1, static_cast<uint32_t>(k)};
   uint64_t c = (512 + tiles - 1) / tiles;
   const uint64_t by_work = k / 64 > 0 ? k / 64 : 1;
   if (c > by_work) c = by_work;
