@@ -709,9 +709,10 @@ __device__ __forceinline__ uint32_t channel_index(const ChannelGeom &g, uint32_t
 }
 
 // Block-wide sums of two doubles, the total in every thread: each wave's butterfly total goes
-// to LDS and every thread adds the kRedWaves wave totals in the same order (one barrier, no
+// to LDS and every thread adds the Waves wave totals in the same order (one barrier, no
 // broadcast step).  `lds` must not be in use by another sum of the same block.
-__device__ __forceinline__ void block_sum2_all(double &a, double &b, double (*lds)[kRedWaves]) {
+template <int Waves>
+__device__ __forceinline__ void block_sum2_all(double &a, double &b, double (*lds)[Waves]) {
   a = wave_sum(a);
   b = wave_sum(b);
   const int wave = threadIdx.x / 64;
@@ -723,25 +724,30 @@ __device__ __forceinline__ void block_sum2_all(double &a, double &b, double (*ld
   a = 0.0;
   b = 0.0;
 #pragma unroll
-  for (int w = 0; w < kRedWaves; ++w) {
+  for (int w = 0; w < Waves; ++w) {
     a += lds[0][w];
     b += lds[1][w];
   }
 }
 
 // Up to kChannelKeep values per thread stay in registers between a channel kernel's sum pass
-// and its elementwise pass (config 5's planes hold at most 2048 values per channel); larger
-// channels read their values again (L2).
+// and its elementwise pass; larger channels read their values again (L2).  Blocks have 256
+// threads, or 1024 when there are few channels (a block per channel would leave most CUs
+// idle), so config 5's channels (at most 6272 values) all keep their values.
 constexpr int kChannelKeep = 8;
+
+int channel_threads(const ChannelGeom &g) {
+  return g.channels <= 128 && g.samples > 256 * kChannelKeep ? 1024 : 256;
+}
 
 // addend (may be null; never with Relu): y = BN(x) + addend, the residual add that follows a
 // block's last BatchNorm, in the same pass.
-template <bool Relu, bool Keep>
-__global__ __launch_bounds__(kRedBlock) void bn_channel_forward_kernel(
+template <bool Relu, bool Keep, int Threads>
+__global__ __launch_bounds__(Threads) void bn_channel_forward_kernel(
     ChannelGeom g, const float *__restrict__ x, const float *__restrict__ weight,
     const float *__restrict__ bias, StatsOut out, const float *__restrict__ addend,
     float *__restrict__ y) {
-  __shared__ double lds[2][kRedWaves];
+  __shared__ double lds[2][Threads / 64];
   const uint32_t c = blockIdx.x;
   const float shift = x[static_cast<uint64_t>(c) * g.spatial];  // x[0, c, 0]
   const double k = static_cast<double>(shift);
@@ -751,25 +757,25 @@ __global__ __launch_bounds__(kRedBlock) void bn_channel_forward_kernel(
   if constexpr (Keep) {
 #pragma unroll
     for (int u = 0; u < kChannelKeep; ++u) {
-      const uint32_t j = threadIdx.x + u * kRedBlock;
+      const uint32_t j = threadIdx.x + u * Threads;
       at[u] = j < g.samples ? channel_index(g, c, j) : 0;
       kept[u] = x[at[u]];
     }
 #pragma unroll
     for (int u = 0; u < kChannelKeep; ++u) {
-      if (threadIdx.x + u * kRedBlock >= g.samples) break;
+      if (threadIdx.x + u * Threads >= g.samples) break;
       const double d = static_cast<double>(kept[u]) - k;
       sum += d;
       sq += d * d;
     }
   } else {
-    for (uint32_t j = threadIdx.x; j < g.samples; j += kRedBlock) {
+    for (uint32_t j = threadIdx.x; j < g.samples; j += Threads) {
       const double d = static_cast<double>(x[channel_index(g, c, j)]) - k;
       sum += d;
       sq += d * d;
     }
   }
-  block_sum2_all(sum, sq, lds);
+  block_sum2_all<Threads / 64>(sum, sq, lds);
   const Moments r = forward_moments(make_double2(sum, sq), shift, g.samples, out.epsilon);
   if (threadIdx.x == 0) write_forward_outputs(out, c, r);
   const float mu = r.mean, inv = r.inv, w = weight[c], b = bias[c];
@@ -781,12 +787,12 @@ __global__ __launch_bounds__(kRedBlock) void bn_channel_forward_kernel(
   if constexpr (Keep) {
 #pragma unroll
     for (int u = 0; u < kChannelKeep; ++u)
-      if (threadIdx.x + u * kRedBlock < g.samples) {
+      if (threadIdx.x + u * Threads < g.samples) {
         const float v = apply(kept[u]);
         y[at[u]] = addend != nullptr ? v + addend[at[u]] : v;
       }
   } else {
-    for (uint32_t j = threadIdx.x; j < g.samples; j += kRedBlock) {
+    for (uint32_t j = threadIdx.x; j < g.samples; j += Threads) {
       const uint32_t idx = channel_index(g, c, j);
       const float v = apply(x[idx]);
       y[idx] = addend != nullptr ? v + addend[idx] : v;
@@ -797,13 +803,13 @@ __global__ __launch_bounds__(kRedBlock) void bn_channel_forward_kernel(
 // With DxSum, the block also sums the dx it writes (fp64, fixed order) into dx_sum[c]: the
 // bias gradient of a convolution whose output is this BatchNorm's input (autograd.rs:412-527
 // reduces the same values over (n, y, x) in a pass of its own).
-template <bool Relu, bool DxSum, bool Keep>
-__global__ __launch_bounds__(kRedBlock) void bn_channel_backward_kernel(
+template <bool Relu, bool DxSum, bool Keep, int Threads>
+__global__ __launch_bounds__(Threads) void bn_channel_backward_kernel(
     ChannelGeom g, const float *__restrict__ grad, const float *__restrict__ relu_out,
     const float *__restrict__ x, const float *__restrict__ weight, const float *__restrict__ mean,
     const float *__restrict__ inverse_std, float *__restrict__ dx, float *__restrict__ dweight,
     float *__restrict__ dbias, float *__restrict__ dx_sum) {
-  __shared__ double lds[2][2][kRedWaves];  // one region per block sum
+  __shared__ double lds[2][2][Threads / 64];  // one region per block sum
   const uint32_t c = blockIdx.x;
   const float mu = mean[c], inv = inverse_std[c];
   double sg = 0.0, sgx = 0.0;
@@ -812,7 +818,7 @@ __global__ __launch_bounds__(kRedBlock) void bn_channel_backward_kernel(
   if constexpr (Keep) {
 #pragma unroll
     for (int u = 0; u < kChannelKeep; ++u) {
-      const uint32_t j = threadIdx.x + u * kRedBlock;
+      const uint32_t j = threadIdx.x + u * Threads;
       at[u] = j < g.samples ? channel_index(g, c, j) : 0;
       float gv = grad[at[u]];
       if constexpr (Relu) gv = relu_masked(gv, relu_out[at[u]]);
@@ -821,12 +827,12 @@ __global__ __launch_bounds__(kRedBlock) void bn_channel_backward_kernel(
     }
 #pragma unroll
     for (int u = 0; u < kChannelKeep; ++u) {
-      if (threadIdx.x + u * kRedBlock >= g.samples) break;
+      if (threadIdx.x + u * Threads >= g.samples) break;
       sg += static_cast<double>(kg[u]);
       sgx += static_cast<double>(kg[u] * kn[u]);
     }
   } else {
-    for (uint32_t j = threadIdx.x; j < g.samples; j += kRedBlock) {
+    for (uint32_t j = threadIdx.x; j < g.samples; j += Threads) {
       const uint32_t idx = channel_index(g, c, j);
       float gv = grad[idx];
       if constexpr (Relu) gv = relu_masked(gv, relu_out[idx]);
@@ -835,7 +841,7 @@ __global__ __launch_bounds__(kRedBlock) void bn_channel_backward_kernel(
       sgx += static_cast<double>(gv * nv);
     }
   }
-  block_sum2_all(sg, sgx, lds[0]);
+  block_sum2_all<Threads / 64>(sg, sgx, lds[0]);
   const float sgf = static_cast<float>(sg), sgxf = static_cast<float>(sgx);
   if (threadIdx.x == 0) {
     dbias[c] = sgf;
@@ -848,13 +854,13 @@ __global__ __launch_bounds__(kRedBlock) void bn_channel_backward_kernel(
   if constexpr (Keep) {
 #pragma unroll
     for (int u = 0; u < kChannelKeep; ++u) {
-      if (threadIdx.x + u * kRedBlock >= g.samples) break;
+      if (threadIdx.x + u * Threads >= g.samples) break;
       const float d = coef * (samples * kg[u] - sgf - kn[u] * sgxf);
       dx[at[u]] = d;
       if constexpr (DxSum) total += static_cast<double>(d);
     }
   } else {
-    for (uint32_t j = threadIdx.x; j < g.samples; j += kRedBlock) {
+    for (uint32_t j = threadIdx.x; j < g.samples; j += Threads) {
       const uint32_t idx = channel_index(g, c, j);
       float gv = grad[idx];
       if constexpr (Relu) gv = relu_masked(gv, relu_out[idx]);
@@ -865,7 +871,7 @@ __global__ __launch_bounds__(kRedBlock) void bn_channel_backward_kernel(
     }
   }
   if constexpr (DxSum) {
-    block_sum2_all(total, unused, lds[1]);
+    block_sum2_all<Threads / 64>(total, unused, lds[1]);
     if (threadIdx.x == 0) dx_sum[c] = static_cast<float>(total);
   }
 }
@@ -1184,13 +1190,18 @@ oxh_status forward_train_impl(const char *name, oxh_stream stream, uint64_t batc
   const StatsOut stats{saved_mean, saved_inverse_std, nullptr, running_mean, running_variance,
                        momentum, epsilon};
   const ChannelGeom cg = make_channel_geom(batch, channels, spatial);
-  const bool keep = cg.samples <= static_cast<uint32_t>(kRedBlock * kChannelKeep);
-  auto kernel = relu ? (keep ? bn_channel_forward_kernel<true, true>
-                             : bn_channel_forward_kernel<true, false>)
-                     : (keep ? bn_channel_forward_kernel<false, true>
-                             : bn_channel_forward_kernel<false, false>);
-  oxh::launch(kernel, dim3(cg.channels), dim3(kRedBlock), 0, oxh::as_stream(stream), cg, input,
-              weight, bias, stats, addend, output);
+  const int threads = channel_threads(cg);
+  const bool keep = cg.samples <= static_cast<uint32_t>(threads * kChannelKeep);
+  using K = decltype(&bn_channel_forward_kernel<true, true, 256>);
+  const K kernels[2][2][2] = {
+      {{bn_channel_forward_kernel<false, false, 256>, bn_channel_forward_kernel<false, true, 256>},
+       {bn_channel_forward_kernel<true, false, 256>, bn_channel_forward_kernel<true, true, 256>}},
+      {{bn_channel_forward_kernel<false, false, 1024>,
+        bn_channel_forward_kernel<false, true, 1024>},
+       {bn_channel_forward_kernel<true, false, 1024>,
+        bn_channel_forward_kernel<true, true, 1024>}}};
+  oxh::launch(kernels[threads == 1024][relu][keep], dim3(cg.channels), dim3(threads), 0,
+              oxh::as_stream(stream), cg, input, weight, bias, stats, addend, output);
   return oxh::launched(name);
 }
 
@@ -1235,19 +1246,23 @@ oxh_status backward_train_impl(const char *name, oxh_stream stream, uint64_t bat
   st = no_overlap(name, input_gradient, bytes, {input, gradient, relu_out}, bytes);
   if (st != OXH_OK) return st;
   const ChannelGeom cg = make_channel_geom(batch, channels, spatial);
-  const bool keep = cg.samples <= static_cast<uint32_t>(kRedBlock * kChannelKeep);
-  using K = decltype(&bn_channel_backward_kernel<true, true, true>);
-  const K kernels[2][2][2] = {
-      {{bn_channel_backward_kernel<false, false, false>,
-        bn_channel_backward_kernel<false, false, true>},
-       {bn_channel_backward_kernel<false, true, false>,
-        bn_channel_backward_kernel<false, true, true>}},
-      {{bn_channel_backward_kernel<true, false, false>,
-        bn_channel_backward_kernel<true, false, true>},
-       {bn_channel_backward_kernel<true, true, false>,
-        bn_channel_backward_kernel<true, true, true>}}};
-  const K kernel = kernels[relu_out != nullptr][input_gradient_sum != nullptr][keep];
-  oxh::launch(kernel, dim3(cg.channels), dim3(kRedBlock), 0, oxh::as_stream(stream), cg,
+  const int threads = channel_threads(cg);
+  const bool keep = cg.samples <= static_cast<uint32_t>(threads * kChannelKeep);
+  using K = decltype(&bn_channel_backward_kernel<true, true, true, 256>);
+#define OXH_BN_BWD(T)                                                                      \
+  {{{bn_channel_backward_kernel<false, false, false, T>,                                   \
+     bn_channel_backward_kernel<false, false, true, T>},                                   \
+    {bn_channel_backward_kernel<false, true, false, T>,                                    \
+     bn_channel_backward_kernel<false, true, true, T>}},                                   \
+   {{bn_channel_backward_kernel<true, false, false, T>,                                    \
+     bn_channel_backward_kernel<true, false, true, T>},                                    \
+    {bn_channel_backward_kernel<true, true, false, T>,                                     \
+     bn_channel_backward_kernel<true, true, true, T>}}}
+  const K kernels[2][2][2][2] = {OXH_BN_BWD(256), OXH_BN_BWD(1024)};
+#undef OXH_BN_BWD
+  const K kernel =
+      kernels[threads == 1024][relu_out != nullptr][input_gradient_sum != nullptr][keep];
+  oxh::launch(kernel, dim3(cg.channels), dim3(threads), 0, oxh::as_stream(stream), cg,
               gradient, relu_out, input, weight, saved_mean, saved_inverse_std, input_gradient,
               weight_gradient, bias_gradient, input_gradient_sum);
   return oxh::launched(name);

@@ -64,11 +64,13 @@ SHAPES = [
     (128, 32, 14, 14), # config 5's largest BN tensor
     (4, 300, 3, 5),    # many channels, odd spatial
     (2, 1, 256, 256),  # one channel, many slices
-    # one block per channel: values kept in registers (<= 2048 per channel) or read twice
+    # one block per channel: values kept in registers (<= 8 per thread) or read twice
     (128, 96, 2, 2),
     (128, 64, 4, 4),   # exactly 2048 values per channel
-    (129, 8, 4, 4),    # 2064: read twice
-    (64, 8, 7, 7),
+    (129, 8, 4, 4),    # 2064: 1024-thread blocks (few channels), kept
+    (64, 8, 7, 7),     # 3136, kept by 1024 threads
+    (200, 4, 7, 7),    # 9800: 1024 threads, read twice
+    (64, 130, 6, 6),   # 2304 values, 130 channels: 256 threads, read twice
 ]
 
 
