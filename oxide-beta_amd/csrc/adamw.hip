@@ -175,6 +175,42 @@ __global__ __launch_bounds__(oxh::kBlock) void adamw_multi_kernel(Hyper h, Tenso
   adamw_range(h, table.s[t], begin, end, vec);
 }
 
+// Device-table variant: the tensor descriptors and each tensor's first chunk live in device
+// memory (any number of tensors, one launch); block b finds its tensor by binary search over
+// the chunk starts.  The step counter is read as t = *step + 1 by every block, and the block
+// that finishes last (a ticket counter, returned to zero by that block) stores t: no separate
+// increment launch, and every block saw the old value (each read it before taking a ticket).
+__global__ __launch_bounds__(oxh::kBlock) void adamw_table_kernel(
+    Hyper h, const oxh_adamw_tensor *__restrict__ table, const uint32_t *__restrict__ starts,
+    uint32_t count, int32_t *step, uint32_t *ticket) {
+  const int32_t t = *step + 1;
+  h.c1 = 1.0f - powi_f32(h.b1, t);
+  h.c2 = 1.0f - powi_f32(h.b2, t);
+  const uint32_t b = blockIdx.x;
+  uint32_t lo = 0, hi = count;  // the last tensor index with starts[i] <= b
+  while (hi - lo > 1) {
+    const uint32_t mid = (lo + hi) / 2;
+    if (starts[mid] <= b) lo = mid;
+    else hi = mid;
+  }
+  const oxh_adamw_tensor d = table[lo];
+  const uint64_t begin = static_cast<uint64_t>(b - starts[lo]) * kChunk;
+  const uint64_t end = begin + kChunk < d.n ? begin + kChunk : d.n;
+  const bool vec = ((reinterpret_cast<uintptr_t>(d.parameter) |
+                     reinterpret_cast<uintptr_t>(d.gradient) |
+                     reinterpret_cast<uintptr_t>(d.first_moment) |
+                     reinterpret_cast<uintptr_t>(d.second_moment)) & 15u) == 0;
+  adamw_range(h,
+              Streams{d.parameter, d.gradient, d.first_moment, d.second_moment, d.parameter,
+                      d.first_moment, d.second_moment},
+              begin, end, vec);
+  __syncthreads();  // every thread of the block has read *step
+  if (threadIdx.x == 0 && atomicAdd(ticket, 1u) == gridDim.x - 1) {
+    *step = t;
+    atomicExch(ticket, 0u);
+  }
+}
+
 bool finite_hyper(const Hyper &h) {
   return std::isfinite(h.lr) && std::isfinite(h.wd) && std::isfinite(h.b1) &&
          std::isfinite(h.b2) && std::isfinite(h.c1) && std::isfinite(h.c2) &&
@@ -253,6 +289,46 @@ oxh_status oxh_adamw_multi_tensor_step(oxh_stream stream, float learning_rate,
   oxh_status st = oxh::launched("oxh_adamw_multi_tensor_step");
   if (st != OXH_OK) return st;
   return adamw_multi("oxh_adamw_multi_tensor_step", stream, h, step, tensors, count);
+}
+
+oxh_status oxh_adamw_table_layout(const oxh_adamw_tensor *tensors, uint32_t count,
+                                  uint32_t *chunk_starts, uint64_t *total_chunks) {
+  OXH_REQUIRE(tensors != nullptr && chunk_starts != nullptr && total_chunks != nullptr,
+              OXH_INVALID_SHAPE, "oxh_adamw_table_layout: null argument");
+  uint64_t chunks = 0;
+  for (uint32_t i = 0; i < count; ++i) {
+    OXH_REQUIRE(tensors[i].n > 0 && tensors[i].n <= (1ull << 44), OXH_INVALID_SHAPE,
+                "oxh_adamw_table_layout: tensor " + std::to_string(i) +
+                    " is empty or too large");
+    chunk_starts[i] = static_cast<uint32_t>(chunks);
+    chunks += (tensors[i].n + kChunk - 1) / kChunk;
+    OXH_REQUIRE(chunks < (1ull << 31), OXH_INVALID_SHAPE,
+                "oxh_adamw_table_layout: more than 2^31 chunks");
+  }
+  chunk_starts[count] = static_cast<uint32_t>(chunks);
+  *total_chunks = chunks;
+  return oxh::ok();
+}
+
+oxh_status oxh_adamw_multi_tensor_table_step(oxh_stream stream, float learning_rate,
+                                             float weight_decay, float beta1, float beta2,
+                                             float epsilon, int32_t *step, uint32_t *ticket,
+                                             const oxh_adamw_tensor *device_tensors,
+                                             const uint32_t *device_chunk_starts,
+                                             uint32_t count, uint64_t total_chunks) {
+  const char *name = "oxh_adamw_multi_tensor_table_step";
+  OXH_REQUIRE(step != nullptr && ticket != nullptr && device_tensors != nullptr &&
+                  device_chunk_starts != nullptr,
+              OXH_INVALID_SHAPE, std::string(name) + ": null pointer");
+  OXH_REQUIRE(count > 0 && total_chunks > 0 && total_chunks < (1ull << 31), OXH_INVALID_SHAPE,
+              std::string(name) + ": empty table or more than 2^31 chunks");
+  const Hyper h{learning_rate, weight_decay, beta1, beta2, 1.0f, 1.0f, epsilon};
+  OXH_REQUIRE(finite_hyper(h), OXH_INVALID_SHAPE,
+              std::string(name) + ": non-finite hyper-parameter");
+  oxh::launch(adamw_table_kernel, dim3(static_cast<uint32_t>(total_chunks)), dim3(oxh::kBlock),
+              0, oxh::as_stream(stream), h, device_tensors, device_chunk_starts, count, step,
+              ticket);
+  return oxh::launched(name);
 }
 
 }  // extern "C"

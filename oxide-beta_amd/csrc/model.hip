@@ -486,6 +486,9 @@ struct oxh_trainer {
   std::vector<float *> saved_mean, saved_inv;  // per node (BN)
   std::vector<float *> pgrad, pm, pv;           // per parameter
   std::vector<oxh_adamw_tensor> adam;
+  oxh_adamw_tensor *adam_table = nullptr;  // device copy of `adam`
+  uint32_t *adam_starts = nullptr, *adam_ticket = nullptr;
+  uint64_t adam_chunks = 0;
   float *scratch = nullptr, *outer = nullptr, *loss = nullptr;
   int32_t *step = nullptr;
   uint32_t *error_flag = nullptr;
@@ -622,7 +625,10 @@ oxh_status build_trainer(oxh_trainer &t) {
     poff[p] = {a.reserve(m.params[p].n * 4), a.reserve(m.params[p].n * 4),
                a.reserve(m.params[p].n * 4)};
   const uint64_t scratch_off = a.reserve(largest * 4), outer_off = a.reserve(4),
-                 step_off = a.reserve(4), flag_off = a.reserve(4);
+                 step_off = a.reserve(4), flag_off = a.reserve(4), ticket_off = a.reserve(4);
+  // the optimizer's device tensor table and chunk starts (one launch over every parameter)
+  const uint64_t table_off = a.reserve(m.params.size() * sizeof(oxh_adamw_tensor));
+  const uint64_t starts_off = a.reserve((m.params.size() + 1) * 4);
   oxh_status st = plan_workspace(g, t.workspace_bytes);
   if (st != OXH_OK) return st;
   const uint64_t ws_off = a.reserve(t.workspace_bytes);
@@ -659,6 +665,9 @@ oxh_status build_trainer(oxh_trainer &t) {
   t.outer = a.at<float>(outer_off);
   t.step = a.at<int32_t>(step_off);
   t.error_flag = a.at<uint32_t>(flag_off);
+  t.adam_ticket = a.at<uint32_t>(ticket_off);
+  t.adam_table = a.at<oxh_adamw_tensor>(table_off);
+  t.adam_starts = a.at<uint32_t>(starts_off);
   t.workspace = a.at<void>(ws_off);
   t.loss = t.value[t.loss_node];
   const float one = 1.0f;
@@ -1066,11 +1075,22 @@ oxh_status build_trainer(oxh_trainer &t) {
   op.tensors.push_back(ref_flat("step", t.step, 1, 2, 1));
   op.attrs = {{"learning_rate", t.lr}, {"weight_decay", t.wd}, {"beta1", t.beta1},
               {"beta2", t.beta2}, {"epsilon", t.eps}};
+  {
+    const uint32_t count = static_cast<uint32_t>(t.adam.size());
+    std::vector<uint32_t> starts(count + 1);
+    st = oxh_adamw_table_layout(t.adam.data(), count, starts.data(), &t.adam_chunks);
+    if (st != OXH_OK) return st;
+    OXH_HIP_CHECK(hipMemcpy(t.adam_table, t.adam.data(), count * sizeof(oxh_adamw_tensor),
+                            hipMemcpyHostToDevice));
+    OXH_HIP_CHECK(hipMemcpy(t.adam_starts, starts.data(), (count + 1) * 4,
+                            hipMemcpyHostToDevice));
+  }
   oxh_trainer *self = &t;
   op.launch = [self](hipStream_t st) {
-    return oxh_adamw_multi_tensor_step(st, self->lr, self->wd, self->beta1, self->beta2,
-                                       self->eps, self->step, self->adam.data(),
-                                       static_cast<uint32_t>(self->adam.size()));
+    return oxh_adamw_multi_tensor_table_step(
+        st, self->lr, self->wd, self->beta1, self->beta2, self->eps, self->step,
+        self->adam_ticket, self->adam_table, self->adam_starts,
+        static_cast<uint32_t>(self->adam.size()), self->adam_chunks);
   };
   ops.push_back(std::move(op));
   return t.program.finalize();

@@ -150,6 +150,10 @@ _SIGNATURES = {
                                     ctypes.POINTER(_f32)]),
     "oxh_adamw_multi_tensor": (_st, [_vp, _f32, _f32, _f32, _f32, _f32, _f32, _f32,
                                      ctypes.POINTER(AdamWTensor), _u32]),
+    "oxh_adamw_table_layout": (_st, [ctypes.POINTER(AdamWTensor), _u32, ctypes.POINTER(_u32),
+                                     ctypes.POINTER(_u64)]),
+    "oxh_adamw_multi_tensor_table_step": (_st, [_vp, _f32, _f32, _f32, _f32, _f32, _vp, _vp,
+                                                _vp, _vp, _u32, _u64]),
     "oxh_adamw_multi_tensor_step": (_st, [_vp, _f32, _f32, _f32, _f32, _f32, _vp,
                                           ctypes.POINTER(AdamWTensor), _u32]),
     "oxh_conv2d_output_size": (_st, [_CS, ctypes.POINTER(_u64), ctypes.POINTER(_u64)]),
@@ -655,6 +659,29 @@ class LoadedModule:
         check(lib().oxh_adamw_multi_tensor_step(_stream(stream), learning_rate, weight_decay,
                                                 beta1, beta2, epsilon, _ptr(step_counter),
                                                 table, len(tensors)))
+
+    def adamw_table_step(self, learning_rate, weight_decay, beta1, beta2, epsilon, step_counter,
+                         ticket, tensors, stream=None):
+        """The device-table variant: the table and its chunk starts are copied to the device
+        (kept alive on the returned object until the launch completes)."""
+        import torch
+
+        count = len(tensors)
+        table = (AdamWTensor * count)()
+        for i, (p, g, m, v) in enumerate(tensors):
+            table[i] = AdamWTensor(_ptr(p), _ptr(g), _ptr(m), _ptr(v), p.numel())
+        starts = (_u32 * (count + 1))()
+        total = _u64()
+        check(lib().oxh_adamw_table_layout(table, count, starts, ctypes.byref(total)))
+        dev_table = torch.frombuffer(bytearray(bytes(table)), dtype=torch.uint8).to(
+            step_counter.device)
+        dev_starts = torch.tensor(list(starts), dtype=torch.int32, device=step_counter.device)
+        torch.cuda.synchronize()
+        check(lib().oxh_adamw_multi_tensor_table_step(
+            _stream(stream), learning_rate, weight_decay, beta1, beta2, epsilon,
+            _ptr(step_counter), _ptr(ticket), dev_table.data_ptr(), dev_starts.data_ptr(),
+            count, total.value))
+        return dev_table, dev_starts
 
     # -- conv2d / avg_pool2d (kernel_module.rs:359-490, 558-825)
     def conv2d_forward(self, shape, x, weight, bias, out, stream=None):

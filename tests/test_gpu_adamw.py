@@ -104,3 +104,27 @@ def test_adamw_first_step_closed_form(module, dev, rng):
     torch.cuda.synchronize()
     expect = p.astype(np.float64) - 1e-2 * (np.sign(g) + 0.1 * p.astype(np.float64))
     np.testing.assert_allclose(host(dp), expect, rtol=1e-5, atol=1e-6)
+
+
+def test_adamw_table_step_matches_multi_tensor_step(module, dev, rng):
+    """The one-launch device-table update equals the step-counting multi-tensor update bit for
+    bit over three steps (186 tensors as in config 5, more than one 48-tensor launch of the
+    latter); the step counter advances once per launch and the ticket returns to zero."""
+    sizes = ([864, 32, 32, 32, 288, 32, 1024, 32, 32, 32] * 18 + [12800, 10, 1280, 10, 5, 7])
+    assert len(sizes) == 186
+    state = [_state(rng, n) for n in sizes]
+    a = [tuple(to_dev(x, dev) for x in s) for s in state]
+    b = [tuple(to_dev(x, dev) for x in s) for s in state]
+    step_a = torch.zeros(1, dtype=torch.int32, device=dev)
+    step_b = torch.zeros(1, dtype=torch.int32, device=dev)
+    ticket = torch.zeros(1, dtype=torch.int32, device=dev)
+    for _ in range(3):
+        module.adamw_multi_tensor_step(LR, 1e-4, B1, B2, EPS, step_a, a)
+        keep = module.adamw_table_step(LR, 1e-4, B1, B2, EPS, step_b, ticket, b)
+        torch.cuda.synchronize()
+        del keep
+    assert int(host(step_a)[0]) == int(host(step_b)[0]) == 3
+    assert int(host(ticket)[0]) == 0
+    for i, (ta, tb) in enumerate(zip(a, b)):
+        for k, what in ((0, "param"), (2, "m"), (3, "v")):
+            assert_bitexact(host(tb[k]), host(ta[k]), f"tensor {i} {what}")
