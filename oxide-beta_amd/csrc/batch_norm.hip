@@ -37,9 +37,23 @@
 #include <cmath>
 #include <string>
 
+#include "bn_channel.h"
 #include "common.h"
 
 namespace {
+
+using oxh::block_sum2_all;
+using oxh::channel_backward_kept;
+using oxh::channel_forward_kept;
+using oxh::channel_index;
+using oxh::ChannelGeom;
+using oxh::forward_moments;
+using oxh::kChannelKeep;
+using oxh::Moments;
+using oxh::relu_masked;
+using oxh::StatsOut;
+using oxh::wave_sum;
+using oxh::write_forward_outputs;
 
 // Launch-shape constants (overridable at build time for tuning sweeps).
 #ifndef OXH_BN_RED_BLOCKS_PER_CU
@@ -142,16 +156,9 @@ PlaneMap make_plane_map(uint64_t batch, uint64_t channels, uint64_t spatial, boo
   return m;
 }
 
-__device__ __forceinline__ double wave_sum(double v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
-
 // Block-wide sum of two doubles; the result is valid in thread 0.
 __device__ __forceinline__ void block_sum2(double &a, double &b, double (*lds)[kRedWaves]) {
-  a = wave_sum(a);
-  b = wave_sum(b);
+  oxh::wave_sum2(a, b);
   const int wave = threadIdx.x / 64, lane_id = threadIdx.x % 64;
   if (lane_id == 0) {
     lds[0][wave] = a;
@@ -216,10 +223,6 @@ __global__ __launch_bounds__(kRedBlock) void bn_reduce_x_kernel(Geometry g,
   block_sum2(sum, sq, lds);
   if (threadIdx.x == 0) partial[static_cast<uint64_t>(c) * g.slices + s] = make_double2(sum, sq);
 }
-
-// ReLU backward applied to the incoming gradient (kernel_module.rs:501-508): g where the ReLU's
-// output r (hence its input) is positive, else 0.
-__device__ __forceinline__ float relu_masked(float g, float r) { return r > 0.0f ? g : 0.0f; }
 
 // Backward partials: (sum g, sum g * x_hat) with x_hat = (x - mean) * inv in fp32 and the
 // product g * x_hat rounded to fp32 as the CPU path forms it (autograd.rs:353-362).  With
@@ -289,31 +292,6 @@ __global__ __launch_bounds__(kRedBlock) void bn_reduce_gx_kernel(
 
 // ---------------------------------------------------------------- finalization
 
-struct Moments {
-  float mean, inv, biased, correction;
-};
-
-// Channel statistics from the sums of (x - shift) and (x - shift)^2 over its M values.
-__device__ __forceinline__ Moments forward_moments(double2 sums, float shift, uint64_t samples,
-                                                   float epsilon) {
-  const double m = static_cast<double>(samples);
-  const double mean_shifted = sums.x / m;
-  double var = sums.y / m - mean_shifted * mean_shifted;
-  if (var < 0.0) var = 0.0;
-  Moments r;
-  r.mean = static_cast<float>(static_cast<double>(shift) + mean_shifted);
-  const float var_f = static_cast<float>(var);
-  // evaluation.rs:531-534: (variance + epsilon).sqrt().recip()
-  r.inv = 1.0f / sqrtf(var_f + epsilon);
-  // evaluation.rs:537-558: the running update recomputes the statistics with epsilon 0 and
-  // recovers the biased variance as inv_std.powi(-2) (== 1 / (inv * inv)); the unbiased
-  // correction M / (M - 1) is formed in fp32.
-  const float inv0 = 1.0f / sqrtf(var_f);
-  r.biased = 1.0f / (inv0 * inv0);
-  r.correction = static_cast<float>(samples) / static_cast<float>(samples - 1);
-  return r;
-}
-
 __device__ __forceinline__ bool lane0() { return threadIdx.x % 64 == 0; }
 
 // Per-lane share of a channel's partials: lane l holds partial l (S <= kMaxSlices = 64, so one
@@ -329,27 +307,9 @@ __device__ __forceinline__ double2 load_lane_partial(const double2 *partial, uin
 // Fixed butterfly over the wave; every lane returns lane 0's sums (bit-identical in all
 // blocks and in the finalize kernels, which use the same reduction).
 __device__ __forceinline__ double2 wave_sums_lane0(double2 v) {
-  const double a = wave_sum(v.x), b = wave_sum(v.y);
+  double a = v.x, b = v.y;
+  oxh::wave_sum2(a, b);
   return make_double2(__shfl(a, 0, 64), __shfl(b, 0, 64));
-}
-
-
-struct StatsOut {
-  float *mean, *inverse_std, *unbiased_variance;  // unbiased_variance may be null
-  float *running_mean, *running_variance;         // null: no running update
-  float momentum, epsilon;
-};
-
-__device__ __forceinline__ void write_forward_outputs(const StatsOut &o, uint32_t c,
-                                                      const Moments &r) {
-  o.mean[c] = r.mean;
-  o.inverse_std[c] = r.inv;
-  if (o.unbiased_variance) o.unbiased_variance[c] = r.biased * r.correction;
-  if (o.running_mean) {
-    const float mom = o.momentum;
-    o.running_mean[c] = (1.0f - mom) * o.running_mean[c] + mom * r.mean;
-    o.running_variance[c] = (1.0f - mom) * o.running_variance[c] + mom * r.biased * r.correction;
-  }
 }
 
 // One wave per channel: the reference's separate statistics output (no consumer kernel).
@@ -698,44 +658,8 @@ __global__ __launch_bounds__(kMapBlock) void bn_flat_map_kernel(FlatMap m, typen
 // read of the channel is served by L2) -- in a single launch.
 constexpr uint64_t kChannelMaxSamples = 65536;
 
-struct ChannelGeom {
-  uint32_t channels, spatial, samples;  // samples = batch * spatial
-  oxh::FastDiv spatial_div;
-};
-
-__device__ __forceinline__ uint32_t channel_index(const ChannelGeom &g, uint32_t c, uint32_t j) {
-  const uint32_t n = oxh::fast_div(j, g.spatial_div);
-  return (n * g.channels + c) * g.spatial + (j - n * g.spatial);
-}
-
-// Block-wide sums of two doubles, the total in every thread: each wave's butterfly total goes
-// to LDS and every thread adds the Waves wave totals in the same order (one barrier, no
-// broadcast step).  `lds` must not be in use by another sum of the same block.
-template <int Waves>
-__device__ __forceinline__ void block_sum2_all(double &a, double &b, double (*lds)[Waves]) {
-  a = wave_sum(a);
-  b = wave_sum(b);
-  const int wave = threadIdx.x / 64;
-  if (threadIdx.x % 64 == 0) {
-    lds[0][wave] = a;
-    lds[1][wave] = b;
-  }
-  __syncthreads();
-  a = 0.0;
-  b = 0.0;
-#pragma unroll
-  for (int w = 0; w < Waves; ++w) {
-    a += lds[0][w];
-    b += lds[1][w];
-  }
-}
-
-// Up to kChannelKeep values per thread stay in registers between a channel kernel's sum pass
-// and its elementwise pass; larger channels read their values again (L2).  Blocks have 256
-// threads, or 1024 when there are few channels (a block per channel would leave most CUs
-// idle), so config 5's channels (at most 6272 values) all keep their values.
-constexpr int kChannelKeep = 8;
-
+// Blocks have 256 threads, or 1024 when there are few channels (a block per channel would
+// leave most CUs idle) and more values than 256 threads keep.
 int channel_threads(const ChannelGeom &g) {
   return g.channels <= 128 && g.samples > 256 * kChannelKeep ? 1024 : 256;
 }
@@ -750,51 +674,33 @@ __global__ __launch_bounds__(Threads) void bn_channel_forward_kernel(
   __shared__ double lds[2][Threads / 64];
   const uint32_t c = blockIdx.x;
   const float shift = x[static_cast<uint64_t>(c) * g.spatial];  // x[0, c, 0]
-  const double k = static_cast<double>(shift);
-  double sum = 0.0, sq = 0.0;
-  float kept[Keep ? kChannelKeep : 1];
-  uint32_t at[Keep ? kChannelKeep : 1];
   if constexpr (Keep) {
+    float kept[kChannelKeep];
+    uint32_t at[kChannelKeep];
 #pragma unroll
     for (int u = 0; u < kChannelKeep; ++u) {
       const uint32_t j = threadIdx.x + u * Threads;
       at[u] = j < g.samples ? channel_index(g, c, j) : 0;
       kept[u] = x[at[u]];
     }
-#pragma unroll
-    for (int u = 0; u < kChannelKeep; ++u) {
-      if (threadIdx.x + u * Threads >= g.samples) break;
-      const double d = static_cast<double>(kept[u]) - k;
-      sum += d;
-      sq += d * d;
-    }
+    channel_forward_kept<Relu, Threads>(g.samples, c, shift, kept, at, weight, bias, out, addend,
+                                        y, lds);
   } else {
+    const double k = static_cast<double>(shift);
+    double sum = 0.0, sq = 0.0;
     for (uint32_t j = threadIdx.x; j < g.samples; j += Threads) {
       const double d = static_cast<double>(x[channel_index(g, c, j)]) - k;
       sum += d;
       sq += d * d;
     }
-  }
-  block_sum2_all<Threads / 64>(sum, sq, lds);
-  const Moments r = forward_moments(make_double2(sum, sq), shift, g.samples, out.epsilon);
-  if (threadIdx.x == 0) write_forward_outputs(out, c, r);
-  const float mu = r.mean, inv = r.inv, w = weight[c], b = bias[c];
-  auto apply = [&](float v) {
-    v = (v - mu) * inv * w + b;  // evaluation.rs:590-595
-    if constexpr (Relu) v = v > 0.0f ? v : 0.0f;
-    return v;
-  };
-  if constexpr (Keep) {
-#pragma unroll
-    for (int u = 0; u < kChannelKeep; ++u)
-      if (threadIdx.x + u * Threads < g.samples) {
-        const float v = apply(kept[u]);
-        y[at[u]] = addend != nullptr ? v + addend[at[u]] : v;
-      }
-  } else {
+    block_sum2_all<Threads / 64>(sum, sq, lds);
+    const Moments r = forward_moments(make_double2(sum, sq), shift, g.samples, out.epsilon);
+    if (threadIdx.x == 0) write_forward_outputs(out, c, r);
+    const float mu = r.mean, inv = r.inv, w = weight[c], b = bias[c];
     for (uint32_t j = threadIdx.x; j < g.samples; j += Threads) {
       const uint32_t idx = channel_index(g, c, j);
-      const float v = apply(x[idx]);
+      float v = (x[idx] - mu) * inv * w + b;  // evaluation.rs:590-595
+      if constexpr (Relu) v = v > 0.0f ? v : 0.0f;
       y[idx] = addend != nullptr ? v + addend[idx] : v;
     }
   }
@@ -812,10 +718,10 @@ __global__ __launch_bounds__(Threads) void bn_channel_backward_kernel(
   __shared__ double lds[2][2][Threads / 64];  // one region per block sum
   const uint32_t c = blockIdx.x;
   const float mu = mean[c], inv = inverse_std[c];
-  double sg = 0.0, sgx = 0.0;
-  float kg[Keep ? kChannelKeep : 1], kn[Keep ? kChannelKeep : 1];
-  uint32_t at[Keep ? kChannelKeep : 1];
+  double total = 0.0, unused = 0.0;
   if constexpr (Keep) {
+    float kg[kChannelKeep], kn[kChannelKeep], d[kChannelKeep];
+    uint32_t at[kChannelKeep];
 #pragma unroll
     for (int u = 0; u < kChannelKeep; ++u) {
       const uint32_t j = threadIdx.x + u * Threads;
@@ -825,13 +731,16 @@ __global__ __launch_bounds__(Threads) void bn_channel_backward_kernel(
       kg[u] = gv;
       kn[u] = (x[at[u]] - mu) * inv;
     }
+    channel_backward_kept<Threads>(g.samples, c, kg, kn, weight[c], inv, dweight, dbias, d,
+                                   lds[0]);
 #pragma unroll
     for (int u = 0; u < kChannelKeep; ++u) {
       if (threadIdx.x + u * Threads >= g.samples) break;
-      sg += static_cast<double>(kg[u]);
-      sgx += static_cast<double>(kg[u] * kn[u]);
+      dx[at[u]] = d[u];
+      if constexpr (DxSum) total += static_cast<double>(d[u]);
     }
   } else {
+    double sg = 0.0, sgx = 0.0;
     for (uint32_t j = threadIdx.x; j < g.samples; j += Threads) {
       const uint32_t idx = channel_index(g, c, j);
       float gv = grad[idx];
@@ -840,26 +749,15 @@ __global__ __launch_bounds__(Threads) void bn_channel_backward_kernel(
       sg += static_cast<double>(gv);
       sgx += static_cast<double>(gv * nv);
     }
-  }
-  block_sum2_all<Threads / 64>(sg, sgx, lds[0]);
-  const float sgf = static_cast<float>(sg), sgxf = static_cast<float>(sgx);
-  if (threadIdx.x == 0) {
-    dbias[c] = sgf;
-    dweight[c] = sgxf;
-  }
-  // autograd.rs:344-373: ((w * inv) / M) * ((M * g - sum_g) - x_hat * sum_g_xhat)
-  const float samples = static_cast<float>(g.samples);
-  const float coef = weight[c] * inv / samples;
-  double total = 0.0, unused = 0.0;
-  if constexpr (Keep) {
-#pragma unroll
-    for (int u = 0; u < kChannelKeep; ++u) {
-      if (threadIdx.x + u * Threads >= g.samples) break;
-      const float d = coef * (samples * kg[u] - sgf - kn[u] * sgxf);
-      dx[at[u]] = d;
-      if constexpr (DxSum) total += static_cast<double>(d);
+    block_sum2_all<Threads / 64>(sg, sgx, lds[0]);
+    const float sgf = static_cast<float>(sg), sgxf = static_cast<float>(sgx);
+    if (threadIdx.x == 0) {
+      dbias[c] = sgf;
+      dweight[c] = sgxf;
     }
-  } else {
+    // autograd.rs:344-373: ((w * inv) / M) * ((M * g - sum_g) - x_hat * sum_g_xhat)
+    const float samples = static_cast<float>(g.samples);
+    const float coef = weight[c] * inv / samples;
     for (uint32_t j = threadIdx.x; j < g.samples; j += Threads) {
       const uint32_t idx = channel_index(g, c, j);
       float gv = grad[idx];

@@ -73,6 +73,15 @@ __device__ __forceinline__ uint32_t fast_div(uint32_t n, const FastDiv &f) {
   return (__umulhi(n, f.mul) + n) >> f.shift;
 }
 
+// Convolution tap terms: p where mask is all ones, else -0.0f (x + (-0.0f) == x for every x),
+// the term of a tap outside the input, so a sum over all taps equals the CPU path's sum that
+// skips them, bit for bit.  Bit operations rather than a select keep the tap's loads
+// unconditional (the compiler turns a select on a loaded value into a branch around the load).
+__device__ __forceinline__ float tap_term(float p, uint32_t mask) {
+  return __uint_as_float((__float_as_uint(p) & mask) | (~mask & 0x80000000u));
+}
+__device__ __forceinline__ uint32_t tap_mask(bool valid) { return valid ? 0xFFFFFFFFu : 0u; }
+
 // 128-bit loads / stores with the non-temporal hint (streamed once: do not keep in cache).
 typedef float vf4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float4 load_nt(const float4 *p) {

@@ -61,13 +61,8 @@ __device__ __forceinline__ int ceil_div0(int a, const oxh::FastDiv &s) {
   return a <= 0 ? 0 : static_cast<int>(fdiv(static_cast<uint32_t>(a) + s.d - 1, s));
 }
 
-// p where mask is all ones, else -0.0f (x + (-0.0f) == x for every x): the term of a tap
-// outside the input.  Bit operations rather than a select keep the tap's loads unconditional
-// (the compiler turns a select on a loaded value into a branch around the load).
-__device__ __forceinline__ float tap_term(float p, uint32_t mask) {
-  return __uint_as_float((__float_as_uint(p) & mask) | (~mask & 0x80000000u));
-}
-__device__ __forceinline__ uint32_t tap_mask(bool valid) { return valid ? 0xFFFFFFFFu : 0u; }
+using oxh::tap_mask;
+using oxh::tap_term;
 
 // ---------------------------------------------------------------- direct kernels
 
@@ -595,12 +590,19 @@ __global__ __launch_bounds__(Threads) void conv2d_depthwise_weight_kernel(
     for (int t = 0; t < kTaps; ++t) acc[t] += tap_term(gv * xv[t], mask[t]);
   }
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  // per-tap xor butterflies, one step of all taps at a time (their exchanges in flight
+  // together; each tap's additions in the same order as a butterfly of its own)
 #pragma unroll
-  for (int t = 0; t < kTaps; ++t) {
-    float v = acc[t];
+  for (int off = 32; off > 0; off >>= 1) {
+    float other[kTaps];
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    if (lane == 0) wave_sums[wave][t] = v;
+    for (int t = 0; t < kTaps; ++t) other[t] = __shfl_xor(acc[t], off, 64);
+#pragma unroll
+    for (int t = 0; t < kTaps; ++t) acc[t] += other[t];
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int t = 0; t < kTaps; ++t) wave_sums[wave][t] = acc[t];
   }
   __syncthreads();
   if (threadIdx.x < kTaps) {

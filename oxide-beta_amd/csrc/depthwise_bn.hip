@@ -1,0 +1,405 @@
+// depthwise_bn.hip -- a depthwise ConvNormAct (nn.rs:362-395 with groups == channels: conv2d,
+// BatchNorm2d in training mode, optional ReLU) in one launch per direction.
+//
+// Output channel c of a depthwise convolution reads input channel c only, and the BatchNorm
+// that follows reduces over channel c only, so one workgroup per channel can run the whole
+// layer: on small planes (the MNIST MobileNetV4's depthwise layers have at most 2048 values
+// per channel) that saves the launches in between, each of which costs more than the
+// layer's arithmetic.  Every value is formed by the same arithmetic, in the same order, as
+// the separate kernels:
+//   forward   conv sum = bias, then + x * w per tap in (ky, kx) order, taps outside the input
+//             adding -0.0f (conv.hip's tap kernels); the BatchNorm (relu) channel pass
+//             (bn_channel.h) over the sums, kept in registers;
+//   backward  the BatchNorm (relu) channel backward in registers; its dx (the convolution's
+//             output gradient) staged in LDS; the bias gradient as the BatchNorm backward's dx
+//             sum; the weight gradient as conv.hip's depthwise weight kernel at 256 threads
+//             (per-tap register sums, fixed butterflies); the input gradient as conv.hip's
+//             input-backward tap kernel (ascending output taps, -0.0f outside, then + addend).
+// The channel's convolution input is staged in LDS once (coalesced plane rows) and read by
+// every tap from there.
+#include <hip/hip_runtime.h>
+
+#include <string>
+
+#include "bn_channel.h"
+#include "common.h"
+
+namespace {
+
+using oxh::ChannelGeom;
+using oxh::kChannelKeep;
+using oxh::StatsOut;
+using oxh::tap_mask;
+using oxh::tap_term;
+
+constexpr int kDwThreads = 256;
+constexpr uint32_t kDwMaxOut = kDwThreads * kChannelKeep;  // output values per channel
+constexpr uint32_t kDwMaxIn = 8192;                        // input values per channel (32 KB)
+constexpr int kStageUnroll = 8;
+
+struct DwGeom {
+  uint32_t h, w, oh, ow, pad;
+  uint32_t in_samples;  // batch * h * w
+  ChannelGeom out;      // channels, oh * ow, batch * oh * ow
+  oxh::FastDiv plane_div, w_div, ow_div;
+};
+
+// LDS copy of input channel c: xs[n * h * w + p] = x[n, c, p], kStageUnroll loads in flight
+// per thread (addresses clamped into the channel, stores guarded).
+__device__ __forceinline__ void stage_channel(const DwGeom &g, uint32_t c,
+                                              const float *__restrict__ x, float *xs) {
+  const uint32_t plane = g.h * g.w, last = g.in_samples - 1;
+  for (uint32_t base = 0; base < g.in_samples; base += kDwThreads * kStageUnroll) {
+    float v[kStageUnroll];
+#pragma unroll
+    for (int u = 0; u < kStageUnroll; ++u) {
+      uint32_t i = base + u * kDwThreads + threadIdx.x;
+      i = i < last ? i : last;
+      const uint32_t n = oxh::fast_div(i, g.plane_div);
+      v[u] = x[(n * g.out.channels + c) * plane + (i - n * plane)];
+    }
+#pragma unroll
+    for (int u = 0; u < kStageUnroll; ++u) {
+      const uint32_t i = base + u * kDwThreads + threadIdx.x;
+      if (i < g.in_samples) xs[i] = v[u];
+    }
+  }
+}
+
+template <int K, int S, bool Relu>
+__global__ __launch_bounds__(kDwThreads) void dw_bn_forward_kernel(
+    DwGeom g, const float *__restrict__ x, const float *__restrict__ conv_weight,
+    const float *__restrict__ conv_bias, float *__restrict__ conv_out,
+    const float *__restrict__ bn_weight, const float *__restrict__ bn_bias, StatsOut stats,
+    float *__restrict__ y) {
+  __shared__ float xs[kDwMaxIn];
+  __shared__ double lds[2][kDwThreads / 64];
+  __shared__ float shift;
+  const uint32_t c = blockIdx.x;
+  stage_channel(g, c, x, xs);
+  float wv[K * K];
+#pragma unroll
+  for (int t = 0; t < K * K; ++t) wv[t] = conv_weight[c * (K * K) + t];
+  const float bias = conv_bias[c];
+  __syncthreads();
+  const uint32_t oplane = g.oh * g.ow, plane = g.h * g.w, samples = g.out.samples;
+  float kept[kChannelKeep];
+  uint32_t at[kChannelKeep];
+#pragma unroll
+  for (int u = 0; u < kChannelKeep; ++u) {
+    const uint32_t j = threadIdx.x + u * kDwThreads;
+    if (j >= samples) break;  // kept / at beyond are never read
+    const uint32_t n = oxh::fast_div(j, g.out.spatial_div), r = j - n * oplane;
+    const uint32_t oy = oxh::fast_div(r, g.ow_div), ox = r - oy * g.ow;
+    const int by = static_cast<int>(oy) * S - static_cast<int>(g.pad);
+    const int bx = static_cast<int>(ox) * S - static_cast<int>(g.pad);
+    const float *xp = xs + n * plane;
+    float sum = bias;
+#pragma unroll
+    for (int t = 0; t < K * K; ++t) {
+      const int iy = by + t / K, ix = bx + t % K;
+      const bool v = static_cast<uint32_t>(iy) < g.h && static_cast<uint32_t>(ix) < g.w;
+      const float xv = xp[v ? iy * static_cast<int>(g.w) + ix : 0];
+      sum += tap_term(xv * wv[t], tap_mask(v));
+    }
+    kept[u] = sum;
+    at[u] = (n * g.out.channels + c) * oplane + r;
+    conv_out[at[u]] = sum;
+  }
+  if (threadIdx.x == 0) shift = kept[0];  // conv_out[0, c, 0] (samples >= 2)
+  __syncthreads();
+  oxh::channel_forward_kept<Relu, kDwThreads>(samples, c, shift, kept, at, bn_weight, bn_bias,
+                                              stats, nullptr, y, lds);
+}
+
+template <int K, int S, bool Relu>
+__global__ __launch_bounds__(kDwThreads) void dw_bn_backward_kernel(
+    DwGeom g, const float *__restrict__ grad, const float *__restrict__ relu_out,
+    const float *__restrict__ conv_out, const float *__restrict__ bn_weight,
+    const float *__restrict__ mean, const float *__restrict__ inverse_std,
+    const float *__restrict__ x, const float *__restrict__ conv_weight, const float *addend,
+    float *__restrict__ conv_grad, float *__restrict__ bn_dweight, float *__restrict__ bn_dbias,
+    float *__restrict__ conv_dbias, float *__restrict__ conv_dweight, float *dx) {
+  constexpr int kTaps = K * K, kWaves = kDwThreads / 64;
+  __shared__ float xs[kDwMaxIn];
+  __shared__ float gs[kDwMaxOut];
+  __shared__ float wts[kTaps];
+  __shared__ double lds[2][2][kWaves];
+  __shared__ float wave_sums[kWaves][kTaps];
+  const uint32_t c = blockIdx.x;
+  const uint32_t oplane = g.oh * g.ow, plane = g.h * g.w, samples = g.out.samples;
+  const float mu = mean[c], inv = inverse_std[c];
+  // BatchNorm (relu) backward from registers
+  float kg[kChannelKeep], kn[kChannelKeep], d[kChannelKeep];
+  uint32_t at[kChannelKeep];
+#pragma unroll
+  for (int u = 0; u < kChannelKeep; ++u) {
+    const uint32_t j = threadIdx.x + u * kDwThreads;
+    at[u] = j < samples ? oxh::channel_index(g.out, c, j) : 0;
+    float gv = grad[at[u]];
+    if constexpr (Relu) gv = oxh::relu_masked(gv, relu_out[at[u]]);
+    kg[u] = gv;
+    kn[u] = (conv_out[at[u]] - mu) * inv;
+  }
+  stage_channel(g, c, x, xs);
+  if (threadIdx.x < kTaps) wts[threadIdx.x] = conv_weight[c * kTaps + threadIdx.x];
+  oxh::channel_backward_kept<kDwThreads>(samples, c, kg, kn, bn_weight[c], inv, bn_dweight,
+                                         bn_dbias, d, lds[0]);
+  double total = 0.0, unused = 0.0;
+#pragma unroll
+  for (int u = 0; u < kChannelKeep; ++u) {
+    const uint32_t j = threadIdx.x + u * kDwThreads;
+    if (j >= samples) break;
+    if (conv_grad != nullptr) conv_grad[at[u]] = d[u];
+    gs[j] = d[u];
+    total += static_cast<double>(d[u]);
+  }
+  // the sum's barrier also publishes gs, xs and wts to the block
+  oxh::block_sum2_all<kWaves>(total, unused, lds[1]);
+  if (threadIdx.x == 0) conv_dbias[c] = static_cast<float>(total);
+
+  // weight gradient: per-tap sums over the channel's output positions j, j + 256, ...
+  float acc[kTaps];
+#pragma unroll
+  for (int t = 0; t < kTaps; ++t) acc[t] = 0.0f;
+  for (uint32_t j = threadIdx.x; j < samples; j += kDwThreads) {
+    const uint32_t n = oxh::fast_div(j, g.out.spatial_div), r = j - n * oplane;
+    const uint32_t oy = oxh::fast_div(r, g.ow_div), ox = r - oy * g.ow;
+    const float gv = gs[j];
+    const float *xp = xs + n * plane;
+    const int by = static_cast<int>(oy * S) - static_cast<int>(g.pad);
+    const int bx = static_cast<int>(ox * S) - static_cast<int>(g.pad);
+    float xv[kTaps];
+    uint32_t mask[kTaps];
+#pragma unroll
+    for (int t = 0; t < kTaps; ++t) {
+      const int iy = by + t / K, ix = bx + t % K;
+      const bool v = static_cast<uint32_t>(iy) < g.h && static_cast<uint32_t>(ix) < g.w;
+      xv[t] = xp[v ? iy * static_cast<int>(g.w) + ix : 0];
+      mask[t] = tap_mask(v);
+    }
+#pragma unroll
+    for (int t = 0; t < kTaps; ++t) acc[t] += tap_term(gv * xv[t], mask[t]);
+  }
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  // per-tap xor butterflies, one step of all taps at a time (their exchanges in flight
+  // together; each tap's additions in the same order as a butterfly of its own)
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    float other[kTaps];
+#pragma unroll
+    for (int t = 0; t < kTaps; ++t) other[t] = __shfl_xor(acc[t], off, 64);
+#pragma unroll
+    for (int t = 0; t < kTaps; ++t) acc[t] += other[t];
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int t = 0; t < kTaps; ++t) wave_sums[wave][t] = acc[t];
+  }
+
+  // input gradient: input (iy, ix) feeds outputs oy = floor(ty / S) - (M - 1) + j, j < M
+  if (dx != nullptr) {
+    constexpr int M = (K + S - 1) / S;
+    for (uint32_t i = threadIdx.x; i < g.in_samples; i += kDwThreads) {
+      const uint32_t n = oxh::fast_div(i, g.plane_div), r = i - n * plane;
+      const uint32_t iy = oxh::fast_div(r, g.w_div), ix = r - iy * g.w;
+      const int ty = static_cast<int>(iy + g.pad), tx = static_cast<int>(ix + g.pad);
+      int grow[M], gcol[M], wrow[M], wcol[M];
+      bool vy[M], vx[M];
+#pragma unroll
+      for (int j = 0; j < M; ++j) {
+        const int oy = ty / S - (M - 1) + j, ox = tx / S - (M - 1) + j;
+        const int ky = ty - oy * S, kx = tx - ox * S;
+        vy[j] = oy >= 0 && oy < static_cast<int>(g.oh) && ky < K;
+        vx[j] = ox >= 0 && ox < static_cast<int>(g.ow) && kx < K;
+        grow[j] = vy[j] ? oy * static_cast<int>(g.ow) : 0;
+        gcol[j] = vx[j] ? ox : 0;
+        wrow[j] = vy[j] ? ky * K : 0;
+        wcol[j] = vx[j] ? kx : 0;
+      }
+      const float *gp = gs + n * oplane;
+      float a = 0.0f;
+#pragma unroll
+      for (int t = 0; t < M * M; ++t) {
+        const float p = gp[grow[t / M] + gcol[t % M]] * wts[wrow[t / M] + wcol[t % M]];
+        a += tap_term(p, tap_mask(vy[t / M] && vx[t % M]));
+      }
+      const uint32_t idx = (n * g.out.channels + c) * plane + r;
+      dx[idx] = addend != nullptr ? a + addend[idx] : a;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < kTaps) {
+    const int t = threadIdx.x;
+    float v = wave_sums[0][t];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) v += wave_sums[w][t];
+    conv_dweight[c * kTaps + t] = v;
+  }
+}
+
+// Shape check; fills g for an eligible shape.
+bool make_dw_geom(const oxh_conv2d_shape *s, DwGeom &g) {
+  if (s == nullptr) return false;
+  const uint64_t c = s->in_channels;
+  if (s->batch == 0 || c == 0 || s->height == 0 || s->width == 0) return false;
+  if (s->groups != c || s->out_channels != c) return false;
+  if (s->kernel_h != s->kernel_w || (s->kernel_h != 3 && s->kernel_h != 5)) return false;
+  if (s->stride != 1 && s->stride != 2) return false;
+  if (s->padding >= (1ull << 20)) return false;
+  if (s->height + 2 * s->padding < s->kernel_h || s->width + 2 * s->padding < s->kernel_w)
+    return false;
+  const uint64_t oh = (s->height + 2 * s->padding - s->kernel_h) / s->stride + 1;
+  const uint64_t ow = (s->width + 2 * s->padding - s->kernel_w) / s->stride + 1;
+  const uint64_t out_samples = s->batch * oh * ow, in_samples = s->batch * s->height * s->width;
+  if (out_samples < 2 || out_samples > kDwMaxOut || in_samples > kDwMaxIn) return false;
+  if (c * in_samples >= (1ull << 31) || c * out_samples >= (1ull << 31)) return false;
+  g.h = static_cast<uint32_t>(s->height);
+  g.w = static_cast<uint32_t>(s->width);
+  g.oh = static_cast<uint32_t>(oh);
+  g.ow = static_cast<uint32_t>(ow);
+  g.pad = static_cast<uint32_t>(s->padding);
+  g.in_samples = static_cast<uint32_t>(in_samples);
+  g.out.channels = static_cast<uint32_t>(c);
+  g.out.spatial = static_cast<uint32_t>(oh * ow);
+  g.out.samples = static_cast<uint32_t>(out_samples);
+  g.out.spatial_div = oxh::make_fastdiv(g.out.spatial);
+  g.plane_div = oxh::make_fastdiv(g.h * g.w);
+  g.w_div = oxh::make_fastdiv(g.w);
+  g.ow_div = oxh::make_fastdiv(g.ow);
+  return true;
+}
+
+int variant(const oxh_conv2d_shape *s) { return static_cast<int>(10 * s->kernel_h + s->stride); }
+
+template <bool Relu>
+void launch_forward(int v, hipStream_t st, uint32_t channels, const DwGeom &g, const float *x,
+                    const float *cw, const float *cb, float *co, const float *bw,
+                    const float *bb, const StatsOut &so, float *y) {
+  const dim3 grid(channels), block(kDwThreads);
+  switch (v) {
+    case 31: oxh::launch(dw_bn_forward_kernel<3, 1, Relu>, grid, block, 0, st, g, x, cw, cb, co, bw, bb, so, y); break;
+    case 32: oxh::launch(dw_bn_forward_kernel<3, 2, Relu>, grid, block, 0, st, g, x, cw, cb, co, bw, bb, so, y); break;
+    case 51: oxh::launch(dw_bn_forward_kernel<5, 1, Relu>, grid, block, 0, st, g, x, cw, cb, co, bw, bb, so, y); break;
+    default: oxh::launch(dw_bn_forward_kernel<5, 2, Relu>, grid, block, 0, st, g, x, cw, cb, co, bw, bb, so, y);
+  }
+}
+
+template <bool Relu>
+void launch_backward(int v, hipStream_t st, uint32_t channels, const DwGeom &g, const float *gr,
+                     const float *ro, const float *co, const float *bw, const float *sm,
+                     const float *si, const float *x, const float *cw, const float *ad,
+                     float *cg, float *dbw, float *dbb, float *dcb, float *dcw, float *dx) {
+  const dim3 grid(channels), block(kDwThreads);
+  switch (v) {
+    case 31: oxh::launch(dw_bn_backward_kernel<3, 1, Relu>, grid, block, 0, st, g, gr, ro, co, bw, sm, si, x, cw, ad, cg, dbw, dbb, dcb, dcw, dx); break;
+    case 32: oxh::launch(dw_bn_backward_kernel<3, 2, Relu>, grid, block, 0, st, g, gr, ro, co, bw, sm, si, x, cw, ad, cg, dbw, dbb, dcb, dcw, dx); break;
+    case 51: oxh::launch(dw_bn_backward_kernel<5, 1, Relu>, grid, block, 0, st, g, gr, ro, co, bw, sm, si, x, cw, ad, cg, dbw, dbb, dcb, dcw, dx); break;
+    default: oxh::launch(dw_bn_backward_kernel<5, 2, Relu>, grid, block, 0, st, g, gr, ro, co, bw, sm, si, x, cw, ad, cg, dbw, dbb, dcb, dcw, dx);
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int oxh_depthwise_conv_batch_norm_supported(const oxh_conv2d_shape *shape) {
+  DwGeom g;
+  return make_dw_geom(shape, g) ? 1 : 0;
+}
+
+oxh_status oxh_depthwise_conv_batch_norm_forward_train(
+    oxh_stream stream, const oxh_conv2d_shape *shape, int relu, float momentum, float epsilon,
+    const float *input, const float *conv_weight, const float *conv_bias, float *conv_output,
+    const float *bn_weight, const float *bn_bias, float *running_mean, float *running_variance,
+    float *saved_mean, float *saved_inverse_std, float *output) {
+  const char *name = "oxh_depthwise_conv_batch_norm_forward_train";
+  DwGeom g;
+  OXH_REQUIRE(make_dw_geom(shape, g), OXH_INVALID_SHAPE,
+              std::string(name) + ": not a supported depthwise shape "
+                                  "(oxh_depthwise_conv_batch_norm_supported)");
+  OXH_REQUIRE(input && conv_weight && conv_bias && conv_output && bn_weight && bn_bias &&
+                  running_mean && running_variance && saved_mean && saved_inverse_std && output,
+              OXH_INVALID_SHAPE, std::string(name) + ": null pointer");
+  const uint64_t c = g.out.channels;
+  const uint64_t in_bytes = c * g.in_samples * 4, out_bytes = c * g.out.samples * 4;
+  OXH_REQUIRE(!oxh::any_overlap(conv_output, out_bytes, input, in_bytes) &&
+                  !oxh::any_overlap(output, out_bytes, input, in_bytes) &&
+                  !oxh::any_overlap(output, out_bytes, conv_output, out_bytes),
+              OXH_INVALID_SHAPE, std::string(name) + ": outputs overlap an input or each other");
+  const StatsOut so{saved_mean, saved_inverse_std, nullptr, running_mean, running_variance,
+                    momentum, epsilon};
+  hipStream_t st = oxh::as_stream(stream);
+  if (relu)
+    launch_forward<true>(variant(shape), st, g.out.channels, g, input, conv_weight, conv_bias,
+                         conv_output, bn_weight, bn_bias, so, output);
+  else
+    launch_forward<false>(variant(shape), st, g.out.channels, g, input, conv_weight, conv_bias,
+                          conv_output, bn_weight, bn_bias, so, output);
+  return oxh::launched(name);
+}
+
+oxh_status oxh_depthwise_conv_batch_norm_backward_train(
+    oxh_stream stream, const oxh_conv2d_shape *shape, const float *gradient,
+    const float *relu_output, const float *conv_output, const float *bn_weight,
+    const float *saved_mean, const float *saved_inverse_std, const float *input,
+    const float *conv_weight, const float *addend, float *conv_output_gradient,
+    float *bn_weight_gradient, float *bn_bias_gradient, float *conv_bias_gradient,
+    float *conv_weight_gradient, float *input_gradient) {
+  const char *name = "oxh_depthwise_conv_batch_norm_backward_train";
+  DwGeom g;
+  OXH_REQUIRE(make_dw_geom(shape, g), OXH_INVALID_SHAPE,
+              std::string(name) + ": not a supported depthwise shape "
+                                  "(oxh_depthwise_conv_batch_norm_supported)");
+  OXH_REQUIRE(gradient && conv_output && bn_weight && saved_mean && saved_inverse_std && input &&
+                  conv_weight && bn_weight_gradient && bn_bias_gradient && conv_bias_gradient &&
+                  conv_weight_gradient,
+              OXH_INVALID_SHAPE, std::string(name) + ": null pointer");
+  OXH_REQUIRE(addend == nullptr || input_gradient != nullptr, OXH_INVALID_SHAPE,
+              std::string(name) + ": addend without input_gradient");
+  const uint64_t c = g.out.channels;
+  const uint64_t in_bytes = c * g.in_samples * 4, out_bytes = c * g.out.samples * 4;
+  if (input_gradient != nullptr) {
+    // every block reads its own channel of these while others write theirs: no overlap at
+    // all (addend may equal input_gradient exactly: each element is read, then written, by
+    // the same thread)
+    for (const void *p : {static_cast<const void *>(gradient), static_cast<const void *>(input),
+                          static_cast<const void *>(conv_output),
+                          static_cast<const void *>(relu_output)})
+      OXH_REQUIRE(p == nullptr || !oxh::any_overlap(input_gradient, in_bytes, p,
+                                                    p == input ? in_bytes : out_bytes),
+                  OXH_INVALID_SHAPE, std::string(name) + ": input_gradient overlaps an input");
+    OXH_REQUIRE(addend == nullptr || addend == input_gradient ||
+                    !oxh::any_overlap(input_gradient, in_bytes, addend, in_bytes),
+                OXH_INVALID_SHAPE, std::string(name) + ": addend partially overlaps");
+  }
+  if (conv_output_gradient != nullptr)
+    for (const void *p : {static_cast<const void *>(gradient), static_cast<const void *>(input),
+                          static_cast<const void *>(conv_output),
+                          static_cast<const void *>(relu_output),
+                          static_cast<const void *>(addend),
+                          static_cast<const void *>(input_gradient)})
+      OXH_REQUIRE(p == nullptr || !oxh::any_overlap(conv_output_gradient, out_bytes, p,
+                                                    (p == input || p == addend ||
+                                                     p == input_gradient)
+                                                        ? in_bytes
+                                                        : out_bytes),
+                  OXH_INVALID_SHAPE,
+                  std::string(name) + ": conv_output_gradient overlaps another tensor");
+  hipStream_t st = oxh::as_stream(stream);
+  if (relu_output)
+    launch_backward<true>(variant(shape), st, g.out.channels, g, gradient, relu_output,
+                          conv_output, bn_weight, saved_mean, saved_inverse_std, input,
+                          conv_weight, addend, conv_output_gradient, bn_weight_gradient,
+                          bn_bias_gradient, conv_bias_gradient, conv_weight_gradient,
+                          input_gradient);
+  else
+    launch_backward<false>(variant(shape), st, g.out.channels, g, gradient, relu_output,
+                           conv_output, bn_weight, saved_mean, saved_inverse_std, input,
+                           conv_weight, addend, conv_output_gradient, bn_weight_gradient,
+                           bn_bias_gradient, conv_bias_gradient, conv_weight_gradient,
+                           input_gradient);
+  return oxh::launched(name);
+}
+
+}  // extern "C"

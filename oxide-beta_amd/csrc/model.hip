@@ -583,6 +583,26 @@ oxh_status build_trainer(oxh_trainer &t) {
       add_absorbed[i] = 1;
     }
   }
+  // a depthwise convolution whose only consumer is the BatchNorm traced next (parameter nodes
+  // aside), on planes the one-launch depthwise ConvNormAct kernels take: the pair runs as one
+  // launch per direction, at the BN's place in each pass (no launch lies between the two in
+  // either order, so every gradient contribution keeps its order)
+  std::vector<char> dw_conv(n, 0);
+  std::vector<int64_t> dw_conv_of(n, -1);  // BN node -> its fused depthwise convolution
+  for (size_t i = 0; i < n; ++i) {
+    const Node &x = g.nodes[i];
+    if (x.op != Op::Conv || consumers[i] != 1) continue;
+    size_t j = i + 1;
+    while (j < n && g.nodes[j].op == Op::Param) ++j;
+    if (j == n || g.nodes[j].op != Op::Bn || g.nodes[j].in[0] != static_cast<int>(i) ||
+        bn_into_add[j] >= 0)
+      continue;
+    if (x.conv.groups != g.nodes[x.in[0]].shape[1] || x.conv.groups != x.shape[1]) continue;
+    const oxh_conv2d_shape s = conv_shape(g, x);
+    if (!oxh_depthwise_conv_batch_norm_supported(&s)) continue;
+    dw_conv[i] = 1;
+    dw_conv_of[j] = static_cast<int64_t>(i);
+  }
   // gradient buffers, consumers before producers
   std::vector<int64_t> grad_of(n, -1);  // node whose grad buffer this node uses (-1: own)
   std::vector<char> has_grad(n, 0), aliased(n, 0);
@@ -745,7 +765,7 @@ oxh_status build_trainer(oxh_trainer &t) {
   for (size_t i = 0; i < n; ++i) {
     const Node &x = g.nodes[i];
     if (x.op == Op::Param || x.op == Op::Input || x.op == Op::Targets || x.op == Op::Reshape ||
-        fused_bn[i] || add_absorbed[i])
+        fused_bn[i] || add_absorbed[i] || dw_conv[i])
       continue;
     float *out = t.value[i];
     OpRec op;
@@ -802,6 +822,34 @@ oxh_status build_trainer(oxh_trainer &t) {
           op.launch = [=](hipStream_t st) {
             return oxh_batch_norm_add_forward_train(st, N, C, HW, kBnMomentum, kBnEpsilon, xi, w,
                                                     b, rm, rv, sm, si, skip, sum, ws, wsb);
+          };
+          ops.push_back(std::move(op));
+          break;
+        }
+        if (dw_conv_of[bi] >= 0) {  // depthwise conv + BN (+ ReLU) in one launch
+          const int ci = static_cast<int>(dw_conv_of[bi]);
+          const Node &cv = g.nodes[ci];
+          const oxh_conv2d_shape s = conv_shape(g, cv);
+          const float *cx = t.value[cv.in[0]], *cw = t.value[cv.in[1]], *cb = t.value[cv.in[2]];
+          float *cy = t.value[ci];
+          op.kind = fused ? "depthwise_conv2d_batch_norm_relu_forward"
+                          : "depthwise_conv2d_batch_norm_forward";
+          op.name = name("conv", ci) + "+" + name("bn", bi) + (fused ? "+" + name("relu", i) : "");
+          op.tensors = {ref("x", const_cast<float *>(cx), g.nodes[cv.in[0]], 0),
+                        ref("conv_weight", const_cast<float *>(cw), g.nodes[cv.in[1]], 0),
+                        ref("conv_bias", const_cast<float *>(cb), g.nodes[cv.in[2]], 0),
+                        ref("weight", const_cast<float *>(w), g.nodes[bn.in[1]], 0),
+                        ref("bias", const_cast<float *>(b), g.nodes[bn.in[2]], 0),
+                        ref("conv_y", cy, cv, 1), ref("y", out, x, 1),
+                        ref_flat("saved_mean", sm, C, 1), ref_flat("saved_inverse_std", si, C, 1),
+                        ref_flat("running_mean", rm, C, 2), ref_flat("running_variance", rv, C, 2)};
+          op.attrs = conv_attrs(cv);
+          op.attrs.push_back({"momentum", kBnMomentum});
+          op.attrs.push_back({"epsilon", kBnEpsilon});
+          op.launch = [=](hipStream_t st) {
+            return oxh_depthwise_conv_batch_norm_forward_train(st, &s, fused ? 1 : 0, kBnMomentum,
+                                                               kBnEpsilon, cx, cw, cb, cy, w, b,
+                                                               rm, rv, sm, si, out);
           };
           ops.push_back(std::move(op));
           break;
@@ -921,6 +969,62 @@ oxh_status build_trainer(oxh_trainer &t) {
         const float *y = fused ? t.value[r] : nullptr;
         const float *sm = t.saved_mean[bi], *si = t.saved_inv[bi];
         float *dg, *db, *dst, *acc, *unused;
+        if (dw_conv_of[bi] >= 0) {  // depthwise conv + BN (+ ReLU) backward in one launch
+          const Node &cv = g.nodes[xin];
+          const int cin = cv.in[0];
+          OXH_REQUIRE(!written[bn.in[1]] && !written[bn.in[2]] && !written[xin] &&
+                          !written[cv.in[1]] && !written[cv.in[2]],
+                      OXH_TRACE, "a fused depthwise layer's gradients have other contributions");
+          float *cgr, *cdw, *cdb;
+          contribution(bn.in[1], dg, unused);
+          contribution(bn.in[2], db, unused);
+          contribution(xin, cgr, unused);
+          contribution(cv.in[2], cdb, unused);
+          contribution(cv.in[1], cdw, unused);
+          const oxh_conv2d_shape s = conv_shape(g, cv);
+          const float *cx = t.value[cin], *cw = t.value[cv.in[1]];
+          const uint64_t C = bn.shape[1];
+          const float *addend = nullptr;
+          dst = nullptr;
+          acc = nullptr;
+          if (g.nodes[cin].op != Op::Input) {  // the network input needs no gradient
+            if (pending[cin].gradient != nullptr && !written[cin]) {
+              addend = pending[cin].gradient;
+              op.tensors.push_back(ref("addend", const_cast<float *>(addend),
+                                       g.nodes[pending[cin].add], 0));
+              pending[cin] = Pending{};
+              written[cin] = 1;
+              dst = t.grad[cin];
+            } else {
+              contribution(cin, dst, acc);
+            }
+          }
+          op.kind = fused ? "depthwise_conv2d_batch_norm_relu_backward"
+                          : "depthwise_conv2d_batch_norm_backward";
+          op.name = name("conv", xin) + "+" + name("bn", bi) + (fused ? "+" + name("relu", r) : "") +
+                    ".backward";
+          op.tensors.push_back(ref("gradient", const_cast<float *>(gr), x, 0));
+          if (fused) op.tensors.push_back(ref("y", const_cast<float *>(y), x, 0));
+          op.tensors.push_back(ref("conv_y", const_cast<float *>(xi), cv, 0));
+          op.tensors.push_back(ref("weight", const_cast<float *>(w), g.nodes[bn.in[1]], 0));
+          op.tensors.push_back(ref_flat("saved_mean", const_cast<float *>(sm), C, 0));
+          op.tensors.push_back(ref_flat("saved_inverse_std", const_cast<float *>(si), C, 0));
+          op.tensors.push_back(ref("x", const_cast<float *>(cx), g.nodes[cin], 0));
+          op.tensors.push_back(ref("conv_weight", const_cast<float *>(cw), g.nodes[cv.in[1]], 0));
+          op.tensors.push_back(ref("conv_output_gradient", cgr, cv, 1));
+          op.tensors.push_back(ref_flat("weight_gradient", dg, C, 1));
+          op.tensors.push_back(ref_flat("bias_gradient", db, C, 1));
+          op.tensors.push_back(ref("conv_bias_gradient", cdb, g.nodes[cv.in[2]], 1));
+          op.tensors.push_back(ref("conv_weight_gradient", cdw, g.nodes[cv.in[1]], 1));
+          if (dst != nullptr) op.tensors.push_back(ref("contribution", dst, g.nodes[cin], 1));
+          op.attrs = conv_attrs(cv);
+          emit(std::move(op), acc, g.nodes[cin], [=](hipStream_t st) {
+            return oxh_depthwise_conv_batch_norm_backward_train(st, &s, gr, y, xi, w, sm, si, cx,
+                                                                cw, addend, cgr, dg, db, cdb, cdw,
+                                                                dst);
+          });
+          break;
+        }
         contribution(bn.in[1], dg, unused);
         contribution(bn.in[2], db, unused);
         contribution(xin, dst, acc);
@@ -1003,6 +1107,7 @@ oxh_status build_trainer(oxh_trainer &t) {
         break;
       }
       case Op::Conv: {
+        if (dw_conv[r]) break;  // its backward ran with its BatchNorm's
         const oxh_conv2d_shape s = conv_shape(g, x);
         const int xin = x.in[0];
         const float *xi = t.value[xin], *w = t.value[x.in[1]];

@@ -163,6 +163,13 @@ _SIGNATURES = {
     "oxh_conv2d_weight_backward_workspace_size": (_st, [_CS, ctypes.POINTER(_u64)]),
     "oxh_conv2d_weight_backward": (_st, [_vp, _CS, _vp, _vp, _vp, _vp, _u64]),
     "oxh_conv2d_bias_backward": (_st, [_vp, _CS, _vp, _vp, _vp, _u64]),
+    "oxh_depthwise_conv_batch_norm_supported": (_int, [_CS]),
+    "oxh_depthwise_conv_batch_norm_forward_train": (_st, [_vp, _CS, _int, _f32, _f32, _vp, _vp,
+                                                          _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                                          _vp, _vp]),
+    "oxh_depthwise_conv_batch_norm_backward_train": (_st, [_vp, _CS, _vp, _vp, _vp, _vp, _vp,
+                                                           _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                                           _vp, _vp, _vp]),
     "oxh_avg_pool2d_forward": (_st, [_vp, _PS, _vp, _vp]),
     "oxh_avg_pool2d_backward": (_st, [_vp, _PS, _vp, _vp]),
     "oxh_initialized_weights": (_st, [ctypes.POINTER(_u64), _u64, ctypes.POINTER(_f32)]),
@@ -391,6 +398,11 @@ def conv2d_shape(batch, in_channels, height, width, out_channels, kernel, stride
                  groups) -> Conv2dShape:
     return Conv2dShape(batch, in_channels, height, width, out_channels, kernel, kernel, stride,
                        padding, groups)
+
+
+def depthwise_conv_batch_norm_supported(shape: Conv2dShape) -> bool:
+    """Whether the one-launch depthwise conv + BatchNorm entry points take this shape."""
+    return bool(lib().oxh_depthwise_conv_batch_norm_supported(ctypes.byref(shape)))
 
 
 def conv2d_output_size(shape: Conv2dShape) -> tuple[int, int]:
@@ -710,6 +722,33 @@ class LoadedModule:
         ws, wsb = self._conv_ws.ptr_bytes(conv2d_workspace_size(shape))
         check(lib().oxh_conv2d_bias_backward(_stream(stream), ctypes.byref(shape),
                                              _ptr(gradient), _ptr(bias_gradient), ws, wsb))
+
+    def depthwise_conv_batch_norm_forward_train(self, shape, relu, momentum, epsilon, x,
+                                                conv_weight, conv_bias, conv_out, bn_weight,
+                                                bn_bias, running_mean, running_variance,
+                                                saved_mean, saved_inverse_std, out,
+                                                stream=None):
+        """Depthwise conv2d + BatchNorm2d training forward (+ ReLU) in one launch."""
+        check(lib().oxh_depthwise_conv_batch_norm_forward_train(
+            _stream(stream), ctypes.byref(shape), int(relu), momentum, epsilon, _ptr(x),
+            _ptr(conv_weight), _ptr(conv_bias), _ptr(conv_out), _ptr(bn_weight), _ptr(bn_bias),
+            _ptr(running_mean), _ptr(running_variance), _ptr(saved_mean),
+            _ptr(saved_inverse_std), _ptr(out)))
+
+    def depthwise_conv_batch_norm_backward_train(self, shape, gradient, relu_out, conv_out,
+                                                 bn_weight, saved_mean, saved_inverse_std, x,
+                                                 conv_weight, addend, conv_out_gradient,
+                                                 bn_weight_gradient, bn_bias_gradient,
+                                                 conv_bias_gradient, conv_weight_gradient,
+                                                 input_gradient, stream=None):
+        """Its backward in one launch (``relu_out``, ``addend``, ``conv_out_gradient`` and
+        ``input_gradient`` may be None)."""
+        check(lib().oxh_depthwise_conv_batch_norm_backward_train(
+            _stream(stream), ctypes.byref(shape), _ptr(gradient), _ptr(relu_out),
+            _ptr(conv_out), _ptr(bn_weight), _ptr(saved_mean), _ptr(saved_inverse_std), _ptr(x),
+            _ptr(conv_weight), _ptr(addend), _ptr(conv_out_gradient), _ptr(bn_weight_gradient),
+            _ptr(bn_bias_gradient), _ptr(conv_bias_gradient), _ptr(conv_weight_gradient),
+            _ptr(input_gradient)))
 
     def avg_pool2d_forward(self, shape, x, out, stream=None):
         check(lib().oxh_avg_pool2d_forward(_stream(stream), ctypes.byref(shape), _ptr(x),

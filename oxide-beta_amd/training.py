@@ -477,6 +477,14 @@ def op_bytes(op: Op) -> tuple[str, int]:
         return "batch_norm2d", 3 * nb(op.reads["x"]) + acc                 # g, x in; dx out
     if k == "batch_norm2d_relu_backward":
         return "batch_norm2d", 4 * nb(op.reads["x"]) + acc                 # g, y, x in; dx out
+    if k.startswith("depthwise_conv2d_batch_norm") and k.endswith("forward"):
+        # x in; convolution output and layer output out
+        return "conv2d+batch_norm2d", nb(op.reads["x"]) + 2 * nb(op.writes["y"])
+    if k.startswith("depthwise_conv2d_batch_norm"):
+        # g (, y), convolution output, x (, addend) in; output and input gradients out
+        outs = nb(op.reads["gradient"]) * (3 + ("y" in op.reads))
+        ins = nb(op.reads["x"]) * (1 + ("contribution" in op.writes) + ("addend" in op.reads))
+        return "conv2d+batch_norm2d", outs + ins + acc
     if k == "add_forward":
         return "elementwise", 3 * nb(op.reads["a"])
     if k == "relu_forward":

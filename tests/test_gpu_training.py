@@ -143,6 +143,59 @@ class OracleChecker:
                                   r["saved_inverse_std"])
         self._conv_bias(op)
 
+    def _depthwise_forward(self, op, r, relu):
+        """Depthwise conv + BN (+ ReLU) in one launch: the convolution output bit-exact, the
+        BatchNorm on it as a separate BatchNorm forward is checked."""
+        a, w = op.attrs, op.writes
+        conv_y = host(w["conv_y"])
+        assert_bitexact(conv_y, oracle.conv2d_forward(r["x"], r["conv_weight"], r["conv_bias"],
+                                                      a["stride"], a["padding"], a["groups"]),
+                        f"{op.name} conv")
+        out = dict(y=host(w["y"]), mean=host(w["saved_mean"]), inv=host(w["saved_inverse_std"]),
+                   rm=host(a["running_mean"]), rv=host(a["running_variance"]))
+        check_batch_norm_forward(out, conv_y, r["weight"], r["bias"],
+                                 self.prior[id(a["running_mean"])],
+                                 self.prior[id(a["running_variance"])], a["momentum"],
+                                 a["epsilon"], relu=relu)
+
+    def depthwise_conv2d_batch_norm_forward(self, op, r):
+        self._depthwise_forward(op, r, False)
+
+    def depthwise_conv2d_batch_norm_relu_forward(self, op, r):
+        self._depthwise_forward(op, r, True)
+
+    def _depthwise_backward(self, op, r, relu):
+        """Its backward: the BatchNorm gradients as a BatchNorm backward's, then the
+        convolution's bias / weight gradients (fixed-order sums) and input gradient (bit-exact,
+        + the residual addend where one is folded in) from the output gradient it wrote."""
+        a, w = op.attrs, op.writes
+        gc = host(w["conv_output_gradient"])
+        g = oracle.relu_backward(r["gradient"], r["y"]) if relu else r["gradient"]
+        check_batch_norm_backward(dict(dx=gc, dw=host(w["weight_gradient"]),
+                                       db=host(w["bias_gradient"])), g, r["conv_y"],
+                                  r["weight"], r["saved_mean"], r["saved_inverse_std"])
+        x, cw = r["x"], r["conv_weight"]
+        s, p, grp = a["stride"], a["padding"], a["groups"]
+        rdx, rdw, rdb = oracle.conv2d_backward(gc, x, cw, s, p, grp)
+        abs_dw = oracle.conv2d_backward(np.abs(gc), np.abs(x), np.abs(cw), s, p, grp)[1]
+        assert_within(host(w["conv_weight_gradient"]), rdw,
+                      1e-5 * abs_dw.astype(np.float64) + 1e-7, f"{op.name} conv weight")
+        assert_within(host(w["conv_bias_gradient"]), rdb,
+                      1e-5 * np.abs(gc).astype(np.float64).sum(axis=(0, 2, 3)) + 1e-7,
+                      f"{op.name} conv bias")
+        self.counts["conv bias in batch norm backward"] += 1
+        if "contribution" in w:
+            if "addend" in r:
+                rdx = oracle.accumulate(r["addend"], rdx)
+                self.counts["conv input backward with addend"] += 1
+            assert_bitexact(host(w["contribution"]), rdx, f"{op.name} input gradient")
+
+    def depthwise_conv2d_batch_norm_backward(self, op, r):
+        self._depthwise_backward(op, r, False)
+
+    def depthwise_conv2d_batch_norm_relu_backward(self, op, r):
+        self._depthwise_backward(op, r, True)
+
     def relu_forward(self, op, r):
         assert_bitexact(host(op.writes["y"]), oracle.relu(r["x"]), op.name)
 
@@ -192,14 +245,17 @@ class OracleChecker:
 
 # 46 BatchNorms, 32 of them followed by a ReLU (fused), each fed by a convolution whose bias
 # gradient its backward forms (the classifier's, fed by no BN, stays with its parameter
-# backward); 10 residual adds, formed by the forward of the BN feeding them, whose first
+# backward); the 15 depthwise convolutions run with their BatchNorm + ReLU in one launch per
+# direction; 10 residual adds, formed by the forward of the BN feeding them, whose first
 # operand's gradient is the add's own buffer and whose second operand's is added by that
 # operand's convolution input backward (no add launches in either direction)
-EXPECTED_KINDS = {"conv2d_forward": 47, "conv2d_parameter_backward": 47,
-                  "conv2d_input_backward": 46, "batch_norm2d_forward": 4,
+EXPECTED_KINDS = {"conv2d_forward": 32, "conv2d_parameter_backward": 32,
+                  "conv2d_input_backward": 31, "batch_norm2d_forward": 4,
                   "batch_norm2d_add_forward": 10,
-                  "batch_norm2d_relu_forward": 32, "batch_norm2d_backward": 14,
-                  "batch_norm2d_relu_backward": 32,
+                  "batch_norm2d_relu_forward": 17, "batch_norm2d_backward": 14,
+                  "batch_norm2d_relu_backward": 17,
+                  "depthwise_conv2d_batch_norm_relu_forward": 15,
+                  "depthwise_conv2d_batch_norm_relu_backward": 15,
                   "conv input backward with addend": 10,
                   "avg_pool2d_forward": 1, "avg_pool2d_backward": 1, "cross_entropy": 1,
                   "adamw": 1, "conv bias in parameter backward": 1,
