@@ -304,12 +304,12 @@ __device__ __forceinline__ double2 load_lane_partial(const double2 *partial, uin
                        : make_double2(0.0, 0.0);
 }
 
-// Fixed butterfly over the wave; every lane returns lane 0's sums (bit-identical in all
-// blocks and in the finalize kernels, which use the same reduction).
+// Fixed-order sums over the wave, the same in every lane (bit-identical in all blocks and in
+// the finalize kernels, which use the same reduction).
 __device__ __forceinline__ double2 wave_sums_lane0(double2 v) {
   double a = v.x, b = v.y;
   oxh::wave_sum2(a, b);
-  return make_double2(__shfl(a, 0, 64), __shfl(b, 0, 64));
+  return make_double2(a, b);
 }
 
 // One wave per channel: the reference's separate statistics output (no consumer kernel).

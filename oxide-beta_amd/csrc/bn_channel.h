@@ -17,21 +17,18 @@
 
 namespace oxh {
 
+// Wave sums of doubles in wave_sums_rows' fixed order (the total in every lane).
 __device__ __forceinline__ double wave_sum(double v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
+  double a[1] = {v};
+  wave_sums_rows(a);
+  return a[0];
 }
 
-// Two wave sums with their butterfly steps interleaved (each value's additions as wave_sum's):
-// both cross-lane exchanges of a step are in flight together.
 __device__ __forceinline__ void wave_sum2(double &a, double &b) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const double x = __shfl_xor(a, off, 64), y = __shfl_xor(b, off, 64);
-    a += x;
-    b += y;
-  }
+  double v[2] = {a, b};
+  wave_sums_rows(v);
+  a = v[0];
+  b = v[1];
 }
 
 // ReLU backward applied to the incoming gradient (kernel_module.rs:501-508): g where the ReLU's

@@ -82,6 +82,56 @@ __device__ __forceinline__ float tap_term(float p, uint32_t mask) {
 }
 __device__ __forceinline__ uint32_t tap_mask(bool valid) { return valid ? 0xFFFFFFFFu : 0u; }
 
+// Cross-lane moves within rows of 16 lanes through the DPP crossbar (no LDS traffic, unlike
+// __shfl_xor's ds_bpermute).  Controls (DPP_CTRL, GCN3 / Vega ISA): quad_perm [1,0,3,2] and
+// [2,3,0,1] (lane ^ 1, lane ^ 2), row_half_mirror (7 - i within 8), row_mirror (15 - i within
+// 16).  Every lane of the wave must be active.
+template <int Ctrl>
+__device__ __forceinline__ float dpp_move(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), Ctrl, 0xF, 0xF, false));
+}
+template <int Ctrl>
+__device__ __forceinline__ double dpp_move(double v) {
+  const unsigned long long b = static_cast<unsigned long long>(__double_as_longlong(v));
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(
+      0, static_cast<int>(static_cast<uint32_t>(b)), Ctrl, 0xF, 0xF, false));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(
+      0, static_cast<int>(static_cast<uint32_t>(b >> 32)), Ctrl, 0xF, 0xF, false));
+  return __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(hi) << 32) | lo));
+}
+__device__ __forceinline__ float read_lane(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+__device__ __forceinline__ double read_lane(double v, int lane) {
+  const unsigned long long b = static_cast<unsigned long long>(__double_as_longlong(v));
+  const uint32_t lo = static_cast<uint32_t>(
+      __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(b)), lane));
+  const uint32_t hi = static_cast<uint32_t>(
+      __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(b >> 32)), lane));
+  return __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(hi) << 32) | lo));
+}
+
+// Wave-wide sums of Count values per lane in one fixed order: within each row of 16 lanes, add
+// the partner at lane ^ 1, ^ 2, then the mirrored half and row (each step's operands are
+// uniform over the group being combined -- fp addition commutes -- so the mirrors add the same
+// values as xor partners 4 and 8); every lane of a row then holds the row's sum, and the total
+// is (row 0 + row 1) + (row 2 + row 3), returned in every lane.  The values' steps are
+// interleaved.
+template <class T, int Count>
+__device__ __forceinline__ void wave_sums_rows(T (&v)[Count]) {
+#pragma unroll
+  for (int i = 0; i < Count; ++i) v[i] += dpp_move<0xB1>(v[i]);
+#pragma unroll
+  for (int i = 0; i < Count; ++i) v[i] += dpp_move<0x4E>(v[i]);
+#pragma unroll
+  for (int i = 0; i < Count; ++i) v[i] += dpp_move<0x141>(v[i]);
+#pragma unroll
+  for (int i = 0; i < Count; ++i) v[i] += dpp_move<0x140>(v[i]);
+#pragma unroll
+  for (int i = 0; i < Count; ++i)
+    v[i] = (read_lane(v[i], 0) + read_lane(v[i], 16)) + (read_lane(v[i], 32) + read_lane(v[i], 48));
+}
+
 // 128-bit loads / stores with the non-temporal hint (streamed once: do not keep in cache).
 typedef float vf4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float4 load_nt(const float4 *p) {

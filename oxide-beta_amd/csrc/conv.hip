@@ -555,7 +555,7 @@ __global__ __launch_bounds__(256) void conv2d_weight_partial_kernel(
 // of Threads per channel (1024 when there are few channels).  Each thread walks the channel's
 // output positions j, j + Threads, ... and keeps one partial sum per kernel tap in registers
 // (all K * K input loads of a position issued together, taps outside the input adding -0.0f);
-// a fixed xor butterfly per wave and a fixed-order sum over the waves combine them
+// fixed-order wave sums (oxh::wave_sums_rows) and a fixed-order sum over the waves combine them
 // (deterministic; within fp32 rounding of the CPU's (n, oy, ox) running sum).  One launch, in
 // place of batch-chunk partials and their sum.
 template <int K, int Threads>
@@ -590,16 +590,7 @@ __global__ __launch_bounds__(Threads) void conv2d_depthwise_weight_kernel(
     for (int t = 0; t < kTaps; ++t) acc[t] += tap_term(gv * xv[t], mask[t]);
   }
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-  // per-tap xor butterflies, one step of all taps at a time (their exchanges in flight
-  // together; each tap's additions in the same order as a butterfly of its own)
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    float other[kTaps];
-#pragma unroll
-    for (int t = 0; t < kTaps; ++t) other[t] = __shfl_xor(acc[t], off, 64);
-#pragma unroll
-    for (int t = 0; t < kTaps; ++t) acc[t] += other[t];
-  }
+  oxh::wave_sums_rows(acc);  // per-tap wave sums, fixed order
   if (lane == 0) {
 #pragma unroll
     for (int t = 0; t < kTaps; ++t) wave_sums[wave][t] = acc[t];

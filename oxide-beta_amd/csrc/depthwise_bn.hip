@@ -13,7 +13,7 @@
 //   backward  the BatchNorm (relu) channel backward in registers; its dx (the convolution's
 //             output gradient) staged in LDS; the bias gradient as the BatchNorm backward's dx
 //             sum; the weight gradient as conv.hip's depthwise weight kernel at 256 threads
-//             (per-tap register sums, fixed butterflies); the input gradient as conv.hip's
+//             (per-tap register sums, fixed-order wave sums); the input gradient as conv.hip's
 //             input-backward tap kernel (ascending output taps, -0.0f outside, then + addend).
 // The channel's convolution input is staged in LDS once (coalesced plane rows) and read by
 // every tap from there.
@@ -182,16 +182,7 @@ __global__ __launch_bounds__(kDwThreads) void dw_bn_backward_kernel(
     for (int t = 0; t < kTaps; ++t) acc[t] += tap_term(gv * xv[t], mask[t]);
   }
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-  // per-tap xor butterflies, one step of all taps at a time (their exchanges in flight
-  // together; each tap's additions in the same order as a butterfly of its own)
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    float other[kTaps];
-#pragma unroll
-    for (int t = 0; t < kTaps; ++t) other[t] = __shfl_xor(acc[t], off, 64);
-#pragma unroll
-    for (int t = 0; t < kTaps; ++t) acc[t] += other[t];
-  }
+  oxh::wave_sums_rows(acc);  // per-tap wave sums, fixed order
   if (lane == 0) {
 #pragma unroll
     for (int t = 0; t < kTaps; ++t) wave_sums[wave][t] = acc[t];
