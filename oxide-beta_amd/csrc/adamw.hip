@@ -176,10 +176,13 @@ __global__ __launch_bounds__(oxh::kBlock) void adamw_multi_kernel(Hyper h, Tenso
 }
 
 // Device-table variant: the tensor descriptors and each tensor's first chunk live in device
-// memory (any number of tensors, one launch); block b finds its tensor by binary search over
-// the chunk starts.  The step counter is read as t = *step + 1 by every block, and the block
-// that finishes last (a ticket counter, returned to zero by that block) stores t: no separate
-// increment launch, and every block saw the old value (each read it before taking a ticket).
+// memory (any number of tensors, one launch); block b finds its tensor among the chunk starts
+// with a block-parallel search: each round the block's threads probe kBlock evenly spaced
+// starts at once, and the probes at or below b form a prefix (starts never decrease), whose
+// length a barrier count gives -- one round for up to kBlock tensors.  The step counter is
+// read as t = *step + 1 by every block, and the block that finishes last (a ticket counter,
+// returned to zero by that block) stores t: no separate increment launch, and every block saw
+// the old value (each read it before taking a ticket).
 __global__ __launch_bounds__(oxh::kBlock) void adamw_table_kernel(
     Hyper h, const oxh_adamw_tensor *__restrict__ table, const uint32_t *__restrict__ starts,
     uint32_t count, int32_t *step, uint32_t *ticket) {
@@ -187,11 +190,14 @@ __global__ __launch_bounds__(oxh::kBlock) void adamw_table_kernel(
   h.c1 = 1.0f - powi_f32(h.b1, t);
   h.c2 = 1.0f - powi_f32(h.b2, t);
   const uint32_t b = blockIdx.x;
-  uint32_t lo = 0, hi = count;  // the last tensor index with starts[i] <= b
-  while (hi - lo > 1) {
-    const uint32_t mid = (lo + hi) / 2;
-    if (starts[mid] <= b) lo = mid;
-    else hi = mid;
+  uint32_t lo = 0, hi = count;  // the last tensor index with starts[i] <= b is in [lo, hi)
+  while (hi - lo > 1) {          // block-uniform
+    const uint32_t spacing = (hi - lo + oxh::kBlock - 1) / oxh::kBlock;
+    const uint32_t probe = lo + threadIdx.x * spacing;
+    const int at_or_below = __syncthreads_count(probe < hi && starts[probe] <= b);
+    const uint32_t first = lo + static_cast<uint32_t>(at_or_below - 1) * spacing;  // >= lo
+    hi = first + spacing < hi ? first + spacing : hi;
+    lo = first;
   }
   const oxh_adamw_tensor d = table[lo];
   const uint64_t begin = static_cast<uint64_t>(b - starts[lo]) * kChunk;

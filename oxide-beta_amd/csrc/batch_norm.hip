@@ -675,7 +675,7 @@ __global__ __launch_bounds__(Threads) void bn_channel_forward_kernel(
   const uint32_t c = blockIdx.x;
   const float shift = x[static_cast<uint64_t>(c) * g.spatial];  // x[0, c, 0]
   if constexpr (Keep) {
-    float kept[kChannelKeep];
+    float kept[kChannelKeep], added[kChannelKeep];
     uint32_t at[kChannelKeep];
 #pragma unroll
     for (int u = 0; u < kChannelKeep; ++u) {
@@ -683,8 +683,12 @@ __global__ __launch_bounds__(Threads) void bn_channel_forward_kernel(
       at[u] = j < g.samples ? channel_index(g, c, j) : 0;
       kept[u] = x[at[u]];
     }
-    channel_forward_kept<Relu, Threads>(g.samples, c, shift, kept, at, weight, bias, out, addend,
-                                        y, lds);
+    if (addend != nullptr) {
+#pragma unroll
+      for (int u = 0; u < kChannelKeep; ++u) added[u] = addend[at[u]];
+    }
+    channel_forward_kept<Relu, Threads>(g.samples, c, shift, kept, at, weight[c], bias[c], out,
+                                        addend != nullptr ? added : nullptr, y, lds);
   } else {
     const double k = static_cast<double>(shift);
     double sum = 0.0, sq = 0.0;
@@ -731,7 +735,7 @@ __global__ __launch_bounds__(Threads) void bn_channel_backward_kernel(
       kg[u] = gv;
       kn[u] = (x[at[u]] - mu) * inv;
     }
-    channel_backward_kept<Threads>(g.samples, c, kg, kn, weight[c], inv, dweight, dbias, d,
+    channel_backward_kept<Threads>(g.samples, kg, kn, weight[c], inv, dweight + c, dbias + c, d,
                                    lds[0]);
 #pragma unroll
     for (int u = 0; u < kChannelKeep; ++u) {

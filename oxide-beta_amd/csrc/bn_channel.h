@@ -119,14 +119,17 @@ constexpr int kChannelKeep = 8;
 
 // Training forward of channel c from the values in registers: fp64 sums of (v - shift) and
 // (v - shift)^2 with shift = the channel's first value (x[0, c, 0]), the statistics (thread 0
-// writes the saved / running outputs), then y = relu?(BN(v)) (+ addend) at the positions `at`.
+// writes the saved / running outputs), then y = relu?(BN(v)) (+ added[u] when `added` is not
+// null) at the positions `at`.  The BatchNorm weight w, bias b and the addend values are
+// passed in, loaded by the caller together with the channel's values (a load issued after the
+// sums' barrier would put a second memory round trip on the block).
 template <bool Relu, int Threads>
 __device__ __forceinline__ void channel_forward_kept(uint32_t samples, uint32_t c, float shift,
                                                      const float (&kept)[kChannelKeep],
-                                                     const uint32_t (&at)[kChannelKeep],
-                                                     const float *weight, const float *bias,
-                                                     const StatsOut &out, const float *addend,
-                                                     float *y, double (*lds)[Threads / 64]) {
+                                                     const uint32_t (&at)[kChannelKeep], float w,
+                                                     float b, const StatsOut &out,
+                                                     const float *added, float *y,
+                                                     double (*lds)[Threads / 64]) {
   const double k = static_cast<double>(shift);
   double sum = 0.0, sq = 0.0;
 #pragma unroll
@@ -139,26 +142,26 @@ __device__ __forceinline__ void channel_forward_kept(uint32_t samples, uint32_t 
   block_sum2_all<Threads / 64>(sum, sq, lds);
   const Moments r = forward_moments(make_double2(sum, sq), shift, samples, out.epsilon);
   if (threadIdx.x == 0) write_forward_outputs(out, c, r);
-  const float mu = r.mean, inv = r.inv, w = weight[c], b = bias[c];
+  const float mu = r.mean, inv = r.inv;
 #pragma unroll
   for (int u = 0; u < kChannelKeep; ++u)
     if (threadIdx.x + u * Threads < samples) {
       float v = (kept[u] - mu) * inv * w + b;  // evaluation.rs:590-595
       if constexpr (Relu) v = v > 0.0f ? v : 0.0f;
-      y[at[u]] = addend != nullptr ? v + addend[at[u]] : v;
+      y[at[u]] = added != nullptr ? v + added[u] : v;
     }
 }
 
-// Training backward of channel c from registers: kg = the incoming gradient (already masked by
+// Training backward of a channel from registers: kg = the incoming gradient (already masked by
 // a following ReLU), kn = x_hat in fp32.  Sums (sum g, sum g * x_hat) in fp64, rounded to fp32
-// as dbias[c] / dweight[c] (thread 0), and d[u] = dx for the thread's valid positions
-// (autograd.rs:344-373).
+// and stored by thread 0 to *dbias_c / *dweight_c when those are not null, and d[u] = dx for
+// the thread's valid positions (autograd.rs:344-373).
 template <int Threads>
-__device__ __forceinline__ void channel_backward_kept(uint32_t samples, uint32_t c,
+__device__ __forceinline__ void channel_backward_kept(uint32_t samples,
                                                       const float (&kg)[kChannelKeep],
                                                       const float (&kn)[kChannelKeep],
-                                                      float weight_c, float inv, float *dweight,
-                                                      float *dbias, float (&d)[kChannelKeep],
+                                                      float weight_c, float inv, float *dweight_c,
+                                                      float *dbias_c, float (&d)[kChannelKeep],
                                                       double (*lds)[Threads / 64]) {
   double sg = 0.0, sgx = 0.0;
 #pragma unroll
@@ -169,9 +172,9 @@ __device__ __forceinline__ void channel_backward_kept(uint32_t samples, uint32_t
   }
   block_sum2_all<Threads / 64>(sg, sgx, lds);
   const float sgf = static_cast<float>(sg), sgxf = static_cast<float>(sgx);
-  if (threadIdx.x == 0) {
-    dbias[c] = sgf;
-    dweight[c] = sgxf;
+  if (threadIdx.x == 0 && dbias_c != nullptr) {
+    *dbias_c = sgf;
+    *dweight_c = sgxf;
   }
   const float m = static_cast<float>(samples);
   const float coef = weight_c * inv / m;

@@ -799,6 +799,20 @@ __global__ __launch_bounds__(Threads) void pointwise_product_kernel(ProductArgs 
 #pragma unroll
     for (int j = 0; j < kMicro; ++j) acc[i][j] = v;
   }
+  // the addend is loaded now, with the first slab (after the k loop it would add a memory
+  // round trip to the block)
+  float added[kMicro][kMicro];
+  if (g.addend != nullptr) {
+#pragma unroll
+    for (int i = 0; i < kMicro; ++i)
+#pragma unroll
+      for (int j = 0; j < kMicro; ++j) {
+        const uint32_t m = m0 + ty * kMicro + i, n = n0 + tx * kMicro + j;
+        added[i][j] = m < g.M && n < g.N
+                          ? g.addend[axis_offset(g.cm, m) + axis_offset(g.cn, n)]
+                          : 0.0f;
+      }
+  }
   const SlabLoader<Tile, Threads, AKFast> la(g.a, m0, g.M);
   const SlabLoader<Tile, Threads, BKFast> lb(g.b, n0, g.N);
   float va[kLoads], vb[kLoads];
@@ -887,7 +901,7 @@ __global__ __launch_bounds__(Threads) void pointwise_product_kernel(ProductArgs 
       const uint32_t n = n0 + tx * kMicro + j;
       if (n >= g.N) continue;
       const uint32_t idx = axis_offset(g.cm, m) + axis_offset(g.cn, n);
-      c[idx] = g.addend != nullptr ? acc[i][j] + g.addend[idx] : acc[i][j];
+      c[idx] = g.addend != nullptr ? acc[i][j] + added[i][j] : acc[i][j];
     }
   }
 }

@@ -80,7 +80,7 @@ __global__ __launch_bounds__(kDwThreads) void dw_bn_forward_kernel(
   float wv[K * K];
 #pragma unroll
   for (int t = 0; t < K * K; ++t) wv[t] = conv_weight[c * (K * K) + t];
-  const float bias = conv_bias[c];
+  const float bias = conv_bias[c], w = bn_weight[c], b = bn_bias[c];
   __syncthreads();
   const uint32_t oplane = g.oh * g.ow, plane = g.h * g.w, samples = g.out.samples;
   float kept[kChannelKeep];
@@ -94,22 +94,30 @@ __global__ __launch_bounds__(kDwThreads) void dw_bn_forward_kernel(
     const int by = static_cast<int>(oy) * S - static_cast<int>(g.pad);
     const int bx = static_cast<int>(ox) * S - static_cast<int>(g.pad);
     const float *xp = xs + n * plane;
+    int row[K], col[K];
+    uint32_t my[K], mx[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const bool vy = static_cast<uint32_t>(by + k) < g.h, vx = static_cast<uint32_t>(bx + k) < g.w;
+      row[k] = vy ? (by + k) * static_cast<int>(g.w) : 0;
+      col[k] = vx ? bx + k : 0;
+      my[k] = tap_mask(vy);
+      mx[k] = tap_mask(vx);
+    }
+    float xv[K * K];
+#pragma unroll
+    for (int t = 0; t < K * K; ++t) xv[t] = xp[row[t / K] + col[t % K]];
     float sum = bias;
 #pragma unroll
-    for (int t = 0; t < K * K; ++t) {
-      const int iy = by + t / K, ix = bx + t % K;
-      const bool v = static_cast<uint32_t>(iy) < g.h && static_cast<uint32_t>(ix) < g.w;
-      const float xv = xp[v ? iy * static_cast<int>(g.w) + ix : 0];
-      sum += tap_term(xv * wv[t], tap_mask(v));
-    }
+    for (int t = 0; t < K * K; ++t) sum += tap_term(xv[t] * wv[t], my[t / K] & mx[t % K]);
     kept[u] = sum;
     at[u] = (n * g.out.channels + c) * oplane + r;
     conv_out[at[u]] = sum;
   }
   if (threadIdx.x == 0) shift = kept[0];  // conv_out[0, c, 0] (samples >= 2)
   __syncthreads();
-  oxh::channel_forward_kept<Relu, kDwThreads>(samples, c, shift, kept, at, bn_weight, bn_bias,
-                                              stats, nullptr, y, lds);
+  oxh::channel_forward_kept<Relu, kDwThreads>(samples, c, shift, kept, at, w, b, stats, nullptr,
+                                              y, lds);
 }
 
 template <int K, int S, bool Relu>
@@ -143,8 +151,8 @@ __global__ __launch_bounds__(kDwThreads) void dw_bn_backward_kernel(
   }
   stage_channel(g, c, x, xs);
   if (threadIdx.x < kTaps) wts[threadIdx.x] = conv_weight[c * kTaps + threadIdx.x];
-  oxh::channel_backward_kept<kDwThreads>(samples, c, kg, kn, bn_weight[c], inv, bn_dweight,
-                                         bn_dbias, d, lds[0]);
+  oxh::channel_backward_kept<kDwThreads>(samples, kg, kn, bn_weight[c], inv, bn_dweight + c,
+                                         bn_dbias + c, d, lds[0]);
   double total = 0.0, unused = 0.0;
 #pragma unroll
   for (int u = 0; u < kChannelKeep; ++u) {
