@@ -58,10 +58,17 @@ __device__ __forceinline__ bool target_index(float t, uint64_t classes, uint64_t
   return true;
 }
 
+// Block max: within each row of 16 lanes through DPP moves (xor 1, xor 2, mirrored half, mirrored
+// row: every lane then holds its row's max), the four rows through lane reads, then the waves
+// through LDS.  max is exact, so the order is immaterial.
 template <int BLOCK>
 __device__ __forceinline__ float block_max(float v, float *lds) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  v = fmaxf(v, oxh::dpp_move<0xB1>(v));
+  v = fmaxf(v, oxh::dpp_move<0x4E>(v));
+  v = fmaxf(v, oxh::dpp_move<0x141>(v));
+  v = fmaxf(v, oxh::dpp_move<0x140>(v));
+  v = fmaxf(fmaxf(oxh::read_lane(v, 0), oxh::read_lane(v, 16)),
+            fmaxf(oxh::read_lane(v, 32), oxh::read_lane(v, 48)));
   constexpr int W = BLOCK / 64;
   const int wave = threadIdx.x / 64;
   if (threadIdx.x % 64 == 0) lds[wave] = v;
@@ -73,10 +80,12 @@ __device__ __forceinline__ float block_max(float v, float *lds) {
   return r;
 }
 
+// Block sum in a fixed order: oxh::wave_sums_rows within each wave, then the waves in order.
 template <int BLOCK>
 __device__ __forceinline__ double block_sum(double v, double *lds) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  double w[1] = {v};
+  oxh::wave_sums_rows(w);
+  v = w[0];
   constexpr int W = BLOCK / 64;
   const int wave = threadIdx.x / 64;
   if (threadIdx.x % 64 == 0) lds[wave] = v;
@@ -138,6 +147,9 @@ __global__ __launch_bounds__(BLOCK, MINW) void ce_row_kernel(CeArgs a) {
   const uint64_t row = blockIdx.x;
   const uint32_t c4 = static_cast<uint32_t>(a.classes / 4);
   const float4 *x4 = reinterpret_cast<const float4 *>(a.logits + row * a.classes);
+  // loaded with the row (read after the reductions they would add a memory round trip)
+  const float target_value = a.targets[row];
+  const float outer = a.grad ? *a.outer : 0.0f;
   auto in_row = [&](int k) { return FULL || threadIdx.x + static_cast<uint32_t>(k) * BLOCK < c4; };
   float4 v[V];
 #pragma unroll
@@ -167,7 +179,7 @@ __global__ __launch_bounds__(BLOCK, MINW) void ce_row_kernel(CeArgs a) {
     for (int k = 0; k + w < V; k += 2 * w) part[k] += part[k + w];
   const float normalizer = static_cast<float>(block_sum<BLOCK>(static_cast<double>(part[0]), lds_d));
   uint64_t target = 0;
-  const bool valid = target_index(a.targets[row], a.classes, target);
+  const bool valid = target_index(target_value, a.classes, target);
   if (!valid && threadIdx.x == 0 && a.error_flag) *a.error_flag = 1u;
   if (a.grad) {
     float4 *g4 = reinterpret_cast<float4 *>(a.grad + row * a.classes);
@@ -180,7 +192,7 @@ __global__ __launch_bounds__(BLOCK, MINW) void ce_row_kernel(CeArgs a) {
       // e * ((outer / B) / normalizer), within 2.5 ulp of the CPU's scale * (e / normalizer),
       // one multiply per logit.  The target logit keeps scale * (e / normalizer - 1) exactly,
       // since the subtraction cancels.
-      const float scale = *a.outer / static_cast<float>(a.batch);
+      const float scale = outer / static_cast<float>(a.batch);
       const float sr = scale / normalizer;
       const uint32_t t4 = static_cast<uint32_t>(target / 4);
       const uint32_t owner = t4 % BLOCK, kt = t4 / BLOCK, ct = static_cast<uint32_t>(target % 4);
@@ -236,6 +248,43 @@ __global__ __launch_bounds__(kGenBlock) void ce_row_general_kernel(CeArgs a) {
   finish_row(a, row, row_loss);
 }
 
+// Small problems (at most kSmallRows rows of at most kSmallClasses classes, e.g. a batch of
+// MNIST logits): one block, one thread per row running the general kernel's per-row steps
+// serially, and the batch mean in the same launch -- the fp64 row losses summed in
+// ce_mean_kernel's order (thread t holds row t).
+constexpr int kSmallRows = 1024;
+constexpr uint64_t kSmallClasses = 64;
+
+__global__ __launch_bounds__(kSmallRows) void ce_small_kernel(CeArgs a) {
+  __shared__ double lds[kSmallRows / 64];
+  const uint64_t row = threadIdx.x;
+  double row_loss = 0.0;
+  if (row < a.batch) {
+    const float *x = a.logits + row * a.classes;
+    float maximum = -INFINITY;
+    for (uint64_t i = 0; i < a.classes; ++i) maximum = fmaxf(maximum, x[i]);
+    double s = 0.0;
+    for (uint64_t i = 0; i < a.classes; ++i) s += static_cast<double>(expf(x[i] - maximum));
+    const float normalizer = static_cast<float>(s);
+    uint64_t target = 0;
+    const bool valid = target_index(a.targets[row], a.classes, target);
+    if (!valid && a.error_flag) *a.error_flag = 1u;
+    if (a.grad) {
+      const float scale = *a.outer / static_cast<float>(a.batch);
+      float *g = a.grad + row * a.classes;
+      for (uint64_t i = 0; i < a.classes; ++i) {
+        const float p = expf(x[i] - maximum) / normalizer;
+        g[i] = valid ? scale * (p - (i == target ? 1.0f : 0.0f)) : NAN;
+      }
+    }
+    row_loss = static_cast<double>(valid ? logf(normalizer) + maximum - x[target] : NAN);
+  }
+  if (a.loss != nullptr) {
+    const double total = block_sum<kSmallRows>(row_loss, lds);
+    if (threadIdx.x == 0) *a.loss = static_cast<float>(total) / static_cast<float>(a.batch);
+  }
+}
+
 uint64_t ce_workspace_bytes(uint64_t batch) { return (batch * 8 + 255) / 256 * 256; }
 
 oxh_status launch_ce(const char *name, oxh_stream stream, CeArgs a, void *workspace,
@@ -265,6 +314,10 @@ oxh_status launch_ce(const char *name, oxh_stream stream, CeArgs a, void *worksp
                 OXH_INVALID_SHAPE, std::string(name) + ": workspace overlaps the logits or grad");
   }
   hipStream_t s = oxh::as_stream(stream);
+  if (a.batch <= static_cast<uint64_t>(kSmallRows) && a.classes <= kSmallClasses) {
+    oxh::launch(ce_small_kernel, dim3(1), dim3(kSmallRows), 0, s, a);
+    return oxh::launched(name);
+  }
   const dim3 grid(static_cast<uint32_t>(a.batch));
   const bool vec = a.classes % 4 == 0 && oxh::aligned16(a.logits) &&
                    (!a.grad || oxh::aligned16(a.grad));

@@ -263,12 +263,15 @@ __device__ __forceinline__ float4 chain_step4(const oxh::ChainStep &s, const flo
                      chain_step(s.op, x0.z, x1.z), chain_step(s.op, x0.w, x1.w));
 }
 
-// A fused chain: per float4 of elements the steps run in order on registers, each loading its
-// other operand (non-temporal) and storing its result where the plan needs it.  The steps are
-// kernel arguments, so every branch on them is uniform; occupancy hides the per-step loads.
+// A fused chain: per float4 of elements the steps run in order on registers, each combining
+// the running value with its other operand and storing its result where the plan needs it.
+// Every step's other operand is loaded before the first step runs (non-temporal; no step
+// writes a buffer a later step reads), so all of a tile's loads are in flight together.  The
+// steps are kernel arguments: the loops over them are unrolled to kChainMax with
+// block-uniform exits, keeping the operand registers statically indexed.
 __global__ __launch_bounds__(oxh::kBlock) void chain_vec4_kernel(oxh::Chain c, uint64_t n4,
                                                                  uint64_t n) {
-  constexpr int U = kUnroll;  // float4 per thread per stream, loads of a step issued together
+  constexpr int U = kUnroll;  // float4 per thread per stream
   const uint64_t tile = static_cast<uint64_t>(oxh::kBlock) * U;
   for (uint64_t base = static_cast<uint64_t>(blockIdx.x) * tile + threadIdx.x; base < n4;
        base += static_cast<uint64_t>(gridDim.x) * tile) {
@@ -282,19 +285,22 @@ __global__ __launch_bounds__(oxh::kBlock) void chain_vec4_kernel(oxh::Chain c, u
       if (!live[u]) idx[u] = base;  // a repeat of element base: loaded, never stored
       acc[u] = oxh::load_nt(reinterpret_cast<const float4 *>(c.first) + idx[u]);
     }
-    for (uint32_t k = 0; k < c.count; ++k) {
+    float4 operand[oxh::kChainMax][U];
+#pragma unroll
+    for (int k = 0; k < oxh::kChainMax; ++k) {
+      if (k >= static_cast<int>(c.count)) break;
+      if (c.steps[k].other < 0) continue;
+      const float4 *src = reinterpret_cast<const float4 *>(c.other[c.steps[k].other]);
+#pragma unroll
+      for (int u = 0; u < U; ++u) operand[k][u] = oxh::load_nt(src + idx[u]);
+    }
+#pragma unroll
+    for (int k = 0; k < oxh::kChainMax; ++k) {
+      if (k >= static_cast<int>(c.count)) break;
       const oxh::ChainStep s = c.steps[k];
-      float4 b[U];
-      if (s.other >= 0) {
-        const float4 *src = reinterpret_cast<const float4 *>(c.other[s.other]);
 #pragma unroll
-        for (int u = 0; u < U; ++u) b[u] = oxh::load_nt(src + idx[u]);
-      } else {
-#pragma unroll
-        for (int u = 0; u < U; ++u) b[u] = acc[u];
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u) acc[u] = chain_step4(s, acc[u], b[u]);
+      for (int u = 0; u < U; ++u)
+        acc[u] = chain_step4(s, acc[u], s.other >= 0 ? operand[k][u] : acc[u]);
       if (s.store >= 0) {
         float4 *dst = reinterpret_cast<float4 *>(c.store[s.store]);
 #pragma unroll

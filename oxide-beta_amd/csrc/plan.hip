@@ -7,7 +7,8 @@
 //            recorded once into a graph and instantiated (47-55);
 //   run:     inputs copied host-to-device into their fixed buffers, one graph replay, the
 //            output copied back synchronously (70-99);
-//   replay:  the graph alone, for callers whose inputs are already resident.
+//   replay:  the graph alone (a single-launch plan: that launch), for callers whose inputs are
+//            already resident.
 // Plan operations are the reference's Add / Mul / Relu plus the backward elementwise kernels.
 // compile fuses each run of operations in which every operation consumes the previous one's
 // result (and reads no buffer an earlier operation of the run wrote) into one streaming kernel
@@ -21,6 +22,10 @@
 
 #include "chain.h"
 #include "common.h"
+
+#ifndef OXH_PLAN_GRAPH_REPLAY
+#define OXH_PLAN_GRAPH_REPLAY 0  // 1: replay single-launch plans through their graph too
+#endif
 
 namespace {
 
@@ -64,6 +69,7 @@ struct oxh_plan {
   int64_t output = -1;
   hipStream_t stream = nullptr;
   oxh_graph *graph = nullptr;
+  std::vector<std::pair<size_t, size_t>> launches;  // compiled launch groups [begin, end)
   bool compiled = false;
 };
 
@@ -287,7 +293,9 @@ oxh_status oxh_plan_compile(oxh_plan *plan) {
     release(plan);
     return st;
   }
+  plan->launches.clear();
   for (const Run &r : form_runs(*plan)) {
+    plan->launches.emplace_back(r.begin, r.end);
     st = r.end - r.begin == 1 ? launch_operation(*plan, plan->operations[r.begin])
                               : launch_run(*plan, r);
     if (st != OXH_OK) {
@@ -327,8 +335,18 @@ oxh_status oxh_plan_run(oxh_plan *plan, const float *const *host_inputs, uint32_
   return oxh_memcpy_d2h(host_output, out.device, out.elements * sizeof(float), plan->stream);
 }
 
+// A plan compiled to a single launch (e.g. a fully fused chain) is replayed by issuing that
+// launch directly -- the same kernel and arguments the graph holds, without the graph
+// launch's extra work per replay; longer plans replay their graph.
 oxh_status oxh_plan_replay(oxh_plan *plan) {
   OXH_REQUIRE(plan != nullptr && plan->compiled, OXH_TRACE, "plan is not compiled");
+#if !OXH_PLAN_GRAPH_REPLAY
+  if (plan->launches.size() == 1) {
+    const Run r{plan->launches[0].first, plan->launches[0].second};
+    return r.end - r.begin == 1 ? launch_operation(*plan, plan->operations[r.begin])
+                                : launch_run(*plan, r);
+  }
+#endif
   return oxh_graph_launch(plan->graph, plan->stream);
 }
 
