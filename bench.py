@@ -125,7 +125,10 @@ def bench_batch_norm(m, steps: int, warmup: int, sets: int = 4):
     kernels = {}
     for nm in names:
         avg_ms = sum(per_kernel[nm]) / len(per_kernel[nm])
+        q = sorted(per_kernel[nm])
+        pct = lambda f: round(q[min(len(q) - 1, int(f * len(q)))] * 1e3, 2)  # noqa: E731
         kernels[nm] = {"avg_us": round(avg_ms * 1e3, 2),
+                       "p10_us": pct(0.1), "median_us": pct(0.5), "p90_us": pct(0.9),
                        "alg_bytes": bytes_per[nm],
                        "gbs": round(bytes_per[nm] / (avg_ms * 1e-3) / 1e9, 1)}
     event_ms_per_step = total_ms / steps
@@ -229,7 +232,7 @@ def bench_elementwise(m, reps: int = 20):
     }
 
 
-def bench_cross_entropy(m, reps: int = 10):
+def bench_cross_entropy(m, reps: int = 20):
     import torch
 
     dev = torch.device("cuda:0")
@@ -264,7 +267,7 @@ def bench_cross_entropy(m, reps: int = 10):
             "fwd_gbs": round(L / fwd / 1e3, 1)}
 
 
-def bench_adamw(m, reps: int = 10):
+def bench_adamw(m, reps: int = 30):
     import torch
 
     import oxide_hip as ox
@@ -371,6 +374,39 @@ def copy_calibration():
     torch.cuda.synchronize()
 
 
+def copy_ceiling(reps: int = 10):
+    """The streaming ceilings the kernels above are read against: 1 GiB device-to-device
+    copies (1 GiB read + 1 GiB written each), timed with events over `reps` back-to-back
+    copies -- torch's vectorized elementwise copy kernel and hipMemcpyAsync's blit kernel."""
+    import torch
+
+    import oxide_hip as ox
+
+    src = torch.zeros(1 << 28, device="cuda")
+    dst = torch.empty_like(src)
+    s = torch.cuda.current_stream()
+
+    def timed(fn):
+        for _ in range(2):
+            fn()
+        e0, e1 = _events(2)
+        e0.record(s)
+        for _ in range(reps):
+            fn()
+        e1.record(s)
+        e1.synchronize()
+        us = e0.elapsed_time(e1) / reps * 1e3
+        return {"us": round(us, 1), "gbs": round(2 * (1 << 30) / (us * 1e-6) / 1e9, 1)}
+
+    out = {"what": "1 GiB device-to-device copy (2 GiB traffic)",
+           "torch_copy": timed(lambda: dst.copy_(src)),
+           "hip_memcpy": timed(lambda: ox.check(ox.lib().oxh_memcpy_d2d_async(
+               dst.data_ptr(), src.data_ptr(), 1 << 30, s.cuda_stream)))}
+    del src, dst
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(budget_s: float = 12.0):
     """The oracle (single-threaded C restatement of the reference CPU path) on one full BN
     step at config 2: forward (statistics, running update, apply) + backward."""
@@ -447,7 +483,8 @@ def main():
              "bn_eager_ms_per_step": round(bn["eager_ms_per_step"], 4),
              "bn_eager_gbs": round(8 * T_BN / (bn["eager_ms_per_step"] * 1e-3) / 1e9, 1),
              "bn_events_ms_per_step": round(bn["event_ms_per_step"], 4),
-             "bn_graph_steps_timed": bn["graph_steps"]}
+             "bn_graph_steps_timed": bn["graph_steps"],
+             "copy_ceiling": copy_ceiling()}
     chosen = [] if args.no_extra else [e for e in args.extras.split(",") if e]
     for name in chosen:
         if name not in EXTRAS:
