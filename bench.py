@@ -421,18 +421,39 @@ def cpu_baseline(budget_s: float = 12.0):
     gamma = r.uniform(0.5, 1.5, 128).astype(np.float32)
     beta = r.uniform(-0.1, 0.1, 128).astype(np.float32)
     rm, rv = np.zeros(128, np.float32), np.ones(128, np.float32)
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while len(times) < 2 or (time.perf_counter() < t_end and len(times) < 20):
-        t0 = time.perf_counter()
-        y, mean, inv, rm, rv = oracle.bn_forward(x, gamma, beta, rm, rv)
+    # one core, as the reference's CPU path runs (no threading): pinned for the timing
+    affinity = os.sched_getaffinity(0) if hasattr(os, "sched_getaffinity") else None
+    core = min(affinity) if affinity else None
+    if core is not None:
+        os.sched_setaffinity(0, {core})
+    try:
+        y, mean, inv, rm, rv = oracle.bn_forward(x, gamma, beta, rm, rv)  # warm-up step
         oracle.bn_backward(g, x, gamma, mean, inv, True)
-        times.append(time.perf_counter() - t0)
+        times = []
+        t_end = time.perf_counter() + budget_s
+        while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 20):
+            t0 = time.perf_counter()
+            y, mean, inv, rm, rv = oracle.bn_forward(x, gamma, beta, rm, rv)
+            oracle.bn_backward(g, x, gamma, mean, inv, True)
+            times.append(time.perf_counter() - t0)
+    finally:
+        if core is not None:
+            os.sched_setaffinity(0, affinity)
     best = sorted(times)[len(times) // 2]
+    cpu_model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            cpu_model = next(line.split(":", 1)[1].strip() for line in f
+                             if line.startswith("model name"))
+    except (OSError, StopIteration):
+        pass
     return {"value": round(8 * T_BN / best / 1e9, 2), "unit": "GB/s", "cores": 1,
             "kind": "port",
-            "sample": f"{len(times)} full config-2 BN fwd+bwd steps (median {best * 1e3:.0f} ms "
-                      f"per step) of oracle/oxide_oracle.c, single thread"}
+            "sample": f"{len(times)} full config-2 BN fwd+bwd steps after one warm-up (median "
+                      f"{best * 1e3:.0f} ms per step) of oracle/oxide_oracle.c, single thread "
+                      f"pinned to core {core}",
+            "host": {"cpu": cpu_model, "nproc": os.cpu_count(),
+                     "affinity_cores": len(affinity) if affinity else None}}
 
 
 def main():
