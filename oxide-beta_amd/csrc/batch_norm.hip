@@ -688,7 +688,7 @@ __global__ __launch_bounds__(Threads) void bn_channel_forward_kernel(
       for (int u = 0; u < kChannelKeep; ++u) added[u] = addend[at[u]];
     }
     channel_forward_kept<Relu, Threads>(g.samples, c, shift, kept, at, weight[c], bias[c], out,
-                                        addend != nullptr ? added : nullptr, y, lds);
+                                        addend != nullptr, added, y, lds);
   } else {
     const double k = static_cast<double>(shift);
     double sum = 0.0, sq = 0.0;

@@ -116,8 +116,9 @@ __global__ __launch_bounds__(kDwThreads) void dw_bn_forward_kernel(
   }
   if (threadIdx.x == 0) shift = kept[0];  // conv_out[0, c, 0] (samples >= 2)
   __syncthreads();
-  oxh::channel_forward_kept<Relu, kDwThreads>(samples, c, shift, kept, at, w, b, stats, nullptr,
-                                              y, lds);
+  const float none[kChannelKeep] = {};
+  oxh::channel_forward_kept<Relu, kDwThreads>(samples, c, shift, kept, at, w, b, stats, false,
+                                              none, y, lds);
 }
 
 template <int K, int S, bool Relu>
