@@ -407,6 +407,75 @@ def copy_ceiling(reps: int = 10):
     return out
 
 
+class _OneCore:
+    """Pins the process to one core for the duration (the reference's CPU path is
+    single-threaded)."""
+
+    def __enter__(self):
+        self.affinity = os.sched_getaffinity(0) if hasattr(os, "sched_getaffinity") else None
+        self.core = min(self.affinity) if self.affinity else None
+        if self.core is not None:
+            os.sched_setaffinity(0, {self.core})
+        return self
+
+    def __exit__(self, *exc):
+        if self.core is not None:
+            os.sched_setaffinity(0, self.affinity)
+
+
+def _cpu_time(fn, reps: int = 3):
+    fn()  # warm-up
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return sorted(times)[len(times) // 2]
+
+
+def cpu_other_configs():
+    """The oracle (one core) on configs 1, 3 and 4, timed beside the GPU figures: 1 warm-up and
+    the median of 3 repetitions each, GB/s over the same algorithmic bytes as the GPU lines."""
+    import numpy as np
+
+    import oracle
+
+    out = {}
+    with _OneCore() as pin:
+        r = np.random.default_rng(0x6F78696400000001)
+        n = 4096 * 4096
+        a, b, c = (r.uniform(-1, 1, n).astype(np.float32) for _ in range(3))
+        fwd = _cpu_time(lambda: oracle.relu(oracle.mul(oracle.add(a, b), c)))
+        bwd = _cpu_time(lambda: oracle.chain_backward_ones(a, b, c))
+        out["elementwise"] = {
+            "sample": "relu((a+b)*c) on 3x[4096,4096]: forward as the CPU plan's three passes, "
+                      "backward of sum()",
+            "fwd_ms": round(fwd * 1e3, 1), "fwd_gbs": round(8 * n * 4 / fwd / 1e9, 2),
+            "bwd_ms": round(bwd * 1e3, 1), "bwd_gbs": round(6 * n * 4 / bwd / 1e9, 2)}
+        rows, classes = 512, 32768
+        r = np.random.default_rng(0x6F78696400000003)
+        logits = (r.standard_normal((rows, classes)) * 2).astype(np.float32)
+        targets = r.integers(0, classes, rows).astype(np.float32)
+        ce = _cpu_time(lambda: (oracle.ce_forward(logits, targets),
+                                oracle.ce_backward(logits, targets, 1.0)))
+        out["cross_entropy"] = {
+            "sample": f"{rows} of config 3's 8192 rows x 32768 classes: loss + gradient",
+            "ms": round(ce * 1e3, 1), "gbs": round(2 * rows * classes * 4 / ce / 1e9, 2),
+            "full_config_ms_est": round(ce * 8192 / rows * 1e3, 0)}
+        n = 64 << 20
+        r = np.random.default_rng(0x6F78696400000004)
+        p = (r.standard_normal(n, dtype=np.float32) * 0.02)
+        g = (r.standard_normal(n, dtype=np.float32) * 1e-3)
+        m = (r.standard_normal(n, dtype=np.float32) * 1e-4)
+        v = np.abs(r.standard_normal(n, dtype=np.float32)) * 1e-9
+        aw = _cpu_time(lambda: oracle.adamw_update(p, g, m, v, 10))
+        out["adamw"] = {"sample": "config 4: 64Mi elements, t=10", "ms": round(aw * 1e3, 1),
+                        "gbs": round(7 * n * 4 / aw / 1e9, 2)}
+        out["cores"] = 1
+        out["pinned_core"] = pin.core
+    return out
+
+
 def cpu_baseline(budget_s: float = 12.0):
     """The oracle (single-threaded C restatement of the reference CPU path) on one full BN
     step at config 2: forward (statistics, running update, apply) + backward."""
@@ -540,6 +609,8 @@ def main():
         "cpu_baseline": None if args.no_cpu else cpu_baseline(),
         "extra": extra,
     }
+    if not args.no_cpu and not args.no_extra:
+        extra["cpu_other_configs"] = cpu_other_configs()
     if args.copy_calibration:
         copy_calibration()
     print(json.dumps(out), flush=True)
