@@ -6,6 +6,7 @@
 // device.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <string>
 
@@ -99,11 +100,32 @@ oxh_status oxh_free(void *ptr) {
   return oxh::ok();
 }
 
+namespace {
+// Zero fill as a kernel rather than hipMemsetAsync, so that a caller may record it into a
+// graph (memset nodes have given wrong results on replays after the first on gfx950 boxes).
+// `head` bytes up to 16-byte alignment, `body` 16-byte words, then `tail` bytes.
+__global__ __launch_bounds__(256) void zero_bytes_kernel(uint8_t *p, uint32_t head, uint64_t body,
+                                                         uint32_t tail) {
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+  const uint64_t first = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (first < head) p[first] = 0;
+  uint4 *words = reinterpret_cast<uint4 *>(p + head);
+  for (uint64_t i = first; i < body; i += stride) words[i] = make_uint4(0u, 0u, 0u, 0u);
+  if (first < tail) p[head + body * 16 + first] = 0;
+}
+}  // namespace
+
 oxh_status oxh_memset0_async(void *ptr, uint64_t bytes, oxh_stream stream) {
   if (bytes == 0) return oxh::ok();
   OXH_REQUIRE(ptr != nullptr, OXH_INVALID_SHAPE, "ptr is null");
-  OXH_HIP_CHECK(hipMemsetAsync(ptr, 0, bytes, oxh::as_stream(stream)));
-  return oxh::ok();
+  const uint32_t head =
+      static_cast<uint32_t>(std::min<uint64_t>(bytes, (16 - reinterpret_cast<uintptr_t>(ptr) % 16) % 16));
+  const uint64_t body = (bytes - head) / 16;
+  const uint32_t tail = static_cast<uint32_t>((bytes - head) % 16);
+  const uint64_t blocks = std::max<uint64_t>(1, std::min<uint64_t>((body + 255) / 256, 4096));
+  oxh::launch(zero_bytes_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0,
+              oxh::as_stream(stream), static_cast<uint8_t *>(ptr), head, body, tail);
+  return oxh::launched("oxh_memset0_async");
 }
 
 oxh_status oxh_memcpy_h2d_async(void *dst, const void *src, uint64_t bytes, oxh_stream stream) {

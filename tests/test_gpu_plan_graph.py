@@ -223,3 +223,36 @@ def test_fused_plan_runs_match_op_by_op(name, n_in, n_work, ops, out, elements):
             inputs = [x[::-1].copy() for x in inputs]
     finally:
         hp.close()
+
+
+@pytest.mark.parametrize("offset,nbytes", [(0, 4), (1, 1), (3, 17), (5, 4093), (16, 4096),
+                                           (7, (1 << 20) + 9), (0, 64 << 20)])
+def test_memset0_zeroes_exactly_the_range(dev, offset, nbytes):
+    """oxh_memset0_async (DeviceBuffer::zeroed, runtime.rs:83-105) at any byte alignment: the
+    range becomes zero and the bytes either side keep their values."""
+    buf = torch.full((offset + nbytes + 32,), 0xAB, dtype=torch.uint8, device=dev)
+    torch.cuda.synchronize()
+    ox.check(ox.lib().oxh_memset0_async(buf.data_ptr() + offset, nbytes, ox.current_stream()))
+    torch.cuda.synchronize()
+    h = host(buf)
+    assert (h[:offset] == 0xAB).all()
+    assert (h[offset:offset + nbytes] == 0).all()
+    assert (h[offset + nbytes:] == 0xAB).all()
+
+
+def test_memset0_replays_in_a_graph(dev):
+    """The zero fill recorded into a graph clears the buffer again on every replay, with eager
+    writes to it between the replays."""
+    s = torch.cuda.Stream()
+    buf = torch.ones(100003, device=dev)
+    torch.cuda.synchronize()
+    graph = ox.HipGraphExec.capture(
+        s, lambda: ox.check(ox.lib().oxh_memset0_async(buf.data_ptr() + 4, 4 * 100000,
+                                                       s.cuda_stream)))
+    for replay in range(4):
+        buf.fill_(float(replay + 2))
+        torch.cuda.synchronize()
+        graph.launch(s)
+        s.synchronize()
+        h = host(buf)
+        assert h[0] == replay + 2 and (h[1:100001] == 0).all() and (h[100001:] == replay + 2).all()
