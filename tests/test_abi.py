@@ -26,6 +26,13 @@ def test_library_exports_every_header_symbol():
     assert ox.lib().oxh_version().decode().startswith("oxide-hip")
 
 
+def test_integration_guide_names_every_header_function():
+    """The binding guide's function table stays in step with the header."""
+    guide = (ox.HEADER_PATH.parent.parent / "INTEGRATION.md").read_text()
+    missing = [s for s in ox.header_symbols() if f"`{s}`" not in guide and f"{s}(" not in guide]
+    assert not missing, missing
+
+
 def _status(call):
     return call
 
