@@ -748,6 +748,17 @@ struct SlabLoader {
         const bool ok = k_ok[j] && ((row_ok >> i) & 1u);
         v[u] = o.ptr[ok ? row_off[i] + koff[j] : 0];
       }
+    } else if (o.k.p.d == 1) {
+      // a linear k axis (offset k * outer, the common case): no division per load; the
+      // branch is uniform (kernel argument)
+      const uint32_t base = row_off[0] + (k0 + static_cast<uint32_t>(kk)) * o.k.outer;
+      const uint32_t step = static_cast<uint32_t>(kKStep) * o.k.outer;
+#pragma unroll
+      for (int u = 0; u < kLoads; ++u) {
+        const uint32_t k = static_cast<uint32_t>(kk + u * kKStep);
+        const bool ok = (row_ok & 1u) && k < kc;
+        v[u] = o.ptr[ok ? base + static_cast<uint32_t>(u) * step : 0];
+      }
     } else {
 #pragma unroll
       for (int u = 0; u < kLoads; ++u) {
