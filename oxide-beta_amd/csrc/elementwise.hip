@@ -267,8 +267,11 @@ __device__ __forceinline__ float4 chain_step4(const oxh::ChainStep &s, const flo
 // the running value with its other operand and storing its result where the plan needs it.
 // Every step's other operand is loaded before the first step runs (non-temporal; no step
 // writes a buffer a later step reads), so all of a tile's loads are in flight together.  The
-// steps are kernel arguments: the loops over them are unrolled to kChainMax with
-// block-uniform exits, keeping the operand registers statically indexed.
+// steps are kernel arguments: the loops over them are unrolled to MaxSteps with
+// block-uniform exits, keeping the operand registers statically indexed.  Chains of up to four
+// steps (config 1's plan has three) take the 4-step instance: half the operand registers, so
+// more waves stay in flight.
+template <int MaxSteps>
 __global__ __launch_bounds__(oxh::kBlock) void chain_vec4_kernel(oxh::Chain c, uint64_t n4,
                                                                  uint64_t n) {
   constexpr int U = kUnroll;  // float4 per thread per stream
@@ -285,9 +288,9 @@ __global__ __launch_bounds__(oxh::kBlock) void chain_vec4_kernel(oxh::Chain c, u
       if (!live[u]) idx[u] = base;  // a repeat of element base: loaded, never stored
       acc[u] = oxh::load_nt(reinterpret_cast<const float4 *>(c.first) + idx[u]);
     }
-    float4 operand[oxh::kChainMax][U];
+    float4 operand[MaxSteps][U];
 #pragma unroll
-    for (int k = 0; k < oxh::kChainMax; ++k) {
+    for (int k = 0; k < MaxSteps; ++k) {
       if (k >= static_cast<int>(c.count)) break;
       if (c.steps[k].other < 0) continue;
       const float4 *src = reinterpret_cast<const float4 *>(c.other[c.steps[k].other]);
@@ -295,7 +298,7 @@ __global__ __launch_bounds__(oxh::kBlock) void chain_vec4_kernel(oxh::Chain c, u
       for (int u = 0; u < U; ++u) operand[k][u] = oxh::load_nt(src + idx[u]);
     }
 #pragma unroll
-    for (int k = 0; k < oxh::kChainMax; ++k) {
+    for (int k = 0; k < MaxSteps; ++k) {
       if (k >= static_cast<int>(c.count)) break;
       const oxh::ChainStep s = c.steps[k];
 #pragma unroll
@@ -338,8 +341,12 @@ oxh_status launch_chain(hipStream_t stream, const Chain &c, uint64_t n) {
   uint64_t grid = (n4 + tile - 1) / tile;
   if (grid == 0) grid = 1;
   if (grid > kMaxGrid) grid = kMaxGrid;
-  launch(chain_vec4_kernel, dim3(static_cast<uint32_t>(grid)), dim3(kBlock), 0, stream, c, n4,
-         n);
+  if (c.count <= 4)
+    launch(chain_vec4_kernel<4>, dim3(static_cast<uint32_t>(grid)), dim3(kBlock), 0, stream, c,
+           n4, n);
+  else
+    launch(chain_vec4_kernel<kChainMax>, dim3(static_cast<uint32_t>(grid)), dim3(kBlock), 0,
+           stream, c, n4, n);
   return launched("elementwise chain");
 }
 
