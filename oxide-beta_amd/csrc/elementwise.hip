@@ -29,6 +29,12 @@ namespace {
 #define OXH_EW_NT_CHAIN 3
 #endif
 constexpr int kUnroll = OXH_EW_UNROLL;
+// The compiled-plan chain kernel streams fastest with one float4 per thread per stream
+// (config 1's plan: 42.3 us at 1, 44.9 at 2, 46.4 at 4), the map kernels with two.
+#ifndef OXH_EW_CHAIN_UNROLL
+#define OXH_EW_CHAIN_UNROLL 1
+#endif
+constexpr int kChainUnroll = OXH_EW_CHAIN_UNROLL;
 
 template <int NT>
 __device__ __forceinline__ float4 ld(const float4 *p) {
@@ -274,7 +280,7 @@ __device__ __forceinline__ float4 chain_step4(const oxh::ChainStep &s, const flo
 template <int MaxSteps>
 __global__ __launch_bounds__(oxh::kBlock) void chain_vec4_kernel(oxh::Chain c, uint64_t n4,
                                                                  uint64_t n) {
-  constexpr int U = kUnroll;  // float4 per thread per stream
+  constexpr int U = kChainUnroll;  // float4 per thread per stream
   const uint64_t tile = static_cast<uint64_t>(oxh::kBlock) * U;
   for (uint64_t base = static_cast<uint64_t>(blockIdx.x) * tile + threadIdx.x; base < n4;
        base += static_cast<uint64_t>(gridDim.x) * tile) {
@@ -337,7 +343,7 @@ oxh_status launch_chain(hipStream_t stream, const Chain &c, uint64_t n) {
               OXH_TRACE, "malformed elementwise chain");
   OXH_REQUIRE(aligned16(c.first), OXH_TRACE, "chain buffers must be 16-byte aligned");
   const uint64_t n4 = n / 4;
-  const uint64_t tile = static_cast<uint64_t>(kBlock) * kUnroll;
+  const uint64_t tile = static_cast<uint64_t>(kBlock) * kChainUnroll;
   uint64_t grid = (n4 + tile - 1) / tile;
   if (grid == 0) grid = 1;
   if (grid > kMaxGrid) grid = kMaxGrid;
