@@ -12,6 +12,8 @@ Tolerances (north star: max rel err 1e-5, abs 1e-6 near zero):
     fp32 terms (the GPU accumulates in fp64).
 """
 
+import json
+
 import numpy as np
 import pytest
 import torch
@@ -120,9 +122,74 @@ def test_batch_norm_config2_full_shape(module, dev):
     x, gamma, beta, g = _case(r, shape)
     rm, rv = np.zeros(128, np.float32), np.ones(128, np.float32)
     out = _run(module, dev, x, gamma, beta, g, rm, rv)
-    frac = _check(out, x, gamma, beta, g, rm, rv)
-    print("config 2 strict-criterion pass fractions:", frac)
-    assert frac["y"] > 0.999 and frac["dx"] > 0.999
+    _check(out, x, gamma, beta, g, rm, rv)  # every element within its bound (raises otherwise)
+    rep = _config2_report(out, x, gamma, beta, g, rm, rv)
+    print("config 2 parity:", json.dumps(rep, sort_keys=True))
+    # Measured on MI355X (deterministic: seeded inputs, fixed-order sums on both sides).  Counts
+    # of elements outside max(1e-5 |cpu|, 1e-6); each of them is inside the conditioning bound
+    # (worst ratio below 1).
+    for k, limit in CONFIG2_OUTSIDE_STRICT.items():
+        assert rep["outside_strict"][k] <= limit, (k, rep["outside_strict"][k])
+    for k in ("y", "dx", "dweight", "dbias"):
+        assert rep["worst_over_bound"][k] <= 1.0, k
+    # against fp64 truth of the same inputs the GPU is at least as accurate as the oracle
+    for k in ("mean", "inverse_std", "dweight", "dbias"):
+        assert rep["max_err_vs_fp64"]["gpu"][k] <= rep["max_err_vs_fp64"]["cpu"][k], k
+
+
+# Elements (of 25 690 112, or of 128 channels) outside the strict criterion at config 2, as
+# measured on MI355X: every y and dx value meets max(1e-5 |cpu|, 1e-6); 46 of 128 dweight and
+# 47 of 128 dbias channel sums do not, because the oracle's sequential fp32 sum of 200 704 terms
+# is itself off by up to 1.5e-2 (dweight) / 8.5e-3 (dbias) against fp64 truth, where the GPU's
+# fp64-accumulated sums are off by 1.1e-4 / 3.3e-5.
+CONFIG2_OUTSIDE_STRICT = {"mean": 0, "inverse_std": 0, "running_mean": 0, "running_variance": 0,
+                          "y": 0, "dx": 0, "dweight": 46, "dbias": 47}
+
+
+def _config2_report(out, x, gamma, beta, g, rm, rv, eps=1e-5):
+    """Per output: elements outside the strict criterion, the worst |gpu - cpu| over its
+    conditioning bound, and each side's max error against fp64 truth of the same inputs."""
+    y, mean, inv, rm1, rv1 = oracle.bn_forward(x, gamma, beta, rm, rv, True, 0.1, eps)
+    dx, dw, db = oracle.bn_backward(g, x, gamma, out["mean"], out["inv"], True)
+    c = x.shape[1]
+    m_ = x.size // c
+    cb = lambda v: np.asarray(v).reshape(1, c, 1, 1)  # noqa: E731
+    x64, g64 = x.astype(np.float64), g.astype(np.float64)
+    mean64 = x64.mean(axis=(0, 2, 3))
+    inv64 = 1.0 / np.sqrt(x64.var(axis=(0, 2, 3)) + eps)
+    xhat64 = (x64 - cb(mean64)) * cb(inv64)
+    dw64 = (g64 * xhat64).sum(axis=(0, 2, 3))
+    db64 = g64.sum(axis=(0, 2, 3))
+    dw_cpu, db_cpu = oracle.bn_backward(g, x, gamma, mean, inv, True)[1:]
+    y_terms = ((np.abs(x) + np.abs(cb(out["mean"]))) * cb(out["inv"]) * np.abs(cb(gamma))
+               + np.abs(cb(beta)))
+    xh = (x - cb(out["mean"])) * cb(out["inv"])
+    dx_terms = np.abs(cb(gamma * out["inv"] / np.float32(m_))) * (
+        m_ * np.abs(g) + np.abs(cb(db)) + np.abs(xh * cb(dw)))
+    sum_abs_g = np.abs(g64).sum(axis=(0, 2, 3))
+    sum_abs_gx = np.abs(g64 * xh.astype(np.float64)).sum(axis=(0, 2, 3))
+
+    def worst(got, ref, terms):
+        d = np.abs(np.asarray(got, np.float64) - np.asarray(ref, np.float64))
+        return float((d / np.maximum(1e-5 * np.asarray(terms, np.float64), 1e-6)).max())
+
+    pairs = dict(mean=(out["mean"], mean), inverse_std=(out["inv"], inv),
+                 running_mean=(out["rm"], rm1), running_variance=(out["rv"], rv1),
+                 y=(out["y"], y), dx=(out["dx"], dx), dweight=(out["dw"], dw),
+                 dbias=(out["db"], db))
+    err = lambda a, t: float(np.abs(np.asarray(a, np.float64) - t).max())  # noqa: E731
+    return {
+        "outside_strict": {k: int((~strict_ok(a, b)).sum()) for k, (a, b) in pairs.items()},
+        "worst_over_bound": {"y": worst(out["y"], y, y_terms),
+                             "dx": worst(out["dx"], dx, dx_terms),
+                             "dweight": worst(out["dw"], dw, sum_abs_gx),
+                             "dbias": worst(out["db"], db, sum_abs_g)},
+        "max_err_vs_fp64": {
+            "gpu": {"mean": err(out["mean"], mean64), "inverse_std": err(out["inv"], inv64),
+                    "dweight": err(out["dw"], dw64), "dbias": err(out["db"], db64)},
+            "cpu": {"mean": err(mean, mean64), "inverse_std": err(inv, inv64),
+                    "dweight": err(dw_cpu, dw64), "dbias": err(db_cpu, db64)}},
+    }
 
 
 def test_batch_norm_reference_kats(module, dev):

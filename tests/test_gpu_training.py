@@ -279,6 +279,31 @@ def test_config5_step_every_op_matches_oracle():
     np.testing.assert_array_equal(classes, oracle.argmax_rows(host(step.logits)))
 
 
+def test_device_parameters_equal_oracle_init():
+    """Every parameter oxh_mnv4_create uploads equals the oracle's nn.rs:657-674 init bit for
+    bit (conv weights; zero conv biases, BatchNorm gamma 1 / beta 0 as nn.rs:139-140 and
+    271-273), and every running statistic starts at mean 0 / variance 1."""
+    model = T.MobileNetV4ConvSmall.mnist()
+    params = model.parameters()
+    assert len(params) == 186
+    kinds = Counter()
+    for i, p in enumerate(params):
+        got = p.value.host()
+        if len(p.shape) == 4:
+            ref = oracle.initialized_weights(list(p.shape), p.shape[1]).reshape(p.shape)
+            kinds["weight"] += 1
+        else:
+            # visit order: conv weight, conv bias, then the BatchNorm's gamma and beta
+            is_gamma = len(params[i - 1].shape) == 1 and len(params[i - 2].shape) == 4
+            ref = np.full(p.shape, 1.0 if is_gamma else 0.0, np.float32)
+            kinds["gamma" if is_gamma else "zero"] += 1
+        assert_bitexact(got, ref, f"parameter {i} {p.shape}")
+    assert kinds == {"weight": 47, "gamma": 46, "zero": 93}
+    for bn in model.batch_norms():
+        assert_bitexact(bn.device_running_mean.host(), np.zeros(bn.channels, np.float32), "rm")
+        assert_bitexact(bn.device_running_variance.host(), np.ones(bn.channels, np.float32), "rv")
+
+
 def test_reference_full_training_step():
     """mobilenet_v4.rs:468-483: zero images [2, 1, 28, 28], targets [3, 7], one AdamW(1e-3,
     1e-4) step.  With zero input every activation is zero, the logits are zero and the loss is
