@@ -35,6 +35,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <mutex>
 #include <string>
 
 #include "bn_channel.h"
@@ -1170,7 +1171,46 @@ oxh_status backward_train_impl(const char *name, oxh_stream stream, uint64_t bat
   return oxh::launched(name);
 }
 
+// ---------------------------------------------------------------- allocation-free forward
+
+// The reduce partials of oxh_batch_norm_forward_train_no_alloc live in this array: one copy per
+// GPU (each device loads its own copy of the code object), held until the process ends.  Host
+// code never passes the array's name to a kernel (on the host it is only a stand-in symbol):
+// the device address of each GPU's copy is looked up once per device and used instead.
 }  // namespace
+
+static __device__ __align__(256) unsigned char scratch[OXH_BN_NO_ALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex scratch_mutex;
+void *scratch_address[kMaxScratchDevices] = {};
+
+// Resolves (once) the device address of `device`'s copy of `scratch`; `device` is current.
+oxh_status resolve_scratch(int device, void **address) {
+  OXH_REQUIRE(device >= 0 && device < kMaxScratchDevices, OXH_INVALID_SHAPE,
+              "device " + std::to_string(device) + " is beyond the scratch table");
+  std::lock_guard<std::mutex> lock(scratch_mutex);
+  if (scratch_address[device] == nullptr) {
+    void *p = nullptr;
+    OXH_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    OXH_REQUIRE(p != nullptr, OXH_HIP_ERROR, "hipGetSymbolAddress returned no address");
+    scratch_address[device] = p;
+  }
+  *address = scratch_address[device];
+  return oxh::ok();
+}
+
+}  // namespace
+
+namespace oxh {
+// Called by oxh_init with `device` current.
+oxh_status bn_scratch_init(int device) {
+  void *unused = nullptr;
+  return resolve_scratch(device, &unused);
+}
+}  // namespace oxh
 
 extern "C" {
 
@@ -1351,6 +1391,43 @@ oxh_status oxh_batch_norm_forward_train(oxh_stream stream, uint64_t batch, uint6
                             momentum, epsilon, input, weight, bias, running_mean,
                             running_variance, saved_mean, saved_inverse_std, output, workspace,
                             workspace_bytes, false);
+}
+
+// The training forward with its partials in the static per-GPU array: no allocation, no
+// workspace argument.  The partials need no initialisation (every reduce block writes its own
+// before the apply reads them), so nothing is cleared between calls.
+oxh_status oxh_batch_norm_forward_train_no_alloc(oxh_stream stream, uint64_t batch,
+                                                 uint64_t channels, uint64_t spatial,
+                                                 float momentum, float epsilon,
+                                                 const float *input, const float *weight,
+                                                 const float *bias, float *running_mean,
+                                                 float *running_variance, float *saved_mean,
+                                                 float *saved_inverse_std, float *output) {
+  const char *name = "oxh_batch_norm_forward_train_no_alloc";
+  oxh_status st = check_shape(name, batch, channels, spatial);
+  if (st != OXH_OK) return st;
+  const uint64_t need = workspace_bytes_for(make_geometry(batch, channels, spatial, false));
+  OXH_REQUIRE(need <= OXH_BN_NO_ALLOC_SCRATCH_BYTES, OXH_INVALID_SHAPE,
+              std::string(name) + ": " + std::to_string(channels) + " channels need " +
+                  std::to_string(need) + " bytes of partials, above the static " +
+                  std::to_string(OXH_BN_NO_ALLOC_SCRATCH_BYTES) + "-byte array");
+  int device = -1;
+  OXH_HIP_CHECK(hipGetDevice(&device));
+  if (stream != nullptr) {
+    int stream_device = -1;
+    OXH_HIP_CHECK(hipStreamGetDevice(oxh::as_stream(stream), &stream_device));
+    OXH_REQUIRE(stream_device == device, OXH_INVALID_SHAPE,
+                std::string(name) + ": the stream belongs to device " +
+                    std::to_string(stream_device) + " but device " + std::to_string(device) +
+                    " is current");
+  }
+  void *partials = nullptr;
+  st = resolve_scratch(device, &partials);
+  if (st != OXH_OK) return st;
+  return forward_train_impl(name, stream, batch, channels, spatial, momentum, epsilon, input,
+                            weight, bias, running_mean, running_variance, saved_mean,
+                            saved_inverse_std, output, partials, OXH_BN_NO_ALLOC_SCRATCH_BYTES,
+                            false);
 }
 
 oxh_status oxh_batch_norm_backward_train(oxh_stream stream, uint64_t batch, uint64_t channels,

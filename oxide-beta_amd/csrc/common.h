@@ -15,6 +15,10 @@
 
 namespace oxh {
 
+// Looks up this device's copy of the batch-norm static scratch array (the allocation-free
+// forward's partials); `device` must be current.  Called by oxh_init.
+oxh_status bn_scratch_init(int device);
+
 // Records `message` as the calling thread's last error and returns `status`.
 oxh_status fail(oxh_status status, const std::string &message);
 // Clears the last error; returns OXH_OK.

@@ -63,7 +63,7 @@ oxh_status oxh_init(int device) {
   std::string arch = prop.gcnArchName;
   OXH_REQUIRE(arch.rfind("gfx950", 0) == 0, OXH_EXECUTION,
               "liboxide_hip is built for gfx950, device reports " + arch);
-  return oxh::ok();
+  return oxh::bn_scratch_init(device);
 }
 
 oxh_status oxh_stream_create(oxh_stream *stream) {

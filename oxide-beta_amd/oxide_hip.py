@@ -129,6 +129,8 @@ _SIGNATURES = {
                                             _vp, _vp, _vp, _vp, _u64]),
     "oxh_batch_norm_forward_train": (_st, [_vp, _u64, _u64, _u64, _f32, _f32, _vp, _vp, _vp,
                                            _vp, _vp, _vp, _vp, _vp, _vp, _u64]),
+    "oxh_batch_norm_forward_train_no_alloc": (_st, [_vp, _u64, _u64, _u64, _f32, _f32, _vp,
+                                                    _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "oxh_batch_norm_backward_train": (_st, [_vp, _u64, _u64, _u64, _vp, _vp, _vp, _vp, _vp,
                                             _vp, _vp, _vp, _vp, _u64]),
     "oxh_batch_norm_relu_forward_train": (_st, [_vp, _u64, _u64, _u64, _f32, _f32, _vp, _vp,
