@@ -11,8 +11,10 @@ written by the input backward).  ``value`` = 8T / step time in GB/s, inputs resi
 
 MALL (256 MB last-level cache) is defeated for the headline: steps rotate over 4 independent
 input/output sets (1.6 GB), so each step's x and g were last touched three steps (1.2 GB of
-traffic) earlier.  The headline step time is a hipGraph replay (the four steps captured once,
-as a fixed plan is deployed).  Per-kernel durations for the roofline come from HIP events
+traffic) earlier.  The K timed steps are R = K / 4 back-to-back launches of a hipGraph of four
+steps (one rotation; a graph of one step when K is not a multiple of 4), with an event between
+consecutive launches: ``ms_per_step`` is the median launch / 4, p10 / p90 and the mean over
+all K steps are reported beside it.  Per-kernel durations for the roofline come from HIP events
 that each dispatch records at its own start and end (oxh_time_next_launch, i.e.
 hipExtLaunchKernelGGL) inside a second, eager timed region; the eager step time is reported
 beside the graph one.
@@ -46,6 +48,30 @@ def _events(n):
     import torch
 
     return [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+
+
+def _stats(samples):
+    """mean / median / p10 / p90 of a list of per-repetition times."""
+    q = sorted(samples)
+    pct = lambda f: q[min(len(q) - 1, int(f * len(q)))]  # noqa: E731
+    return {"mean": sum(q) / len(q), "median": pct(0.5), "p10": pct(0.1), "p90": pct(0.9),
+            "reps": len(q)}
+
+
+def _timed_reps(stream, fn, reps: int, warmup: int = 3):
+    """Runs ``fn`` ``reps`` times back to back on ``stream`` with an event between
+    consecutive repetitions (rep i = event i -> event i + 1, no gaps left out); returns the
+    per-repetition statistics in microseconds."""
+    for _ in range(warmup):
+        fn()
+    evs = _events(reps + 1)
+    evs[0].record(stream)
+    for i in range(reps):
+        fn()
+        evs[i + 1].record(stream)
+    evs[-1].synchronize()
+    st = _stats([evs[i].elapsed_time(evs[i + 1]) * 1e3 for i in range(reps)])
+    return {k: (round(v, 2) if k != "reps" else v) for k, v in st.items()}
 
 
 def _read_traffic(kernel: str):
@@ -140,17 +166,27 @@ def bench_batch_norm(m, steps: int, warmup: int, sets: int = 4):
     e_stop.record(s)
     s.synchronize()
     eager_ms = e_start.elapsed_time(e_stop) / steps
-    # headline: the K timed steps (rotating over the input sets) captured into one hipGraph,
-    # replayed once untimed, then once timed -- one graph launch, no per-launch gaps
-    graph = ox.HipGraphExec.capture(s, lambda: [step(k) for k in range(steps)])
-    graph.launch(s)
+    # headline: the K timed steps as R back-to-back launches of one hipGraph of G steps (one
+    # rotation over the input sets, G = 4, or G = 1 when K is not a multiple of 4), an event
+    # between consecutive launches; ms_per_step is the median launch over G
+    group = sets if steps % sets == 0 else 1
+    launches = steps // group
+    graph = ox.HipGraphExec.capture(s, lambda: [step(k) for k in range(group)])
+    for _ in range(max(1, -(-warmup // group))):
+        graph.launch(s)
     s.synchronize()
-    g_start, g_stop = _events(2)
-    g_start.record(s)
-    graph.launch(s)
-    g_stop.record(s)
+    evs = _events(launches + 1)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    evs[0].record(s)
+    for i in range(launches):
+        graph.launch(s)
+        evs[i + 1].record(s)
     s.synchronize()
-    ms_per_step = g_start.elapsed_time(g_stop) / steps
+    graph_wall = time.perf_counter() - t0
+    per_step = _stats([evs[i].elapsed_time(evs[i + 1]) / group for i in range(launches)])
+    ms_per_step = per_step["median"]
+    graph_mean_ms = evs[0].elapsed_time(evs[-1]) / steps
     # hot-cache reference: the same step repeated on one input set (x, g fit in the MALL)
     hot_start, hot_stop = _events(2)
     hot_start.record(s)
@@ -160,13 +196,16 @@ def bench_batch_norm(m, steps: int, warmup: int, sets: int = 4):
     s.synchronize()
     hot_ms = hot_start.elapsed_time(hot_stop) / steps
     host_inputs = None
-    return dict(ms_per_step=ms_per_step, eager_ms_per_step=eager_ms,
+    del graph
+    return dict(ms_per_step=ms_per_step, per_step=per_step, graph_mean_ms=graph_mean_ms,
+                graph_launches=launches, graph_group=group,
+                graph_wall_ms_per_step=graph_wall * 1e3 / steps, eager_ms_per_step=eager_ms,
                 event_ms_per_step=event_ms_per_step, wall_ms_per_step=wall * 1e3 / steps,
                 kernels=kernels, hot_ms_per_step=hot_ms, host_inputs=host_inputs, sets=sets,
                 graph_steps=steps)
 
 
-def bench_elementwise(m, reps: int = 20):
+def bench_elementwise(m, reps: int = 20, plan_reps: int = 100):
     import numpy as np
     import torch
 
@@ -185,19 +224,13 @@ def bench_elementwise(m, reps: int = 20):
     torch.cuda.synchronize()
 
     def timed(fn):
-        for i in range(3):
-            fn(i)
-        e0, e1 = _events(2)
-        e0.record(s)
-        for i in range(reps):
-            fn(i)
-        e1.record(s)
-        s.synchronize()
-        return e0.elapsed_time(e1) / reps * 1e3  # us
+        counter = iter(range(1 << 30))
+        return _timed_reps(s, lambda: fn(next(counter)), reps)
 
-    fwd = timed(lambda i: m.elementwise_chain_forward(*abc[i % sets], y[i % sets], stream=s))
-    bwd = timed(lambda i: m.elementwise_chain_backward(*abc[i % sets], None, *d[i % sets],
-                                                       stream=s))
+    fwd_st = timed(lambda i: m.elementwise_chain_forward(*abc[i % sets], y[i % sets], stream=s))
+    bwd_st = timed(lambda i: m.elementwise_chain_backward(*abc[i % sets], None, *d[i % sets],
+                                                          stream=s))
+    fwd, bwd = fwd_st["median"], bwd_st["median"]
     # the reference's JIT plan: add -> mul -> relu over three workspaces; compile fuses the
     # dependent run into one kernel (a, b, c read, y written) captured into a graph
     module = ox.compile(lambda a, b, c: ((a + b) * c).relu())
@@ -207,16 +240,11 @@ def bench_elementwise(m, reps: int = 20):
     plan = module.plan_for(((4096, 4096),) * 3)
     pstream = plan.stream()
     ext = torch.cuda.ExternalStream(pstream)
-    for _ in range(3):
-        plan.replay()
+    # µs per plan replay: back-to-back hipGraph launches (cuda_graph.rs:157-164), an event
+    # between consecutive replays; beside it the same kernel issued without the graph
+    replay = _timed_reps(ext, plan.replay, plan_reps)
+    direct = _timed_reps(ext, plan.launch, plan_reps)
     ox.check(ox.lib().oxh_stream_synchronize(pstream))
-    p0, p1 = _events(2)
-    p0.record(ext)
-    for _ in range(reps):
-        plan.replay()
-    p1.record(ext)
-    ox.check(ox.lib().oxh_stream_synchronize(pstream))
-    replay_us = p0.elapsed_time(p1) / reps * 1e3
     t0 = time.perf_counter()
     for _ in range(3):
         module.run(*host)
@@ -224,15 +252,20 @@ def bench_elementwise(m, reps: int = 20):
     plan.close()
     return {
         "config": "relu((a+b)*c) fp32 3x[4096,4096]",
-        "fused_fwd_us": round(fwd, 2), "fused_fwd_gbs": round(4 * n * 4 / fwd / 1e3, 1),
-        "fused_bwd_us": round(bwd, 2), "fused_bwd_gbs": round(6 * n * 4 / bwd / 1e3, 1),
-        "plan_replay_us": round(replay_us, 2),
-        "plan_replay_gbs": round(4 * n * 4 / replay_us / 1e3, 1),
+        "fused_fwd_us": fwd, "fused_fwd_gbs": round(4 * n * 4 / fwd / 1e3, 1),
+        "fused_fwd": fwd_st,
+        "fused_bwd_us": bwd, "fused_bwd_gbs": round(6 * n * 4 / bwd / 1e3, 1),
+        "fused_bwd": bwd_st,
+        "plan_replay_us": replay["median"],
+        "plan_replay": replay,
+        "plan_replay_gbs": round(4 * n * 4 / replay["median"] / 1e3, 1),
+        "plan_direct_launch_us": direct["median"],
+        "plan_direct_launch": direct,
         "plan_run_with_copies_us": round(run_us, 1),
     }
 
 
-def bench_cross_entropy(m, reps: int = 20):
+def bench_cross_entropy(m, reps: int = 50):
     import torch
 
     dev = torch.device("cuda:0")
@@ -247,27 +280,18 @@ def bench_cross_entropy(m, reps: int = 20):
     s = torch.cuda.Stream()
     torch.cuda.synchronize()
 
-    def timed(fn):
-        for _ in range(2):
-            fn()
-        e0, e1 = _events(2)
-        e0.record(s)
-        for _ in range(reps):
-            fn()
-        e1.record(s)
-        s.synchronize()
-        return e0.elapsed_time(e1) / reps * 1e3
-
-    fused = timed(lambda: m.cross_entropy_forward_backward(b, k, logits, targets, outer, loss,
-                                                           grad, stream=s))
-    fwd = timed(lambda: m.cross_entropy_forward(b, k, logits, targets, loss, stream=s))
+    fused_st = _timed_reps(s, lambda: m.cross_entropy_forward_backward(
+        b, k, logits, targets, outer, loss, grad, stream=s), reps, warmup=10)
+    fwd_st = _timed_reps(s, lambda: m.cross_entropy_forward(b, k, logits, targets, loss,
+                                                            stream=s), reps, warmup=10)
+    fused, fwd = fused_st["median"], fwd_st["median"]
     L = b * k * 4
-    return {"config": "CE fp32 [8192,32768]", "fused_fwd_bwd_us": round(fused, 1),
-            "fused_fwd_bwd_gbs": round(2 * L / fused / 1e3, 1), "fwd_us": round(fwd, 1),
-            "fwd_gbs": round(L / fwd / 1e3, 1)}
+    return {"config": "CE fp32 [8192,32768]", "fused_fwd_bwd_us": fused,
+            "fused_fwd_bwd_gbs": round(2 * L / fused / 1e3, 1), "fused_fwd_bwd": fused_st,
+            "fwd_us": fwd, "fwd_gbs": round(L / fwd / 1e3, 1), "fwd": fwd_st}
 
 
-def bench_adamw(m, reps: int = 30):
+def bench_adamw(m, reps: int = 50):
     import torch
 
     import oxide_hip as ox
@@ -288,16 +312,9 @@ def bench_adamw(m, reps: int = 30):
     def fn():
         m.adamw(1e-3, 0.01, 0.9, 0.999, c1, c2, 1e-8, p, g, mom, vel, p, mom, vel, stream=s)
 
-    for _ in range(2):
-        fn()
-    e0, e1 = _events(2)
-    e0.record(s)
-    for _ in range(reps):
-        fn()
-    e1.record(s)
-    s.synchronize()
-    us = e0.elapsed_time(e1) / reps * 1e3
-    return {"config": "AdamW fp32 64Mi elements t=10", "us": round(us, 1),
+    st = _timed_reps(s, fn, reps, warmup=10)
+    us = st["median"]
+    return {"config": "AdamW fp32 64Mi elements t=10", "us": us, "reps": st,
             "gbs": round(7 * n * 4 / us / 1e3, 1),
             "frac_of_peak": round(7 * n * 4 / us / 1e3 / PEAK_HBM_GBS, 3)}
 
@@ -347,14 +364,14 @@ def bench_mnist_step(steps: int = 20, batch: int = 128):
         k["gbs"] = round(k["alg_bytes"] / (k["us"] * 1e-6) / 1e9, 1) if k["alg_bytes"] else None
         k["us"] = round(k["us"], 1)
     step.capture()
-    for _ in range(3):
-        step.replay()
-    graph_ms = timed(step.replay, steps)
+    replay_st = _timed_reps(step.stream, step.replay, max(steps, 50))
+    graph_ms = replay_st["median"] / 1e3
     loss = step.loss_value()
     return {"config": f"MobileNetV4-Conv-S MNIST train step, batch {batch}, fp32",
-            "graph_ms_per_step": round(graph_ms, 4), "eager_ms_per_step": round(eager_ms, 3),
+            "graph_ms_per_step": round(graph_ms, 4), "graph_replay_us": replay_st,
+            "eager_ms_per_step": round(eager_ms, 3),
             "images_per_s": round(batch / (graph_ms * 1e-3), 1),
-            "launch_groups_per_step": len(step.ops), "steps_timed": steps,
+            "launch_groups_per_step": len(step.ops), "steps_timed": replay_st["reps"],
             "parameters": step.model.parameter_count(), "loss_after": round(loss, 5),
             "per_kind": kinds}
 
@@ -452,16 +469,18 @@ def cpu_other_configs():
                       "backward of sum()",
             "fwd_ms": round(fwd * 1e3, 1), "fwd_gbs": round(8 * n * 4 / fwd / 1e9, 2),
             "bwd_ms": round(bwd * 1e3, 1), "bwd_gbs": round(6 * n * 4 / bwd / 1e9, 2)}
-        rows, classes = 512, 32768
+        rows, classes = 8192, 32768
         r = np.random.default_rng(0x6F78696400000003)
-        logits = (r.standard_normal((rows, classes)) * 2).astype(np.float32)
+        logits = r.standard_normal((rows, classes), dtype=np.float32) * np.float32(2.0)
         targets = r.integers(0, classes, rows).astype(np.float32)
-        ce = _cpu_time(lambda: (oracle.ce_forward(logits, targets),
-                                oracle.ce_backward(logits, targets, 1.0)))
+        t0 = time.perf_counter()
+        oracle.ce_forward(logits, targets)
+        oracle.ce_backward(logits, targets, 1.0)
+        ce = time.perf_counter() - t0
+        del logits
         out["cross_entropy"] = {
-            "sample": f"{rows} of config 3's 8192 rows x 32768 classes: loss + gradient",
-            "ms": round(ce * 1e3, 1), "gbs": round(2 * rows * classes * 4 / ce / 1e9, 2),
-            "full_config_ms_est": round(ce * 8192 / rows * 1e3, 0)}
+            "sample": "config 3 in full (8192 rows x 32768 classes): loss + gradient, one run",
+            "ms": round(ce * 1e3, 1), "gbs": round(2 * rows * classes * 4 / ce / 1e9, 2)}
         n = 64 << 20
         r = np.random.default_rng(0x6F78696400000004)
         p = (r.standard_normal(n, dtype=np.float32) * 0.02)
@@ -528,7 +547,7 @@ def cpu_baseline(budget_s: float = 12.0):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-extra", action="store_true", help="headline BN config only")
     ap.add_argument("--extras", default=",".join(EXTRAS),
@@ -574,6 +593,17 @@ def main():
              "bn_eager_gbs": round(8 * T_BN / (bn["eager_ms_per_step"] * 1e-3) / 1e9, 1),
              "bn_events_ms_per_step": round(bn["event_ms_per_step"], 4),
              "bn_graph_steps_timed": bn["graph_steps"],
+             "bn_step_ms": {"median": round(bn["per_step"]["median"], 4),
+                            "p10": round(bn["per_step"]["p10"], 4),
+                            "p90": round(bn["per_step"]["p90"], 4),
+                            "mean": round(bn["graph_mean_ms"], 4),
+                            "graph_launches": bn["graph_launches"],
+                            "steps_per_graph": bn["graph_group"],
+                            "what": "per step: one event-timed launch of a hipGraph of "
+                                    "steps_per_graph steps, divided by that count; mean = all "
+                                    "K steps between the first and last event"},
+             "bn_gbs_p10_p90": [round(8 * T_BN / (bn["per_step"]["p90"] * 1e-3) / 1e9, 1),
+                                round(8 * T_BN / (bn["per_step"]["p10"] * 1e-3) / 1e9, 1)],
              "copy_ceiling": copy_ceiling()}
     chosen = [] if args.no_extra else [e for e in args.extras.split(",") if e]
     for name in chosen:
@@ -605,7 +635,13 @@ def main():
         "roofline": {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBS, 3),
-                     "traffic": _read_traffic(dominant)},
+                     "traffic": _read_traffic(dominant),
+                     "traffic_source": "profiles/traffic.json: rocprofv3 --pmc FETCH_SIZE, "
+                                       "WRITE_SIZE per dispatch of this kernel, scaled by a "
+                                       "1 GiB copy; L2-to-fabric bytes, Infinity Cache (MALL) "
+                                       "hits included, not measured in this run",
+                     "achieved_from": "algorithmic bytes / average dispatch duration (HIP "
+                                      "events recorded by each dispatch, eager pass)"},
         "cpu_baseline": None if args.no_cpu else cpu_baseline(),
         "extra": extra,
     }

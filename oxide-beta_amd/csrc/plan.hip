@@ -7,8 +7,8 @@
 //            recorded once into a graph and instantiated (47-55);
 //   run:     inputs copied host-to-device into their fixed buffers, one graph replay, the
 //            output copied back synchronously (70-99);
-//   replay:  the graph alone (a single-launch plan: that launch), for callers whose inputs are
-//            already resident.
+//   replay:  one launch of the graph alone, for callers whose inputs are already resident;
+//   launch:  the graph's launches issued directly on the plan's stream (no graph launch).
 // Plan operations are the reference's Add / Mul / Relu plus the backward elementwise kernels.
 // compile fuses each run of operations in which every operation consumes the previous one's
 // result (and reads no buffer an earlier operation of the run wrote) into one streaming kernel
@@ -22,10 +22,6 @@
 
 #include "chain.h"
 #include "common.h"
-
-#ifndef OXH_PLAN_GRAPH_REPLAY
-#define OXH_PLAN_GRAPH_REPLAY 0  // 1: replay single-launch plans through their graph too
-#endif
 
 namespace {
 
@@ -335,19 +331,22 @@ oxh_status oxh_plan_run(oxh_plan *plan, const float *const *host_inputs, uint32_
   return oxh_memcpy_d2h(host_output, out.device, out.elements * sizeof(float), plan->stream);
 }
 
-// A plan compiled to a single launch (e.g. a fully fused chain) is replayed by issuing that
-// launch directly -- the same kernel and arguments the graph holds, without the graph
-// launch's extra work per replay; longer plans replay their graph.
+// cuda/jit.rs:86-97 / cuda_graph.rs:157-164: one launch of the plan's hipGraph.
 oxh_status oxh_plan_replay(oxh_plan *plan) {
   OXH_REQUIRE(plan != nullptr && plan->compiled, OXH_TRACE, "plan is not compiled");
-#if !OXH_PLAN_GRAPH_REPLAY
-  if (plan->launches.size() == 1) {
-    const Run r{plan->launches[0].first, plan->launches[0].second};
-    return r.end - r.begin == 1 ? launch_operation(*plan, plan->operations[r.begin])
-                                : launch_run(*plan, r);
-  }
-#endif
   return oxh_graph_launch(plan->graph, plan->stream);
+}
+
+// The same launches the graph holds, issued directly on the plan's stream.
+oxh_status oxh_plan_launch(oxh_plan *plan) {
+  OXH_REQUIRE(plan != nullptr && plan->compiled, OXH_TRACE, "plan is not compiled");
+  for (const auto &l : plan->launches) {
+    const Run r{l.first, l.second};
+    oxh_status st = r.end - r.begin == 1 ? launch_operation(*plan, plan->operations[r.begin])
+                                         : launch_run(*plan, r);
+    if (st != OXH_OK) return st;
+  }
+  return oxh::ok();
 }
 
 oxh_status oxh_plan_stream(const oxh_plan *plan, oxh_stream *stream) {

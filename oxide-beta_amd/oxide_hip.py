@@ -206,6 +206,7 @@ _SIGNATURES = {
     "oxh_plan_compile": (_st, [_vp]),
     "oxh_plan_run": (_st, [_vp, ctypes.POINTER(_vp), _u32, _vp, _u64]),
     "oxh_plan_replay": (_st, [_vp]),
+    "oxh_plan_launch": (_st, [_vp]),
     "oxh_plan_stream": (_st, [_vp, ctypes.POINTER(_vp)]),
     "oxh_plan_buffer": (_st, [_vp, _u32, ctypes.POINTER(_vp), ctypes.POINTER(_u64)]),
     "oxh_plan_destroy": (_st, [_vp]),
@@ -895,7 +896,12 @@ class HipJitPlan:
         return out
 
     def replay(self) -> None:
+        """One launch of the plan's hipGraph."""
         check(lib().oxh_plan_replay(self._handle))
+
+    def launch(self) -> None:
+        """The graph's kernel launches issued directly (no graph launch)."""
+        check(lib().oxh_plan_launch(self._handle))
 
     def stream(self) -> int:
         s = _vp()

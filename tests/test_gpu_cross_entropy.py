@@ -119,3 +119,29 @@ def test_cross_entropy_exp_accuracy_within_rows(module, dev):
         ratio = grad[row][mask[row]].astype(np.float64) / e64[row][mask[row]]
         spread = (ratio.max() - ratio.min()) / ratio.mean()
         assert spread < 5e-7, (row, spread)
+
+
+@pytest.mark.parametrize("rows", [512, 513, 600, 1024 + 37])
+@pytest.mark.parametrize("mode", ["fused", "separate"])
+def test_cross_entropy_pipelined_rows(module, dev, rows, mode):
+    """Rows of 32 768 classes from 512 rows up take the two-rows-in-flight path (a block walks
+    rows b, b + 256, ...): every block count parity and ragged tail, with invalid targets in
+    the middle and at the end (NaN rows, NaN loss, flag) and the valid rows against the
+    oracle."""
+    k = 32768
+    r = np.random.default_rng(rows * 7 + (mode == "fused"))
+    logits = (r.standard_normal((rows, k), dtype=np.float32) * np.float32(2.0))
+    targets = r.integers(0, k, rows).astype(np.float32)
+    targets[[0, rows - 1]] = [k - 1, 0]  # target in the last and the first float4 of the row
+    loss, grad, flag = _run(module, dev, logits, targets, 1.25, mode)
+    assert flag == 0
+    _check(loss, grad, logits, targets, 1.25)
+    bad = targets.copy()
+    bad[[rows // 2, rows - 1]] = [np.nan, float(k)]
+    loss, grad, flag = _run(module, dev, logits, bad, 1.25, mode)
+    assert flag == 1 and np.isnan(loss)
+    assert np.isnan(grad[[rows // 2, rows - 1]]).all()
+    good = np.ones(rows, bool)
+    good[[rows // 2, rows - 1]] = False
+    ref = oracle.ce_backward(logits[good], targets[good], 1.25) * np.float32(good.sum() / rows)
+    assert_close(grad[good], ref, rtol=2e-5, atol=1e-6 * 1.25 / rows, what="valid rows")

@@ -52,6 +52,12 @@ def test_config1_plan_matches_oracle():
     got = np.empty(m, np.float32)
     ox.check(ox.lib().oxh_memcpy_d2h(got.ctypes.data, out_ptr, m * 4, stream))
     assert_bitexact(got, oracle.chain_forward(a2.ravel(), b.ravel(), c.ravel()), "replay")
+    # the same launches issued directly (no graph launch)
+    a3 = r.uniform(-1, 1, (4096, 4096)).astype(np.float32)
+    ox.check(ox.lib().oxh_memcpy_h2d_async(ptr, a3.ctypes.data, n * 4, stream))
+    plan.launch()
+    ox.check(ox.lib().oxh_memcpy_d2h(got.ctypes.data, out_ptr, m * 4, stream))
+    assert_bitexact(got, oracle.chain_forward(a3.ravel(), b.ravel(), c.ravel()), "launch")
     plan.close()
 
 
