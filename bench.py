@@ -209,6 +209,7 @@ def bench_elementwise(m, reps: int = 20, plan_reps: int = 100):
     import numpy as np
     import torch
 
+    import jit
     import oxide_hip as ox
 
     dev = torch.device("cuda:0")
@@ -233,10 +234,10 @@ def bench_elementwise(m, reps: int = 20, plan_reps: int = 100):
     fwd, bwd = fwd_st["median"], bwd_st["median"]
     # the reference's JIT plan: add -> mul -> relu over three workspaces; compile fuses the
     # dependent run into one kernel (a, b, c read, y written) captured into a graph
-    module = ox.compile(lambda a, b, c: ((a + b) * c).relu())
     rr = np.random.default_rng(0x6F78696400000001)
     host = [rr.uniform(-1, 1, (4096, 4096)).astype(np.float32) for _ in range(3)]
-    module.run(*host)
+    module = jit.trace(host, lambda i: ((i[0] + i[1]) * i[2]).relu())
+    module.run(host)
     plan = module.plan_for(((4096, 4096),) * 3)
     pstream = plan.stream()
     ext = torch.cuda.ExternalStream(pstream)
@@ -247,7 +248,7 @@ def bench_elementwise(m, reps: int = 20, plan_reps: int = 100):
     ox.check(ox.lib().oxh_stream_synchronize(pstream))
     t0 = time.perf_counter()
     for _ in range(3):
-        module.run(*host)
+        module.run(host)
     run_us = (time.perf_counter() - t0) / 3 * 1e6
     plan.close()
     return {

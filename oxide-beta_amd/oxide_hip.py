@@ -12,9 +12,9 @@ reference's own code:
   ``cross_entropy_forward``, ``cross_entropy_backward``, ``adamw`` -- plus the fused entry
   points.  Arguments are device tensors (torch is only the allocator and stream provider).
 * ``HipGraphExec``: ``CudaGraphExec::{capture, launch}`` (cuda_graph.rs:47-165).
-* ``GraphPlan`` / ``HipJitPlan``: the fixed-buffer plan of jit.rs:24-56 and ``CudaJitPlan``
-  (cuda/jit.rs:10-99); ``trace`` / ``compile`` / ``JitModule`` mirror jit.rs:89-176 for the
-  elementwise operations the reference plans support.
+
+The lazy graph, its device programs and autograd are in tensor.py, the modules in nn.py, the
+JIT (fused plans and their eager fallback) in jit.py.
 
 Errors raise ``OxideError`` whose ``kind`` names the reference's Error variant
 (crates/oxide-torch/src/error.rs): ``InvalidShape``, ``Execution``, ``Hip`` (for ``Cuda``),
@@ -26,9 +26,8 @@ from __future__ import annotations
 import ctypes
 import os
 import re
-from dataclasses import dataclass, field
 from pathlib import Path
-from typing import Callable, Sequence
+from typing import Callable
 
 _HERE = Path(__file__).resolve().parent
 LIB_PATH = _HERE / "liboxide_hip.so"
@@ -803,258 +802,3 @@ class HipGraphExec:
         if getattr(self, "_handle", None) and _lib is not None:
             _lib.oxh_graph_destroy(self._handle)
             self._handle = None
-
-
-# ----------------------------------------------------------------------------- plans
-
-@dataclass
-class Input:
-    elements: int
-
-
-@dataclass
-class Constant:
-    values: Sequence[float]
-
-
-@dataclass
-class WorkspaceBuffer:
-    elements: int
-
-
-@dataclass
-class Operation:
-    op: int
-    inputs: tuple[int, ...]
-    output: int
-
-
-@dataclass
-class GraphPlan:
-    """jit.rs:24-56: buffers, operations, input slots, output slot."""
-
-    buffers: list = field(default_factory=list)
-    operations: list[Operation] = field(default_factory=list)
-    inputs: list[int] = field(default_factory=list)
-    output: int = -1
-
-
-class HipJitPlan:
-    """``CudaJitPlan`` (cuda/jit.rs:10-99) on liboxide_hip's plan runtime."""
-
-    def __init__(self, plan: GraphPlan, device: int = 0):
-        import numpy as np
-
-        handle = _vp()
-        check(lib().oxh_plan_create(device, ctypes.byref(handle)))
-        self._handle = handle.value
-        self._slots: list[int] = []
-        self._input_slots: list[int] = []
-        try:
-            for buf in plan.buffers:
-                slot = _u32()
-                if isinstance(buf, Input):
-                    check(lib().oxh_plan_add_input(self._handle, buf.elements,
-                                                   ctypes.byref(slot)))
-                    self._input_slots.append(len(self._slots))
-                elif isinstance(buf, Constant):
-                    arr = np.ascontiguousarray(buf.values, dtype=np.float32)
-                    check(lib().oxh_plan_add_constant(self._handle, arr.ctypes.data, arr.size,
-                                                      ctypes.byref(slot)))
-                else:
-                    check(lib().oxh_plan_add_workspace(self._handle, buf.elements,
-                                                       ctypes.byref(slot)))
-                self._slots.append(slot.value)
-            if [self._input_slots[i] for i in range(len(self._input_slots))] != list(
-                    plan.inputs):
-                raise OxideError(TRACE, "plan inputs must be the Input buffers in order")
-            for op in plan.operations:
-                ins = (_u32 * len(op.inputs))(*[self._slots[i] for i in op.inputs])
-                check(lib().oxh_plan_add_operation(self._handle, op.op, ins, len(op.inputs),
-                                                   self._slots[op.output]))
-            check(lib().oxh_plan_set_output(self._handle, self._slots[plan.output]))
-            check(lib().oxh_plan_compile(self._handle))
-        except Exception:
-            lib().oxh_plan_destroy(self._handle)
-            self._handle = None
-            raise
-        elements = _u64()
-        ptr = _vp()
-        check(lib().oxh_plan_buffer(self._handle, self._slots[plan.output], ctypes.byref(ptr),
-                                    ctypes.byref(elements)))
-        self.output_elements = elements.value
-        self.plan = plan
-
-    def run(self, inputs: Sequence) -> "np.ndarray":  # noqa: F821
-        """H2D inputs, one replay, synchronous D2H of the output (cuda/jit.rs:70-99)."""
-        import numpy as np
-
-        arrays = [np.ascontiguousarray(x, dtype=np.float32) for x in inputs]
-        ptrs = (_vp * len(arrays))(*[a.ctypes.data for a in arrays])
-        out = np.empty(self.output_elements, dtype=np.float32)
-        check(lib().oxh_plan_run(self._handle, ptrs, len(arrays), out.ctypes.data, out.size))
-        return out
-
-    def replay(self) -> None:
-        """One launch of the plan's hipGraph."""
-        check(lib().oxh_plan_replay(self._handle))
-
-    def launch(self) -> None:
-        """The graph's kernel launches issued directly (no graph launch)."""
-        check(lib().oxh_plan_launch(self._handle))
-
-    def stream(self) -> int:
-        s = _vp()
-        check(lib().oxh_plan_stream(self._handle, ctypes.byref(s)))
-        return s.value or 0
-
-    def buffer(self, index: int) -> tuple[int, int]:
-        """(device address, elements) of the plan's buffer ``index``."""
-        ptr, n = _vp(), _u64()
-        check(lib().oxh_plan_buffer(self._handle, self._slots[index], ctypes.byref(ptr),
-                                    ctypes.byref(n)))
-        return ptr.value, n.value
-
-    def close(self) -> None:
-        if self._handle is not None:
-            check(lib().oxh_plan_destroy(self._handle))
-            self._handle = None
-
-    def __del__(self):
-        if getattr(self, "_handle", None) is not None and _lib is not None:
-            _lib.oxh_plan_destroy(self._handle)
-            self._handle = None
-
-
-# ----------------------------------------------------------------------------- trace / compile
-
-class Placeholder:
-    """A traced value: a placeholder input, a constant or an elementwise op of traced values.
-
-    Mirrors the lazy ``Tensor`` builders the reference plans lower (tensor/mod.rs:103-122:
-    equal shapes, no broadcasting)."""
-
-    _next_id = 0
-
-    def __init__(self, shape, kind, args=(), value=None):
-        self.shape = tuple(int(s) for s in shape)
-        self.kind = kind  # "input", "constant", "add", "mul", "relu"
-        self.args = args
-        self.value = value
-        Placeholder._next_id += 1
-        self.id = Placeholder._next_id
-
-    def numel(self) -> int:
-        n = 1
-        for s in self.shape:
-            n *= s
-        return n
-
-    def _binary(self, other, kind):
-        if not isinstance(other, Placeholder):
-            other = constant(other, self.shape)
-        if other.shape != self.shape:
-            raise OxideError(INVALID_SHAPE, f"shape mismatch {self.shape} vs {other.shape}")
-        return Placeholder(self.shape, kind, (self, other))
-
-    def add(self, other):
-        return self._binary(other, "add")
-
-    def mul(self, other):
-        return self._binary(other, "mul")
-
-    def relu(self):
-        return Placeholder(self.shape, "relu", (self,))
-
-    __add__ = add
-    __mul__ = mul
-
-
-def constant(values, shape=None) -> Placeholder:
-    import numpy as np
-
-    arr = np.ascontiguousarray(values, dtype=np.float32)
-    if shape is not None:
-        arr = np.broadcast_to(arr, shape).astype(np.float32)
-    return Placeholder(arr.shape, "constant", value=arr.ravel())
-
-
-def lower(output: Placeholder, inputs: Sequence[Placeholder]) -> GraphPlan:
-    """``PlanBuilder::lower`` (jit.rs:276-412): post-order, one buffer per node, memoised."""
-    plan = GraphPlan()
-    slots: dict[int, int] = {}
-    input_slot = {p.id: None for p in inputs}
-    opcode = {"add": PLAN_ADD, "mul": PLAN_MUL, "relu": PLAN_RELU}
-
-    # Inputs become the first buffers so their slots follow the argument order.
-    for p in inputs:
-        slots[p.id] = len(plan.buffers)
-        plan.buffers.append(Input(p.numel()))
-        input_slot[p.id] = slots[p.id]
-
-    def visit(node: Placeholder) -> int:
-        if node.id in slots:
-            return slots[node.id]
-        if node.kind == "input":
-            raise OxideError(TRACE, "traced graph reads a placeholder that is not an input")
-        if node.kind == "constant":
-            slots[node.id] = len(plan.buffers)
-            plan.buffers.append(Constant(node.value))
-            return slots[node.id]
-        args = tuple(visit(a) for a in node.args)
-        slot = len(plan.buffers)
-        plan.buffers.append(WorkspaceBuffer(node.numel()))
-        plan.operations.append(Operation(opcode[node.kind], args, slot))
-        slots[node.id] = slot
-        return slot
-
-    plan.output = visit(output)
-    used = set()
-    for op in plan.operations:
-        used.update(op.inputs)
-    used.add(plan.output)
-    for i, p in enumerate(inputs):
-        if slots[p.id] not in used:
-            raise OxideError(TRACE, f"traced input {i} is unused")  # jit.rs:259-266
-    plan.inputs = [slots[p.id] for p in inputs]
-    return plan
-
-
-class JitModule:
-    """``jit::trace`` / ``jit::compile`` result (jit.rs:14-176): one compiled plan per input
-    shape signature, created on first use and replayed afterwards."""
-
-    def __init__(self, fn: Callable, device: int = 0):
-        self.fn = fn
-        self.device = device
-        self._plans: dict[tuple, HipJitPlan] = {}
-
-    def cached_specializations(self) -> int:
-        return len(self._plans)
-
-    def plan_for(self, shapes: tuple) -> HipJitPlan:
-        if shapes not in self._plans:
-            holders = [Placeholder(s, "input") for s in shapes]
-            out = self.fn(*holders)
-            self._plans[shapes] = HipJitPlan(lower(out, holders), self.device)
-        return self._plans[shapes]
-
-    def run(self, *inputs):
-        import numpy as np
-
-        arrays = [np.ascontiguousarray(x, dtype=np.float32) for x in inputs]
-        shapes = tuple(a.shape for a in arrays)
-        plan = self.plan_for(shapes)
-        out_shape = self._out_shape(shapes)
-        return plan.run(arrays).reshape(out_shape)
-
-    def _out_shape(self, shapes):
-        holders = [Placeholder(s, "input") for s in shapes]
-        return self.fn(*holders).shape
-
-
-def compile(fn: Callable, device: int = 0) -> JitModule:  # noqa: A001 - mirrors jit::compile
-    return JitModule(fn, device)
-
-
-trace = compile

@@ -8,8 +8,10 @@ import ctypes
 import numpy as np
 import pytest
 
+import jit
 import oracle
 import oxide_hip as ox
+import tensor as tn
 
 
 def test_library_exports_every_header_symbol():
@@ -19,9 +21,10 @@ def test_library_exports_every_header_symbol():
     missing = [s for s in symbols if not hasattr(lib, s)]
     assert not missing, missing
     # every declared function also has a ctypes signature in the front ends
+    import tensor
     import training
 
-    bound = set(ox._SIGNATURES) | set(training.signatures())
+    bound = set(ox._SIGNATURES) | set(training.signatures()) | set(tensor.signatures())
     assert set(symbols) <= bound, set(symbols) - bound
     assert ox.lib().oxh_version().decode().startswith("oxide-hip")
 
@@ -137,8 +140,8 @@ def test_plan_builder_validation():
 
 def test_trace_lowering_matches_reference_plan_shape():
     """PlanBuilder::lower (jit.rs:276-412): relu((a + b) * c) -> 3 inputs, 3 workspaces."""
-    a, b, c = (ox.Placeholder((4096, 4096), "input") for _ in range(3))
-    plan = ox.lower(((a + b) * c).relu(), [a, b, c])
+    a, b, c = (tn.input((4096, 4096)) for _ in range(3))
+    plan = jit.lower(((a + b) * c).relu(), [a, b, c])
     kinds = [type(x).__name__ for x in plan.buffers]
     assert kinds == ["Input"] * 3 + ["WorkspaceBuffer"] * 3
     assert [o.op for o in plan.operations] == [ox.PLAN_ADD, ox.PLAN_MUL, ox.PLAN_RELU]
@@ -148,17 +151,114 @@ def test_trace_lowering_matches_reference_plan_shape():
 
 def test_trace_rejects_unused_input_and_shape_mismatch():
     """jit.rs:259-266 (unused traced input) and tensor/mod.rs:536-552 (equal shapes)."""
-    a, b = ox.Placeholder((2,), "input"), ox.Placeholder((2,), "input")
+    a, b = tn.input((2,)), tn.input((2,))
     with pytest.raises(ox.OxideError) as err:
-        ox.lower(a.relu(), [a, b])
+        jit.lower(a.relu(), [a, b])
     assert err.value.kind == "Trace"
     with pytest.raises(ox.OxideError) as err:
-        ox.Placeholder((2,), "input") + ox.Placeholder((3,), "input")
+        tn.input((2,)) + tn.input((3,))
     assert err.value.kind == "InvalidShape"
 
 
 def test_trace_constants_become_constant_buffers():
-    x = ox.Placeholder((2,), "input")
-    plan = ox.lower((x + ox.constant([1.0, 1.0])).relu(), [x])
+    x = tn.input((2,))
+    plan = jit.lower((x + tn.constant([1.0, 1.0])).relu(), [x])
     assert [type(b).__name__ for b in plan.buffers] == ["Input", "Constant", "WorkspaceBuffer",
                                                        "WorkspaceBuffer"]
+
+
+def test_reshape_lowers_as_an_alias():
+    """jit.rs:345: Reshape takes its input's buffer, no operation and no new buffer."""
+    x = tn.input((2, 3))
+    y = x.relu().reshape((3, 2)).reshape((6,)).relu()
+    plan = jit.lower(y, [x])
+    assert [type(b).__name__ for b in plan.buffers] == ["Input", "WorkspaceBuffer",
+                                                       "WorkspaceBuffer"]
+    assert [(o.op, o.inputs, o.output) for o in plan.operations] == [
+        (ox.PLAN_RELU, (0,), 1), (ox.PLAN_RELU, (1,), 2)]
+    with pytest.raises(ox.OxideError) as err:
+        x.reshape((4,))
+    assert err.value.kind == "InvalidShape"
+
+
+def test_graphs_plans_cannot_take_lower_to_no_plan():
+    """jit.rs:405-408 (supported = false -> CompiledPlan::Eager): BatchNorm, cross entropy,
+    conv and pooling are not plan operations, and an unused input is then no error."""
+    x, t = tn.input((2, 3, 1, 2)), tn.input((2,))
+    state = tn.BatchNormState.__new__(tn.BatchNormState)
+    state.channels = 3
+    w, b = tn.constant(np.ones(3)), tn.constant(np.zeros(3))
+    y = x.batch_norm2d(w, b, state, True, 0.1, 1e-5).relu()
+    assert jit.lower(y, [x]) is None
+    assert jit.lower(y.reshape((2, 6)).cross_entropy(t), [x, t]) is None
+    assert jit.lower(y.avg_pool2d((1, 2), (1, 2)), [x, tn.input((5,))]) is None
+
+
+def test_lazy_builders_follow_reference_shape_rules():
+    """tensor/mod.rs:158-389: conv2d, avg_pool2d, batch_norm2d and cross_entropy argument
+    errors with the reference's kinds."""
+    x = tn.input((2, 4, 5, 5))
+    w = tn.constant(np.zeros((8, 2, 3, 3)))
+    b = tn.constant(np.zeros(8))
+    assert x.conv2d(w, b, 2, 1, 2).shape == (2, 8, 3, 3)
+    for args in [(tn.constant(np.zeros((8, 2, 3, 2))), b, 1, 1, 2),   # non-square kernel
+                 (w, b, 1, 1, 3),                                      # groups
+                 (w, tn.constant(np.zeros(7)), 1, 1, 2),               # bias size
+                 (w, b, 0, 1, 2)]:                                     # stride 0
+        with pytest.raises(ox.OxideError) as err:
+            x.conv2d(*args)
+        assert err.value.kind == "InvalidShape"
+    with pytest.raises(ox.OxideError):
+        tn.input((1, 1, 2, 2)).conv2d(tn.constant(np.zeros((1, 1, 5, 5))), tn.constant([0.0]),
+                                      1, 1, 1)  # kernel exceeds the padded input
+    assert x.avg_pool2d((2, 3), (2, 1)).shape == (2, 4, 2, 3)
+    assert x.global_avg_pool2d().shape == (2, 4, 1, 1)
+    with pytest.raises(ox.OxideError):
+        x.avg_pool2d((6, 1), (1, 1))
+    state = tn.BatchNormState.__new__(tn.BatchNormState)
+    state.channels = 4
+    ones = tn.constant(np.ones(4))
+    for m, e in [(1.5, 1e-5), (float("nan"), 1e-5), (0.1, 0.0), (0.1, float("inf"))]:
+        with pytest.raises(ox.OxideError) as err:
+            x.batch_norm2d(ones, ones, state, True, m, e)
+        assert err.value.kind == "Execution"
+    with pytest.raises(ox.OxideError) as err:
+        tn.input((2, 3)).cross_entropy(tn.input((3,)))
+    assert err.value.kind == "InvalidShape"
+
+
+def test_net_builders_check_shapes_on_the_host():
+    """oxh_net_* validation (no device work): the same rules in the C ABI."""
+    import ctypes
+
+    import tensor
+
+    L = tensor._lib()
+    h = ctypes.c_void_p()
+    assert L.oxh_net_create(ctypes.byref(h)) == ox.OK
+    u32 = ctypes.c_uint32
+    node = lambda: u32()  # noqa: E731
+    shape = lambda *d: (ctypes.c_uint64 * len(d))(*d)  # noqa: E731
+    x, w, b, t, r = node(), node(), node(), node(), node()
+    assert L.oxh_net_input(h, 4, shape(2, 3, 4, 4), 0, ctypes.byref(x)) == ox.OK
+    assert L.oxh_net_parameter(h, 4, shape(5, 3, 3, 3), 4096, ctypes.byref(w)) == ox.OK
+    assert L.oxh_net_parameter(h, 1, shape(5), 8192, ctypes.byref(b)) == ox.OK
+    assert L.oxh_net_conv2d(h, x.value, w.value, b.value, 1, 1, 1, ctypes.byref(r)) == ox.OK
+    rank, dims = u32(), (ctypes.c_uint64 * 4)()
+    assert L.oxh_net_node_shape(h, r.value, ctypes.byref(rank), dims) == ox.OK
+    assert rank.value == 4 and list(dims) == [2, 5, 4, 4]
+    assert L.oxh_net_conv2d(h, x.value, w.value, b.value, 1, 1, 2, ctypes.byref(r)) == \
+        ox.INVALID_SHAPE
+    assert L.oxh_net_add(h, x.value, r.value, ctypes.byref(t)) == ox.INVALID_SHAPE
+    assert L.oxh_net_input(h, 0, shape(1), 0, ctypes.byref(t)) == ox.INVALID_SHAPE
+    assert b"scalar" in L.oxh_last_error()
+    assert L.oxh_net_batch_norm2d(h, r.value, b.value, b.value, 256, 512, 1, 0.1, 0.0,
+                                  ctypes.byref(t)) == ox.EXECUTION
+    assert L.oxh_net_reshape(h, r.value, 2, shape(10, 17), ctypes.byref(t)) == ox.INVALID_SHAPE
+    assert L.oxh_net_relu(h, 999, ctypes.byref(t)) == ox.INVALID_SHAPE
+    # a training program needs a one-element root (tensor/mod.rs:399-404), checked before
+    # anything is allocated
+    prog = ctypes.c_void_p()
+    assert L.oxh_net_training_program(h, r.value, None, ctypes.byref(prog)) == ox.EXECUTION
+    assert b"scalar" in L.oxh_last_error()
+    assert L.oxh_net_destroy(h) == ox.OK

@@ -1,0 +1,228 @@
+"""Traced graphs on the GPU through the generic builder (oxh_net_*): the JIT's eager path, the
+reference's autograd test on BatchNorm -> reshape -> cross entropy, a general graph with every
+op kind, and MobileNetV4-Conv-S assembled from the generic modules against the native trainer.
+Every launch of every program is recomputed by the oracle from the device tensors it read."""
+
+import numpy as np
+import pytest
+import torch
+
+import jit
+import nn
+import oracle
+import oxide_hip as ox
+import tensor as tn
+import training as T
+from helpers import assert_bitexact, assert_close, host
+from oracle_checker import OracleChecker
+
+pytestmark = pytest.mark.gpu
+
+
+def _run_checked(program):
+    checker = OracleChecker()
+    for op in program.ops:
+        checker.before(op)
+        op.launch()
+        checker.after(op)
+    program.check()
+    return checker.counts
+
+
+def test_traced_batch_norm_recomputes_batch_statistics_each_run():
+    """jit.rs:763-782 through trace: BatchNorm2d is no plan operation, so the traced graph runs
+    eagerly (CompiledPlan::Eager); each run normalizes with its own batch statistics (about
+    [-1, 1] for both [1, 3] and [10, 20]) and updates the running statistics as the oracle's
+    two training forwards do."""
+    layer = nn.BatchNorm2d(1)
+    example = np.array([1.0, 3.0], np.float32).reshape(1, 1, 1, 2)
+    module = jit.trace([example], lambda i: layer(i[0]))
+    first = module.run([example])
+    second = module.run([np.array([10.0, 20.0], np.float32).reshape(1, 1, 1, 2)])
+    for out in (first, second):
+        assert out.shape == (1, 1, 1, 2)
+        assert abs(out.ravel()[0] + 1) < 1e-4 and abs(out.ravel()[1] - 1) < 1e-4
+    assert module.cached_specializations() == 1
+    assert isinstance(module.plan_for(((1, 1, 1, 2),)), jit.EagerPlan)
+    rm, rv = np.zeros(1, np.float32), np.ones(1, np.float32)
+    one, zero = np.ones(1, np.float32), np.zeros(1, np.float32)
+    for x in (example, np.array([10.0, 20.0], np.float32).reshape(1, 1, 1, 2)):
+        y, _, _, rm, rv = oracle.bn_forward(x, one, zero, rm, rv)
+    assert_close(second.ravel(), y.ravel(), what="second run")
+    assert_close(host(layer.state.running_mean), rm, what="running mean")
+    assert_close(host(layer.state.running_variance), rv, what="running variance")
+
+
+def _bn_reshape_ce():
+    x = tn.input((3, 2, 1, 1), requires_grad=True)
+    w, b = nn.Parameter([1.2, 0.7]), nn.Parameter([0.1, -0.2])
+    t = tn.input((3,))
+    loss = (x.batch_norm2d(w.tensor(), b.tensor(), tn.BatchNormState(2), True, 0.1, 1e-5)
+            .reshape((3, 2)).cross_entropy(t))
+    return x, w, b, t, loss
+
+
+def test_batch_norm_reshape_cross_entropy_gradient_matches_finite_difference():
+    """tensor/mod.rs:627-686 through the generic builder: BN (train) -> reshape [3, 2] -> cross
+    entropy on data [1, 4, 2, 0, -1, 3], targets [0, 1, 0].  Every launch against the oracle;
+    the input gradient equals the oracle's chain (autograd.rs:315-383, 529-554) and the
+    central finite difference of device forward runs (step 1e-3, tolerance 2e-3); the weight
+    and bias gradients exist."""
+    data = np.array([1.0, 4.0, 2.0, 0.0, -1.0, 3.0], np.float32).reshape(3, 2, 1, 1)
+    targets = np.array([0.0, 1.0, 0.0], np.float32)
+    x, w, b, t, loss = _bn_reshape_ce()
+    prog = tn.training_program(loss)
+    prog.feed(x, data)
+    prog.feed(t, targets)
+    counts = _run_checked(prog)
+    assert counts == {"batch_norm2d_forward": 1, "cross_entropy": 1,
+                      "batch_norm2d_backward": 1}
+    analytic = prog.gradient(x).host()
+    assert prog.gradient(w.tensor()) is not None and prog.gradient(b.tensor()) is not None
+    # the oracle's whole chain on the same inputs
+    gamma, beta = np.float32([1.2, 0.7]), np.float32([0.1, -0.2])
+    y, mean, inv, _, _ = oracle.bn_forward(data, gamma, beta, np.zeros(2, np.float32),
+                                           np.ones(2, np.float32))
+    dl = oracle.ce_backward(y.reshape(3, 2), targets, 1.0)
+    dx, dw, db = oracle.bn_backward(dl.reshape(3, 2, 1, 1), data, gamma, mean, inv)
+    assert_close(analytic, dx, rtol=1e-5, atol=1e-6, what="input gradient")
+    assert_close(prog.gradient(w.tensor()).host(), dw, rtol=1e-5, atol=1e-6, what="dweight")
+    assert_close(prog.gradient(b.tensor()).host(), db, rtol=1e-5, atol=1e-6, what="dbias")
+    # finite differences of device forward runs (fresh running statistics each build)
+    fx, _, _, ft, floss = _bn_reshape_ce()
+    fwd = tn.forward_program(floss, [fx, ft])
+    fwd.feed(ft, targets)
+
+    def device_loss(values):
+        fwd.feed(fx, values)
+        fwd.run()
+        fwd.check()
+        return float(fwd.value(floss).host()[0])
+
+    step = 1e-3
+    for i in range(data.size):
+        pos, neg = data.copy().ravel(), data.copy().ravel()
+        pos[i] += step
+        neg[i] -= step
+        numerical = (device_loss(pos.reshape(data.shape)) -
+                     device_loss(neg.reshape(data.shape))) / (2 * step)
+        assert abs(analytic.ravel()[i] - numerical) < 2e-3, (i, analytic.ravel()[i], numerical)
+
+
+def test_general_graph_every_op_matches_oracle():
+    """A graph with every op kind the builder takes, some constants and an input requiring a
+    gradient: conv (parameter weight, constant bias), eval-mode BatchNorm, ReLU, mul by a
+    constant mask, a second consumer of a value (accumulated gradient), average pool, a
+    reshape whose input has two consumers (copied gradient), a cross entropy that is not the
+    root, the root scaled by a constant.  Every launch against the oracle, the input and
+    parameter gradients against torch float64 autograd of the same graph."""
+    r = np.random.default_rng(31)
+    n, c, h, w = 4, 3, 6, 6
+    xv = r.standard_normal((n, c, h, w)).astype(np.float32)
+    wv = (r.standard_normal((5, c, 3, 3)) * 0.3).astype(np.float32)
+    bv = r.standard_normal(5).astype(np.float32)
+    gam, bet = r.uniform(0.5, 1.5, 5).astype(np.float32), r.uniform(-0.2, 0.2, 5).astype(np.float32)
+    rm, rv = r.uniform(-0.3, 0.3, 5).astype(np.float32), r.uniform(0.5, 2.0, 5).astype(np.float32)
+    mask = (r.uniform(0, 1, (n, 5, h, w)) > 0.3).astype(np.float32) * 1.5
+    targets = r.integers(0, 45, n).astype(np.float32)
+
+    x = tn.input((n, c, h, w), requires_grad=True)
+    weight = nn.Parameter(wv)
+    gamma, beta = nn.Parameter(gam), nn.Parameter(bet)
+    state = tn.BatchNormState(5, torch.from_numpy(rm).cuda(), torch.from_numpy(rv).cuda())
+    conv = x.conv2d(weight.tensor(), tn.constant(bv), 1, 1, 1)
+    a = conv.batch_norm2d(gamma.tensor(), beta.tensor(), state, False, 0.1, 1e-5).relu()
+    m = a.mul(tn.constant(mask)).add(a)          # a has two consumers
+    pooled = m.avg_pool2d((2, 2), (2, 2))        # [4, 5, 3, 3]
+    flat = pooled.reshape((n, 45))
+    other = pooled.mul(pooled)                   # pooled's second consumer
+    t = tn.input((n,))
+    ce = flat.cross_entropy(t)
+    side = other.reshape((n * 45,)).reshape((n, 45)).cross_entropy(t)
+    loss = ce.add(side).mul(tn.constant([0.5]))
+    prog = tn.training_program(loss)
+    prog.feed(x, xv)
+    prog.feed(t, targets)
+    counts = _run_checked(prog)
+    for kind in ("conv2d_forward", "batch_norm2d_eval_forward", "relu_forward", "mul_forward",
+                 "add_forward", "avg_pool2d_forward", "cross_entropy_forward", "seed",
+                 "mul_backward", "add_backward", "reshape_backward", "cross_entropy_backward",
+                 "avg_pool2d_backward", "relu_backward", "batch_norm2d_eval_backward",
+                 "conv2d_parameter_backward", "conv2d_input_backward"):
+        assert counts[kind] >= 1, (kind, dict(counts))
+    # torch float64 autograd of the same graph
+    d = lambda v: torch.tensor(v, dtype=torch.float64, requires_grad=True)  # noqa: E731
+    tx, tw, tg, tb = d(xv), d(wv), d(gam), d(bet)
+    tconv = torch.nn.functional.conv2d(tx, tw, torch.tensor(bv, dtype=torch.float64), 1, 1)
+    ta = torch.nn.functional.batch_norm(tconv, torch.tensor(rm, dtype=torch.float64),
+                                        torch.tensor(rv, dtype=torch.float64), tg, tb, False,
+                                        0.1, 1e-5).relu()
+    tm = ta * torch.tensor(mask, dtype=torch.float64) + ta
+    tp = torch.nn.functional.avg_pool2d(tm, 2, 2)
+    tt = torch.tensor(targets, dtype=torch.long)
+    tl = 0.5 * (torch.nn.functional.cross_entropy(tp.reshape(n, 45), tt) +
+                torch.nn.functional.cross_entropy((tp * tp).reshape(n, 45), tt))
+    tl.backward()
+    assert abs(float(prog.value(loss).host()[0]) - tl.item()) <= 1e-5 * abs(tl.item())
+    for got, ref, what in ((prog.gradient(x), tx.grad, "dx"), (prog.gradient(weight.tensor()),
+                           tw.grad, "dweight"), (prog.gradient(gamma.tensor()), tg.grad, "dgamma"),
+                           (prog.gradient(beta.tensor()), tb.grad, "dbeta")):
+        ref = ref.numpy()
+        np.testing.assert_allclose(got.host(), ref, rtol=1e-4, atol=1e-6 * np.abs(ref).max(),
+                                   err_msg=what)
+    # running statistics untouched in eval mode; constants get no gradient buffer
+    np.testing.assert_array_equal(host(state.running_mean), rm)
+    assert prog.gradient(t) is None
+
+
+def _mnist_batch(r, n):
+    images = (r.integers(0, 256, (n, 1, 28, 28)) / 255.0).astype(np.float32)
+    labels = r.integers(0, 10, n).astype(np.float32)
+    return images, labels
+
+
+def test_mobilenet_through_generic_builder_matches_native_trainer():
+    """MobileNetV4-Conv-S assembled from the generic modules (nn.py) and compiled by
+    oxh_net_training_program schedules exactly the native trainer's launch list (same kinds,
+    names, tensor roles and shapes), and two eager steps plus one graph replay leave loss,
+    all 186 parameters and all running statistics bit-identical."""
+    batch = 128
+    native = T.TrainingStep(T.MobileNetV4ConvSmall.mnist(), batch)
+    model = nn.MobileNetV4ConvSmall.mnist()
+    x, t = tn.input((batch, 1, 28, 28)), tn.input((batch,))
+    loss = model(x).cross_entropy(t)
+    prog = tn.training_program(loss, nn.AdamW(1e-3, 1e-4))
+    assert [(o.kind, o.name) for o in prog.ops] == [(o.kind, o.name) for o in native.ops]
+    for a, b in zip(prog.ops, native.ops):
+        assert ({k: [v.shape for v in vs] for k, vs in a.by_role.items()} ==
+                {k: [v.shape for v in vs] for k, vs in b.by_role.items()}), a.name
+        assert a.attrs.keys() == b.attrs.keys(), a.name
+    images, labels = _mnist_batch(np.random.default_rng(41), batch)
+    native.set_batch(images, labels)
+    prog.feed(x, images)
+    prog.feed(t, labels)
+    native_params = [p.value for p in native.model.parameters()]
+    params = model.parameters()
+    assert len(params) == len(native_params) == 186
+
+    def compare(when):
+        torch.cuda.synchronize()
+        assert_bitexact(prog.value(loss).host(), np.float32([native.loss_value()]), when)
+        for i, (p, q) in enumerate(zip(params, native_params)):
+            assert_bitexact(p.host(), q.host(), f"{when}: parameter {i}")
+        for i, (bn, nbn) in enumerate(zip(model.batch_norms(), native.model.batch_norms())):
+            assert_bitexact(host(bn.state.running_mean), nbn.device_running_mean.host(),
+                            f"{when}: running mean {i}")
+            assert_bitexact(host(bn.state.running_variance),
+                            nbn.device_running_variance.host(), f"{when}: running var {i}")
+
+    for step in range(2):
+        native.run_eager()
+        prog.run()
+        compare(f"eager step {step}")
+    native.capture()
+    prog.capture()
+    native.replay()
+    prog.replay()
+    compare("graph replay")
+    assert prog.steps() == native.steps_taken() == 3

@@ -7,39 +7,60 @@ import numpy as np
 import pytest
 import torch
 
+import jit
 import oracle
 import oxide_hip as ox
+import tensor as tn
 from helpers import assert_bitexact, host, to_dev
 
 pytestmark = pytest.mark.gpu
 
 
 def test_trace_caches_and_reuses_a_graph():
-    """jit.rs:721-736: relu(x + bias) with bias [1, 1] on [-2, 3] -> [0, 4]; one plan."""
-    module = ox.trace(lambda x: (x + ox.constant([1.0, 1.0])).relu())
-    assert module.run(np.array([-2.0, 3.0], np.float32)).tolist() == [0.0, 4.0]
+    """jit.rs:721-736: trace(x + bias).relu() with x = [-2, 3], bias = ones -> [0, 4]; the plan
+    is compiled on the first run and reused."""
+    x, bias = np.array([-2.0, 3.0], np.float32), np.ones(2, np.float32)
+    module = jit.trace([x, bias], lambda inputs: inputs[0].add(inputs[1]).relu())
+    assert module.cached_specializations() == 0
+    assert module.run([x, bias]).tolist() == [0.0, 4.0]
     assert module.cached_specializations() == 1
-    assert module.run(np.array([5.0, -7.0], np.float32)).tolist() == [6.0, 0.0]
+    assert module.run([np.array([5.0, -7.0], np.float32), bias]).tolist() == [6.0, 0.0]
+    assert module.cached_specializations() == 1
+    assert isinstance(module.plan_for(((2,), (2,))), jit.HipJitPlan)
+
+
+def test_run_validates_inputs_like_reference():
+    """jit.rs:183-203: input count and shape must match the trace (Error::Trace)."""
+    a = np.array([1, -1], np.float32)
+    module = jit.trace([a, a], lambda i: (i[0] * i[1]).relu())
+    assert module.run([a, np.array([2, 2], np.float32)]).tolist() == [2.0, 0.0]
+    assert module.run([np.array([1, 3], np.float32), np.array([2, 2], np.float32)]).tolist() \
+        == [2.0, 6.0]
+    for bad in ([a], [a, a, a], [a, np.ones(3, np.float32)]):
+        with pytest.raises(ox.OxideError) as err:
+            module.run(bad)
+        assert err.value.kind == "Trace"
     assert module.cached_specializations() == 1
 
 
-def test_compile_specializes_per_shape():
-    module = ox.compile(lambda a, b: (a * b).relu())
-    assert module.run(np.array([1, -1], np.float32), np.array([2, 2], np.float32)).tolist() \
-        == [2.0, 0.0]
-    assert module.run(np.ones((2, 3), np.float32), np.ones((2, 3), np.float32)).shape == (2, 3)
-    assert module.cached_specializations() == 2
-    with pytest.raises(ox.OxideError) as err:
-        module.plan_for(((2,), (2,))).run([np.ones(2, np.float32)])  # one input missing
-    assert err.value.kind == "Trace"
+def test_reshape_in_a_plan_is_an_alias():
+    """jit.rs:345: reshape between plan ops costs no buffer and no launch; the output has the
+    traced shape."""
+    x = np.arange(-3, 3, dtype=np.float32).reshape(2, 3)
+    module = jit.trace([x], lambda i: i[0].relu().reshape((3, 2)).mul(
+        tn.constant(np.full((3, 2), 2.0))))
+    y = module.run([x])
+    assert y.shape == (3, 2)
+    np.testing.assert_array_equal(y, np.maximum(x, 0).reshape(3, 2) * 2)
+    assert isinstance(module.plan_for(((2, 3),)), jit.HipJitPlan)
 
 
 def test_config1_plan_matches_oracle():
     """Config 1 via compile: relu((a+b)*c), three [4096, 4096] inputs, values U(-1, 1)."""
     r = np.random.default_rng(0x6F78696400000001)
     a, b, c = (r.uniform(-1, 1, (4096, 4096)).astype(np.float32) for _ in range(3))
-    module = ox.compile(lambda a, b, c: ((a + b) * c).relu())
-    y = module.run(a, b, c)
+    module = jit.trace([a, b, c], lambda i: ((i[0] + i[1]) * i[2]).relu())
+    y = module.run([a, b, c])
     assert_bitexact(y.ravel(), oracle.chain_forward(a.ravel(), b.ravel(), c.ravel()), "plan")
     # replay with device-resident inputs: write new inputs into the plan's buffers, replay
     plan = module.plan_for(((4096, 4096),) * 3)
@@ -159,10 +180,10 @@ def _host_plan(plan, inputs, state=None):
     the next (``state``); returns (output, state)."""
     bufs, k = [], 0
     for i, b in enumerate(plan.buffers):
-        if isinstance(b, ox.Input):
+        if isinstance(b, jit.Input):
             bufs.append(np.asarray(inputs[k], np.float32).ravel())
             k += 1
-        elif isinstance(b, ox.Constant):
+        elif isinstance(b, jit.Constant):
             bufs.append(np.asarray(b.values, np.float32))
         else:
             bufs.append(state[i] if state is not None else np.zeros(b.elements, np.float32))
@@ -176,11 +197,11 @@ def _host_plan(plan, inputs, state=None):
 
 
 def _plan(n_inputs, n_work, ops, output, elements, constant=None):
-    buffers = [ox.Input(elements) for _ in range(n_inputs)]
+    buffers = [jit.Input(elements) for _ in range(n_inputs)]
     if constant is not None:
-        buffers.append(ox.Constant(constant))
-    buffers += [ox.WorkspaceBuffer(elements) for _ in range(n_work)]
-    return ox.GraphPlan(buffers=buffers, operations=[ox.Operation(*o) for o in ops],
+        buffers.append(jit.Constant(constant))
+    buffers += [jit.WorkspaceBuffer(elements) for _ in range(n_work)]
+    return jit.GraphPlan(buffers=buffers, operations=[jit.Operation(*o) for o in ops],
                         inputs=list(range(n_inputs)), output=output)
 
 
@@ -219,7 +240,7 @@ def test_fused_plan_runs_match_op_by_op(name, n_in, n_work, ops, out, elements):
     r = np.random.default_rng(hash(name) & 0xFFFF)
     inputs = [r.uniform(-1, 1, elements).astype(np.float32) for _ in range(n_in)]
     inputs[0][:3] = [0.0, -0.0, np.nan]
-    hp = ox.HipJitPlan(plan)
+    hp = jit.HipJitPlan(plan)
     state = None
     try:
         for _ in range(3):  # later replays start from the earlier ones' workspaces
