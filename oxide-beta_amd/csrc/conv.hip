@@ -220,9 +220,13 @@ constexpr int kLdsR = 4;
 __device__ __forceinline__ uint32_t round4(uint32_t v) { return (v + 3) & ~3u; }
 
 // Block-wide global -> LDS staging with kStageUnroll loads in flight per thread (a load, a
-// wait and a store per element would put one memory latency per element on the block).
-// Element i < count is src[src_index(i)], stored at dst[dst_index(i)].
-constexpr int kStageUnroll = 8;
+// wait and a store per element would put one memory latency per element on the block; each
+// pass of the loop costs one).  Element i < count is src[src_index(i)], stored at
+// dst[dst_index(i)].
+#ifndef OXH_STAGE_UNROLL
+#define OXH_STAGE_UNROLL 16
+#endif
+constexpr int kStageUnroll = OXH_STAGE_UNROLL;
 
 template <class SrcMap, class DstMap>
 __device__ __forceinline__ void stage(float *dst, const float *src, uint32_t count,
@@ -243,8 +247,30 @@ __device__ __forceinline__ void stage(float *dst, const float *src, uint32_t cou
   }
 }
 __device__ __forceinline__ uint32_t same_index(uint32_t i) { return i; }
+// A contiguous run: 128-bit loads and stores when both ends are 16-byte aligned and the count
+// is a multiple of 4 (a block-uniform test), kStageUnroll float4 in flight per thread.
 __device__ __forceinline__ void stage_plain(float *dst, const float *src, uint32_t count) {
-  stage(dst, src, count, same_index, same_index);
+  if (((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15u) != 0 ||
+      (count & 3u) != 0) {
+    stage(dst, src, count, same_index, same_index);
+    return;
+  }
+  const uint32_t nt = blockDim.x, n4 = count / 4;
+  const float4 *s4 = reinterpret_cast<const float4 *>(src);
+  float4 *d4 = reinterpret_cast<float4 *>(dst);
+  for (uint32_t b = threadIdx.x; b < n4; b += nt * kStageUnroll) {
+    float4 v[kStageUnroll];
+#pragma unroll
+    for (int u = 0; u < kStageUnroll; ++u) {
+      const uint32_t i = b + u * nt;
+      v[u] = s4[i < n4 ? i : n4 - 1];
+    }
+#pragma unroll
+    for (int u = 0; u < kStageUnroll; ++u) {
+      const uint32_t i = b + u * nt;
+      if (i < n4) d4[i] = v[u];
+    }
+  }
 }
 __device__ __forceinline__ void zero_fill(float *dst, uint32_t count, uint32_t stride,
                                           uint32_t first, uint32_t width) {
@@ -783,23 +809,32 @@ struct SlabLoader {
   }
 };
 
+// LDS rows of a tiling: kSlab k plus one group of read-ahead, padded by 4 floats (rows start
+// in different banks; 16-byte alignment kept).
+template <int Tile, int Threads>
+struct ProductRow {
+  using S = TileShape<Tile, Threads>;
+  static constexpr int kG4 = S::kMicro == 1 ? 4 : 2;  // float4 per row per group (16 or 8 k)
+  static constexpr int kGroupK = 4 * kG4;
+  static constexpr int value = S::kSlab + kGroupK + 4;
+};
+
 // C[m, n] = init[m] + sum_{k in chunk, ascending} A[m, k] * B[n, k]: one serial fp32 sum per
 // output (each product rounded, then added: -ffp-contract=off).  Within a slab, groups of kG4
 // float4 (4 k each) per row are read from LDS as 128-bit accesses, the next group's reads
-// issued before the current group's arithmetic.
+// issued before the current group's arithmetic.  One block's tile (bx, by) of chunk bz, with
+// the block's LDS operand tiles as and bs.
 template <int Tile, int Threads, bool AKFast, bool BKFast>
-__global__ __launch_bounds__(Threads) void pointwise_product_kernel(ProductArgs g) {
+__device__ __forceinline__ void product_tile(const ProductArgs &g, uint32_t bx, uint32_t by,
+                                             uint32_t bz,
+                                             float (*as)[ProductRow<Tile, Threads>::value],
+                                             float (*bs)[ProductRow<Tile, Threads>::value]) {
   using S = TileShape<Tile, Threads>;
   constexpr int kMicro = S::kMicro, kLoads = S::kLoads, kSlab = S::kSlab, kCols = S::kCols;
-  constexpr int kG4 = kMicro == 1 ? 4 : 2;  // float4 per row per group (16 or 8 k)
-  constexpr int kGroupK = 4 * kG4;
-  // rows of kSlab k plus one group of read-ahead, padded by 4 floats (rows start in different
-  // banks; 16-byte alignment kept)
-  constexpr int kRow = kSlab + kGroupK + 4;
-  __shared__ __align__(16) float as[Tile][kRow];
-  __shared__ __align__(16) float bs[Tile][kRow];
-  const uint32_t m0 = blockIdx.y * Tile, n0 = blockIdx.x * Tile;
-  const uint32_t kb = blockIdx.z * g.k_chunk;
+  constexpr int kG4 = ProductRow<Tile, Threads>::kG4;
+  constexpr int kGroupK = ProductRow<Tile, Threads>::kGroupK;
+  const uint32_t m0 = by * Tile, n0 = bx * Tile;
+  const uint32_t kb = bz * g.k_chunk;
   const uint32_t ke = min(kb + g.k_chunk, g.K);
   const int tx = threadIdx.x % kCols, ty = threadIdx.x / kCols;
   float acc[kMicro][kMicro];
@@ -902,7 +937,7 @@ __global__ __launch_bounds__(Threads) void pointwise_product_kernel(ProductArgs 
     }
     __syncthreads();
   }
-  float *c = g.c + static_cast<uint64_t>(blockIdx.z) * g.c_chunk;
+  float *c = g.c + static_cast<uint64_t>(bz) * g.c_chunk;
 #pragma unroll
   for (int i = 0; i < kMicro; ++i) {
     const uint32_t m = m0 + ty * kMicro + i;
@@ -914,6 +949,38 @@ __global__ __launch_bounds__(Threads) void pointwise_product_kernel(ProductArgs 
       const uint32_t idx = axis_offset(g.cm, m) + axis_offset(g.cn, n);
       c[idx] = g.addend != nullptr ? acc[i][j] + added[i][j] : acc[i][j];
     }
+  }
+}
+
+template <int Tile, int Threads, bool AKFast, bool BKFast>
+__global__ __launch_bounds__(Threads) void pointwise_product_kernel(ProductArgs g) {
+  constexpr int kRow = ProductRow<Tile, Threads>::value;
+  __shared__ __align__(16) float as[Tile][kRow];
+  __shared__ __align__(16) float bs[Tile][kRow];
+  product_tile<Tile, Threads, AKFast, BKFast>(g, blockIdx.x, blockIdx.y, blockIdx.z, as, bs);
+}
+
+// Two independent products in one launch (a convolution's weight gradient and input
+// gradient): blocks [0, blocks1) take product 1's tiles, the rest product 2's, each tile
+// computed exactly as pointwise_product_kernel computes it.
+struct DualGrid {
+  uint32_t nx1, ny1, blocks1, nx2, ny2;
+};
+
+template <int Tile, int Threads, bool A1, bool B1, bool A2, bool B2>
+__global__ __launch_bounds__(Threads) void pointwise_dual_kernel(ProductArgs g1, ProductArgs g2,
+                                                                 DualGrid d) {
+  constexpr int kRow = ProductRow<Tile, Threads>::value;
+  __shared__ __align__(16) float as[Tile][kRow];
+  __shared__ __align__(16) float bs[Tile][kRow];
+  uint32_t b = blockIdx.x;
+  if (b < d.blocks1) {
+    const uint32_t plane = d.nx1 * d.ny1, z = b / plane, r = b - z * plane;
+    product_tile<Tile, Threads, A1, B1>(g1, r % d.nx1, r / d.nx1, z, as, bs);
+  } else {
+    b -= d.blocks1;
+    const uint32_t plane = d.nx2 * d.ny2, z = b / plane, r = b - z * plane;
+    product_tile<Tile, Threads, A2, B2>(g2, r % d.nx2, r / d.nx2, z, as, bs);
   }
 }
 
@@ -1255,6 +1322,77 @@ oxh_status make_pool_geom(const char *name, const oxh_pool2d_shape *s, PoolGeom 
   return oxh::ok();
 }
 
+// dW[oc, ic] = sum_{(n, p)} G[oc, (n, p)] X[ic, (n, p)], k = (n, p) in split.per-sized chunks;
+// c is the weight gradient (one chunk) or the chunk partials.
+ProductArgs weight_product(const ConvGeom &g, const KSplit &split, const float *gradient,
+                           const float *input, float *c) {
+  const uint32_t plane = g.h * g.w;
+  ProductArgs a{};
+  a.a = operand(gradient, linear(plane), batch_plane(plane, g.out_c));
+  a.b = operand(input, linear(plane), batch_plane(plane, g.in_c));
+  a.c = c;
+  a.cm = linear(g.in_c);
+  a.cn = linear(1);
+  a.c_chunk = g.out_c * g.in_c;
+  a.init = nullptr;
+  a.M = g.out_c;
+  a.N = g.in_c;
+  a.K = g.batch * plane;
+  a.k_chunk = split.per;
+  return a;
+}
+
+// dX[ic, (n, p)] = 0 + sum_oc W[oc, ic] G[(n, p), oc], plus the addend when given.
+ProductArgs input_product(const ConvGeom &g, const float *gradient, const float *weight,
+                          const float *addend, float *input_gradient) {
+  const uint32_t plane = g.h * g.w;
+  ProductArgs a{};
+  a.a = operand(weight, linear(1), linear(g.in_c));
+  a.b = operand(gradient, batch_plane(plane, g.out_c), linear(plane));
+  a.c = input_gradient;
+  a.cm = linear(plane);
+  a.cn = batch_plane(plane, g.in_c);
+  a.init = nullptr;
+  a.addend = addend;
+  a.M = g.in_c;
+  a.N = g.batch * plane;
+  a.K = g.out_c;
+  a.k_chunk = a.K;
+  return a;
+}
+
+uint64_t big_tiles(const ProductArgs &a, uint32_t chunks) {
+  return static_cast<uint64_t>((a.N + kTile - 1) / kTile) * ((a.M + kTile - 1) / kTile) * chunks;
+}
+
+// Both backward products of a pointwise convolution in one launch when together they stay
+// below the small-grid threshold (each alone would run the small-grid tiling) and their operand
+// layouts are the ones a convolution's planes give (plane > 1: weight gradient k-fast on both
+// operands, input gradient row-fast on both; plane 1: weight gradient row-fast, input gradient
+// k-fast on its second operand).  Every output is the same serial sum as in the separate
+// launches.  Returns false, launching nothing, otherwise.
+bool launch_dual(hipStream_t s, const ProductArgs &w, uint32_t w_chunks, const ProductArgs &x) {
+  constexpr int Tile = 8, Threads = 64;
+  if (OXH_TINY_TILE != Tile || big_tiles(w, w_chunks) + big_tiles(x, 1) >= kSmallGrid)
+    return false;
+  DualGrid d;
+  d.nx1 = (w.N + Tile - 1) / Tile;
+  d.ny1 = (w.M + Tile - 1) / Tile;
+  d.blocks1 = d.nx1 * d.ny1 * w_chunks;
+  d.nx2 = (x.N + Tile - 1) / Tile;
+  d.ny2 = (x.M + Tile - 1) / Tile;
+  const dim3 grid(d.blocks1 + d.nx2 * d.ny2), block(Threads);
+  if (w.a.k_fast && w.b.k_fast && !x.a.k_fast && !x.b.k_fast)
+    oxh::launch(pointwise_dual_kernel<Tile, Threads, true, true, false, false>, grid, block, 0, s,
+                w, x, d);
+  else if (!w.a.k_fast && !w.b.k_fast && !x.a.k_fast && x.b.k_fast)
+    oxh::launch(pointwise_dual_kernel<Tile, Threads, false, false, false, true>, grid, block, 0,
+                s, w, x, d);
+  else
+    return false;
+  return true;
+}
+
 oxh_status input_backward_impl(const char *name, oxh_stream stream,
                                const oxh_conv2d_shape *shape, const float *gradient,
                                const float *weight, const float *addend,
@@ -1266,23 +1404,8 @@ oxh_status input_backward_impl(const char *name, oxh_stream stream,
               std::string(name) + ": null pointer");
   const uint64_t in_n = input_elems(g);
   hipStream_t s = oxh::as_stream(stream);
-  if (pointwise(g)) {
-    // dX[ic, (n, p)] = 0 + sum_oc W[oc, ic] G[(n, p), oc]
-    const uint32_t plane = g.h * g.w;
-    ProductArgs a{};
-    a.a = operand(weight, linear(1), linear(g.in_c));
-    a.b = operand(gradient, batch_plane(plane, g.out_c), linear(plane));
-    a.c = input_gradient;
-    a.cm = linear(plane);
-    a.cn = batch_plane(plane, g.in_c);
-    a.init = nullptr;
-    a.addend = addend;
-    a.M = g.in_c;
-    a.N = g.batch * plane;
-    a.K = g.out_c;
-    a.k_chunk = a.K;
-    return launch_product(name, s, a, 1);
-  }
+  if (pointwise(g))
+    return launch_product(name, s, input_product(g, gradient, weight, addend, input_gradient), 1);
   const LdsPlan lp = input_backward_lds_plan(g);
   if (lp.tile > 0) {
     const dim3 lgrid(lp.tiles, g.batch), lblock(256);
@@ -1419,22 +1542,11 @@ oxh_status oxh_conv2d_weight_backward(oxh_stream stream, const oxh_conv2d_shape 
   float *partial = static_cast<float *>(workspace);
   hipStream_t s = oxh::as_stream(stream);
   if (pointwise(g)) {
-    // dW[oc, ic] = sum_{(n, p)} G[oc, (n, p)] X[ic, (n, p)], k = (n, p) in chunks
-    const uint32_t plane = g.h * g.w;
     const KSplit split = product_split(g);
-    ProductArgs a{};
-    a.a = operand(gradient, linear(plane), batch_plane(plane, g.out_c));
-    a.b = operand(input, linear(plane), batch_plane(plane, g.in_c));
-    a.c = split.chunks > 1 ? partial : weight_gradient;
-    a.cm = linear(g.in_c);
-    a.cn = linear(1);
-    a.c_chunk = g.out_c * g.in_c;
-    a.init = nullptr;
-    a.M = g.out_c;
-    a.N = g.in_c;
-    a.K = g.batch * plane;
-    a.k_chunk = split.per;
-    st = launch_product(name, s, a, split.chunks);
+    st = launch_product(
+        name, s,
+        weight_product(g, split, gradient, input, split.chunks > 1 ? partial : weight_gradient),
+        split.chunks);
     if (st != OXH_OK || split.chunks == 1) return st;
     const uint32_t count = g.out_c * g.in_c;
     oxh::launch(sum_chunks_kernel, dim3(grid_for(count)), dim3(256), 0, s, count, split.chunks,
@@ -1502,6 +1614,66 @@ oxh_status oxh_conv2d_bias_backward(oxh_stream stream, const oxh_conv2d_shape *s
               g.batch, g.out_c, g.oh * g.ow, oxh::make_fastdiv(g.oh * g.ow), gradient,
               bias_gradient);
   return oxh::launched(name);
+}
+
+oxh_status oxh_conv2d_backward(oxh_stream stream, const oxh_conv2d_shape *shape,
+                               const float *gradient, const float *input, const float *weight,
+                               const float *addend, float *input_gradient,
+                               float *weight_gradient, float *bias_gradient, void *workspace,
+                               uint64_t workspace_bytes) {
+  const char *name = "oxh_conv2d_backward";
+  ConvGeom g;
+  oxh_status st = make_conv_geom(name, shape, g);
+  if (st != OXH_OK) return st;
+  OXH_REQUIRE(gradient && input && weight && input_gradient && weight_gradient,
+              OXH_INVALID_SHAPE, std::string(name) + ": null pointer");
+  const uint64_t need = weight_partial_bytes(g);
+  OXH_REQUIRE(need == 0 || (workspace != nullptr && workspace_bytes >= need), OXH_INVALID_SHAPE,
+              std::string(name) +
+                  ": workspace too small (oxh_conv2d_weight_backward_workspace_size)");
+  // the two gradients are formed concurrently: neither may overlap what the other reads
+  const uint64_t gx = input_elems(g) * 4, gy = output_elems(g) * 4, gw = weight_elems(g) * 4;
+  const uint64_t gb = bias_gradient != nullptr ? g.out_c * 4ull : 0;
+  OXH_REQUIRE(!oxh::any_overlap(input_gradient, gx, gradient, gy) &&
+                  !oxh::any_overlap(input_gradient, gx, input, gx) &&
+                  !oxh::any_overlap(input_gradient, gx, weight, gw) &&
+                  !oxh::any_overlap(input_gradient, gx, weight_gradient, gw) &&
+                  !oxh::any_overlap(input_gradient, gx, bias_gradient, gb) &&
+                  !oxh::any_overlap(input_gradient, gx, workspace, need) &&
+                  !oxh::any_overlap(weight_gradient, gw, weight, gw) &&
+                  !oxh::any_overlap(weight_gradient, gw, gradient, gy) &&
+                  !oxh::any_overlap(weight_gradient, gw, input, gx),
+              OXH_INVALID_SHAPE, std::string(name) + ": a gradient overlaps an operand");
+  hipStream_t s = oxh::as_stream(stream);
+  if (pointwise(g)) {
+    const KSplit split = product_split(g);
+    float *partial = static_cast<float *>(workspace);
+    const ProductArgs w =
+        weight_product(g, split, gradient, input, split.chunks > 1 ? partial : weight_gradient);
+    const ProductArgs x = input_product(g, gradient, weight, addend, input_gradient);
+    if (launch_dual(s, w, split.chunks, x)) {
+      st = oxh::launched(name);
+      if (st != OXH_OK) return st;
+      if (split.chunks > 1) {
+        const uint32_t count = g.out_c * g.in_c;
+        oxh::launch(sum_chunks_kernel, dim3(grid_for(count)), dim3(256), 0, s, count,
+                    split.chunks, static_cast<const float *>(partial), weight_gradient);
+        st = oxh::launched(name);
+        if (st != OXH_OK) return st;
+      }
+      if (bias_gradient != nullptr)
+        return oxh_conv2d_bias_backward(stream, shape, gradient, bias_gradient, nullptr, 0);
+      return OXH_OK;
+    }
+  }
+  st = oxh_conv2d_weight_backward(stream, shape, gradient, input, weight_gradient, workspace,
+                                  workspace_bytes);
+  if (st != OXH_OK) return st;
+  if (bias_gradient != nullptr) {
+    st = oxh_conv2d_bias_backward(stream, shape, gradient, bias_gradient, nullptr, 0);
+    if (st != OXH_OK) return st;
+  }
+  return input_backward_impl(name, stream, shape, gradient, weight, addend, input_gradient);
 }
 
 oxh_status oxh_avg_pool2d_forward(oxh_stream stream, const oxh_pool2d_shape *shape,

@@ -680,6 +680,18 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
     if (want(static_cast<int>(i)) && (g.nodes[i].op == Op::Bn || dw_conv[i]))
       for (int k : g.nodes[i].in) discards = discards || !want(k);
   const uint64_t discard_off = a.reserve(discards ? kDiscardSlots * largest * 4 : 4);
+  // A gradient a launch forms beside its main contribution (a convolution's or BatchNorm's
+  // parameters) whose node already holds a contribution (a value feeding several layers) goes
+  // to one of kSideSlots side buffers and is added into the node's gradient after the launch.
+  constexpr size_t kSideSlots = 5;
+  bool sides = false;
+  for (size_t i = 0; i < n; ++i) {
+    const Node &x = g.nodes[i];
+    if (!active[i] || (x.op != Op::Conv && x.op != Op::Bn)) continue;
+    for (size_t k = 1; k < x.in.size(); ++k)
+      sides = sides || (want(x.in[k]) && consumers[x.in[k]] > 1);
+  }
+  const uint64_t side_off = a.reserve(sides ? kSideSlots * largest * 4 : 4);
   uint64_t ws_bytes = 0;
   oxh_status st = plan_workspace(g, active, ws_bytes);
   if (st != OXH_OK) return st;
@@ -712,8 +724,10 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
     }
   }
   float *scratch = a.at<float>(scratch_off), *discard = a.at<float>(discard_off);
+  float *side_base = a.at<float>(side_off);
   int discard_next = 0;
   bool discard_unplanned = false;  // a discard the arena did not plan for (a scheduling bug)
+  bool side_unplanned = false;     // likewise for a side buffer
   float *one = a.at<float>(one_off);
   p.step = a.at<int32_t>(step_off);
   p.error_flag = a.at<uint32_t>(flag_off);
@@ -778,6 +792,43 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
       acc = p.grad[x];
     }
   };
+  // A side contribution to node x (role: the launch's output it is): in place when it is the
+  // node's first, else into the next side buffer, added after the launch by attach_sides.
+  struct SideAdd {
+    float *into, *part;
+    uint64_t count;
+    std::string role;
+    int node;
+  };
+  std::vector<SideAdd> side_adds;
+  auto side = [&](int x, float *&dst, const char *role) {
+    float *acc;
+    contribution(x, dst, acc);
+    if (acc == nullptr) return;
+    if (!sides || side_adds.size() >= kSideSlots) {
+      side_unplanned = true;
+      return;
+    }
+    dst = side_base + side_adds.size() * largest;
+    side_adds.push_back(SideAdd{acc, dst, g.nodes[x].numel(), role, x});
+  };
+  auto attach_sides = [&](OpRec &op) {
+    if (side_adds.empty()) return;
+    std::vector<SideAdd> adds;
+    adds.swap(side_adds);
+    for (const SideAdd &sa : adds)
+      op.tensors.push_back(ref(("accumulate_into:" + sa.role).c_str(), sa.into,
+                               g.nodes[sa.node], 2));
+    auto body = std::move(op.launch);
+    op.launch = [body, adds](hipStream_t st) {
+      oxh_status e = body(st);
+      for (const SideAdd &sa : adds) {
+        if (e != OXH_OK) return e;
+        e = oxh_accumulate(st, sa.into, sa.part, sa.into, sa.count);
+      }
+      return e;
+    };
+  };
   auto emit = [&](OpRec op, float *acc, const Node &target,
                   std::function<oxh_status(hipStream_t)> body) {
     if (acc == nullptr) {
@@ -792,6 +843,7 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
         return oxh_accumulate(s, acc, part, acc, cnt);
       };
     }
+    attach_sides(op);
     ops.push_back(std::move(op));
   };
   // a copy contribution: d2d copy of `gradient` (the backward of an identity)
@@ -1047,11 +1099,11 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
         const float *y = fused ? p.value[r] : nullptr;
         const float *sm = p.saved_mean[bi], *si = p.saved_inv[bi];
         const uint64_t N = bn.shape[0], C = bn.shape[1], HW = bn.shape[2] * bn.shape[3];
-        float *dg, *db, *dst, *acc, *unused;
+        float *dg, *db, *dst, *acc;
         if (!bn.training) {  // autograd.rs:340-381 with running statistics
           const float *rm = bn.running_mean;
-          contribution(bn.in[1], dg, unused);
-          contribution(bn.in[2], db, unused);
+          side(bn.in[1], dg, "weight_gradient");
+          side(bn.in[2], db, "bias_gradient");
           op.kind = "batch_norm2d_eval_backward";
           op.name = name("bn", bi) + ".backward";
           op.tensors = {ref("gradient", const_cast<float *>(gr), x, 0),
@@ -1079,15 +1131,12 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
         if (dw_conv_of[bi] >= 0) {  // depthwise conv + BN (+ ReLU) backward in one launch
           const Node &cv = g.nodes[xin];
           const int cin = cv.in[0];
-          OXH_REQUIRE(!written[bn.in[1]] && !written[bn.in[2]] && !written[xin] &&
-                          !written[cv.in[1]] && !written[cv.in[2]],
-                      OXH_TRACE, "a fused depthwise layer's gradients have other contributions");
           float *cgr, *cdw, *cdb;
-          contribution(bn.in[1], dg, unused);
-          contribution(bn.in[2], db, unused);
-          contribution(xin, cgr, unused);
-          contribution(cv.in[2], cdb, unused);
-          contribution(cv.in[1], cdw, unused);
+          side(bn.in[1], dg, "weight_gradient");
+          side(bn.in[2], db, "bias_gradient");
+          side(xin, cgr, "conv_output_gradient");  // the BN is its only consumer
+          side(cv.in[2], cdb, "conv_bias_gradient");
+          side(cv.in[1], cdw, "conv_weight_gradient");
           const oxh_conv2d_shape s = conv_shape(g, cv);
           const float *cx = p.value[cin], *cw = p.value[cv.in[1]];
           const float *addend = nullptr;
@@ -1131,16 +1180,16 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
           });
           break;
         }
-        contribution(bn.in[1], dg, unused);
-        contribution(bn.in[2], db, unused);
+        side(bn.in[1], dg, "weight_gradient");
+        side(bn.in[2], db, "bias_gradient");
         contribution(xin, dst, acc);
         // a convolution whose only consumer is this BN: its output gradient is this dx, whose
         // per-channel sum (the convolution's bias gradient) the BN backward forms in passing
         float *conv_db = nullptr;
         const Node &src = g.nodes[xin];
         if (src.op == Op::Conv && consumers[xin] == 1 && acc == nullptr && want(xin) &&
-            want(src.in[2]) && !written[src.in[2]]) {
-          contribution(src.in[2], conv_db, unused);
+            want(src.in[2])) {
+          side(src.in[2], conv_db, "conv_bias_gradient");
           conv_bias_done[xin] = 1;
         }
         op.kind = fused ? "batch_norm2d_relu_backward" : "batch_norm2d_backward";
@@ -1203,11 +1252,40 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
         const oxh_conv2d_shape s = conv_shape(g, x);
         const int xin = x.in[0];
         const float *xi = p.value[xin], *w = p.value[x.in[1]];
-        float *dw = nullptr, *db = nullptr, *unused;
+        float *dw = nullptr, *db = nullptr;
         const bool weight_here = want(x.in[1]);
-        if (weight_here) contribution(x.in[1], dw, unused);
+        if (weight_here) side(x.in[1], dw, "weight_gradient");
         const bool bias_here = !conv_bias_done[r] && want(x.in[2]);  // else the BN formed it
-        if (bias_here) contribution(x.in[2], db, unused);
+        if (bias_here) side(x.in[2], db, "bias_gradient");
+        if (weight_here && want(xin)) {  // the whole VJP in one launch group
+          float *dst, *acc;
+          const float *addend = nullptr;
+          if (pending[xin].gradient != nullptr && !written[xin]) {
+            addend = pending[xin].gradient;
+            op.tensors.push_back(ref("addend", const_cast<float *>(addend),
+                                     g.nodes[pending[xin].add], 0));
+            pending[xin] = Pending{};
+            written[xin] = 1;
+            dst = p.grad[xin];
+            acc = nullptr;
+          } else {
+            contribution(xin, dst, acc);
+          }
+          op.kind = "conv2d_backward";
+          op.name = name("conv", r) + ".backward";
+          op.tensors.push_back(ref("gradient", const_cast<float *>(gr), x, 0));
+          op.tensors.push_back(ref("x", const_cast<float *>(xi), g.nodes[xin], 0));
+          op.tensors.push_back(ref("weight", const_cast<float *>(w), g.nodes[x.in[1]], 0));
+          op.tensors.push_back(ref("weight_gradient", dw, g.nodes[x.in[1]], 1));
+          if (bias_here) op.tensors.push_back(ref("bias_gradient", db, g.nodes[x.in[2]], 1));
+          op.tensors.push_back(ref("contribution", dst, g.nodes[xin], 1));
+          op.attrs = conv_attrs(x);
+          emit(std::move(op), acc, g.nodes[xin],
+               [s, gr, xi, w, addend, dst, dw, db, ws, wsb](hipStream_t st) {
+                 return oxh_conv2d_backward(st, &s, gr, xi, w, addend, dst, dw, db, ws, wsb);
+               });
+          break;
+        }
         if (weight_here || bias_here) {
           OpRec pr;
           pr.kind = "conv2d_parameter_backward";
@@ -1226,6 +1304,7 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
             if (db == nullptr) return oxh::ok();
             return oxh_conv2d_bias_backward(st, &s, gr, db, ws, wsb);
           };
+          attach_sides(pr);
           ops.push_back(std::move(pr));
         }
         if (!want(xin)) break;  // e.g. the network input needs no gradient
@@ -1261,6 +1340,8 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
   }
   for (size_t i = 0; i < n; ++i) flush(static_cast<int>(i));
   OXH_REQUIRE(!discard_unplanned, OXH_EXECUTION, "internal: unplanned gradient discard");
+  OXH_REQUIRE(!side_unplanned && side_adds.empty(), OXH_EXECUTION,
+              "internal: unplanned side contribution");
 
   // AdamW over every parameter that received a gradient (creation order)
   if (adam != nullptr && !trained.empty()) {

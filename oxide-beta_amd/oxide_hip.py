@@ -163,6 +163,7 @@ _SIGNATURES = {
     "oxh_conv2d_input_backward_accumulate": (_st, [_vp, _CS, _vp, _vp, _vp, _vp]),
     "oxh_conv2d_weight_backward_workspace_size": (_st, [_CS, ctypes.POINTER(_u64)]),
     "oxh_conv2d_weight_backward": (_st, [_vp, _CS, _vp, _vp, _vp, _vp, _u64]),
+    "oxh_conv2d_backward": (_st, [_vp, _CS, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u64]),
     "oxh_conv2d_bias_backward": (_st, [_vp, _CS, _vp, _vp, _vp, _u64]),
     "oxh_depthwise_conv_batch_norm_supported": (_int, [_CS]),
     "oxh_depthwise_conv_batch_norm_forward_train": (_st, [_vp, _CS, _int, _f32, _f32, _vp, _vp,
@@ -719,6 +720,15 @@ class LoadedModule:
         check(lib().oxh_conv2d_weight_backward(_stream(stream), ctypes.byref(shape),
                                                _ptr(gradient), _ptr(x), _ptr(weight_gradient),
                                                ws, wsb))
+
+    def conv2d_backward(self, shape, gradient, x, weight, input_gradient, weight_gradient,
+                        bias_gradient=None, addend=None, stream=None):
+        """The whole conv VJP: weight, optional bias and input gradients in one call."""
+        ws, wsb = self._conv_ws.ptr_bytes(conv2d_workspace_size(shape))
+        check(lib().oxh_conv2d_backward(
+            _stream(stream), ctypes.byref(shape), _ptr(gradient), _ptr(x), _ptr(weight),
+            _ptr(addend), _ptr(input_gradient), _ptr(weight_gradient), _ptr(bias_gradient),
+            ws, wsb))
 
     def conv2d_bias_backward(self, shape, gradient, bias_gradient, stream=None):
         ws, wsb = self._conv_ws.ptr_bytes(conv2d_workspace_size(shape))

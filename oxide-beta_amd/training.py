@@ -145,7 +145,9 @@ class Op:
     ``writes`` map unique roles to views; ``inplace`` lists the views it updates in place
     (their values before the launch are part of its input); ``by_role`` maps every role to
     its views in order; ``attrs`` holds the scalar arguments; ``accumulate_into`` is set when
-    the group adds its ``contribution`` into an existing gradient."""
+    the group adds its ``contribution`` into an existing gradient, and ``side_accumulate`` maps
+    a written role (a parameter gradient of a value with several consumers) to the gradient it
+    is added into after the launch."""
 
     def __init__(self, program, index: int, stream: int):
         info = OpInfo()
@@ -154,6 +156,7 @@ class Op:
         self.kind, self.name = info.kind.decode(), info.name.decode()
         self.reads, self.writes, self.inplace, self.by_role = {}, {}, [], {}
         self.accumulate_into = None
+        self.side_accumulate = {}
         for i in range(info.tensor_count):
             t = info.tensors[i]
             role = t.role.decode()
@@ -162,6 +165,9 @@ class Op:
             self.by_role.setdefault(role, []).append(v)
             if role == "accumulate_into":
                 self.accumulate_into = v
+                self.inplace.append(v)
+            elif role.startswith("accumulate_into:"):
+                self.side_accumulate[role.split(":", 1)[1]] = v
                 self.inplace.append(v)
             elif t.access == 0:
                 self.reads.setdefault(role, v)

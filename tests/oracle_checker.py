@@ -37,6 +37,11 @@ class OracleChecker:
             assert_bitexact(host(op.accumulate_into),
                             oracle.accumulate(prev, host(op.writes["contribution"])),
                             f"{op.name} accumulate")
+        for role, into in op.side_accumulate.items():
+            assert_bitexact(host(into),
+                            oracle.accumulate(self.prior[id(into)], host(op.writes[role])),
+                            f"{op.name} accumulate {role}")
+            self.counts["side accumulate"] += 1
         self.counts[op.kind] += 1
 
     # -- per kind
@@ -68,6 +73,12 @@ class OracleChecker:
                           1e-5 * np.abs(g).astype(np.float64).sum(axis=(0, 2, 3)) + 1e-7,
                           f"{op.name} bias")
             self.counts["conv bias in parameter backward"] += 1
+
+    def conv2d_backward(self, op, r):
+        """The whole conv VJP in one group: parameter gradients within their bound, the input
+        gradient (plus a residual add's gradient) bit-exact."""
+        self.conv2d_parameter_backward(op, r)
+        self.conv2d_input_backward(op, r)
 
     def _conv_bias(self, op):
         """The bias gradient of the convolution feeding a BatchNorm, formed by the BN backward

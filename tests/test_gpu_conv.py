@@ -98,6 +98,51 @@ def test_conv2d_input_backward_accumulate(module, dev, case, in_place):
         module.conv2d_input_backward_accumulate(shape, dg_, dw_, None, out)
 
 
+@pytest.mark.parametrize("case", [
+    (128, 96, 4, 4, 192, 1, 1, 1),     # config-5 shapes: both products in one launch (plane > 1)
+    (128, 512, 1, 1, 128, 1, 1, 1),    # plane 1: the other operand layouts, one launch
+    (128, 64, 8, 8, 256, 1, 1, 1),     # chunked weight gradient, grids too large to pair
+    (128, 960, 1, 1, 1280, 1, 1, 1),
+    (1, 1, 3, 3, 5, 1, 1, 1),          # one input channel: layouts outside the paired set
+    (3, 12, 6, 5, 8, 3, 1, 4),         # grouped 3 x 3 and ungrouped 3 x 3: the separate kernels
+    (128, 32, 7, 7, 96, 3, 2, 1),
+])
+@pytest.mark.parametrize("variant", ["plain", "bias", "addend", "addend in place"])
+def test_conv2d_backward_equals_separate_calls(module, dev, case, variant):
+    """oxh_conv2d_backward (the whole VJP in one call) writes exactly what the separate weight,
+    bias and input (or input + addend) backward entry points write."""
+    n, cin, h, w, cout, k, s, groups = case
+    pad = k // 2
+    r = np.random.default_rng(hash((case, variant)) & 0xFFFFFF)
+    shape = ox.conv2d_shape(n, cin, h, w, cout, k, s, pad, groups)
+    oh, ow = ox.conv2d_output_size(shape)
+    x = to_dev(r.standard_normal((n, cin, h, w)).astype(np.float32), dev)
+    wt = to_dev((r.standard_normal((cout, cin // groups, k, k)) * 0.3).astype(np.float32), dev)
+    g = to_dev(r.standard_normal((n, cout, oh, ow)).astype(np.float32), dev)
+    addend = to_dev(r.standard_normal((n, cin, h, w)).astype(np.float32), dev)
+    ref_dx, ref_dw, ref_db = torch.empty_like(x), torch.empty_like(wt), torch.empty(cout, device=dev)
+    if variant.startswith("addend"):
+        module.conv2d_input_backward_accumulate(shape, g, wt, addend, ref_dx)
+    else:
+        module.conv2d_input_backward(shape, g, wt, ref_dx)
+    module.conv2d_weight_backward(shape, g, x, ref_dw)
+    module.conv2d_bias_backward(shape, g, ref_db)
+    dx = addend.clone() if variant == "addend in place" else torch.full_like(x, float("nan"))
+    dw, db = torch.full_like(wt, float("nan")), torch.full((cout,), float("nan"), device=dev)
+    module.conv2d_backward(shape, g, x, wt, dx, dw, db if variant == "bias" else None,
+                           addend=(dx if variant == "addend in place" else
+                                   addend if variant == "addend" else None))
+    torch.cuda.synchronize()
+    assert_bitexact(host(dx), host(ref_dx), "input gradient")
+    assert_bitexact(host(dw), host(ref_dw), "weight gradient")
+    if variant == "bias":
+        assert_bitexact(host(db), host(ref_db), "bias gradient")
+    else:
+        assert np.isnan(host(db)).all()  # not written
+    with pytest.raises(ox.OxideError):  # the input gradient may not overlap the gradient
+        module.conv2d_backward(shape, g, x, wt, g if g.numel() >= x.numel() else x, dw)
+
+
 @pytest.mark.parametrize("shape,kernel,stride", [((2, 3, 4, 4), (2, 2), (2, 2)),
                                                  ((128, 960, 1, 1), (1, 1), (1, 1)),
                                                  ((2, 5, 7, 7), (7, 7), (7, 7)),

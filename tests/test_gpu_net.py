@@ -148,7 +148,7 @@ def test_general_graph_every_op_matches_oracle():
                  "add_forward", "avg_pool2d_forward", "cross_entropy_forward", "seed",
                  "mul_backward", "add_backward", "reshape_backward", "cross_entropy_backward",
                  "avg_pool2d_backward", "relu_backward", "batch_norm2d_eval_backward",
-                 "conv2d_parameter_backward", "conv2d_input_backward"):
+                 "conv2d_backward"):
         assert counts[kind] >= 1, (kind, dict(counts))
     # torch float64 autograd of the same graph
     d = lambda v: torch.tensor(v, dtype=torch.float64, requires_grad=True)  # noqa: E731
@@ -173,6 +173,79 @@ def test_general_graph_every_op_matches_oracle():
     # running statistics untouched in eval mode; constants get no gradient buffer
     np.testing.assert_array_equal(host(state.running_mean), rm)
     assert prog.gradient(t) is None
+
+
+def test_shared_parameters_accumulate_every_use():
+    """One 1x1 convolution's weight and bias used by two layers, one BatchNorm's gamma and beta
+    by three (two after those convolutions, one fused with a depthwise convolution), a
+    residual add: every use after a parameter's first adds its gradient into the parameter's
+    (the later ones are formed beside the launch's main output and accumulated after it).
+    Every launch against the oracle, the gradients against torch float64 autograd."""
+    r = np.random.default_rng(47)
+    n, c, h, w = 4, 4, 6, 6
+    xv = r.standard_normal((n, c, h, w)).astype(np.float32)
+    wv = (r.standard_normal((c, c, 1, 1)) * 0.5).astype(np.float32)
+    bv = r.standard_normal(c).astype(np.float32)
+    dwv = (r.standard_normal((c, 1, 3, 3)) * 0.5).astype(np.float32)
+    dbv = r.standard_normal(c).astype(np.float32)
+    gam, bet = r.uniform(0.5, 1.5, c).astype(np.float32), r.uniform(-0.2, 0.2, c).astype(np.float32)
+    targets = r.integers(0, c * 9, n).astype(np.float32)
+
+    x = tn.input((n, c, h, w), requires_grad=True)
+    weight, bias = nn.Parameter(wv), nn.Parameter(bv)
+    dweight, dbias = nn.Parameter(dwv), nn.Parameter(dbv)
+    gamma, beta = nn.Parameter(gam), nn.Parameter(bet)
+
+    def block(v, wt, b, stride, pad, groups):
+        conv = v.conv2d(wt.tensor(), b.tensor(), stride, pad, groups)
+        return conv.batch_norm2d(gamma.tensor(), beta.tensor(), tn.BatchNormState(c), True,
+                                 0.1, 1e-5)
+
+    a = block(x, weight, bias, 1, 0, 1).relu()
+    b2 = block(a, weight, bias, 1, 0, 1).relu()
+    s = block(b2, dweight, dbias, 1, 1, c).add(b2)
+    t = tn.input((n,))
+    loss = s.avg_pool2d((2, 2), (2, 2)).reshape((n, c * 9)).cross_entropy(t)
+    prog = tn.training_program(loss)
+    prog.feed(x, xv)
+    prog.feed(t, targets)
+    counts = _run_checked(prog)
+    assert counts["side accumulate"] >= 4, dict(counts)
+    assert counts["conv2d_backward"] >= 2, dict(counts)
+
+    d = lambda v: torch.tensor(v, dtype=torch.float64, requires_grad=True)  # noqa: E731
+    tx, tw, tb, tdw, tdb, tg, tbe = d(xv), d(wv), d(bv), d(dwv), d(dbv), d(gam), d(bet)
+    F = torch.nn.functional
+
+    conv_out = []
+
+    def tblock(v, wt, b, pad, groups):
+        y = F.conv2d(v, wt, b, 1, pad, 1, groups)
+        y.retain_grad()
+        conv_out.append(y)
+        return F.batch_norm(y, torch.zeros(c, dtype=torch.float64),
+                            torch.ones(c, dtype=torch.float64), tg, tbe, True, 0.1, 1e-5)
+
+    ta = tblock(tx, tw, tb, 0, 1).relu()
+    tb2 = tblock(ta, tw, tb, 0, 1).relu()
+    ts = tblock(tb2, tdw, tdb, 1, c) + tb2
+    tl = F.cross_entropy(F.avg_pool2d(ts, 2, 2).reshape(n, c * 9),
+                         torch.tensor(targets, dtype=torch.long))
+    tl.backward()
+    assert abs(float(prog.value(loss).host()[0]) - tl.item()) <= 1e-5 * abs(tl.item())
+    for got, ref, what in ((x, tx, "dx"), (weight.tensor(), tw, "dweight"),
+                           (dweight.tensor(), tdw, "dw dweight"), (gamma.tensor(), tg, "dgamma"),
+                           (beta.tensor(), tbe, "dbeta")):
+        ref = ref.grad.numpy()
+        np.testing.assert_allclose(prog.gradient(got).host(), ref, rtol=1e-4,
+                                   atol=1e-5 * np.abs(ref).max() + 1e-7, err_msg=what)
+    # a bias feeding a training-mode BatchNorm has gradient 0 in exact arithmetic: within the
+    # conditioning bound of its sums, 1e-5 * sum|terms| over every use
+    terms = [np.abs(y.grad.numpy()).sum(axis=(0, 2, 3)) for y in conv_out]
+    for got, ref, bound, what in ((bias.tensor(), tb, terms[0] + terms[1], "dbias"),
+                                  (dbias.tensor(), tdb, terms[2], "dw dbias")):
+        err = np.abs(prog.gradient(got).host() - ref.grad.numpy())
+        assert (err <= 1e-5 * bound + 1e-7).all(), (what, err, bound)
 
 
 def _mnist_batch(r, n):

@@ -29,14 +29,16 @@ def _mnist_batch(r, n):
     return images, labels
 
 
+# Every convolution but the stem (whose input, the image, takes no gradient) forms its weight
+# and input gradients in one launch group.
 # 46 BatchNorms, 32 of them followed by a ReLU (fused), each fed by a convolution whose bias
 # gradient its backward forms (the classifier's, fed by no BN, stays with its parameter
 # backward); the 15 depthwise convolutions run with their BatchNorm + ReLU in one launch per
 # direction; 10 residual adds, formed by the forward of the BN feeding them, whose first
 # operand's gradient is the add's own buffer and whose second operand's is added by that
 # operand's convolution input backward (no add launches in either direction)
-EXPECTED_KINDS = {"conv2d_forward": 32, "conv2d_parameter_backward": 32,
-                  "conv2d_input_backward": 31, "batch_norm2d_forward": 4,
+EXPECTED_KINDS = {"conv2d_forward": 32, "conv2d_parameter_backward": 1,
+                  "conv2d_backward": 31, "batch_norm2d_forward": 4,
                   "batch_norm2d_add_forward": 10,
                   "batch_norm2d_relu_forward": 17, "batch_norm2d_backward": 14,
                   "batch_norm2d_relu_backward": 17,
