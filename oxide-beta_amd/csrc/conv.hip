@@ -301,7 +301,7 @@ __global__ __launch_bounds__(256) void conv2d_forward_lds_kernel(
   if (ocp > ocn) zero_fill(wl, rows, ocp, ocn, ocp - ocn);
   __syncthreads();
   const uint32_t oplane = g.oh * g.ow, items = (ocp / kLdsR) * oplane;
-  for (uint32_t it = threadIdx.x; it < items; it += 256) {
+  for (uint32_t it = threadIdx.x; it < items; it += blockDim.x) {
     const uint32_t q = fdiv(it, oplane_div), pos = it - q * oplane;
     const uint32_t oy = fdiv(pos, g.ow_div), ox = pos - oy * g.ow;
     const int by = static_cast<int>(oy) * S - static_cast<int>(g.pad);
@@ -372,7 +372,7 @@ __global__ __launch_bounds__(256) void conv2d_input_backward_lds_kernel(
   if (icp > icn) zero_fill(wl, rows, icp, icn, icp - icn);
   __syncthreads();
   const uint32_t plane = g.h * g.w, items = (icp / kLdsR) * plane;
-  for (uint32_t it = threadIdx.x; it < items; it += 256) {
+  for (uint32_t it = threadIdx.x; it < items; it += blockDim.x) {
     const uint32_t q = fdiv(it, plane_div), pos = it - q * plane;
     const uint32_t iy = fdiv(pos, g.w_div), ix = pos - iy * g.w;
     const int ty = static_cast<int>(iy + g.pad), tx = static_cast<int>(ix + g.pad);
@@ -742,8 +742,7 @@ struct SlabLoader {
   uint32_t row_ok;  // bit i: row i inside the operand
   int r, kk;        // first (row, k) of the thread
 
-  __device__ __forceinline__ SlabLoader(const Operand &o, uint32_t r0, uint32_t rows) {
-    const int t = static_cast<int>(threadIdx.x);
+  __device__ __forceinline__ SlabLoader(const Operand &o, uint32_t r0, uint32_t rows, int t) {
     r = KFast ? (kSlab > Threads ? 0 : t / kSlab) : t % Tile;
     kk = KFast ? t % kSlab : t / Tile;
     row_ok = 0;
@@ -819,48 +818,25 @@ struct ProductRow {
   static constexpr int value = S::kSlab + kGroupK + 4;
 };
 
-// C[m, n] = init[m] + sum_{k in chunk, ascending} A[m, k] * B[n, k]: one serial fp32 sum per
-// output (each product rounded, then added: -ffp-contract=off).  Within a slab, groups of kG4
-// float4 (4 k each) per row are read from LDS as 128-bit accesses, the next group's reads
-// issued before the current group's arithmetic.  One block's tile (bx, by) of chunk bz, with
-// the block's LDS operand tiles as and bs.
+// sum_{k in [kb, ke), ascending} A[m, k] * B[n, k] added to acc, one serial fp32 sum per
+// output (each product rounded, then added: -ffp-contract=off), for the tile at rows m0 (of A)
+// and n0 (of B), computed by the Threads threads t = 0 .. Threads - 1 with the LDS operand tiles
+// as and bs.  `slabs` stages run (at least ceil((ke - kb) / kSlab); later ones are empty), each
+// with two block-wide barriers, so groups of threads sharing a block run equal counts.  Within a
+// slab, groups of kG4 float4 (4 k each) per row are read from LDS as 128-bit accesses, the next
+// group's reads issued before the current group's arithmetic.
 template <int Tile, int Threads, bool AKFast, bool BKFast>
-__device__ __forceinline__ void product_tile(const ProductArgs &g, uint32_t bx, uint32_t by,
-                                             uint32_t bz,
-                                             float (*as)[ProductRow<Tile, Threads>::value],
-                                             float (*bs)[ProductRow<Tile, Threads>::value]) {
+__device__ __forceinline__ void product_sum(
+    const ProductArgs &g, uint32_t m0, uint32_t n0, uint32_t kb, uint32_t ke, uint32_t slabs,
+    int t, float (&acc)[TileShape<Tile, Threads>::kMicro][TileShape<Tile, Threads>::kMicro],
+    float (*as)[ProductRow<Tile, Threads>::value], float (*bs)[ProductRow<Tile, Threads>::value]) {
   using S = TileShape<Tile, Threads>;
   constexpr int kMicro = S::kMicro, kLoads = S::kLoads, kSlab = S::kSlab, kCols = S::kCols;
   constexpr int kG4 = ProductRow<Tile, Threads>::kG4;
   constexpr int kGroupK = ProductRow<Tile, Threads>::kGroupK;
-  const uint32_t m0 = by * Tile, n0 = bx * Tile;
-  const uint32_t kb = bz * g.k_chunk;
-  const uint32_t ke = min(kb + g.k_chunk, g.K);
-  const int tx = threadIdx.x % kCols, ty = threadIdx.x / kCols;
-  float acc[kMicro][kMicro];
-#pragma unroll
-  for (int i = 0; i < kMicro; ++i) {
-    const uint32_t m = m0 + ty * kMicro + i;
-    const float v = (g.init != nullptr && m < g.M) ? g.init[m] : 0.0f;
-#pragma unroll
-    for (int j = 0; j < kMicro; ++j) acc[i][j] = v;
-  }
-  // the addend is loaded now, with the first slab (after the k loop it would add a memory
-  // round trip to the block)
-  float added[kMicro][kMicro];
-  if (g.addend != nullptr) {
-#pragma unroll
-    for (int i = 0; i < kMicro; ++i)
-#pragma unroll
-      for (int j = 0; j < kMicro; ++j) {
-        const uint32_t m = m0 + ty * kMicro + i, n = n0 + tx * kMicro + j;
-        added[i][j] = m < g.M && n < g.N
-                          ? g.addend[axis_offset(g.cm, m) + axis_offset(g.cn, n)]
-                          : 0.0f;
-      }
-  }
-  const SlabLoader<Tile, Threads, AKFast> la(g.a, m0, g.M);
-  const SlabLoader<Tile, Threads, BKFast> lb(g.b, n0, g.N);
+  const int tx = t % kCols, ty = t / kCols;
+  const SlabLoader<Tile, Threads, AKFast> la(g.a, m0, g.M, t);
+  const SlabLoader<Tile, Threads, BKFast> lb(g.b, n0, g.N, t);
   float va[kLoads], vb[kLoads];
   if (kb < ke) {
     const uint32_t kc = min(ke - kb, static_cast<uint32_t>(kSlab));
@@ -893,16 +869,19 @@ __device__ __forceinline__ void product_tile(const ProductArgs &g, uint32_t bx, 
           p[i][j][4 * q + 3] = av[i][q].w * bv[j][q].w;
         }
 #pragma unroll
-    for (int t = 0; t < 4 * kG4; ++t)
+    for (int u = 0; u < 4 * kG4; ++u)
 #pragma unroll
       for (int i = 0; i < kMicro; ++i)
 #pragma unroll
-        for (int j = 0; j < kMicro; ++j) acc[i][j] += p[i][j][t];
+        for (int j = 0; j < kMicro; ++j) acc[i][j] += p[i][j][u];
   };
-  for (uint32_t k0 = kb; k0 < ke; k0 += kSlab) {
-    const uint32_t kc = min(ke - k0, static_cast<uint32_t>(kSlab));
-    la.stage(va, as);
-    lb.stage(vb, bs);
+  for (uint32_t s = 0; s < slabs; ++s) {
+    const uint32_t k0 = kb + s * kSlab;
+    const uint32_t kc = k0 < ke ? min(ke - k0, static_cast<uint32_t>(kSlab)) : 0;
+    if (kc > 0) {
+      la.stage(va, as);
+      lb.stage(vb, bs);
+    }
     __syncthreads();
     const uint32_t k1 = k0 + kSlab;
     if (k1 < ke) {  // the next slab's loads overlap this slab's arithmetic
@@ -937,19 +916,56 @@ __device__ __forceinline__ void product_tile(const ProductArgs &g, uint32_t bx, 
     }
     __syncthreads();
   }
+}
+
+// Output (m, n) of chunk bz: c[bz * c_chunk + offset(cm, m) + offset(cn, n)] = sum (+ addend).
+__device__ __forceinline__ void product_store(const ProductArgs &g, uint32_t bz, uint32_t m,
+                                              uint32_t n, float sum, float added) {
+  if (m >= g.M || n >= g.N) return;
   float *c = g.c + static_cast<uint64_t>(bz) * g.c_chunk;
+  c[axis_offset(g.cm, m) + axis_offset(g.cn, n)] = g.addend != nullptr ? sum + added : sum;
+}
+
+// C[m, n] = init[m] + sum_{k in chunk bz, ascending} A[m, k] * B[n, k] (+ addend) for the tile
+// (bx, by): one serial sum per output, computed by the block's Threads threads.
+template <int Tile, int Threads, bool AKFast, bool BKFast>
+__device__ __forceinline__ void product_tile(const ProductArgs &g, uint32_t bx, uint32_t by,
+                                             uint32_t bz,
+                                             float (*as)[ProductRow<Tile, Threads>::value],
+                                             float (*bs)[ProductRow<Tile, Threads>::value]) {
+  using S = TileShape<Tile, Threads>;
+  constexpr int kMicro = S::kMicro, kCols = S::kCols;
+  const uint32_t m0 = by * Tile, n0 = bx * Tile;
+  const uint32_t kb = bz * g.k_chunk;
+  const uint32_t ke = min(kb + g.k_chunk, g.K);
+  const int t = static_cast<int>(threadIdx.x), tx = t % kCols, ty = t / kCols;
+  float acc[kMicro][kMicro];
 #pragma unroll
   for (int i = 0; i < kMicro; ++i) {
     const uint32_t m = m0 + ty * kMicro + i;
-    if (m >= g.M) continue;
+    const float v = (g.init != nullptr && m < g.M) ? g.init[m] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < kMicro; ++j) acc[i][j] = v;
+  }
+  // the addend is loaded now, with the first slab (after the k loop it would add a memory
+  // round trip to the block)
+  float added[kMicro][kMicro];
+#pragma unroll
+  for (int i = 0; i < kMicro; ++i)
 #pragma unroll
     for (int j = 0; j < kMicro; ++j) {
-      const uint32_t n = n0 + tx * kMicro + j;
-      if (n >= g.N) continue;
-      const uint32_t idx = axis_offset(g.cm, m) + axis_offset(g.cn, n);
-      c[idx] = g.addend != nullptr ? acc[i][j] + added[i][j] : acc[i][j];
+      const uint32_t m = m0 + ty * kMicro + i, n = n0 + tx * kMicro + j;
+      added[i][j] = g.addend != nullptr && m < g.M && n < g.N
+                        ? g.addend[axis_offset(g.cm, m) + axis_offset(g.cn, n)]
+                        : 0.0f;
     }
-  }
+  const uint32_t slabs = kb < ke ? (ke - kb + S::kSlab - 1) / S::kSlab : 0;
+  product_sum<Tile, Threads, AKFast, BKFast>(g, m0, n0, kb, ke, slabs, t, acc, as, bs);
+#pragma unroll
+  for (int i = 0; i < kMicro; ++i)
+#pragma unroll
+    for (int j = 0; j < kMicro; ++j)
+      product_store(g, bz, m0 + ty * kMicro + i, n0 + tx * kMicro + j, acc[i][j], added[i][j]);
 }
 
 template <int Tile, int Threads, bool AKFast, bool BKFast>
@@ -960,27 +976,75 @@ __global__ __launch_bounds__(Threads) void pointwise_product_kernel(ProductArgs 
   product_tile<Tile, Threads, AKFast, BKFast>(g, blockIdx.x, blockIdx.y, blockIdx.z, as, bs);
 }
 
-// Two independent products in one launch (a convolution's weight gradient and input
-// gradient): blocks [0, blocks1) take product 1's tiles, the rest product 2's, each tile
-// computed exactly as pointwise_product_kernel computes it.
+// Products whose sums need not follow the serial order (the weight gradient, already reduced in
+// k chunks): an 8 x 8 tile per kSplitWaves-wave block, wave w summing the w-th contiguous part
+// of the chunk's k range serially, the parts then added in wave order.  Four times the waves of
+// the one-wave tile and a quarter of its serial chain.  No initial value or addend.
+constexpr int kSplitWaves = 4;
+constexpr int kSplitThreads = 64 * kSplitWaves;
+struct SplitLds {
+  float as[kSplitWaves][8][ProductRow<8, 64>::value];
+  float bs[kSplitWaves][8][ProductRow<8, 64>::value];
+  float part[kSplitWaves - 1][64];
+};
+
+template <bool AKFast, bool BKFast>
+__device__ __forceinline__ void split_tile(const ProductArgs &g, uint32_t bx, uint32_t by,
+                                           uint32_t bz, SplitLds &lds) {
+  constexpr int kSlab = TileShape<8, 64>::kSlab;
+  const uint32_t m0 = by * 8, n0 = bx * 8;
+  const uint32_t kb = bz * g.k_chunk;
+  const uint32_t ke = min(kb + g.k_chunk, g.K);
+  const uint32_t span = kb < ke ? ke - kb : 0;
+  const uint32_t part = (span + kSplitWaves - 1) / kSplitWaves;
+  const int w = static_cast<int>(threadIdx.x) / 64, t = static_cast<int>(threadIdx.x) % 64;
+  const uint32_t wb = min(kb + w * part, ke), we = min(wb + part, ke);
+  const uint32_t slabs = (part + kSlab - 1) / kSlab;  // equal for every wave (barriers)
+  float acc[1][1] = {{0.0f}};
+  product_sum<8, 64, AKFast, BKFast>(g, m0, n0, wb, we, slabs, t, acc, lds.as[w], lds.bs[w]);
+  if (w > 0) lds.part[w - 1][t] = acc[0][0];
+  __syncthreads();
+  if (w > 0) return;
+  float sum = acc[0][0];
+#pragma unroll
+  for (int q = 0; q < kSplitWaves - 1; ++q) sum += lds.part[q][t];
+  product_store(g, bz, m0 + t / 8, n0 + t % 8, sum, 0.0f);
+}
+
+template <bool AKFast, bool BKFast>
+__global__ __launch_bounds__(kSplitThreads) void pointwise_split_kernel(ProductArgs g) {
+  __shared__ __align__(16) SplitLds lds;
+  split_tile<AKFast, BKFast>(g, blockIdx.x, blockIdx.y, blockIdx.z, lds);
+}
+
+// A convolution's input gradient (16 x 16 serial tiles, one output per thread: g1) and weight
+// gradient (split tiles: g2) in one launch.  Blocks [0, blocks1) take the input gradient's
+// tiles, dispatched first (their serial chains over the output channels are the longer ones),
+// the rest the weight gradient's, each computed exactly as its own kernel computes it.
 struct DualGrid {
   uint32_t nx1, ny1, blocks1, nx2, ny2;
 };
 
-template <int Tile, int Threads, bool A1, bool B1, bool A2, bool B2>
-__global__ __launch_bounds__(Threads) void pointwise_dual_kernel(ProductArgs g1, ProductArgs g2,
-                                                                 DualGrid d) {
-  constexpr int kRow = ProductRow<Tile, Threads>::value;
-  __shared__ __align__(16) float as[Tile][kRow];
-  __shared__ __align__(16) float bs[Tile][kRow];
+template <bool A1, bool B1, bool A2, bool B2>
+__global__ __launch_bounds__(kSplitThreads) void pointwise_dual_kernel(ProductArgs g1,
+                                                                       ProductArgs g2,
+                                                                       DualGrid d) {
+  constexpr int kRow = ProductRow<16, 256>::value;
+  union Lds {
+    SplitLds split;
+    struct {
+      float as[16][kRow];
+      float bs[16][kRow];
+    } tile;
+  };
+  __shared__ __align__(16) Lds lds;
   uint32_t b = blockIdx.x;
   if (b < d.blocks1) {
-    const uint32_t plane = d.nx1 * d.ny1, z = b / plane, r = b - z * plane;
-    product_tile<Tile, Threads, A1, B1>(g1, r % d.nx1, r / d.nx1, z, as, bs);
+    product_tile<16, 256, A1, B1>(g1, b % d.nx1, b / d.nx1, 0, lds.tile.as, lds.tile.bs);
   } else {
     b -= d.blocks1;
     const uint32_t plane = d.nx2 * d.ny2, z = b / plane, r = b - z * plane;
-    product_tile<Tile, Threads, A2, B2>(g2, r % d.nx2, r / d.nx2, z, as, bs);
+    split_tile<A2, B2>(g2, r % d.nx2, r / d.nx2, z, lds.split);
   }
 }
 
@@ -1113,7 +1177,7 @@ int tap_kernel(const ConvGeom &g) {
 // Plans of the LDS-staged per-image kernels: `tile` channels per block (0: not applicable).
 struct LdsPlan {
   uint32_t tile = 0, tiles = 0, chunks = 1, per_chunk = 0, lds_bytes = 0;
-  uint32_t groups = 1, threads = 256;  // weight gradient: position ranges, block size
+  uint32_t groups = 1, threads = 256;  // weight gradient position ranges; block size
 };
 
 bool lds_eligible(const ConvGeom &g) {
@@ -1122,7 +1186,8 @@ bool lds_eligible(const ConvGeom &g) {
 
 // `staged` floats per block plus `per` per tile channel (tiles of kLdsR-channel groups,
 // weights padded to a multiple of kLdsR), over `channels` channels of `plane` positions: about
-// one group per thread per block.
+// one group per thread per block, in blocks of as many 64-thread waves as their items fill (at
+// most 256 threads).  Every item is a serial sum, so the tiling never changes a result.
 LdsPlan channel_tiles(uint64_t staged, uint64_t per, uint64_t channels, uint64_t plane) {
   LdsPlan p;
   staged = (staged + 3) / 4 * 4;
@@ -1134,8 +1199,10 @@ LdsPlan channel_tiles(uint64_t staged, uint64_t per, uint64_t channels, uint64_t
   const uint64_t all = (channels + kLdsR - 1) / kLdsR * kLdsR;
   if (tile > all) tile = all;
   if (tile > fit) tile = fit;
+  const uint64_t items = tile / kLdsR * plane;
   p.tile = static_cast<uint32_t>(tile);
   p.tiles = static_cast<uint32_t>((channels + tile - 1) / tile);
+  p.threads = static_cast<uint32_t>(items >= 256 ? 256 : (items + 63) / 64 * 64);
   p.lds_bytes = static_cast<uint32_t>((staged + tile * per) * 4);
   return p;
 }
@@ -1205,27 +1272,6 @@ Operand operand(const float *ptr, Axis row, Axis k) {
 #define OXH_SINGLE_K 1024  // weight gradients with at most this many k terms: one pass, no chunks
 #endif
 
-// k chunks of the pointwise weight gradient: about 512 blocks in total, at least 64 k per
-// chunk, every chunk non-empty.
-struct KSplit {
-  uint32_t chunks, per;
-};
-KSplit product_split(const ConvGeom &g) {
-  const uint64_t tiles = static_cast<uint64_t>((g.out_c + kTile - 1) / kTile) *
-                         ((g.in_c + kTile - 1) / kTile);
-  const uint64_t k = static_cast<uint64_t>(g.batch) * g.h * g.w;
-  const uint64_t weights = static_cast<uint64_t>(g.out_c) * g.in_c;
-  if (k <= OXH_SINGLE_K) return KSplit{1, static_cast<uint32_t>(k)};
-  uint64_t c = (512 + tiles - 1) / tiles;
-  const uint64_t by_work = k / 64 > 0 ? k / 64 : 1;
-  if (c > by_work) c = by_work;
-  if (c > 1024) c = 1024;
-  while (c > 1 && c * weights >= kMaxElems) --c;
-  if (c < 1) c = 1;
-  const uint64_t per = (k + c - 1) / c;
-  return KSplit{static_cast<uint32_t>((k + per - 1) / per), static_cast<uint32_t>(per)};
-}
-
 #ifndef OXH_TINY_TILE
 #define OXH_TINY_TILE 8  // small-grid tiling: 8 (8 x 8, 64 threads) or 16 (16 x 16, 256)
 #endif
@@ -1233,6 +1279,43 @@ KSplit product_split(const ConvGeom &g) {
 #define OXH_SMALL_GRID 512  // below this many 32 x 32 blocks the small-grid tiling runs
 #endif
 constexpr uint64_t kSmallGrid = OXH_SMALL_GRID;
+
+// k chunks of the pointwise weight gradient.  Grids of >= kSmallGrid 32 x 32 tiles (with their
+// chunks: about 512 blocks, at least 64 k per chunk, when k > OXH_SINGLE_K) take the serial
+// 32 x 32 tiling (serial32); smaller ones the split tiles, chunked for about kSplitTarget waves
+// with at least 4 * 128 k per chunk.  Every chunk is non-empty.
+#ifndef OXH_SPLIT_TARGET
+#define OXH_SPLIT_TARGET 1024
+#endif
+struct KSplit {
+  uint32_t chunks, per;
+  bool serial32;
+};
+KSplit product_split(const ConvGeom &g) {
+  const uint64_t tiles = static_cast<uint64_t>((g.out_c + kTile - 1) / kTile) *
+                         ((g.in_c + kTile - 1) / kTile);
+  const uint64_t k = static_cast<uint64_t>(g.batch) * g.h * g.w;
+  const uint64_t weights = static_cast<uint64_t>(g.out_c) * g.in_c;
+  uint64_t c = 1;
+  if (k > OXH_SINGLE_K) {
+    c = (512 + tiles - 1) / tiles;
+    const uint64_t by_work = k / 64 > 0 ? k / 64 : 1;
+    if (c > by_work) c = by_work;
+    if (c > 1024) c = 1024;
+  }
+  bool serial32 = tiles * c >= kSmallGrid;
+  if (!serial32) {
+    const uint64_t tiles8 = static_cast<uint64_t>((g.out_c + 7) / 8) * ((g.in_c + 7) / 8);
+    c = (OXH_SPLIT_TARGET + tiles8 * kSplitWaves - 1) / (tiles8 * kSplitWaves);
+    const uint64_t by_work = k / (kSplitWaves * 128) > 0 ? k / (kSplitWaves * 128) : 1;
+    if (c > by_work) c = by_work;
+  }
+  while (c > 1 && c * weights >= kMaxElems) --c;
+  if (c < 1) c = 1;
+  const uint64_t per = (k + c - 1) / c;
+  return KSplit{static_cast<uint32_t>((k + per - 1) / per), static_cast<uint32_t>(per), serial32};
+}
+
 
 template <int Tile, int Threads>
 void launch_tiled(hipStream_t s, const ProductArgs &a, uint32_t chunks) {
@@ -1365,29 +1448,51 @@ uint64_t big_tiles(const ProductArgs &a, uint32_t chunks) {
   return static_cast<uint64_t>((a.N + kTile - 1) / kTile) * ((a.M + kTile - 1) / kTile) * chunks;
 }
 
+// The weight-gradient product: the serial 32 x 32 tiling or the split tiles (sums over
+// contiguous parts of each chunk, added in order), as product_split chose.
+template <bool A, bool B>
+void launch_split(hipStream_t s, const ProductArgs &a, uint32_t chunks) {
+  const dim3 grid((a.N + 7) / 8, (a.M + 7) / 8, chunks);
+  oxh::launch(pointwise_split_kernel<A, B>, grid, dim3(kSplitThreads), 0, s, a);
+}
+
+oxh_status launch_weight_product(const char *name, hipStream_t s, const ProductArgs &a,
+                                 const KSplit &split) {
+  const uint32_t chunks = split.chunks;
+  if (split.serial32) {
+    launch_tiled<kTile, 256>(s, a, chunks);
+  } else if (a.a.k_fast && a.b.k_fast) {
+    launch_split<true, true>(s, a, chunks);
+  } else if (a.a.k_fast) {
+    launch_split<true, false>(s, a, chunks);
+  } else if (a.b.k_fast) {
+    launch_split<false, true>(s, a, chunks);
+  } else {
+    launch_split<false, false>(s, a, chunks);
+  }
+  return oxh::launched(name);
+}
+
 // Both backward products of a pointwise convolution in one launch when together they stay
-// below the small-grid threshold (each alone would run the small-grid tiling) and their operand
-// layouts are the ones a convolution's planes give (plane > 1: weight gradient k-fast on both
-// operands, input gradient row-fast on both; plane 1: weight gradient row-fast, input gradient
-// k-fast on its second operand).  Every output is the same serial sum as in the separate
-// launches.  Returns false, launching nothing, otherwise.
-bool launch_dual(hipStream_t s, const ProductArgs &w, uint32_t w_chunks, const ProductArgs &x) {
-  constexpr int Tile = 8, Threads = 64;
-  if (OXH_TINY_TILE != Tile || big_tiles(w, w_chunks) + big_tiles(x, 1) >= kSmallGrid)
-    return false;
+// below the small-grid threshold (the weight gradient alone would take the split tiles) and
+// their operand layouts are the ones a convolution's planes give (plane > 1: weight gradient
+// k-fast on both operands, input gradient row-fast on both; plane 1: weight gradient row-fast,
+// input gradient k-fast on its second operand).  Every output is the same sum as in the
+// separate launches (the input gradient's serial sum does not depend on the tiling).  Returns
+// false, launching nothing, otherwise.
+bool launch_dual(hipStream_t s, const ProductArgs &w, const KSplit &split, const ProductArgs &x) {
+  if (split.serial32 || big_tiles(w, split.chunks) + big_tiles(x, 1) >= kSmallGrid) return false;
   DualGrid d;
-  d.nx1 = (w.N + Tile - 1) / Tile;
-  d.ny1 = (w.M + Tile - 1) / Tile;
-  d.blocks1 = d.nx1 * d.ny1 * w_chunks;
-  d.nx2 = (x.N + Tile - 1) / Tile;
-  d.ny2 = (x.M + Tile - 1) / Tile;
-  const dim3 grid(d.blocks1 + d.nx2 * d.ny2), block(Threads);
+  d.nx1 = (x.N + 15) / 16;
+  d.ny1 = (x.M + 15) / 16;
+  d.blocks1 = d.nx1 * d.ny1;
+  d.nx2 = (w.N + 7) / 8;
+  d.ny2 = (w.M + 7) / 8;
+  const dim3 grid(d.blocks1 + d.nx2 * d.ny2 * split.chunks), block(kSplitThreads);
   if (w.a.k_fast && w.b.k_fast && !x.a.k_fast && !x.b.k_fast)
-    oxh::launch(pointwise_dual_kernel<Tile, Threads, true, true, false, false>, grid, block, 0, s,
-                w, x, d);
+    oxh::launch(pointwise_dual_kernel<false, false, true, true>, grid, block, 0, s, x, w, d);
   else if (!w.a.k_fast && !w.b.k_fast && !x.a.k_fast && x.b.k_fast)
-    oxh::launch(pointwise_dual_kernel<Tile, Threads, false, false, false, true>, grid, block, 0,
-                s, w, x, d);
+    oxh::launch(pointwise_dual_kernel<false, true, false, false>, grid, block, 0, s, x, w, d);
   else
     return false;
   return true;
@@ -1408,7 +1513,7 @@ oxh_status input_backward_impl(const char *name, oxh_stream stream,
     return launch_product(name, s, input_product(g, gradient, weight, addend, input_gradient), 1);
   const LdsPlan lp = input_backward_lds_plan(g);
   if (lp.tile > 0) {
-    const dim3 lgrid(lp.tiles, g.batch), lblock(256);
+    const dim3 lgrid(lp.tiles, g.batch), lblock(lp.threads);
     const oxh::FastDiv pd = oxh::make_fastdiv(g.h * g.w);
     switch (tap_kernel(g)) {
       case 31: oxh::launch(conv2d_input_backward_lds_kernel<3, 1>, lgrid, lblock, lp.lds_bytes, s, g, lp.tile, pd, gradient, weight, addend, input_gradient); break;
@@ -1476,7 +1581,7 @@ oxh_status oxh_conv2d_forward(oxh_stream stream, const oxh_conv2d_shape *shape,
   }
   const LdsPlan lp = forward_lds_plan(g);
   if (lp.tile > 0) {
-    const dim3 lgrid(lp.tiles, g.batch), lblock(256);
+    const dim3 lgrid(lp.tiles, g.batch), lblock(lp.threads);
     const oxh::FastDiv od = oxh::make_fastdiv(g.oh * g.ow);
     const oxh::FastDiv rd = oxh::make_fastdiv(g.in_c * g.kh * g.kw);
     switch (tap_kernel(g)) {
@@ -1543,10 +1648,10 @@ oxh_status oxh_conv2d_weight_backward(oxh_stream stream, const oxh_conv2d_shape 
   hipStream_t s = oxh::as_stream(stream);
   if (pointwise(g)) {
     const KSplit split = product_split(g);
-    st = launch_product(
+    st = launch_weight_product(
         name, s,
         weight_product(g, split, gradient, input, split.chunks > 1 ? partial : weight_gradient),
-        split.chunks);
+        split);
     if (st != OXH_OK || split.chunks == 1) return st;
     const uint32_t count = g.out_c * g.in_c;
     oxh::launch(sum_chunks_kernel, dim3(grid_for(count)), dim3(256), 0, s, count, split.chunks,
@@ -1651,7 +1756,7 @@ oxh_status oxh_conv2d_backward(oxh_stream stream, const oxh_conv2d_shape *shape,
     const ProductArgs w =
         weight_product(g, split, gradient, input, split.chunks > 1 ? partial : weight_gradient);
     const ProductArgs x = input_product(g, gradient, weight, addend, input_gradient);
-    if (launch_dual(s, w, split.chunks, x)) {
+    if (launch_dual(s, w, split, x)) {
       st = oxh::launched(name);
       if (st != OXH_OK) return st;
       if (split.chunks > 1) {
