@@ -120,16 +120,18 @@ constexpr int kChannelKeep = 8;
 // Training forward of channel c from the values in registers: fp64 sums of (v - shift) and
 // (v - shift)^2 with shift = the channel's first value (x[0, c, 0]), the statistics (thread 0
 // writes the saved / running outputs), then y = relu?(BN(v)) (+ added[u] when `add`) at the
-// positions `at`.  The BatchNorm weight w, bias b and the addend values are passed in, loaded
-// by the caller together with the channel's values (a load issued after the sums' barrier
-// would put a second memory round trip on the block).
+// positions `at`, and to copy[j] (channel-relative j) when copy is not null.  The BatchNorm
+// weight w, bias b and the addend values are passed in, loaded by the caller together with the
+// channel's values (a load issued after the sums' barrier would put a second memory round trip
+// on the block).
 template <bool Relu, int Threads>
 __device__ __forceinline__ void channel_forward_kept(uint32_t samples, uint32_t c, float shift,
                                                      const float (&kept)[kChannelKeep],
                                                      const uint32_t (&at)[kChannelKeep], float w,
                                                      float b, const StatsOut &out, bool add,
                                                      const float (&added)[kChannelKeep], float *y,
-                                                     double (*lds)[Threads / 64]) {
+                                                     double (*lds)[Threads / 64],
+                                                     float *copy = nullptr) {
   const double k = static_cast<double>(shift);
   double sum = 0.0, sq = 0.0;
 #pragma unroll
@@ -148,7 +150,9 @@ __device__ __forceinline__ void channel_forward_kept(uint32_t samples, uint32_t 
     if (threadIdx.x + u * Threads < samples) {
       float v = (kept[u] - mu) * inv * w + b;  // evaluation.rs:590-595
       if constexpr (Relu) v = v > 0.0f ? v : 0.0f;
-      y[at[u]] = add ? v + added[u] : v;
+      if (add) v = v + added[u];
+      y[at[u]] = v;
+      if (copy != nullptr) copy[threadIdx.x + u * Threads] = v;
     }
 }
 

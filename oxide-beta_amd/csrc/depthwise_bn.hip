@@ -44,6 +44,32 @@ struct DwGeom {
   oxh::FastDiv plane_div, w_div, ow_div;
 };
 
+// The BatchNorm (ReLU when Pre == kPreBnRelu) in front of the depthwise convolution, fused into
+// its kernels when the convolution is its only consumer: a channel of the convolution's input
+// is a channel of that BatchNorm, so the same block owns both.
+constexpr int kPreNone = 0, kPreBn = 1, kPreBnRelu = 2;
+struct PreBnForward {
+  const float *input;          // the BatchNorm's input [N, C, H, W]
+  const float *weight, *bias;  // its affine parameters
+  StatsOut stats;              // its saved and running statistics
+  float *output;               // its output: the convolution's input, stored
+};
+struct PreBnBackward {
+  const float *input;             // the BatchNorm's input, for x_hat
+  const float *weight;            // gamma
+  const float *mean, *inverse_std;  // saved statistics
+  float *dweight, *dbias;         // its affine gradients
+  float *input_gradient;          // its dx: the gradient of the layer feeding it
+  float *input_sum;               // per-channel sum of input_gradient (the feeding
+                                  // convolution's bias gradient), or null
+};
+
+// Channel-relative value j of the convolution's input channel c: (n, p) = (j / plane, j % plane).
+__device__ __forceinline__ uint32_t input_index(const DwGeom &g, uint32_t c, uint32_t j) {
+  const uint32_t plane = g.h * g.w, n = oxh::fast_div(j, g.plane_div);
+  return (n * g.out.channels + c) * plane + (j - n * plane);
+}
+
 // LDS copy of input channel c: xs[n * h * w + p] = x[n, c, p], kStageUnroll loads in flight
 // per thread (addresses clamped into the channel, stores guarded).
 __device__ __forceinline__ void stage_channel(const DwGeom &g, uint32_t c,
@@ -66,17 +92,36 @@ __device__ __forceinline__ void stage_channel(const DwGeom &g, uint32_t c,
   }
 }
 
-template <int K, int S, bool Relu>
+template <int K, int S, bool Relu, int Pre>
 __global__ __launch_bounds__(kDwThreads) void dw_bn_forward_kernel(
     DwGeom g, const float *__restrict__ x, const float *__restrict__ conv_weight,
     const float *__restrict__ conv_bias, float *__restrict__ conv_out,
     const float *__restrict__ bn_weight, const float *__restrict__ bn_bias, StatsOut stats,
-    float *__restrict__ y) {
+    float *__restrict__ y, PreBnForward pre) {
   __shared__ float xs[kDwMaxIn];
   __shared__ double lds[2][kDwThreads / 64];
   __shared__ float shift;
   const uint32_t c = blockIdx.x;
-  stage_channel(g, c, x, xs);
+  if constexpr (Pre != kPreNone) {
+    // the BatchNorm (relu) in front over input channel c (at most kDwThreads * kChannelKeep
+    // values), exactly as its channel kernel forms it; its output goes to LDS for the taps
+    float kin[kChannelKeep];
+    uint32_t ain[kChannelKeep];
+#pragma unroll
+    for (int u = 0; u < kChannelKeep; ++u) {
+      const uint32_t j = threadIdx.x + u * kDwThreads;
+      ain[u] = j < g.in_samples ? input_index(g, c, j) : 0;
+      kin[u] = pre.input[ain[u]];
+    }
+    const float pshift = pre.input[input_index(g, c, 0)];
+    const float none[kChannelKeep] = {};
+    oxh::channel_forward_kept<Pre == kPreBnRelu, kDwThreads>(g.in_samples, c, pshift, kin, ain,
+                                                             pre.weight[c], pre.bias[c],
+                                                             pre.stats, false, none, pre.output,
+                                                             lds, xs);
+  } else {
+    stage_channel(g, c, x, xs);
+  }
   float wv[K * K];
 #pragma unroll
   for (int t = 0; t < K * K; ++t) wv[t] = conv_weight[c * (K * K) + t];
@@ -121,23 +166,40 @@ __global__ __launch_bounds__(kDwThreads) void dw_bn_forward_kernel(
                                               none, y, lds);
 }
 
-template <int K, int S, bool Relu>
+template <int K, int S, bool Relu, int Pre>
 __global__ __launch_bounds__(kDwThreads) void dw_bn_backward_kernel(
     DwGeom g, const float *__restrict__ grad, const float *__restrict__ relu_out,
     const float *__restrict__ conv_out, const float *__restrict__ bn_weight,
     const float *__restrict__ mean, const float *__restrict__ inverse_std,
     const float *__restrict__ x, const float *__restrict__ conv_weight, const float *addend,
     float *__restrict__ conv_grad, float *__restrict__ bn_dweight, float *__restrict__ bn_dbias,
-    float *__restrict__ conv_dbias, float *__restrict__ conv_dweight, float *dx) {
+    float *__restrict__ conv_dbias, float *__restrict__ conv_dweight, float *dx,
+    PreBnBackward pre) {
   constexpr int kTaps = K * K, kWaves = kDwThreads / 64;
   __shared__ float xs[kDwMaxIn];
   __shared__ float gs[kDwMaxOut];
   __shared__ float wts[kTaps];
   __shared__ double lds[2][2][kWaves];
+  __shared__ double lds_pre[2][2][kWaves];
   __shared__ float wave_sums[kWaves][kTaps];
   const uint32_t c = blockIdx.x;
   const uint32_t oplane = g.oh * g.ow, plane = g.h * g.w, samples = g.out.samples;
   const float mu = mean[c], inv = inverse_std[c];
+  // the BatchNorm in front: its input values (x_hat) and statistics, loaded with the rest
+  float pin[kChannelKeep];
+  uint32_t pat[kChannelKeep];
+  float pmu = 0.0f, pinv = 0.0f, pw = 0.0f;
+  if constexpr (Pre != kPreNone) {
+#pragma unroll
+    for (int u = 0; u < kChannelKeep; ++u) {
+      const uint32_t j = threadIdx.x + u * kDwThreads;
+      pat[u] = j < g.in_samples ? input_index(g, c, j) : 0;
+      pin[u] = pre.input[pat[u]];
+    }
+    pmu = pre.mean[c];
+    pinv = pre.inverse_std[c];
+    pw = pre.weight[c];
+  }
   // BatchNorm (relu) backward from registers
   float kg[kChannelKeep], kn[kChannelKeep], d[kChannelKeep];
   uint32_t at[kChannelKeep];
@@ -198,33 +260,62 @@ __global__ __launch_bounds__(kDwThreads) void dw_bn_backward_kernel(
   }
 
   // input gradient: input (iy, ix) feeds outputs oy = floor(ty / S) - (M - 1) + j, j < M
-  if (dx != nullptr) {
+  auto input_sum = [&](uint32_t i) {
     constexpr int M = (K + S - 1) / S;
+    const uint32_t n = oxh::fast_div(i, g.plane_div), r = i - n * plane;
+    const uint32_t iy = oxh::fast_div(r, g.w_div), ix = r - iy * g.w;
+    const int ty = static_cast<int>(iy + g.pad), tx = static_cast<int>(ix + g.pad);
+    int grow[M], gcol[M], wrow[M], wcol[M];
+    bool vy[M], vx[M];
+#pragma unroll
+    for (int j = 0; j < M; ++j) {
+      const int oy = ty / S - (M - 1) + j, ox = tx / S - (M - 1) + j;
+      const int ky = ty - oy * S, kx = tx - ox * S;
+      vy[j] = oy >= 0 && oy < static_cast<int>(g.oh) && ky < K;
+      vx[j] = ox >= 0 && ox < static_cast<int>(g.ow) && kx < K;
+      grow[j] = vy[j] ? oy * static_cast<int>(g.ow) : 0;
+      gcol[j] = vx[j] ? ox : 0;
+      wrow[j] = vy[j] ? ky * K : 0;
+      wcol[j] = vx[j] ? kx : 0;
+    }
+    const float *gp = gs + n * oplane;
+    float a = 0.0f;
+#pragma unroll
+    for (int t = 0; t < M * M; ++t) {
+      const float p = gp[grow[t / M] + gcol[t % M]] * wts[wrow[t / M] + wcol[t % M]];
+      a += tap_term(p, tap_mask(vy[t / M] && vx[t % M]));
+    }
+    return a;
+  };
+  if constexpr (Pre != kPreNone) {
+    // the BatchNorm (relu) in front, backward over its channel from the input gradient just
+    // formed (its relu output is the staged convolution input), exactly as its channel
+    // backward forms it; its dx sum is the feeding convolution's bias gradient
+    float kg[kChannelKeep], kn[kChannelKeep], d[kChannelKeep];
+#pragma unroll
+    for (int u = 0; u < kChannelKeep; ++u) {
+      const uint32_t i = threadIdx.x + u * kDwThreads;
+      if (i >= g.in_samples) break;
+      const float a = input_sum(i);
+      kg[u] = Pre == kPreBnRelu ? oxh::relu_masked(a, xs[i]) : a;
+      kn[u] = (pin[u] - pmu) * pinv;
+    }
+    oxh::channel_backward_kept<kDwThreads>(g.in_samples, kg, kn, pw, pinv, pre.dweight + c,
+                                           pre.dbias + c, d, lds_pre[0]);
+    double ptotal = 0.0, punused = 0.0;
+#pragma unroll
+    for (int u = 0; u < kChannelKeep; ++u) {
+      const uint32_t i = threadIdx.x + u * kDwThreads;
+      if (i >= g.in_samples) break;
+      pre.input_gradient[pat[u]] = d[u];
+      ptotal += static_cast<double>(d[u]);
+    }
+    oxh::block_sum2_all<kWaves>(ptotal, punused, lds_pre[1]);
+    if (threadIdx.x == 0 && pre.input_sum != nullptr) pre.input_sum[c] = static_cast<float>(ptotal);
+  } else if (dx != nullptr) {
     for (uint32_t i = threadIdx.x; i < g.in_samples; i += kDwThreads) {
-      const uint32_t n = oxh::fast_div(i, g.plane_div), r = i - n * plane;
-      const uint32_t iy = oxh::fast_div(r, g.w_div), ix = r - iy * g.w;
-      const int ty = static_cast<int>(iy + g.pad), tx = static_cast<int>(ix + g.pad);
-      int grow[M], gcol[M], wrow[M], wcol[M];
-      bool vy[M], vx[M];
-#pragma unroll
-      for (int j = 0; j < M; ++j) {
-        const int oy = ty / S - (M - 1) + j, ox = tx / S - (M - 1) + j;
-        const int ky = ty - oy * S, kx = tx - ox * S;
-        vy[j] = oy >= 0 && oy < static_cast<int>(g.oh) && ky < K;
-        vx[j] = ox >= 0 && ox < static_cast<int>(g.ow) && kx < K;
-        grow[j] = vy[j] ? oy * static_cast<int>(g.ow) : 0;
-        gcol[j] = vx[j] ? ox : 0;
-        wrow[j] = vy[j] ? ky * K : 0;
-        wcol[j] = vx[j] ? kx : 0;
-      }
-      const float *gp = gs + n * oplane;
-      float a = 0.0f;
-#pragma unroll
-      for (int t = 0; t < M * M; ++t) {
-        const float p = gp[grow[t / M] + gcol[t % M]] * wts[wrow[t / M] + wcol[t % M]];
-        a += tap_term(p, tap_mask(vy[t / M] && vx[t % M]));
-      }
-      const uint32_t idx = (n * g.out.channels + c) * plane + r;
+      const float a = input_sum(i);
+      const uint32_t idx = input_index(g, c, i);
       dx[idx] = addend != nullptr ? a + addend[idx] : a;
     }
   }
@@ -272,30 +363,65 @@ bool make_dw_geom(const oxh_conv2d_shape *s, DwGeom &g) {
 
 int variant(const oxh_conv2d_shape *s) { return static_cast<int>(10 * s->kernel_h + s->stride); }
 
-template <bool Relu>
-void launch_forward(int v, hipStream_t st, uint32_t channels, const DwGeom &g, const float *x,
-                    const float *cw, const float *cb, float *co, const float *bw,
-                    const float *bb, const StatsOut &so, float *y) {
-  const dim3 grid(channels), block(kDwThreads);
-  switch (v) {
-    case 31: oxh::launch(dw_bn_forward_kernel<3, 1, Relu>, grid, block, 0, st, g, x, cw, cb, co, bw, bb, so, y); break;
-    case 32: oxh::launch(dw_bn_forward_kernel<3, 2, Relu>, grid, block, 0, st, g, x, cw, cb, co, bw, bb, so, y); break;
-    case 51: oxh::launch(dw_bn_forward_kernel<5, 1, Relu>, grid, block, 0, st, g, x, cw, cb, co, bw, bb, so, y); break;
-    default: oxh::launch(dw_bn_forward_kernel<5, 2, Relu>, grid, block, 0, st, g, x, cw, cb, co, bw, bb, so, y);
-  }
+// The fused BatchNorm in front keeps its channel in registers: at most kDwThreads *
+// kChannelKeep values, at least 2 (the unbiased running variance).
+bool pre_eligible(const DwGeom &g) {
+  return g.in_samples >= 2 && g.in_samples <= static_cast<uint32_t>(kDwThreads * kChannelKeep);
+}
+
+template <int K, int S, bool Relu>
+void launch_forward_pre(int pre_kind, hipStream_t st, const dim3 grid, const DwGeom &g,
+                        const float *x, const float *cw, const float *cb, float *co,
+                        const float *bw, const float *bb, const StatsOut &so, float *y,
+                        const PreBnForward &pre) {
+  const dim3 block(kDwThreads);
+  if (pre_kind == kPreBnRelu)
+    oxh::launch(dw_bn_forward_kernel<K, S, Relu, kPreBnRelu>, grid, block, 0, st, g, x, cw, cb, co, bw, bb, so, y, pre);
+  else if (pre_kind == kPreBn)
+    oxh::launch(dw_bn_forward_kernel<K, S, Relu, kPreBn>, grid, block, 0, st, g, x, cw, cb, co, bw, bb, so, y, pre);
+  else
+    oxh::launch(dw_bn_forward_kernel<K, S, Relu, kPreNone>, grid, block, 0, st, g, x, cw, cb, co, bw, bb, so, y, pre);
 }
 
 template <bool Relu>
-void launch_backward(int v, hipStream_t st, uint32_t channels, const DwGeom &g, const float *gr,
-                     const float *ro, const float *co, const float *bw, const float *sm,
-                     const float *si, const float *x, const float *cw, const float *ad,
-                     float *cg, float *dbw, float *dbb, float *dcb, float *dcw, float *dx) {
-  const dim3 grid(channels), block(kDwThreads);
+void launch_forward(int v, int pre_kind, hipStream_t st, uint32_t channels, const DwGeom &g,
+                    const float *x, const float *cw, const float *cb, float *co, const float *bw,
+                    const float *bb, const StatsOut &so, float *y, const PreBnForward &pre) {
+  const dim3 grid(channels);
   switch (v) {
-    case 31: oxh::launch(dw_bn_backward_kernel<3, 1, Relu>, grid, block, 0, st, g, gr, ro, co, bw, sm, si, x, cw, ad, cg, dbw, dbb, dcb, dcw, dx); break;
-    case 32: oxh::launch(dw_bn_backward_kernel<3, 2, Relu>, grid, block, 0, st, g, gr, ro, co, bw, sm, si, x, cw, ad, cg, dbw, dbb, dcb, dcw, dx); break;
-    case 51: oxh::launch(dw_bn_backward_kernel<5, 1, Relu>, grid, block, 0, st, g, gr, ro, co, bw, sm, si, x, cw, ad, cg, dbw, dbb, dcb, dcw, dx); break;
-    default: oxh::launch(dw_bn_backward_kernel<5, 2, Relu>, grid, block, 0, st, g, gr, ro, co, bw, sm, si, x, cw, ad, cg, dbw, dbb, dcb, dcw, dx);
+    case 31: launch_forward_pre<3, 1, Relu>(pre_kind, st, grid, g, x, cw, cb, co, bw, bb, so, y, pre); break;
+    case 32: launch_forward_pre<3, 2, Relu>(pre_kind, st, grid, g, x, cw, cb, co, bw, bb, so, y, pre); break;
+    case 51: launch_forward_pre<5, 1, Relu>(pre_kind, st, grid, g, x, cw, cb, co, bw, bb, so, y, pre); break;
+    default: launch_forward_pre<5, 2, Relu>(pre_kind, st, grid, g, x, cw, cb, co, bw, bb, so, y, pre);
+  }
+}
+
+struct BackwardArgs {
+  const float *gr, *ro, *co, *bw, *sm, *si, *x, *cw, *ad;
+  float *cg, *dbw, *dbb, *dcb, *dcw, *dx;
+};
+
+template <int K, int S, bool Relu>
+void launch_backward_pre(int pre_kind, hipStream_t st, const dim3 grid, const DwGeom &g,
+                         const BackwardArgs &a, const PreBnBackward &pre) {
+  const dim3 block(kDwThreads);
+  if (pre_kind == kPreBnRelu)
+    oxh::launch(dw_bn_backward_kernel<K, S, Relu, kPreBnRelu>, grid, block, 0, st, g, a.gr, a.ro, a.co, a.bw, a.sm, a.si, a.x, a.cw, a.ad, a.cg, a.dbw, a.dbb, a.dcb, a.dcw, a.dx, pre);
+  else if (pre_kind == kPreBn)
+    oxh::launch(dw_bn_backward_kernel<K, S, Relu, kPreBn>, grid, block, 0, st, g, a.gr, a.ro, a.co, a.bw, a.sm, a.si, a.x, a.cw, a.ad, a.cg, a.dbw, a.dbb, a.dcb, a.dcw, a.dx, pre);
+  else
+    oxh::launch(dw_bn_backward_kernel<K, S, Relu, kPreNone>, grid, block, 0, st, g, a.gr, a.ro, a.co, a.bw, a.sm, a.si, a.x, a.cw, a.ad, a.cg, a.dbw, a.dbb, a.dcb, a.dcw, a.dx, pre);
+}
+
+template <bool Relu>
+void launch_backward(int v, int pre_kind, hipStream_t st, uint32_t channels, const DwGeom &g,
+                     const BackwardArgs &a, const PreBnBackward &pre) {
+  const dim3 grid(channels);
+  switch (v) {
+    case 31: launch_backward_pre<3, 1, Relu>(pre_kind, st, grid, g, a, pre); break;
+    case 32: launch_backward_pre<3, 2, Relu>(pre_kind, st, grid, g, a, pre); break;
+    case 51: launch_backward_pre<5, 1, Relu>(pre_kind, st, grid, g, a, pre); break;
+    default: launch_backward_pre<5, 2, Relu>(pre_kind, st, grid, g, a, pre);
   }
 }
 
@@ -330,12 +456,13 @@ oxh_status oxh_depthwise_conv_batch_norm_forward_train(
   const StatsOut so{saved_mean, saved_inverse_std, nullptr, running_mean, running_variance,
                     momentum, epsilon};
   hipStream_t st = oxh::as_stream(stream);
+  const PreBnForward none{};
   if (relu)
-    launch_forward<true>(variant(shape), st, g.out.channels, g, input, conv_weight, conv_bias,
-                         conv_output, bn_weight, bn_bias, so, output);
+    launch_forward<true>(variant(shape), kPreNone, st, g.out.channels, g, input, conv_weight,
+                         conv_bias, conv_output, bn_weight, bn_bias, so, output, none);
   else
-    launch_forward<false>(variant(shape), st, g.out.channels, g, input, conv_weight, conv_bias,
-                          conv_output, bn_weight, bn_bias, so, output);
+    launch_forward<false>(variant(shape), kPreNone, st, g.out.channels, g, input, conv_weight,
+                          conv_bias, conv_output, bn_weight, bn_bias, so, output, none);
   return oxh::launched(name);
 }
 
@@ -387,18 +514,121 @@ oxh_status oxh_depthwise_conv_batch_norm_backward_train(
                   OXH_INVALID_SHAPE,
                   std::string(name) + ": conv_output_gradient overlaps another tensor");
   hipStream_t st = oxh::as_stream(stream);
+  const BackwardArgs a{gradient, relu_output, conv_output, bn_weight, saved_mean,
+                       saved_inverse_std, input, conv_weight, addend, conv_output_gradient,
+                       bn_weight_gradient, bn_bias_gradient, conv_bias_gradient,
+                       conv_weight_gradient, input_gradient};
+  const PreBnBackward none{};
   if (relu_output)
-    launch_backward<true>(variant(shape), st, g.out.channels, g, gradient, relu_output,
-                          conv_output, bn_weight, saved_mean, saved_inverse_std, input,
-                          conv_weight, addend, conv_output_gradient, bn_weight_gradient,
-                          bn_bias_gradient, conv_bias_gradient, conv_weight_gradient,
-                          input_gradient);
+    launch_backward<true>(variant(shape), kPreNone, st, g.out.channels, g, a, none);
   else
-    launch_backward<false>(variant(shape), st, g.out.channels, g, gradient, relu_output,
-                           conv_output, bn_weight, saved_mean, saved_inverse_std, input,
-                           conv_weight, addend, conv_output_gradient, bn_weight_gradient,
-                           bn_bias_gradient, conv_bias_gradient, conv_weight_gradient,
-                           input_gradient);
+    launch_backward<false>(variant(shape), kPreNone, st, g.out.channels, g, a, none);
+  return oxh::launched(name);
+}
+
+int oxh_batch_norm_depthwise_conv_batch_norm_supported(const oxh_conv2d_shape *shape) {
+  DwGeom g;
+  return make_dw_geom(shape, g) && pre_eligible(g) ? 1 : 0;
+}
+
+oxh_status oxh_batch_norm_depthwise_conv_batch_norm_forward_train(
+    oxh_stream stream, const oxh_conv2d_shape *shape, int pre_relu, float pre_momentum,
+    float pre_epsilon, const float *pre_input, const float *pre_weight, const float *pre_bias,
+    float *pre_running_mean, float *pre_running_variance, float *pre_saved_mean,
+    float *pre_saved_inverse_std, float *pre_output, int relu, float momentum, float epsilon,
+    const float *conv_weight, const float *conv_bias, float *conv_output,
+    const float *bn_weight, const float *bn_bias, float *running_mean, float *running_variance,
+    float *saved_mean, float *saved_inverse_std, float *output) {
+  const char *name = "oxh_batch_norm_depthwise_conv_batch_norm_forward_train";
+  DwGeom g;
+  OXH_REQUIRE(make_dw_geom(shape, g) && pre_eligible(g), OXH_INVALID_SHAPE,
+              std::string(name) + ": not a supported shape "
+                                  "(oxh_batch_norm_depthwise_conv_batch_norm_supported)");
+  OXH_REQUIRE(pre_input && pre_weight && pre_bias && pre_running_mean && pre_running_variance &&
+                  pre_saved_mean && pre_saved_inverse_std && pre_output && conv_weight &&
+                  conv_bias && conv_output && bn_weight && bn_bias && running_mean &&
+                  running_variance && saved_mean && saved_inverse_std && output,
+              OXH_INVALID_SHAPE, std::string(name) + ": null pointer");
+  const uint64_t c = g.out.channels;
+  const uint64_t in_bytes = c * g.in_samples * 4, out_bytes = c * g.out.samples * 4;
+  OXH_REQUIRE(!oxh::any_overlap(pre_output, in_bytes, pre_input, in_bytes) &&
+                  !oxh::any_overlap(conv_output, out_bytes, pre_input, in_bytes) &&
+                  !oxh::any_overlap(conv_output, out_bytes, pre_output, in_bytes) &&
+                  !oxh::any_overlap(output, out_bytes, pre_input, in_bytes) &&
+                  !oxh::any_overlap(output, out_bytes, pre_output, in_bytes) &&
+                  !oxh::any_overlap(output, out_bytes, conv_output, out_bytes),
+              OXH_INVALID_SHAPE, std::string(name) + ": outputs overlap an input or each other");
+  const StatsOut so{saved_mean, saved_inverse_std, nullptr, running_mean, running_variance,
+                    momentum, epsilon};
+  const PreBnForward pre{pre_input, pre_weight, pre_bias,
+                         StatsOut{pre_saved_mean, pre_saved_inverse_std, nullptr,
+                                  pre_running_mean, pre_running_variance, pre_momentum,
+                                  pre_epsilon},
+                         pre_output};
+  const int kind = pre_relu ? kPreBnRelu : kPreBn;
+  hipStream_t st = oxh::as_stream(stream);
+  if (relu)
+    launch_forward<true>(variant(shape), kind, st, g.out.channels, g, pre_output, conv_weight,
+                         conv_bias, conv_output, bn_weight, bn_bias, so, output, pre);
+  else
+    launch_forward<false>(variant(shape), kind, st, g.out.channels, g, pre_output, conv_weight,
+                          conv_bias, conv_output, bn_weight, bn_bias, so, output, pre);
+  return oxh::launched(name);
+}
+
+oxh_status oxh_batch_norm_depthwise_conv_batch_norm_backward_train(
+    oxh_stream stream, const oxh_conv2d_shape *shape, const float *gradient,
+    const float *relu_output, const float *conv_output, const float *bn_weight,
+    const float *saved_mean, const float *saved_inverse_std, const float *conv_input,
+    const float *conv_weight, int pre_relu, const float *pre_input, const float *pre_weight,
+    const float *pre_saved_mean, const float *pre_saved_inverse_std,
+    float *conv_output_gradient, float *bn_weight_gradient, float *bn_bias_gradient,
+    float *conv_bias_gradient, float *conv_weight_gradient, float *pre_weight_gradient,
+    float *pre_bias_gradient, float *pre_input_gradient, float *pre_input_gradient_sum) {
+  const char *name = "oxh_batch_norm_depthwise_conv_batch_norm_backward_train";
+  DwGeom g;
+  OXH_REQUIRE(make_dw_geom(shape, g) && pre_eligible(g), OXH_INVALID_SHAPE,
+              std::string(name) + ": not a supported shape "
+                                  "(oxh_batch_norm_depthwise_conv_batch_norm_supported)");
+  OXH_REQUIRE(gradient && conv_output && bn_weight && saved_mean && saved_inverse_std &&
+                  conv_input && conv_weight && pre_input && pre_weight && pre_saved_mean &&
+                  pre_saved_inverse_std && bn_weight_gradient && bn_bias_gradient &&
+                  conv_bias_gradient && conv_weight_gradient && pre_weight_gradient &&
+                  pre_bias_gradient && pre_input_gradient,
+              OXH_INVALID_SHAPE, std::string(name) + ": null pointer");
+  const uint64_t c = g.out.channels;
+  const uint64_t in_bytes = c * g.in_samples * 4, out_bytes = c * g.out.samples * 4;
+  // every block reads its own channel of the inputs while others write theirs: the gradients
+  // overlap none of them
+  for (const void *p : {static_cast<const void *>(gradient), static_cast<const void *>(relu_output),
+                        static_cast<const void *>(conv_output)}) {
+    OXH_REQUIRE(p == nullptr || (!oxh::any_overlap(pre_input_gradient, in_bytes, p, out_bytes) &&
+                                 (conv_output_gradient == nullptr ||
+                                  !oxh::any_overlap(conv_output_gradient, out_bytes, p, out_bytes))),
+                OXH_INVALID_SHAPE, std::string(name) + ": a gradient overlaps an input");
+  }
+  for (const void *p : {static_cast<const void *>(conv_input), static_cast<const void *>(pre_input)}) {
+    OXH_REQUIRE(!oxh::any_overlap(pre_input_gradient, in_bytes, p, in_bytes) &&
+                    (conv_output_gradient == nullptr ||
+                     !oxh::any_overlap(conv_output_gradient, out_bytes, p, in_bytes)),
+                OXH_INVALID_SHAPE, std::string(name) + ": a gradient overlaps an input");
+  }
+  OXH_REQUIRE(conv_output_gradient == nullptr ||
+                  !oxh::any_overlap(conv_output_gradient, out_bytes, pre_input_gradient, in_bytes),
+              OXH_INVALID_SHAPE, std::string(name) + ": the gradients overlap");
+  hipStream_t st = oxh::as_stream(stream);
+  const BackwardArgs a{gradient, relu_output, conv_output, bn_weight, saved_mean,
+                       saved_inverse_std, conv_input, conv_weight, nullptr,
+                       conv_output_gradient, bn_weight_gradient, bn_bias_gradient,
+                       conv_bias_gradient, conv_weight_gradient, nullptr};
+  const PreBnBackward pre{pre_input, pre_weight, pre_saved_mean, pre_saved_inverse_std,
+                          pre_weight_gradient, pre_bias_gradient, pre_input_gradient,
+                          pre_input_gradient_sum};
+  const int kind = pre_relu ? kPreBnRelu : kPreBn;
+  if (relu_output)
+    launch_backward<true>(variant(shape), kind, st, g.out.channels, g, a, pre);
+  else
+    launch_backward<false>(variant(shape), kind, st, g.out.channels, g, a, pre);
   return oxh::launched(name);
 }
 

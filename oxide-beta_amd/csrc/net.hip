@@ -604,6 +604,28 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
     dw_conv[i] = 1;
     dw_conv_of[j] = static_cast<int64_t>(i);
   }
+  // a training BatchNorm (+ ReLU) whose only consumer is such a fused depthwise convolution,
+  // on planes of at most 2048 values per channel: it runs inside that layer's launches (its
+  // statistics, output and backward per channel, in the same workgroup as the layer's channel);
+  // in either pass nothing reads its output or writes its inputs in between
+  std::vector<int64_t> pre_bn_of(n, -1);  // fused depthwise convolution -> BN in front
+  std::vector<char> pre_fused(n, 0);      // that BN and its ReLU: no launch of their own
+  for (size_t i = 0; i < n; ++i) {
+    if (!dw_conv[i]) continue;
+    const int cin = g.nodes[i].in[0];
+    int b1 = -1;
+    if (fused_relu[cin] && consumers[cin] == 1)
+      b1 = g.nodes[cin].in[0];
+    else if (train_bn(cin) && !fused_bn[cin] && bn_into_add[cin] < 0 && dw_conv_of[cin] < 0 &&
+             consumers[cin] == 1)
+      b1 = cin;
+    if (b1 < 0 || dw_conv_of[b1] >= 0) continue;
+    const oxh_conv2d_shape s = conv_shape(g, g.nodes[i]);
+    if (!oxh_batch_norm_depthwise_conv_batch_norm_supported(&s)) continue;
+    pre_bn_of[i] = b1;
+    pre_fused[b1] = 1;
+    pre_fused[cin] = 1;
+  }
   // gradient buffers, consumers before producers
   std::vector<int64_t> grad_of(n, -1);  // node whose grad buffer this node uses (-1: own)
   std::vector<char> has_grad(n, 0);
@@ -613,7 +635,7 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
       g.nodes[root].op == Op::CrossEntropy && want(g.nodes[root].in[0]);
   for (size_t r = n; r-- > 0;) {
     const Node &x = g.nodes[r];
-    if (!want(static_cast<int>(r)) || fused_bn[r]) continue;
+    if (!want(static_cast<int>(r)) || fused_bn[r] || pre_fused[r]) continue;
     if (static_cast<int>(r) == root && root_fused_ce) continue;  // its outer gradient is 1
     if (x.op == Op::Param) continue;  // its gradient buffer is the optimizer's
     has_grad[r] = 1;
@@ -683,7 +705,7 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
   // A gradient a launch forms beside its main contribution (a convolution's or BatchNorm's
   // parameters) whose node already holds a contribution (a value feeding several layers) goes
   // to one of kSideSlots side buffers and is added into the node's gradient after the launch.
-  constexpr size_t kSideSlots = 5;
+  constexpr size_t kSideSlots = 8;
   bool sides = false;
   for (size_t i = 0; i < n; ++i) {
     const Node &x = g.nodes[i];
@@ -866,7 +888,7 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
   for (size_t i = 0; i < n; ++i) {
     const Node &x = g.nodes[i];
     if (!active[i] || x.leaf() || x.op == Op::Reshape || fused_bn[i] || add_absorbed[i] ||
-        dw_conv[i])
+        dw_conv[i] || pre_fused[i])
       continue;
     float *out = p.value[i];
     OpRec op;
@@ -938,6 +960,41 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
           op.attrs = conv_attrs(cv);
           op.attrs.push_back({"momentum", mom});
           op.attrs.push_back({"epsilon", eps});
+          if (pre_bn_of[ci] >= 0) {  // the BN (+ ReLU) in front, inside the same launch
+            const int b1 = static_cast<int>(pre_bn_of[ci]);
+            const Node &pb = g.nodes[b1];
+            const bool prelu = cv.in[0] != b1;
+            const float *px = p.value[pb.in[0]], *pw = p.value[pb.in[1]],
+                        *pbb = p.value[pb.in[2]];
+            float *psm = p.saved_mean[b1], *psi = p.saved_inv[b1];
+            float *prm = pb.running_mean, *prv = pb.running_variance;
+            float *py = const_cast<float *>(cx);
+            const float pmom = pb.momentum, peps = pb.epsilon;
+            const uint64_t PC = pb.shape[1];
+            op.kind = std::string(prelu ? "batch_norm2d_relu_" : "batch_norm2d_") +
+                      (fused ? "depthwise_conv2d_batch_norm_relu_forward"
+                             : "depthwise_conv2d_batch_norm_forward");
+            op.name = (prelu ? name("bn", b1) + "+" + name("relu", cv.in[0]) : name("bn", b1)) +
+                      "+" + op.name;
+            op.tensors.erase(op.tensors.begin());  // the layer's input is pre_y, written here
+            op.tensors.push_back(ref("pre_x", const_cast<float *>(px), g.nodes[pb.in[0]], 0));
+            op.tensors.push_back(ref("pre_weight", const_cast<float *>(pw), g.nodes[pb.in[1]], 0));
+            op.tensors.push_back(ref("pre_bias", const_cast<float *>(pbb), g.nodes[pb.in[2]], 0));
+            op.tensors.push_back(ref("pre_y", py, g.nodes[cv.in[0]], 1));
+            op.tensors.push_back(ref_flat("pre_saved_mean", psm, PC, 1));
+            op.tensors.push_back(ref_flat("pre_saved_inverse_std", psi, PC, 1));
+            op.tensors.push_back(ref_flat("pre_running_mean", prm, PC, 2));
+            op.tensors.push_back(ref_flat("pre_running_variance", prv, PC, 2));
+            op.attrs.push_back({"pre_momentum", pmom});
+            op.attrs.push_back({"pre_epsilon", peps});
+            op.launch = [=](hipStream_t st) {
+              return oxh_batch_norm_depthwise_conv_batch_norm_forward_train(
+                  st, &s, prelu ? 1 : 0, pmom, peps, px, pw, pbb, prm, prv, psm, psi, py,
+                  fused ? 1 : 0, mom, eps, cw, cb, cy, w, b, rm, rv, sm, si, out);
+            };
+            ops.push_back(std::move(op));
+            break;
+          }
           op.launch = [=](hipStream_t st) {
             return oxh_depthwise_conv_batch_norm_forward_train(st, &s, fused ? 1 : 0, mom, eps,
                                                                cx, cw, cb, cy, w, b, rm, rv, sm,
@@ -1019,7 +1076,7 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
   // backward, reverse topological order
   for (size_t r = n; r-- > 0;) {
     const Node &x = g.nodes[r];
-    if (!want(static_cast<int>(r)) || x.leaf() || fused_bn[r]) continue;
+    if (!want(static_cast<int>(r)) || x.leaf() || fused_bn[r] || pre_fused[r]) continue;
     if (x.op == Op::CrossEntropy && static_cast<int>(r) == root && root_fused_ce) continue;
     flush(static_cast<int>(r));  // a gradient still waiting for a second contribution
     OXH_REQUIRE(written[r], OXH_TRACE, "a traced value receives no gradient");
@@ -1139,6 +1196,62 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
           side(cv.in[1], cdw, "conv_weight_gradient");
           const oxh_conv2d_shape s = conv_shape(g, cv);
           const float *cx = p.value[cin], *cw = p.value[cv.in[1]];
+          if (pre_bn_of[xin] >= 0) {  // with the BN (+ ReLU) in front, in the same launch
+            const int b1 = static_cast<int>(pre_bn_of[xin]);
+            const Node &pb = g.nodes[b1];
+            const bool prelu = cin != b1;
+            const int px_node = pb.in[0];
+            const float *px = p.value[px_node], *pw = p.value[pb.in[1]];
+            const float *psm = p.saved_mean[b1], *psi = p.saved_inv[b1];
+            const uint64_t PC = pb.shape[1];
+            float *pdg, *pdb;
+            side(pb.in[1], pdg, "pre_weight_gradient");
+            side(pb.in[2], pdb, "pre_bias_gradient");
+            contribution(px_node, dst, acc);
+            // a convolution feeding only this BN: its bias gradient is the sum of this dx
+            float *pconv_db = nullptr;
+            const Node &src = g.nodes[px_node];
+            if (src.op == Op::Conv && consumers[px_node] == 1 && acc == nullptr &&
+                want(px_node) && want(src.in[2])) {
+              side(src.in[2], pconv_db, "pre_conv_bias_gradient");
+              conv_bias_done[px_node] = 1;
+            }
+            op.kind = std::string(prelu ? "batch_norm2d_relu_" : "batch_norm2d_") +
+                      (fused ? "depthwise_conv2d_batch_norm_relu_backward"
+                             : "depthwise_conv2d_batch_norm_backward");
+            op.name = (prelu ? name("bn", b1) + "+" + name("relu", cin) : name("bn", b1)) + "+" +
+                      name("conv", xin) + "+" + name("bn", bi) +
+                      (fused ? "+" + name("relu", r) : "") + ".backward";
+            op.tensors.push_back(ref("gradient", const_cast<float *>(gr), x, 0));
+            if (fused) op.tensors.push_back(ref("y", const_cast<float *>(y), x, 0));
+            op.tensors.push_back(ref("conv_y", const_cast<float *>(xi), cv, 0));
+            op.tensors.push_back(ref("weight", const_cast<float *>(w), g.nodes[bn.in[1]], 0));
+            op.tensors.push_back(ref_flat("saved_mean", const_cast<float *>(sm), C, 0));
+            op.tensors.push_back(ref_flat("saved_inverse_std", const_cast<float *>(si), C, 0));
+            op.tensors.push_back(ref("x", const_cast<float *>(cx), g.nodes[cin], 0));
+            op.tensors.push_back(ref("conv_weight", const_cast<float *>(cw), g.nodes[cv.in[1]], 0));
+            op.tensors.push_back(ref("pre_x", const_cast<float *>(px), g.nodes[px_node], 0));
+            op.tensors.push_back(ref("pre_weight", const_cast<float *>(pw), g.nodes[pb.in[1]], 0));
+            op.tensors.push_back(ref_flat("pre_saved_mean", const_cast<float *>(psm), PC, 0));
+            op.tensors.push_back(ref_flat("pre_saved_inverse_std", const_cast<float *>(psi), PC, 0));
+            op.tensors.push_back(ref("conv_output_gradient", cgr, cv, 1));
+            op.tensors.push_back(ref_flat("weight_gradient", dg, C, 1));
+            op.tensors.push_back(ref_flat("bias_gradient", db, C, 1));
+            op.tensors.push_back(ref("conv_bias_gradient", cdb, g.nodes[cv.in[2]], 1));
+            op.tensors.push_back(ref("conv_weight_gradient", cdw, g.nodes[cv.in[1]], 1));
+            op.tensors.push_back(ref_flat("pre_weight_gradient", pdg, PC, 1));
+            op.tensors.push_back(ref_flat("pre_bias_gradient", pdb, PC, 1));
+            if (pconv_db)
+              op.tensors.push_back(ref_flat("pre_conv_bias_gradient", pconv_db, PC, 1));
+            op.tensors.push_back(ref("contribution", dst, g.nodes[px_node], 1));
+            op.attrs = conv_attrs(cv);
+            emit(std::move(op), acc, g.nodes[px_node], [=](hipStream_t st) {
+              return oxh_batch_norm_depthwise_conv_batch_norm_backward_train(
+                  st, &s, gr, y, xi, w, sm, si, cx, cw, prelu ? 1 : 0, px, pw, psm, psi, cgr, dg,
+                  db, cdb, cdw, pdg, pdb, dst, pconv_db);
+            });
+            break;
+          }
           const float *addend = nullptr;
           dst = nullptr;
           acc = nullptr;

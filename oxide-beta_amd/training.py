@@ -188,7 +188,8 @@ class Op:
             self.attrs["tensors"] = list(zip(r["parameter"], r["gradient"], r["first_moment"],
                                              r["second_moment"]))
             self.attrs["step_counter"] = r["step"][0]
-        for role in ("running_mean", "running_variance"):
+        for role in ("running_mean", "running_variance", "pre_running_mean",
+                     "pre_running_variance"):
             if role in self.by_role and self.kind != "batch_norm2d_eval_forward":
                 self.attrs[role] = self.by_role[role][0]
 
@@ -483,6 +484,14 @@ def op_bytes(op: Op) -> tuple[str, int]:
         return "batch_norm2d", 3 * nb(op.reads["x"]) + acc                 # g, x in; dx out
     if k == "batch_norm2d_relu_backward":
         return "batch_norm2d", 4 * nb(op.reads["x"]) + acc                 # g, y, x in; dx out
+    if k.startswith("batch_norm2d") and "depthwise" in k and k.endswith("forward"):
+        # BN input in; its output, the convolution output and the layer output out
+        return ("batch_norm2d+conv2d+batch_norm2d",
+                2 * nb(op.reads["pre_x"]) + 2 * nb(op.writes["y"]))
+    if k.startswith("batch_norm2d") and "depthwise" in k:
+        # g (, y), convolution output, its input and the BN input in; output gradients out
+        outs = nb(op.reads["gradient"]) * (3 + ("y" in op.reads))
+        return "batch_norm2d+conv2d+batch_norm2d", outs + 3 * nb(op.reads["x"]) + acc
     if k.startswith("depthwise_conv2d_batch_norm") and k.endswith("forward"):
         # x in; convolution output and layer output out
         return "conv2d+batch_norm2d", nb(op.reads["x"]) + 2 * nb(op.writes["y"])

@@ -163,10 +163,11 @@ class OracleChecker:
     def depthwise_conv2d_batch_norm_relu_forward(self, op, r):
         self._depthwise_forward(op, r, True)
 
-    def _depthwise_backward(self, op, r, relu):
+    def _depthwise_backward(self, op, r, relu, input_gradient=True):
         """Its backward: the BatchNorm gradients as a BatchNorm backward's, then the
         convolution's bias / weight gradients (fixed-order sums) and input gradient (bit-exact,
-        + the residual addend where one is folded in) from the output gradient it wrote."""
+        + the residual addend where one is folded in) from the output gradient it wrote.
+        Returns the oracle's input gradient of the convolution (before any addend)."""
         a, w = op.attrs, op.writes
         gc = host(w["conv_output_gradient"])
         g = oracle.relu_backward(r["gradient"], r["y"]) if relu else r["gradient"]
@@ -183,11 +184,72 @@ class OracleChecker:
                       1e-5 * np.abs(gc).astype(np.float64).sum(axis=(0, 2, 3)) + 1e-7,
                       f"{op.name} conv bias")
         self.counts["conv bias in batch norm backward"] += 1
-        if "contribution" in w:
+        if input_gradient and "contribution" in w:
+            ref = rdx
             if "addend" in r:
-                rdx = oracle.accumulate(r["addend"], rdx)
+                ref = oracle.accumulate(r["addend"], rdx)
                 self.counts["conv input backward with addend"] += 1
-            assert_bitexact(host(w["contribution"]), rdx, f"{op.name} input gradient")
+            assert_bitexact(host(w["contribution"]), ref, f"{op.name} input gradient")
+        return rdx
+
+    def _pre_forward(self, op, r, pre_relu, relu):
+        """A BatchNorm (+ ReLU) in front of a depthwise layer, run in the layer's launch: the
+        BatchNorm checked as its own forward (statistics, output, running update), then the
+        layer from the output it wrote."""
+        a, w = op.attrs, op.writes
+        out = dict(y=host(w["pre_y"]), mean=host(w["pre_saved_mean"]),
+                   inv=host(w["pre_saved_inverse_std"]), rm=host(a["pre_running_mean"]),
+                   rv=host(a["pre_running_variance"]))
+        check_batch_norm_forward(out, r["pre_x"], r["pre_weight"], r["pre_bias"],
+                                 self.prior[id(a["pre_running_mean"])],
+                                 self.prior[id(a["pre_running_variance"])], a["pre_momentum"],
+                                 a["pre_epsilon"], relu=pre_relu)
+        self._depthwise_forward(op, dict(r, x=out["y"]), relu)
+        self.counts["batch norm before depthwise"] += 1
+
+    def _pre_backward(self, op, r, pre_relu, relu):
+        """Its backward: the layer's gradients as its own backward's; the BatchNorm in front
+        from the layer's input gradient (the oracle's, bit-exact from the output gradient the
+        launch wrote) through its ReLU, as a BatchNorm backward's; the bias gradient of a
+        convolution feeding it as that BatchNorm backward's dx sum."""
+        w = op.writes
+        da = self._depthwise_backward(op, r, relu, input_gradient=False)
+        g = oracle.relu_backward(da, r["x"]) if pre_relu else da
+        dx = host(w["contribution"])
+        check_batch_norm_backward(dict(dx=dx, dw=host(w["pre_weight_gradient"]),
+                                       db=host(w["pre_bias_gradient"])), g, r["pre_x"],
+                                  r["pre_weight"], r["pre_saved_mean"],
+                                  r["pre_saved_inverse_std"])
+        if "pre_conv_bias_gradient" in w:
+            assert_within(host(w["pre_conv_bias_gradient"]), oracle.conv2d_bias_backward(dx),
+                          1e-5 * np.abs(dx).astype(np.float64).sum(axis=(0, 2, 3)) + 1e-7,
+                          f"{op.name} conv bias in front")
+            self.counts["conv bias in batch norm backward"] += 1
+        self.counts["batch norm before depthwise"] += 1
+
+    def batch_norm2d_relu_depthwise_conv2d_batch_norm_relu_forward(self, op, r):
+        self._pre_forward(op, r, True, True)
+
+    def batch_norm2d_relu_depthwise_conv2d_batch_norm_forward(self, op, r):
+        self._pre_forward(op, r, True, False)
+
+    def batch_norm2d_depthwise_conv2d_batch_norm_relu_forward(self, op, r):
+        self._pre_forward(op, r, False, True)
+
+    def batch_norm2d_depthwise_conv2d_batch_norm_forward(self, op, r):
+        self._pre_forward(op, r, False, False)
+
+    def batch_norm2d_relu_depthwise_conv2d_batch_norm_relu_backward(self, op, r):
+        self._pre_backward(op, r, True, True)
+
+    def batch_norm2d_relu_depthwise_conv2d_batch_norm_backward(self, op, r):
+        self._pre_backward(op, r, True, False)
+
+    def batch_norm2d_depthwise_conv2d_batch_norm_relu_backward(self, op, r):
+        self._pre_backward(op, r, False, True)
+
+    def batch_norm2d_depthwise_conv2d_batch_norm_backward(self, op, r):
+        self._pre_backward(op, r, False, False)
 
     def depthwise_conv2d_batch_norm_backward(self, op, r):
         self._depthwise_backward(op, r, False)
