@@ -977,9 +977,10 @@ __global__ __launch_bounds__(Threads) void pointwise_product_kernel(ProductArgs 
 }
 
 // Products whose sums need not follow the serial order (the weight gradient, already reduced in
-// k chunks): an 8 x 8 tile per kSplitWaves-wave block, wave w summing the w-th contiguous part
-// of the chunk's k range serially, the parts then added in wave order.  Four times the waves of
-// the one-wave tile and a quarter of its serial chain.  No initial value or addend.
+// k chunks; the forward of a small pointwise convolution): an 8 x 8 tile per kSplitWaves-wave
+// block, wave w summing the w-th contiguous part of the chunk's k range serially (wave 0 from
+// the initial value), the parts then added in wave order, then the addend.  Four times the
+// waves of the one-wave tile and a quarter of its serial chain.
 constexpr int kSplitWaves = 4;
 constexpr int kSplitThreads = 64 * kSplitWaves;
 struct SplitLds {
@@ -1000,7 +1001,11 @@ __device__ __forceinline__ void split_tile(const ProductArgs &g, uint32_t bx, ui
   const int w = static_cast<int>(threadIdx.x) / 64, t = static_cast<int>(threadIdx.x) % 64;
   const uint32_t wb = min(kb + w * part, ke), we = min(wb + part, ke);
   const uint32_t slabs = (part + kSlab - 1) / kSlab;  // equal for every wave (barriers)
-  float acc[1][1] = {{0.0f}};
+  const uint32_t m = m0 + t / 8, n = n0 + t % 8;
+  float acc[1][1] = {{w == 0 && g.init != nullptr && m < g.M ? g.init[m] : 0.0f}};
+  const float added = w == 0 && g.addend != nullptr && m < g.M && n < g.N
+                          ? g.addend[axis_offset(g.cm, m) + axis_offset(g.cn, n)]
+                          : 0.0f;
   product_sum<8, 64, AKFast, BKFast>(g, m0, n0, wb, we, slabs, t, acc, lds.as[w], lds.bs[w]);
   if (w > 0) lds.part[w - 1][t] = acc[0][0];
   __syncthreads();
@@ -1008,7 +1013,7 @@ __device__ __forceinline__ void split_tile(const ProductArgs &g, uint32_t bx, ui
   float sum = acc[0][0];
 #pragma unroll
   for (int q = 0; q < kSplitWaves - 1; ++q) sum += lds.part[q][t];
-  product_store(g, bz, m0 + t / 8, n0 + t % 8, sum, 0.0f);
+  product_store(g, bz, m, n, sum, added);
 }
 
 template <bool AKFast, bool BKFast>
@@ -1331,12 +1336,27 @@ void launch_tiled(hipStream_t s, const ProductArgs &a, uint32_t chunks) {
     oxh::launch(pointwise_product_kernel<Tile, Threads, false, false>, grid, block, 0, s, a);
 }
 
+template <bool A, bool B>
+void launch_split(hipStream_t s, const ProductArgs &a, uint32_t chunks);
+
+// Serial sums (one per output, the CPU path's order): grids of >= kSmallGrid 32 x 32 tiles take
+// the 32 x 32 tiling, smaller ones the one-wave 8 x 8 tiles.  With `split`, small grids take
+// the split tiles instead (contiguous parts of k added in order: the same sum within a few
+// roundings, a quarter of the serial chain).
 oxh_status launch_product(const char *name, hipStream_t s, const ProductArgs &a,
-                          uint32_t chunks) {
+                          uint32_t chunks, bool split = false) {
   const uint64_t big =
       static_cast<uint64_t>((a.N + kTile - 1) / kTile) * ((a.M + kTile - 1) / kTile) * chunks;
   if (big >= kSmallGrid)
     launch_tiled<kTile, 256>(s, a, chunks);
+  else if (split && a.a.k_fast && a.b.k_fast)
+    launch_split<true, true>(s, a, chunks);
+  else if (split && a.a.k_fast)
+    launch_split<true, false>(s, a, chunks);
+  else if (split && a.b.k_fast)
+    launch_split<false, true>(s, a, chunks);
+  else if (split)
+    launch_split<false, false>(s, a, chunks);
   else if (OXH_TINY_TILE == 8)
     launch_tiled<8, 64>(s, a, chunks);
   else
@@ -1577,7 +1597,7 @@ oxh_status oxh_conv2d_forward(oxh_stream stream, const oxh_conv2d_shape *shape,
     a.N = g.batch * plane;
     a.K = g.in_c;
     a.k_chunk = a.K;
-    return launch_product(name, s, a, 1);
+    return launch_product(name, s, a, 1, true);
   }
   const LdsPlan lp = forward_lds_plan(g);
   if (lp.tile > 0) {

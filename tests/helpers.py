@@ -46,6 +46,20 @@ def assert_close(got, ref, rtol=1e-5, atol=1e-6, what=""):
                              f" worst at {worst}: got {g[worst]!r} ref {r[worst]!r}")
 
 
+def assert_conv_forward(got, x, weight, bias, stride, padding, groups, what=""):
+    """A conv2d forward against the oracle: bit-exact, except a pointwise convolution (1x1,
+    stride 1, no padding, one group), whose small grids sum contiguous parts of the input
+    channels in order: within 1e-5 * sum|terms| (the terms' magnitudes through the oracle)."""
+    import oracle
+
+    ref = oracle.conv2d_forward(x, weight, bias, stride, padding, groups)
+    if weight.shape[2:] == (1, 1) and stride == 1 and padding == 0 and groups == 1:
+        mag = oracle.conv2d_forward(np.abs(x), np.abs(weight), np.abs(bias), 1, 0, 1)
+        assert_within(got, ref, 1e-5 * mag.astype(np.float64) + 1e-7, what)
+    else:
+        assert_bitexact(got, ref, what)
+
+
 def assert_within(got, ref, bound, what=""):
     """|got - ref| <= bound elementwise (bound: a conditioning-aware error bound)."""
     d = np.abs(np.asarray(got, np.float64) - np.asarray(ref, np.float64))
