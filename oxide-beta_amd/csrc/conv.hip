@@ -1340,13 +1340,19 @@ template <bool A, bool B>
 void launch_split(hipStream_t s, const ProductArgs &a, uint32_t chunks);
 
 // Serial sums (one per output, the CPU path's order): grids of >= kSmallGrid 32 x 32 tiles take
-// the 32 x 32 tiling, smaller ones the one-wave 8 x 8 tiles.  With `split`, small grids take
-// the split tiles instead (contiguous parts of k added in order: the same sum within a few
-// roundings, a quarter of the serial chain).
+// the 32 x 32 tiling, smaller ones the one-wave 8 x 8 tiles.  With `split`, grids of at most
+// kSplitMaxTiles 8 x 8 tiles with at least kSplitMinK terms per sum take the split tiles
+// instead (contiguous parts of k added in order: the same sum within a few roundings, a
+// quarter of the serial chain, four times the waves of a grid that leaves most of the chip
+// idle).
+constexpr uint64_t kSplitMaxTiles = 512;
+constexpr uint32_t kSplitMinK = 256;
 oxh_status launch_product(const char *name, hipStream_t s, const ProductArgs &a,
                           uint32_t chunks, bool split = false) {
   const uint64_t big =
       static_cast<uint64_t>((a.N + kTile - 1) / kTile) * ((a.M + kTile - 1) / kTile) * chunks;
+  const uint64_t tiles8 = static_cast<uint64_t>((a.N + 7) / 8) * ((a.M + 7) / 8) * chunks;
+  split = split && a.k_chunk >= kSplitMinK && tiles8 <= kSplitMaxTiles;
   if (big >= kSmallGrid)
     launch_tiled<kTile, 256>(s, a, chunks);
   else if (split && a.a.k_fast && a.b.k_fast)
