@@ -343,6 +343,92 @@ __global__ __launch_bounds__(256) void conv2d_forward_lds_kernel(
   }
 }
 
+// The forward of an ungrouped K x K convolution whose output plane is small, its input-channel
+// sums split: block (output-channel tile of kLdsR-channel groups, image) stages the image and
+// the tile's weights as conv2d_forward_lds_kernel; thread (part, item) sums input channels
+// [part * in_c / kFwdParts, (part + 1) * in_c / kFwdParts) for the item's kLdsR outputs (part 0
+// from the bias), and the parts are added in order.  A quarter of the serial chain per thread
+// and four times the waves of the serial kernel.
+constexpr int kFwdParts = 4;
+
+template <int K, int S>
+__global__ __launch_bounds__(256) void conv2d_forward_split_kernel(
+    ConvGeom g, uint32_t oc_tile, uint32_t items, oxh::FastDiv oplane_div,
+    oxh::FastDiv rows_div, const float *__restrict__ x, const float *__restrict__ wt,
+    const float *__restrict__ bias, float *__restrict__ y) {
+  extern __shared__ float lds[];
+  constexpr int T = K * K;
+  const uint32_t n = blockIdx.y, oc0 = blockIdx.x * oc_tile;
+  const uint32_t ocn = min(oc_tile, g.out_c - oc0), ocp = round4(ocn);
+  const uint32_t plane = g.h * g.w, xs = g.in_c * plane;
+  const uint32_t rows = g.in_c * T;  // r = ic * T + tap
+  float *xl = lds, *wl = lds + round4(xs);  // wl[(ic * T + tap) * ocp + ocl]
+  float *red = wl + round4(rows * ocp);     // red[(part - 1) * items * kLdsR + ...]
+  stage_plain(xl, x + static_cast<uint64_t>(n) * xs, xs);
+  stage(wl, wt + static_cast<uint64_t>(oc0) * rows, ocn * rows, same_index, [&](uint32_t i) {
+    const uint32_t ocl = fdiv(i, rows_div);
+    return (i - ocl * rows) * ocp + ocl;
+  });
+  if (ocp > ocn) zero_fill(wl, rows, ocp, ocn, ocp - ocn);
+  __syncthreads();
+  const uint32_t oplane = g.oh * g.ow;
+  const uint32_t it = threadIdx.x % items, part = threadIdx.x / items;
+  const bool active = part < kFwdParts;  // threads past parts * items idle
+  const uint32_t q = fdiv(it, oplane_div), pos = it - q * oplane;
+  float acc[kLdsR] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (active) {
+    const uint32_t oy = fdiv(pos, g.ow_div), ox = pos - oy * g.ow;
+    const int by = static_cast<int>(oy) * S - static_cast<int>(g.pad);
+    const int bx = static_cast<int>(ox) * S - static_cast<int>(g.pad);
+    int off[T];
+    uint32_t mask[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const int iy = by + t / K, ix = bx + t % K;
+      const bool v = static_cast<uint32_t>(iy) < g.h && static_cast<uint32_t>(ix) < g.w;
+      off[t] = v ? iy * static_cast<int>(g.w) + ix : 0;
+      mask[t] = tap_mask(v);
+    }
+    if (part == 0) {
+#pragma unroll
+      for (int r = 0; r < kLdsR; ++r) {
+        const uint32_t ocl = q * kLdsR + r;
+        acc[r] = ocl < ocn ? bias[oc0 + ocl] : 0.0f;
+      }
+    }
+    const uint32_t ic0 = part * g.in_c / kFwdParts, ic1 = (part + 1) * g.in_c / kFwdParts;
+    const float *wq = wl + q * kLdsR;
+    for (uint32_t ic = ic0; ic < ic1; ++ic) {
+      const float *xp = xl + ic * plane;
+      const float *wp = wq + ic * T * ocp;
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const float xv = xp[off[t]];
+        const float4 w4 = *reinterpret_cast<const float4 *>(wp + t * ocp);
+        acc[0] += tap_term(xv * w4.x, mask[t]);
+        acc[1] += tap_term(xv * w4.y, mask[t]);
+        acc[2] += tap_term(xv * w4.z, mask[t]);
+        acc[3] += tap_term(xv * w4.w, mask[t]);
+      }
+    }
+    if (part > 0) {
+#pragma unroll
+      for (int r = 0; r < kLdsR; ++r) red[((part - 1) * items + it) * kLdsR + r] = acc[r];
+    }
+  }
+  __syncthreads();
+  if (!active || part != 0) return;
+#pragma unroll
+  for (int p = 1; p < kFwdParts; ++p)
+#pragma unroll
+    for (int r = 0; r < kLdsR; ++r) acc[r] += red[((p - 1) * items + it) * kLdsR + r];
+#pragma unroll
+  for (int r = 0; r < kLdsR; ++r) {
+    const uint32_t ocl = q * kLdsR + r;
+    if (ocl < ocn) y[(static_cast<uint64_t>(n) * g.out_c + oc0 + ocl) * oplane + pos] = acc[r];
+  }
+}
+
 // Input gradient: block (input-channel tile, image) stages the image's whole output gradient
 // and the weights of the tile's input channels as wl[(oc * K * K + tap) * icp + icl].
 template <int K, int S>
@@ -1219,6 +1305,37 @@ LdsPlan forward_lds_plan(const ConvGeom &g) {
                        static_cast<uint64_t>(g.oh) * g.ow);
 }
 
+// The split forward: output planes of at most 64 positions, at least 4 input channels per
+// part, the serial kernel's grid under 2048 waves (most of the chip idle); tiles of as many
+// kLdsR-channel groups as fill 64 items (one per position and group), threads kFwdParts * items
+// rounded to waves.  tile == 0: not taken.
+#ifndef OXH_FWD_SPLIT
+#define OXH_FWD_SPLIT 1  // 0: every K x K forward takes the serial kernels
+#endif
+LdsPlan forward_split_plan(const ConvGeom &g) {
+  LdsPlan p;
+  const uint64_t oplane = static_cast<uint64_t>(g.oh) * g.ow;
+  if (!OXH_FWD_SPLIT || !lds_eligible(g) || oplane > 64 || g.in_c < 4 * kFwdParts) return p;
+  const LdsPlan serial = forward_lds_plan(g);
+  if (serial.tile > 0 &&
+      static_cast<uint64_t>(serial.tiles) * g.batch * ((serial.threads + 63) / 64) >= 2048)
+    return p;
+  uint64_t groups = 64 / oplane;
+  const uint64_t all = (g.out_c + kLdsR - 1) / kLdsR;
+  if (groups > all) groups = all;
+  const uint64_t tile = groups * kLdsR, items = groups * oplane;
+  const uint64_t taps = static_cast<uint64_t>(g.kh) * g.kw;
+  const uint64_t floats = (static_cast<uint64_t>(g.in_c) * g.h * g.w + 3) / 4 * 4 +
+                          (g.in_c * taps * tile + 3) / 4 * 4 + (kFwdParts - 1) * items * kLdsR;
+  if (floats > kLdsFloats) return p;
+  p.tile = static_cast<uint32_t>(tile);
+  p.tiles = static_cast<uint32_t>((g.out_c + tile - 1) / tile);
+  p.groups = static_cast<uint32_t>(items);  // items per block
+  p.threads = static_cast<uint32_t>((kFwdParts * items + 63) / 64 * 64);
+  p.lds_bytes = static_cast<uint32_t>(floats * 4);
+  return p;
+}
+
 LdsPlan input_backward_lds_plan(const ConvGeom &g) {
   if (!lds_eligible(g)) return LdsPlan{};
   const uint64_t taps = g.kh * g.kw;
@@ -1347,12 +1464,17 @@ void launch_split(hipStream_t s, const ProductArgs &a, uint32_t chunks);
 // idle).
 constexpr uint64_t kSplitMaxTiles = 512;
 constexpr uint32_t kSplitMinK = 256;
+bool split_pays(uint32_t M, uint32_t N, uint32_t k_chunk, uint32_t chunks) {
+  const uint64_t big =
+      static_cast<uint64_t>((N + kTile - 1) / kTile) * ((M + kTile - 1) / kTile) * chunks;
+  const uint64_t tiles8 = static_cast<uint64_t>((N + 7) / 8) * ((M + 7) / 8) * chunks;
+  return big < kSmallGrid && k_chunk >= kSplitMinK && tiles8 <= kSplitMaxTiles;
+}
 oxh_status launch_product(const char *name, hipStream_t s, const ProductArgs &a,
                           uint32_t chunks, bool split = false) {
   const uint64_t big =
       static_cast<uint64_t>((a.N + kTile - 1) / kTile) * ((a.M + kTile - 1) / kTile) * chunks;
-  const uint64_t tiles8 = static_cast<uint64_t>((a.N + 7) / 8) * ((a.M + 7) / 8) * chunks;
-  split = split && a.k_chunk >= kSplitMinK && tiles8 <= kSplitMaxTiles;
+  split = split && split_pays(a.M, a.N, a.k_chunk, chunks);
   if (big >= kSmallGrid)
     launch_tiled<kTile, 256>(s, a, chunks);
   else if (split && a.a.k_fast && a.b.k_fast)
@@ -1576,6 +1698,13 @@ oxh_status oxh_conv2d_output_size(const oxh_conv2d_shape *shape, uint64_t *out_h
   return oxh::ok();
 }
 
+int oxh_conv2d_forward_serial(const oxh_conv2d_shape *shape) {
+  ConvGeom g;
+  if (make_conv_geom("oxh_conv2d_forward_serial", shape, g) != OXH_OK) return -1;
+  if (pointwise(g)) return split_pays(g.out_c, g.batch * g.h * g.w, g.in_c, 1) ? 0 : 1;
+  return forward_split_plan(g).tile > 0 ? 0 : 1;
+}
+
 oxh_status oxh_conv2d_forward(oxh_stream stream, const oxh_conv2d_shape *shape,
                               const float *input, const float *weight, const float *bias,
                               float *output) {
@@ -1604,6 +1733,19 @@ oxh_status oxh_conv2d_forward(oxh_stream stream, const oxh_conv2d_shape *shape,
     a.K = g.in_c;
     a.k_chunk = a.K;
     return launch_product(name, s, a, 1, true);
+  }
+  const LdsPlan sp = forward_split_plan(g);
+  if (sp.tile > 0) {
+    const dim3 lgrid(sp.tiles, g.batch), lblock(sp.threads);
+    const oxh::FastDiv od = oxh::make_fastdiv(g.oh * g.ow);
+    const oxh::FastDiv rd = oxh::make_fastdiv(g.in_c * g.kh * g.kw);
+    switch (tap_kernel(g)) {
+      case 31: oxh::launch(conv2d_forward_split_kernel<3, 1>, lgrid, lblock, sp.lds_bytes, s, g, sp.tile, sp.groups, od, rd, input, weight, bias, output); break;
+      case 32: oxh::launch(conv2d_forward_split_kernel<3, 2>, lgrid, lblock, sp.lds_bytes, s, g, sp.tile, sp.groups, od, rd, input, weight, bias, output); break;
+      case 51: oxh::launch(conv2d_forward_split_kernel<5, 1>, lgrid, lblock, sp.lds_bytes, s, g, sp.tile, sp.groups, od, rd, input, weight, bias, output); break;
+      default: oxh::launch(conv2d_forward_split_kernel<5, 2>, lgrid, lblock, sp.lds_bytes, s, g, sp.tile, sp.groups, od, rd, input, weight, bias, output);
+    }
+    return oxh::launched(name);
   }
   const LdsPlan lp = forward_lds_plan(g);
   if (lp.tile > 0) {

@@ -159,6 +159,7 @@ _SIGNATURES = {
                                           ctypes.POINTER(AdamWTensor), _u32]),
     "oxh_conv2d_output_size": (_st, [_CS, ctypes.POINTER(_u64), ctypes.POINTER(_u64)]),
     "oxh_conv2d_forward": (_st, [_vp, _CS, _vp, _vp, _vp, _vp]),
+    "oxh_conv2d_forward_serial": (_int, [_CS]),
     "oxh_conv2d_input_backward": (_st, [_vp, _CS, _vp, _vp, _vp]),
     "oxh_conv2d_input_backward_accumulate": (_st, [_vp, _CS, _vp, _vp, _vp, _vp]),
     "oxh_conv2d_weight_backward_workspace_size": (_st, [_CS, ctypes.POINTER(_u64)]),
@@ -417,6 +418,15 @@ def conv2d_output_size(shape: Conv2dShape) -> tuple[int, int]:
     oh, ow = _u64(), _u64()
     check(lib().oxh_conv2d_output_size(ctypes.byref(shape), ctypes.byref(oh), ctypes.byref(ow)))
     return oh.value, ow.value
+
+
+def conv2d_forward_serial(shape: Conv2dShape) -> bool:
+    """True when oxh_conv2d_forward sums each output in the CPU path's order (bit-identical),
+    False when in four ordered parts over the input channels."""
+    v = lib().oxh_conv2d_forward_serial(ctypes.byref(shape))
+    if v < 0:
+        raise OxideError(INVALID_SHAPE, "invalid conv2d shape")
+    return bool(v)
 
 
 def conv2d_workspace_size(shape: Conv2dShape) -> int:

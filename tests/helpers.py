@@ -47,17 +47,21 @@ def assert_close(got, ref, rtol=1e-5, atol=1e-6, what=""):
 
 
 def assert_conv_forward(got, x, weight, bias, stride, padding, groups, what=""):
-    """A conv2d forward against the oracle: bit-exact, except a pointwise convolution (1x1,
-    stride 1, no padding, one group), whose small grids sum contiguous parts of the input
-    channels in order: within 1e-5 * sum|terms| (the terms' magnitudes through the oracle)."""
+    """A conv2d forward against the oracle: bit-exact where the library sums in the CPU path's
+    order (oxh_conv2d_forward_serial), else (four ordered parts over the input channels) within
+    1e-5 * sum|terms| (the terms' magnitudes through the oracle)."""
     import oracle
+    import oxide_hip as ox
 
     ref = oracle.conv2d_forward(x, weight, bias, stride, padding, groups)
-    if weight.shape[2:] == (1, 1) and stride == 1 and padding == 0 and groups == 1:
-        mag = oracle.conv2d_forward(np.abs(x), np.abs(weight), np.abs(bias), 1, 0, 1)
-        assert_within(got, ref, 1e-5 * mag.astype(np.float64) + 1e-7, what)
-    else:
+    n, cin, h, w = x.shape
+    cout, _, k, _ = weight.shape
+    if ox.conv2d_forward_serial(ox.conv2d_shape(n, cin, h, w, cout, k, stride, padding, groups)):
         assert_bitexact(got, ref, what)
+    else:
+        mag = oracle.conv2d_forward(np.abs(x), np.abs(weight), np.abs(bias), stride, padding,
+                                    groups)
+        assert_within(got, ref, 1e-5 * mag.astype(np.float64) + 1e-7, what)
 
 
 def assert_within(got, ref, bound, what=""):

@@ -2,11 +2,11 @@
 group updates in place, ``after`` recomputes the group with the oracle from the device tensors
 it actually read and compares what it wrote.
 
-Bars per kind: conv input gradient, conv forward (but that of small pointwise convolutions),
-pooling, ReLU, add, mul, copies, accumulate and AdamW bit-exact; BatchNorm and cross entropy
-within the north star's 1e-5 relative (1e-6 absolute, or the conditioning bound of a cancelling
-sum); small pointwise conv forwards, conv weight / bias and BatchNorm affine gradients within
-1e-5 * sum|terms| (fixed-order sums)."""
+Bars per kind: conv input gradient, conv forwards summed in the CPU path's order
+(oxh_conv2d_forward_serial), pooling, ReLU, add, mul, copies, accumulate and AdamW bit-exact;
+BatchNorm and cross entropy within the north star's 1e-5 relative (1e-6 absolute, or the
+conditioning bound of a cancelling sum); the other conv forwards, conv weight / bias and
+BatchNorm affine gradients within 1e-5 * sum|terms| (fixed-order sums)."""
 
 from collections import Counter
 

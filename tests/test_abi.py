@@ -262,3 +262,19 @@ def test_net_builders_check_shapes_on_the_host():
     assert L.oxh_net_training_program(h, r.value, None, ctypes.byref(prog)) == ox.EXECUTION
     assert b"scalar" in L.oxh_last_error()
     assert L.oxh_net_destroy(h) == ox.OK
+
+
+def test_conv_forward_order_query():
+    """oxh_conv2d_forward_serial: the forwards that would leave most of the chip idle sum four
+    ordered parts (the MNIST MobileNetV4's long-channel 1x1 layers on 1x1 planes, the fused
+    blocks' 3x3 convolutions); the stem, short-channel and large-grid forwards stay serial."""
+    sh = ox.conv2d_shape
+    assert ox.conv2d_forward_serial(sh(128, 1, 28, 28, 32, 3, 2, 1, 1))        # stem
+    assert not ox.conv2d_forward_serial(sh(128, 32, 14, 14, 32, 3, 2, 1, 1))   # 7x7 output
+    assert not ox.conv2d_forward_serial(sh(128, 32, 7, 7, 96, 3, 2, 1, 1))     # 4x4 output
+    assert not ox.conv2d_forward_serial(sh(128, 512, 1, 1, 128, 1, 1, 0, 1))   # UIB project
+    assert ox.conv2d_forward_serial(sh(128, 128, 1, 1, 512, 1, 1, 0, 1))       # 128 channels
+    assert ox.conv2d_forward_serial(sh(128, 64, 8, 8, 256, 1, 1, 0, 1))        # large grid
+    assert ox.conv2d_forward_serial(sh(2, 8, 5, 5, 8, 3, 1, 1, 8))             # grouped
+    with pytest.raises(ox.OxideError):
+        ox.conv2d_forward_serial(sh(1, 1, 1, 1, 1, 3, 1, 0, 1))                # kernel > input
