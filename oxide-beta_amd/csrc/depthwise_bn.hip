@@ -51,8 +51,9 @@ constexpr int kPreNone = 0, kPreBn = 1, kPreBnRelu = 2;
 struct PreBnForward {
   const float *input;          // the BatchNorm's input [N, C, H, W]
   const float *weight, *bias;  // its affine parameters
+  const float *residual;       // added to the BatchNorm's output (a residual add), or null
   StatsOut stats;              // its saved and running statistics
-  float *output;               // its output: the convolution's input, stored
+  float *output;               // its output (+ residual): the convolution's input, stored
 };
 struct PreBnBackward {
   const float *input;             // the BatchNorm's input, for x_hat
@@ -105,19 +106,20 @@ __global__ __launch_bounds__(kDwThreads) void dw_bn_forward_kernel(
   if constexpr (Pre != kPreNone) {
     // the BatchNorm (relu) in front over input channel c (at most kDwThreads * kChannelKeep
     // values), exactly as its channel kernel forms it; its output goes to LDS for the taps
-    float kin[kChannelKeep];
+    float kin[kChannelKeep], kadd[kChannelKeep];
     uint32_t ain[kChannelKeep];
+    const bool add = pre.residual != nullptr;
 #pragma unroll
     for (int u = 0; u < kChannelKeep; ++u) {
       const uint32_t j = threadIdx.x + u * kDwThreads;
       ain[u] = j < g.in_samples ? input_index(g, c, j) : 0;
       kin[u] = pre.input[ain[u]];
+      kadd[u] = add ? pre.residual[ain[u]] : 0.0f;
     }
     const float pshift = pre.input[input_index(g, c, 0)];
-    const float none[kChannelKeep] = {};
     oxh::channel_forward_kept<Pre == kPreBnRelu, kDwThreads>(g.in_samples, c, pshift, kin, ain,
                                                              pre.weight[c], pre.bias[c],
-                                                             pre.stats, false, none, pre.output,
+                                                             pre.stats, add, kadd, pre.output,
                                                              lds, xs);
   } else {
     stage_channel(g, c, x, xs);
@@ -289,14 +291,18 @@ __global__ __launch_bounds__(kDwThreads) void dw_bn_backward_kernel(
   };
   if constexpr (Pre != kPreNone) {
     // the BatchNorm (relu) in front, backward over its channel from the input gradient just
-    // formed (its relu output is the staged convolution input), exactly as its channel
-    // backward forms it; its dx sum is the feeding convolution's bias gradient
+    // formed plus the addend (the convolution input's other gradient contributions: its whole
+    // gradient, stored to dx when given; its relu output is the staged convolution input),
+    // exactly as its channel backward forms it; its dx sum is the feeding convolution's bias
+    // gradient
     float kg[kChannelKeep], kn[kChannelKeep], d[kChannelKeep];
 #pragma unroll
     for (int u = 0; u < kChannelKeep; ++u) {
       const uint32_t i = threadIdx.x + u * kDwThreads;
       if (i >= g.in_samples) break;
-      const float a = input_sum(i);
+      float a = input_sum(i);
+      if (addend != nullptr) a = a + addend[pat[u]];
+      if (dx != nullptr) dx[pat[u]] = a;
       kg[u] = Pre == kPreBnRelu ? oxh::relu_masked(a, xs[i]) : a;
       kn[u] = (pin[u] - pmu) * pinv;
     }
@@ -534,8 +540,9 @@ int oxh_batch_norm_depthwise_conv_batch_norm_supported(const oxh_conv2d_shape *s
 oxh_status oxh_batch_norm_depthwise_conv_batch_norm_forward_train(
     oxh_stream stream, const oxh_conv2d_shape *shape, int pre_relu, float pre_momentum,
     float pre_epsilon, const float *pre_input, const float *pre_weight, const float *pre_bias,
-    float *pre_running_mean, float *pre_running_variance, float *pre_saved_mean,
-    float *pre_saved_inverse_std, float *pre_output, int relu, float momentum, float epsilon,
+    const float *pre_residual, float *pre_running_mean, float *pre_running_variance,
+    float *pre_saved_mean, float *pre_saved_inverse_std, float *pre_output, int relu,
+    float momentum, float epsilon,
     const float *conv_weight, const float *conv_bias, float *conv_output,
     const float *bn_weight, const float *bn_bias, float *running_mean, float *running_variance,
     float *saved_mean, float *saved_inverse_std, float *output) {
@@ -549,8 +556,13 @@ oxh_status oxh_batch_norm_depthwise_conv_batch_norm_forward_train(
                   conv_bias && conv_output && bn_weight && bn_bias && running_mean &&
                   running_variance && saved_mean && saved_inverse_std && output,
               OXH_INVALID_SHAPE, std::string(name) + ": null pointer");
+  OXH_REQUIRE(pre_residual == nullptr || !pre_relu, OXH_INVALID_SHAPE,
+              std::string(name) + ": a residual after a ReLU");
   const uint64_t c = g.out.channels;
   const uint64_t in_bytes = c * g.in_samples * 4, out_bytes = c * g.out.samples * 4;
+  OXH_REQUIRE(pre_residual == nullptr ||
+                  !oxh::any_overlap(pre_output, in_bytes, pre_residual, in_bytes),
+              OXH_INVALID_SHAPE, std::string(name) + ": pre_output overlaps the residual");
   OXH_REQUIRE(!oxh::any_overlap(pre_output, in_bytes, pre_input, in_bytes) &&
                   !oxh::any_overlap(conv_output, out_bytes, pre_input, in_bytes) &&
                   !oxh::any_overlap(conv_output, out_bytes, pre_output, in_bytes) &&
@@ -560,7 +572,7 @@ oxh_status oxh_batch_norm_depthwise_conv_batch_norm_forward_train(
               OXH_INVALID_SHAPE, std::string(name) + ": outputs overlap an input or each other");
   const StatsOut so{saved_mean, saved_inverse_std, nullptr, running_mean, running_variance,
                     momentum, epsilon};
-  const PreBnForward pre{pre_input, pre_weight, pre_bias,
+  const PreBnForward pre{pre_input, pre_weight, pre_bias, pre_residual,
                          StatsOut{pre_saved_mean, pre_saved_inverse_std, nullptr,
                                   pre_running_mean, pre_running_variance, pre_momentum,
                                   pre_epsilon},
@@ -580,11 +592,12 @@ oxh_status oxh_batch_norm_depthwise_conv_batch_norm_backward_train(
     oxh_stream stream, const oxh_conv2d_shape *shape, const float *gradient,
     const float *relu_output, const float *conv_output, const float *bn_weight,
     const float *saved_mean, const float *saved_inverse_std, const float *conv_input,
-    const float *conv_weight, int pre_relu, const float *pre_input, const float *pre_weight,
-    const float *pre_saved_mean, const float *pre_saved_inverse_std,
+    const float *conv_weight, const float *addend, int pre_relu, const float *pre_input,
+    const float *pre_weight, const float *pre_saved_mean, const float *pre_saved_inverse_std,
     float *conv_output_gradient, float *bn_weight_gradient, float *bn_bias_gradient,
-    float *conv_bias_gradient, float *conv_weight_gradient, float *pre_weight_gradient,
-    float *pre_bias_gradient, float *pre_input_gradient, float *pre_input_gradient_sum) {
+    float *conv_bias_gradient, float *conv_weight_gradient, float *conv_input_gradient,
+    float *pre_weight_gradient, float *pre_bias_gradient, float *pre_input_gradient,
+    float *pre_input_gradient_sum) {
   const char *name = "oxh_batch_norm_depthwise_conv_batch_norm_backward_train";
   DwGeom g;
   OXH_REQUIRE(make_dw_geom(shape, g) && pre_eligible(g), OXH_INVALID_SHAPE,
@@ -616,11 +629,32 @@ oxh_status oxh_batch_norm_depthwise_conv_batch_norm_backward_train(
   OXH_REQUIRE(conv_output_gradient == nullptr ||
                   !oxh::any_overlap(conv_output_gradient, out_bytes, pre_input_gradient, in_bytes),
               OXH_INVALID_SHAPE, std::string(name) + ": the gradients overlap");
+  // the convolution input's whole gradient (+ addend), each element read then written by one
+  // thread: it may equal the addend, and overlaps nothing else
+  if (conv_input_gradient != nullptr)
+    for (const void *p : {static_cast<const void *>(gradient),
+                          static_cast<const void *>(relu_output),
+                          static_cast<const void *>(conv_output),
+                          static_cast<const void *>(conv_input),
+                          static_cast<const void *>(pre_input),
+                          static_cast<const void *>(pre_input_gradient),
+                          static_cast<const void *>(conv_output_gradient)})
+      OXH_REQUIRE(p == nullptr ||
+                      !oxh::any_overlap(conv_input_gradient, in_bytes, p,
+                                        (p == conv_input || p == pre_input ||
+                                         p == pre_input_gradient)
+                                            ? in_bytes
+                                            : out_bytes),
+                  OXH_INVALID_SHAPE,
+                  std::string(name) + ": conv_input_gradient overlaps another tensor");
+  OXH_REQUIRE(addend == nullptr || addend == conv_input_gradient ||
+                  !oxh::any_overlap(pre_input_gradient, in_bytes, addend, in_bytes),
+              OXH_INVALID_SHAPE, std::string(name) + ": addend overlaps a gradient");
   hipStream_t st = oxh::as_stream(stream);
   const BackwardArgs a{gradient, relu_output, conv_output, bn_weight, saved_mean,
-                       saved_inverse_std, conv_input, conv_weight, nullptr,
+                       saved_inverse_std, conv_input, conv_weight, addend,
                        conv_output_gradient, bn_weight_gradient, bn_bias_gradient,
-                       conv_bias_gradient, conv_weight_gradient, nullptr};
+                       conv_bias_gradient, conv_weight_gradient, conv_input_gradient};
   const PreBnBackward pre{pre_input, pre_weight, pre_saved_mean, pre_saved_inverse_std,
                           pre_weight_gradient, pre_bias_gradient, pre_input_gradient,
                           pre_input_gradient_sum};

@@ -608,23 +608,34 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
   // on planes of at most 2048 values per channel: it runs inside that layer's launches (its
   // statistics, output and backward per channel, in the same workgroup as the layer's channel);
   // in either pass nothing reads its output or writes its inputs in between
+  // The layer's input may be the BN's output, its ReLU's, or a residual add's whose first
+  // operand is the BN (BN + add as one pass); other consumers of that input must come after the
+  // layer, so that in the backward their gradient contributions are in place (written, or
+  // waiting as an add's) when the fused launch adds them to the layer's input gradient.
+  std::vector<int64_t> first_consumer(n, -1);
+  for (size_t i = 0; i < n; ++i)
+    if (active[i])
+      for (int k : g.nodes[i].in)
+        if (first_consumer[k] < 0) first_consumer[k] = static_cast<int64_t>(i);
   std::vector<int64_t> pre_bn_of(n, -1);  // fused depthwise convolution -> BN in front
   std::vector<char> pre_fused(n, 0);      // that BN and its ReLU: no launch of their own
   for (size_t i = 0; i < n; ++i) {
     if (!dw_conv[i]) continue;
     const int cin = g.nodes[i].in[0];
+    if (first_consumer[cin] != static_cast<int64_t>(i)) continue;
     int b1 = -1;
-    if (fused_relu[cin] && consumers[cin] == 1)
+    if (fused_relu[cin])
       b1 = g.nodes[cin].in[0];
-    else if (train_bn(cin) && !fused_bn[cin] && bn_into_add[cin] < 0 && dw_conv_of[cin] < 0 &&
-             consumers[cin] == 1)
+    else if (train_bn(cin) && !fused_bn[cin] && bn_into_add[cin] < 0 && dw_conv_of[cin] < 0)
       b1 = cin;
+    else if (g.nodes[cin].op == Op::Add && add_absorbed[cin])
+      b1 = g.nodes[cin].in[0];
     if (b1 < 0 || dw_conv_of[b1] >= 0) continue;
     const oxh_conv2d_shape s = conv_shape(g, g.nodes[i]);
     if (!oxh_batch_norm_depthwise_conv_batch_norm_supported(&s)) continue;
     pre_bn_of[i] = b1;
     pre_fused[b1] = 1;
-    pre_fused[cin] = 1;
+    if (g.nodes[cin].op != Op::Add) pre_fused[cin] = 1;  // an add keeps its backward
   }
   // gradient buffers, consumers before producers
   std::vector<int64_t> grad_of(n, -1);  // node whose grad buffer this node uses (-1: own)
@@ -963,23 +974,32 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
           if (pre_bn_of[ci] >= 0) {  // the BN (+ ReLU) in front, inside the same launch
             const int b1 = static_cast<int>(pre_bn_of[ci]);
             const Node &pb = g.nodes[b1];
-            const bool prelu = cv.in[0] != b1;
+            const Node &pin = g.nodes[cv.in[0]];
+            const bool padd = pin.op == Op::Add;  // BN + residual add in front
+            const bool prelu = cv.in[0] != b1 && !padd;
             const float *px = p.value[pb.in[0]], *pw = p.value[pb.in[1]],
                         *pbb = p.value[pb.in[2]];
+            const float *pres = padd ? p.value[pin.in[1]] : nullptr;
             float *psm = p.saved_mean[b1], *psi = p.saved_inv[b1];
             float *prm = pb.running_mean, *prv = pb.running_variance;
             float *py = const_cast<float *>(cx);
             const float pmom = pb.momentum, peps = pb.epsilon;
             const uint64_t PC = pb.shape[1];
-            op.kind = std::string(prelu ? "batch_norm2d_relu_" : "batch_norm2d_") +
+            op.kind = std::string(prelu ? "batch_norm2d_relu_" : padd ? "batch_norm2d_add_"
+                                                                       : "batch_norm2d_") +
                       (fused ? "depthwise_conv2d_batch_norm_relu_forward"
                              : "depthwise_conv2d_batch_norm_forward");
-            op.name = (prelu ? name("bn", b1) + "+" + name("relu", cv.in[0]) : name("bn", b1)) +
+            op.name = (prelu  ? name("bn", b1) + "+" + name("relu", cv.in[0])
+                       : padd ? name("bn", b1) + "+" + name("add", cv.in[0])
+                              : name("bn", b1)) +
                       "+" + op.name;
             op.tensors.erase(op.tensors.begin());  // the layer's input is pre_y, written here
             op.tensors.push_back(ref("pre_x", const_cast<float *>(px), g.nodes[pb.in[0]], 0));
             op.tensors.push_back(ref("pre_weight", const_cast<float *>(pw), g.nodes[pb.in[1]], 0));
             op.tensors.push_back(ref("pre_bias", const_cast<float *>(pbb), g.nodes[pb.in[2]], 0));
+            if (padd)
+              op.tensors.push_back(ref("pre_residual", const_cast<float *>(pres),
+                                       g.nodes[pin.in[1]], 0));
             op.tensors.push_back(ref("pre_y", py, g.nodes[cv.in[0]], 1));
             op.tensors.push_back(ref_flat("pre_saved_mean", psm, PC, 1));
             op.tensors.push_back(ref_flat("pre_saved_inverse_std", psi, PC, 1));
@@ -989,7 +1009,7 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
             op.attrs.push_back({"pre_epsilon", peps});
             op.launch = [=](hipStream_t st) {
               return oxh_batch_norm_depthwise_conv_batch_norm_forward_train(
-                  st, &s, prelu ? 1 : 0, pmom, peps, px, pw, pbb, prm, prv, psm, psi, py,
+                  st, &s, prelu ? 1 : 0, pmom, peps, px, pw, pbb, pres, prm, prv, psm, psi, py,
                   fused ? 1 : 0, mom, eps, cw, cb, cy, w, b, rm, rv, sm, si, out);
             };
             ops.push_back(std::move(op));
@@ -1199,8 +1219,27 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
           if (pre_bn_of[xin] >= 0) {  // with the BN (+ ReLU) in front, in the same launch
             const int b1 = static_cast<int>(pre_bn_of[xin]);
             const Node &pb = g.nodes[b1];
-            const bool prelu = cin != b1;
+            const bool padd = g.nodes[cin].op == Op::Add;
+            const bool prelu = cin != b1 && !padd;
             const int px_node = pb.in[0];
+            // the layer input's other gradient contributions (its later consumers', already
+            // made) are added to the layer's input gradient; an add in front keeps its node's
+            // gradient (its second operand takes it)
+            const float *addend = nullptr;
+            if (pending[cin].gradient != nullptr && !written[cin]) {
+              addend = pending[cin].gradient;
+              op.tensors.push_back(ref("addend", const_cast<float *>(addend),
+                                       g.nodes[pending[cin].add], 0));
+              pending[cin] = Pending{};
+            } else if (written[cin]) {
+              addend = p.grad[cin];
+              op.tensors.push_back(ref("addend", const_cast<float *>(addend), g.nodes[cin], 0));
+            }
+            float *cdx = nullptr;
+            if (padd) {
+              cdx = p.grad[cin];
+              written[cin] = 1;
+            }
             const float *px = p.value[px_node], *pw = p.value[pb.in[1]];
             const float *psm = p.saved_mean[b1], *psi = p.saved_inv[b1];
             const uint64_t PC = pb.shape[1];
@@ -1216,11 +1255,14 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
               side(src.in[2], pconv_db, "pre_conv_bias_gradient");
               conv_bias_done[px_node] = 1;
             }
-            op.kind = std::string(prelu ? "batch_norm2d_relu_" : "batch_norm2d_") +
+            op.kind = std::string(prelu ? "batch_norm2d_relu_" : padd ? "batch_norm2d_add_"
+                                                                       : "batch_norm2d_") +
                       (fused ? "depthwise_conv2d_batch_norm_relu_backward"
                              : "depthwise_conv2d_batch_norm_backward");
-            op.name = (prelu ? name("bn", b1) + "+" + name("relu", cin) : name("bn", b1)) + "+" +
-                      name("conv", xin) + "+" + name("bn", bi) +
+            op.name = (prelu  ? name("bn", b1) + "+" + name("relu", cin)
+                       : padd ? name("bn", b1) + "+" + name("add", cin)
+                              : name("bn", b1)) +
+                      "+" + name("conv", xin) + "+" + name("bn", bi) +
                       (fused ? "+" + name("relu", r) : "") + ".backward";
             op.tensors.push_back(ref("gradient", const_cast<float *>(gr), x, 0));
             if (fused) op.tensors.push_back(ref("y", const_cast<float *>(y), x, 0));
@@ -1243,12 +1285,15 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
             op.tensors.push_back(ref_flat("pre_bias_gradient", pdb, PC, 1));
             if (pconv_db)
               op.tensors.push_back(ref_flat("pre_conv_bias_gradient", pconv_db, PC, 1));
+            if (cdx)
+              op.tensors.push_back(ref("conv_input_gradient", cdx, g.nodes[cin],
+                                       addend == cdx ? 2 : 1));
             op.tensors.push_back(ref("contribution", dst, g.nodes[px_node], 1));
             op.attrs = conv_attrs(cv);
             emit(std::move(op), acc, g.nodes[px_node], [=](hipStream_t st) {
               return oxh_batch_norm_depthwise_conv_batch_norm_backward_train(
-                  st, &s, gr, y, xi, w, sm, si, cx, cw, prelu ? 1 : 0, px, pw, psm, psi, cgr, dg,
-                  db, cdb, cdw, pdg, pdb, dst, pconv_db);
+                  st, &s, gr, y, xi, w, sm, si, cx, cw, addend, prelu ? 1 : 0, px, pw, psm, psi,
+                  cgr, dg, db, cdb, cdw, cdx, pdg, pdb, dst, pconv_db);
             });
             break;
           }

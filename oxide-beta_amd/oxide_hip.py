@@ -175,9 +175,9 @@ _SIGNATURES = {
                                                            _vp, _vp, _vp]),
     "oxh_batch_norm_depthwise_conv_batch_norm_supported": (_int, [_CS]),
     "oxh_batch_norm_depthwise_conv_batch_norm_forward_train": (
-        _st, [_vp, _CS, _int, _f32, _f32] + [_vp] * 8 + [_int, _f32, _f32] + [_vp] * 10),
+        _st, [_vp, _CS, _int, _f32, _f32] + [_vp] * 9 + [_int, _f32, _f32] + [_vp] * 10),
     "oxh_batch_norm_depthwise_conv_batch_norm_backward_train": (
-        _st, [_vp, _CS] + [_vp] * 8 + [_int] + [_vp] * 13),
+        _st, [_vp, _CS] + [_vp] * 9 + [_int] + [_vp] * 14),
     "oxh_avg_pool2d_forward": (_st, [_vp, _PS, _vp, _vp]),
     "oxh_avg_pool2d_backward": (_st, [_vp, _PS, _vp, _vp]),
     "oxh_initialized_weights": (_st, [ctypes.POINTER(_u64), _u64, ctypes.POINTER(_f32)]),
@@ -780,15 +780,17 @@ class LoadedModule:
     def batch_norm_depthwise_conv_batch_norm_forward_train(self, shape, pre, layer,
                                                            stream=None):
         """A BatchNorm (+ ReLU) feeding a depthwise ConvNormAct, in one launch with it.
-        ``pre``: dict relu, momentum, epsilon, x, weight, bias, running_mean,
-        running_variance, saved_mean, saved_inverse_std, out; ``layer``: dict relu, momentum,
+        ``pre``: dict relu, momentum, epsilon, x, weight, bias, residual (optional),
+        running_mean, running_variance, saved_mean, saved_inverse_std, out; ``layer``: dict
+        relu, momentum,
         epsilon, conv_weight, conv_bias, conv_out, weight, bias, running_mean,
         running_variance, saved_mean, saved_inverse_std, out."""
         p, q = pre, layer
         check(lib().oxh_batch_norm_depthwise_conv_batch_norm_forward_train(
             _stream(stream), ctypes.byref(shape), int(p["relu"]), p["momentum"], p["epsilon"],
-            *[_ptr(p[k]) for k in ("x", "weight", "bias", "running_mean", "running_variance",
-                                   "saved_mean", "saved_inverse_std", "out")],
+            _ptr(p["x"]), _ptr(p["weight"]), _ptr(p["bias"]), _ptr(p.get("residual")),
+            *[_ptr(p[k]) for k in ("running_mean", "running_variance", "saved_mean",
+                                   "saved_inverse_std", "out")],
             int(q["relu"]), q["momentum"], q["epsilon"],
             *[_ptr(q[k]) for k in ("conv_weight", "conv_bias", "conv_out", "weight", "bias",
                                    "running_mean", "running_variance", "saved_mean",
@@ -797,8 +799,9 @@ class LoadedModule:
     def batch_norm_depthwise_conv_batch_norm_backward_train(self, shape, layer, pre,
                                                             stream=None):
         """Its backward.  ``layer``: dict gradient, relu_out (or None), conv_out, weight,
-        saved_mean, saved_inverse_std, conv_in, conv_weight, conv_out_gradient (or None),
-        weight_gradient, bias_gradient, conv_bias_gradient, conv_weight_gradient; ``pre``:
+        saved_mean, saved_inverse_std, conv_in, conv_weight, addend and conv_in_gradient
+        (optional), conv_out_gradient (or None), weight_gradient, bias_gradient,
+        conv_bias_gradient, conv_weight_gradient; ``pre``:
         dict relu, x, weight, saved_mean, saved_inverse_std, weight_gradient, bias_gradient,
         input_gradient, input_gradient_sum (or None)."""
         q, p = layer, pre
@@ -806,10 +809,11 @@ class LoadedModule:
             _stream(stream), ctypes.byref(shape),
             *[_ptr(q[k]) for k in ("gradient", "relu_out", "conv_out", "weight", "saved_mean",
                                    "saved_inverse_std", "conv_in", "conv_weight")],
-            int(p["relu"]),
+            _ptr(q.get("addend")), int(p["relu"]),
             *[_ptr(p[k]) for k in ("x", "weight", "saved_mean", "saved_inverse_std")],
             *[_ptr(q[k]) for k in ("conv_out_gradient", "weight_gradient", "bias_gradient",
                                    "conv_bias_gradient", "conv_weight_gradient")],
+            _ptr(q.get("conv_in_gradient")),
             *[_ptr(p[k]) for k in ("weight_gradient", "bias_gradient", "input_gradient",
                                    "input_gradient_sum")]))
 

@@ -485,9 +485,10 @@ def op_bytes(op: Op) -> tuple[str, int]:
     if k == "batch_norm2d_relu_backward":
         return "batch_norm2d", 4 * nb(op.reads["x"]) + acc                 # g, y, x in; dx out
     if k.startswith("batch_norm2d") and "depthwise" in k and k.endswith("forward"):
-        # BN input in; its output, the convolution output and the layer output out
+        # BN input (and residual) in; its output, the convolution output and the layer output
         return ("batch_norm2d+conv2d+batch_norm2d",
-                2 * nb(op.reads["pre_x"]) + 2 * nb(op.writes["y"]))
+                (2 + ("pre_residual" in op.reads)) * nb(op.reads["pre_x"]) +
+                2 * nb(op.writes["y"]))
     if k.startswith("batch_norm2d") and "depthwise" in k:
         # g (, y), convolution output, its input and the BN input in; output gradients out
         outs = nb(op.reads["gradient"]) * (3 + ("y" in op.reads))

@@ -197,14 +197,21 @@ class OracleChecker:
         BatchNorm checked as its own forward (statistics, output, running update), then the
         layer from the output it wrote."""
         a, w = op.attrs, op.writes
-        out = dict(y=host(w["pre_y"]), mean=host(w["pre_saved_mean"]),
+        pre_y = host(w["pre_y"])
+        out = dict(y=pre_y, mean=host(w["pre_saved_mean"]),
                    inv=host(w["pre_saved_inverse_std"]), rm=host(a["pre_running_mean"]),
                    rv=host(a["pre_running_variance"]))
+        if "pre_residual" in r:  # BN + residual add: the normalized values, then the add
+            x, gamma, beta = r["pre_x"], r["pre_weight"], r["pre_bias"]
+            sh = (1, x.shape[1], 1, 1)
+            out["y"] = ((x - out["mean"].reshape(sh)) * out["inv"].reshape(sh)) * \
+                gamma.reshape(sh) + beta.reshape(sh)
+            assert_bitexact(pre_y, oracle.add(out["y"], r["pre_residual"]), f"{op.name} add")
         check_batch_norm_forward(out, r["pre_x"], r["pre_weight"], r["pre_bias"],
                                  self.prior[id(a["pre_running_mean"])],
                                  self.prior[id(a["pre_running_variance"])], a["pre_momentum"],
                                  a["pre_epsilon"], relu=pre_relu)
-        self._depthwise_forward(op, dict(r, x=out["y"]), relu)
+        self._depthwise_forward(op, dict(r, x=pre_y), relu)
         self.counts["batch norm before depthwise"] += 1
 
     def _pre_backward(self, op, r, pre_relu, relu):
@@ -214,7 +221,18 @@ class OracleChecker:
         convolution feeding it as that BatchNorm backward's dx sum."""
         w = op.writes
         da = self._depthwise_backward(op, r, relu, input_gradient=False)
-        g = oracle.relu_backward(da, r["x"]) if pre_relu else da
+        whole = da
+        inplace = op.by_role.get("conv_input_gradient", [None])[0]
+        if "addend" in r:  # the layer input's other contributions (before an in-place update)
+            addend = r["addend"]
+            if inplace is not None and id(inplace) in self.prior and \
+                    op.by_role["addend"][0].ptr == inplace.ptr:
+                addend = self.prior[id(inplace)]
+            whole = oracle.accumulate(addend, da)
+            self.counts["conv input backward with addend"] += 1
+        if inplace is not None:
+            assert_bitexact(host(inplace), whole, f"{op.name} layer input gradient")
+        g = oracle.relu_backward(whole, r["x"]) if pre_relu else whole
         dx = host(w["contribution"])
         check_batch_norm_backward(dict(dx=dx, dw=host(w["pre_weight_gradient"]),
                                        db=host(w["pre_bias_gradient"])), g, r["pre_x"],
@@ -226,6 +244,18 @@ class OracleChecker:
                           f"{op.name} conv bias in front")
             self.counts["conv bias in batch norm backward"] += 1
         self.counts["batch norm before depthwise"] += 1
+
+    def batch_norm2d_add_depthwise_conv2d_batch_norm_relu_forward(self, op, r):
+        self._pre_forward(op, r, False, True)
+
+    def batch_norm2d_add_depthwise_conv2d_batch_norm_forward(self, op, r):
+        self._pre_forward(op, r, False, False)
+
+    def batch_norm2d_add_depthwise_conv2d_batch_norm_relu_backward(self, op, r):
+        self._pre_backward(op, r, False, True)
+
+    def batch_norm2d_add_depthwise_conv2d_batch_norm_backward(self, op, r):
+        self._pre_backward(op, r, False, False)
 
     def batch_norm2d_relu_depthwise_conv2d_batch_norm_relu_forward(self, op, r):
         self._pre_forward(op, r, True, True)

@@ -212,14 +212,18 @@ PRE_SHAPES = [
 
 
 @pytest.mark.parametrize("case", PRE_SHAPES)
-@pytest.mark.parametrize("pre_relu,relu", [(True, True), (False, True), (True, False)])
+@pytest.mark.parametrize("pre_relu,relu,residual", [(True, True, False), (False, True, False),
+                                                    (True, False, False), (False, True, True),
+                                                    (False, False, True)])
 def test_batch_norm_feeding_depthwise_layer_equals_separate_launches(module, dev, case, pre_relu,
-                                                                     relu):
-    """oxh_batch_norm_depthwise_conv_batch_norm_{forward,backward}_train: the BatchNorm (+ ReLU)
-    in front of a depthwise ConvNormAct run inside that layer's launches writes exactly what the
-    separate BatchNorm and depthwise-layer launches write (the same channel arithmetic), in
-    both directions; the BatchNorm in front against the oracle too."""
-    r = np.random.default_rng(hash((case, pre_relu, relu)) & 0xFFFFFF)
+                                                                     relu, residual):
+    """oxh_batch_norm_depthwise_conv_batch_norm_{forward,backward}_train: the BatchNorm (+ ReLU,
+    or + a residual add) in front of a depthwise ConvNormAct run inside that layer's launches
+    writes exactly what the separate BatchNorm and depthwise-layer launches write (the same
+    channel arithmetic), in both directions, with the layer input's other gradient
+    contributions (an addend) folded in where there is a residual; the BatchNorm in front
+    against the oracle too."""
+    r = np.random.default_rng(hash((case, pre_relu, relu, residual)) & 0xFFFFFF)
     sh, oshape, d = _case(r, *case)
     b, c = case[0], case[1]
     ishape = (b, c, case[2], case[3])
@@ -228,6 +232,8 @@ def test_batch_norm_feeding_depthwise_layer_equals_separate_launches(module, dev
     b1 = r.uniform(-0.3, 0.3, c).astype(np.float32)
     rm1 = r.uniform(-0.5, 0.5, c).astype(np.float32)
     rv1 = r.uniform(0.5, 2.0, c).astype(np.float32)
+    res = r.standard_normal(ishape).astype(np.float32)
+    other = r.standard_normal(ishape).astype(np.float32)  # the input's other contributions
     t = {k: to_dev(v, dev) for k, v in d.items()}
     e = lambda s: torch.empty(s, device=dev)  # noqa: E731
 
@@ -236,13 +242,15 @@ def test_batch_norm_feeding_depthwise_layer_equals_separate_launches(module, dev
                  rm2=t["rm"].clone(), rv2=t["rv"].clone(), sm1=e(c), si1=e(c), a1=e(ishape),
                  conv=e(oshape), y2=e(oshape), sm2=e(c), si2=e(c), gconv=e(oshape),
                  dg2=e(c), db2=e(c), dcb=e(c), dcw=torch.empty_like(t["cw"]), dg1=e(c),
-                 db1=e(c), dy1=e(ishape), dsum=e(c))
+                 db1=e(c), dy1=e(ishape), dsum=e(c), da1=e(ishape))
         g1d, b1d = to_dev(g1, dev), to_dev(b1, dev)
+        resd, otherd = (to_dev(res, dev), to_dev(other, dev)) if residual else (None, None)
         if fused:
             module.batch_norm_depthwise_conv_batch_norm_forward_train(
                 sh, dict(relu=pre_relu, momentum=0.1, epsilon=1e-5, x=s["y1"], weight=g1d,
-                         bias=b1d, running_mean=s["rm1"], running_variance=s["rv1"],
-                         saved_mean=s["sm1"], saved_inverse_std=s["si1"], out=s["a1"]),
+                         bias=b1d, residual=resd, running_mean=s["rm1"],
+                         running_variance=s["rv1"], saved_mean=s["sm1"],
+                         saved_inverse_std=s["si1"], out=s["a1"]),
                 dict(relu=relu, momentum=0.1, epsilon=1e-5, conv_weight=t["cw"],
                      conv_bias=t["cb"], conv_out=s["conv"], weight=t["gamma"], bias=t["beta"],
                      running_mean=s["rm2"], running_variance=s["rv2"], saved_mean=s["sm2"],
@@ -252,31 +260,40 @@ def test_batch_norm_feeding_depthwise_layer_equals_separate_launches(module, dev
                          weight=t["gamma"], saved_mean=s["sm2"], saved_inverse_std=s["si2"],
                          conv_in=s["a1"], conv_weight=t["cw"], conv_out_gradient=s["gconv"],
                          weight_gradient=s["dg2"], bias_gradient=s["db2"],
-                         conv_bias_gradient=s["dcb"], conv_weight_gradient=s["dcw"]),
+                         conv_bias_gradient=s["dcb"], conv_weight_gradient=s["dcw"],
+                         addend=otherd, conv_in_gradient=s["da1"] if residual else None),
                 dict(relu=pre_relu, x=s["y1"], weight=g1d, saved_mean=s["sm1"],
                      saved_inverse_std=s["si1"], weight_gradient=s["dg1"], bias_gradient=s["db1"],
                      input_gradient=s["dy1"], input_gradient_sum=s["dsum"]))
         else:
-            fwd = (module.batch_norm_relu_forward_train if pre_relu
-                   else module.batch_norm_forward_train)
-            fwd(s["y1"], g1d, b1d, s["rm1"], s["rv1"], s["sm1"], s["si1"], s["a1"])
+            if residual:
+                module.batch_norm_add_forward_train(s["y1"], g1d, b1d, s["rm1"], s["rv1"],
+                                                    s["sm1"], s["si1"], resd, s["a1"])
+            else:
+                fwd = (module.batch_norm_relu_forward_train if pre_relu
+                       else module.batch_norm_forward_train)
+                fwd(s["y1"], g1d, b1d, s["rm1"], s["rv1"], s["sm1"], s["si1"], s["a1"])
             module.depthwise_conv_batch_norm_forward_train(
                 sh, relu, 0.1, 1e-5, s["a1"], t["cw"], t["cb"], s["conv"], t["gamma"], t["beta"],
                 s["rm2"], s["rv2"], s["sm2"], s["si2"], s["y2"])
-            da1 = e(ishape)
             module.depthwise_conv_batch_norm_backward_train(
                 sh, t["g"], s["y2"] if relu else None, s["conv"], t["gamma"], s["sm2"], s["si2"],
-                s["a1"], t["cw"], None, s["gconv"], s["dg2"], s["db2"], s["dcb"], s["dcw"], da1)
+                s["a1"], t["cw"], otherd, s["gconv"], s["dg2"], s["db2"], s["dcb"], s["dcw"],
+                s["da1"])
             module.conv_batch_norm_backward_train(
-                da1, s["a1"] if pre_relu else None, s["y1"], g1d, s["sm1"], s["si1"], s["dy1"],
-                s["dg1"], s["db1"], s["dsum"])
+                s["da1"], s["a1"] if pre_relu else None, s["y1"], g1d, s["sm1"], s["si1"],
+                s["dy1"], s["dg1"], s["db1"], s["dsum"])
         torch.cuda.synchronize()
         return {k: host(v) for k, v in s.items()}
 
     fused, separate = run(True), run(False)
     for k in separate:
+        if k == "da1" and not residual:
+            continue  # not formed by the fused launch without a residual
         assert_bitexact(fused[k], separate[k], k)
     # the BatchNorm in front against the oracle (its statistics and output)
-    check_batch_norm_forward(dict(y=fused["a1"], mean=fused["sm1"], inv=fused["si1"],
-                                  rm=fused["rm1"], rv=fused["rv1"]),
-                             y1, g1, b1, rm1, rv1, relu=pre_relu)
+    bn_out = fused["a1"] - res if residual else fused["a1"]
+    if not residual:
+        check_batch_norm_forward(dict(y=bn_out, mean=fused["sm1"], inv=fused["si1"],
+                                      rm=fused["rm1"], rv=fused["rv1"]),
+                                 y1, g1, b1, rm1, rv1, relu=pre_relu)

@@ -32,9 +32,9 @@ def _mnist_batch(r, n):
 
 # Every convolution but the stem (whose input, the image, takes no gradient) forms its weight
 # and input gradients in one launch group.
-# The 11 UIB expand BatchNorms (+ ReLU) in front of a middle depthwise layer, and the second
-# fused block's last BatchNorm in front of the first UIB's start depthwise layer, run inside
-# that layer's launches.
+# The BatchNorm in front of each of the 15 depthwise layers runs inside that layer's launches:
+# the 11 UIB expand BatchNorms (+ ReLU) before the middle depthwise layers, and before the 4
+# start depthwise layers the previous block's last BatchNorm (2 with the residual add).
 # 46 BatchNorms, 32 of them followed by a ReLU (fused), each fed by a convolution whose bias
 # gradient its backward forms (the classifier's, fed by no BN, stays with its parameter
 # backward); the 15 depthwise convolutions run with their BatchNorm + ReLU in one launch per
@@ -42,17 +42,17 @@ def _mnist_batch(r, n):
 # operand's gradient is the add's own buffer and whose second operand's is added by that
 # operand's convolution input backward (no add launches in either direction)
 EXPECTED_KINDS = {"conv2d_forward": 32, "conv2d_parameter_backward": 1,
-                  "conv2d_backward": 31, "batch_norm2d_forward": 3,
-                  "batch_norm2d_add_forward": 10,
-                  "batch_norm2d_relu_forward": 6, "batch_norm2d_backward": 13,
+                  "conv2d_backward": 31, "batch_norm2d_forward": 2,
+                  "batch_norm2d_add_forward": 8,
+                  "batch_norm2d_relu_forward": 6, "batch_norm2d_backward": 10,
                   "batch_norm2d_relu_backward": 6,
-                  "depthwise_conv2d_batch_norm_relu_forward": 3,
-                  "depthwise_conv2d_batch_norm_relu_backward": 3,
                   "batch_norm2d_relu_depthwise_conv2d_batch_norm_relu_forward": 11,
                   "batch_norm2d_relu_depthwise_conv2d_batch_norm_relu_backward": 11,
-                  "batch_norm2d_depthwise_conv2d_batch_norm_relu_forward": 1,
-                  "batch_norm2d_depthwise_conv2d_batch_norm_relu_backward": 1,
-                  "batch norm before depthwise": 24,
+                  "batch_norm2d_depthwise_conv2d_batch_norm_relu_forward": 2,
+                  "batch_norm2d_depthwise_conv2d_batch_norm_relu_backward": 2,
+                  "batch_norm2d_add_depthwise_conv2d_batch_norm_relu_forward": 2,
+                  "batch_norm2d_add_depthwise_conv2d_batch_norm_relu_backward": 2,
+                  "batch norm before depthwise": 30,
                   "conv input backward with addend": 10,
                   "avg_pool2d_forward": 1, "avg_pool2d_backward": 1, "cross_entropy": 1,
                   "adamw": 1, "conv bias in parameter backward": 1,
