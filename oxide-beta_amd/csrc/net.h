@@ -148,7 +148,7 @@ struct oxh_program {
   oxh::net::AdamConfig adam_config;
   std::vector<oxh_adamw_tensor> adam;
   oxh_adamw_tensor *adam_table = nullptr;  // device copy of `adam`
-  uint32_t *adam_starts = nullptr, *adam_ticket = nullptr;
+  uint32_t *adam_starts = nullptr;
   uint64_t adam_chunks = 0;
   int32_t *step = nullptr;
   uint32_t *error_flag = nullptr;  // raised by a cross entropy with an invalid target

@@ -700,7 +700,7 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
                adam ? static_cast<int64_t>(a.reserve(bytes)) : -1};
   }
   const uint64_t scratch_off = a.reserve(largest * 4), one_off = a.reserve(4),
-                 step_off = a.reserve(4), flag_off = a.reserve(4), ticket_off = a.reserve(4);
+                 step_off = a.reserve(4), flag_off = a.reserve(4);
   const uint64_t table_off = a.reserve(std::max<size_t>(trained.size(), 1) *
                                        sizeof(oxh_adamw_tensor));
   const uint64_t starts_off = a.reserve((trained.size() + 1) * 4);
@@ -764,7 +764,6 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
   float *one = a.at<float>(one_off);
   p.step = a.at<int32_t>(step_off);
   p.error_flag = a.at<uint32_t>(flag_off);
-  p.adam_ticket = a.at<uint32_t>(ticket_off);
   p.adam_table = a.at<oxh_adamw_tensor>(table_off);
   p.adam_starts = a.at<uint32_t>(starts_off);
   p.root = root;
@@ -1533,7 +1532,7 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
       const AdamConfig &c = self->adam_config;
       return oxh_adamw_multi_tensor_table_step(
           s, c.learning_rate, c.weight_decay, c.beta1, c.beta2, c.epsilon, self->step,
-          self->adam_ticket, self->adam_table, self->adam_starts,
+          self->adam_table, self->adam_starts,
           static_cast<uint32_t>(self->adam.size()), self->adam_chunks);
     };
     ops.push_back(std::move(op));

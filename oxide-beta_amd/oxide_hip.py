@@ -154,7 +154,7 @@ _SIGNATURES = {
     "oxh_adamw_table_layout": (_st, [ctypes.POINTER(AdamWTensor), _u32, ctypes.POINTER(_u32),
                                      ctypes.POINTER(_u64)]),
     "oxh_adamw_multi_tensor_table_step": (_st, [_vp, _f32, _f32, _f32, _f32, _f32, _vp, _vp,
-                                                _vp, _vp, _u32, _u64]),
+                                                _vp, _u32, _u64]),
     "oxh_adamw_multi_tensor_step": (_st, [_vp, _f32, _f32, _f32, _f32, _f32, _vp,
                                           ctypes.POINTER(AdamWTensor), _u32]),
     "oxh_conv2d_output_size": (_st, [_CS, ctypes.POINTER(_u64), ctypes.POINTER(_u64)]),
@@ -691,7 +691,7 @@ class LoadedModule:
                                                 table, len(tensors)))
 
     def adamw_table_step(self, learning_rate, weight_decay, beta1, beta2, epsilon, step_counter,
-                         ticket, tensors, stream=None):
+                         tensors, stream=None):
         """The device-table variant: the table and its chunk starts are copied to the device
         (kept alive on the returned object until the launch completes)."""
         import torch
@@ -709,7 +709,7 @@ class LoadedModule:
         torch.cuda.synchronize()
         check(lib().oxh_adamw_multi_tensor_table_step(
             _stream(stream), learning_rate, weight_decay, beta1, beta2, epsilon,
-            _ptr(step_counter), _ptr(ticket), dev_table.data_ptr(), dev_starts.data_ptr(),
+            _ptr(step_counter), dev_table.data_ptr(), dev_starts.data_ptr(),
             count, total.value))
         return dev_table, dev_starts
 

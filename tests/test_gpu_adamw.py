@@ -114,8 +114,7 @@ def test_adamw_table_step_matches_multi_tensor_step(module, dev, rng, table):
     """The one-launch device-table update equals the step-counting multi-tensor update bit for
     bit over three steps (186 tensors as in config 5, more than one 48-tensor launch of the
     latter; and 700 tensors of 1 to 5000 values, whose chunk search takes two rounds of the
-    block's 256 probes); the step counter advances once per launch and the ticket returns to
-    zero."""
+    block's 256 probes); the step counter advances once per call."""
     if table == "config5":
         sizes = CONFIG5_SIZES
         assert len(sizes) == 186
@@ -126,14 +125,12 @@ def test_adamw_table_step_matches_multi_tensor_step(module, dev, rng, table):
     b = [tuple(to_dev(x, dev) for x in s) for s in state]
     step_a = torch.zeros(1, dtype=torch.int32, device=dev)
     step_b = torch.zeros(1, dtype=torch.int32, device=dev)
-    ticket = torch.zeros(1, dtype=torch.int32, device=dev)
     for _ in range(3):
         module.adamw_multi_tensor_step(LR, 1e-4, B1, B2, EPS, step_a, a)
-        keep = module.adamw_table_step(LR, 1e-4, B1, B2, EPS, step_b, ticket, b)
+        keep = module.adamw_table_step(LR, 1e-4, B1, B2, EPS, step_b, b)
         torch.cuda.synchronize()
         del keep
     assert int(host(step_a)[0]) == int(host(step_b)[0]) == 3
-    assert int(host(ticket)[0]) == 0
     for i, (ta, tb) in enumerate(zip(a, b)):
         for k, what in ((0, "param"), (2, "m"), (3, "v")):
             assert_bitexact(host(tb[k]), host(ta[k]), f"tensor {i} {what}")
