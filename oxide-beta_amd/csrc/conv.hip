@@ -215,6 +215,9 @@ __global__ __launch_bounds__(256) void conv2d_input_backward_taps_kernel(
 // -0.0f padding terms (bit-exact forward and input gradient).  kLdsFloats bounds one block's
 // staging.
 constexpr uint32_t kLdsFloats = 16384;  // 64 KB
+#ifndef OXH_TAP_PRED
+#define OXH_TAP_PRED 0
+#endif
 constexpr int kLdsR = 4;
 
 __device__ __forceinline__ uint32_t round4(uint32_t v) { return (v + 3) & ~3u; }
@@ -329,10 +332,19 @@ __global__ __launch_bounds__(256) void conv2d_forward_lds_kernel(
       for (int t = 0; t < T; ++t) {
         const float xv = xp[off[t]];
         const float4 w4 = *reinterpret_cast<const float4 *>(wp + t * ocp);
+#if OXH_TAP_PRED
+        if (mask[t]) {
+          acc[0] += xv * w4.x;
+          acc[1] += xv * w4.y;
+          acc[2] += xv * w4.z;
+          acc[3] += xv * w4.w;
+        }
+#else
         acc[0] += tap_term(xv * w4.x, mask[t]);
         acc[1] += tap_term(xv * w4.y, mask[t]);
         acc[2] += tap_term(xv * w4.z, mask[t]);
         acc[3] += tap_term(xv * w4.w, mask[t]);
+#endif
       }
     }
 #pragma unroll
@@ -405,10 +417,19 @@ __global__ __launch_bounds__(256) void conv2d_forward_split_kernel(
       for (int t = 0; t < T; ++t) {
         const float xv = xp[off[t]];
         const float4 w4 = *reinterpret_cast<const float4 *>(wp + t * ocp);
+#if OXH_TAP_PRED
+        if (mask[t]) {
+          acc[0] += xv * w4.x;
+          acc[1] += xv * w4.y;
+          acc[2] += xv * w4.z;
+          acc[3] += xv * w4.w;
+        }
+#else
         acc[0] += tap_term(xv * w4.x, mask[t]);
         acc[1] += tap_term(xv * w4.y, mask[t]);
         acc[2] += tap_term(xv * w4.z, mask[t]);
         acc[3] += tap_term(xv * w4.w, mask[t]);
+#endif
       }
     }
     if (part > 0) {
@@ -483,10 +504,19 @@ __global__ __launch_bounds__(256) void conv2d_input_backward_lds_kernel(
       for (int t = 0; t < M * M; ++t) {
         const float gv = gp[goff[t]];
         const float4 w4 = *reinterpret_cast<const float4 *>(wp + woff[t]);
+#if OXH_TAP_PRED
+        if (mask[t]) {
+          acc[0] += gv * w4.x;
+          acc[1] += gv * w4.y;
+          acc[2] += gv * w4.z;
+          acc[3] += gv * w4.w;
+        }
+#else
         acc[0] += tap_term(gv * w4.x, mask[t]);
         acc[1] += tap_term(gv * w4.y, mask[t]);
         acc[2] += tap_term(gv * w4.z, mask[t]);
         acc[3] += tap_term(gv * w4.w, mask[t]);
+#endif
       }
     }
 #pragma unroll

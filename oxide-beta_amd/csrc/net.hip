@@ -296,6 +296,18 @@ std::vector<std::pair<std::string, double>> pool_attrs(const Node &x) {
           {"stride_w", static_cast<double>(x.stride_w)}};
 }
 
+// A node whose values are its input's, so it shares the input's storage and launches nothing:
+// a reshape (an alias, jit.rs:345) or an average pool with a 1 x 1 window that keeps every
+// position (each output is one input value divided by 1, evaluation.rs:405-445; the CPU sum
+// 0 + v turns -0 into +0, a difference the fp32 comparisons treat as none).  MobileNetV4's
+// global pool of a 1 x 1 plane is one.
+bool is_view(const Graph &g, const Node &x) {
+  if (x.op == Op::Reshape) return true;
+  if (x.op != Op::Pool || x.kernel_h != 1 || x.kernel_w != 1) return false;
+  const Node &in = g.nodes[x.in[0]];
+  return x.shape[2] == in.shape[2] && x.shape[3] == in.shape[3];
+}
+
 // The root's ancestors (collect_topological's reach, runtime.rs:1388-1476).
 std::vector<char> ancestors(const Graph &g, int root) {
   std::vector<char> active(g.nodes.size(), 0);
@@ -425,7 +437,7 @@ oxh_status build_forward(const Graph &g, int output, oxh_program &p) {
   for (size_t i = 0; i < n; ++i) {
     const Node &x = g.nodes[i];
     if (x.op == Op::Input) voff[i] = a.reserve(node_bytes(x));  // fed per run, even if unused
-    if (!active[i] || x.leaf() || x.op == Op::Reshape) continue;
+    if (!active[i] || x.leaf() || is_view(g, x)) continue;
     voff[i] = a.reserve(node_bytes(x));
     if (x.op == Op::Bn) {
       soff[i] = a.reserve(x.shape[1] * 4);
@@ -449,7 +461,7 @@ oxh_status build_forward(const Graph &g, int output, oxh_program &p) {
     if (voff[i] >= 0) p.value[i] = a.at<float>(voff[i]);
     if (soff[i] >= 0) p.saved_mean[i] = a.at<float>(soff[i]);
     if (ioff[i] >= 0) p.saved_inv[i] = a.at<float>(ioff[i]);
-    if (x.op == Op::Reshape) p.value[i] = p.value[x.in[0]];  // an alias (jit.rs:345)
+    if (is_view(g, x)) p.value[i] = p.value[x.in[0]];
   }
   p.error_flag = a.at<uint32_t>(flag_off);
   p.root = output;
@@ -457,7 +469,7 @@ oxh_status build_forward(const Graph &g, int output, oxh_program &p) {
   const uint64_t wsb = ws_bytes;
   for (size_t i = 0; i < n; ++i) {
     const Node &x = g.nodes[i];
-    if (!active[i] || x.leaf() || x.op == Op::Reshape) continue;
+    if (!active[i] || x.leaf() || is_view(g, x)) continue;
     switch (x.op) {
       case Op::Conv:
         p.ops.push_back(conv_forward_op(g, p.value, i));
@@ -641,7 +653,7 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
   std::vector<int64_t> grad_of(n, -1);  // node whose grad buffer this node uses (-1: own)
   std::vector<char> has_grad(n, 0);
   std::vector<char> aliased(n, 0);      // an add's first operand using the add's buffer
-  std::vector<char> reshape_alias(n, 0);  // a reshape whose input uses its buffer
+  std::vector<char> view_alias(n, 0);  // a view (is_view) whose input uses its buffer
   const bool root_fused_ce =
       g.nodes[root].op == Op::CrossEntropy && want(g.nodes[root].in[0]);
   for (size_t r = n; r-- > 0;) {
@@ -650,11 +662,11 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
     if (static_cast<int>(r) == root && root_fused_ce) continue;  // its outer gradient is 1
     if (x.op == Op::Param) continue;  // its gradient buffer is the optimizer's
     has_grad[r] = 1;
-    if (x.op == Op::Reshape) {
+    if (is_view(g, x)) {
       const int in = x.in[0];
       if (!g.nodes[in].leaf() && consumers[in] == 1 && want(in)) {
         grad_of[in] = grad_of[r] >= 0 ? grad_of[r] : static_cast<int64_t>(r);
-        reshape_alias[r] = 1;
+        view_alias[r] = 1;
       }
     } else if (x.op == Op::Add) {
       const int first = x.in[0];
@@ -681,7 +693,7 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
       smoff[i] = a.reserve(x.shape[1] * 4);
       sioff[i] = a.reserve(x.shape[1] * 4);
     }
-    if (x.leaf() || x.op == Op::Reshape || fused_bn[i]) continue;
+    if (x.leaf() || is_view(g, x) || fused_bn[i]) continue;
     voff[i] = a.reserve(node_bytes(x));
     if (x.op != Op::CrossEntropy) largest = std::max(largest, x.numel());
   }
@@ -745,7 +757,7 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
     if (goff[i] >= 0) p.grad[i] = a.at<float>(goff[i]);
   }
   for (size_t i = 0; i < n; ++i)
-    if (g.nodes[i].op == Op::Reshape) p.value[i] = p.value[g.nodes[i].in[0]];
+    if (is_view(g, g.nodes[i])) p.value[i] = p.value[g.nodes[i].in[0]];
   for (size_t i = 0; i < n; ++i)
     if (grad_of[i] >= 0) p.grad[i] = p.grad[grad_of[i]];
   std::vector<float *> pm(n, nullptr), pv(n, nullptr);
@@ -897,7 +909,7 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
   // forward
   for (size_t i = 0; i < n; ++i) {
     const Node &x = g.nodes[i];
-    if (!active[i] || x.leaf() || x.op == Op::Reshape || fused_bn[i] || add_absorbed[i] ||
+    if (!active[i] || x.leaf() || is_view(g, x) || fused_bn[i] || add_absorbed[i] ||
         dw_conv[i] || pre_fused[i])
       continue;
     float *out = p.value[i];
@@ -1101,15 +1113,17 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
     OXH_REQUIRE(written[r], OXH_TRACE, "a traced value receives no gradient");
     const float *gr = p.grad[r];
     OpRec op;
+    if (is_view(g, x)) {
+      if (view_alias[r]) {
+        written[x.in[0]] = 1;  // shares this gradient buffer
+      } else {
+        const bool reshape = x.op == Op::Reshape;
+        copy_contribution(reshape ? "reshape_backward" : "avg_pool2d_view_backward",
+                          name(reshape ? "reshape" : "pool", r) + ".backward", gr, x, x.in[0]);
+      }
+      continue;
+    }
     switch (x.op) {
-      case Op::Reshape:
-        if (reshape_alias[r]) {
-          written[x.in[0]] = 1;  // shares this gradient buffer
-        } else {
-          copy_contribution("reshape_backward", name("reshape", r) + ".backward", gr, x,
-                            x.in[0]);
-        }
-        break;
       case Op::CrossEntropy: {  // autograd.rs:529-554 with the node's gradient as outer
         const Node &ln = g.nodes[x.in[0]];
         const float *lg = p.value[x.in[0]], *tg = p.value[x.in[1]];

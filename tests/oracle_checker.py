@@ -344,6 +344,10 @@ class OracleChecker:
     def reshape_backward(self, op, r):
         assert_bitexact(host(op.writes["contribution"]).ravel(), r["gradient"].ravel(), op.name)
 
+    def avg_pool2d_view_backward(self, op, r):  # a 1 x 1 window: the gradient passes unchanged
+        assert_bitexact(host(op.writes["contribution"]), oracle.avg_pool2d_backward(
+            r["gradient"], op.writes["contribution"].shape, (1, 1), (1, 1)), op.name)
+
     def seed(self, op, r):
         assert host(op.writes["gradient"]).ravel().tolist() == [1.0]
 

@@ -110,7 +110,9 @@ def test_train_save_load_evaluate(tmp_path):
     checker = EvalChecker()
     fresh.run(checker.before, checker.after)
     torch.cuda.synchronize()
-    assert checker.count == 47 + 46 + 32 + 10 + 1
+    # 47 convolutions, 46 BatchNorms, 32 ReLUs, 10 residual adds; the global pool of the 1 x 1
+    # plane is a view (no launch)
+    assert checker.count == 47 + 46 + 32 + 10
     assert_bitexact(host(fresh.logits), host(shared.logits), "logits")
     np.testing.assert_array_equal(fresh.predicted_classes(),
                                   oracle.argmax_rows(host(fresh.logits)))

@@ -135,7 +135,10 @@ def test_general_graph_every_op_matches_oracle():
     m = a.mul(tn.constant(mask)).add(a)          # a has two consumers
     pooled = m.avg_pool2d((2, 2), (2, 2))        # [4, 5, 3, 3]
     flat = pooled.reshape((n, 45))
-    other = pooled.mul(pooled)                   # pooled's second consumer
+    # 1 x 1 windows keep every value: views of their inputs (no launch); the first one's input
+    # has other consumers (its gradient is copied), the second one's only it (the gradient
+    # buffer is shared).  other = pooled * pooled
+    other = pooled.avg_pool2d((1, 1), (1, 1)).mul(pooled).avg_pool2d((1, 1), (1, 1))
     t = tn.input((n,))
     ce = flat.cross_entropy(t)
     side = other.reshape((n * 45,)).reshape((n, 45)).cross_entropy(t)
@@ -144,11 +147,12 @@ def test_general_graph_every_op_matches_oracle():
     prog.feed(x, xv)
     prog.feed(t, targets)
     counts = _run_checked(prog)
+    assert counts["avg_pool2d_forward"] == 1, dict(counts)  # the 1 x 1 windows launch nothing
     for kind in ("conv2d_forward", "batch_norm2d_eval_forward", "relu_forward", "mul_forward",
                  "add_forward", "avg_pool2d_forward", "cross_entropy_forward", "seed",
                  "mul_backward", "add_backward", "reshape_backward", "cross_entropy_backward",
                  "avg_pool2d_backward", "relu_backward", "batch_norm2d_eval_backward",
-                 "conv2d_backward"):
+                 "conv2d_backward", "avg_pool2d_view_backward"):
         assert counts[kind] >= 1, (kind, dict(counts))
     # torch float64 autograd of the same graph
     d = lambda v: torch.tensor(v, dtype=torch.float64, requires_grad=True)  # noqa: E731
