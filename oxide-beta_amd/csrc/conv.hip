@@ -749,23 +749,33 @@ __global__ __launch_bounds__(Threads) void conv2d_depthwise_weight_kernel(
 
 // Bias gradient: one wave per output channel.  Lane l adds the channel's terms l, l + 64, ...
 // of the (n, oy, ox) order in fp32; a fixed xor butterfly combines the 64 lane sums
-// (deterministic; within fp32 rounding of the CPU's single running sum).
-__global__ __launch_bounds__(256) void conv2d_bias_kernel(uint32_t batch, uint32_t out_c,
-                                                          uint32_t plane, oxh::FastDiv plane_div,
-                                                          const float *__restrict__ grad,
-                                                          float *__restrict__ out) {
-  const uint32_t oc = blockIdx.x * 4 + threadIdx.x / 64;
-  if (oc >= out_c) return;  // wave-uniform
-  const uint32_t lane = threadIdx.x % 64, total = batch * plane;
+// (deterministic; within fp32 rounding of the CPU's single running sum).  Block b of 256
+// threads covers channels 4b .. 4b + 3.
+struct BiasArgs {
+  const float *grad;
+  float *out;
+  uint32_t batch, out_c, plane;
+  oxh::FastDiv plane_div;
+};
+__device__ __forceinline__ void bias_block(const BiasArgs &a, uint32_t b) {
+  const uint32_t oc = b * 4 + threadIdx.x / 64;
+  if (oc >= a.out_c) return;  // wave-uniform
+  const uint32_t lane = threadIdx.x % 64, total = a.batch * a.plane;
   float acc = 0.0f;
 #pragma unroll 4
   for (uint32_t j = lane; j < total; j += 64) {
-    const uint32_t n = fdiv(j, plane_div), p = j - n * plane;
-    acc += grad[(n * out_c + oc) * plane + p];
+    const uint32_t n = fdiv(j, a.plane_div), p = j - n * a.plane;
+    acc += a.grad[(n * a.out_c + oc) * a.plane + p];
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
-  if (lane == 0) out[oc] = acc;
+  if (lane == 0) a.out[oc] = acc;
+}
+__global__ __launch_bounds__(256) void conv2d_bias_kernel(BiasArgs a) { bias_block(a, blockIdx.x); }
+uint32_t bias_blocks(uint32_t out_c) { return (out_c + 3) / 4; }
+BiasArgs bias_args(const ConvGeom &g, const float *gradient, float *bias_gradient) {
+  return BiasArgs{gradient, bias_gradient, g.batch, g.out_c, g.oh * g.ow,
+                  oxh::make_fastdiv(g.oh * g.ow)};
 }
 
 // Weight gradient, phase 2: out[e] = sum over chunks of partial[chunk][e], in chunk order
@@ -1143,7 +1153,8 @@ __global__ __launch_bounds__(kSplitThreads) void pointwise_split_kernel(ProductA
 // tiles, dispatched first (their serial chains over the output channels are the longer ones),
 // the rest the weight gradient's, each computed exactly as its own kernel computes it.
 struct DualGrid {
-  uint32_t nx1, ny1, blocks1, nx2, ny2;
+  uint32_t nx1, ny1, blocks1, nx2, ny2, blocks2;
+  BiasArgs bias;  // bias.out null: no bias blocks
 };
 
 template <bool A1, bool B1, bool A2, bool B2>
@@ -1162,10 +1173,12 @@ __global__ __launch_bounds__(kSplitThreads) void pointwise_dual_kernel(ProductAr
   uint32_t b = blockIdx.x;
   if (b < d.blocks1) {
     product_tile<16, 256, A1, B1>(g1, b % d.nx1, b / d.nx1, 0, lds.tile.as, lds.tile.bs);
-  } else {
+  } else if (b < d.blocks1 + d.blocks2) {
     b -= d.blocks1;
     const uint32_t plane = d.nx2 * d.ny2, z = b / plane, r = b - z * plane;
     split_tile<A2, B2>(g2, r % d.nx2, r / d.nx2, z, lds.split);
+  } else {
+    bias_block(d.bias, b - d.blocks1 - d.blocks2);
   }
 }
 
@@ -1658,7 +1671,10 @@ oxh_status launch_weight_product(const char *name, hipStream_t s, const ProductA
 // input gradient k-fast on its second operand).  Every output is the same sum as in the
 // separate launches (the input gradient's serial sum does not depend on the tiling).  Returns
 // false, launching nothing, otherwise.
-bool launch_dual(hipStream_t s, const ProductArgs &w, const KSplit &split, const ProductArgs &x) {
+// The input gradient x (16 x 16 serial tiles), the weight gradient w (split tiles, per chunk)
+// and, when bias.out is set, the bias gradient in one launch.
+bool launch_dual(hipStream_t s, const ProductArgs &w, const KSplit &split, const ProductArgs &x,
+                 const BiasArgs &bias) {
   if (split.serial32 || big_tiles(w, split.chunks) + big_tiles(x, 1) >= kSmallGrid) return false;
   DualGrid d;
   d.nx1 = (x.N + 15) / 16;
@@ -1666,7 +1682,10 @@ bool launch_dual(hipStream_t s, const ProductArgs &w, const KSplit &split, const
   d.blocks1 = d.nx1 * d.ny1;
   d.nx2 = (w.N + 7) / 8;
   d.ny2 = (w.M + 7) / 8;
-  const dim3 grid(d.blocks1 + d.nx2 * d.ny2 * split.chunks), block(kSplitThreads);
+  d.blocks2 = d.nx2 * d.ny2 * split.chunks;
+  d.bias = bias;
+  const uint32_t blocks3 = bias.out != nullptr ? bias_blocks(bias.out_c) : 0;
+  const dim3 grid(d.blocks1 + d.blocks2 + blocks3), block(kSplitThreads);
   if (w.a.k_fast && w.b.k_fast && !x.a.k_fast && !x.b.k_fast)
     oxh::launch(pointwise_dual_kernel<false, false, true, true>, grid, block, 0, s, x, w, d);
   else if (!w.a.k_fast && !w.b.k_fast && !x.a.k_fast && x.b.k_fast)
@@ -1913,9 +1932,8 @@ oxh_status oxh_conv2d_bias_backward(oxh_stream stream, const oxh_conv2d_shape *s
   OXH_REQUIRE(gradient && bias_gradient, OXH_INVALID_SHAPE, std::string(name) + ": null pointer");
   (void)workspace;  // the single-pass reduction needs none
   (void)workspace_bytes;
-  oxh::launch(conv2d_bias_kernel, dim3((g.out_c + 3) / 4), dim3(256), 0, oxh::as_stream(stream),
-              g.batch, g.out_c, g.oh * g.ow, oxh::make_fastdiv(g.oh * g.ow), gradient,
-              bias_gradient);
+  oxh::launch(conv2d_bias_kernel, dim3(bias_blocks(g.out_c)), dim3(256), 0,
+              oxh::as_stream(stream), bias_args(g, gradient, bias_gradient));
   return oxh::launched(name);
 }
 
@@ -1945,7 +1963,10 @@ oxh_status oxh_conv2d_backward(oxh_stream stream, const oxh_conv2d_shape *shape,
                   !oxh::any_overlap(input_gradient, gx, workspace, need) &&
                   !oxh::any_overlap(weight_gradient, gw, weight, gw) &&
                   !oxh::any_overlap(weight_gradient, gw, gradient, gy) &&
-                  !oxh::any_overlap(weight_gradient, gw, input, gx),
+                  !oxh::any_overlap(weight_gradient, gw, input, gx) &&
+                  !oxh::any_overlap(weight_gradient, gw, bias_gradient, gb) &&
+                  !oxh::any_overlap(bias_gradient, gb, gradient, gy) &&
+                  !oxh::any_overlap(bias_gradient, gb, workspace, need),
               OXH_INVALID_SHAPE, std::string(name) + ": a gradient overlaps an operand");
   hipStream_t s = oxh::as_stream(stream);
   if (pointwise(g)) {
@@ -1954,19 +1975,13 @@ oxh_status oxh_conv2d_backward(oxh_stream stream, const oxh_conv2d_shape *shape,
     const ProductArgs w =
         weight_product(g, split, gradient, input, split.chunks > 1 ? partial : weight_gradient);
     const ProductArgs x = input_product(g, gradient, weight, addend, input_gradient);
-    if (launch_dual(s, w, split, x)) {
+    if (launch_dual(s, w, split, x, bias_args(g, gradient, bias_gradient))) {
       st = oxh::launched(name);
-      if (st != OXH_OK) return st;
-      if (split.chunks > 1) {
-        const uint32_t count = g.out_c * g.in_c;
-        oxh::launch(sum_chunks_kernel, dim3(grid_for(count)), dim3(256), 0, s, count,
-                    split.chunks, static_cast<const float *>(partial), weight_gradient);
-        st = oxh::launched(name);
-        if (st != OXH_OK) return st;
-      }
-      if (bias_gradient != nullptr)
-        return oxh_conv2d_bias_backward(stream, shape, gradient, bias_gradient, nullptr, 0);
-      return OXH_OK;
+      if (st != OXH_OK || split.chunks == 1) return st;
+      const uint32_t count = g.out_c * g.in_c;
+      oxh::launch(sum_chunks_kernel, dim3(grid_for(count)), dim3(256), 0, s, count,
+                  split.chunks, static_cast<const float *>(partial), weight_gradient);
+      return oxh::launched(name);
     }
   }
   st = oxh_conv2d_weight_backward(stream, shape, gradient, input, weight_gradient, workspace,

@@ -105,6 +105,7 @@ def test_conv2d_input_backward_accumulate(module, dev, case, in_place):
     (128, 512, 1, 1, 128, 1, 1, 1),    # plane 1: the other operand layouts, one launch
     (128, 64, 8, 8, 256, 1, 1, 1),     # chunked weight gradient, grids too large to pair
     (128, 960, 1, 1, 1280, 1, 1, 1),
+    (128, 1280, 1, 1, 10, 1, 1, 1),    # the classifier: the bias gradient in the paired launch
     (1, 1, 3, 3, 5, 1, 1, 1),          # one input channel: layouts outside the paired set
     (3, 12, 6, 5, 8, 3, 1, 4),         # grouped 3 x 3 and ungrouped 3 x 3: the separate kernels
     (128, 32, 7, 7, 96, 3, 2, 1),
@@ -143,6 +144,9 @@ def test_conv2d_backward_equals_separate_calls(module, dev, case, variant):
         assert np.isnan(host(db)).all()  # not written
     with pytest.raises(ox.OxideError):  # the input gradient may not overlap the gradient
         module.conv2d_backward(shape, g, x, wt, g if g.numel() >= x.numel() else x, dw)
+    if variant == "bias" and dw.numel() >= cout:
+        with pytest.raises(ox.OxideError):  # nor the bias gradient the weight gradient
+            module.conv2d_backward(shape, g, x, wt, dx, dw, dw.view(-1)[:cout])
 
 
 @pytest.mark.parametrize("shape,kernel,stride", [((2, 3, 4, 4), (2, 2), (2, 2)),
