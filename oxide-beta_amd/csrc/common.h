@@ -85,6 +85,12 @@ __device__ __forceinline__ float tap_term(float p, uint32_t mask) {
   return __uint_as_float((__float_as_uint(p) & mask) | (~mask & 0x80000000u));
 }
 __device__ __forceinline__ uint32_t tap_mask(bool valid) { return valid ? 0xFFFFFFFFu : 0u; }
+// An operand read at a tap outside the input, replaced by +0 (one AND for every product that
+// shares it): its products are +-0, which leave a sum unchanged except for the sign of an
+// exactly zero sum, when the other factor is finite.
+__device__ __forceinline__ float tap_operand(float v, uint32_t mask) {
+  return __uint_as_float(__float_as_uint(v) & mask);
+}
 
 // Cross-lane moves within rows of 16 lanes through the DPP crossbar (no LDS traffic, unlike
 // __shfl_xor's ds_bpermute).  Controls (DPP_CTRL, GCN3 / Vega ISA): quad_perm [1,0,3,2] and

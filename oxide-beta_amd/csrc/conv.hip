@@ -62,6 +62,7 @@ __device__ __forceinline__ int ceil_div0(int a, const oxh::FastDiv &s) {
 }
 
 using oxh::tap_mask;
+using oxh::tap_operand;
 using oxh::tap_term;
 
 // ---------------------------------------------------------------- direct kernels
@@ -211,13 +212,11 @@ __global__ __launch_bounds__(256) void conv2d_input_backward_taps_kernel(
 // per-lane gathers are bound by the L1 address rate); each thread then computes kLdsR
 // channels at one position, reading each staged plane value once for all of them and the
 // kLdsR weights as one float4 broadcast (weights staged channel-innermost, the tile padded to
-// a multiple of kLdsR with zeros).  Sums run in the CPU path's order with the tap kernels'
-// -0.0f padding terms (bit-exact forward and input gradient).  kLdsFloats bounds one block's
-// staging.
+// a multiple of kLdsR with zeros).  Sums run in the CPU path's order; a tap outside the input
+// reads a +0 operand (tap_operand: one AND shared by the thread's kLdsR products), so for
+// finite weights and gradients the forward and input gradient equal the CPU path's, which skips
+// those taps, up to the sign of an exactly zero sum.  kLdsFloats bounds one block's staging.
 constexpr uint32_t kLdsFloats = 16384;  // 64 KB
-#ifndef OXH_TAP_PRED
-#define OXH_TAP_PRED 0
-#endif
 constexpr int kLdsR = 4;
 
 __device__ __forceinline__ uint32_t round4(uint32_t v) { return (v + 3) & ~3u; }
@@ -330,21 +329,12 @@ __global__ __launch_bounds__(256) void conv2d_forward_lds_kernel(
       const float *wp = wq + ic * T * ocp;
 #pragma unroll
       for (int t = 0; t < T; ++t) {
-        const float xv = xp[off[t]];
         const float4 w4 = *reinterpret_cast<const float4 *>(wp + t * ocp);
-#if OXH_TAP_PRED
-        if (mask[t]) {
-          acc[0] += xv * w4.x;
-          acc[1] += xv * w4.y;
-          acc[2] += xv * w4.z;
-          acc[3] += xv * w4.w;
-        }
-#else
-        acc[0] += tap_term(xv * w4.x, mask[t]);
-        acc[1] += tap_term(xv * w4.y, mask[t]);
-        acc[2] += tap_term(xv * w4.z, mask[t]);
-        acc[3] += tap_term(xv * w4.w, mask[t]);
-#endif
+        const float xv = tap_operand(xp[off[t]], mask[t]);
+        acc[0] += xv * w4.x;
+        acc[1] += xv * w4.y;
+        acc[2] += xv * w4.z;
+        acc[3] += xv * w4.w;
       }
     }
 #pragma unroll
@@ -415,21 +405,12 @@ __global__ __launch_bounds__(256) void conv2d_forward_split_kernel(
       const float *wp = wq + ic * T * ocp;
 #pragma unroll
       for (int t = 0; t < T; ++t) {
-        const float xv = xp[off[t]];
         const float4 w4 = *reinterpret_cast<const float4 *>(wp + t * ocp);
-#if OXH_TAP_PRED
-        if (mask[t]) {
-          acc[0] += xv * w4.x;
-          acc[1] += xv * w4.y;
-          acc[2] += xv * w4.z;
-          acc[3] += xv * w4.w;
-        }
-#else
-        acc[0] += tap_term(xv * w4.x, mask[t]);
-        acc[1] += tap_term(xv * w4.y, mask[t]);
-        acc[2] += tap_term(xv * w4.z, mask[t]);
-        acc[3] += tap_term(xv * w4.w, mask[t]);
-#endif
+        const float xv = tap_operand(xp[off[t]], mask[t]);
+        acc[0] += xv * w4.x;
+        acc[1] += xv * w4.y;
+        acc[2] += xv * w4.z;
+        acc[3] += xv * w4.w;
       }
     }
     if (part > 0) {
@@ -502,21 +483,12 @@ __global__ __launch_bounds__(256) void conv2d_input_backward_lds_kernel(
       const float *wp = wq + oc * T * icp;
 #pragma unroll
       for (int t = 0; t < M * M; ++t) {
-        const float gv = gp[goff[t]];
         const float4 w4 = *reinterpret_cast<const float4 *>(wp + woff[t]);
-#if OXH_TAP_PRED
-        if (mask[t]) {
-          acc[0] += gv * w4.x;
-          acc[1] += gv * w4.y;
-          acc[2] += gv * w4.z;
-          acc[3] += gv * w4.w;
-        }
-#else
-        acc[0] += tap_term(gv * w4.x, mask[t]);
-        acc[1] += tap_term(gv * w4.y, mask[t]);
-        acc[2] += tap_term(gv * w4.z, mask[t]);
-        acc[3] += tap_term(gv * w4.w, mask[t]);
-#endif
+        const float gv = tap_operand(gp[goff[t]], mask[t]);
+        acc[0] += gv * w4.x;
+        acc[1] += gv * w4.y;
+        acc[2] += gv * w4.z;
+        acc[3] += gv * w4.w;
       }
     }
 #pragma unroll
@@ -586,10 +558,9 @@ __global__ __launch_bounds__(kDwMaxThreads) void conv2d_weight_lds_kernel(
       }
       const int iy = static_cast<int>(oy) * S + ky, ix = static_cast<int>(ox) * S + kx;
       const bool ok = static_cast<uint32_t>(iy) < g.h && static_cast<uint32_t>(ix) < g.w;
-      const float xv = xl[ok ? base + iy * static_cast<int>(g.w) + ix : 0];
-      const uint32_t m = tap_mask(ok);
+      const float xv = tap_operand(xl[ok ? base + iy * static_cast<int>(g.w) + ix : 0], tap_mask(ok));
 #pragma unroll
-      for (int o = 0; o < kDwOcTile; ++o) acc[o] += tap_term(gv[o] * xv, m);
+      for (int o = 0; o < kDwOcTile; ++o) acc[o] += gv[o] * xv;
       if (++ox == g.ow) {
         ox = 0;
         ++oy;
