@@ -749,25 +749,44 @@ BiasArgs bias_args(const ConvGeom &g, const float *gradient, float *bias_gradien
                   oxh::make_fastdiv(g.oh * g.ow)};
 }
 
-// Weight gradient, phase 2: out[e] = sum over chunks of partial[chunk][e], in chunk order
-// (loads issued in groups of 8 ahead of the serial adds).
+// Weight gradient, phase 2: out[e] = sum over chunks of partial[chunk][e] in a fixed order.
+// `lanes` threads share an element (a block serves 256 / lanes elements; thread t takes lane
+// t / (256 / lanes) of element t % (256 / lanes), so each lane's loads are contiguous across
+// elements): lane l sums the l-th contiguous part of the chunks serially (loads issued in
+// groups of 8 ahead of the adds), and the lane sums are then added in lane order.  A chain of
+// chunks / lanes loads per thread in place of chunks.
 __global__ __launch_bounds__(256) void sum_chunks_kernel(uint32_t count, uint32_t chunks,
+                                                         uint32_t lanes,
                                                          const float *__restrict__ partial,
                                                          float *__restrict__ out) {
-  for (uint32_t e = blockIdx.x * 256 + threadIdx.x; e < count; e += gridDim.x * 256) {
-    float acc = 0.0f;
-    uint32_t c = 0;
-    for (; c + 8 <= chunks; c += 8) {
+  __shared__ float part[256];
+  const uint32_t per_block = 256 / lanes;
+  const uint32_t l = threadIdx.x / per_block, j = threadIdx.x - l * per_block;
+  const uint32_t e = blockIdx.x * per_block + j;
+  float acc = 0.0f;
+  if (e < count) {
+    const uint32_t c1 = (l + 1) * chunks / lanes;
+    uint32_t c = l * chunks / lanes;
+    for (; c + 8 <= c1; c += 8) {
       float v[8];
 #pragma unroll
       for (int u = 0; u < 8; ++u) v[u] = partial[static_cast<uint64_t>(c + u) * count + e];
 #pragma unroll
       for (int u = 0; u < 8; ++u) acc += v[u];
     }
-    for (; c < chunks; ++c) acc += partial[static_cast<uint64_t>(c) * count + e];
-    out[e] = acc;
+    for (; c < c1; ++c) acc += partial[static_cast<uint64_t>(c) * count + e];
   }
+  if (lanes == 1) {
+    if (e < count) out[e] = acc;
+    return;
+  }
+  part[threadIdx.x] = acc;
+  __syncthreads();
+  if (l != 0 || e >= count) return;
+  for (uint32_t r = 1; r < lanes; ++r) acc += part[r * per_block + j];
+  out[e] = acc;
 }
+
 
 // ---------------------------------------------------------------- pointwise product
 
@@ -1205,6 +1224,17 @@ uint32_t grid_for(uint64_t items) {
   if (g < 1) g = 1;
   if (g > (1u << 20)) g = 1u << 20;
   return static_cast<uint32_t>(g);
+}
+
+// Lanes per element for sum_chunks_kernel: a power of two up to 16 leaving at most 8 chunks
+// per lane.
+void launch_sum_chunks(hipStream_t s, uint32_t count, uint32_t chunks, const void *partial,
+                       float *out) {
+  uint32_t lanes = 1;
+  while (lanes < 16 && chunks > 8 * lanes) lanes *= 2;
+  const uint32_t per_block = 256 / lanes;
+  oxh::launch(sum_chunks_kernel, dim3((count + per_block - 1) / per_block), dim3(256), 0, s,
+              count, chunks, lanes, static_cast<const float *>(partial), out);
 }
 
 uint64_t input_elems(const ConvGeom &g) {
@@ -1842,8 +1872,7 @@ oxh_status oxh_conv2d_weight_backward(oxh_stream stream, const oxh_conv2d_shape 
         split);
     if (st != OXH_OK || split.chunks == 1) return st;
     const uint32_t count = g.out_c * g.in_c;
-    oxh::launch(sum_chunks_kernel, dim3(grid_for(count)), dim3(256), 0, s, count, split.chunks,
-                static_cast<const float *>(partial), weight_gradient);
+    launch_sum_chunks(s, count, split.chunks, partial, weight_gradient);
     return oxh::launched(name);
   }
   if (depthwise_single_pass(g)) {
@@ -1877,8 +1906,7 @@ oxh_status oxh_conv2d_weight_backward(oxh_stream stream, const oxh_conv2d_shape 
     }
     st = oxh::launched(name);
     if (st != OXH_OK || lp.chunks == 1) return st;
-    oxh::launch(sum_chunks_kernel, dim3(grid_for(weights)), dim3(256), 0, s, weights, lp.chunks,
-                static_cast<const float *>(partial), weight_gradient);
+    launch_sum_chunks(s, weights, lp.chunks, partial, weight_gradient);
     return oxh::launched(name);
   }
   const uint32_t chunks = weight_chunks(g);
@@ -1888,8 +1916,7 @@ oxh_status oxh_conv2d_weight_backward(oxh_stream stream, const oxh_conv2d_shape 
               weights, oxh::make_fastdiv(weights), chunks, gradient, input, partial);
   st = oxh::launched(name);
   if (st != OXH_OK) return st;
-  oxh::launch(sum_chunks_kernel, dim3(grid_for(weights)), dim3(256), 0, s, weights, chunks,
-              static_cast<const float *>(partial), weight_gradient);
+  launch_sum_chunks(s, weights, chunks, partial, weight_gradient);
   return oxh::launched(name);
 }
 
@@ -1950,8 +1977,7 @@ oxh_status oxh_conv2d_backward(oxh_stream stream, const oxh_conv2d_shape *shape,
       st = oxh::launched(name);
       if (st != OXH_OK || split.chunks == 1) return st;
       const uint32_t count = g.out_c * g.in_c;
-      oxh::launch(sum_chunks_kernel, dim3(grid_for(count)), dim3(256), 0, s, count,
-                  split.chunks, static_cast<const float *>(partial), weight_gradient);
+      launch_sum_chunks(s, count, split.chunks, partial, weight_gradient);
       return oxh::launched(name);
     }
   }
