@@ -219,7 +219,7 @@ __global__ __launch_bounds__(256) void conv2d_input_backward_taps_kernel(
 constexpr uint32_t kLdsFloats = 16384;  // 64 KB
 constexpr int kLdsR = 4;
 
-__device__ __forceinline__ uint32_t round4(uint32_t v) { return (v + 3) & ~3u; }
+__host__ __device__ __forceinline__ uint32_t round4(uint32_t v) { return (v + 3) & ~3u; }
 
 // Block-wide global -> LDS staging with kStageUnroll loads in flight per thread (a load, a
 // wait and a store per element would put one memory latency per element on the block; each
@@ -498,6 +498,118 @@ __global__ __launch_bounds__(256) void conv2d_input_backward_lds_kernel(
       const uint64_t i = (static_cast<uint64_t>(n) * g.in_c + ic0 + icl) * plane + pos;
       dx[i] = addend != nullptr ? acc[r] + addend[i] : acc[r];
     }
+  }
+}
+
+// Input gradient of a stride-2 K x K convolution by phase: thread (input channel, phase block
+// (a, b)) forms the 2 x 2 input positions (ty, tx) = (2a + py, 2b + px) in padded coordinates
+// (iy = ty - pad), whose candidate output positions are the same M x M ones,
+// (a - (M - 1) + jy, b - (M - 1) + jx), M = ceil(K / 2), with kernel offset
+// ky = py + 2 (M - 1 - jy) (a candidate with ky >= K is no term).  Per output channel, in
+// order, and per candidate in (oy, ox) order it adds exactly the valid terms g * w of each of
+// the four positions: the CPU path's order and terms, a candidate outside the output plane
+// reading the zero halo (a +-0 product; for finite values equal to the CPU path's skipped term
+// up to the sign of an exactly zero sum).  The output gradient is staged output-channel-
+// innermost around that halo, gl[(py * owp + px) * ocs + oc] (lo rows / columns before the
+// plane, enough after it for every candidate; positions ocs = ocp or ocp + 4 floats apart, an
+// odd number of 16-byte units, so neighbouring positions' 128-bit reads use different banks),
+// and the tile's weights as wl[(icl * T + tap) * ocp + oc]: a group of 4 output channels is one
+// 128-bit read per candidate and one per tap (shared by the wave's threads of one channel).
+// Each thread's 4 sums use all of its terms (the candidate kernels' threads spend 7 of 16
+// candidate terms of a 3 x 3 stride-2 kernel on offsets outside the kernel).
+struct PhaseGeom {
+  uint32_t lo, ohp, owp, ocp, ocs, ic_tile, a0, na, nb;
+  oxh::FastDiv ab_div, nb_div;
+};
+
+template <int K>
+__global__ __launch_bounds__(256) void conv2d_input_backward_s2_kernel(
+    ConvGeom g, PhaseGeom pg, const float *__restrict__ grad, const float *__restrict__ wt,
+    const float *addend, float *dx) {
+  extern __shared__ float lds[];
+  constexpr int T = K * K, M = (K + 1) / 2;
+  const uint32_t n = blockIdx.y, ic0 = blockIdx.x * pg.ic_tile;
+  const uint32_t ocp = pg.ocp, ocs = pg.ocs;
+  const uint32_t icn = min(pg.ic_tile, g.in_c - ic0);
+  const uint32_t gcount = pg.ohp * pg.owp * ocs, wcount = pg.ic_tile * T * ocp;
+  float *gl = lds, *wl = lds + gcount;  // gcount is a multiple of 4
+  {
+    float4 *l4 = reinterpret_cast<float4 *>(lds);
+    const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (uint32_t i = threadIdx.x; i < (gcount + wcount) / 4; i += blockDim.x) l4[i] = z;
+  }
+  __syncthreads();
+  const uint32_t oplane = g.oh * g.ow;
+  const oxh::FastDiv oplane_div = oxh::make_fastdiv(oplane);
+  stage(gl, grad + static_cast<uint64_t>(n) * g.out_c * oplane, g.out_c * oplane, same_index,
+        [&](uint32_t e) {
+          const uint32_t oc = fdiv(e, oplane_div), opos = e - oc * oplane;
+          const uint32_t oy = fdiv(opos, g.ow_div), ox = opos - oy * g.ow;
+          return ((oy + pg.lo) * pg.owp + ox + pg.lo) * ocs + oc;
+        });
+  const uint32_t run = icn * T;
+  const oxh::FastDiv run_div = oxh::make_fastdiv(run);
+  stage(
+      wl, wt + static_cast<uint64_t>(ic0) * T, g.out_c * run,
+      [&](uint32_t e) {
+        const uint32_t oc = fdiv(e, run_div);
+        return oc * g.in_c * T + (e - oc * run);
+      },
+      [&](uint32_t e) {
+        const uint32_t oc = fdiv(e, run_div);
+        return (e - oc * run) * ocp + oc;  // (icl * T + tap) * ocp + oc
+      });
+  __syncthreads();
+  const uint32_t blocks_ab = pg.na * pg.nb, items = icn * blocks_ab;
+  for (uint32_t it = threadIdx.x; it < items; it += blockDim.x) {
+    const uint32_t icl = fdiv(it, pg.ab_div), ab = it - icl * blocks_ab;
+    const uint32_t ai = fdiv(ab, pg.nb_div), bi = ab - ai * pg.nb;
+    const uint32_t a = pg.a0 + ai, b = pg.a0 + bi;
+    const float *gp[M][M];
+#pragma unroll
+    for (int jy = 0; jy < M; ++jy)
+#pragma unroll
+      for (int jx = 0; jx < M; ++jx)  // (oy + lo, ox + lo) with oy = a - (M - 1) + jy
+        gp[jy][jx] = gl + ((a + pg.lo - (M - 1) + jy) * pg.owp + b + pg.lo - (M - 1) + jx) * ocs;
+    const float *wq = wl + icl * T * ocp;
+    float acc[2][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}};
+    for (uint32_t oc0 = 0; oc0 < ocp; oc0 += 4) {
+      float4 gv[M][M], wv[T];
+#pragma unroll
+      for (int jy = 0; jy < M; ++jy)
+#pragma unroll
+        for (int jx = 0; jx < M; ++jx)
+          gv[jy][jx] = *reinterpret_cast<const float4 *>(gp[jy][jx] + oc0);
+#pragma unroll
+      for (int t = 0; t < T; ++t) wv[t] = *reinterpret_cast<const float4 *>(wq + t * ocp + oc0);
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int py = 0; py < 2; ++py)
+#pragma unroll
+          for (int px = 0; px < 2; ++px)
+#pragma unroll
+            for (int jy = 0; jy < M; ++jy)
+#pragma unroll
+              for (int jx = 0; jx < M; ++jx) {
+                const int ky = py + 2 * (M - 1 - jy), kx = px + 2 * (M - 1 - jx);
+                if (ky >= K || kx >= K) continue;
+                const float4 &gq = gv[jy][jx];
+                const float4 &wt4 = wv[ky * K + kx];
+                const float gu = u == 0 ? gq.x : u == 1 ? gq.y : u == 2 ? gq.z : gq.w;
+                const float wu = u == 0 ? wt4.x : u == 1 ? wt4.y : u == 2 ? wt4.z : wt4.w;
+                acc[py][px] += gu * wu;
+              }
+    }
+#pragma unroll
+    for (int py = 0; py < 2; ++py)
+#pragma unroll
+      for (int px = 0; px < 2; ++px) {
+        const uint32_t iy = 2 * a + py - g.pad, ix = 2 * b + px - g.pad;  // wraps below 0
+        if (iy >= g.h || ix >= g.w) continue;
+        const uint64_t i = ((static_cast<uint64_t>(n) * g.in_c + ic0 + icl) * g.h + iy) * g.w + ix;
+        dx[i] = addend != nullptr ? acc[py][px] + addend[i] : acc[py][px];
+      }
   }
 }
 
@@ -1387,6 +1499,48 @@ LdsPlan input_backward_lds_plan(const ConvGeom &g) {
                        static_cast<uint64_t>(g.h) * g.w);
 }
 
+// The phase-blocked stride-2 input gradient: input channels per block for about 256
+// (channel, phase block) items, the halo-padded gradient planes and the tile's weights within
+// the LDS budget.  lds_bytes == 0: not taken.
+#ifndef OXH_IG_PHASE
+#define OXH_IG_PHASE 1  // 0: stride-2 input gradients take the candidate kernels
+#endif
+struct PhasePlan {
+  PhaseGeom pg{};
+  uint32_t tiles = 0, threads = 0, lds_bytes = 0;
+};
+PhasePlan input_backward_s2_plan(const ConvGeom &g) {
+  PhasePlan p;
+  if (!OXH_IG_PHASE || !lds_eligible(g) || g.stride != 2) return p;
+  const uint32_t K = g.kh, M = (K + 1) / 2;
+  PhaseGeom &h = p.pg;
+  h.a0 = g.pad / 2;
+  const uint32_t ay = (g.h - 1 + g.pad) / 2, ax = (g.w - 1 + g.pad) / 2;
+  h.na = ay - h.a0 + 1;
+  h.nb = ax - h.a0 + 1;
+  h.lo = M - 1 > h.a0 ? M - 1 - h.a0 : 0;
+  h.ohp = h.lo + (g.oh > ay + 1 ? g.oh : ay + 1);
+  h.owp = h.lo + (g.ow > ax + 1 ? g.ow : ax + 1);
+  h.ocp = round4(g.out_c);
+  h.ocs = (h.ocp / 4) % 2 == 0 ? h.ocp + 4 : h.ocp;
+  const uint64_t blocks_ab = static_cast<uint64_t>(h.na) * h.nb;
+  uint64_t tile = blocks_ab >= 256 ? 1 : 256 / blocks_ab;
+  if (tile > g.in_c) tile = g.in_c;
+  const uint64_t gfloats = static_cast<uint64_t>(h.ohp) * h.owp * h.ocs;
+  const uint64_t per_ic = static_cast<uint64_t>(K) * K * h.ocp;
+  while (tile > 1 && gfloats + tile * per_ic > kLdsFloats) --tile;
+  const uint64_t floats = gfloats + tile * per_ic;
+  if (floats > kLdsFloats) return p;
+  h.ic_tile = static_cast<uint32_t>(tile);
+  h.ab_div = oxh::make_fastdiv(static_cast<uint32_t>(blocks_ab));
+  h.nb_div = oxh::make_fastdiv(h.nb);
+  const uint64_t items = tile * blocks_ab;
+  p.tiles = static_cast<uint32_t>((g.in_c + tile - 1) / tile);
+  p.threads = static_cast<uint32_t>(items >= 256 ? 256 : (items + 63) / 64 * 64);
+  p.lds_bytes = static_cast<uint32_t>(floats * 4);
+  return p;
+}
+
 // Weight gradient: one thread per (ic, tap) pair and position range (pairs <= kDwMaxThreads;
 // ranges so that a block has about 256 threads), the image planes plus a full output-channel
 // tile (or the range sums) within the LDS budget; image chunks for about 512 blocks.
@@ -1709,6 +1863,17 @@ oxh_status input_backward_impl(const char *name, oxh_stream stream,
   hipStream_t s = oxh::as_stream(stream);
   if (pointwise(g))
     return launch_product(name, s, input_product(g, gradient, weight, addend, input_gradient), 1);
+  const PhasePlan pp = input_backward_s2_plan(g);
+  if (pp.lds_bytes > 0) {
+    const dim3 pgrid(pp.tiles, g.batch), pblock(pp.threads);
+    if (g.kh == 3)
+      oxh::launch(conv2d_input_backward_s2_kernel<3>, pgrid, pblock, pp.lds_bytes, s, g, pp.pg,
+                  gradient, weight, addend, input_gradient);
+    else
+      oxh::launch(conv2d_input_backward_s2_kernel<5>, pgrid, pblock, pp.lds_bytes, s, g, pp.pg,
+                  gradient, weight, addend, input_gradient);
+    return oxh::launched(name);
+  }
   const LdsPlan lp = input_backward_lds_plan(g);
   if (lp.tile > 0) {
     const dim3 lgrid(lp.tiles, g.batch), lblock(lp.threads);
