@@ -407,10 +407,10 @@ __global__ __launch_bounds__(256) void conv2d_forward_split_kernel(
       for (int t = 0; t < T; ++t) {
         const float4 w4 = *reinterpret_cast<const float4 *>(wp + t * ocp);
         const float xv = tap_operand(xp[off[t]], mask[t]);
-        acc[0] += xv * w4.x;
-        acc[1] += xv * w4.y;
-        acc[2] += xv * w4.z;
-        acc[3] += xv * w4.w;
+        acc[0] = __builtin_fmaf(xv, w4.x, acc[0]);
+        acc[1] = __builtin_fmaf(xv, w4.y, acc[1]);
+        acc[2] = __builtin_fmaf(xv, w4.z, acc[2]);
+        acc[3] = __builtin_fmaf(xv, w4.w, acc[3]);
       }
     }
     if (part > 0) {
@@ -672,7 +672,7 @@ __global__ __launch_bounds__(kDwMaxThreads) void conv2d_weight_lds_kernel(
       const bool ok = static_cast<uint32_t>(iy) < g.h && static_cast<uint32_t>(ix) < g.w;
       const float xv = tap_operand(xl[ok ? base + iy * static_cast<int>(g.w) + ix : 0], tap_mask(ok));
 #pragma unroll
-      for (int o = 0; o < kDwOcTile; ++o) acc[o] += gv[o] * xv;
+      for (int o = 0; o < kDwOcTile; ++o) acc[o] = __builtin_fmaf(gv[o], xv, acc[o]);
       if (++ox == g.ow) {
         ox = 0;
         ++oy;
@@ -945,7 +945,8 @@ template <int Tile, int Threads>
 struct TileShape {
   static constexpr int kCols = Threads == 256 ? 16 : 8;       // threads per tile row
   static constexpr int kMicro = Tile / kCols;                  // outputs per thread per axis
-  static constexpr int kSlab = Tile == kTile ? 128 : OXH_SMALL_SLAB;  // k per LDS stage
+  static constexpr int kSlab =  // k per LDS stage
+      Tile == kTile ? 128 : (Tile == 16 && Threads == 64 ? 64 : OXH_SMALL_SLAB);
   static constexpr int kLoads = Tile * kSlab / Threads;        // per thread, per operand
   static_assert(kCols * kCols == Threads && kMicro * kCols == Tile, "tile shape");
   static_assert(Threads % kSlab == 0 || kSlab % Threads == 0, "slab");
@@ -1053,7 +1054,10 @@ struct ProductRow {
 // with two block-wide barriers, so groups of threads sharing a block run equal counts.  Within a
 // slab, groups of kG4 float4 (4 k each) per row are read from LDS as 128-bit accesses, the next
 // group's reads issued before the current group's arithmetic.
-template <int Tile, int Threads, bool AKFast, bool BKFast>
+// Fma: each term is added by one fused multiply-add (one rounding in place of the CPU path's
+// two: sums that need not follow the CPU path bit for bit -- the weight gradients and the
+// split forward -- at half the VALU work).
+template <int Tile, int Threads, bool AKFast, bool BKFast, bool Fma = false>
 __device__ __forceinline__ void product_sum(
     const ProductArgs &g, uint32_t m0, uint32_t n0, uint32_t kb, uint32_t ke, uint32_t slabs,
     int t, float (&acc)[TileShape<Tile, Threads>::kMicro][TileShape<Tile, Threads>::kMicro],
@@ -1084,6 +1088,20 @@ __device__ __forceinline__ void product_sum(
   // the group's products first, then each accumulator's adds in ascending k (the adds form
   // the dependent chain; the products stay off it)
   auto add_group = [&](const float4 (&av)[kMicro][kG4], const float4 (&bv)[kMicro][kG4]) {
+    if constexpr (Fma) {
+#pragma unroll
+      for (int q = 0; q < kG4; ++q)
+#pragma unroll
+        for (int i = 0; i < kMicro; ++i)
+#pragma unroll
+          for (int j = 0; j < kMicro; ++j) {
+            acc[i][j] = __builtin_fmaf(av[i][q].x, bv[j][q].x, acc[i][j]);
+            acc[i][j] = __builtin_fmaf(av[i][q].y, bv[j][q].y, acc[i][j]);
+            acc[i][j] = __builtin_fmaf(av[i][q].z, bv[j][q].z, acc[i][j]);
+            acc[i][j] = __builtin_fmaf(av[i][q].w, bv[j][q].w, acc[i][j]);
+          }
+      return;
+    }
     float p[kMicro][kMicro][4 * kG4];
 #pragma unroll
     for (int q = 0; q < kG4; ++q)
@@ -1140,7 +1158,10 @@ __device__ __forceinline__ void product_sum(
 #pragma unroll
       for (int i = 0; i < kMicro; ++i)
 #pragma unroll
-        for (int j = 0; j < kMicro; ++j) acc[i][j] += av[i] * bv[j];
+        for (int j = 0; j < kMicro; ++j) {
+          if constexpr (Fma) acc[i][j] = __builtin_fmaf(av[i], bv[j], acc[i][j]);
+          else acc[i][j] += av[i] * bv[j];
+        }
     }
     __syncthreads();
   }
@@ -1156,7 +1177,7 @@ __device__ __forceinline__ void product_store(const ProductArgs &g, uint32_t bz,
 
 // C[m, n] = init[m] + sum_{k in chunk bz, ascending} A[m, k] * B[n, k] (+ addend) for the tile
 // (bx, by): one serial sum per output, computed by the block's Threads threads.
-template <int Tile, int Threads, bool AKFast, bool BKFast>
+template <int Tile, int Threads, bool AKFast, bool BKFast, bool Fma = false>
 __device__ __forceinline__ void product_tile(const ProductArgs &g, uint32_t bx, uint32_t by,
                                              uint32_t bz,
                                              float (*as)[ProductRow<Tile, Threads>::value],
@@ -1188,7 +1209,7 @@ __device__ __forceinline__ void product_tile(const ProductArgs &g, uint32_t bx, 
                         : 0.0f;
     }
   const uint32_t slabs = kb < ke ? (ke - kb + S::kSlab - 1) / S::kSlab : 0;
-  product_sum<Tile, Threads, AKFast, BKFast>(g, m0, n0, kb, ke, slabs, t, acc, as, bs);
+  product_sum<Tile, Threads, AKFast, BKFast, Fma>(g, m0, n0, kb, ke, slabs, t, acc, as, bs);
 #pragma unroll
   for (int i = 0; i < kMicro; ++i)
 #pragma unroll
@@ -1196,12 +1217,13 @@ __device__ __forceinline__ void product_tile(const ProductArgs &g, uint32_t bx, 
       product_store(g, bz, m0 + ty * kMicro + i, n0 + tx * kMicro + j, acc[i][j], added[i][j]);
 }
 
-template <int Tile, int Threads, bool AKFast, bool BKFast>
+template <int Tile, int Threads, bool AKFast, bool BKFast, bool Fma = false>
 __global__ __launch_bounds__(Threads) void pointwise_product_kernel(ProductArgs g) {
   constexpr int kRow = ProductRow<Tile, Threads>::value;
   __shared__ __align__(16) float as[Tile][kRow];
   __shared__ __align__(16) float bs[Tile][kRow];
-  product_tile<Tile, Threads, AKFast, BKFast>(g, blockIdx.x, blockIdx.y, blockIdx.z, as, bs);
+  product_tile<Tile, Threads, AKFast, BKFast, Fma>(g, blockIdx.x, blockIdx.y, blockIdx.z, as,
+                                                   bs);
 }
 
 // Products whose sums need not follow the serial order (the weight gradient, already reduced in
@@ -1234,7 +1256,8 @@ __device__ __forceinline__ void split_tile(const ProductArgs &g, uint32_t bx, ui
   const float added = w == 0 && g.addend != nullptr && m < g.M && n < g.N
                           ? g.addend[axis_offset(g.cm, m) + axis_offset(g.cn, n)]
                           : 0.0f;
-  product_sum<8, 64, AKFast, BKFast>(g, m0, n0, wb, we, slabs, t, acc, lds.as[w], lds.bs[w]);
+  product_sum<8, 64, AKFast, BKFast, true>(g, m0, n0, wb, we, slabs, t, acc, lds.as[w],
+                                           lds.bs[w]);
   if (w > 0) lds.part[w - 1][t] = acc[0][0];
   __syncthreads();
   if (w > 0) return;
@@ -1248,6 +1271,67 @@ template <bool AKFast, bool BKFast>
 __global__ __launch_bounds__(kSplitThreads) void pointwise_split_kernel(ProductArgs g) {
   __shared__ __align__(16) SplitLds lds;
   split_tile<AKFast, BKFast>(g, blockIdx.x, blockIdx.y, blockIdx.z, lds);
+}
+
+// The split tiles at 16 x 16 outputs, 2 x 2 per lane (product_sum<16, 64>): the same parts of
+// k in the same order per output as split_tile, half the operand reads per product (grids of
+// many 8 x 8 tiles are bound by those reads).
+struct SplitLds16 {
+  float as[kSplitWaves][16][ProductRow<16, 64>::value];
+  float bs[kSplitWaves][16][ProductRow<16, 64>::value];
+  float part[kSplitWaves - 1][4][64];
+};
+
+template <bool AKFast, bool BKFast>
+__device__ __forceinline__ void split_tile16(const ProductArgs &g, uint32_t bx, uint32_t by,
+                                             uint32_t bz, SplitLds16 &lds) {
+  using S = TileShape<16, 64>;
+  constexpr int kMicro = S::kMicro, kCols = S::kCols;
+  const uint32_t m0 = by * 16, n0 = bx * 16;
+  const uint32_t kb = bz * g.k_chunk;
+  const uint32_t ke = min(kb + g.k_chunk, g.K);
+  const uint32_t span = kb < ke ? ke - kb : 0;
+  const uint32_t part = (span + kSplitWaves - 1) / kSplitWaves;
+  const int w = static_cast<int>(threadIdx.x) / 64, t = static_cast<int>(threadIdx.x) % 64;
+  const int tx = t % kCols, ty = t / kCols;
+  const uint32_t wb = min(kb + w * part, ke), we = min(wb + part, ke);
+  const uint32_t slabs = (part + S::kSlab - 1) / S::kSlab;  // equal for every wave (barriers)
+  float acc[kMicro][kMicro], added[kMicro][kMicro];
+#pragma unroll
+  for (int i = 0; i < kMicro; ++i)
+#pragma unroll
+    for (int j = 0; j < kMicro; ++j) {
+      const uint32_t m = m0 + ty * kMicro + i, n = n0 + tx * kMicro + j;
+      acc[i][j] = w == 0 && g.init != nullptr && m < g.M ? g.init[m] : 0.0f;
+      added[i][j] = w == 0 && g.addend != nullptr && m < g.M && n < g.N
+                        ? g.addend[axis_offset(g.cm, m) + axis_offset(g.cn, n)]
+                        : 0.0f;
+    }
+  product_sum<16, 64, AKFast, BKFast, true>(g, m0, n0, wb, we, slabs, t, acc, lds.as[w],
+                                            lds.bs[w]);
+  if (w > 0) {
+#pragma unroll
+    for (int i = 0; i < kMicro; ++i)
+#pragma unroll
+      for (int j = 0; j < kMicro; ++j) lds.part[w - 1][i * kMicro + j][t] = acc[i][j];
+  }
+  __syncthreads();
+  if (w > 0) return;
+#pragma unroll
+  for (int i = 0; i < kMicro; ++i)
+#pragma unroll
+    for (int j = 0; j < kMicro; ++j) {
+      float sum = acc[i][j];
+#pragma unroll
+      for (int q = 0; q < kSplitWaves - 1; ++q) sum += lds.part[q][i * kMicro + j][t];
+      product_store(g, bz, m0 + ty * kMicro + i, n0 + tx * kMicro + j, sum, added[i][j]);
+    }
+}
+
+template <bool AKFast, bool BKFast>
+__global__ __launch_bounds__(kSplitThreads) void pointwise_split16_kernel(ProductArgs g) {
+  __shared__ __align__(16) SplitLds16 lds;
+  split_tile16<AKFast, BKFast>(g, blockIdx.x, blockIdx.y, blockIdx.z, lds);
 }
 
 // A convolution's input gradient (16 x 16 serial tiles, one output per thread: g1) and weight
@@ -1637,18 +1721,19 @@ KSplit product_split(const ConvGeom &g) {
 }
 
 
-template <int Tile, int Threads>
+template <int Tile, int Threads, bool Fma = false>
 void launch_tiled(hipStream_t s, const ProductArgs &a, uint32_t chunks) {
   const dim3 grid((a.N + Tile - 1) / Tile, (a.M + Tile - 1) / Tile, chunks);
   const dim3 block(Threads);
   if (a.a.k_fast && a.b.k_fast)
-    oxh::launch(pointwise_product_kernel<Tile, Threads, true, true>, grid, block, 0, s, a);
+    oxh::launch(pointwise_product_kernel<Tile, Threads, true, true, Fma>, grid, block, 0, s, a);
   else if (a.a.k_fast)
-    oxh::launch(pointwise_product_kernel<Tile, Threads, true, false>, grid, block, 0, s, a);
+    oxh::launch(pointwise_product_kernel<Tile, Threads, true, false, Fma>, grid, block, 0, s, a);
   else if (a.b.k_fast)
-    oxh::launch(pointwise_product_kernel<Tile, Threads, false, true>, grid, block, 0, s, a);
+    oxh::launch(pointwise_product_kernel<Tile, Threads, false, true, Fma>, grid, block, 0, s, a);
   else
-    oxh::launch(pointwise_product_kernel<Tile, Threads, false, false>, grid, block, 0, s, a);
+    oxh::launch(pointwise_product_kernel<Tile, Threads, false, false, Fma>, grid, block, 0, s,
+                a);
 }
 
 template <bool A, bool B>
@@ -1662,27 +1747,51 @@ void launch_split(hipStream_t s, const ProductArgs &a, uint32_t chunks);
 // idle).
 constexpr uint64_t kSplitMaxTiles = 512;
 constexpr uint32_t kSplitMinK = 256;
-bool split_pays(uint32_t M, uint32_t N, uint32_t k_chunk, uint32_t chunks) {
+// Which tiling a product that may split takes: 0 the serial tiles, 1 the split 8 x 8 tiles
+// (grids of at most kSplitMaxTiles of them), 2 the split 16 x 16 tiles (larger grids, still
+// under kSmallGrid 32 x 32 tiles: bound by operand reads, which 2 x 2 outputs per lane halve).
+#ifndef OXH_SPLIT16
+#define OXH_SPLIT16 1
+#endif
+int split_kind(uint32_t M, uint32_t N, uint32_t k_chunk, uint32_t chunks) {
   const uint64_t big =
       static_cast<uint64_t>((N + kTile - 1) / kTile) * ((M + kTile - 1) / kTile) * chunks;
   const uint64_t tiles8 = static_cast<uint64_t>((N + 7) / 8) * ((M + 7) / 8) * chunks;
-  return big < kSmallGrid && k_chunk >= kSplitMinK && tiles8 <= kSplitMaxTiles;
+  if (big >= kSmallGrid || k_chunk < kSplitMinK) return 0;
+  if (tiles8 <= kSplitMaxTiles) return 1;
+  return OXH_SPLIT16 ? 2 : 0;
 }
+
+template <bool A, bool B>
+void launch_split16(hipStream_t s, const ProductArgs &a, uint32_t chunks) {
+  const dim3 grid((a.N + 15) / 16, (a.M + 15) / 16, chunks);
+  oxh::launch(pointwise_split16_kernel<A, B>, grid, dim3(kSplitThreads), 0, s, a);
+}
+
 oxh_status launch_product(const char *name, hipStream_t s, const ProductArgs &a,
                           uint32_t chunks, bool split = false) {
+  const int kind = split ? split_kind(a.M, a.N, a.k_chunk, chunks) : 0;
   const uint64_t big =
       static_cast<uint64_t>((a.N + kTile - 1) / kTile) * ((a.M + kTile - 1) / kTile) * chunks;
-  split = split && split_pays(a.M, a.N, a.k_chunk, chunks);
+  const bool ak = a.a.k_fast, bk = a.b.k_fast;
   if (big >= kSmallGrid)
     launch_tiled<kTile, 256>(s, a, chunks);
-  else if (split && a.a.k_fast && a.b.k_fast)
+  else if (kind == 1 && ak && bk)
     launch_split<true, true>(s, a, chunks);
-  else if (split && a.a.k_fast)
+  else if (kind == 1 && ak)
     launch_split<true, false>(s, a, chunks);
-  else if (split && a.b.k_fast)
+  else if (kind == 1 && bk)
     launch_split<false, true>(s, a, chunks);
-  else if (split)
+  else if (kind == 1)
     launch_split<false, false>(s, a, chunks);
+  else if (kind == 2 && ak && bk)
+    launch_split16<true, true>(s, a, chunks);
+  else if (kind == 2 && ak)
+    launch_split16<true, false>(s, a, chunks);
+  else if (kind == 2 && bk)
+    launch_split16<false, true>(s, a, chunks);
+  else if (kind == 2)
+    launch_split16<false, false>(s, a, chunks);
   else if (OXH_TINY_TILE == 8)
     launch_tiled<8, 64>(s, a, chunks);
   else
@@ -1806,7 +1915,7 @@ oxh_status launch_weight_product(const char *name, hipStream_t s, const ProductA
                                  const KSplit &split) {
   const uint32_t chunks = split.chunks;
   if (split.serial32) {
-    launch_tiled<kTile, 256>(s, a, chunks);
+    launch_tiled<kTile, 256, true>(s, a, chunks);
   } else if (a.a.k_fast && a.b.k_fast) {
     launch_split<true, true>(s, a, chunks);
   } else if (a.a.k_fast) {
@@ -1916,7 +2025,7 @@ oxh_status oxh_conv2d_output_size(const oxh_conv2d_shape *shape, uint64_t *out_h
 int oxh_conv2d_forward_serial(const oxh_conv2d_shape *shape) {
   ConvGeom g;
   if (make_conv_geom("oxh_conv2d_forward_serial", shape, g) != OXH_OK) return -1;
-  if (pointwise(g)) return split_pays(g.out_c, g.batch * g.h * g.w, g.in_c, 1) ? 0 : 1;
+  if (pointwise(g)) return split_kind(g.out_c, g.batch * g.h * g.w, g.in_c, 1) != 0 ? 0 : 1;
   return forward_split_plan(g).tile > 0 ? 0 : 1;
 }
 

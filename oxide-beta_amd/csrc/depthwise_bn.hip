@@ -103,6 +103,12 @@ __global__ __launch_bounds__(kDwThreads) void dw_bn_forward_kernel(
   __shared__ double lds[2][kDwThreads / 64];
   __shared__ float shift;
   const uint32_t c = blockIdx.x;
+  // the layer's parameters, loaded before the first reduction (after it they would add a
+  // memory round trip to the block)
+  float wv[K * K];
+#pragma unroll
+  for (int t = 0; t < K * K; ++t) wv[t] = conv_weight[c * (K * K) + t];
+  const float bias = conv_bias[c], w = bn_weight[c], b = bn_bias[c];
   if constexpr (Pre != kPreNone) {
     // the BatchNorm (relu) in front over input channel c (at most kDwThreads * kChannelKeep
     // values), exactly as its channel kernel forms it; its output goes to LDS for the taps
@@ -124,10 +130,6 @@ __global__ __launch_bounds__(kDwThreads) void dw_bn_forward_kernel(
   } else {
     stage_channel(g, c, x, xs);
   }
-  float wv[K * K];
-#pragma unroll
-  for (int t = 0; t < K * K; ++t) wv[t] = conv_weight[c * (K * K) + t];
-  const float bias = conv_bias[c], w = bn_weight[c], b = bn_bias[c];
   __syncthreads();
   const uint32_t oplane = g.oh * g.ow, plane = g.h * g.w, samples = g.out.samples;
   float kept[kChannelKeep];
@@ -187,17 +189,27 @@ __global__ __launch_bounds__(kDwThreads) void dw_bn_backward_kernel(
   const uint32_t c = blockIdx.x;
   const uint32_t oplane = g.oh * g.ow, plane = g.h * g.w, samples = g.out.samples;
   const float mu = mean[c], inv = inverse_std[c];
-  // the BatchNorm in front: its input values (x_hat) and statistics, loaded with the rest
-  float pin[kChannelKeep];
+  // every load the block needs is issued here, before the first reduction: the convolution's
+  // input channel (kept in registers when it fits, for the LDS copy), the addend, the
+  // convolution weights, and the BatchNorm in front's input values and statistics
+  const bool kept_in = g.in_samples <= static_cast<uint32_t>(kDwThreads * kChannelKeep);
+  float xin[kChannelKeep], addv[kChannelKeep], pin[kChannelKeep];
   uint32_t pat[kChannelKeep];
-  float pmu = 0.0f, pinv = 0.0f, pw = 0.0f;
-  if constexpr (Pre != kPreNone) {
+  if (kept_in) {
 #pragma unroll
     for (int u = 0; u < kChannelKeep; ++u) {
       const uint32_t j = threadIdx.x + u * kDwThreads;
       pat[u] = j < g.in_samples ? input_index(g, c, j) : 0;
-      pin[u] = pre.input[pat[u]];
+      xin[u] = x[pat[u]];
+      addv[u] = addend != nullptr ? addend[pat[u]] : 0.0f;
     }
+  }
+  const float wt_reg = threadIdx.x < static_cast<uint32_t>(kTaps)
+                           ? conv_weight[c * kTaps + threadIdx.x] : 0.0f;
+  float pmu = 0.0f, pinv = 0.0f, pw = 0.0f;
+  if constexpr (Pre != kPreNone) {  // pre_eligible: the input channel is kept
+#pragma unroll
+    for (int u = 0; u < kChannelKeep; ++u) pin[u] = pre.input[pat[u]];
     pmu = pre.mean[c];
     pinv = pre.inverse_std[c];
     pw = pre.weight[c];
@@ -214,8 +226,16 @@ __global__ __launch_bounds__(kDwThreads) void dw_bn_backward_kernel(
     kg[u] = gv;
     kn[u] = (conv_out[at[u]] - mu) * inv;
   }
-  stage_channel(g, c, x, xs);
-  if (threadIdx.x < kTaps) wts[threadIdx.x] = conv_weight[c * kTaps + threadIdx.x];
+  if (kept_in) {
+#pragma unroll
+    for (int u = 0; u < kChannelKeep; ++u) {
+      const uint32_t j = threadIdx.x + u * kDwThreads;
+      if (j < g.in_samples) xs[j] = xin[u];
+    }
+  } else {
+    stage_channel(g, c, x, xs);
+  }
+  if (threadIdx.x < kTaps) wts[threadIdx.x] = wt_reg;
   oxh::channel_backward_kept<kDwThreads>(samples, kg, kn, bn_weight[c], inv, bn_dweight + c,
                                          bn_dbias + c, d, lds[0]);
   double total = 0.0, unused = 0.0;
@@ -301,7 +321,7 @@ __global__ __launch_bounds__(kDwThreads) void dw_bn_backward_kernel(
       const uint32_t i = threadIdx.x + u * kDwThreads;
       if (i >= g.in_samples) break;
       float a = input_sum(i);
-      if (addend != nullptr) a = a + addend[pat[u]];
+      if (addend != nullptr) a = a + addv[u];
       if (dx != nullptr) dx[pat[u]] = a;
       kg[u] = Pre == kPreBnRelu ? oxh::relu_masked(a, xs[i]) : a;
       kn[u] = (pin[u] - pmu) * pinv;
@@ -318,6 +338,14 @@ __global__ __launch_bounds__(kDwThreads) void dw_bn_backward_kernel(
     }
     oxh::block_sum2_all<kWaves>(ptotal, punused, lds_pre[1]);
     if (threadIdx.x == 0 && pre.input_sum != nullptr) pre.input_sum[c] = static_cast<float>(ptotal);
+  } else if (dx != nullptr && kept_in) {
+#pragma unroll
+    for (int u = 0; u < kChannelKeep; ++u) {
+      const uint32_t i = threadIdx.x + u * kDwThreads;
+      if (i >= g.in_samples) break;
+      const float a = input_sum(i);
+      dx[pat[u]] = addend != nullptr ? a + addv[u] : a;
+    }
   } else if (dx != nullptr) {
     for (uint32_t i = threadIdx.x; i < g.in_samples; i += kDwThreads) {
       const float a = input_sum(i);

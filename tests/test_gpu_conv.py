@@ -25,7 +25,8 @@ CASES = [
     (4, 96, 2, 2, 192, 1, 1, 1),
     (3, 12, 6, 5, 8, 3, 1, 4),
     (5, 20, 1, 1, 30, 1, 1, 1),
-    (128, 960, 1, 1, 1280, 1, 1, 1),   # config 5's largest layer
+    (128, 960, 1, 1, 1280, 1, 1, 1),   # config 5's largest layer (split 16 x 16 forward tiles)
+    (128, 384, 2, 2, 96, 1, 1, 1),     # split 16 x 16 forward tiles, plane > 1
     # pointwise (1x1, stride 1) product path: k over several 128-slabs, partial 32-tiles,
     # the weight gradient split over (n, p) chunks, plane 1 and plane > 1
     (3, 300, 3, 3, 40, 1, 1, 1),
