@@ -1334,31 +1334,44 @@ __global__ __launch_bounds__(kSplitThreads) void pointwise_split16_kernel(Produc
   split_tile16<AKFast, BKFast>(g, blockIdx.x, blockIdx.y, blockIdx.z, lds);
 }
 
-// A convolution's input gradient (16 x 16 serial tiles, one output per thread: g1) and weight
-// gradient (split tiles: g2) in one launch.  Blocks [0, blocks1) take the input gradient's
-// tiles, dispatched first (their serial chains over the output channels are the longer ones),
-// the rest the weight gradient's, each computed exactly as its own kernel computes it.
+// A convolution's input gradient (16 x 16 serial tiles, one output per thread, or with Split1
+// the 16 x 16 split tiles its own launch takes for that shape: g1) and weight gradient (split
+// tiles: g2) in one launch.  Blocks [0, blocks1) take the input gradient's tiles, dispatched
+// first (their chains over the output channels are the longer ones), the rest the weight
+// gradient's, each computed exactly as its own kernel computes it.
 struct DualGrid {
   uint32_t nx1, ny1, blocks1, nx2, ny2, blocks2;
   BiasArgs bias;  // bias.out null: no bias blocks
 };
 
-template <bool A1, bool B1, bool A2, bool B2>
+struct SerialTileLds16 {
+  float as[16][ProductRow<16, 256>::value];
+  float bs[16][ProductRow<16, 256>::value];
+};
+// The paired launch's LDS: the weight gradient's split tiles and the input gradient's tiles
+// (only the kind it takes, so the serial pairing keeps its occupancy).
+template <bool Split1>
+union DualLds {
+  SplitLds split;
+  SerialTileLds16 tile;
+};
+template <>
+union DualLds<true> {
+  SplitLds split;
+  SplitLds16 split16;
+};
+
+template <bool A1, bool B1, bool A2, bool B2, bool Split1 = false>
 __global__ __launch_bounds__(kSplitThreads) void pointwise_dual_kernel(ProductArgs g1,
                                                                        ProductArgs g2,
                                                                        DualGrid d) {
-  constexpr int kRow = ProductRow<16, 256>::value;
-  union Lds {
-    SplitLds split;
-    struct {
-      float as[16][kRow];
-      float bs[16][kRow];
-    } tile;
-  };
-  __shared__ __align__(16) Lds lds;
+  __shared__ __align__(16) DualLds<Split1> lds;
   uint32_t b = blockIdx.x;
   if (b < d.blocks1) {
-    product_tile<16, 256, A1, B1>(g1, b % d.nx1, b / d.nx1, 0, lds.tile.as, lds.tile.bs);
+    if constexpr (Split1)  // the input gradient as its own launch splits it (input_splits)
+      split_tile16<A1, B1>(g1, b % d.nx1, b / d.nx1, 0, lds.split16);
+    else
+      product_tile<16, 256, A1, B1>(g1, b % d.nx1, b / d.nx1, 0, lds.tile.as, lds.tile.bs);
   } else if (b < d.blocks1 + d.blocks2) {
     b -= d.blocks1;
     const uint32_t plane = d.nx2 * d.ny2, z = b / plane, r = b - z * plane;
@@ -1762,6 +1775,16 @@ int split_kind(uint32_t M, uint32_t N, uint32_t k_chunk, uint32_t chunks) {
   return OXH_SPLIT16 ? 2 : 0;
 }
 
+// A pointwise input gradient leaves the serial order only for grids of many small tiles (the
+// 16 x 16 split tiles): there the serial chain of every output over the output channels sets
+// the time.
+#ifndef OXH_IG_SPLIT
+#define OXH_IG_SPLIT 1
+#endif
+bool input_splits(const ProductArgs &x) {
+  return OXH_IG_SPLIT && split_kind(x.M, x.N, x.k_chunk, 1) == 2;
+}
+
 template <bool A, bool B>
 void launch_split16(hipStream_t s, const ProductArgs &a, uint32_t chunks) {
   const dim3 grid((a.N + 15) / 16, (a.M + 15) / 16, chunks);
@@ -1939,7 +1962,8 @@ oxh_status launch_weight_product(const char *name, hipStream_t s, const ProductA
 // and, when bias.out is set, the bias gradient in one launch.
 bool launch_dual(hipStream_t s, const ProductArgs &w, const KSplit &split, const ProductArgs &x,
                  const BiasArgs &bias) {
-  if (split.serial32 || big_tiles(w, split.chunks) + big_tiles(x, 1) >= kSmallGrid) return false;
+  if (split.serial32 || big_tiles(w, split.chunks) + big_tiles(x, 1) >= kSmallGrid)
+    return false;
   DualGrid d;
   d.nx1 = (x.N + 15) / 16;
   d.ny1 = (x.M + 15) / 16;
@@ -1950,12 +1974,22 @@ bool launch_dual(hipStream_t s, const ProductArgs &w, const KSplit &split, const
   d.bias = bias;
   const uint32_t blocks3 = bias.out != nullptr ? bias_blocks(bias.out_c) : 0;
   const dim3 grid(d.blocks1 + d.blocks2 + blocks3), block(kSplitThreads);
-  if (w.a.k_fast && w.b.k_fast && !x.a.k_fast && !x.b.k_fast)
-    oxh::launch(pointwise_dual_kernel<false, false, true, true>, grid, block, 0, s, x, w, d);
-  else if (!w.a.k_fast && !w.b.k_fast && !x.a.k_fast && x.b.k_fast)
-    oxh::launch(pointwise_dual_kernel<false, true, false, false>, grid, block, 0, s, x, w, d);
-  else
+  const bool split1 = input_splits(x);
+  if (w.a.k_fast && w.b.k_fast && !x.a.k_fast && !x.b.k_fast) {
+    if (split1)
+      oxh::launch(pointwise_dual_kernel<false, false, true, true, true>, grid, block, 0, s, x, w,
+                  d);
+    else
+      oxh::launch(pointwise_dual_kernel<false, false, true, true>, grid, block, 0, s, x, w, d);
+  } else if (!w.a.k_fast && !w.b.k_fast && !x.a.k_fast && x.b.k_fast) {
+    if (split1)
+      oxh::launch(pointwise_dual_kernel<false, true, false, false, true>, grid, block, 0, s, x,
+                  w, d);
+    else
+      oxh::launch(pointwise_dual_kernel<false, true, false, false>, grid, block, 0, s, x, w, d);
+  } else {
     return false;
+  }
   return true;
 }
 
@@ -1970,8 +2004,10 @@ oxh_status input_backward_impl(const char *name, oxh_stream stream,
               std::string(name) + ": null pointer");
   const uint64_t in_n = input_elems(g);
   hipStream_t s = oxh::as_stream(stream);
-  if (pointwise(g))
-    return launch_product(name, s, input_product(g, gradient, weight, addend, input_gradient), 1);
+  if (pointwise(g)) {
+    const ProductArgs x = input_product(g, gradient, weight, addend, input_gradient);
+    return launch_product(name, s, x, 1, input_splits(x));
+  }
   const PhasePlan pp = input_backward_s2_plan(g);
   if (pp.lds_bytes > 0) {
     const dim3 pgrid(pp.tiles, g.batch), pblock(pp.threads);
@@ -2020,6 +2056,13 @@ oxh_status oxh_conv2d_output_size(const oxh_conv2d_shape *shape, uint64_t *out_h
   *out_h = g.oh;
   *out_w = g.ow;
   return oxh::ok();
+}
+
+int oxh_conv2d_input_backward_serial(const oxh_conv2d_shape *shape) {
+  ConvGeom g;
+  if (make_conv_geom("oxh_conv2d_input_backward_serial", shape, g) != OXH_OK) return -1;
+  if (!pointwise(g)) return 1;
+  return input_splits(input_product(g, nullptr, nullptr, nullptr, nullptr)) ? 0 : 1;
 }
 
 int oxh_conv2d_forward_serial(const oxh_conv2d_shape *shape) {

@@ -160,6 +160,7 @@ _SIGNATURES = {
     "oxh_conv2d_output_size": (_st, [_CS, ctypes.POINTER(_u64), ctypes.POINTER(_u64)]),
     "oxh_conv2d_forward": (_st, [_vp, _CS, _vp, _vp, _vp, _vp]),
     "oxh_conv2d_forward_serial": (_int, [_CS]),
+    "oxh_conv2d_input_backward_serial": (_int, [_CS]),
     "oxh_conv2d_input_backward": (_st, [_vp, _CS, _vp, _vp, _vp]),
     "oxh_conv2d_input_backward_accumulate": (_st, [_vp, _CS, _vp, _vp, _vp, _vp]),
     "oxh_conv2d_weight_backward_workspace_size": (_st, [_CS, ctypes.POINTER(_u64)]),
@@ -424,6 +425,15 @@ def conv2d_forward_serial(shape: Conv2dShape) -> bool:
     """True when oxh_conv2d_forward sums each output in the CPU path's order (bit-identical),
     False when in four ordered parts over the input channels."""
     v = lib().oxh_conv2d_forward_serial(ctypes.byref(shape))
+    if v < 0:
+        raise OxideError(INVALID_SHAPE, "invalid conv2d shape")
+    return bool(v)
+
+
+def conv2d_input_backward_serial(shape: Conv2dShape) -> bool:
+    """True when the input gradient sums each value in the CPU path's order (bit-identical),
+    False when in four ordered parts over the output channels."""
+    v = lib().oxh_conv2d_input_backward_serial(ctypes.byref(shape))
     if v < 0:
         raise OxideError(INVALID_SHAPE, "invalid conv2d shape")
     return bool(v)

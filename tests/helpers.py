@@ -64,6 +64,32 @@ def assert_conv_forward(got, x, weight, bias, stride, padding, groups, what=""):
         assert_within(got, ref, 1e-5 * mag.astype(np.float64) + 1e-7, what)
 
 
+def assert_conv_input_gradient(got, gradient, weight, stride, padding, groups, input_shape,
+                               addend=None, what=""):
+    """A conv2d input gradient (+ addend) against the oracle: bit-exact where the library sums
+    in the CPU path's order (oxh_conv2d_input_backward_serial), else (four ordered parts over
+    the output channels) within 1e-5 * sum|terms| (+ one rounding of the addend's add)."""
+    import oracle
+    import oxide_hip as ox
+
+    zeros = np.zeros(input_shape, np.float32)
+    ref = oracle.conv2d_backward(gradient, zeros, weight, stride, padding, groups)[0]
+    if addend is not None:
+        ref = oracle.accumulate(addend, ref)
+    n, cin, h, w = input_shape
+    cout, _, k, _ = weight.shape
+    if ox.conv2d_input_backward_serial(ox.conv2d_shape(n, cin, h, w, cout, k, stride, padding,
+                                                       groups)):
+        assert_bitexact(got, ref, what)
+    else:
+        mag = oracle.conv2d_backward(np.abs(gradient), zeros, np.abs(weight), stride, padding,
+                                     groups)[0].astype(np.float64)
+        bound = 1e-5 * mag + 1e-7
+        if addend is not None:
+            bound = bound + np.abs(np.asarray(ref, np.float64)) * 2.0 ** -23
+        assert_within(got, ref, bound, what)
+
+
 def assert_within(got, ref, bound, what=""):
     """|got - ref| <= bound elementwise (bound: a conditioning-aware error bound)."""
     d = np.abs(np.asarray(got, np.float64) - np.asarray(ref, np.float64))

@@ -278,3 +278,17 @@ def test_conv_forward_order_query():
     assert ox.conv2d_forward_serial(sh(2, 8, 5, 5, 8, 3, 1, 1, 8))             # grouped
     with pytest.raises(ox.OxideError):
         ox.conv2d_forward_serial(sh(1, 1, 1, 1, 1, 3, 1, 0, 1))                # kernel > input
+
+
+def test_conv_input_gradient_order_query():
+    """oxh_conv2d_input_backward_serial: only a pointwise input gradient over many output
+    channels whose grid has many small tiles (the MNIST MobileNetV4's 960 -> 1280 head) sums
+    four ordered parts; the paired backward launches and the K x K kernels stay serial."""
+    sh = ox.conv2d_shape
+    assert not ox.conv2d_input_backward_serial(sh(128, 960, 1, 1, 1280, 1, 1, 0, 1))  # head
+    assert ox.conv2d_input_backward_serial(sh(128, 128, 1, 1, 960, 1, 1, 0, 1))       # paired
+    assert ox.conv2d_input_backward_serial(sh(128, 128, 1, 1, 512, 1, 1, 0, 1))
+    assert ox.conv2d_input_backward_serial(sh(128, 1280, 1, 1, 10, 1, 1, 0, 1))       # classifier
+    assert ox.conv2d_input_backward_serial(sh(128, 32, 7, 7, 96, 3, 2, 1, 1))         # K x K
+    with pytest.raises(ox.OxideError):
+        ox.conv2d_input_backward_serial(sh(1, 1, 1, 1, 1, 3, 1, 0, 1))

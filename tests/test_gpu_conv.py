@@ -12,7 +12,8 @@ import torch
 
 import oracle
 import oxide_hip as ox
-from helpers import assert_bitexact, assert_conv_forward, assert_within, host, to_dev
+from helpers import (assert_bitexact, assert_conv_forward, assert_conv_input_gradient,
+                     assert_within, host, to_dev)
 
 pytestmark = pytest.mark.gpu
 
@@ -67,7 +68,7 @@ def test_conv2d_matches_oracle(module, dev, case):
     torch.cuda.synchronize()
     assert_conv_forward(host(y), x, wt, b, s, pad, groups, "forward")
     rdx, rdw, rdb = oracle.conv2d_backward(g, x, wt, s, pad, groups)
-    assert_bitexact(host(gx), rdx, "input gradient")
+    assert_conv_input_gradient(host(gx), g, wt, s, pad, groups, x.shape, what="input gradient")
     # weight / bias gradient conditioning bounds from the magnitudes of their terms
     abs_dw = oracle.conv2d_backward(np.abs(g), np.abs(x), np.abs(wt), s, pad, groups)[1]
     assert_within(host(gw), rdw, 1e-5 * abs_dw.astype(np.float64) + 1e-7, "weight gradient")
@@ -95,8 +96,8 @@ def test_conv2d_input_backward_accumulate(module, dev, case, in_place):
     out = da_ if in_place else torch.empty_like(da_)
     module.conv2d_input_backward_accumulate(shape, dg_, dw_, da_, out)
     torch.cuda.synchronize()
-    rdx = oracle.conv2d_backward(g, np.zeros((n, cin, h, w), np.float32), wt, s, pad, groups)[0]
-    assert_bitexact(host(out), oracle.accumulate(addend, rdx), "accumulated input gradient")
+    assert_conv_input_gradient(host(out), g, wt, s, pad, groups, (n, cin, h, w), addend,
+                               "accumulated input gradient")
     with pytest.raises(ox.OxideError):
         module.conv2d_input_backward_accumulate(shape, dg_, dw_, None, out)
 

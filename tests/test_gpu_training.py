@@ -2,11 +2,12 @@
 through liboxide_hip.so, every scheduled launch recomputed by the oracle from the device
 inputs it actually read.
 
-Per-op bars: conv input gradient, the conv forwards the library sums in the CPU path's order
-(oxh_conv2d_forward_serial), pooling, ReLU, add, accumulate, argmax and AdamW bit-exact;
-BatchNorm and cross entropy within the north star's 1e-5 relative (1e-6 absolute, or the
-conditioning bound of a cancelling sum); the other conv forwards and conv weight / bias
-gradients within 1e-5 * sum|terms| (fixed-order sums over contiguous parts)."""
+Per-op bars: the conv input gradients and forwards the library sums in the CPU path's order
+(oxh_conv2d_input_backward_serial, oxh_conv2d_forward_serial), pooling, ReLU, add,
+accumulate, argmax and AdamW bit-exact; BatchNorm and cross entropy within the north star's
+1e-5 relative (1e-6 absolute, or the conditioning bound of a cancelling sum); the other conv
+input gradients and forwards and conv weight / bias gradients within 1e-5 * sum|terms|
+(fixed-order sums over contiguous parts)."""
 
 from collections import Counter
 
