@@ -1759,7 +1759,10 @@ void launch_split(hipStream_t s, const ProductArgs &a, uint32_t chunks);
 // quarter of the serial chain, four times the waves of a grid that leaves most of the chip
 // idle).
 constexpr uint64_t kSplitMaxTiles = 512;
-constexpr uint32_t kSplitMinK = 256;
+#ifndef OXH_SPLIT_MIN_K
+#define OXH_SPLIT_MIN_K 256
+#endif
+constexpr uint32_t kSplitMinK = OXH_SPLIT_MIN_K;
 // Which tiling a product that may split takes: 0 the serial tiles, 1 the split 8 x 8 tiles
 // (grids of at most kSplitMaxTiles of them), 2 the split 16 x 16 tiles (larger grids, still
 // under kSmallGrid 32 x 32 tiles: bound by operand reads, which 2 x 2 outputs per lane halve).

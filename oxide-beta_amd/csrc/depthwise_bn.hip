@@ -93,7 +93,14 @@ __device__ __forceinline__ void stage_channel(const DwGeom &g, uint32_t c,
   }
 }
 
-template <int K, int S, bool Relu, int Pre>
+// C: the input plane is 1 x 1 (one output per image), where the only tap inside the input is
+// the centre (ky, kx) = (pad, pad): the other taps' -0.0f terms leave every sum unchanged and
+// are skipped (bit-identical to the general path).
+__host__ __device__ inline bool centre_only(uint32_t h, uint32_t w, uint32_t oh, uint32_t ow) {
+  return h == 1 && w == 1 && oh == 1 && ow == 1;
+}
+
+template <int K, int S, bool Relu, int Pre, bool C = false>
 __global__ __launch_bounds__(kDwThreads) void dw_bn_forward_kernel(
     DwGeom g, const float *__restrict__ x, const float *__restrict__ conv_weight,
     const float *__restrict__ conv_bias, float *__restrict__ conv_out,
@@ -143,22 +150,27 @@ __global__ __launch_bounds__(kDwThreads) void dw_bn_forward_kernel(
     const int by = static_cast<int>(oy) * S - static_cast<int>(g.pad);
     const int bx = static_cast<int>(ox) * S - static_cast<int>(g.pad);
     const float *xp = xs + n * plane;
-    int row[K], col[K];
-    uint32_t my[K], mx[K];
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-      const bool vy = static_cast<uint32_t>(by + k) < g.h, vx = static_cast<uint32_t>(bx + k) < g.w;
-      row[k] = vy ? (by + k) * static_cast<int>(g.w) : 0;
-      col[k] = vx ? bx + k : 0;
-      my[k] = tap_mask(vy);
-      mx[k] = tap_mask(vx);
-    }
-    float xv[K * K];
-#pragma unroll
-    for (int t = 0; t < K * K; ++t) xv[t] = xp[row[t / K] + col[t % K]];
     float sum = bias;
+    if constexpr (C) {
+      sum += xs[n] * wv[g.pad * K + g.pad];
+    } else {
+      int row[K], col[K];
+      uint32_t my[K], mx[K];
 #pragma unroll
-    for (int t = 0; t < K * K; ++t) sum += tap_term(xv[t] * wv[t], my[t / K] & mx[t % K]);
+      for (int k = 0; k < K; ++k) {
+        const bool vy = static_cast<uint32_t>(by + k) < g.h;
+        const bool vx = static_cast<uint32_t>(bx + k) < g.w;
+        row[k] = vy ? (by + k) * static_cast<int>(g.w) : 0;
+        col[k] = vx ? bx + k : 0;
+        my[k] = tap_mask(vy);
+        mx[k] = tap_mask(vx);
+      }
+      float xv[K * K];
+#pragma unroll
+      for (int t = 0; t < K * K; ++t) xv[t] = xp[row[t / K] + col[t % K]];
+#pragma unroll
+      for (int t = 0; t < K * K; ++t) sum += tap_term(xv[t] * wv[t], my[t / K] & mx[t % K]);
+    }
     kept[u] = sum;
     at[u] = (n * g.out.channels + c) * oplane + r;
     conv_out[at[u]] = sum;
@@ -170,7 +182,7 @@ __global__ __launch_bounds__(kDwThreads) void dw_bn_forward_kernel(
                                               none, y, lds);
 }
 
-template <int K, int S, bool Relu, int Pre>
+template <int K, int S, bool Relu, int Pre, bool C = false>
 __global__ __launch_bounds__(kDwThreads) void dw_bn_backward_kernel(
     DwGeom g, const float *__restrict__ grad, const float *__restrict__ relu_out,
     const float *__restrict__ conv_out, const float *__restrict__ bn_weight,
@@ -252,10 +264,13 @@ __global__ __launch_bounds__(kDwThreads) void dw_bn_backward_kernel(
   if (threadIdx.x == 0) conv_dbias[c] = static_cast<float>(total);
 
   // weight gradient: per-tap sums over the channel's output positions j, j + 256, ...
-  float acc[kTaps];
+  constexpr int kSums = C ? 1 : kTaps;  // with C only the centre tap's (the others are +0)
+  float acc[kSums];
 #pragma unroll
-  for (int t = 0; t < kTaps; ++t) acc[t] = 0.0f;
-  for (uint32_t j = threadIdx.x; j < samples; j += kDwThreads) {
+  for (int t = 0; t < kSums; ++t) acc[t] = 0.0f;
+  if constexpr (C) {
+    for (uint32_t j = threadIdx.x; j < samples; j += kDwThreads) acc[0] += gs[j] * xs[j];
+  } else for (uint32_t j = threadIdx.x; j < samples; j += kDwThreads) {
     const uint32_t n = oxh::fast_div(j, g.out.spatial_div), r = j - n * oplane;
     const uint32_t oy = oxh::fast_div(r, g.ow_div), ox = r - oy * g.ow;
     const float gv = gs[j];
@@ -278,11 +293,16 @@ __global__ __launch_bounds__(kDwThreads) void dw_bn_backward_kernel(
   oxh::wave_sums_rows(acc);  // per-tap wave sums, fixed order
   if (lane == 0) {
 #pragma unroll
-    for (int t = 0; t < kTaps; ++t) wave_sums[wave][t] = acc[t];
+    for (int t = 0; t < kSums; ++t) wave_sums[wave][t] = acc[t];
   }
 
   // input gradient: input (iy, ix) feeds outputs oy = floor(ty / S) - (M - 1) + j, j < M
   auto input_sum = [&](uint32_t i) {
+    if constexpr (C) {  // image i's one output, through the centre tap
+      float a = 0.0f;
+      a += gs[i] * wts[g.pad * K + g.pad];
+      return a;
+    }
     constexpr int M = (K + S - 1) / S;
     const uint32_t n = oxh::fast_div(i, g.plane_div), r = i - n * plane;
     const uint32_t iy = oxh::fast_div(r, g.w_div), ix = r - iy * g.w;
@@ -356,9 +376,11 @@ __global__ __launch_bounds__(kDwThreads) void dw_bn_backward_kernel(
   __syncthreads();
   if (threadIdx.x < kTaps) {
     const int t = threadIdx.x;
-    float v = wave_sums[0][t];
+    const int r = C ? 0 : t;
+    float v = wave_sums[0][r];
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) v += wave_sums[w][t];
+    for (int w = 1; w < kWaves; ++w) v += wave_sums[w][r];
+    if (C && t != static_cast<int>(g.pad * K + g.pad)) v = 0.0f;
     conv_dweight[c * kTaps + t] = v;
   }
 }
@@ -409,10 +431,17 @@ void launch_forward_pre(int pre_kind, hipStream_t st, const dim3 grid, const DwG
                         const float *bw, const float *bb, const StatsOut &so, float *y,
                         const PreBnForward &pre) {
   const dim3 block(kDwThreads);
-  if (pre_kind == kPreBnRelu)
+  const bool c = centre_only(g.h, g.w, g.oh, g.ow);
+  if (pre_kind == kPreBnRelu && c)
+    oxh::launch(dw_bn_forward_kernel<K, S, Relu, kPreBnRelu, true>, grid, block, 0, st, g, x, cw, cb, co, bw, bb, so, y, pre);
+  else if (pre_kind == kPreBnRelu)
     oxh::launch(dw_bn_forward_kernel<K, S, Relu, kPreBnRelu>, grid, block, 0, st, g, x, cw, cb, co, bw, bb, so, y, pre);
+  else if (pre_kind == kPreBn && c)
+    oxh::launch(dw_bn_forward_kernel<K, S, Relu, kPreBn, true>, grid, block, 0, st, g, x, cw, cb, co, bw, bb, so, y, pre);
   else if (pre_kind == kPreBn)
     oxh::launch(dw_bn_forward_kernel<K, S, Relu, kPreBn>, grid, block, 0, st, g, x, cw, cb, co, bw, bb, so, y, pre);
+  else if (c)
+    oxh::launch(dw_bn_forward_kernel<K, S, Relu, kPreNone, true>, grid, block, 0, st, g, x, cw, cb, co, bw, bb, so, y, pre);
   else
     oxh::launch(dw_bn_forward_kernel<K, S, Relu, kPreNone>, grid, block, 0, st, g, x, cw, cb, co, bw, bb, so, y, pre);
 }
@@ -439,10 +468,17 @@ template <int K, int S, bool Relu>
 void launch_backward_pre(int pre_kind, hipStream_t st, const dim3 grid, const DwGeom &g,
                          const BackwardArgs &a, const PreBnBackward &pre) {
   const dim3 block(kDwThreads);
-  if (pre_kind == kPreBnRelu)
+  const bool c = centre_only(g.h, g.w, g.oh, g.ow);
+  if (pre_kind == kPreBnRelu && c)
+    oxh::launch(dw_bn_backward_kernel<K, S, Relu, kPreBnRelu, true>, grid, block, 0, st, g, a.gr, a.ro, a.co, a.bw, a.sm, a.si, a.x, a.cw, a.ad, a.cg, a.dbw, a.dbb, a.dcb, a.dcw, a.dx, pre);
+  else if (pre_kind == kPreBnRelu)
     oxh::launch(dw_bn_backward_kernel<K, S, Relu, kPreBnRelu>, grid, block, 0, st, g, a.gr, a.ro, a.co, a.bw, a.sm, a.si, a.x, a.cw, a.ad, a.cg, a.dbw, a.dbb, a.dcb, a.dcw, a.dx, pre);
+  else if (pre_kind == kPreBn && c)
+    oxh::launch(dw_bn_backward_kernel<K, S, Relu, kPreBn, true>, grid, block, 0, st, g, a.gr, a.ro, a.co, a.bw, a.sm, a.si, a.x, a.cw, a.ad, a.cg, a.dbw, a.dbb, a.dcb, a.dcw, a.dx, pre);
   else if (pre_kind == kPreBn)
     oxh::launch(dw_bn_backward_kernel<K, S, Relu, kPreBn>, grid, block, 0, st, g, a.gr, a.ro, a.co, a.bw, a.sm, a.si, a.x, a.cw, a.ad, a.cg, a.dbw, a.dbb, a.dcb, a.dcw, a.dx, pre);
+  else if (c)
+    oxh::launch(dw_bn_backward_kernel<K, S, Relu, kPreNone, true>, grid, block, 0, st, g, a.gr, a.ro, a.co, a.bw, a.sm, a.si, a.x, a.cw, a.ad, a.cg, a.dbw, a.dbb, a.dcb, a.dcw, a.dx, pre);
   else
     oxh::launch(dw_bn_backward_kernel<K, S, Relu, kPreNone>, grid, block, 0, st, g, a.gr, a.ro, a.co, a.bw, a.sm, a.si, a.x, a.cw, a.ad, a.cg, a.dbw, a.dbb, a.dcb, a.dcw, a.dx, pre);
 }

@@ -29,7 +29,8 @@ SHAPES = [
     (128, 192, 2, 2, 3, 1, 1),
     (128, 96, 2, 2, 3, 1, 1),
     (128, 576, 2, 2, 3, 2, 1),   # stride 2 to 1x1
-    (128, 512, 1, 1, 5, 1, 2),   # 1x1 planes: one valid tap
+    (128, 512, 1, 1, 5, 1, 2),   # 1x1 planes: one valid tap (the centre-only kernels)
+    (128, 64, 1, 1, 3, 2, 1),
     (3, 5, 7, 6, 3, 2, 1),       # ragged, output 4 x 3
     (2, 3, 9, 9, 5, 1, 2),
     (16, 4, 4, 4, 3, 1, 0),      # no padding
