@@ -12,8 +12,8 @@
 //             (bn_channel.h) over the sums, kept in registers;
 //   backward  the BatchNorm (relu) channel backward in registers; its dx (the convolution's
 //             output gradient) staged in LDS; the bias gradient as the BatchNorm backward's dx
-//             sum; the weight gradient as conv.hip's depthwise weight kernel at 256 threads
-//             (per-tap register sums, fixed-order wave sums); the input gradient as conv.hip's
+//             sum; the weight gradient as conv.hip's depthwise weight kernel at the block's
+//             thread count (per-tap register sums, fixed-order wave sums); the input gradient as conv.hip's
 //             input-backward tap kernel (ascending output taps, -0.0f outside, then + addend).
 // The channel's convolution input is staged in LDS once (coalesced plane rows) and read by
 // every tap from there.
@@ -73,21 +73,22 @@ __device__ __forceinline__ uint32_t input_index(const DwGeom &g, uint32_t c, uin
 
 // LDS copy of input channel c: xs[n * h * w + p] = x[n, c, p], kStageUnroll loads in flight
 // per thread (addresses clamped into the channel, stores guarded).
+template <int T>
 __device__ __forceinline__ void stage_channel(const DwGeom &g, uint32_t c,
                                               const float *__restrict__ x, float *xs) {
   const uint32_t plane = g.h * g.w, last = g.in_samples - 1;
-  for (uint32_t base = 0; base < g.in_samples; base += kDwThreads * kStageUnroll) {
+  for (uint32_t base = 0; base < g.in_samples; base += T * kStageUnroll) {
     float v[kStageUnroll];
 #pragma unroll
     for (int u = 0; u < kStageUnroll; ++u) {
-      uint32_t i = base + u * kDwThreads + threadIdx.x;
+      uint32_t i = base + u * T + threadIdx.x;
       i = i < last ? i : last;
       const uint32_t n = oxh::fast_div(i, g.plane_div);
       v[u] = x[(n * g.out.channels + c) * plane + (i - n * plane)];
     }
 #pragma unroll
     for (int u = 0; u < kStageUnroll; ++u) {
-      const uint32_t i = base + u * kDwThreads + threadIdx.x;
+      const uint32_t i = base + u * T + threadIdx.x;
       if (i < g.in_samples) xs[i] = v[u];
     }
   }
@@ -100,14 +101,14 @@ __host__ __device__ inline bool centre_only(uint32_t h, uint32_t w, uint32_t oh,
   return h == 1 && w == 1 && oh == 1 && ow == 1;
 }
 
-template <int K, int S, bool Relu, int Pre, bool C = false>
-__global__ __launch_bounds__(kDwThreads) void dw_bn_forward_kernel(
+template <int K, int S, bool Relu, int Pre, bool C = false, int T = 256>
+__global__ __launch_bounds__(T) void dw_bn_forward_kernel(
     DwGeom g, const float *__restrict__ x, const float *__restrict__ conv_weight,
     const float *__restrict__ conv_bias, float *__restrict__ conv_out,
     const float *__restrict__ bn_weight, const float *__restrict__ bn_bias, StatsOut stats,
     float *__restrict__ y, PreBnForward pre) {
   __shared__ float xs[kDwMaxIn];
-  __shared__ double lds[2][kDwThreads / 64];
+  __shared__ double lds[2][T / 64];
   __shared__ float shift;
   const uint32_t c = blockIdx.x;
   // the layer's parameters, loaded before the first reduction (after it they would add a
@@ -117,25 +118,25 @@ __global__ __launch_bounds__(kDwThreads) void dw_bn_forward_kernel(
   for (int t = 0; t < K * K; ++t) wv[t] = conv_weight[c * (K * K) + t];
   const float bias = conv_bias[c], w = bn_weight[c], b = bn_bias[c];
   if constexpr (Pre != kPreNone) {
-    // the BatchNorm (relu) in front over input channel c (at most kDwThreads * kChannelKeep
+    // the BatchNorm (relu) in front over input channel c (at most T * kChannelKeep
     // values), exactly as its channel kernel forms it; its output goes to LDS for the taps
     float kin[kChannelKeep], kadd[kChannelKeep];
     uint32_t ain[kChannelKeep];
     const bool add = pre.residual != nullptr;
 #pragma unroll
     for (int u = 0; u < kChannelKeep; ++u) {
-      const uint32_t j = threadIdx.x + u * kDwThreads;
+      const uint32_t j = threadIdx.x + u * T;
       ain[u] = j < g.in_samples ? input_index(g, c, j) : 0;
       kin[u] = pre.input[ain[u]];
       kadd[u] = add ? pre.residual[ain[u]] : 0.0f;
     }
     const float pshift = pre.input[input_index(g, c, 0)];
-    oxh::channel_forward_kept<Pre == kPreBnRelu, kDwThreads>(g.in_samples, c, pshift, kin, ain,
+    oxh::channel_forward_kept<Pre == kPreBnRelu, T>(g.in_samples, c, pshift, kin, ain,
                                                              pre.weight[c], pre.bias[c],
                                                              pre.stats, add, kadd, pre.output,
                                                              lds, xs);
   } else {
-    stage_channel(g, c, x, xs);
+    stage_channel<T>(g, c, x, xs);
   }
   __syncthreads();
   const uint32_t oplane = g.oh * g.ow, plane = g.h * g.w, samples = g.out.samples;
@@ -143,7 +144,7 @@ __global__ __launch_bounds__(kDwThreads) void dw_bn_forward_kernel(
   uint32_t at[kChannelKeep];
 #pragma unroll
   for (int u = 0; u < kChannelKeep; ++u) {
-    const uint32_t j = threadIdx.x + u * kDwThreads;
+    const uint32_t j = threadIdx.x + u * T;
     if (j >= samples) break;  // kept / at beyond are never read
     const uint32_t n = oxh::fast_div(j, g.out.spatial_div), r = j - n * oplane;
     const uint32_t oy = oxh::fast_div(r, g.ow_div), ox = r - oy * g.ow;
@@ -178,12 +179,12 @@ __global__ __launch_bounds__(kDwThreads) void dw_bn_forward_kernel(
   if (threadIdx.x == 0) shift = kept[0];  // conv_out[0, c, 0] (samples >= 2)
   __syncthreads();
   const float none[kChannelKeep] = {};
-  oxh::channel_forward_kept<Relu, kDwThreads>(samples, c, shift, kept, at, w, b, stats, false,
+  oxh::channel_forward_kept<Relu, T>(samples, c, shift, kept, at, w, b, stats, false,
                                               none, y, lds);
 }
 
-template <int K, int S, bool Relu, int Pre, bool C = false>
-__global__ __launch_bounds__(kDwThreads) void dw_bn_backward_kernel(
+template <int K, int S, bool Relu, int Pre, bool C = false, int T = 256>
+__global__ __launch_bounds__(T) void dw_bn_backward_kernel(
     DwGeom g, const float *__restrict__ grad, const float *__restrict__ relu_out,
     const float *__restrict__ conv_out, const float *__restrict__ bn_weight,
     const float *__restrict__ mean, const float *__restrict__ inverse_std,
@@ -191,7 +192,7 @@ __global__ __launch_bounds__(kDwThreads) void dw_bn_backward_kernel(
     float *__restrict__ conv_grad, float *__restrict__ bn_dweight, float *__restrict__ bn_dbias,
     float *__restrict__ conv_dbias, float *__restrict__ conv_dweight, float *dx,
     PreBnBackward pre) {
-  constexpr int kTaps = K * K, kWaves = kDwThreads / 64;
+  constexpr int kTaps = K * K, kWaves = T / 64;
   __shared__ float xs[kDwMaxIn];
   __shared__ float gs[kDwMaxOut];
   __shared__ float wts[kTaps];
@@ -204,13 +205,13 @@ __global__ __launch_bounds__(kDwThreads) void dw_bn_backward_kernel(
   // every load the block needs is issued here, before the first reduction: the convolution's
   // input channel (kept in registers when it fits, for the LDS copy), the addend, the
   // convolution weights, and the BatchNorm in front's input values and statistics
-  const bool kept_in = g.in_samples <= static_cast<uint32_t>(kDwThreads * kChannelKeep);
+  const bool kept_in = g.in_samples <= static_cast<uint32_t>(T * kChannelKeep);
   float xin[kChannelKeep], addv[kChannelKeep], pin[kChannelKeep];
   uint32_t pat[kChannelKeep];
   if (kept_in) {
 #pragma unroll
     for (int u = 0; u < kChannelKeep; ++u) {
-      const uint32_t j = threadIdx.x + u * kDwThreads;
+      const uint32_t j = threadIdx.x + u * T;
       pat[u] = j < g.in_samples ? input_index(g, c, j) : 0;
       xin[u] = x[pat[u]];
       addv[u] = addend != nullptr ? addend[pat[u]] : 0.0f;
@@ -231,7 +232,7 @@ __global__ __launch_bounds__(kDwThreads) void dw_bn_backward_kernel(
   uint32_t at[kChannelKeep];
 #pragma unroll
   for (int u = 0; u < kChannelKeep; ++u) {
-    const uint32_t j = threadIdx.x + u * kDwThreads;
+    const uint32_t j = threadIdx.x + u * T;
     at[u] = j < samples ? oxh::channel_index(g.out, c, j) : 0;
     float gv = grad[at[u]];
     if constexpr (Relu) gv = oxh::relu_masked(gv, relu_out[at[u]]);
@@ -241,19 +242,19 @@ __global__ __launch_bounds__(kDwThreads) void dw_bn_backward_kernel(
   if (kept_in) {
 #pragma unroll
     for (int u = 0; u < kChannelKeep; ++u) {
-      const uint32_t j = threadIdx.x + u * kDwThreads;
+      const uint32_t j = threadIdx.x + u * T;
       if (j < g.in_samples) xs[j] = xin[u];
     }
   } else {
-    stage_channel(g, c, x, xs);
+    stage_channel<T>(g, c, x, xs);
   }
   if (threadIdx.x < kTaps) wts[threadIdx.x] = wt_reg;
-  oxh::channel_backward_kept<kDwThreads>(samples, kg, kn, bn_weight[c], inv, bn_dweight + c,
+  oxh::channel_backward_kept<T>(samples, kg, kn, bn_weight[c], inv, bn_dweight + c,
                                          bn_dbias + c, d, lds[0]);
   double total = 0.0, unused = 0.0;
 #pragma unroll
   for (int u = 0; u < kChannelKeep; ++u) {
-    const uint32_t j = threadIdx.x + u * kDwThreads;
+    const uint32_t j = threadIdx.x + u * T;
     if (j >= samples) break;
     if (conv_grad != nullptr) conv_grad[at[u]] = d[u];
     gs[j] = d[u];
@@ -269,8 +270,8 @@ __global__ __launch_bounds__(kDwThreads) void dw_bn_backward_kernel(
 #pragma unroll
   for (int t = 0; t < kSums; ++t) acc[t] = 0.0f;
   if constexpr (C) {
-    for (uint32_t j = threadIdx.x; j < samples; j += kDwThreads) acc[0] += gs[j] * xs[j];
-  } else for (uint32_t j = threadIdx.x; j < samples; j += kDwThreads) {
+    for (uint32_t j = threadIdx.x; j < samples; j += T) acc[0] += gs[j] * xs[j];
+  } else for (uint32_t j = threadIdx.x; j < samples; j += T) {
     const uint32_t n = oxh::fast_div(j, g.out.spatial_div), r = j - n * oplane;
     const uint32_t oy = oxh::fast_div(r, g.ow_div), ox = r - oy * g.ow;
     const float gv = gs[j];
@@ -338,7 +339,7 @@ __global__ __launch_bounds__(kDwThreads) void dw_bn_backward_kernel(
     float kg[kChannelKeep], kn[kChannelKeep], d[kChannelKeep];
 #pragma unroll
     for (int u = 0; u < kChannelKeep; ++u) {
-      const uint32_t i = threadIdx.x + u * kDwThreads;
+      const uint32_t i = threadIdx.x + u * T;
       if (i >= g.in_samples) break;
       float a = input_sum(i);
       if (addend != nullptr) a = a + addv[u];
@@ -346,12 +347,12 @@ __global__ __launch_bounds__(kDwThreads) void dw_bn_backward_kernel(
       kg[u] = Pre == kPreBnRelu ? oxh::relu_masked(a, xs[i]) : a;
       kn[u] = (pin[u] - pmu) * pinv;
     }
-    oxh::channel_backward_kept<kDwThreads>(g.in_samples, kg, kn, pw, pinv, pre.dweight + c,
+    oxh::channel_backward_kept<T>(g.in_samples, kg, kn, pw, pinv, pre.dweight + c,
                                            pre.dbias + c, d, lds_pre[0]);
     double ptotal = 0.0, punused = 0.0;
 #pragma unroll
     for (int u = 0; u < kChannelKeep; ++u) {
-      const uint32_t i = threadIdx.x + u * kDwThreads;
+      const uint32_t i = threadIdx.x + u * T;
       if (i >= g.in_samples) break;
       pre.input_gradient[pat[u]] = d[u];
       ptotal += static_cast<double>(d[u]);
@@ -361,13 +362,13 @@ __global__ __launch_bounds__(kDwThreads) void dw_bn_backward_kernel(
   } else if (dx != nullptr && kept_in) {
 #pragma unroll
     for (int u = 0; u < kChannelKeep; ++u) {
-      const uint32_t i = threadIdx.x + u * kDwThreads;
+      const uint32_t i = threadIdx.x + u * T;
       if (i >= g.in_samples) break;
       const float a = input_sum(i);
       dx[pat[u]] = addend != nullptr ? a + addv[u] : a;
     }
   } else if (dx != nullptr) {
-    for (uint32_t i = threadIdx.x; i < g.in_samples; i += kDwThreads) {
+    for (uint32_t i = threadIdx.x; i < g.in_samples; i += T) {
       const float a = input_sum(i);
       const uint32_t idx = input_index(g, c, i);
       dx[idx] = addend != nullptr ? a + addend[idx] : a;
@@ -425,25 +426,40 @@ bool pre_eligible(const DwGeom &g) {
   return g.in_samples >= 2 && g.in_samples <= static_cast<uint32_t>(kDwThreads * kChannelKeep);
 }
 
+// Threads per channel block: 1024 for few channels (at most 128, as the separate depthwise
+// weight kernel) with at least 1024 output values, where 256 threads would leave most CUs
+// idle and each thread several values; else 256.  C: the centre-only kernels (1 x 1 planes).
+enum class DwBlock { k256, k1024, kCentre };
+DwBlock dw_block(const DwGeom &g) {
+  if (centre_only(g.h, g.w, g.oh, g.ow)) return DwBlock::kCentre;
+  return g.out.channels <= 128 && g.out.samples >= 1024 ? DwBlock::k1024 : DwBlock::k256;
+}
+
+template <int K, int S, bool Relu, int Pre>
+void launch_forward_kind(DwBlock kind, hipStream_t st, const dim3 grid, const DwGeom &g,
+                         const float *x, const float *cw, const float *cb, float *co,
+                         const float *bw, const float *bb, const StatsOut &so, float *y,
+                         const PreBnForward &pre) {
+  if (kind == DwBlock::kCentre)
+    oxh::launch(dw_bn_forward_kernel<K, S, Relu, Pre, true>, grid, dim3(256), 0, st, g, x, cw, cb, co, bw, bb, so, y, pre);
+  else if (kind == DwBlock::k1024)
+    oxh::launch(dw_bn_forward_kernel<K, S, Relu, Pre, false, 1024>, grid, dim3(1024), 0, st, g, x, cw, cb, co, bw, bb, so, y, pre);
+  else
+    oxh::launch(dw_bn_forward_kernel<K, S, Relu, Pre>, grid, dim3(256), 0, st, g, x, cw, cb, co, bw, bb, so, y, pre);
+}
+
 template <int K, int S, bool Relu>
 void launch_forward_pre(int pre_kind, hipStream_t st, const dim3 grid, const DwGeom &g,
                         const float *x, const float *cw, const float *cb, float *co,
                         const float *bw, const float *bb, const StatsOut &so, float *y,
                         const PreBnForward &pre) {
-  const dim3 block(kDwThreads);
-  const bool c = centre_only(g.h, g.w, g.oh, g.ow);
-  if (pre_kind == kPreBnRelu && c)
-    oxh::launch(dw_bn_forward_kernel<K, S, Relu, kPreBnRelu, true>, grid, block, 0, st, g, x, cw, cb, co, bw, bb, so, y, pre);
-  else if (pre_kind == kPreBnRelu)
-    oxh::launch(dw_bn_forward_kernel<K, S, Relu, kPreBnRelu>, grid, block, 0, st, g, x, cw, cb, co, bw, bb, so, y, pre);
-  else if (pre_kind == kPreBn && c)
-    oxh::launch(dw_bn_forward_kernel<K, S, Relu, kPreBn, true>, grid, block, 0, st, g, x, cw, cb, co, bw, bb, so, y, pre);
+  const DwBlock kind = dw_block(g);
+  if (pre_kind == kPreBnRelu)
+    launch_forward_kind<K, S, Relu, kPreBnRelu>(kind, st, grid, g, x, cw, cb, co, bw, bb, so, y, pre);
   else if (pre_kind == kPreBn)
-    oxh::launch(dw_bn_forward_kernel<K, S, Relu, kPreBn>, grid, block, 0, st, g, x, cw, cb, co, bw, bb, so, y, pre);
-  else if (c)
-    oxh::launch(dw_bn_forward_kernel<K, S, Relu, kPreNone, true>, grid, block, 0, st, g, x, cw, cb, co, bw, bb, so, y, pre);
+    launch_forward_kind<K, S, Relu, kPreBn>(kind, st, grid, g, x, cw, cb, co, bw, bb, so, y, pre);
   else
-    oxh::launch(dw_bn_forward_kernel<K, S, Relu, kPreNone>, grid, block, 0, st, g, x, cw, cb, co, bw, bb, so, y, pre);
+    launch_forward_kind<K, S, Relu, kPreNone>(kind, st, grid, g, x, cw, cb, co, bw, bb, so, y, pre);
 }
 
 template <bool Relu>
@@ -464,23 +480,27 @@ struct BackwardArgs {
   float *cg, *dbw, *dbb, *dcb, *dcw, *dx;
 };
 
+template <int K, int S, bool Relu, int Pre>
+void launch_backward_kind(DwBlock kind, hipStream_t st, const dim3 grid, const DwGeom &g,
+                          const BackwardArgs &a, const PreBnBackward &pre) {
+  if (kind == DwBlock::kCentre)
+    oxh::launch(dw_bn_backward_kernel<K, S, Relu, Pre, true>, grid, dim3(256), 0, st, g, a.gr, a.ro, a.co, a.bw, a.sm, a.si, a.x, a.cw, a.ad, a.cg, a.dbw, a.dbb, a.dcb, a.dcw, a.dx, pre);
+  else if (kind == DwBlock::k1024)
+    oxh::launch(dw_bn_backward_kernel<K, S, Relu, Pre, false, 1024>, grid, dim3(1024), 0, st, g, a.gr, a.ro, a.co, a.bw, a.sm, a.si, a.x, a.cw, a.ad, a.cg, a.dbw, a.dbb, a.dcb, a.dcw, a.dx, pre);
+  else
+    oxh::launch(dw_bn_backward_kernel<K, S, Relu, Pre>, grid, dim3(256), 0, st, g, a.gr, a.ro, a.co, a.bw, a.sm, a.si, a.x, a.cw, a.ad, a.cg, a.dbw, a.dbb, a.dcb, a.dcw, a.dx, pre);
+}
+
 template <int K, int S, bool Relu>
 void launch_backward_pre(int pre_kind, hipStream_t st, const dim3 grid, const DwGeom &g,
                          const BackwardArgs &a, const PreBnBackward &pre) {
-  const dim3 block(kDwThreads);
-  const bool c = centre_only(g.h, g.w, g.oh, g.ow);
-  if (pre_kind == kPreBnRelu && c)
-    oxh::launch(dw_bn_backward_kernel<K, S, Relu, kPreBnRelu, true>, grid, block, 0, st, g, a.gr, a.ro, a.co, a.bw, a.sm, a.si, a.x, a.cw, a.ad, a.cg, a.dbw, a.dbb, a.dcb, a.dcw, a.dx, pre);
-  else if (pre_kind == kPreBnRelu)
-    oxh::launch(dw_bn_backward_kernel<K, S, Relu, kPreBnRelu>, grid, block, 0, st, g, a.gr, a.ro, a.co, a.bw, a.sm, a.si, a.x, a.cw, a.ad, a.cg, a.dbw, a.dbb, a.dcb, a.dcw, a.dx, pre);
-  else if (pre_kind == kPreBn && c)
-    oxh::launch(dw_bn_backward_kernel<K, S, Relu, kPreBn, true>, grid, block, 0, st, g, a.gr, a.ro, a.co, a.bw, a.sm, a.si, a.x, a.cw, a.ad, a.cg, a.dbw, a.dbb, a.dcb, a.dcw, a.dx, pre);
+  const DwBlock kind = dw_block(g);
+  if (pre_kind == kPreBnRelu)
+    launch_backward_kind<K, S, Relu, kPreBnRelu>(kind, st, grid, g, a, pre);
   else if (pre_kind == kPreBn)
-    oxh::launch(dw_bn_backward_kernel<K, S, Relu, kPreBn>, grid, block, 0, st, g, a.gr, a.ro, a.co, a.bw, a.sm, a.si, a.x, a.cw, a.ad, a.cg, a.dbw, a.dbb, a.dcb, a.dcw, a.dx, pre);
-  else if (c)
-    oxh::launch(dw_bn_backward_kernel<K, S, Relu, kPreNone, true>, grid, block, 0, st, g, a.gr, a.ro, a.co, a.bw, a.sm, a.si, a.x, a.cw, a.ad, a.cg, a.dbw, a.dbb, a.dcb, a.dcw, a.dx, pre);
+    launch_backward_kind<K, S, Relu, kPreBn>(kind, st, grid, g, a, pre);
   else
-    oxh::launch(dw_bn_backward_kernel<K, S, Relu, kPreNone>, grid, block, 0, st, g, a.gr, a.ro, a.co, a.bw, a.sm, a.si, a.x, a.cw, a.ad, a.cg, a.dbw, a.dbb, a.dcb, a.dcw, a.dx, pre);
+    launch_backward_kind<K, S, Relu, kPreNone>(kind, st, grid, g, a, pre);
 }
 
 template <bool Relu>
