@@ -1349,27 +1349,33 @@ struct SerialTileLds16 {
   float bs[16][ProductRow<16, 256>::value];
 };
 // The paired launch's LDS: the weight gradient's split tiles and the input gradient's tiles
-// (only the kind it takes, so the serial pairing keeps its occupancy).
-template <bool Split1>
+// of the kind S1 (input_splits) it takes, and only those, so each pairing keeps its occupancy.
+template <int S1>
 union DualLds {
   SplitLds split;
   SerialTileLds16 tile;
 };
 template <>
-union DualLds<true> {
+union DualLds<1> {
+  SplitLds split;
+};
+template <>
+union DualLds<2> {
   SplitLds split;
   SplitLds16 split16;
 };
 
-template <bool A1, bool B1, bool A2, bool B2, bool Split1 = false>
+template <bool A1, bool B1, bool A2, bool B2, int S1 = 0>
 __global__ __launch_bounds__(kSplitThreads) void pointwise_dual_kernel(ProductArgs g1,
                                                                        ProductArgs g2,
                                                                        DualGrid d) {
-  __shared__ __align__(16) DualLds<Split1> lds;
+  __shared__ __align__(16) DualLds<S1> lds;
   uint32_t b = blockIdx.x;
   if (b < d.blocks1) {
-    if constexpr (Split1)  // the input gradient as its own launch splits it (input_splits)
+    if constexpr (S1 == 2)
       split_tile16<A1, B1>(g1, b % d.nx1, b / d.nx1, 0, lds.split16);
+    else if constexpr (S1 == 1)
+      split_tile<A1, B1>(g1, b % d.nx1, b / d.nx1, 0, lds.split);
     else
       product_tile<16, 256, A1, B1>(g1, b % d.nx1, b / d.nx1, 0, lds.tile.as, lds.tile.bs);
   } else if (b < d.blocks1 + d.blocks2) {
@@ -1778,14 +1784,15 @@ int split_kind(uint32_t M, uint32_t N, uint32_t k_chunk, uint32_t chunks) {
   return OXH_SPLIT16 ? 2 : 0;
 }
 
-// A pointwise input gradient leaves the serial order only for grids of many small tiles (the
-// 16 x 16 split tiles): there the serial chain of every output over the output channels sets
-// the time.
+// A pointwise input gradient over at least kSplitMinK output channels whose grid would leave
+// the chip waiting on the serial chain of every output takes the split tiles of the forward's
+// rule (split_kind: 0 serial, 1 split 8 x 8, 2 split 16 x 16), alone and in the paired launch.
 #ifndef OXH_IG_SPLIT
-#define OXH_IG_SPLIT 1
+#define OXH_IG_SPLIT 2  // the largest split kind the input gradient takes (0: always serial)
 #endif
-bool input_splits(const ProductArgs &x) {
-  return OXH_IG_SPLIT && split_kind(x.M, x.N, x.k_chunk, 1) == 2;
+int input_splits(const ProductArgs &x) {
+  const int kind = split_kind(x.M, x.N, x.k_chunk, 1);
+  return kind <= OXH_IG_SPLIT ? kind : 0;
 }
 
 template <bool A, bool B>
@@ -1967,9 +1974,11 @@ bool launch_dual(hipStream_t s, const ProductArgs &w, const KSplit &split, const
                  const BiasArgs &bias) {
   if (split.serial32 || big_tiles(w, split.chunks) + big_tiles(x, 1) >= kSmallGrid)
     return false;
+  const int s1 = input_splits(x);
+  const uint32_t t1 = s1 == 1 ? 8 : 16;  // the input gradient's tile
   DualGrid d;
-  d.nx1 = (x.N + 15) / 16;
-  d.ny1 = (x.M + 15) / 16;
+  d.nx1 = (x.N + t1 - 1) / t1;
+  d.ny1 = (x.M + t1 - 1) / t1;
   d.blocks1 = d.nx1 * d.ny1;
   d.nx2 = (w.N + 7) / 8;
   d.ny2 = (w.M + 7) / 8;
@@ -1977,17 +1986,20 @@ bool launch_dual(hipStream_t s, const ProductArgs &w, const KSplit &split, const
   d.bias = bias;
   const uint32_t blocks3 = bias.out != nullptr ? bias_blocks(bias.out_c) : 0;
   const dim3 grid(d.blocks1 + d.blocks2 + blocks3), block(kSplitThreads);
-  const bool split1 = input_splits(x);
   if (w.a.k_fast && w.b.k_fast && !x.a.k_fast && !x.b.k_fast) {
-    if (split1)
-      oxh::launch(pointwise_dual_kernel<false, false, true, true, true>, grid, block, 0, s, x, w,
-                  d);
+    if (s1 == 2)
+      oxh::launch(pointwise_dual_kernel<false, false, true, true, 2>, grid, block, 0, s, x, w, d);
+    else if (s1 == 1)
+      oxh::launch(pointwise_dual_kernel<false, false, true, true, 1>, grid, block, 0, s, x, w, d);
     else
       oxh::launch(pointwise_dual_kernel<false, false, true, true>, grid, block, 0, s, x, w, d);
   } else if (!w.a.k_fast && !w.b.k_fast && !x.a.k_fast && x.b.k_fast) {
-    if (split1)
-      oxh::launch(pointwise_dual_kernel<false, true, false, false, true>, grid, block, 0, s, x,
-                  w, d);
+    if (s1 == 2)
+      oxh::launch(pointwise_dual_kernel<false, true, false, false, 2>, grid, block, 0, s, x, w,
+                  d);
+    else if (s1 == 1)
+      oxh::launch(pointwise_dual_kernel<false, true, false, false, 1>, grid, block, 0, s, x, w,
+                  d);
     else
       oxh::launch(pointwise_dual_kernel<false, true, false, false>, grid, block, 0, s, x, w, d);
   } else {
@@ -2009,7 +2021,7 @@ oxh_status input_backward_impl(const char *name, oxh_stream stream,
   hipStream_t s = oxh::as_stream(stream);
   if (pointwise(g)) {
     const ProductArgs x = input_product(g, gradient, weight, addend, input_gradient);
-    return launch_product(name, s, x, 1, input_splits(x));
+    return launch_product(name, s, x, 1, input_splits(x) != 0);
   }
   const PhasePlan pp = input_backward_s2_plan(g);
   if (pp.lds_bytes > 0) {
@@ -2065,7 +2077,7 @@ int oxh_conv2d_input_backward_serial(const oxh_conv2d_shape *shape) {
   ConvGeom g;
   if (make_conv_geom("oxh_conv2d_input_backward_serial", shape, g) != OXH_OK) return -1;
   if (!pointwise(g)) return 1;
-  return input_splits(input_product(g, nullptr, nullptr, nullptr, nullptr)) ? 0 : 1;
+  return input_splits(input_product(g, nullptr, nullptr, nullptr, nullptr)) != 0 ? 0 : 1;
 }
 
 int oxh_conv2d_forward_serial(const oxh_conv2d_shape *shape) {

@@ -281,14 +281,17 @@ def test_conv_forward_order_query():
 
 
 def test_conv_input_gradient_order_query():
-    """oxh_conv2d_input_backward_serial: only a pointwise input gradient over many output
-    channels whose grid has many small tiles (the MNIST MobileNetV4's 960 -> 1280 head) sums
-    four ordered parts; the paired backward launches and the K x K kernels stay serial."""
+    """oxh_conv2d_input_backward_serial: a pointwise input gradient over at least 256 output
+    channels on a grid that leaves the chip waiting on its serial chains (the MNIST
+    MobileNetV4's head, its 1x1-plane expands and the 960-channel conv) sums four ordered parts;
+    short channel sums, large grids and the K x K kernels stay serial."""
     sh = ox.conv2d_shape
     assert not ox.conv2d_input_backward_serial(sh(128, 960, 1, 1, 1280, 1, 1, 0, 1))  # head
-    assert ox.conv2d_input_backward_serial(sh(128, 128, 1, 1, 960, 1, 1, 0, 1))       # paired
-    assert ox.conv2d_input_backward_serial(sh(128, 128, 1, 1, 512, 1, 1, 0, 1))
+    assert not ox.conv2d_input_backward_serial(sh(128, 128, 1, 1, 960, 1, 1, 0, 1))
+    assert not ox.conv2d_input_backward_serial(sh(128, 128, 1, 1, 512, 1, 1, 0, 1))   # expand
+    assert ox.conv2d_input_backward_serial(sh(128, 512, 1, 1, 128, 1, 1, 0, 1))       # project
     assert ox.conv2d_input_backward_serial(sh(128, 1280, 1, 1, 10, 1, 1, 0, 1))       # classifier
+    assert ox.conv2d_input_backward_serial(sh(128, 64, 8, 8, 256, 1, 1, 0, 1))        # large grid
     assert ox.conv2d_input_backward_serial(sh(128, 32, 7, 7, 96, 3, 2, 1, 1))         # K x K
     with pytest.raises(ox.OxideError):
         ox.conv2d_input_backward_serial(sh(1, 1, 1, 1, 1, 3, 1, 0, 1))
