@@ -126,13 +126,25 @@ __device__ __forceinline__ void finish_row(const CeArgs &a, uint64_t row, float 
 // Batch mean of the row losses (one block): thread t adds rows t, t + 1024, ... in order, then a
 // fixed-shape tree, so the result is deterministic.  evaluation.rs:616-619 divides the summed
 // loss by the batch size in fp32.
-constexpr int kMeanBlock = 1024;
+constexpr int kMeanBlock = 1024, kMeanLoads = 8;
 
 __global__ __launch_bounds__(kMeanBlock) void ce_mean_kernel(const double *__restrict__ row_loss,
                                                              uint64_t batch, float *loss) {
   __shared__ double lds[kMeanBlock / 64];
   double s = 0.0;
-  for (uint64_t r = threadIdx.x; r < batch; r += kMeanBlock) s += row_loss[r];
+  // kMeanLoads loads in flight per round (the row losses come from other XCDs' writes: one
+  // memory round trip each), then the adds in row order
+  for (uint64_t base = 0; base < batch; base += kMeanBlock * kMeanLoads) {
+    double v[kMeanLoads];
+#pragma unroll
+    for (int i = 0; i < kMeanLoads; ++i) {
+      const uint64_t r = base + threadIdx.x + static_cast<uint64_t>(i) * kMeanBlock;
+      v[i] = r < batch ? row_loss[r] : 0.0;
+    }
+#pragma unroll
+    for (int i = 0; i < kMeanLoads; ++i)
+      if (base + threadIdx.x + static_cast<uint64_t>(i) * kMeanBlock < batch) s += v[i];
+  }
   s = block_sum<kMeanBlock>(s, lds);
   if (threadIdx.x == 0) *loss = static_cast<float>(s) / static_cast<float>(batch);
 }
@@ -243,20 +255,36 @@ __global__ __launch_bounds__(BLOCK, MINW) void ce_row_kernel(CeArgs a) {
 // a block keeps two rows in VGPRs and walks rows blockIdx.x, blockIdx.x + gridDim.x, ...; the
 // next row's loads are issued before the current row's reductions, exp and gradient stores, so
 // a CU's memory pipe stays busy through the compute phases (barriers wait only on LDS, never on
-// outstanding global loads).  One 512-lane block per CU (230 VGPRs).  Measured at [8192, 32768]
+// outstanding global loads).  One 512-lane block per CU (~240 VGPRs).  Measured at [8192, 32768]
 // fused: 375 us against 378-412 us for two independent row blocks per CU (whose load, compute
 // and store phases fall into step); a forward alone (reads only) is faster with the two
-// independent blocks (160 against 225 us), so it keeps them.  Nothing is read from global memory after the next row's loads are in flight: the
-// target logit comes from the owner lane's registers, which also writes the row's loss.
-// Arithmetic per element and per row as ce_row_kernel.
+// independent blocks (160 against 225 us), so it keeps them.  The logits and the gradient move
+// through non-temporal buffer loads and stores on a per-row resource (the lane's offset in a
+// VGPR, the part's offset k * BLOCK * 16 in a scalar): 364 against 373 us with 64-bit lane
+// addresses.  The same launch copying the rows without the softmax takes as long (366 us), so
+// the arithmetic is hidden and the row-per-CU access pattern sets the rate.  Nothing is read
+// from global memory after the next row's loads are in flight: the target logit comes from the
+// owner lane's registers, which also writes the row's loss.  Arithmetic per element and per row
+// as ce_row_kernel.
+constexpr int kBufferNt = 2;  // buffer instruction cache policy: non-temporal
+typedef unsigned u32x4_t __attribute__((vector_size(16)));
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_resource(const float *row, uint64_t classes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(row), 0,
+                                           static_cast<int>(classes * 4), 0x00020000);
+}
+
 template <int BLOCK, int V>
 __device__ __forceinline__ void ce_pipe_load(const CeArgs &a, uint64_t row, float4 (&v)[V],
                                              float &target_value) {
-  const float4 *x4 = reinterpret_cast<const float4 *>(a.logits + row * a.classes);
+  const __amdgpu_buffer_rsrc_t r = row_resource(a.logits + row * a.classes, a.classes);
 #pragma unroll
-  for (int k = 0; k < V; ++k)
-    v[k] = (OXH_CE_NT & 1) != 0 ? oxh::load_nt(x4 + threadIdx.x + k * BLOCK)
-                                : x4[threadIdx.x + k * BLOCK];
+  for (int k = 0; k < V; ++k) {
+    const u32x4_t u =
+        __builtin_amdgcn_raw_buffer_load_b128(r, threadIdx.x * 16, k * BLOCK * 16, kBufferNt);
+    v[k] = make_float4(__uint_as_float(u[0]), __uint_as_float(u[1]), __uint_as_float(u[2]),
+                       __uint_as_float(u[3]));
+  }
   target_value = a.targets[row];
 }
 
@@ -277,15 +305,17 @@ __device__ __forceinline__ void ce_pipe_row(const CeArgs &a, uint64_t row, float
   const uint32_t t4 = static_cast<uint32_t>(target / 4);
   const uint32_t owner = t4 % BLOCK, kt = t4 / BLOCK, ct = static_cast<uint32_t>(target % 4);
   const bool own = valid && threadIdx.x == owner;
-  float xt = 0.0f;
+  // the target's logit and exp by selects (kt and ct are uniform; only the owner lane's values
+  // are used), so no lane diverges
+  float xt = 0.0f, et = 0.0f;
 #pragma unroll
-  for (int k = 0; k < V; ++k)
-    if (own && static_cast<uint32_t>(k) == kt) xt = component(v[k], ct);
+  for (int k = 0; k < V; ++k) xt = static_cast<uint32_t>(k) == kt ? component(v[k], ct) : xt;
   float part[V];
 #pragma unroll
   for (int k = 0; k < V; ++k) {
     v[k] = exp4_nonpos(v[k], maximum);
     part[k] = (v[k].x + v[k].y) + (v[k].z + v[k].w);
+    et = static_cast<uint32_t>(k) == kt ? component(v[k], ct) : et;
   }
 #pragma unroll
   for (int w = 1; w < V; w *= 2)
@@ -295,22 +325,22 @@ __device__ __forceinline__ void ce_pipe_row(const CeArgs &a, uint64_t row, float
       static_cast<float>(block_sum<BLOCK>(static_cast<double>(part[0]), lds_d));
   if (!valid && threadIdx.x == 0 && a.error_flag) *a.error_flag = 1u;
   if (a.grad) {
-    float4 *g4 = reinterpret_cast<float4 *>(a.grad + row * a.classes);
+    const __amdgpu_buffer_rsrc_t gr = row_resource(a.grad + row * a.classes, a.classes);
     const float scale = outer / static_cast<float>(a.batch);
     const float sr = scale / normalizer;
+    const float gt = scale * (et / normalizer - 1.0f);
 #pragma unroll
     for (int k = 0; k < V; ++k) {
       float4 r = valid ? make_float4(v[k].x * sr, v[k].y * sr, v[k].z * sr, v[k].w * sr)
                        : make_float4(NAN, NAN, NAN, NAN);
-      if (own && static_cast<uint32_t>(k) == kt) {
-        const float gt = scale * (component(v[k], ct) / normalizer - 1.0f);
-        if (ct == 0) r.x = gt;
-        else if (ct == 1) r.y = gt;
-        else if (ct == 2) r.z = gt;
-        else r.w = gt;
-      }
-      if constexpr ((OXH_CE_NT & 2) != 0) oxh::store_nt(g4 + threadIdx.x + k * BLOCK, r);
-      else g4[threadIdx.x + k * BLOCK] = r;
+      const bool here = own && static_cast<uint32_t>(k) == kt;
+      r.x = here && ct == 0 ? gt : r.x;
+      r.y = here && ct == 1 ? gt : r.y;
+      r.z = here && ct == 2 ? gt : r.z;
+      r.w = here && ct == 3 ? gt : r.w;
+      const u32x4_t u = {__float_as_uint(r.x), __float_as_uint(r.y), __float_as_uint(r.z),
+                         __float_as_uint(r.w)};
+      __builtin_amdgcn_raw_buffer_store_b128(u, gr, threadIdx.x * 16, k * BLOCK * 16, kBufferNt);
     }
   }
   if (a.loss != nullptr && (valid ? own : threadIdx.x == 0))
