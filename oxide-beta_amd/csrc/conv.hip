@@ -1167,6 +1167,78 @@ __device__ __forceinline__ void product_sum(
   }
 }
 
+#ifndef OXH_SPLIT_MFMA
+#define OXH_SPLIT_MFMA 1  // 1: the 16 x 16 split tiles sum on the matrix cores
+#endif
+#ifndef OXH_TILE32_MFMA
+#define OXH_TILE32_MFMA 1  // 1: the 32 x 32 tiles' fused-multiply-add sums on the matrix cores
+#endif
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// A tile's sum over [kb, ke) on the matrix cores: the Threads threads (t = 0 .. Threads - 1)
+// stage Tile x kSlab slabs of both operands as product_sum<Tile, Threads> does (same loads,
+// staging and barriers), and wave w = t / 64 sums the 16 x 16 quadrant (w / (Tile / 16),
+// w % (Tile / 16)) of the tile.  v_mfma_f32_16x16x4_f32 takes A[i][k] from lane i + 16 k and
+// B[k][j] from lane j + 16 k and leaves D[i][j] in lane j + 16 (i / 4), register i % 4 (the
+// layout acc uses).  Per 16 k, lane (i, q) reads A[i][k + 4q .. 4q + 3] and B's row i likewise
+// as 128-bit LDS accesses and issues four MFMAs, the s-th with component s, so lane group q
+// supplies k + 4q + s: the 16 k of the group, each once.  k at or past the slab's count are
+// zeroed in both operands.  Each MFMA adds its four products to the accumulator with fused
+// roundings (a tolerance-bar sum).
+template <int Tile, int Threads, bool AKFast, bool BKFast>
+__device__ __forceinline__ void product_sum_mfma(const ProductArgs &g, uint32_t m0, uint32_t n0,
+                                                 uint32_t kb, uint32_t ke, uint32_t slabs, int t,
+                                                 f32x4_t &acc,
+                                                 float (*as)[ProductRow<Tile, Threads>::value],
+                                                 float (*bs)[ProductRow<Tile, Threads>::value]) {
+  using S = TileShape<Tile, Threads>;
+  constexpr int kLoads = S::kLoads, kSlab = S::kSlab, kQuads = Tile / 16;
+  static_assert(Threads == 64 * kQuads * kQuads, "one wave per 16 x 16 quadrant");
+  static_assert(kSlab % 16 == 0 && kSlab + 4 <= ProductRow<Tile, Threads>::value, "mfma slab");
+  const SlabLoader<Tile, Threads, AKFast> la(g.a, m0, g.M, t);
+  const SlabLoader<Tile, Threads, BKFast> lb(g.b, n0, g.N, t);
+  float va[kLoads], vb[kLoads];
+  if (kb < ke) {
+    const uint32_t kc = min(ke - kb, static_cast<uint32_t>(kSlab));
+    la.fetch(g.a, kb, kc, va);
+    lb.fetch(g.b, kb, kc, vb);
+  }
+  const int w = t / 64, lane = t % 64;
+  const int ia = 16 * (w / kQuads) + lane % 16, ib = 16 * (w % kQuads) + lane % 16;
+  const int q = lane / 16;
+  for (uint32_t s = 0; s < slabs; ++s) {
+    const uint32_t k0 = kb + s * kSlab;
+    const uint32_t kc = k0 < ke ? min(ke - k0, static_cast<uint32_t>(kSlab)) : 0;
+    if (kc > 0) {
+      la.stage(va, as);
+      lb.stage(vb, bs);
+    }
+    __syncthreads();
+    const uint32_t k1 = k0 + kSlab;
+    if (k1 < ke) {
+      const uint32_t kc1 = min(ke - k1, static_cast<uint32_t>(kSlab));
+      la.fetch(g.a, k1, kc1, va);
+      lb.fetch(g.b, k1, kc1, vb);
+    }
+    for (uint32_t kk = 0; kk < kc; kk += 16) {
+      float4 a = *reinterpret_cast<const float4 *>(&as[ia][kk + 4 * q]);
+      float4 b = *reinterpret_cast<const float4 *>(&bs[ib][kk + 4 * q]);
+      if (kk + 16 > kc) {
+        const uint32_t k = kk + 4 * static_cast<uint32_t>(q);
+        if (k >= kc) a.x = b.x = 0.0f;
+        if (k + 1 >= kc) a.y = b.y = 0.0f;
+        if (k + 2 >= kc) a.z = b.z = 0.0f;
+        if (k + 3 >= kc) a.w = b.w = 0.0f;
+      }
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b.x, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b.y, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b.z, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b.w, acc, 0, 0, 0);
+    }
+    __syncthreads();
+  }
+}
+
 // Output (m, n) of chunk bz: c[bz * c_chunk + offset(cm, m) + offset(cn, n)] = sum (+ addend).
 __device__ __forceinline__ void product_store(const ProductArgs &g, uint32_t bz, uint32_t m,
                                               uint32_t n, float sum, float added) {
@@ -1188,6 +1260,28 @@ __device__ __forceinline__ void product_tile(const ProductArgs &g, uint32_t bx, 
   const uint32_t kb = bz * g.k_chunk;
   const uint32_t ke = min(kb + g.k_chunk, g.K);
   const int t = static_cast<int>(threadIdx.x), tx = t % kCols, ty = t / kCols;
+  if constexpr (Fma && Tile == kTile && Threads == 256 && OXH_TILE32_MFMA != 0) {
+    // wave w sums quadrant (w / 2, w % 2); lane l holds outputs
+    // (m0 + 16 (w / 2) + 4 (l / 16) + r, n0 + 16 (w % 2) + l % 16), r = 0 .. 3
+    const int w = t / 64, l = t % 64;
+    const uint32_t mq = m0 + 16 * static_cast<uint32_t>(w / 2) + 4 * static_cast<uint32_t>(l / 16);
+    const uint32_t n = n0 + 16 * static_cast<uint32_t>(w % 2) + static_cast<uint32_t>(l % 16);
+    f32x4_t acc;
+    float added[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t m = mq + r;
+      acc[r] = g.init != nullptr && m < g.M ? g.init[m] : 0.0f;
+      added[r] = g.addend != nullptr && m < g.M && n < g.N
+                     ? g.addend[axis_offset(g.cm, m) + axis_offset(g.cn, n)]
+                     : 0.0f;
+    }
+    const uint32_t slabs = kb < ke ? (ke - kb + S::kSlab - 1) / S::kSlab : 0;
+    product_sum_mfma<Tile, Threads, AKFast, BKFast>(g, m0, n0, kb, ke, slabs, t, acc, as, bs);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) product_store(g, bz, mq + r, n, acc[r], added[r]);
+    return;
+  }
   float acc[kMicro][kMicro];
 #pragma unroll
   for (int i = 0; i < kMicro; ++i) {
@@ -1296,6 +1390,36 @@ __device__ __forceinline__ void split_tile16(const ProductArgs &g, uint32_t bx, 
   const int tx = t % kCols, ty = t / kCols;
   const uint32_t wb = min(kb + w * part, ke), we = min(wb + part, ke);
   const uint32_t slabs = (part + S::kSlab - 1) / S::kSlab;  // equal for every wave (barriers)
+  if constexpr (OXH_SPLIT_MFMA != 0) {
+    // lane t holds outputs (m0 + 4 (t / 16) + r, n0 + t % 16), r = 0 .. 3
+    const uint32_t n = n0 + static_cast<uint32_t>(t % 16);
+    f32x4_t acc;
+    float added[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t m = m0 + 4 * static_cast<uint32_t>(t / 16) + r;
+      acc[r] = w == 0 && g.init != nullptr && m < g.M ? g.init[m] : 0.0f;
+      added[r] = w == 0 && g.addend != nullptr && m < g.M && n < g.N
+                     ? g.addend[axis_offset(g.cm, m) + axis_offset(g.cn, n)]
+                     : 0.0f;
+    }
+    product_sum_mfma<16, 64, AKFast, BKFast>(g, m0, n0, wb, we, slabs, t, acc, lds.as[w],
+                                             lds.bs[w]);
+    if (w > 0) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) lds.part[w - 1][r][t] = acc[r];
+    }
+    __syncthreads();
+    if (w > 0) return;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float sum = acc[r];
+#pragma unroll
+      for (int p = 0; p < kSplitWaves - 1; ++p) sum += lds.part[p][r][t];
+      product_store(g, bz, m0 + 4 * static_cast<uint32_t>(t / 16) + r, n, sum, added[r]);
+    }
+    return;
+  }
   float acc[kMicro][kMicro], added[kMicro][kMicro];
 #pragma unroll
   for (int i = 0; i < kMicro; ++i)
@@ -1764,7 +1888,10 @@ void launch_split(hipStream_t s, const ProductArgs &a, uint32_t chunks);
 // instead (contiguous parts of k added in order: the same sum within a few roundings, a
 // quarter of the serial chain, four times the waves of a grid that leaves most of the chip
 // idle).
-constexpr uint64_t kSplitMaxTiles = 512;
+#ifndef OXH_SPLIT_MAX_TILES
+#define OXH_SPLIT_MAX_TILES 512
+#endif
+constexpr uint64_t kSplitMaxTiles = OXH_SPLIT_MAX_TILES;
 #ifndef OXH_SPLIT_MIN_K
 #define OXH_SPLIT_MIN_K 256
 #endif
