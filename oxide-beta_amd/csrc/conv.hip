@@ -1239,6 +1239,71 @@ __device__ __forceinline__ void product_sum_mfma(const ProductArgs &g, uint32_t 
   }
 }
 
+#ifndef OXH_SPLIT8_MFMA
+#define OXH_SPLIT8_MFMA 1  // 1: the 8 x 8 split tiles sum on the matrix cores
+#endif
+
+// An 8 x 8 tile's sum over [kb, ke) on the matrix cores (one wave, t = lane), with slab loads,
+// staging and barriers as product_sum<8, 64>.  v_mfma_f32_4x4x1f32 runs 16 independent 4 x 4
+// outer products: block b takes A_b[i] from lane 4 b + i and B_b[j] from lane 4 b + j and
+// leaves D_b[i][j] in lane 4 b + j, register i.  Block b = 4 d + p sums quadrant d (rows
+// 4 (d / 2) .. + 3, columns 4 (d % 2) .. + 3) over the k of phase p: per 16 k, lane (b, i)
+// reads A's row 4 (d / 2) + i at k + 4p .. 4p + 3 (and B's row 4 (d % 2) + i) as 128-bit LDS
+// accesses and issues four MFMAs, the c-th with component c (k + 4p + c).  k at or past the
+// slab's count are zeroed in both operands.  acc[i] of lane 4 b + j: phase p's sum for output
+// (4 (d / 2) + i, 4 (d % 2) + j) of the tile.
+template <bool AKFast, bool BKFast>
+__device__ __forceinline__ void product_sum_mfma8(const ProductArgs &g, uint32_t m0, uint32_t n0,
+                                                  uint32_t kb, uint32_t ke, uint32_t slabs,
+                                                  int t, f32x4_t &acc,
+                                                  float (*as)[ProductRow<8, 64>::value],
+                                                  float (*bs)[ProductRow<8, 64>::value]) {
+  using S = TileShape<8, 64>;
+  constexpr int kLoads = S::kLoads, kSlab = S::kSlab;
+  static_assert(kSlab % 16 == 0 && kSlab + 4 <= ProductRow<8, 64>::value, "mfma slab");
+  const SlabLoader<8, 64, AKFast> la(g.a, m0, g.M, t);
+  const SlabLoader<8, 64, BKFast> lb(g.b, n0, g.N, t);
+  float va[kLoads], vb[kLoads];
+  if (kb < ke) {
+    const uint32_t kc = min(ke - kb, static_cast<uint32_t>(kSlab));
+    la.fetch(g.a, kb, kc, va);
+    lb.fetch(g.b, kb, kc, vb);
+  }
+  const int d = t / 16, p = (t / 4) % 4, i = t % 4;
+  const int ra = 4 * (d / 2) + i, rb = 4 * (d % 2) + i;
+  for (uint32_t s = 0; s < slabs; ++s) {
+    const uint32_t k0 = kb + s * kSlab;
+    const uint32_t kc = k0 < ke ? min(ke - k0, static_cast<uint32_t>(kSlab)) : 0;
+    if (kc > 0) {
+      la.stage(va, as);
+      lb.stage(vb, bs);
+    }
+    __syncthreads();
+    const uint32_t k1 = k0 + kSlab;
+    if (k1 < ke) {
+      const uint32_t kc1 = min(ke - k1, static_cast<uint32_t>(kSlab));
+      la.fetch(g.a, k1, kc1, va);
+      lb.fetch(g.b, k1, kc1, vb);
+    }
+    for (uint32_t kk = 0; kk < kc; kk += 16) {
+      float4 a = *reinterpret_cast<const float4 *>(&as[ra][kk + 4 * p]);
+      float4 b = *reinterpret_cast<const float4 *>(&bs[rb][kk + 4 * p]);
+      if (kk + 16 > kc) {
+        const uint32_t k = kk + 4 * static_cast<uint32_t>(p);
+        if (k >= kc) a.x = b.x = 0.0f;
+        if (k + 1 >= kc) a.y = b.y = 0.0f;
+        if (k + 2 >= kc) a.z = b.z = 0.0f;
+        if (k + 3 >= kc) a.w = b.w = 0.0f;
+      }
+      acc = __builtin_amdgcn_mfma_f32_4x4x1f32(a.x, b.x, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_4x4x1f32(a.y, b.y, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_4x4x1f32(a.z, b.z, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_4x4x1f32(a.w, b.w, acc, 0, 0, 0);
+    }
+    __syncthreads();
+  }
+}
+
 // Output (m, n) of chunk bz: c[bz * c_chunk + offset(cm, m) + offset(cn, n)] = sum (+ addend).
 __device__ __forceinline__ void product_store(const ProductArgs &g, uint32_t bz, uint32_t m,
                                               uint32_t n, float sum, float added) {
@@ -1330,7 +1395,7 @@ constexpr int kSplitThreads = 64 * kSplitWaves;
 struct SplitLds {
   float as[kSplitWaves][8][ProductRow<8, 64>::value];
   float bs[kSplitWaves][8][ProductRow<8, 64>::value];
-  float part[kSplitWaves - 1][64];
+  float part[kSplitWaves][64];
 };
 
 template <bool AKFast, bool BKFast>
@@ -1346,6 +1411,33 @@ __device__ __forceinline__ void split_tile(const ProductArgs &g, uint32_t bx, ui
   const uint32_t wb = min(kb + w * part, ke), we = min(wb + part, ke);
   const uint32_t slabs = (part + kSlab - 1) / kSlab;  // equal for every wave (barriers)
   const uint32_t m = m0 + t / 8, n = n0 + t % 8;
+  if constexpr (OXH_SPLIT8_MFMA != 0) {
+    const float init = w == 0 && g.init != nullptr && m < g.M ? g.init[m] : 0.0f;
+    const float added = w == 0 && g.addend != nullptr && m < g.M && n < g.N
+                            ? g.addend[axis_offset(g.cm, m) + axis_offset(g.cn, n)]
+                            : 0.0f;
+    f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    product_sum_mfma8<AKFast, BKFast>(g, m0, n0, wb, we, slabs, t, acc, lds.as[w], lds.bs[w]);
+    // the four k phases of a quadrant (lanes 16 d + 4 p + j, p = 0 .. 3), added as
+    // (p0 + p1) + (p2 + p3); lanes of phase 0 then hold the wave's part of the quadrant
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      acc[r] += __shfl_xor(acc[r], 4);
+      acc[r] += __shfl_xor(acc[r], 8);
+    }
+    if ((t / 4) % 4 == 0) {
+      const int d = t / 16, j = t % 4;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) lds.part[w][(4 * (d / 2) + r) * 8 + 4 * (d % 2) + j] = acc[r];
+    }
+    __syncthreads();
+    if (w > 0) return;
+    float sum = init;
+#pragma unroll
+    for (int q = 0; q < kSplitWaves; ++q) sum += lds.part[q][t];
+    product_store(g, bz, m, n, sum, added);
+    return;
+  }
   float acc[1][1] = {{w == 0 && g.init != nullptr && m < g.M ? g.init[m] : 0.0f}};
   const float added = w == 0 && g.addend != nullptr && m < g.M && n < g.N
                           ? g.addend[axis_offset(g.cm, m) + axis_offset(g.cn, n)]
