@@ -1921,8 +1921,8 @@ constexpr uint64_t kSmallGrid = OXH_SMALL_GRID;
 
 // k chunks of the pointwise weight gradient.  Grids of >= kSmallGrid 32 x 32 tiles (with their
 // chunks: about 512 blocks, at least 64 k per chunk, when k > OXH_SINGLE_K) take the serial
-// 32 x 32 tiling (serial32); smaller ones the split tiles, chunked for about OXH_SPLIT_TARGET waves
-// with at least 4 * 128 k per chunk.  Every chunk is non-empty.
+// 32 x 32 tiling (serial32); smaller ones the split tiles, chunked for about OXH_SPLIT_TARGET
+// waves with at least 4 * 128 k per chunk.  Every chunk is non-empty.
 #ifndef OXH_SPLIT_TARGET
 #define OXH_SPLIT_TARGET 512
 #endif
