@@ -41,6 +41,7 @@ CASES = [
     # plane too large to stage (per-thread tap kernels)
     (128, 32, 7, 7, 96, 3, 2, 1),      # config 5's second fused-IB convolution at full batch
     (5, 24, 6, 6, 40, 3, 1, 1),
+    (2, 18, 6, 6, 20, 3, 1, 1),        # matrix-core forward: channels not multiples of 4 / 16
     (4, 16, 9, 7, 24, 5, 1, 1),
     (3, 8, 11, 10, 12, 5, 2, 1),
     (2, 64, 20, 20, 16, 3, 1, 1),
