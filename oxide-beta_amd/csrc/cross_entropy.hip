@@ -420,33 +420,63 @@ __global__ __launch_bounds__(kGenBlock) void ce_row_general_kernel(CeArgs a) {
 constexpr int kSmallRows = 1024;
 constexpr uint64_t kSmallClasses = 64;
 
+// One thread per row, the block as many waves as the rows fill.  The row's C <= 64 logits are
+// loaded at once (indices clamped into the row, the extra lanes of the array unused), each exp
+// is formed once and kept for the gradient; sums in class order (fp64), as the CPU path.  The
+// batch loss: wave sums, then the block's waves in order (bit-identical to a block of 1024
+// threads whose extra rows add 0).
+template <int C>
 __global__ __launch_bounds__(kSmallRows) void ce_small_kernel(CeArgs a) {
   __shared__ double lds[kSmallRows / 64];
   const uint64_t row = threadIdx.x;
   double row_loss = 0.0;
   if (row < a.batch) {
+    const uint32_t classes = static_cast<uint32_t>(a.classes);
     const float *x = a.logits + row * a.classes;
+    float v[C];
+#pragma unroll
+    for (int i = 0; i < C; ++i) v[i] = x[static_cast<uint32_t>(i) < classes ? i : classes - 1];
+    const float target_value = a.targets[row];
     float maximum = -INFINITY;
-    for (uint64_t i = 0; i < a.classes; ++i) maximum = fmaxf(maximum, x[i]);
+#pragma unroll
+    for (int i = 0; i < C; ++i)
+      if (static_cast<uint32_t>(i) < classes) maximum = fmaxf(maximum, v[i]);
     double s = 0.0;
-    for (uint64_t i = 0; i < a.classes; ++i) s += static_cast<double>(expf(x[i] - maximum));
+#pragma unroll
+    for (int i = 0; i < C; ++i) {
+      if (static_cast<uint32_t>(i) < classes) {
+        v[i] = expf(v[i] - maximum);  // v now holds e
+        s += static_cast<double>(v[i]);
+      }
+    }
     const float normalizer = static_cast<float>(s);
     uint64_t target = 0;
-    const bool valid = target_index(a.targets[row], a.classes, target);
+    const bool valid = target_index(target_value, a.classes, target);
     if (!valid && a.error_flag) *a.error_flag = 1u;
     if (a.grad) {
       const float scale = *a.outer / static_cast<float>(a.batch);
       float *g = a.grad + row * a.classes;
-      for (uint64_t i = 0; i < a.classes; ++i) {
-        const float p = expf(x[i] - maximum) / normalizer;
-        g[i] = valid ? scale * (p - (i == target ? 1.0f : 0.0f)) : NAN;
+#pragma unroll
+      for (int i = 0; i < C; ++i) {
+        if (static_cast<uint32_t>(i) < classes) {
+          const float p = v[i] / normalizer;
+          g[i] = valid ? scale * (p - (static_cast<uint64_t>(i) == target ? 1.0f : 0.0f)) : NAN;
+        }
       }
     }
     row_loss = static_cast<double>(valid ? logf(normalizer) + maximum - x[target] : NAN);
   }
   if (a.loss != nullptr) {
-    const double total = block_sum<kSmallRows>(row_loss, lds);
-    if (threadIdx.x == 0) *a.loss = static_cast<float>(total) / static_cast<float>(a.batch);
+    double w[1] = {row_loss};
+    oxh::wave_sums_rows(w);
+    const uint32_t waves = blockDim.x / 64, wave = threadIdx.x / 64;
+    if (threadIdx.x % 64 == 0) lds[wave] = w[0];
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      double total = 0.0;
+      for (uint32_t i = 0; i < waves; ++i) total += lds[i];
+      *a.loss = static_cast<float>(total) / static_cast<float>(a.batch);
+    }
   }
 }
 
@@ -480,7 +510,10 @@ oxh_status launch_ce(const char *name, oxh_stream stream, CeArgs a, void *worksp
   }
   hipStream_t s = oxh::as_stream(stream);
   if (a.batch <= static_cast<uint64_t>(kSmallRows) && a.classes <= kSmallClasses) {
-    oxh::launch(ce_small_kernel, dim3(1), dim3(kSmallRows), 0, s, a);
+    const dim3 block(static_cast<uint32_t>((a.batch + 63) / 64 * 64));
+    if (a.classes <= 16) oxh::launch(ce_small_kernel<16>, dim3(1), block, 0, s, a);
+    else if (a.classes <= 32) oxh::launch(ce_small_kernel<32>, dim3(1), block, 0, s, a);
+    else oxh::launch(ce_small_kernel<64>, dim3(1), block, 0, s, a);
     return oxh::launched(name);
   }
   const dim3 grid(static_cast<uint32_t>(a.batch));
