@@ -66,6 +66,7 @@ using oxh::write_forward_outputs;
 #ifndef OXH_BN_NT_STORE
 #define OXH_BN_NT_STORE 3  // non-temporal stores: 1 = apply's y, 2 = input backward's dx
 #endif
+constexpr int kStorePolicy = 2 | 16;  // buffer store cache policy of the map outputs: nt | sc1
 #ifndef OXH_BN_MAP_VEC
 #define OXH_BN_MAP_VEC 2  // float4 per thread per stream in a map block
 #endif
@@ -584,10 +585,19 @@ __global__ __launch_bounds__(kMapBlock) void bn_map_kernel(PlaneMap m, typename 
         r.y = P::element(a, cv, x1);
         r.z = P::element(a, cv, x2);
         r.w = P::element(a, cv, x3);
-        if constexpr ((OXH_BN_NT_STORE & P::kNtStoreBit) != 0)
-          oxh::store_nt(reinterpret_cast<float4 *>(out + e0) + q, r);
-        else
+        if constexpr ((OXH_BN_NT_STORE & P::kNtStoreBit) != 0) {
+          // non-temporal, system scope (buffer cache policy nt | sc1): the apply's y and the
+          // input backward's dx are not read again in the step; 0.1290 -> 0.1279 ms per
+          // headline step against nt alone (sc0 | sc1 without nt: 0.137 ms)
+          const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+              out + e0, 0, static_cast<int>(n4 * 16), 0x00020000);
+          typedef unsigned u32x4_t __attribute__((vector_size(16)));
+          const u32x4_t bits = {__float_as_uint(r.x), __float_as_uint(r.y), __float_as_uint(r.z),
+                                __float_as_uint(r.w)};
+          __builtin_amdgcn_raw_buffer_store_b128(bits, rs, q * 16, 0, kStorePolicy);
+        } else {
           reinterpret_cast<float4 *>(out + e0)[q] = r;
+        }
       }
     }
   } else {
