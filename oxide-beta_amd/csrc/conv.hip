@@ -1184,7 +1184,8 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 // as 128-bit LDS accesses and issues four MFMAs, the s-th with component s, so lane group q
 // supplies k + 4q + s: the 16 k of the group, each once.  k at or past the slab's count are
 // zeroed in both operands.  Each MFMA adds its four products to the accumulator with fused
-// roundings (a tolerance-bar sum).
+// roundings: for sums that need not follow the CPU path bit for bit (within 1e-5 * sum|terms|
+// of it), as the fused-multiply-add sums they replace.
 template <int Tile, int Threads, bool AKFast, bool BKFast>
 __device__ __forceinline__ void product_sum_mfma(const ProductArgs &g, uint32_t m0, uint32_t n0,
                                                  uint32_t kb, uint32_t ke, uint32_t slabs, int t,
