@@ -42,7 +42,10 @@ def _check(loss, grad, logits, targets, outer=1.0):
 
 @pytest.mark.parametrize("shape", [(2, 2), (4, 7), (3, 1000), (2, 1), (128, 10), (5, 4096),
                                    (3, 8192), (2, 32768), (2, 65536), (2, 70000), (1, 4),
-                                   (300, 260)])
+                                   (300, 260),
+                                   # one-block path: class buckets 32 and 64, 1024 rows, a
+                                   # partial second wave
+                                   (9, 17), (6, 64), (1024, 33), (65, 20)])
 @pytest.mark.parametrize("mode", ["fused", "separate"])
 def test_cross_entropy_matches_oracle(module, dev, shape, mode):
     r = np.random.default_rng(shape[0] * 100003 + shape[1])
