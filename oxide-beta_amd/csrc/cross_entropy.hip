@@ -33,7 +33,7 @@ namespace {
 #define OXH_CE_BLOCK 512
 #endif
 #ifndef OXH_CE_NT
-#define OXH_CE_NT 3  // 1: non-temporal logit loads, 2: non-temporal gradient stores, 3: both
+#define OXH_CE_NT 3  // ce_row_kernel: 1 non-temporal logit loads, 2 gradient stores, 3 both
 #endif
 #ifndef OXH_CE_MINW
 #define OXH_CE_MINW 4
