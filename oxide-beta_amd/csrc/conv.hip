@@ -2238,6 +2238,15 @@ oxh_status input_backward_impl(const char *name, oxh_stream stream,
   OXH_REQUIRE(gradient && weight && input_gradient, OXH_INVALID_SHAPE,
               std::string(name) + ": null pointer");
   const uint64_t in_n = input_elems(g);
+  // the addend may be input_gradient itself (each element is read before the same lane
+  // writes it), never a part of it
+  const uint64_t gx = in_n * 4;
+  OXH_REQUIRE(!oxh::any_overlap(input_gradient, gx, gradient, output_elems(g) * 4) &&
+                  !oxh::any_overlap(input_gradient, gx, weight, weight_elems(g) * 4),
+              OXH_INVALID_SHAPE, std::string(name) + ": input_gradient overlaps an operand");
+  OXH_REQUIRE(addend == nullptr || addend == input_gradient ||
+                  !oxh::any_overlap(input_gradient, gx, addend, gx),
+              OXH_INVALID_SHAPE, std::string(name) + ": addend partially overlaps input_gradient");
   hipStream_t s = oxh::as_stream(stream);
   if (pointwise(g)) {
     const ProductArgs x = input_product(g, gradient, weight, addend, input_gradient);
@@ -2518,6 +2527,14 @@ oxh_status oxh_conv2d_backward(oxh_stream stream, const oxh_conv2d_shape *shape,
                   !oxh::any_overlap(bias_gradient, gb, gradient, gy) &&
                   !oxh::any_overlap(bias_gradient, gb, workspace, need),
               OXH_INVALID_SHAPE, std::string(name) + ": a gradient overlaps an operand");
+  // the addend is read while the other gradients and the workspace are written; it may be
+  // input_gradient itself (read before the same lane writes it), never a part of it
+  const uint64_t ga = addend != nullptr ? gx : 0;
+  OXH_REQUIRE(!oxh::any_overlap(addend, ga, weight_gradient, gw) &&
+                  !oxh::any_overlap(addend, ga, bias_gradient, gb) &&
+                  !oxh::any_overlap(addend, ga, workspace, need) &&
+                  (addend == input_gradient || !oxh::any_overlap(addend, ga, input_gradient, gx)),
+              OXH_INVALID_SHAPE, std::string(name) + ": the addend overlaps an output");
   hipStream_t s = oxh::as_stream(stream);
   if (pointwise(g)) {
     const KSplit split = product_split(g);

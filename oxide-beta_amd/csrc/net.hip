@@ -584,7 +584,8 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
     }
   }
   // a training BN (without ReLU) whose only consumer is a residual add, as the add's first
-  // operand: its forward writes the add's output (BN + addend) and the add launches nothing
+  // operand: one launch at the add's place writes the add's output (BN + addend), and the BN
+  // launches nothing of its own
   std::vector<int64_t> bn_into_add(n, -1);
   std::vector<char> add_absorbed(n, 0);
   for (size_t i = 0; i < n; ++i) {
@@ -607,8 +608,8 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
     if (!active[i] || x.op != Op::Conv || consumers[i] != 1) continue;
     size_t j = i + 1;
     while (j < n && g.nodes[j].leaf()) ++j;
-    if (j == n || !train_bn(static_cast<int>(j)) || g.nodes[j].in[0] != static_cast<int>(i) ||
-        bn_into_add[j] >= 0)
+    if (j == n || !active[j] || !train_bn(static_cast<int>(j)) ||
+        g.nodes[j].in[0] != static_cast<int>(i) || bn_into_add[j] >= 0)
       continue;
     if (x.groups != g.nodes[x.in[0]].shape[1] || x.groups != x.shape[1]) continue;
     const oxh_conv2d_shape s = conv_shape(g, x);
@@ -909,9 +910,13 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
   // forward
   for (size_t i = 0; i < n; ++i) {
     const Node &x = g.nodes[i];
-    if (!active[i] || x.leaf() || is_view(g, x) || fused_bn[i] || add_absorbed[i] ||
-        dw_conv[i] || pre_fused[i])
+    if (!active[i] || x.leaf() || is_view(g, x) || fused_bn[i] || dw_conv[i] || pre_fused[i])
       continue;
+    // a BatchNorm absorbed by its residual add launches at the add's place, where the addend
+    // (possibly created after the BatchNorm) has been written; one whose add feeds a fused
+    // depthwise layer launches inside that layer
+    if (x.op == Op::Bn && bn_into_add[i] >= 0) continue;
+    if (add_absorbed[i] && pre_fused[x.in[0]]) continue;
     float *out = p.value[i];
     OpRec op;
     switch (x.op) {
@@ -919,6 +924,33 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
         ops.push_back(conv_forward_op(g, p.value, i));
         break;
       case Op::Add:
+        if (add_absorbed[i]) {  // BN + residual add in one launch
+          const int bi = x.in[0];
+          const Node &bn = g.nodes[bi];
+          const float *xi = p.value[bn.in[0]], *w = p.value[bn.in[1]], *b = p.value[bn.in[2]];
+          const float *skip = p.value[x.in[1]];
+          float *sm = p.saved_mean[bi], *si = p.saved_inv[bi];
+          float *rm = bn.running_mean, *rv = bn.running_variance;
+          const uint64_t N = bn.shape[0], C = bn.shape[1], HW = bn.shape[2] * bn.shape[3];
+          const float mom = bn.momentum, eps = bn.epsilon;
+          op.kind = "batch_norm2d_add_forward";
+          op.name = name("bn", bi) + "+" + name("add", i);
+          op.tensors = {ref("x", const_cast<float *>(xi), g.nodes[bn.in[0]], 0),
+                        ref("weight", const_cast<float *>(w), g.nodes[bn.in[1]], 0),
+                        ref("bias", const_cast<float *>(b), g.nodes[bn.in[2]], 0),
+                        ref("addend", const_cast<float *>(skip), g.nodes[x.in[1]], 0),
+                        ref("y", out, x, 1), ref_flat("saved_mean", sm, C, 1),
+                        ref_flat("saved_inverse_std", si, C, 1),
+                        ref_flat("running_mean", rm, C, 2), ref_flat("running_variance", rv, C, 2)};
+          op.attrs = {{"momentum", mom}, {"epsilon", eps}};
+          op.launch = [=](hipStream_t st) {
+            return oxh_batch_norm_add_forward_train(st, N, C, HW, mom, eps, xi, w, b, rm, rv, sm,
+                                                    si, skip, out, ws, wsb);
+          };
+          ops.push_back(std::move(op));
+          break;
+        }
+        [[fallthrough]];
       case Op::Mul:
         ops.push_back(elementwise_forward_op(g, p.value, i));
         break;
@@ -941,27 +973,6 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
         float *rm = bn.running_mean, *rv = bn.running_variance;
         const uint64_t N = bn.shape[0], C = bn.shape[1], HW = bn.shape[2] * bn.shape[3];
         const float mom = bn.momentum, eps = bn.epsilon;
-        if (!fused && bn_into_add[i] >= 0) {  // BN + residual add in one launch
-          const Node &ad = g.nodes[bn_into_add[i]];
-          const float *skip = p.value[ad.in[1]];
-          float *sum = p.value[bn_into_add[i]];
-          op.kind = "batch_norm2d_add_forward";
-          op.name = name("bn", bi) + "+" + name("add", bn_into_add[i]);
-          op.tensors = {ref("x", const_cast<float *>(xi), g.nodes[bn.in[0]], 0),
-                        ref("weight", const_cast<float *>(w), g.nodes[bn.in[1]], 0),
-                        ref("bias", const_cast<float *>(b), g.nodes[bn.in[2]], 0),
-                        ref("addend", const_cast<float *>(skip), g.nodes[ad.in[1]], 0),
-                        ref("y", sum, ad, 1), ref_flat("saved_mean", sm, C, 1),
-                        ref_flat("saved_inverse_std", si, C, 1),
-                        ref_flat("running_mean", rm, C, 2), ref_flat("running_variance", rv, C, 2)};
-          op.attrs = {{"momentum", mom}, {"epsilon", eps}};
-          op.launch = [=](hipStream_t st) {
-            return oxh_batch_norm_add_forward_train(st, N, C, HW, mom, eps, xi, w, b, rm, rv, sm,
-                                                    si, skip, sum, ws, wsb);
-          };
-          ops.push_back(std::move(op));
-          break;
-        }
         if (dw_conv_of[bi] >= 0) {  // depthwise conv + BN (+ ReLU) in one launch
           const int ci = static_cast<int>(dw_conv_of[bi]);
           const Node &cv = g.nodes[ci];

@@ -295,3 +295,35 @@ def test_conv_input_gradient_order_query():
     assert ox.conv2d_input_backward_serial(sh(128, 32, 7, 7, 96, 3, 2, 1, 1))         # K x K
     with pytest.raises(ox.OxideError):
         ox.conv2d_input_backward_serial(sh(1, 1, 1, 1, 1, 3, 1, 0, 1))
+
+
+def test_conv_backward_rejects_an_overlapping_addend():
+    """oxh_conv2d_backward forms the input and weight gradients in one launch: the addend it
+    reads may be input_gradient itself, never a part of it, nor any other buffer the launch
+    writes.  oxh_conv2d_input_backward_accumulate takes the same rule.  Host checks only (the
+    pointers are never dereferenced)."""
+    lib = ox.lib()
+    shape = ox.conv2d_shape(2, 8, 4, 4, 16, 1, 1, 0, 1)
+    ws = ox.conv2d_workspace_size(shape)
+    nx, ny, nw = 2 * 8 * 16 * 4, 2 * 16 * 16 * 4, 16 * 8 * 4
+    base = 1 << 24
+    g, x, w = base, base + (1 << 16), base + (2 << 16)
+    dx, dw, db, wsp = base + (3 << 16), base + (4 << 16), base + (5 << 16), base + (6 << 16)
+    assert nx < (1 << 16) and ny < (1 << 16) and nw < (1 << 16) and ws < (1 << 16)
+
+    def backward(addend, bias=db):
+        return lib.oxh_conv2d_backward(None, ctypes.byref(shape), g, x, w, addend, dx, dw, bias,
+                                       wsp if ws else None, ws)
+
+    for bad in (dx + 4, dw, dw - nx + 4, db - 4, wsp):
+        if bad == wsp and ws == 0:
+            continue
+        assert backward(bad) == ox.INVALID_SHAPE, hex(bad)
+        assert b"overlap" in lib.oxh_last_error()
+    # a partial overlap with input_gradient is refused by the accumulate entry point too
+    assert lib.oxh_conv2d_input_backward_accumulate(None, ctypes.byref(shape), g, w, dx + 4,
+                                                    dx) == ox.INVALID_SHAPE
+    assert b"partially overlaps" in lib.oxh_last_error()
+    assert lib.oxh_conv2d_input_backward_accumulate(None, ctypes.byref(shape), g, w, x,
+                                                    g) == ox.INVALID_SHAPE
+    assert b"overlaps an operand" in lib.oxh_last_error()

@@ -146,5 +146,7 @@ def test_cross_entropy_pipelined_rows(module, dev, rows, mode):
     assert np.isnan(grad[[rows // 2, rows - 1]]).all()
     good = np.ones(rows, bool)
     good[[rows // 2, rows - 1]] = False
-    ref = oracle.ce_backward(logits[good], targets[good], 1.25) * np.float32(good.sum() / rows)
-    assert_close(grad[good], ref, rtol=2e-5, atol=1e-6 * 1.25 / rows, what="valid rows")
+    # a gradient row depends only on its own logits and target and on B: the oracle over the
+    # same B (the invalid rows given valid targets) pins the valid rows to the usual bar
+    ref = oracle.ce_backward(logits, targets, 1.25)[good]
+    assert_close(grad[good], ref, rtol=1e-5, atol=1e-6 * 1.25 / rows, what="valid rows")

@@ -252,6 +252,75 @@ def test_shared_parameters_accumulate_every_use():
         assert (err <= 1e-5 * bound + 1e-7).all(), (what, err, bound)
 
 
+
+@pytest.mark.parametrize("shortcut", ["relu", "projection"])
+def test_batch_norm_add_with_shortcut_built_after_it(shortcut):
+    """A training BatchNorm whose only consumer is a residual add, as the add's first operand,
+    runs with the add as one launch that writes BN(x) + addend.  Here the addend is created
+    after the BatchNorm: relu(x), or a 1x1 convolution + BatchNorm projection of x.  The fused
+    launch must run where the addend has been written.  Two runs on different inputs; every
+    launch against the oracle, and the loss, the sum and the gradients against torch float64
+    autograd each time (the arena starts zero-filled, so an addend read too early shows as
+    zeros in the first run and as the previous run's values in the second)."""
+    r = np.random.default_rng(53)
+    n, c, h, w = 4, 6, 5, 5
+    wv = (r.standard_normal((c, c, 3, 3)) * 0.3).astype(np.float32)
+    pv = (r.standard_normal((c, c, 1, 1)) * 0.5).astype(np.float32)
+    gam, gam2 = r.uniform(0.5, 1.5, c).astype(np.float32), r.uniform(0.5, 1.5, c).astype(np.float32)
+    bet, bet2 = r.uniform(-0.2, 0.2, c).astype(np.float32), r.uniform(-0.2, 0.2, c).astype(np.float32)
+    zero = np.zeros(c, np.float32)
+
+    x = tn.input((n, c, h, w), requires_grad=True)
+    weight, proj = nn.Parameter(wv), nn.Parameter(pv)
+    gamma, beta, gamma2, beta2 = (nn.Parameter(v) for v in (gam, bet, gam2, bet2))
+    main = x.conv2d(weight.tensor(), tn.constant(zero), 1, 1, 1).batch_norm2d(
+        gamma.tensor(), beta.tensor(), tn.BatchNormState(c), True, 0.1, 1e-5)
+    if shortcut == "relu":
+        skip = x.relu()
+    else:
+        skip = x.conv2d(proj.tensor(), tn.constant(zero), 1, 0, 1).batch_norm2d(
+            gamma2.tensor(), beta2.tensor(), tn.BatchNormState(c), True, 0.1, 1e-5)
+    s = main.add(skip)
+    t = tn.input((n,))
+    loss = s.avg_pool2d((h, w), (h, w)).reshape((n, c)).cross_entropy(t)
+    prog = tn.training_program(loss)
+    assert [o.kind for o in prog.ops].count("batch_norm2d_add_forward") == 1
+
+    F = torch.nn.functional
+    d = lambda v: torch.tensor(v, dtype=torch.float64, requires_grad=True)  # noqa: E731
+    for run in range(2):
+        xv = r.standard_normal((n, c, h, w)).astype(np.float32)
+        targets = r.integers(0, c, n).astype(np.float32)
+        prog.feed(x, xv)
+        prog.feed(t, targets)
+        counts = _run_checked(prog)
+        assert counts["batch_norm2d_add_forward"] == 1, dict(counts)
+        tx, tw, tp, tg, tb, tg2, tb2 = (d(v) for v in (xv, wv, pv, gam, bet, gam2, bet2))
+        stats = lambda: (torch.zeros(c, dtype=torch.float64),  # noqa: E731
+                         torch.ones(c, dtype=torch.float64))
+        tmain = F.batch_norm(F.conv2d(tx, tw, None, 1, 1), *stats(), tg, tb, True, 0.1, 1e-5)
+        tskip = (tx.relu() if shortcut == "relu" else
+                 F.batch_norm(F.conv2d(tx, tp), *stats(), tg2, tb2, True, 0.1, 1e-5))
+        ts = tmain + tskip
+        tl = F.cross_entropy(F.avg_pool2d(ts, (h, w)).reshape(n, c),
+                             torch.tensor(targets, dtype=torch.long))
+        tl.backward()
+        got_loss = float(prog.value(loss).host()[0])
+        assert abs(got_loss - tl.item()) <= 1e-5 * abs(tl.item()), (run, got_loss, tl.item())
+        ref_s = ts.detach().numpy()
+        np.testing.assert_allclose(prog.value(s).host(), ref_s, rtol=1e-4,
+                                   atol=1e-5 * np.abs(ref_s).max(), err_msg=f"run {run}: sum")
+        grads = [(x, tx, "dx"), (weight.tensor(), tw, "dweight"), (gamma.tensor(), tg, "dgamma"),
+                 (beta.tensor(), tb, "dbeta")]
+        if shortcut == "projection":
+            grads += [(proj.tensor(), tp, "dproj"), (gamma2.tensor(), tg2, "dgamma2"),
+                      (beta2.tensor(), tb2, "dbeta2")]
+        for got, ref, what in grads:
+            ref = ref.grad.numpy()
+            np.testing.assert_allclose(prog.gradient(got).host(), ref, rtol=1e-4,
+                                       atol=1e-5 * np.abs(ref).max() + 1e-7,
+                                       err_msg=f"run {run}: {what}")
+
 def _mnist_batch(r, n):
     images = (r.integers(0, 256, (n, 1, 28, 28)) / 255.0).astype(np.float32)
     labels = r.integers(0, 10, n).astype(np.float32)

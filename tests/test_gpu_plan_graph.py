@@ -29,6 +29,68 @@ def test_trace_caches_and_reuses_a_graph():
     assert isinstance(module.plan_for(((2,), (2,))), jit.HipJitPlan)
 
 
+
+class _AffineRelu:
+    """relu(x * weight + bias) over equal shapes with weight and bias as parameters: the
+    reference's compile KAT model (jit.rs:706-719) with its matmul, which is outside this
+    path, replaced by the elementwise product."""
+
+    def __init__(self, weight, bias):
+        import nn
+
+        self.weight, self.bias = nn.Parameter(weight), nn.Parameter(bias)
+
+    def __call__(self, x):
+        return x.mul(self.weight.tensor()).add(self.bias.tensor()).relu()
+
+
+def test_compile_user_module_parameters_become_plan_constants():
+    """jit.rs:131-135, 738-761 (compiles_a_user_defined_module_and_reuses_fixed_workspace):
+    compile traces the module's forward on one example; its parameters become Constant buffers
+    of the plan, holding their values; two runs on other inputs reuse the one compiled plan and
+    its fixed buffers, giving [3, 2] then [0, 0]; one specialisation remains."""
+    weight, bias = np.array([[2.0, 3.0]], np.float32), np.array([[1.0, -1.0]], np.float32)
+    model = _AffineRelu(weight, bias)
+    compiled = jit.compile(model, np.zeros((1, 2), np.float32))
+    assert compiled.cached_specializations() == 0
+    lowered = jit.lower(compiled.graph, compiled.placeholders)
+    kinds = [type(b).__name__ for b in lowered.buffers]
+    assert kinds == ["Input", "Constant", "WorkspaceBuffer", "Constant", "WorkspaceBuffer",
+                     "WorkspaceBuffer"], kinds
+    assert [list(b.values) for b in lowered.buffers if isinstance(b, jit.Constant)] == \
+        [[2.0, 3.0], [1.0, -1.0]]
+    assert [(o.op, o.inputs, o.output) for o in lowered.operations] == \
+        [(ox.PLAN_MUL, (0, 1), 2), (ox.PLAN_ADD, (2, 3), 4), (ox.PLAN_RELU, (4,), 5)]
+    first = compiled.run([np.array([[1.0, 1.0]], np.float32)])
+    plan = compiled.plan_for(((1, 2),))
+    assert isinstance(plan, jit.HipJitPlan)
+    buffers = [plan.buffer(i) for i in range(len(plan.plan.buffers))]
+    second = compiled.run([np.array([[-1.0, -1.0]], np.float32)])
+    assert first.tolist() == [[3.0, 2.0]]
+    assert second.tolist() == [[0.0, 0.0]]
+    assert compiled.cached_specializations() == 1
+    assert compiled.plan_for(((1, 2),)) is plan
+    assert [plan.buffer(i) for i in range(len(plan.plan.buffers))] == buffers
+    # the constants were taken at compile time: a later change of the parameter is not seen
+    # by the compiled plan (its values were copied into the plan's own buffers)
+    model.weight.data.fill_(100.0)
+    assert compiled.run([np.array([[1.0, 1.0]], np.float32)]).tolist() == [[3.0, 2.0]]
+
+
+def test_compile_user_module_matches_oracle_on_ragged_shape():
+    """The compiled relu(x * w + b) on [257, 1031] (not a multiple of the float4 width) with
+    random parameters, run on two inputs: bit-exact against the oracle's add / mul / relu
+    (evaluation.rs:21-34) each time, one specialisation."""
+    r = np.random.default_rng(0x6F78696400000011)
+    shape = (257, 1031)
+    weight, bias = (r.uniform(-1, 1, shape).astype(np.float32) for _ in range(2))
+    compiled = jit.compile(_AffineRelu(weight, bias), np.zeros(shape, np.float32))
+    for _ in range(2):
+        x = r.uniform(-1, 1, shape).astype(np.float32)
+        ref = oracle.relu(oracle.add(oracle.mul(x.ravel(), weight.ravel()), bias.ravel()))
+        assert_bitexact(compiled.run([x]).ravel(), ref, "compiled module")
+    assert compiled.cached_specializations() == 1
+
 def test_run_validates_inputs_like_reference():
     """jit.rs:183-203: input count and shape must match the trace (Error::Trace)."""
     a = np.array([1, -1], np.float32)
