@@ -11,13 +11,13 @@ written by the input backward).  ``value`` = 8T / step time in GB/s, inputs resi
 
 MALL (256 MB last-level cache) is defeated for the headline: steps rotate over 4 independent
 input/output sets (1.6 GB), so each step's x and g were last touched three steps (1.2 GB of
-traffic) earlier.  The K timed steps are R = K / 4 back-to-back launches of a hipGraph of four
-steps (one rotation; a graph of one step when K is not a multiple of 4), with an event between
-consecutive launches: ``ms_per_step`` is the median launch / 4, p10 / p90 and the mean over
-all K steps are reported beside it.  Per-kernel durations for the roofline come from HIP events
-that each dispatch records at its own start and end (oxh_time_next_launch, i.e.
-hipExtLaunchKernelGGL) inside a second, eager timed region; the eager step time is reported
-beside the graph one.
+traffic) earlier.  The K timed steps are launched directly on one stream with an event between
+consecutive steps: ``ms_per_step`` is the median of the K per-step samples, p10 / p90 and the
+mean over all K steps are reported beside it.  The same K steps as K launches of one-step
+hipGraphs, and as K / 4 launches of a four-step hipGraph, are reported beside the headline
+(each hipGraphLaunch adds a fixed ~5 us on the device).  Per-kernel durations for the
+roofline come from HIP events that each dispatch records at its own start and end
+(oxh_time_next_launch, i.e. hipExtLaunchKernelGGL) inside a separate eager timed pass.
 
 The other configs (elementwise chain + JIT-plan replay, cross entropy, AdamW) are measured
 after the headline and reported under "extra" in the same line.  ``cpu_baseline`` times the
@@ -166,27 +166,56 @@ def bench_batch_norm(m, steps: int, warmup: int, sets: int = 4):
     e_stop.record(s)
     s.synchronize()
     eager_ms = e_start.elapsed_time(e_stop) / steps
-    # headline: the K timed steps as R back-to-back launches of one hipGraph of G steps (one
-    # rotation over the input sets, G = 4, or G = 1 when K is not a multiple of 4), an event
-    # between consecutive launches; ms_per_step is the median launch over G
-    group = sets if steps % sets == 0 else 1
-    launches = steps // group
-    graph = ox.HipGraphExec.capture(s, lambda: [step(k) for k in range(group)])
-    for _ in range(max(1, -(-warmup // group))):
-        graph.launch(s)
-    s.synchronize()
-    evs = _events(launches + 1)
+    # headline: the K timed steps launched directly on one stream, rotating over the input
+    # sets, an event between consecutive steps: K per-step samples; ms_per_step is their
+    # median (an event costs the stream ~2 us)
+    for i in range(warmup):
+        step(i)
+    evs = _events(steps + 1)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     evs[0].record(s)
-    for i in range(launches):
-        graph.launch(s)
+    for i in range(steps):
+        step(i)
         evs[i + 1].record(s)
     s.synchronize()
-    graph_wall = time.perf_counter() - t0
-    per_step = _stats([evs[i].elapsed_time(evs[i + 1]) / group for i in range(launches)])
-    ms_per_step = per_step["median"]
-    graph_mean_ms = evs[0].elapsed_time(evs[-1]) / steps
+    wall_headline = time.perf_counter() - t0
+    per_step = _stats([evs[i].elapsed_time(evs[i + 1]) for i in range(steps)])
+    mean_ms = evs[0].elapsed_time(evs[-1]) / steps
+    # beside it, the same K steps as K hipGraph launches, one step per graph (four one-step
+    # graphs, one per input set, launched round-robin), an event between launches: each
+    # hipGraphLaunch adds a fixed ~5 us on the device
+    graphs = [ox.HipGraphExec.capture(s, lambda k=k: step(k)) for k in range(sets)]
+    for i in range(warmup):
+        graphs[i % sets].launch(s)
+    s.synchronize()
+    evs = _events(steps + 1)
+    evs[0].record(s)
+    for i in range(steps):
+        graphs[i % sets].launch(s)
+        evs[i + 1].record(s)
+    s.synchronize()
+    graph_step = _stats([evs[i].elapsed_time(evs[i + 1]) for i in range(steps)])
+    graph_step["launches"] = steps
+    graph_step["steps_per_graph"] = 1
+    del graphs
+    # and one hipGraph of a whole rotation (four steps) per launch, K / 4 launches, which
+    # spreads one launch's cost over four steps
+    group = sets if steps % sets == 0 else 1
+    g4 = ox.HipGraphExec.capture(s, lambda: [step(k) for k in range(group)])
+    for _ in range(max(1, -(-warmup // group))):
+        g4.launch(s)
+    s.synchronize()
+    evs = _events(steps // group + 1)
+    evs[0].record(s)
+    for i in range(steps // group):
+        g4.launch(s)
+        evs[i + 1].record(s)
+    s.synchronize()
+    rotation = _stats([evs[i].elapsed_time(evs[i + 1]) / group for i in range(steps // group)])
+    rotation["launches"] = steps // group
+    rotation["steps_per_graph"] = group
+    del g4
     # hot-cache reference: the same step repeated on one input set (x, g fit in the MALL)
     hot_start, hot_stop = _events(2)
     hot_start.record(s)
@@ -195,14 +224,10 @@ def bench_batch_norm(m, steps: int, warmup: int, sets: int = 4):
     hot_stop.record(s)
     s.synchronize()
     hot_ms = hot_start.elapsed_time(hot_stop) / steps
-    host_inputs = None
-    del graph
-    return dict(ms_per_step=ms_per_step, per_step=per_step, graph_mean_ms=graph_mean_ms,
-                graph_launches=launches, graph_group=group,
-                graph_wall_ms_per_step=graph_wall * 1e3 / steps, eager_ms_per_step=eager_ms,
-                event_ms_per_step=event_ms_per_step, wall_ms_per_step=wall * 1e3 / steps,
-                kernels=kernels, hot_ms_per_step=hot_ms, host_inputs=host_inputs, sets=sets,
-                graph_steps=steps)
+    return dict(ms_per_step=per_step["median"], per_step=per_step, mean_ms=mean_ms,
+                graph_step=graph_step, rotation=rotation, eager_ms_per_step=eager_ms,
+                event_ms_per_step=event_ms_per_step, wall_ms_per_step=wall_headline * 1e3 / steps,
+                kernels=kernels, hot_ms_per_step=hot_ms, sets=sets, steps=steps)
 
 
 def bench_elementwise(m, reps: int = 20, plan_reps: int = 100):
@@ -245,6 +270,14 @@ def bench_elementwise(m, reps: int = 20, plan_reps: int = 100):
     # between consecutive replays; beside it the same kernel issued without the graph
     replay = _timed_reps(ext, plan.replay, plan_reps)
     direct = _timed_reps(ext, plan.launch, plan_reps)
+    # host time of one replay call (Python -> ctypes -> hipGraphLaunch), no wait in between:
+    # the queue stays ahead of the device when this is below the kernel time
+    host_us = []
+    for _ in range(plan_reps):
+        t0 = time.perf_counter()
+        plan.replay()
+        host_us.append((time.perf_counter() - t0) * 1e6)
+    ox.check(ox.lib().oxh_stream_synchronize(pstream))
     ox.check(ox.lib().oxh_stream_synchronize(pstream))
     t0 = time.perf_counter()
     for _ in range(3):
@@ -260,6 +293,7 @@ def bench_elementwise(m, reps: int = 20, plan_reps: int = 100):
         "plan_replay_us": replay["median"],
         "plan_replay": replay,
         "plan_replay_gbs": round(4 * n * 4 / replay["median"] / 1e3, 1),
+        "plan_replay_host_call_us": round(sorted(host_us)[len(host_us) // 2], 2),
         "plan_direct_launch_us": direct["median"],
         "plan_direct_launch": direct,
         "plan_run_with_copies_us": round(run_us, 1),
@@ -593,18 +627,19 @@ def main():
              "bn_eager_ms_per_step": round(bn["eager_ms_per_step"], 4),
              "bn_eager_gbs": round(8 * T_BN / (bn["eager_ms_per_step"] * 1e-3) / 1e9, 1),
              "bn_events_ms_per_step": round(bn["event_ms_per_step"], 4),
-             "bn_graph_steps_timed": bn["graph_steps"],
              "bn_step_ms": {"median": round(bn["per_step"]["median"], 4),
                             "p10": round(bn["per_step"]["p10"], 4),
                             "p90": round(bn["per_step"]["p90"], 4),
-                            "mean": round(bn["graph_mean_ms"], 4),
-                            "graph_launches": bn["graph_launches"],
-                            "steps_per_graph": bn["graph_group"],
-                            "what": "per step: one event-timed launch of a hipGraph of "
-                                    "steps_per_graph steps, divided by that count; mean = all "
-                                    "K steps between the first and last event"},
+                            "mean": round(bn["mean_ms"], 4), "samples": bn["per_step"]["reps"],
+                            "what": "per step: the four kernels launched directly, an event "
+                                    "between consecutive steps (one sample per timed step); "
+                                    "mean = all K steps between the first and last event"},
              "bn_gbs_p10_p90": [round(8 * T_BN / (bn["per_step"]["p90"] * 1e-3) / 1e9, 1),
                                 round(8 * T_BN / (bn["per_step"]["p10"] * 1e-3) / 1e9, 1)],
+             "bn_graph_step_ms": {k: round(v, 4) if isinstance(v, float) else v
+                                  for k, v in bn["graph_step"].items()},
+             "bn_rotation_graph_step_ms": {k: round(v, 4) if isinstance(v, float) else v
+                                           for k, v in bn["rotation"].items()},
              "copy_ceiling": copy_ceiling()}
     chosen = [] if args.no_extra else [e for e in args.extras.split(",") if e]
     for name in chosen:
@@ -630,8 +665,8 @@ def main():
         "dtype": "f32",
         "data": "synthetic (x, g ~ N(0,1) seeded; gamma ~ U(0.5,1.5), beta ~ U(-0.1,0.1))",
         "config": {"workload": "BatchNorm2d train fwd+bwd NCHW [64,128,56,56] fp32, momentum "
-                               "0.1, eps 1e-5, 4 rotating input sets (MALL-flushed), "
-                               "hipGraph replay",
+                               "0.1, eps 1e-5, 4 rotating input sets (MALL-flushed), direct "
+                               "launches, an event per step",
                    "algorithmic_bytes_per_step": 8 * T_BN},
         "roofline": {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s",
