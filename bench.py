@@ -17,7 +17,9 @@ mean over all K steps are reported beside it.  The same K steps as K launches of
 hipGraphs, and as K / 4 launches of a four-step hipGraph, are reported beside the headline
 (each hipGraphLaunch adds a fixed ~5 us on the device).  Per-kernel durations for the
 roofline come from HIP events that each dispatch records at its own start and end
-(oxh_time_next_launch, i.e. hipExtLaunchKernelGGL) inside a separate eager timed pass.
+(oxh_time_next_launch, i.e. hipExtLaunchKernelGGL) in a separate eager pass before the
+headline's.  The secondary workloads warm up for at least 30 ms of device time before their
+timed repetitions.
 
 The other configs (elementwise chain + JIT-plan replay, cross entropy, AdamW) are measured
 after the headline and reported under "extra" in the same line.  ``cpu_baseline`` times the
@@ -58,12 +60,23 @@ def _stats(samples):
             "reps": len(q)}
 
 
-def _timed_reps(stream, fn, reps: int, warmup: int = 3):
+def _timed_reps(stream, fn, reps: int, warmup: int = 3, warm_ms: float = 30.0):
     """Runs ``fn`` ``reps`` times back to back on ``stream`` with an event between
     consecutive repetitions (rep i = event i -> event i + 1, no gaps left out); returns the
-    per-repetition statistics in microseconds."""
-    for _ in range(warmup):
-        fn()
+    per-repetition statistics in microseconds.  Warm-up: at least ``warmup`` untimed
+    repetitions and at least ``warm_ms`` of device time (the GPU reaches its steady clocks
+    some milliseconds into a streaming workload: the first ~5 ms of 0.4 ms cross-entropy
+    launches run up to 10 % slower)."""
+    done, spent = 0, 0.0
+    while done < warmup or (spent < warm_ms and done < 1000):
+        e0, e1 = _events(2)
+        e0.record(stream)
+        for _ in range(max(1, warmup)):
+            fn()
+        e1.record(stream)
+        e1.synchronize()
+        spent += e0.elapsed_time(e1)
+        done += max(1, warmup)
     evs = _events(reps + 1)
     evs[0].record(stream)
     for i in range(reps):
@@ -135,14 +148,11 @@ def bench_batch_norm(m, steps: int, warmup: int, sets: int = 4):
     # per-kernel durations: each dispatch records its own start / stop events
     timers = [[ox.KernelTimer() for _ in names] for _ in range(steps)]
     start, stop = _events(2)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
     start.record(s)
     for i in range(steps):
         step(warmup + i, timers[i])
     stop.record(s)
     s.synchronize()
-    wall = time.perf_counter() - t0
     total_ms = start.elapsed_time(stop)
     per_kernel = {nm: [] for nm in names}
     for tm in timers:
