@@ -171,6 +171,15 @@ oxh_status launch_run(const oxh_plan &p, const Run &r) {
       c.store[n_store++] = p.buffers[o.output].device;
     }
   }
+  // relu((a + b) * c) with only its result stored -- config 1's plan, the reference's own
+  // chain -- runs on the dedicated fused kernel: the same three fp32 operations per element in
+  // the same order, two float4 per lane per stream (a generic chain keeps one: its step
+  // registers would otherwise cost occupancy)
+  if (c.count == 3 && c.steps[0].op == OXH_PLAN_ADD && c.steps[0].other == 0 &&
+      c.steps[1].op == OXH_PLAN_MUL && c.steps[1].other == 1 && c.steps[2].op == OXH_PLAN_RELU &&
+      c.steps[0].store < 0 && c.steps[1].store < 0 && c.steps[2].store == 0 && n_store == 1)
+    return oxh_elementwise_chain_forward(p.stream, c.first, c.other[0], c.other[1], c.store[0],
+                                         p.buffers[ops[r.begin].output].elements);
   return oxh::launch_chain(p.stream, c, p.buffers[ops[r.begin].output].elements);
 }
 
