@@ -102,7 +102,7 @@ oxh_status oxh_checkpoint_load(const char *path, oxh_checkpoint **out) {
       return truncated();
     }
     std::vector<float> values(len);
-    std::memcpy(values.data(), bytes.data() + r.pos, len * 4);
+    if (len != 0) std::memcpy(values.data(), bytes.data() + r.pos, len * 4);
     r.pos += len * 4;
     ck->shapes.push_back(std::move(shape));
     ck->values.push_back(std::move(values));
