@@ -77,6 +77,35 @@ __device__ __forceinline__ uint32_t fast_div(uint32_t n, const FastDiv &f) {
   return (__umulhi(n, f.mul) + n) >> f.shift;
 }
 
+#ifndef OXH_XCD_REMAP
+#define OXH_XCD_REMAP 1  // 1: tiled kernels give each XCD a contiguous run of their tiles
+#endif
+
+// Workgroups reach the 8 XCDs round-robin in dispatch order (linear id, x fastest), and each
+// XCD has its own L2.  For the ids [base, base + count) of a grid, xcd_contiguous maps the
+// local id l (the workgroup base + l, on XCD (base + l) % 8) to the tile it computes so that
+// each XCD takes one contiguous run of count / 8 tiles (ids at or past the largest multiple of
+// 8 keep theirs).  Neighbouring tiles share operand rows (one image's input, one strip of
+// weights), which one L2 then fetches once instead of every XCD fetching all of them.  A
+// bijection: XCD s takes l = ((s - base) mod 8) + 8 k, k < count / 8, as tile s * count / 8 + k.
+__device__ __forceinline__ uint32_t xcd_contiguous(uint32_t l, uint32_t count,
+                                                   uint32_t base = 0) {
+  if constexpr (OXH_XCD_REMAP == 0) return l;
+  const uint32_t per = count >> 3;
+  return l < (per << 3) ? ((base + l) & 7u) * per + (l >> 3) : l;
+}
+struct BlockTile {
+  uint32_t x, y, z;
+};
+// blockIdx remapped over the whole grid as above.
+__device__ __forceinline__ BlockTile xcd_block() {
+  const uint32_t gx = gridDim.x, gy = gridDim.y;
+  const uint32_t id = (blockIdx.z * gy + blockIdx.y) * gx + blockIdx.x;
+  const uint32_t r = xcd_contiguous(id, gx * gy * gridDim.z);
+  const uint32_t xy = r % (gx * gy);
+  return {xy % gx, xy / gx, r / (gx * gy)};
+}
+
 // Convolution tap terms: p where mask is all ones, else -0.0f (x + (-0.0f) == x for every x),
 // the term of a tap outside the input, so a sum over all taps equals the CPU path's sum that
 // skips them, bit for bit.  Bit operations rather than a select keep the tap's loads

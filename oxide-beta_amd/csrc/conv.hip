@@ -290,7 +290,8 @@ __global__ __launch_bounds__(256) void conv2d_forward_lds_kernel(
     float *__restrict__ y) {
   extern __shared__ float lds[];
   constexpr int T = K * K;
-  const uint32_t n = blockIdx.y, oc0 = blockIdx.x * oc_tile;
+  const oxh::BlockTile bt = oxh::xcd_block();
+  const uint32_t n = bt.y, oc0 = bt.x * oc_tile;
   const uint32_t ocn = min(oc_tile, g.out_c - oc0), ocp = round4(ocn);
   const uint32_t plane = g.h * g.w, xs = g.in_c * plane;
   float *xl = lds, *wl = lds + round4(xs);  // wl[(ic * T + tap) * ocp + ocl]
@@ -360,7 +361,8 @@ __global__ __launch_bounds__(256) void conv2d_forward_split_kernel(
     const float *__restrict__ bias, float *__restrict__ y) {
   extern __shared__ float lds[];
   constexpr int T = K * K;
-  const uint32_t n = blockIdx.y, oc0 = blockIdx.x * oc_tile;
+  const oxh::BlockTile bt = oxh::xcd_block();
+  const uint32_t n = bt.y, oc0 = bt.x * oc_tile;
   const uint32_t ocn = min(oc_tile, g.out_c - oc0), ocp = round4(ocn);
   const uint32_t plane = g.h * g.w, xs = g.in_c * plane;
   const uint32_t rows = g.in_c * T;  // r = ic * T + tap
@@ -439,7 +441,8 @@ __global__ __launch_bounds__(256) void conv2d_input_backward_lds_kernel(
     const float *__restrict__ wt, const float *addend, float *dx) {
   extern __shared__ float lds[];
   constexpr int T = K * K, M = (K + S - 1) / S;
-  const uint32_t n = blockIdx.y, ic0 = blockIdx.x * ic_tile;
+  const oxh::BlockTile bt = oxh::xcd_block();
+  const uint32_t n = bt.y, ic0 = bt.x * ic_tile;
   const uint32_t icn = min(ic_tile, g.in_c - ic0), icp = round4(icn);
   const uint32_t oplane = g.oh * g.ow, gs = g.out_c * oplane;
   float *gl = lds, *wl = lds + round4(gs);
@@ -528,7 +531,8 @@ __global__ __launch_bounds__(256) void conv2d_input_backward_s2_kernel(
     const float *addend, float *dx) {
   extern __shared__ float lds[];
   constexpr int T = K * K, M = (K + 1) / 2;
-  const uint32_t n = blockIdx.y, ic0 = blockIdx.x * pg.ic_tile;
+  const oxh::BlockTile bt = oxh::xcd_block();
+  const uint32_t n = bt.y, ic0 = bt.x * pg.ic_tile;
   const uint32_t ocp = pg.ocp, ocs = pg.ocs;
   const uint32_t icn = min(pg.ic_tile, g.in_c - ic0);
   const uint32_t gcount = pg.ohp * pg.owp * ocs, wcount = pg.ic_tile * T * ocp;
@@ -628,7 +632,8 @@ __global__ __launch_bounds__(kDwMaxThreads) void conv2d_weight_lds_kernel(
     const float *__restrict__ grad, const float *__restrict__ x, float *__restrict__ partial) {
   extern __shared__ float lds[];
   constexpr int T = K * K;
-  const uint32_t oc0 = blockIdx.x * kDwOcTile, chunk = blockIdx.y;
+  const oxh::BlockTile bt = oxh::xcd_block();
+  const uint32_t oc0 = bt.x * kDwOcTile, chunk = bt.y;
   const uint32_t ocn = min(static_cast<uint32_t>(kDwOcTile), g.out_c - oc0);
   const uint32_t plane = g.h * g.w, oplane = g.oh * g.ow, xs = g.in_c * plane;
   const uint32_t pairs = g.in_c * T;
@@ -1382,8 +1387,8 @@ __global__ __launch_bounds__(Threads) void pointwise_product_kernel(ProductArgs 
   constexpr int kRow = ProductRow<Tile, Threads>::value;
   __shared__ __align__(16) float as[Tile][kRow];
   __shared__ __align__(16) float bs[Tile][kRow];
-  product_tile<Tile, Threads, AKFast, BKFast, Fma>(g, blockIdx.x, blockIdx.y, blockIdx.z, as,
-                                                   bs);
+  const oxh::BlockTile bt = oxh::xcd_block();
+  product_tile<Tile, Threads, AKFast, BKFast, Fma>(g, bt.x, bt.y, bt.z, as, bs);
 }
 
 // Products whose sums need not follow the serial order (the weight gradient, already reduced in
@@ -1457,7 +1462,8 @@ __device__ __forceinline__ void split_tile(const ProductArgs &g, uint32_t bx, ui
 template <bool AKFast, bool BKFast>
 __global__ __launch_bounds__(kSplitThreads) void pointwise_split_kernel(ProductArgs g) {
   __shared__ __align__(16) SplitLds lds;
-  split_tile<AKFast, BKFast>(g, blockIdx.x, blockIdx.y, blockIdx.z, lds);
+  const oxh::BlockTile bt = oxh::xcd_block();
+  split_tile<AKFast, BKFast>(g, bt.x, bt.y, bt.z, lds);
 }
 
 // The split tiles at 16 x 16 outputs, 2 x 2 per lane (product_sum<16, 64>): the same parts of
@@ -1548,7 +1554,8 @@ __device__ __forceinline__ void split_tile16(const ProductArgs &g, uint32_t bx, 
 template <bool AKFast, bool BKFast>
 __global__ __launch_bounds__(kSplitThreads) void pointwise_split16_kernel(ProductArgs g) {
   __shared__ __align__(16) SplitLds16 lds;
-  split_tile16<AKFast, BKFast>(g, blockIdx.x, blockIdx.y, blockIdx.z, lds);
+  const oxh::BlockTile bt = oxh::xcd_block();
+  split_tile16<AKFast, BKFast>(g, bt.x, bt.y, bt.z, lds);
 }
 
 // A convolution's input gradient (16 x 16 serial tiles, one output per thread, or with Split1
@@ -1588,6 +1595,11 @@ __global__ __launch_bounds__(kSplitThreads) void pointwise_dual_kernel(ProductAr
                                                                        DualGrid d) {
   __shared__ __align__(16) DualLds<S1> lds;
   uint32_t b = blockIdx.x;
+  // each part's tiles remapped on their own, so every XCD keeps a share of both parts
+  if (b < d.blocks1)
+    b = oxh::xcd_contiguous(b, d.blocks1);
+  else if (b < d.blocks1 + d.blocks2)
+    b = d.blocks1 + oxh::xcd_contiguous(b - d.blocks1, d.blocks2, d.blocks1);
   if (b < d.blocks1) {
     if constexpr (S1 == 2)
       split_tile16<A1, B1>(g1, b % d.nx1, b / d.nx1, 0, lds.split16);
