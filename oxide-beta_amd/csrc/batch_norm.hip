@@ -1181,6 +1181,14 @@ oxh_status backward_train_impl(const char *name, oxh_stream stream, uint64_t bat
   return oxh::launched(name);
 }
 
+}  // namespace
+
+bool oxh::batch_norm_single_launch(uint64_t batch, uint64_t channels, uint64_t spatial) {
+  return use_channel(batch, channels, spatial);
+}
+
+namespace {
+
 // ---------------------------------------------------------------- allocation-free forward
 
 // The reduce partials of oxh_batch_norm_forward_train_no_alloc live in this array: one copy per

@@ -19,6 +19,10 @@ namespace oxh {
 // forward's partials); `device` must be current.  Called by oxh_init.
 oxh_status bn_scratch_init(int device);
 
+// Whether a training BatchNorm of this shape runs one block per channel (its backward then
+// sums the input gradient per channel in passing: a preceding convolution's bias gradient).
+bool batch_norm_single_launch(uint64_t batch, uint64_t channels, uint64_t spatial);
+
 // Records `message` as the calling thread's last error and returns `status`.
 oxh_status fail(oxh_status status, const std::string &message);
 // Clears the last error; returns OXH_OK.

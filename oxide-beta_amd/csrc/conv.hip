@@ -622,24 +622,31 @@ __global__ __launch_bounds__(256) void conv2d_input_backward_s2_kernel(
 // (gl[pos * kDwOcTile + ocl], zero past the tile).  Thread t < pairs * groups owns one
 // (ic, tap) pair for every channel of the tile over one of `groups` position ranges (groups > 1
 // when there are few pairs); the ranges' sums are added in range order at the end.  Partials
-// over the chunk (the chunk sums then run in chunk order).
+// over the chunk (the chunk sums then run in chunk order).  With Bias, `groups` more threads
+// sum the output gradient itself over the same ranges (the bias gradient: a pair whose operand
+// is 1), the weight threads unchanged.  The chunk's weight sums go to out_w + chunk * stride
+// ([oc][ic][tap]), its bias sums to out_b + chunk * stride ([oc]).
 constexpr int kDwOcTile = 16;
 constexpr uint32_t kDwMaxThreads = 512;
 
-template <int K, int S>
+template <int K, int S, bool Bias>
 __global__ __launch_bounds__(kDwMaxThreads) void conv2d_weight_lds_kernel(
     ConvGeom g, uint32_t per_chunk, uint32_t groups, oxh::FastDiv oplane_div,
-    const float *__restrict__ grad, const float *__restrict__ x, float *__restrict__ partial) {
+    const float *__restrict__ grad, const float *__restrict__ x, float *__restrict__ out_w,
+    float *__restrict__ out_b, uint32_t stride) {
   extern __shared__ float lds[];
   constexpr int T = K * K;
   const oxh::BlockTile bt = oxh::xcd_block();
   const uint32_t oc0 = bt.x * kDwOcTile, chunk = bt.y;
   const uint32_t ocn = min(static_cast<uint32_t>(kDwOcTile), g.out_c - oc0);
   const uint32_t plane = g.h * g.w, oplane = g.oh * g.ow, xs = g.in_c * plane;
-  const uint32_t pairs = g.in_c * T;
+  const uint32_t pairs = g.in_c * T, wpairs = pairs * groups;
   float *gl = lds, *xl = lds + kDwOcTile * oplane;
-  const uint32_t item = threadIdx.x, grp = item / pairs, pr = item - grp * pairs;
-  const bool active = item < pairs * groups;
+  const uint32_t item = threadIdx.x;
+  const bool bias_item = Bias && item >= wpairs && item < wpairs + groups;
+  const uint32_t grp = bias_item ? item - wpairs : item / pairs;
+  const uint32_t pr = bias_item ? pairs : item - grp * pairs;
+  const bool active = item < wpairs || bias_item;
   const uint32_t ic = pr / T, tap = pr - ic * T;
   const int ky = static_cast<int>(tap / K) - static_cast<int>(g.pad);
   const int kx = static_cast<int>(tap % K) - static_cast<int>(g.pad);
@@ -675,7 +682,10 @@ __global__ __launch_bounds__(kDwMaxThreads) void conv2d_weight_lds_kernel(
       }
       const int iy = static_cast<int>(oy) * S + ky, ix = static_cast<int>(ox) * S + kx;
       const bool ok = static_cast<uint32_t>(iy) < g.h && static_cast<uint32_t>(ix) < g.w;
-      const float xv = tap_operand(xl[ok ? base + iy * static_cast<int>(g.w) + ix : 0], tap_mask(ok));
+      // a bias thread's operand is 1 (fma(g, 1, acc) == acc + g exactly)
+      const float xv = bias_item ? 1.0f
+                                 : tap_operand(xl[ok ? base + iy * static_cast<int>(g.w) + ix : 0],
+                                               tap_mask(ok));
 #pragma unroll
       for (int o = 0; o < kDwOcTile; ++o) acc[o] = __builtin_fmaf(gv[o], xv, acc[o]);
       if (++ox == g.ow) {
@@ -684,27 +694,39 @@ __global__ __launch_bounds__(kDwMaxThreads) void conv2d_weight_lds_kernel(
       }
     }
   }
-  const uint32_t weights = g.out_c * pairs;
-  float *out = partial + static_cast<uint64_t>(chunk) * weights;
+  float *ow = out_w + static_cast<uint64_t>(chunk) * stride;
+  float *ob = Bias ? out_b + static_cast<uint64_t>(chunk) * stride : nullptr;
   if (groups == 1) {
     if (!active) return;
 #pragma unroll
-    for (int o = 0; o < kDwOcTile; ++o)
-      if (static_cast<uint32_t>(o) < ocn) out[(oc0 + o) * pairs + pr] = acc[o];
+    for (int o = 0; o < kDwOcTile; ++o) {
+      if (static_cast<uint32_t>(o) >= ocn) continue;
+      if (bias_item)
+        ob[oc0 + o] = acc[o];
+      else
+        ow[(oc0 + o) * pairs + pr] = acc[o];
+    }
     return;
   }
   __syncthreads();  // the staged planes are read: the block's LDS holds the range sums
-  float *red = lds;  // red[(grp * pairs + pr) * kDwOcTile + o]
+  float *red = lds;  // red[(grp * pairs + pr) * kDwOcTile + o], the bias ranges after them
   if (active) {
 #pragma unroll
     for (int o = 0; o < kDwOcTile; ++o) red[item * kDwOcTile + o] = acc[o];
   }
   __syncthreads();
-  for (uint32_t e = threadIdx.x; e < pairs * ocn; e += blockDim.x) {
-    const uint32_t o = e / pairs, q = e - o * pairs;
+  const uint32_t total = (pairs + (Bias ? 1 : 0)) * ocn;
+  for (uint32_t e = threadIdx.x; e < total; e += blockDim.x) {
     float v = 0.0f;
-    for (uint32_t r = 0; r < groups; ++r) v += red[(r * pairs + q) * kDwOcTile + o];
-    out[(oc0 + o) * pairs + q] = v;
+    if (e < pairs * ocn) {
+      const uint32_t o = e / pairs, q = e - o * pairs;
+      for (uint32_t r = 0; r < groups; ++r) v += red[(r * pairs + q) * kDwOcTile + o];
+      ow[(oc0 + o) * pairs + q] = v;
+    } else {
+      const uint32_t o = e - pairs * ocn;
+      for (uint32_t r = 0; r < groups; ++r) v += red[(wpairs + r) * kDwOcTile + o];
+      ob[oc0 + o] = v;
+    }
   }
 }
 
@@ -872,10 +894,12 @@ BiasArgs bias_args(const ConvGeom &g, const float *gradient, float *bias_gradien
 // elements): lane l sums the l-th contiguous part of the chunks serially (loads issued in
 // groups of 8 ahead of the adds), and the lane sums are then added in lane order.  A chain of
 // chunks / lanes loads per thread in place of chunks.
+// Elements e >= split go to out2[e - split] (a second output sharing the chunks' layout).
 __global__ __launch_bounds__(256) void sum_chunks_kernel(uint32_t count, uint32_t chunks,
                                                          uint32_t lanes,
                                                          const float *__restrict__ partial,
-                                                         float *__restrict__ out) {
+                                                         float *__restrict__ out, uint32_t split,
+                                                         float *__restrict__ out2) {
   __shared__ float part[256];
   const uint32_t per_block = 256 / lanes;
   const uint32_t l = threadIdx.x / per_block, j = threadIdx.x - l * per_block;
@@ -894,14 +918,14 @@ __global__ __launch_bounds__(256) void sum_chunks_kernel(uint32_t count, uint32_
     for (; c < c1; ++c) acc += partial[static_cast<uint64_t>(c) * count + e];
   }
   if (lanes == 1) {
-    if (e < count) out[e] = acc;
+    if (e < count) (e < split ? out[e] : out2[e - split]) = acc;
     return;
   }
   part[threadIdx.x] = acc;
   __syncthreads();
   if (l != 0 || e >= count) return;
   for (uint32_t r = 1; r < lanes; ++r) acc += part[r * per_block + j];
-  out[e] = acc;
+  (e < split ? out[e] : out2[e - split]) = acc;
 }
 
 
@@ -1672,13 +1696,15 @@ uint32_t grid_for(uint64_t items) {
 
 // Lanes per element for sum_chunks_kernel: a power of two up to 16 leaving at most 8 chunks
 // per lane.
+// Elements at or past `split` (default: none) go to out2.
 void launch_sum_chunks(hipStream_t s, uint32_t count, uint32_t chunks, const void *partial,
-                       float *out) {
+                       float *out, uint32_t split = UINT32_MAX, float *out2 = nullptr) {
   uint32_t lanes = 1;
   while (lanes < 16 && chunks > 8 * lanes) lanes *= 2;
   const uint32_t per_block = 256 / lanes;
   oxh::launch(sum_chunks_kernel, dim3((count + per_block - 1) / per_block), dim3(256), 0, s,
-              count, chunks, lanes, static_cast<const float *>(partial), out);
+              count, chunks, lanes, static_cast<const float *>(partial), out,
+              split < count ? split : count, out2);
 }
 
 uint64_t input_elems(const ConvGeom &g) {
@@ -1876,7 +1902,9 @@ PhasePlan input_backward_s2_plan(const ConvGeom &g) {
 // Weight gradient: one thread per (ic, tap) pair and position range (pairs <= kDwMaxThreads;
 // ranges so that a block has about 256 threads), the image planes plus a full output-channel
 // tile (or the range sums) within the LDS budget; image chunks for about 512 blocks.
-LdsPlan weight_lds_plan(const ConvGeom &g) {
+// bias: the launch also sums the bias gradient (groups more threads, same ranges); tile == 0
+// when that does not fit (the weight plan alone does not depend on it).
+LdsPlan weight_lds_plan(const ConvGeom &g, bool bias = false) {
   LdsPlan p;
   if (!lds_eligible(g)) return p;
   const uint64_t pairs = static_cast<uint64_t>(g.in_c) * g.kh * g.kw;
@@ -1885,14 +1913,16 @@ LdsPlan weight_lds_plan(const ConvGeom &g) {
   uint64_t groups = 256 / pairs;
   if (groups < 1) groups = 1;
   if (groups > oplane) groups = oplane;
+  const uint64_t items = (pairs + (bias ? 1 : 0)) * groups;
+  if (items > kDwMaxThreads) return p;
   const uint64_t staged = static_cast<uint64_t>(g.in_c) * g.h * g.w + kDwOcTile * oplane;
-  const uint64_t reduce = groups > 1 ? pairs * groups * kDwOcTile : 0;
+  const uint64_t reduce = groups > 1 ? items * kDwOcTile : 0;
   const uint64_t floats = staged > reduce ? staged : reduce;
   if (floats > kLdsFloats) return p;
   p.tile = kDwOcTile;
   p.tiles = (g.out_c + kDwOcTile - 1) / kDwOcTile;
   p.groups = static_cast<uint32_t>(groups);
-  p.threads = static_cast<uint32_t>((pairs * groups + 63) / 64 * 64);
+  p.threads = static_cast<uint32_t>((items + 63) / 64 * 64);
   uint32_t chunks = 512 / p.tiles;
   if (chunks < 1) chunks = 1;
   if (chunks > g.batch) chunks = g.batch;
@@ -2083,8 +2113,9 @@ bool depthwise_single_pass(const ConvGeom &g) {
 
 uint64_t weight_partial_bytes(const ConvGeom &g) {
   if (depthwise_single_pass(g)) return 0;
+  // room for the bias sums of a parameter-only oxh_conv2d_backward after each chunk's weights
   const LdsPlan lp = weight_lds_plan(g);
-  if (lp.tile > 0) return lp.chunks > 1 ? lp.chunks * weight_elems(g) * 4 : 0;
+  if (lp.tile > 0) return lp.chunks > 1 ? lp.chunks * (weight_elems(g) + g.out_c) * 4 : 0;
   if (pointwise(g)) {
     const KSplit k = product_split(g);
     return k.chunks > 1 ? static_cast<uint64_t>(k.chunks) * g.out_c * g.in_c * 4 : 0;
@@ -2299,6 +2330,87 @@ oxh_status input_backward_impl(const char *name, oxh_stream stream,
   return oxh::launched(name);
 }
 
+// The weight gradient (oxh_conv2d_weight_backward), and with bias_gradient not null the bias
+// gradient in the same launches where the per-image LDS kernels take the shape (bias_done is
+// then set; otherwise the caller forms the bias).  partial: the workspace.
+oxh_status weight_backward_impl(const char *name, hipStream_t s, const ConvGeom &g,
+                                const float *gradient, const float *input, float *weight_gradient,
+                                float *bias_gradient, float *partial, bool &bias_done) {
+  bias_done = false;
+  if (pointwise(g)) {
+    const KSplit split = product_split(g);
+    oxh_status st = launch_weight_product(
+        name, s,
+        weight_product(g, split, gradient, input, split.chunks > 1 ? partial : weight_gradient),
+        split);
+    if (st != OXH_OK || split.chunks == 1) return st;
+    const uint32_t count = g.out_c * g.in_c;
+    launch_sum_chunks(s, count, split.chunks, partial, weight_gradient);
+    return oxh::launched(name);
+  }
+  if (depthwise_single_pass(g)) {
+    const oxh::FastDiv oplane_div = oxh::make_fastdiv(g.oh * g.ow);
+    const bool wide = g.out_c <= 128;  // few channels: more threads per channel
+    if (g.kh == 3 && wide)
+      oxh::launch(conv2d_depthwise_weight_kernel<3, 1024>, dim3(g.out_c), dim3(1024), 0, s, g,
+                  oplane_div, gradient, input, weight_gradient);
+    else if (g.kh == 3)
+      oxh::launch(conv2d_depthwise_weight_kernel<3, 256>, dim3(g.out_c), dim3(256), 0, s, g,
+                  oplane_div, gradient, input, weight_gradient);
+    else if (wide)
+      oxh::launch(conv2d_depthwise_weight_kernel<5, 1024>, dim3(g.out_c), dim3(1024), 0, s, g,
+                  oplane_div, gradient, input, weight_gradient);
+    else
+      oxh::launch(conv2d_depthwise_weight_kernel<5, 256>, dim3(g.out_c), dim3(256), 0, s, g,
+                  oplane_div, gradient, input, weight_gradient);
+    return oxh::launched(name);
+  }
+  // the bias sums ride along where their threads fit; else the caller forms the bias
+  bool bias = bias_gradient != nullptr && weight_lds_plan(g, true).tile > 0;
+  const LdsPlan lp = weight_lds_plan(g, bias);
+  if (lp.tile > 0) {
+    const uint32_t weights = static_cast<uint32_t>(weight_elems(g));
+    const bool chunked = lp.chunks > 1;
+    // chunk partials [chunk][weights (+ out_c bias sums)], or the gradients themselves
+    const uint32_t stride = weights + (bias ? g.out_c : 0);
+    float *ow = chunked ? partial : weight_gradient;
+    float *ob = !bias ? nullptr : chunked ? partial + weights : bias_gradient;
+    const dim3 lgrid(lp.tiles, lp.chunks), lblock(lp.threads);
+    const oxh::FastDiv od = oxh::make_fastdiv(g.oh * g.ow);
+#define OXH_WEIGHT_LDS(KK, SS)                                                                \
+  do {                                                                                        \
+    if (bias)                                                                                 \
+      oxh::launch(conv2d_weight_lds_kernel<KK, SS, true>, lgrid, lblock, lp.lds_bytes, s, g,  \
+                  lp.per_chunk, lp.groups, od, gradient, input, ow, ob, stride);              \
+    else                                                                                      \
+      oxh::launch(conv2d_weight_lds_kernel<KK, SS, false>, lgrid, lblock, lp.lds_bytes, s, g, \
+                  lp.per_chunk, lp.groups, od, gradient, input, ow, ob, stride);              \
+  } while (0)
+    switch (tap_kernel(g)) {
+      case 31: OXH_WEIGHT_LDS(3, 1); break;
+      case 32: OXH_WEIGHT_LDS(3, 2); break;
+      case 51: OXH_WEIGHT_LDS(5, 1); break;
+      default: OXH_WEIGHT_LDS(5, 2);
+    }
+#undef OXH_WEIGHT_LDS
+    bias_done = bias;
+    oxh_status st = oxh::launched(name);
+    if (st != OXH_OK || !chunked) return st;
+    launch_sum_chunks(s, stride, lp.chunks, partial, weight_gradient, weights, bias_gradient);
+    return oxh::launched(name);
+  }
+  const uint32_t chunks = weight_chunks(g);
+  const uint32_t weights = static_cast<uint32_t>(weight_elems(g));
+  oxh::launch(conv2d_weight_partial_kernel,
+              dim3(grid_for(static_cast<uint64_t>(weights) * chunks)), dim3(256), 0, s, g,
+              weights, oxh::make_fastdiv(weights), chunks, gradient, input, partial);
+  const oxh_status st = oxh::launched(name);
+  if (st != OXH_OK) return st;
+  launch_sum_chunks(s, weights, chunks, partial, weight_gradient);
+  return oxh::launched(name);
+}
+
+
 }  // namespace
 
 extern "C" {
@@ -2435,62 +2547,9 @@ oxh_status oxh_conv2d_weight_backward(oxh_stream stream, const oxh_conv2d_shape 
   OXH_REQUIRE(need == 0 || (workspace != nullptr && workspace_bytes >= need), OXH_INVALID_SHAPE,
               std::string(name) +
                   ": workspace too small (oxh_conv2d_weight_backward_workspace_size)");
-  float *partial = static_cast<float *>(workspace);
-  hipStream_t s = oxh::as_stream(stream);
-  if (pointwise(g)) {
-    const KSplit split = product_split(g);
-    st = launch_weight_product(
-        name, s,
-        weight_product(g, split, gradient, input, split.chunks > 1 ? partial : weight_gradient),
-        split);
-    if (st != OXH_OK || split.chunks == 1) return st;
-    const uint32_t count = g.out_c * g.in_c;
-    launch_sum_chunks(s, count, split.chunks, partial, weight_gradient);
-    return oxh::launched(name);
-  }
-  if (depthwise_single_pass(g)) {
-    const oxh::FastDiv oplane_div = oxh::make_fastdiv(g.oh * g.ow);
-    const bool wide = g.out_c <= 128;  // few channels: more threads per channel
-    if (g.kh == 3 && wide)
-      oxh::launch(conv2d_depthwise_weight_kernel<3, 1024>, dim3(g.out_c), dim3(1024), 0, s, g,
-                  oplane_div, gradient, input, weight_gradient);
-    else if (g.kh == 3)
-      oxh::launch(conv2d_depthwise_weight_kernel<3, 256>, dim3(g.out_c), dim3(256), 0, s, g,
-                  oplane_div, gradient, input, weight_gradient);
-    else if (wide)
-      oxh::launch(conv2d_depthwise_weight_kernel<5, 1024>, dim3(g.out_c), dim3(1024), 0, s, g,
-                  oplane_div, gradient, input, weight_gradient);
-    else
-      oxh::launch(conv2d_depthwise_weight_kernel<5, 256>, dim3(g.out_c), dim3(256), 0, s, g,
-                  oplane_div, gradient, input, weight_gradient);
-    return oxh::launched(name);
-  }
-  const LdsPlan lp = weight_lds_plan(g);
-  if (lp.tile > 0) {
-    const uint32_t weights = static_cast<uint32_t>(weight_elems(g));
-    float *out = lp.chunks > 1 ? partial : weight_gradient;
-    const dim3 lgrid(lp.tiles, lp.chunks), lblock(lp.threads);
-    const oxh::FastDiv od = oxh::make_fastdiv(g.oh * g.ow);
-    switch (tap_kernel(g)) {
-      case 31: oxh::launch(conv2d_weight_lds_kernel<3, 1>, lgrid, lblock, lp.lds_bytes, s, g, lp.per_chunk, lp.groups, od, gradient, input, out); break;
-      case 32: oxh::launch(conv2d_weight_lds_kernel<3, 2>, lgrid, lblock, lp.lds_bytes, s, g, lp.per_chunk, lp.groups, od, gradient, input, out); break;
-      case 51: oxh::launch(conv2d_weight_lds_kernel<5, 1>, lgrid, lblock, lp.lds_bytes, s, g, lp.per_chunk, lp.groups, od, gradient, input, out); break;
-      default: oxh::launch(conv2d_weight_lds_kernel<5, 2>, lgrid, lblock, lp.lds_bytes, s, g, lp.per_chunk, lp.groups, od, gradient, input, out);
-    }
-    st = oxh::launched(name);
-    if (st != OXH_OK || lp.chunks == 1) return st;
-    launch_sum_chunks(s, weights, lp.chunks, partial, weight_gradient);
-    return oxh::launched(name);
-  }
-  const uint32_t chunks = weight_chunks(g);
-  const uint32_t weights = static_cast<uint32_t>(weight_elems(g));
-  oxh::launch(conv2d_weight_partial_kernel,
-              dim3(grid_for(static_cast<uint64_t>(weights) * chunks)), dim3(256), 0, s, g,
-              weights, oxh::make_fastdiv(weights), chunks, gradient, input, partial);
-  st = oxh::launched(name);
-  if (st != OXH_OK) return st;
-  launch_sum_chunks(s, weights, chunks, partial, weight_gradient);
-  return oxh::launched(name);
+  bool bias_done = false;
+  return weight_backward_impl(name, oxh::as_stream(stream), g, gradient, input, weight_gradient,
+                              nullptr, static_cast<float *>(workspace), bias_done);
 }
 
 oxh_status oxh_conv2d_bias_backward(oxh_stream stream, const oxh_conv2d_shape *shape,
@@ -2517,21 +2576,25 @@ oxh_status oxh_conv2d_backward(oxh_stream stream, const oxh_conv2d_shape *shape,
   ConvGeom g;
   oxh_status st = make_conv_geom(name, shape, g);
   if (st != OXH_OK) return st;
-  OXH_REQUIRE(gradient && input && weight && input_gradient && weight_gradient,
-              OXH_INVALID_SHAPE, std::string(name) + ": null pointer");
+  OXH_REQUIRE(gradient && input && weight && weight_gradient, OXH_INVALID_SHAPE,
+              std::string(name) + ": null pointer");
+  // a null input_gradient: the parameter gradients only (no addend then)
+  OXH_REQUIRE(input_gradient != nullptr || addend == nullptr, OXH_INVALID_SHAPE,
+              std::string(name) + ": an addend needs an input gradient");
   const uint64_t need = weight_partial_bytes(g);
   OXH_REQUIRE(need == 0 || (workspace != nullptr && workspace_bytes >= need), OXH_INVALID_SHAPE,
               std::string(name) +
                   ": workspace too small (oxh_conv2d_weight_backward_workspace_size)");
   // the two gradients are formed concurrently: neither may overlap what the other reads
   const uint64_t gx = input_elems(g) * 4, gy = output_elems(g) * 4, gw = weight_elems(g) * 4;
+  const uint64_t gi = input_gradient != nullptr ? gx : 0;
   const uint64_t gb = bias_gradient != nullptr ? g.out_c * 4ull : 0;
-  OXH_REQUIRE(!oxh::any_overlap(input_gradient, gx, gradient, gy) &&
-                  !oxh::any_overlap(input_gradient, gx, input, gx) &&
-                  !oxh::any_overlap(input_gradient, gx, weight, gw) &&
-                  !oxh::any_overlap(input_gradient, gx, weight_gradient, gw) &&
-                  !oxh::any_overlap(input_gradient, gx, bias_gradient, gb) &&
-                  !oxh::any_overlap(input_gradient, gx, workspace, need) &&
+  OXH_REQUIRE(!oxh::any_overlap(input_gradient, gi, gradient, gy) &&
+                  !oxh::any_overlap(input_gradient, gi, input, gx) &&
+                  !oxh::any_overlap(input_gradient, gi, weight, gw) &&
+                  !oxh::any_overlap(input_gradient, gi, weight_gradient, gw) &&
+                  !oxh::any_overlap(input_gradient, gi, bias_gradient, gb) &&
+                  !oxh::any_overlap(input_gradient, gi, workspace, need) &&
                   !oxh::any_overlap(weight_gradient, gw, weight, gw) &&
                   !oxh::any_overlap(weight_gradient, gw, gradient, gy) &&
                   !oxh::any_overlap(weight_gradient, gw, input, gx) &&
@@ -2548,7 +2611,7 @@ oxh_status oxh_conv2d_backward(oxh_stream stream, const oxh_conv2d_shape *shape,
                   (addend == input_gradient || !oxh::any_overlap(addend, ga, input_gradient, gx)),
               OXH_INVALID_SHAPE, std::string(name) + ": the addend overlaps an output");
   hipStream_t s = oxh::as_stream(stream);
-  if (pointwise(g)) {
+  if (pointwise(g) && input_gradient != nullptr) {
     const KSplit split = product_split(g);
     float *partial = static_cast<float *>(workspace);
     const ProductArgs w =
@@ -2562,13 +2625,19 @@ oxh_status oxh_conv2d_backward(oxh_stream stream, const oxh_conv2d_shape *shape,
       return oxh::launched(name);
     }
   }
-  st = oxh_conv2d_weight_backward(stream, shape, gradient, input, weight_gradient, workspace,
-                                  workspace_bytes);
+  // parameter gradients only: the bias sums ride in the weight gradient's launches where its
+  // kernel takes them (the full VJP keeps the separate bias launch: equal to
+  // oxh_conv2d_bias_backward bit for bit)
+  bool bias_done = false;
+  st = weight_backward_impl(name, s, g, gradient, input, weight_gradient,
+                            input_gradient == nullptr ? bias_gradient : nullptr,
+                            static_cast<float *>(workspace), bias_done);
   if (st != OXH_OK) return st;
-  if (bias_gradient != nullptr) {
+  if (bias_gradient != nullptr && !bias_done) {
     st = oxh_conv2d_bias_backward(stream, shape, gradient, bias_gradient, nullptr, 0);
     if (st != OXH_OK) return st;
   }
+  if (input_gradient == nullptr) return oxh::ok();
   return input_backward_impl(name, stream, shape, gradient, weight, addend, input_gradient);
 }
 

@@ -1367,10 +1367,12 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
         contribution(xin, dst, acc);
         // a convolution whose only consumer is this BN: its output gradient is this dx, whose
         // per-channel sum (the convolution's bias gradient) the BN backward forms in passing
+        // when it runs one block per channel (else in two launches of its own: the
+        // convolution's parameter backward forms it instead)
         float *conv_db = nullptr;
         const Node &src = g.nodes[xin];
         if (src.op == Op::Conv && consumers[xin] == 1 && acc == nullptr && want(xin) &&
-            want(src.in[2])) {
+            want(src.in[2]) && oxh::batch_norm_single_launch(N, C, HW)) {
           side(src.in[2], conv_db, "conv_bias_gradient");
           conv_bias_done[xin] = 1;
         }
@@ -1478,12 +1480,11 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
           if (weight_here) pr.tensors.push_back(ref("weight_gradient", dw, g.nodes[x.in[1]], 1));
           if (bias_here) pr.tensors.push_back(ref("bias_gradient", db, g.nodes[x.in[2]], 1));
           pr.attrs = conv_attrs(x);
-          pr.launch = [s, gr, xi, dw, db, ws, wsb](hipStream_t st) {
-            if (dw != nullptr) {
-              oxh_status e = oxh_conv2d_weight_backward(st, &s, gr, xi, dw, ws, wsb);
-              if (e != OXH_OK) return e;
-            }
-            if (db == nullptr) return oxh::ok();
+          pr.launch = [s, gr, xi, w, dw, db, ws, wsb](hipStream_t st) {
+            // both: one parameter-only VJP (the bias summed with the weights where it can be)
+            if (dw != nullptr && db != nullptr)
+              return oxh_conv2d_backward(st, &s, gr, xi, w, nullptr, nullptr, dw, db, ws, wsb);
+            if (dw != nullptr) return oxh_conv2d_weight_backward(st, &s, gr, xi, dw, ws, wsb);
             return oxh_conv2d_bias_backward(st, &s, gr, db, ws, wsb);
           };
           attach_sides(pr);

@@ -748,7 +748,8 @@ class LoadedModule:
 
     def conv2d_backward(self, shape, gradient, x, weight, input_gradient, weight_gradient,
                         bias_gradient=None, addend=None, stream=None):
-        """The whole conv VJP: weight, optional bias and input gradients in one call."""
+        """The whole conv VJP: weight, optional bias and input gradients in one call
+        (input_gradient None: the parameter gradients only)."""
         ws, wsb = self._conv_ws.ptr_bytes(conv2d_workspace_size(shape))
         check(lib().oxh_conv2d_backward(
             _stream(stream), ctypes.byref(shape), _ptr(gradient), _ptr(x), _ptr(weight),

@@ -153,6 +153,40 @@ def test_conv2d_backward_equals_separate_calls(module, dev, case, variant):
             module.conv2d_backward(shape, g, x, wt, dx, dw, dw.view(-1)[:cout])
 
 
+@pytest.mark.parametrize("case", [
+    (128, 1, 28, 28, 32, 3, 2, 1),     # config 5's stem: bias in the weight launch, chunked
+    (128, 32, 7, 7, 96, 3, 2, 1),      # one pair per thread (no position ranges)
+    (2, 18, 6, 6, 20, 3, 1, 1),        # ragged channel tile, one chunk per image
+    (1, 5, 8, 8, 6, 5, 2, 1),          # one chunk: the sums written in place
+    (3, 12, 6, 5, 8, 3, 1, 4),         # grouped: the separate bias kernel
+    (4, 96, 2, 2, 192, 1, 1, 1),       # pointwise: the separate kernels
+])
+def test_conv2d_parameter_backward(module, dev, case):
+    """oxh_conv2d_backward without an input gradient: the weight gradient bit-equal to
+    oxh_conv2d_weight_backward's, the bias gradient (summed in the weight gradient's launches
+    where the per-image kernels take the shape) within 1e-5 * sum|terms| of the oracle."""
+    n, cin, h, w, cout, k, s, groups = case
+    pad = k // 2
+    r = np.random.default_rng(hash(case) & 0xFFFFFF)
+    shape = ox.conv2d_shape(n, cin, h, w, cout, k, s, pad, groups)
+    oh, ow = ox.conv2d_output_size(shape)
+    x = r.standard_normal((n, cin, h, w)).astype(np.float32)
+    wt = (r.standard_normal((cout, cin // groups, k, k)) * 0.3).astype(np.float32)
+    g = r.standard_normal((n, cout, oh, ow)).astype(np.float32)
+    dx_, dw_, dg_ = to_dev(x, dev), to_dev(wt, dev), to_dev(g, dev)
+    ref_dw = torch.empty_like(dw_)
+    module.conv2d_weight_backward(shape, dg_, dx_, ref_dw)
+    dw, db = torch.full_like(dw_, float("nan")), torch.full((cout,), float("nan"), device=dev)
+    module.conv2d_backward(shape, dg_, dx_, dw_, None, dw, db)
+    torch.cuda.synchronize()
+    assert_bitexact(host(dw), host(ref_dw), "weight gradient")
+    assert_within(host(db), oracle.conv2d_bias_backward(g),
+                  1e-5 * np.abs(g).astype(np.float64).sum(axis=(0, 2, 3)) + 1e-7,
+                  "bias gradient")
+    with pytest.raises(ox.OxideError):  # an addend needs an input gradient
+        module.conv2d_backward(shape, dg_, dx_, dw_, None, dw, db, addend=dx_)
+
+
 @pytest.mark.parametrize("shape,kernel,stride", [((2, 3, 4, 4), (2, 2), (2, 2)),
                                                  ((128, 960, 1, 1), (1, 1), (1, 1)),
                                                  ((2, 5, 7, 7), (7, 7), (7, 7)),

@@ -37,8 +37,9 @@ def _mnist_batch(r, n):
 # the 11 UIB expand BatchNorms (+ ReLU) before the middle depthwise layers, and before the 4
 # start depthwise layers the previous block's last BatchNorm (2 with the residual add).
 # 46 BatchNorms, 32 of them followed by a ReLU (fused), each fed by a convolution whose bias
-# gradient its backward forms (the classifier's, fed by no BN, stays with its parameter
-# backward); the 15 depthwise convolutions run with their BatchNorm + ReLU in one launch per
+# gradient its backward forms, but for the stem's (its 14x14 BatchNorm is no one-block-per-
+# channel kernel: the stem's parameter backward sums the bias with its weight gradient) and the
+# classifier's (fed by no BN); the 15 depthwise convolutions run with their BatchNorm + ReLU in one launch per
 # direction; 10 residual adds, formed by the forward of the BN feeding them, whose first
 # operand's gradient is the add's own buffer and whose second operand's is added by that
 # operand's convolution input backward (no add launches in either direction)
@@ -56,8 +57,8 @@ EXPECTED_KINDS = {"conv2d_forward": 32, "conv2d_parameter_backward": 1,
                   "batch norm before depthwise": 30,
                   "conv input backward with addend": 10,
                   "cross_entropy": 1,
-                  "adamw": 1, "conv bias in parameter backward": 1,
-                  "conv bias in batch norm backward": 46}
+                  "adamw": 1, "conv bias in parameter backward": 2,
+                  "conv bias in batch norm backward": 45}
 
 
 def test_config5_step_every_op_matches_oracle():
