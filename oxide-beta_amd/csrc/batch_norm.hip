@@ -54,6 +54,8 @@ using oxh::Moments;
 using oxh::relu_masked;
 using oxh::StatsOut;
 using oxh::wave_sum;
+using oxh::load_running;
+using oxh::RunningPrev;
 using oxh::write_forward_outputs;
 
 // Launch-shape constants (overridable at build time for tuning sweeps).
@@ -685,6 +687,7 @@ __global__ __launch_bounds__(Threads) void bn_channel_forward_kernel(
   __shared__ double lds[2][Threads / 64];
   const uint32_t c = blockIdx.x;
   const float shift = x[static_cast<uint64_t>(c) * g.spatial];  // x[0, c, 0]
+  const RunningPrev prev = load_running(out, c);
   if constexpr (Keep) {
     float kept[kChannelKeep], added[kChannelKeep];
     uint32_t at[kChannelKeep];
@@ -699,7 +702,7 @@ __global__ __launch_bounds__(Threads) void bn_channel_forward_kernel(
       for (int u = 0; u < kChannelKeep; ++u) added[u] = addend[at[u]];
     }
     channel_forward_kept<Relu, Threads>(g.samples, c, shift, kept, at, weight[c], bias[c], out,
-                                        addend != nullptr, added, y, lds);
+                                        prev, addend != nullptr, added, y, lds);
   } else {
     const double k = static_cast<double>(shift);
     double sum = 0.0, sq = 0.0;
@@ -710,7 +713,7 @@ __global__ __launch_bounds__(Threads) void bn_channel_forward_kernel(
     }
     block_sum2_all<Threads / 64>(sum, sq, lds);
     const Moments r = forward_moments(make_double2(sum, sq), shift, g.samples, out.epsilon);
-    if (threadIdx.x == 0) write_forward_outputs(out, c, r);
+    if (threadIdx.x == 0) write_forward_outputs(out, c, r, prev);
     const float mu = r.mean, inv = r.inv, w = weight[c], b = bias[c];
     for (uint32_t j = threadIdx.x; j < g.samples; j += Threads) {
       const uint32_t idx = channel_index(g, c, j);

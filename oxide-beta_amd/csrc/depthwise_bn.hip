@@ -117,6 +117,10 @@ __global__ __launch_bounds__(T) void dw_bn_forward_kernel(
 #pragma unroll
   for (int t = 0; t < K * K; ++t) wv[t] = conv_weight[c * (K * K) + t];
   const float bias = conv_bias[c], w = bn_weight[c], b = bn_bias[c];
+  // both BatchNorms' running statistics before their update, loaded now for the same reason
+  const oxh::RunningPrev prev = oxh::load_running(stats, c);
+  oxh::RunningPrev pre_prev{0.0f, 0.0f};
+  if constexpr (Pre != kPreNone) pre_prev = oxh::load_running(pre.stats, c);
   if constexpr (Pre != kPreNone) {
     // the BatchNorm (relu) in front over input channel c (at most T * kChannelKeep
     // values), exactly as its channel kernel forms it; its output goes to LDS for the taps
@@ -133,8 +137,8 @@ __global__ __launch_bounds__(T) void dw_bn_forward_kernel(
     const float pshift = pre.input[input_index(g, c, 0)];
     oxh::channel_forward_kept<Pre == kPreBnRelu, T>(g.in_samples, c, pshift, kin, ain,
                                                              pre.weight[c], pre.bias[c],
-                                                             pre.stats, add, kadd, pre.output,
-                                                             lds, xs);
+                                                             pre.stats, pre_prev, add, kadd,
+                                                             pre.output, lds, xs);
   } else {
     stage_channel<T>(g, c, x, xs);
   }
@@ -179,7 +183,7 @@ __global__ __launch_bounds__(T) void dw_bn_forward_kernel(
   if (threadIdx.x == 0) shift = kept[0];  // conv_out[0, c, 0] (samples >= 2)
   __syncthreads();
   const float none[kChannelKeep] = {};
-  oxh::channel_forward_kept<Relu, T>(samples, c, shift, kept, at, w, b, stats, false,
+  oxh::channel_forward_kept<Relu, T>(samples, c, shift, kept, at, w, b, stats, prev, false,
                                               none, y, lds);
 }
 
