@@ -209,17 +209,19 @@ __global__ __launch_bounds__(T) void dw_bn_backward_kernel(
   // every load the block needs is issued here, before the first reduction: the convolution's
   // input channel (kept in registers when it fits, for the LDS copy), the addend, the
   // convolution weights, and the BatchNorm in front's input values and statistics
+  // These loads are unconditional (indices clamped into the channel, the addend read from x
+  // when there is none, unused then): a branch around them makes its merge wait for every
+  // load in flight (the merged registers are their destinations), a memory round trip before
+  // the next loads issue.
   const bool kept_in = g.in_samples <= static_cast<uint32_t>(T * kChannelKeep);
+  const float *add_src = addend != nullptr ? addend : x;
   float xin[kChannelKeep], addv[kChannelKeep], pin[kChannelKeep];
   uint32_t pat[kChannelKeep];
-  if (kept_in) {
 #pragma unroll
-    for (int u = 0; u < kChannelKeep; ++u) {
-      const uint32_t j = threadIdx.x + u * T;
-      pat[u] = j < g.in_samples ? input_index(g, c, j) : 0;
-      xin[u] = x[pat[u]];
-      addv[u] = addend != nullptr ? addend[pat[u]] : 0.0f;
-    }
+  for (int u = 0; u < kChannelKeep; ++u) {
+    pat[u] = input_index(g, c, min(threadIdx.x + u * T, g.in_samples - 1));
+    xin[u] = x[pat[u]];
+    addv[u] = add_src[pat[u]];
   }
   const float wt_reg = threadIdx.x < static_cast<uint32_t>(kTaps)
                            ? conv_weight[c * kTaps + threadIdx.x] : 0.0f;
