@@ -23,17 +23,21 @@
 // closed form, so the inner loops carry no bounds tests.
 //   * Pointwise convolutions (1x1, stride 1, no padding, one group) are matrix products
 //     Y[oc, (n,p)] = b[oc] + sum_ic W[oc, ic] X[ic, (n,p)], and likewise the input and weight
-//     gradients.  They run as an LDS-tiled product: 32 x 32 outputs per 256-thread block, 2 x 2
-//     per thread, k-slabs of 128 staged through LDS with the next slab's loads in flight during
-//     the current slab's arithmetic.  Each output is still one serial sum in ascending k from
-//     its initial value -- the CPU order -- so forward and input gradient stay bit-identical;
-//     the weight gradient splits k into fixed chunks.  No MFMA: a matrix-core instruction
-//     reorders the additions inside each tile.
-//   * Other convolutions (depthwise, and the strided 3 x 3 full convolutions) run one output
-//     (or input, or weight-chunk) element per thread.
+//     gradients.  They run as LDS-tiled products (32 x 32 or 8 x 8 outputs per block), k-slabs
+//     staged through LDS with the next slab's loads in flight during the current slab's
+//     arithmetic; each output one serial sum in ascending k from its initial value -- the CPU
+//     order, bit-identical.  Products whose grids would leave the chip idle take split tiles
+//     (8 x 8 or 16 x 16 outputs, k in four contiguous parts added in order, summed on the
+//     matrix cores), as do the weight gradients (k in fixed chunks): deterministic, within
+//     1e-5 * sum|terms| of the CPU's serial sum.
+//   * Ungrouped K x K convolutions with small planes stage one image's planes and a channel
+//     tile's weights in LDS per block; the rest (and depthwise convolutions not fused with
+//     their BatchNorm, depthwise_bn.hip) run one output (or input, or weight-chunk) element
+//     per thread.
 #include <hip/hip_runtime.h>
 
 #include <string>
+#include <type_traits>
 
 #include "common.h"
 
@@ -1583,10 +1587,11 @@ __global__ __launch_bounds__(kSplitThreads) void pointwise_split16_kernel(Produc
 }
 
 // A convolution's input gradient (16 x 16 serial tiles, one output per thread, or with Split1
-// the 16 x 16 split tiles its own launch takes for that shape: g1) and weight gradient (split
-// tiles: g2) in one launch.  Blocks [0, blocks1) take the input gradient's tiles, dispatched
-// first (their chains over the output channels are the longer ones), the rest the weight
-// gradient's, each computed exactly as its own kernel computes it.
+// the 16 x 16 split tiles its own launch takes for that shape: g1) and weight gradient (8 x 8
+// split tiles, or 16 x 16 with S2 == 2, as its own launch takes them: g2) in one launch.  Blocks
+// [0, blocks1) take the input gradient's tiles, dispatched first (their chains over the output
+// channels are the longer ones), the rest the weight gradient's, each computed exactly as its
+// own kernel computes it.
 struct DualGrid {
   uint32_t nx1, ny1, blocks1, nx2, ny2, blocks2;
   BiasArgs bias;  // bias.out null: no bias blocks
@@ -1596,28 +1601,21 @@ struct SerialTileLds16 {
   float as[16][ProductRow<16, 256>::value];
   float bs[16][ProductRow<16, 256>::value];
 };
-// The paired launch's LDS: the weight gradient's split tiles and the input gradient's tiles
-// of the kind S1 (input_splits) it takes, and only those, so each pairing keeps its occupancy.
-template <int S1>
+// The paired launch's LDS: the tiles of the kinds it takes (input gradient S1, weight gradient
+// S2) and only those, so each pairing keeps its occupancy.
+struct NoLds {};
+template <int S1, int S2>
 union DualLds {
   SplitLds split;
-  SerialTileLds16 tile;
-};
-template <>
-union DualLds<1> {
-  SplitLds split;
-};
-template <>
-union DualLds<2> {
-  SplitLds split;
-  SplitLds16 split16;
+  std::conditional_t<S1 == 0, SerialTileLds16, NoLds> tile;
+  std::conditional_t<S1 == 2 || S2 == 2, SplitLds16, NoLds> split16;
 };
 
-template <bool A1, bool B1, bool A2, bool B2, int S1 = 0>
+template <bool A1, bool B1, bool A2, bool B2, int S1 = 0, int S2 = 0>
 __global__ __launch_bounds__(kSplitThreads) void pointwise_dual_kernel(ProductArgs g1,
                                                                        ProductArgs g2,
                                                                        DualGrid d) {
-  __shared__ __align__(16) DualLds<S1> lds;
+  __shared__ __align__(16) DualLds<S1, S2> lds;
   uint32_t b = blockIdx.x;
   // each part's tiles remapped on their own, so every XCD keeps a share of both parts
   if (b < d.blocks1)
@@ -1634,7 +1632,10 @@ __global__ __launch_bounds__(kSplitThreads) void pointwise_dual_kernel(ProductAr
   } else if (b < d.blocks1 + d.blocks2) {
     b -= d.blocks1;
     const uint32_t plane = d.nx2 * d.ny2, z = b / plane, r = b - z * plane;
-    split_tile<A2, B2>(g2, r % d.nx2, r / d.nx2, z, lds.split);
+    if constexpr (S2 == 2)
+      split_tile16<A2, B2>(g2, r % d.nx2, r / d.nx2, z, lds.split16);
+    else
+      split_tile<A2, B2>(g2, r % d.nx2, r / d.nx2, z, lds.split);
   } else {
     bias_block(d.bias, b - d.blocks1 - d.blocks2);
   }
@@ -2207,11 +2208,32 @@ void launch_split(hipStream_t s, const ProductArgs &a, uint32_t chunks) {
   oxh::launch(pointwise_split_kernel<A, B>, grid, dim3(kSplitThreads), 0, s, a);
 }
 
+// Weight gradients on split tiles whose 8 x 8 tiles (with their chunks) exceed
+// OXH_WEIGHT_SPLIT16 take 16 x 16 split tiles, alone and in the paired launch: a quarter of the
+// blocks (a paired launch then fits the chip in one round of blocks: its LDS allows 4 per CU)
+// and half the operand reads per output.  0: always 8 x 8.
+#ifndef OXH_WEIGHT_SPLIT16
+#define OXH_WEIGHT_SPLIT16 512
+#endif
+bool weight_split16(const ProductArgs &a, uint32_t chunks) {
+  const uint64_t tiles8 = static_cast<uint64_t>((a.N + 7) / 8) * ((a.M + 7) / 8) * chunks;
+  return OXH_WEIGHT_SPLIT16 > 0 && tiles8 > OXH_WEIGHT_SPLIT16;
+}
+
 oxh_status launch_weight_product(const char *name, hipStream_t s, const ProductArgs &a,
                                  const KSplit &split) {
   const uint32_t chunks = split.chunks;
+  const bool t16 = weight_split16(a, chunks);
   if (split.serial32) {
     launch_tiled<kTile, 256, true>(s, a, chunks);
+  } else if (t16 && a.a.k_fast && a.b.k_fast) {
+    launch_split16<true, true>(s, a, chunks);
+  } else if (t16 && a.a.k_fast) {
+    launch_split16<true, false>(s, a, chunks);
+  } else if (t16 && a.b.k_fast) {
+    launch_split16<false, true>(s, a, chunks);
+  } else if (t16) {
+    launch_split16<false, false>(s, a, chunks);
   } else if (a.a.k_fast && a.b.k_fast) {
     launch_split<true, true>(s, a, chunks);
   } else if (a.a.k_fast) {
@@ -2238,36 +2260,40 @@ bool launch_dual(hipStream_t s, const ProductArgs &w, const KSplit &split, const
   if (split.serial32 || big_tiles(w, split.chunks) + big_tiles(x, 1) >= kSmallGrid)
     return false;
   const int s1 = input_splits(x);
-  const uint32_t t1 = s1 == 1 ? 8 : 16;  // the input gradient's tile
+  const bool t16 = weight_split16(w, split.chunks);
+  const uint32_t t1 = s1 == 1 ? 8 : 16, t2 = t16 ? 16 : 8;  // the two products' tiles
   DualGrid d;
   d.nx1 = (x.N + t1 - 1) / t1;
   d.ny1 = (x.M + t1 - 1) / t1;
   d.blocks1 = d.nx1 * d.ny1;
-  d.nx2 = (w.N + 7) / 8;
-  d.ny2 = (w.M + 7) / 8;
+  d.nx2 = (w.N + t2 - 1) / t2;
+  d.ny2 = (w.M + t2 - 1) / t2;
   d.blocks2 = d.nx2 * d.ny2 * split.chunks;
   d.bias = bias;
   const uint32_t blocks3 = bias.out != nullptr ? bias_blocks(bias.out_c) : 0;
   const dim3 grid(d.blocks1 + d.blocks2 + blocks3), block(kSplitThreads);
-  if (w.a.k_fast && w.b.k_fast && !x.a.k_fast && !x.b.k_fast) {
-    if (s1 == 2)
-      oxh::launch(pointwise_dual_kernel<false, false, true, true, 2>, grid, block, 0, s, x, w, d);
-    else if (s1 == 1)
-      oxh::launch(pointwise_dual_kernel<false, false, true, true, 1>, grid, block, 0, s, x, w, d);
-    else
-      oxh::launch(pointwise_dual_kernel<false, false, true, true>, grid, block, 0, s, x, w, d);
-  } else if (!w.a.k_fast && !w.b.k_fast && !x.a.k_fast && x.b.k_fast) {
-    if (s1 == 2)
-      oxh::launch(pointwise_dual_kernel<false, true, false, false, 2>, grid, block, 0, s, x, w,
-                  d);
-    else if (s1 == 1)
-      oxh::launch(pointwise_dual_kernel<false, true, false, false, 1>, grid, block, 0, s, x, w,
-                  d);
-    else
-      oxh::launch(pointwise_dual_kernel<false, true, false, false>, grid, block, 0, s, x, w, d);
-  } else {
+#define OXH_DUAL(A1, B1, A2, B2)                                                             \
+  do {                                                                                       \
+    if (s1 == 2 && t16)                                                                      \
+      oxh::launch(pointwise_dual_kernel<A1, B1, A2, B2, 2, 2>, grid, block, 0, s, x, w, d);  \
+    else if (s1 == 2)                                                                        \
+      oxh::launch(pointwise_dual_kernel<A1, B1, A2, B2, 2, 0>, grid, block, 0, s, x, w, d);  \
+    else if (s1 == 1 && t16)                                                                 \
+      oxh::launch(pointwise_dual_kernel<A1, B1, A2, B2, 1, 2>, grid, block, 0, s, x, w, d);  \
+    else if (s1 == 1)                                                                        \
+      oxh::launch(pointwise_dual_kernel<A1, B1, A2, B2, 1, 0>, grid, block, 0, s, x, w, d);  \
+    else if (t16)                                                                            \
+      oxh::launch(pointwise_dual_kernel<A1, B1, A2, B2, 0, 2>, grid, block, 0, s, x, w, d);  \
+    else                                                                                     \
+      oxh::launch(pointwise_dual_kernel<A1, B1, A2, B2, 0, 0>, grid, block, 0, s, x, w, d);  \
+  } while (0)
+  if (w.a.k_fast && w.b.k_fast && !x.a.k_fast && !x.b.k_fast)
+    OXH_DUAL(false, false, true, true);
+  else if (!w.a.k_fast && !w.b.k_fast && !x.a.k_fast && x.b.k_fast)
+    OXH_DUAL(false, true, false, false);
+  else
     return false;
-  }
+#undef OXH_DUAL
   return true;
 }
 
