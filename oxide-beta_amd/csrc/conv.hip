@@ -2058,6 +2058,18 @@ int input_splits(const ProductArgs &x) {
   return kind <= OXH_IG_SPLIT ? kind : 0;
 }
 
+// One-wave 8 x 8 serial tiles hold ~9.5 KB of LDS each: 16 blocks per CU, 4096 on the chip at
+// once.  A larger grid would run a second round of blocks; the 16 x 16 serial tiling (four
+// waves, 8 blocks per CU, a quarter of the blocks) then takes it: the same sums (one serial
+// chain per output in either tiling), one round fewer.
+#ifndef OXH_TINY_ROUND
+#define OXH_TINY_ROUND 4096  // 8 x 8 blocks per round (0: always 8 x 8)
+#endif
+bool tiny_grid_rounds(const ProductArgs &a, uint32_t chunks) {
+  const uint64_t tiles8 = static_cast<uint64_t>((a.N + 7) / 8) * ((a.M + 7) / 8) * chunks;
+  return OXH_TINY_ROUND > 0 && tiles8 > OXH_TINY_ROUND;
+}
+
 template <bool A, bool B>
 void launch_split16(hipStream_t s, const ProductArgs &a, uint32_t chunks) {
   const dim3 grid((a.N + 15) / 16, (a.M + 15) / 16, chunks);
@@ -2088,7 +2100,7 @@ oxh_status launch_product(const char *name, hipStream_t s, const ProductArgs &a,
     launch_split16<false, true>(s, a, chunks);
   else if (kind == 2)
     launch_split16<false, false>(s, a, chunks);
-  else if (OXH_TINY_TILE == 8)
+  else if (OXH_TINY_TILE == 8 && !tiny_grid_rounds(a, chunks))
     launch_tiled<8, 64>(s, a, chunks);
   else
     launch_tiled<16, 256>(s, a, chunks);

@@ -37,6 +37,7 @@ CASES = [
     (128, 1280, 1, 1, 10, 1, 1, 1),    # config 5's classifier
     (128, 64, 8, 8, 256, 1, 1, 1),     # grids of >= 512 32 x 32 tiles (the others take 16 x 16)
     (128, 100, 4, 4, 300, 1, 1, 1),    # weight gradient on 32 x 32 tiles, ragged in both axes
+    (128, 64, 4, 4, 192, 1, 1, 1),     # 6144 8 x 8 serial tiles (over one round): 16 x 16 ones
     (2, 6, 7, 7, 4, 1, 2, 1),          # 1x1 with stride 2: direct path
     # ungrouped 3x3 / 5x5: per-image LDS staging (every K, S pair; ragged channel tiles), and a
     # plane too large to stage (per-thread tap kernels)
