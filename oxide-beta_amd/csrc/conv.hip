@@ -969,6 +969,12 @@ struct ProductArgs {
 // chain of each thread sets the time, 8 x 8 outputs per 64-thread block (one per thread: a
 // quarter of the chain work per thread, four times the blocks, and one wave per CU rather than
 // four sharing its LDS), or 16 x 16 per 256 threads with OXH_TINY_TILE=16.
+// k per LDS stage of the 32 x 32 tiling: 64 keeps a block's two slabs at ~19 KB (8 blocks per
+// CU), where 128-k slabs (~35 KB, 4 per CU) put config 5's largest weight gradient (1200
+// blocks) in two rounds of blocks.
+#ifndef OXH_TILE32_SLAB
+#define OXH_TILE32_SLAB 64
+#endif
 #ifndef OXH_SMALL_SLAB
 #define OXH_SMALL_SLAB 128  // k per LDS stage of the small-grid tilings
 #endif
@@ -979,7 +985,7 @@ struct TileShape {
   static constexpr int kCols = Threads == 256 ? 16 : 8;       // threads per tile row
   static constexpr int kMicro = Tile / kCols;                  // outputs per thread per axis
   static constexpr int kSlab =  // k per LDS stage
-      Tile == kTile ? 128 : (Tile == 16 && Threads == 64 ? 64 : OXH_SMALL_SLAB);
+      Tile == kTile ? OXH_TILE32_SLAB : (Tile == 16 && Threads == 64 ? 64 : OXH_SMALL_SLAB);
   static constexpr int kLoads = Tile * kSlab / Threads;        // per thread, per operand
   static_assert(kCols * kCols == Threads && kMicro * kCols == Tile, "tile shape");
   static_assert(Threads % kSlab == 0 || kSlab % Threads == 0, "slab");
