@@ -69,6 +69,8 @@ using oxh::tap_mask;
 using oxh::tap_operand;
 using oxh::tap_term;
 
+typedef float f32x4_t __attribute__((ext_vector_type(4)));  // MFMA accumulators
+
 // ---------------------------------------------------------------- direct kernels
 
 __global__ __launch_bounds__(256) void conv2d_forward_kernel(ConvGeom g, uint32_t total,
@@ -434,6 +436,164 @@ __global__ __launch_bounds__(256) void conv2d_forward_split_kernel(
   for (int r = 0; r < kLdsR; ++r) {
     const uint32_t ocl = q * kLdsR + r;
     if (ocl < ocn) y[(static_cast<uint64_t>(n) * g.out_c + oc0 + ocl) * oplane + pos] = acc[r];
+  }
+}
+
+// The forward of an ungrouped K x K convolution on the matrix cores, as an implicit GEMM per
+// image: y[oc][p] = bias[oc] + sum over (input channel ic, tap t) of X[ic][iy(p, t)][ix(p, t)] *
+// W[oc][ic][t], a tolerance-bar sum (the MFMA's fused roundings, in place of the split
+// kernel's fused multiply-adds).  Block (16-channel output tile, image) stages the image with a
+// zero halo -- channel ic at xl[ic * cs + yy * wp + xx], yy = iy + pad, xx = ix + pad, a hp x wp
+// plane that covers every tap of every output position, so no tap needs a mask -- and the
+// tile's weights as wl[(t * C + ic) * 16 + ocl] (zero past the channels).  Wave w takes position
+// tile pt = w % pos_tiles and part w / pos_tiles of the input channels (kparts parts: the four
+// waves busy when the plane has fewer than three 16-position tiles); per step of 4 channels and
+// per tap, v_mfma_f32_16x16x4_f32 with lane (i, q) supplying A[i][q] = X[ic + q] at output
+// position 16 pt + i (positions past the plane read position 0 and are not stored) and B[q][i] =
+// W[oc0 + i][ic + q][t]; D[4 q + r][i] (lane i + 16 q, register r) is output channel oc0 + i at
+// position 16 pt + 4 q + r.  Part 0 starts from the bias; the other parts' sums are added to it
+// in part order.  in_c is a multiple of 4; the operands are 16-byte aligned.
+struct MfmaForward {
+  uint32_t hp, wp, cs, ocs, oc_tile, pos_tiles, kparts;
+  oxh::FastDiv plane_div, rows_div;  // rows = in_c * K * K
+};
+
+template <int K, int S>
+__global__ __launch_bounds__(256) void conv2d_forward_mfma_kernel(
+    ConvGeom g, MfmaForward f, const float *__restrict__ x, const float *__restrict__ wt,
+    const float *__restrict__ bias, float *__restrict__ y) {
+  extern __shared__ float lds[];
+  constexpr int T = K * K;
+  const oxh::BlockTile bt = oxh::xcd_block();
+  const uint32_t n = bt.y, oc0 = bt.x * f.oc_tile;
+  const uint32_t ocn = min(f.oc_tile, g.out_c - oc0);
+  const uint32_t C = g.in_c, plane = g.h * g.w;
+  float *xl = lds, *wl = lds + round4(C * f.cs);
+  // Staging, every global load of a round in flight at once (one round for config 5's
+  // shapes): the image and the weights as float4, while the LDS image region is zeroed (the
+  // halo keeps the zeros) and the weight columns past the channels are cleared; a barrier; then
+  // the image's values at ic * cs + (iy + pad) * wp + ix + pad and the weights at
+  // (t * C + ic) * ocs + ocl.
+  constexpr int U = 8;  // float4 per thread per source per round
+  const uint32_t rows = C * T, nt = blockDim.x;
+  const float4 *x4 = reinterpret_cast<const float4 *>(x + static_cast<uint64_t>(n) * C * plane);
+  const float4 *w4 = reinterpret_cast<const float4 *>(wt + static_cast<uint64_t>(oc0) * rows);
+  const uint32_t n4 = C * plane / 4, m4 = ocn * rows / 4;
+  const uint32_t most = n4 > m4 ? n4 : m4;
+  for (uint32_t b = 0; b < most; b += nt * U) {
+    float4 xv[U], wv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t e = b + threadIdx.x + u * nt;
+      xv[u] = x4[e < n4 ? e : 0];
+      wv[u] = w4[e < m4 ? e : 0];
+    }
+    if (b == 0) {
+      float4 *z = reinterpret_cast<float4 *>(xl);
+      for (uint32_t e = threadIdx.x; e < round4(C * f.cs) / 4; e += nt)
+        z[e] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (f.ocs > ocn) zero_fill(wl, rows, f.ocs, ocn, f.ocs - ocn);
+      __syncthreads();
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t e = b + threadIdx.x + u * nt;
+      if (e < n4) {
+        uint32_t ic = fdiv(4 * e, f.plane_div), rem = 4 * e - ic * plane;
+        uint32_t iy = fdiv(rem, g.w_div), ix = rem - iy * g.w;
+        const float v[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          xl[ic * f.cs + (iy + g.pad) * f.wp + ix + g.pad] = v[c];
+          const bool row_end = ++ix == g.w;
+          ix = row_end ? 0 : ix;
+          iy += row_end ? 1 : 0;
+          const bool plane_end = iy == g.h;
+          iy = plane_end ? 0 : iy;
+          ic += plane_end ? 1 : 0;
+        }
+      }
+      if (e < m4) {
+        uint32_t ocl = fdiv(4 * e, f.rows_div), rem = 4 * e - ocl * rows;
+        uint32_t ic = rem / T, t = rem - ic * T;
+        const float v[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          wl[(t * C + ic) * f.ocs + ocl] = v[c];
+          const bool tap_end = ++t == static_cast<uint32_t>(T);
+          t = tap_end ? 0 : t;
+          ic += tap_end ? 1 : 0;
+          const bool ch_end = ic == C;
+          ic = ch_end ? 0 : ic;
+          ocl += ch_end ? 1 : 0;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  // wave w: position tile w % pos_tiles, part w / pos_tiles of the input-channel steps
+  const uint32_t lane = threadIdx.x % 64, i = lane % 16, q = lane / 16, w = threadIdx.x / 64;
+  const uint32_t P = g.oh * g.ow, jobs = f.pos_tiles, parts = f.kparts;
+  const uint32_t pt = w % jobs, kp = w / jobs;
+  const bool active = w < jobs * parts;
+  const uint32_t steps = C / 4, per = (steps + parts - 1) / parts;
+  const uint32_t s0 = min(kp * per, steps), s1 = min(s0 + per, steps);
+  const uint32_t p = pt * 16 + i, pc = p < P ? p : 0;
+  const uint32_t oy = fdiv(pc, g.ow_div), ox = pc - oy * g.ow;
+  const uint32_t abase = q * f.cs + oy * S * f.wp + ox * S;
+  const uint32_t oc = i;  // this lane's channel of the tile (B column, D column)
+  const uint32_t bbase = q * f.ocs + oc;
+  const float b0 = kp == 0 && oc < ocn ? bias[oc0 + oc] : 0.0f;
+  f32x4_t acc = {b0, b0, b0, b0};
+  if (active && s0 < s1) {
+    // per step of 4 input channels the K * K taps' MFMAs, the next step's operands read from
+    // LDS before them
+    const uint32_t astep = 4 * f.cs, bstep = 4 * f.ocs, tstride = C * f.ocs;
+    float av[T], bv[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      av[t] = xl[abase + s0 * astep + (t / K) * f.wp + (t % K)];
+      bv[t] = wl[bbase + s0 * bstep + t * tstride];
+    }
+    for (uint32_t j = s0; j < s1; ++j) {
+      const uint32_t jn = j + 1 < s1 ? j + 1 : j;
+      float an[T], bn[T];
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        an[t] = xl[abase + jn * astep + (t / K) * f.wp + (t % K)];
+        bn[t] = wl[bbase + jn * bstep + t * tstride];
+      }
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[t], bv[t], acc, 0, 0, 0);
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        av[t] = an[t];
+        bv[t] = bn[t];
+      }
+    }
+  }
+  if (parts > 1) {  // the parts added in order by the part-0 wave
+    float *red = wl + rows * f.ocs;  // red[((kp - 1) * jobs + pt) * 256 + r * 64 + lane]
+    if (active && kp > 0) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[((kp - 1) * jobs + pt) * 256 + r * 64 + lane] = acc[r];
+    }
+    __syncthreads();
+    if (active && kp == 0) {
+      for (uint32_t k = 1; k < parts; ++k) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] += red[((k - 1) * jobs + pt) * 256 + r * 64 + lane];
+      }
+    }
+  }
+  if (active && kp == 0 && oc < ocn) {
+    float *yo = y + (static_cast<uint64_t>(n) * g.out_c + oc0 + oc) * P;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t pos = pt * 16 + 4 * q + r;
+      if (pos < P) yo[pos] = acc[r];
+    }
   }
 }
 
@@ -1212,7 +1372,6 @@ __device__ __forceinline__ void product_sum(
 #ifndef OXH_TILE32_MFMA
 #define OXH_TILE32_MFMA 1  // 1: the 32 x 32 tiles' fused-multiply-add sums on the matrix cores
 #endif
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 // A tile's sum over [kb, ke) on the matrix cores: the Threads threads (t = 0 .. Threads - 1)
 // stage Tile x kSlab slabs of both operands as product_sum<Tile, Threads> does (same loads,
@@ -1854,6 +2013,39 @@ LdsPlan forward_split_plan(const ConvGeom &g) {
   p.groups = static_cast<uint32_t>(items);  // items per block
   p.threads = static_cast<uint32_t>((kFwdParts * items + 63) / 64 * 64);
   p.lds_bytes = static_cast<uint32_t>(floats * 4);
+  return p;
+}
+
+// The matrix-core forward takes the split forward's shapes (output planes of <= 64 positions)
+// whose input channels are a multiple of 4: blocks of 256 threads over (16-channel tile, image),
+// the halo-padded image, the tile's weights and the parts' partial sums within the LDS budget.
+// lds_bytes == 0: not taken.
+#ifndef OXH_FWD_MFMA
+#define OXH_FWD_MFMA 1  // 0: the split forward keeps its fused-multiply-add kernel
+#endif
+struct MfmaForwardPlan {
+  MfmaForward f{};
+  uint32_t tiles = 0, lds_bytes = 0;
+};
+MfmaForwardPlan forward_mfma_plan(const ConvGeom &g) {
+  MfmaForwardPlan p;
+  if (!OXH_FWD_MFMA || g.in_c % 4 != 0 || forward_split_plan(g).tile == 0) return p;
+  MfmaForward &f = p.f;
+  f.hp = (g.oh - 1) * g.stride + g.kh;
+  f.wp = (g.ow - 1) * g.stride + g.kw;
+  f.cs = f.hp * f.wp | 1u;  // odd: the four input-channel lane groups start in different banks
+  const uint32_t P = g.oh * g.ow;
+  f.pos_tiles = (P + 15) / 16;  // at most 4: the split forward's planes hold <= 64 positions
+  f.kparts = f.pos_tiles >= 3 ? 1 : 4 / f.pos_tiles;
+  f.oc_tile = 16;
+  f.ocs = 16;
+  const uint64_t image = round4(g.in_c * f.cs), rows = static_cast<uint64_t>(g.in_c) * g.kh * g.kw;
+  const uint64_t red = f.kparts > 1 ? static_cast<uint64_t>(f.kparts - 1) * f.pos_tiles * 256 : 0;
+  if (f.pos_tiles > 4 || image + rows * f.ocs + red > kLdsFloats) return p;
+  f.plane_div = oxh::make_fastdiv(g.h * g.w);
+  f.rows_div = oxh::make_fastdiv(static_cast<uint32_t>(rows));
+  p.tiles = (g.out_c + f.oc_tile - 1) / f.oc_tile;
+  p.lds_bytes = static_cast<uint32_t>((image + rows * f.ocs + red) * 4);
   return p;
 }
 
@@ -2512,6 +2704,17 @@ oxh_status oxh_conv2d_forward(oxh_stream stream, const oxh_conv2d_shape *shape,
     a.K = g.in_c;
     a.k_chunk = a.K;
     return launch_product(name, s, a, 1, true);
+  }
+  const MfmaForwardPlan mp = forward_mfma_plan(g);
+  if (mp.lds_bytes > 0 && oxh::aligned16(input) && oxh::aligned16(weight)) {
+    const dim3 lgrid(mp.tiles, g.batch), lblock(256);
+    switch (tap_kernel(g)) {
+      case 31: oxh::launch(conv2d_forward_mfma_kernel<3, 1>, lgrid, lblock, mp.lds_bytes, s, g, mp.f, input, weight, bias, output); break;
+      case 32: oxh::launch(conv2d_forward_mfma_kernel<3, 2>, lgrid, lblock, mp.lds_bytes, s, g, mp.f, input, weight, bias, output); break;
+      case 51: oxh::launch(conv2d_forward_mfma_kernel<5, 1>, lgrid, lblock, mp.lds_bytes, s, g, mp.f, input, weight, bias, output); break;
+      default: oxh::launch(conv2d_forward_mfma_kernel<5, 2>, lgrid, lblock, mp.lds_bytes, s, g, mp.f, input, weight, bias, output);
+    }
+    return oxh::launched(name);
   }
   const LdsPlan sp = forward_split_plan(g);
   if (sp.tile > 0) {

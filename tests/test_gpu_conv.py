@@ -38,11 +38,14 @@ CASES = [
     (128, 64, 8, 8, 256, 1, 1, 1),     # grids of >= 512 32 x 32 tiles (the others take 16 x 16)
     (128, 100, 4, 4, 300, 1, 1, 1),    # weight gradient on 32 x 32 tiles, ragged in both axes
     (128, 64, 4, 4, 192, 1, 1, 1),     # 6144 8 x 8 serial tiles (over one round): 16 x 16 ones
+    (6, 24, 2, 2, 40, 1, 1, 1),        # weight gradient parts of 6 k: float4 slab loads from
+                                       # k = 0, 12 (ragged), scalar ones from k = 6, 18
     (2, 6, 7, 7, 4, 1, 2, 1),          # 1x1 with stride 2: direct path
     # ungrouped 3x3 / 5x5: per-image LDS staging (every K, S pair; ragged channel tiles), and a
     # plane too large to stage (per-thread tap kernels)
     (128, 32, 7, 7, 96, 3, 2, 1),      # config 5's second fused-IB convolution at full batch
     (5, 24, 6, 6, 40, 3, 1, 1),
+    (3, 20, 10, 10, 24, 3, 2, 1),      # matrix-core forward: 2 position tiles x 2 channel parts
     (2, 18, 6, 6, 20, 3, 1, 1),        # matrix-core forward: channels not multiples of 4 / 16
     (4, 16, 9, 7, 24, 5, 1, 1),
     (3, 8, 11, 10, 12, 5, 2, 1),
@@ -108,6 +111,7 @@ def test_conv2d_input_backward_accumulate(module, dev, case, in_place):
 @pytest.mark.parametrize("case", [
     (128, 96, 4, 4, 192, 1, 1, 1),     # config-5 shapes: both products in one launch (plane > 1)
     (128, 512, 1, 1, 128, 1, 1, 1),    # plane 1: the other operand layouts, one launch
+    (6, 24, 2, 2, 40, 1, 1, 1),        # float4 and scalar slab loads in one paired launch
     (128, 64, 8, 8, 256, 1, 1, 1),     # chunked weight gradient, grids too large to pair
     (128, 960, 1, 1, 1280, 1, 1, 1),
     (128, 1280, 1, 1, 10, 1, 1, 1),    # the classifier: the bias gradient in the paired launch
