@@ -781,6 +781,158 @@ __global__ __launch_bounds__(256) void conv2d_input_backward_s2_kernel(
   }
 }
 
+// The weight gradient of an ungrouped K x K convolution on the matrix cores:
+// dW[oc][ic][t] = sum over images n and output positions p of G[n][oc][p] *
+// X[n][ic][iy(p, t)][ix(p, t)], a GEMM of M = out_c rows, N = in_c * K * K columns (ic, t) and
+// k = (image, position), summed per chunk of ipc images (a tolerance-bar sum: the MFMA's fused
+// roundings; the chunks' partials are then added in chunk order).  Block (job group, chunk)
+// stages the chunk's images with a zero halo as conv2d_forward_mfma_kernel does
+// (xl[(img * C + ic) * cs + yy * wp + xx]) and the output gradient as
+// gl[oc * kpad + img * P + p] (zero past the chunk's positions and the channels).  Job j of the chunk (wave j % 4 of block j / 4)
+// is M tile mt = j / ngroups and N tiles [NG * (j % ngroups), + NG): per step of 4 k, lane
+// (i, q) supplies A[i][q] = G[16 mt + i][k + q] and, per N tile, B[q][i] = the image value of
+// column 16 nt + i = (ic, t) at k + q, xl[o(k + q) + ic * cs + (t / K) * wp + t % K] with
+// o(k) = img * C * cs + oy * S * wp + ox * S (columns past the weights and k past the chunk read
+// in-range values whose products are not stored or are multiplied by zero); D[4 q + r][i] is dW[16 mt + 4 q + r] at
+// column 16 nt + i.  The images and the gradient are 16-byte aligned with C * h * w and
+// out_c * oh * ow multiples of 4.
+struct MfmaWeight {
+  uint32_t hp, wp, cs, ipc, kpad, mtiles, ntiles, ng, ngroups, jobs;
+  oxh::FastDiv plane_div, oplane_div, m_div;
+};
+
+template <int K, int S, int NG>
+__global__ __launch_bounds__(256) void conv2d_weight_mfma_kernel(
+    ConvGeom g, MfmaWeight f, const float *__restrict__ grad, const float *__restrict__ x,
+    float *__restrict__ out) {
+  extern __shared__ float lds[];
+  constexpr int T = K * K;
+  const uint32_t chunk = blockIdx.y, n0 = chunk * f.ipc;
+  const uint32_t imgs = min(f.ipc, g.batch - n0);
+  const uint32_t C = g.in_c, M = g.out_c, plane = g.h * g.w, P = g.oh * g.ow;
+  const uint32_t xcount = round4(f.ipc * C * f.cs), gcount = f.mtiles * 16 * f.kpad;
+  float *xl = lds, *gl = lds + xcount;
+  const uint32_t nt_ = blockDim.x;
+  // every global load of a round in flight at once while the LDS regions are zeroed
+  constexpr int U = 8;
+  const float4 *x4 = reinterpret_cast<const float4 *>(x + static_cast<uint64_t>(n0) * C * plane);
+  const float4 *g4 = reinterpret_cast<const float4 *>(grad + static_cast<uint64_t>(n0) * M * P);
+  const uint32_t n4 = imgs * C * plane / 4, m4 = imgs * M * P / 4;
+  const uint32_t most = n4 > m4 ? n4 : m4;
+  for (uint32_t b = 0; b < most; b += nt_ * U) {
+    float4 xv[U], gv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t e = b + threadIdx.x + u * nt_;
+      xv[u] = x4[e < n4 ? e : 0];
+      gv[u] = g4[e < m4 ? e : 0];
+    }
+    if (b == 0) {
+      float4 *z = reinterpret_cast<float4 *>(lds);
+      for (uint32_t e = threadIdx.x; e < (xcount + gcount) / 4; e += nt_)
+        z[e] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      __syncthreads();
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t e = b + threadIdx.x + u * nt_;
+      if (e < n4) {  // image values: (img, ic) plane index, then row and column, with carries
+        uint32_t pl = fdiv(4 * e, f.plane_div), rem = 4 * e - pl * plane;
+        uint32_t iy = fdiv(rem, g.w_div), ix = rem - iy * g.w;
+        const float v[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          xl[pl * f.cs + (iy + g.pad) * f.wp + ix + g.pad] = v[c];
+          const bool row_end = ++ix == g.w;
+          ix = row_end ? 0 : ix;
+          iy += row_end ? 1 : 0;
+          const bool plane_end = iy == g.h;
+          iy = plane_end ? 0 : iy;
+          pl += plane_end ? 1 : 0;
+        }
+      }
+      if (e < m4) {  // gradient values: image, channel, position, with carries
+        const uint32_t pl = fdiv(4 * e, f.oplane_div);
+        uint32_t p = 4 * e - pl * P, img = fdiv(pl, f.m_div), oc = pl - img * M;
+        const float v[4] = {gv[u].x, gv[u].y, gv[u].z, gv[u].w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          gl[oc * f.kpad + img * P + p] = v[c];
+          const bool plane_end = ++p == P;
+          p = plane_end ? 0 : p;
+          oc += plane_end ? 1 : 0;
+          const bool image_end = oc == M;
+          oc = image_end ? 0 : oc;
+          img += image_end ? 1 : 0;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  const uint32_t job = blockIdx.x * 4 + threadIdx.x / 64;
+  if (job >= f.jobs) return;  // no barrier follows
+  const uint32_t lane = threadIdx.x % 64, i = lane % 16, q = lane / 16;
+  const uint32_t mt = job / f.ngroups, nt0 = (job - mt * f.ngroups) * f.ng;
+  const uint32_t cols = C * T;
+  // NG N tiles per job (tiles past the last one read in-range values and are not stored)
+  uint32_t boff[NG];
+#pragma unroll
+  for (int u = 0; u < NG; ++u) {
+    const uint32_t col = (nt0 + u) * 16 + i;
+    const uint32_t ic = col / T, t = col - ic * T;
+    boff[u] = col < cols ? ic * f.cs + (t / K) * f.wp + (t % K) : 0;
+  }
+  f32x4_t acc[NG];
+#pragma unroll
+  for (int u = 0; u < NG; ++u) acc[u] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  // per step of 4 k: lane k = 4 s + q's image offset formed in registers
+  const float *ga = gl + (mt * 16 + i) * f.kpad + q;
+  const uint32_t steps = f.kpad / 4, kc = imgs * P;
+  auto image_offset = [&](uint32_t k) {
+    const uint32_t img = fdiv(k, f.oplane_div), p = k - img * P;
+    const uint32_t oy = fdiv(p, g.ow_div), ox = p - oy * g.ow;
+    const uint32_t off = img * C * f.cs + oy * S * f.wp + ox * S;
+    return off & (k < kc ? 0xFFFFFFFFu : 0u);  // k past the chunk: A is zero there
+  };
+  // two operand sets in turn: the next step's loads are in flight during this step's MFMAs
+  auto load = [&](uint32_t st, float &av, float (&bv)[NG]) {
+    av = ga[4 * st];
+    const uint32_t base = image_offset(4 * st + q);
+#pragma unroll
+    for (int u = 0; u < NG; ++u) bv[u] = xl[base + boff[u]];
+  };
+  auto step = [&](float av, const float (&bv)[NG]) {
+#pragma unroll
+    for (int u = 0; u < NG; ++u)
+      acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[u], acc[u], 0, 0, 0);
+  };
+  float a0, a1, b0[NG], b1[NG];
+  load(0, a0, b0);
+  uint32_t s4 = 0;
+  for (; s4 + 1 < steps; s4 += 2) {  // sched_barrier: the loads stay ahead of the MFMAs
+    load(s4 + 1, a1, b1);
+    __builtin_amdgcn_sched_barrier(0);
+    step(a0, b0);
+    __builtin_amdgcn_sched_barrier(0);
+    load(s4 + 2 < steps ? s4 + 2 : s4 + 1, a0, b0);
+    __builtin_amdgcn_sched_barrier(0);
+    step(a1, b1);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (s4 < steps) step(a0, b0);
+  float *oc_out = out + static_cast<uint64_t>(chunk) * M * cols;
+#pragma unroll
+  for (int u = 0; u < NG; ++u) {
+    const uint32_t col = (nt0 + u) * 16 + i;
+    if (col >= cols) continue;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t oc = mt * 16 + 4 * q + r;
+      if (oc < M) oc_out[oc * cols + col] = acc[u][r];
+    }
+  }
+}
+
 // Weight gradient partials: block (output-channel tile of kDwOcTile, image chunk) stages each
 // image's input planes and the tile's output-gradient planes position-major
 // (gl[pos * kDwOcTile + ocl], zero past the tile).  Thread t < pairs * groups owns one
@@ -2132,6 +2284,58 @@ LdsPlan weight_lds_plan(const ConvGeom &g, bool bias = false) {
   return p;
 }
 
+// The matrix-core weight gradient: ungrouped K x K convolutions whose image and gradient runs
+// allow 16-byte loads (C * h * w and out_c * oh * ow multiples of 4) and whose chunk of ipc
+// images (at least 32 positions) holds at most 64 positions; N tiles per job for about
+// OXH_WGT_JOB_MFMA MFMAs per wave; the images, the gradient and nothing else in LDS.
+// lds_bytes == 0: not taken.
+#ifndef OXH_WGT_MFMA
+#define OXH_WGT_MFMA 1  // 0: K x K weight gradients keep the LDS fused-multiply-add kernel
+#endif
+#ifndef OXH_WGT_JOB_MFMA
+#define OXH_WGT_JOB_MFMA 80
+#endif
+struct MfmaWeightPlan {
+  MfmaWeight f{};
+  uint32_t chunks = 0, blocks = 0, lds_bytes = 0;
+};
+MfmaWeightPlan weight_mfma_plan(const ConvGeom &g) {
+  MfmaWeightPlan p;
+  const uint64_t plane = static_cast<uint64_t>(g.h) * g.w, P = static_cast<uint64_t>(g.oh) * g.ow;
+  if (!OXH_WGT_MFMA || !lds_eligible(g) || (g.in_c * plane) % 4 != 0 || (g.out_c * P) % 4 != 0 ||
+      P > 64)
+    return p;
+  MfmaWeight &f = p.f;
+  f.hp = (g.oh - 1) * g.stride + g.kh;
+  f.wp = (g.ow - 1) * g.stride + g.kw;
+  f.cs = f.hp * f.wp | 1u;
+  uint64_t ipc = (32 + P - 1) / P;
+  if (ipc > g.batch) ipc = g.batch;
+  f.ipc = static_cast<uint32_t>(ipc);
+  f.kpad = static_cast<uint32_t>(round4(static_cast<uint32_t>(ipc * P)));
+  if (f.kpad > 64) return p;
+  const uint32_t steps = f.kpad / 4;
+  f.mtiles = (g.out_c + 15) / 16;
+  f.ntiles = (g.in_c * g.kh * g.kw + 15) / 16;
+  // N tiles per job: 3, 6 or 9 (the kernel's instantiations), about OXH_WGT_JOB_MFMA MFMAs
+  const uint32_t want = OXH_WGT_JOB_MFMA / steps;
+  f.ng = want >= 9 ? 9 : want >= 6 ? 6 : 3;
+  if (f.ng > 3 && (f.ntiles + 2) / 3 * 3 <= f.ng) f.ng = (f.ntiles + 2) / 3 * 3;  // small N
+  f.ngroups = (f.ntiles + f.ng - 1) / f.ng;
+  f.jobs = f.mtiles * f.ngroups;
+  const uint64_t floats = round4(static_cast<uint32_t>(ipc * g.in_c * f.cs)) +
+                          static_cast<uint64_t>(f.mtiles) * 16 * f.kpad;
+  if (floats > kLdsFloats) return p;
+  f.plane_div = oxh::make_fastdiv(static_cast<uint32_t>(plane));
+  f.oplane_div = oxh::make_fastdiv(static_cast<uint32_t>(P));
+  f.m_div = oxh::make_fastdiv(g.out_c);
+  p.chunks = static_cast<uint32_t>((g.batch + ipc - 1) / ipc);
+  if (p.chunks > 1 && static_cast<uint64_t>(p.chunks) * weight_elems(g) >= kMaxElems) return p;
+  p.blocks = (f.jobs + 3) / 4;
+  p.lds_bytes = static_cast<uint32_t>(floats * 4);
+  return p;
+}
+
 // 1x1, stride 1, no padding, one group: the convolution is a matrix product over channels.
 bool pointwise(const ConvGeom &g) {
   return g.kh == 1 && g.kw == 1 && g.stride == 1 && g.pad == 0 && g.groups == 1 &&
@@ -2324,9 +2528,20 @@ bool depthwise_single_pass(const ConvGeom &g) {
 
 uint64_t weight_partial_bytes(const ConvGeom &g) {
   if (depthwise_single_pass(g)) return 0;
-  // room for the bias sums of a parameter-only oxh_conv2d_backward after each chunk's weights
+  // the matrix-core kernel's chunks, or the LDS kernel's with room for the bias sums of a
+  // parameter-only oxh_conv2d_backward after each chunk's weights, or (operands the matrix-core
+  // kernel does not take) the generic kernel's
+  const MfmaWeightPlan mp = weight_mfma_plan(g);
+  const uint64_t mbytes = mp.lds_bytes > 0 && mp.chunks > 1 ? mp.chunks * weight_elems(g) * 4 : 0;
   const LdsPlan lp = weight_lds_plan(g);
-  if (lp.tile > 0) return lp.chunks > 1 ? lp.chunks * (weight_elems(g) + g.out_c) * 4 : 0;
+  if (lp.tile > 0) {
+    const uint64_t lbytes = lp.chunks > 1 ? lp.chunks * (weight_elems(g) + g.out_c) * 4 : 0;
+    return lbytes > mbytes ? lbytes : mbytes;
+  }
+  if (mp.lds_bytes > 0) {
+    const uint64_t generic = weight_elems(g) * weight_chunks(g) * 4;
+    return generic > mbytes ? generic : mbytes;
+  }
   if (pointwise(g)) {
     const KSplit k = product_split(g);
     return k.chunks > 1 ? static_cast<uint64_t>(k.chunks) * g.out_c * g.in_c * 4 : 0;
@@ -2599,6 +2814,36 @@ oxh_status weight_backward_impl(const char *name, hipStream_t s, const ConvGeom 
     else
       oxh::launch(conv2d_depthwise_weight_kernel<5, 256>, dim3(g.out_c), dim3(256), 0, s, g,
                   oplane_div, gradient, input, weight_gradient);
+    return oxh::launched(name);
+  }
+  // the matrix-core kernel where it takes the shape (the caller then forms the bias)
+  const MfmaWeightPlan mp = weight_mfma_plan(g);
+  if (mp.lds_bytes > 0 && oxh::aligned16(gradient) && oxh::aligned16(input)) {
+    float *out = mp.chunks > 1 ? partial : weight_gradient;
+    const dim3 mgrid(mp.blocks, mp.chunks), mblock(256);
+#define OXH_WGT_MFMA_LAUNCH(KK, SS)                                                           \
+  do {                                                                                      \
+    if (mp.f.ng == 9)                                                                       \
+      oxh::launch(conv2d_weight_mfma_kernel<KK, SS, 9>, mgrid, mblock, mp.lds_bytes, s, g,  \
+                  mp.f, gradient, input, out);                                              \
+    else if (mp.f.ng == 6)                                                                  \
+      oxh::launch(conv2d_weight_mfma_kernel<KK, SS, 6>, mgrid, mblock, mp.lds_bytes, s, g,  \
+                  mp.f, gradient, input, out);                                              \
+    else                                                                                    \
+      oxh::launch(conv2d_weight_mfma_kernel<KK, SS, 3>, mgrid, mblock, mp.lds_bytes, s, g,  \
+                  mp.f, gradient, input, out);                                              \
+  } while (0)
+    switch (tap_kernel(g)) {
+      case 31: OXH_WGT_MFMA_LAUNCH(3, 1); break;
+      case 32: OXH_WGT_MFMA_LAUNCH(3, 2); break;
+      case 51: OXH_WGT_MFMA_LAUNCH(5, 1); break;
+      default: OXH_WGT_MFMA_LAUNCH(5, 2);
+    }
+#undef OXH_WGT_MFMA_LAUNCH
+    oxh_status st = oxh::launched(name);
+    if (st != OXH_OK || mp.chunks == 1) return st;
+    launch_sum_chunks(s, static_cast<uint32_t>(weight_elems(g)), mp.chunks, partial,
+                      weight_gradient);
     return oxh::launched(name);
   }
   // the bias sums ride along where their threads fit; else the caller forms the bias

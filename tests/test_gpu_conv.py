@@ -46,6 +46,7 @@ CASES = [
     (128, 32, 7, 7, 96, 3, 2, 1),      # config 5's second fused-IB convolution at full batch
     (5, 24, 6, 6, 40, 3, 1, 1),
     (3, 20, 10, 10, 24, 3, 2, 1),      # matrix-core forward: 2 position tiles x 2 channel parts
+    (2, 16, 9, 9, 64, 5, 2, 1),        # 5 x 5 stride-2 input gradient staging 64 weights per thread
     (2, 18, 6, 6, 20, 3, 1, 1),        # matrix-core forward: channels not multiples of 4 / 16
     (4, 16, 9, 7, 24, 5, 1, 1),
     (3, 8, 11, 10, 12, 5, 2, 1),
