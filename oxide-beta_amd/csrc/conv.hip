@@ -685,7 +685,7 @@ __global__ __launch_bounds__(256) void conv2d_input_backward_lds_kernel(
 // Each thread's 4 sums use all of its terms (the candidate kernels' threads spend 7 of 16
 // candidate terms of a 3 x 3 stride-2 kernel on offsets outside the kernel).
 struct PhaseGeom {
-  uint32_t lo, ohp, owp, ocp, ocs, ic_tile, a0, na, nb;
+  uint32_t lo, ohp, owp, ocp, ocs, ocw, ic_tile, a0, na, nb;
   oxh::FastDiv ab_div, nb_div;
 };
 
@@ -699,12 +699,12 @@ __global__ __launch_bounds__(256) void conv2d_input_backward_s2_kernel(
   const uint32_t n = bt.y, ic0 = bt.x * pg.ic_tile;
   const uint32_t ocp = pg.ocp, ocs = pg.ocs;
   const uint32_t icn = min(pg.ic_tile, g.in_c - ic0);
-  const uint32_t gcount = pg.ohp * pg.owp * ocs, wcount = pg.ic_tile * T * ocp;
+  const uint32_t gcount = pg.ohp * pg.owp * ocs, ocw = pg.ocw;
   float *gl = lds, *wl = lds + gcount;  // gcount is a multiple of 4
-  {
+  {  // the gradient's halo is zero
     float4 *l4 = reinterpret_cast<float4 *>(lds);
     const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (uint32_t i = threadIdx.x; i < (gcount + wcount) / 4; i += blockDim.x) l4[i] = z;
+    for (uint32_t i = threadIdx.x; i < gcount / 4; i += blockDim.x) l4[i] = z;
   }
   __syncthreads();
   const uint32_t oplane = g.oh * g.ow;
@@ -715,18 +715,38 @@ __global__ __launch_bounds__(256) void conv2d_input_backward_s2_kernel(
           const uint32_t oy = fdiv(opos, g.ow_div), ox = opos - oy * g.ow;
           return ((oy + pg.lo) * pg.owp + ox + pg.lo) * ocs + oc;
         });
-  const uint32_t run = icn * T;
+  // the tile's weights as wl[(icl * T + tap) * ocw + oc] (zero for oc past out_c), written as
+  // float4 of four output channels: element e = (oc group, r = icl * T + tap), r fastest, so a
+  // wave's four loads per element read contiguous runs of r and its 128-bit stores, ocw = 4 mod
+  // 32 floats apart, cover all banks
+  const uint32_t run = icn * T, groups = ocp / 4, wtotal = run * groups;
   const oxh::FastDiv run_div = oxh::make_fastdiv(run);
-  stage(
-      wl, wt + static_cast<uint64_t>(ic0) * T, g.out_c * run,
-      [&](uint32_t e) {
-        const uint32_t oc = fdiv(e, run_div);
-        return oc * g.in_c * T + (e - oc * run);
-      },
-      [&](uint32_t e) {
-        const uint32_t oc = fdiv(e, run_div);
-        return (e - oc * run) * ocp + oc;  // (icl * T + tap) * ocp + oc
-      });
+  const float *wsrc = wt + static_cast<uint64_t>(ic0) * T;
+  const uint32_t wrow = g.in_c * T;
+  constexpr int UW = 8;
+  for (uint32_t b0 = threadIdx.x; b0 < wtotal; b0 += blockDim.x * UW) {
+    float v[UW][4];
+#pragma unroll
+    for (int u = 0; u < UW; ++u) {
+      const uint32_t e = b0 + u * blockDim.x, ec = e < wtotal ? e : 0;
+      const uint32_t og = fdiv(ec, run_div), r = ec - og * run;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const uint32_t oc = 4 * og + c;
+        const bool ok = oc < g.out_c;
+        v[u][c] = tap_operand(wsrc[ok ? oc * wrow + r : 0], tap_mask(ok));
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < UW; ++u) {
+      const uint32_t e = b0 + u * blockDim.x;
+      if (e < wtotal) {
+        const uint32_t og = fdiv(e, run_div), r = e - og * run;
+        *reinterpret_cast<float4 *>(wl + r * ocw + 4 * og) =
+            make_float4(v[u][0], v[u][1], v[u][2], v[u][3]);
+      }
+    }
+  }
   __syncthreads();
   const uint32_t blocks_ab = pg.na * pg.nb, items = icn * blocks_ab;
   for (uint32_t it = threadIdx.x; it < items; it += blockDim.x) {
@@ -739,7 +759,7 @@ __global__ __launch_bounds__(256) void conv2d_input_backward_s2_kernel(
 #pragma unroll
       for (int jx = 0; jx < M; ++jx)  // (oy + lo, ox + lo) with oy = a - (M - 1) + jy
         gp[jy][jx] = gl + ((a + pg.lo - (M - 1) + jy) * pg.owp + b + pg.lo - (M - 1) + jx) * ocs;
-    const float *wq = wl + icl * T * ocp;
+    const float *wq = wl + icl * T * ocw;
     float acc[2][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}};
     for (uint32_t oc0 = 0; oc0 < ocp; oc0 += 4) {
       float4 gv[M][M], wv[T];
@@ -749,7 +769,7 @@ __global__ __launch_bounds__(256) void conv2d_input_backward_s2_kernel(
         for (int jx = 0; jx < M; ++jx)
           gv[jy][jx] = *reinterpret_cast<const float4 *>(gp[jy][jx] + oc0);
 #pragma unroll
-      for (int t = 0; t < T; ++t) wv[t] = *reinterpret_cast<const float4 *>(wq + t * ocp + oc0);
+      for (int t = 0; t < T; ++t) wv[t] = *reinterpret_cast<const float4 *>(wq + t * ocw + oc0);
 #pragma unroll
       for (int u = 0; u < 4; ++u)
 #pragma unroll
@@ -2232,11 +2252,15 @@ PhasePlan input_backward_s2_plan(const ConvGeom &g) {
   h.owp = h.lo + (g.ow > ax + 1 ? g.ow : ax + 1);
   h.ocp = round4(g.out_c);
   h.ocs = (h.ocp / 4) % 2 == 0 ? h.ocp + 4 : h.ocp;
+  h.ocw = h.ocp + ((36 - h.ocp % 32) % 32);  // 4 mod 32: conflict-free 128-bit weight stores
   const uint64_t blocks_ab = static_cast<uint64_t>(h.na) * h.nb;
   uint64_t tile = blocks_ab >= 256 ? 1 : 256 / blocks_ab;
   if (tile > g.in_c) tile = g.in_c;
+  // smaller tiles where the grid would leave the chip with one block per CU or fewer
+  while (tile > 1 && (g.in_c + tile - 1) / tile * static_cast<uint64_t>(g.batch) < 512)
+    tile = (tile + 1) / 2;
   const uint64_t gfloats = static_cast<uint64_t>(h.ohp) * h.owp * h.ocs;
-  const uint64_t per_ic = static_cast<uint64_t>(K) * K * h.ocp;
+  const uint64_t per_ic = static_cast<uint64_t>(K) * K * h.ocw;
   while (tile > 1 && gfloats + tile * per_ic > kLdsFloats) --tile;
   const uint64_t floats = gfloats + tile * per_ic;
   if (floats > kLdsFloats) return p;
