@@ -1541,6 +1541,12 @@ __device__ __forceinline__ void product_sum(
 #ifndef OXH_SPLIT_MFMA
 #define OXH_SPLIT_MFMA 1  // 1: the 16 x 16 split tiles sum on the matrix cores
 #endif
+#ifndef OXH_RING16
+#define OXH_RING16 2  // register slabs in flight in the 16 x 16 split tiles' matrix-core sums
+#endif
+#ifndef OXH_RING32
+#define OXH_RING32 1  // ... and in the 32 x 32 tiles'
+#endif
 #ifndef OXH_TILE32_MFMA
 #define OXH_TILE32_MFMA 1  // 1: the 32 x 32 tiles' fused-multiply-add sums on the matrix cores
 #endif
@@ -1556,7 +1562,7 @@ __device__ __forceinline__ void product_sum(
 // zeroed in both operands.  Each MFMA adds its four products to the accumulator with fused
 // roundings: for sums that need not follow the CPU path bit for bit (within 1e-5 * sum|terms|
 // of it), as the fused-multiply-add sums they replace.
-template <int Tile, int Threads, bool AKFast, bool BKFast>
+template <int Tile, int Threads, bool AKFast, bool BKFast, int D = 1>
 __device__ __forceinline__ void product_sum_mfma(const ProductArgs &g, uint32_t m0, uint32_t n0,
                                                  uint32_t kb, uint32_t ke, uint32_t slabs, int t,
                                                  f32x4_t &acc,
@@ -1568,45 +1574,56 @@ __device__ __forceinline__ void product_sum_mfma(const ProductArgs &g, uint32_t 
   static_assert(kSlab % 16 == 0 && kSlab + 4 <= ProductRow<Tile, Threads>::value, "mfma slab");
   const SlabLoader<Tile, Threads, AKFast> la(g.a, m0, g.M, t);
   const SlabLoader<Tile, Threads, BKFast> lb(g.b, n0, g.N, t);
-  float va[kLoads], vb[kLoads];
-  if (kb < ke) {
-    const uint32_t kc = min(ke - kb, static_cast<uint32_t>(kSlab));
-    la.fetch(g.a, kb, kc, va);
-    lb.fetch(g.b, kb, kc, vb);
+  // a ring of D register slabs: slab s is staged from set s % D, whose loads were issued D
+  // slabs earlier (each slab's global loads take about a memory round trip)
+  float va[D][kLoads], vb[D][kLoads];
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    const uint32_t k0 = kb + d * kSlab;
+    if (k0 < ke) {
+      const uint32_t kc = min(ke - k0, static_cast<uint32_t>(kSlab));
+      la.fetch(g.a, k0, kc, va[d]);
+      lb.fetch(g.b, k0, kc, vb[d]);
+    }
   }
   const int w = t / 64, lane = t % 64;
   const int ia = 16 * (w / kQuads) + lane % 16, ib = 16 * (w % kQuads) + lane % 16;
   const int q = lane / 16;
-  for (uint32_t s = 0; s < slabs; ++s) {
-    const uint32_t k0 = kb + s * kSlab;
-    const uint32_t kc = k0 < ke ? min(ke - k0, static_cast<uint32_t>(kSlab)) : 0;
-    if (kc > 0) {
-      la.stage(va, as);
-      lb.stage(vb, bs);
-    }
-    __syncthreads();
-    const uint32_t k1 = k0 + kSlab;
-    if (k1 < ke) {
-      const uint32_t kc1 = min(ke - k1, static_cast<uint32_t>(kSlab));
-      la.fetch(g.a, k1, kc1, va);
-      lb.fetch(g.b, k1, kc1, vb);
-    }
-    for (uint32_t kk = 0; kk < kc; kk += 16) {
-      float4 a = *reinterpret_cast<const float4 *>(&as[ia][kk + 4 * q]);
-      float4 b = *reinterpret_cast<const float4 *>(&bs[ib][kk + 4 * q]);
-      if (kk + 16 > kc) {
-        const uint32_t k = kk + 4 * static_cast<uint32_t>(q);
-        if (k >= kc) a.x = b.x = 0.0f;
-        if (k + 1 >= kc) a.y = b.y = 0.0f;
-        if (k + 2 >= kc) a.z = b.z = 0.0f;
-        if (k + 3 >= kc) a.w = b.w = 0.0f;
+  for (uint32_t s0 = 0; s0 < slabs; s0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const uint32_t s = s0 + d;
+      if (s >= slabs) break;  // block-uniform
+      const uint32_t k0 = kb + s * kSlab;
+      const uint32_t kc = k0 < ke ? min(ke - k0, static_cast<uint32_t>(kSlab)) : 0;
+      if (kc > 0) {
+        la.stage(va[d], as);
+        lb.stage(vb[d], bs);
       }
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b.x, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b.y, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b.z, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b.w, acc, 0, 0, 0);
+      __syncthreads();
+      const uint32_t k1 = k0 + D * kSlab;
+      if (k1 < ke) {
+        const uint32_t kc1 = min(ke - k1, static_cast<uint32_t>(kSlab));
+        la.fetch(g.a, k1, kc1, va[d]);
+        lb.fetch(g.b, k1, kc1, vb[d]);
+      }
+      for (uint32_t kk = 0; kk < kc; kk += 16) {
+        float4 a = *reinterpret_cast<const float4 *>(&as[ia][kk + 4 * q]);
+        float4 b = *reinterpret_cast<const float4 *>(&bs[ib][kk + 4 * q]);
+        if (kk + 16 > kc) {
+          const uint32_t k = kk + 4 * static_cast<uint32_t>(q);
+          if (k >= kc) a.x = b.x = 0.0f;
+          if (k + 1 >= kc) a.y = b.y = 0.0f;
+          if (k + 2 >= kc) a.z = b.z = 0.0f;
+          if (k + 3 >= kc) a.w = b.w = 0.0f;
+        }
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b.x, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b.y, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b.z, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b.w, acc, 0, 0, 0);
+      }
+      __syncthreads();
     }
-    __syncthreads();
   }
 }
 
@@ -1713,7 +1730,8 @@ __device__ __forceinline__ void product_tile(const ProductArgs &g, uint32_t bx, 
                      : 0.0f;
     }
     const uint32_t slabs = kb < ke ? (ke - kb + S::kSlab - 1) / S::kSlab : 0;
-    product_sum_mfma<Tile, Threads, AKFast, BKFast>(g, m0, n0, kb, ke, slabs, t, acc, as, bs);
+    product_sum_mfma<Tile, Threads, AKFast, BKFast, OXH_RING32>(g, m0, n0, kb, ke, slabs, t, acc,
+                                                                as, bs);
 #pragma unroll
     for (int r = 0; r < 4; ++r) product_store(g, bz, mq + r, n, acc[r], added[r]);
     return;
@@ -1867,8 +1885,8 @@ __device__ __forceinline__ void split_tile16(const ProductArgs &g, uint32_t bx, 
                      ? g.addend[axis_offset(g.cm, m) + axis_offset(g.cn, n)]
                      : 0.0f;
     }
-    product_sum_mfma<16, 64, AKFast, BKFast>(g, m0, n0, wb, we, slabs, t, acc, lds.as[w],
-                                             lds.bs[w]);
+    product_sum_mfma<16, 64, AKFast, BKFast, OXH_RING16>(g, m0, n0, wb, we, slabs, t, acc,
+                                                         lds.as[w], lds.bs[w]);
     if (w > 0) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) lds.part[w - 1][r][t] = acc[r];
