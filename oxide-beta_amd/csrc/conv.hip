@@ -1428,7 +1428,7 @@ struct ProductRow {
 // Fma: each term is added by one fused multiply-add (one rounding in place of the CPU path's
 // two: sums that need not follow the CPU path bit for bit -- the weight gradients and the
 // split forward -- at half the VALU work).
-template <int Tile, int Threads, bool AKFast, bool BKFast, bool Fma = false>
+template <int Tile, int Threads, bool AKFast, bool BKFast, bool Fma = false, int D = 1>
 __device__ __forceinline__ void product_sum(
     const ProductArgs &g, uint32_t m0, uint32_t n0, uint32_t kb, uint32_t ke, uint32_t slabs,
     int t, float (&acc)[TileShape<Tile, Threads>::kMicro][TileShape<Tile, Threads>::kMicro],
@@ -1440,11 +1440,17 @@ __device__ __forceinline__ void product_sum(
   const int tx = t % kCols, ty = t / kCols;
   const SlabLoader<Tile, Threads, AKFast> la(g.a, m0, g.M, t);
   const SlabLoader<Tile, Threads, BKFast> lb(g.b, n0, g.N, t);
-  float va[kLoads], vb[kLoads];
-  if (kb < ke) {
-    const uint32_t kc = min(ke - kb, static_cast<uint32_t>(kSlab));
-    la.fetch(g.a, kb, kc, va);
-    lb.fetch(g.b, kb, kc, vb);
+  // a ring of D register slabs: slab s is staged from set s % D, whose loads were issued D
+  // slabs earlier
+  float va[D][kLoads], vb[D][kLoads];
+#pragma unroll
+  for (int slot = 0; slot < D; ++slot) {
+    const uint32_t k0 = kb + slot * kSlab;
+    if (k0 < ke) {
+      const uint32_t kc = min(ke - k0, static_cast<uint32_t>(kSlab));
+      la.fetch(g.a, k0, kc, va[slot]);
+      lb.fetch(g.b, k0, kc, vb[slot]);
+    }
   }
   float4 a0[kMicro][kG4], b0[kMicro][kG4], a1[kMicro][kG4], b1[kMicro][kG4];
   auto read_group = [&](uint32_t k, float4 (&av)[kMicro][kG4], float4 (&bv)[kMicro][kG4]) {
@@ -1492,49 +1498,54 @@ __device__ __forceinline__ void product_sum(
 #pragma unroll
         for (int j = 0; j < kMicro; ++j) acc[i][j] += p[i][j][u];
   };
-  for (uint32_t s = 0; s < slabs; ++s) {
-    const uint32_t k0 = kb + s * kSlab;
-    const uint32_t kc = k0 < ke ? min(ke - k0, static_cast<uint32_t>(kSlab)) : 0;
-    if (kc > 0) {
-      la.stage(va, as);
-      lb.stage(vb, bs);
-    }
-    __syncthreads();
-    const uint32_t k1 = k0 + kSlab;
-    if (k1 < ke) {  // the next slab's loads overlap this slab's arithmetic
-      const uint32_t kc1 = min(ke - k1, static_cast<uint32_t>(kSlab));
-      la.fetch(g.a, k1, kc1, va);
-      lb.fetch(g.b, k1, kc1, vb);
-    }
-    // whole groups, two per iteration so the read-ahead alternates register sets; a group read
-    // starts at k <= kSlab, inside the row
-    const uint32_t full = kc / kGroupK * kGroupK;
-    uint32_t kk = 0;
-    if (full > 0) read_group(0, a0, b0);
-    while (kk < full) {
-      read_group(kk + kGroupK, a1, b1);
-      add_group(a0, b0);
-      kk += kGroupK;
-      if (kk >= full) break;
-      read_group(kk + kGroupK, a0, b0);
-      add_group(a1, b1);
-      kk += kGroupK;
-    }
-    for (; kk < kc; ++kk) {
-      float av[kMicro], bv[kMicro];
+  for (uint32_t s0 = 0; s0 < slabs; s0 += D) {
 #pragma unroll
-      for (int i = 0; i < kMicro; ++i) av[i] = as[ty * kMicro + i][kk];
+    for (int slot = 0; slot < D; ++slot) {
+      const uint32_t s = s0 + slot;
+      if (s >= slabs) break;  // block-uniform
+      const uint32_t k0 = kb + s * kSlab;
+      const uint32_t kc = k0 < ke ? min(ke - k0, static_cast<uint32_t>(kSlab)) : 0;
+      if (kc > 0) {
+        la.stage(va[slot], as);
+        lb.stage(vb[slot], bs);
+      }
+      __syncthreads();
+      const uint32_t k1 = k0 + D * kSlab;
+      if (k1 < ke) {  // the next slab's loads overlap this slab's arithmetic
+        const uint32_t kc1 = min(ke - k1, static_cast<uint32_t>(kSlab));
+        la.fetch(g.a, k1, kc1, va[slot]);
+        lb.fetch(g.b, k1, kc1, vb[slot]);
+      }
+      // whole groups, two per iteration so the read-ahead alternates register sets; a group read
+      // starts at k <= kSlab, inside the row
+      const uint32_t full = kc / kGroupK * kGroupK;
+      uint32_t kk = 0;
+      if (full > 0) read_group(0, a0, b0);
+      while (kk < full) {
+        read_group(kk + kGroupK, a1, b1);
+        add_group(a0, b0);
+        kk += kGroupK;
+        if (kk >= full) break;
+        read_group(kk + kGroupK, a0, b0);
+        add_group(a1, b1);
+        kk += kGroupK;
+      }
+      for (; kk < kc; ++kk) {
+        float av[kMicro], bv[kMicro];
 #pragma unroll
-      for (int j = 0; j < kMicro; ++j) bv[j] = bs[tx * kMicro + j][kk];
+        for (int i = 0; i < kMicro; ++i) av[i] = as[ty * kMicro + i][kk];
 #pragma unroll
-      for (int i = 0; i < kMicro; ++i)
+        for (int j = 0; j < kMicro; ++j) bv[j] = bs[tx * kMicro + j][kk];
 #pragma unroll
-        for (int j = 0; j < kMicro; ++j) {
-          if constexpr (Fma) acc[i][j] = __builtin_fmaf(av[i], bv[j], acc[i][j]);
-          else acc[i][j] += av[i] * bv[j];
-        }
+        for (int i = 0; i < kMicro; ++i)
+#pragma unroll
+          for (int j = 0; j < kMicro; ++j) {
+            if constexpr (Fma) acc[i][j] = __builtin_fmaf(av[i], bv[j], acc[i][j]);
+            else acc[i][j] += av[i] * bv[j];
+          }
+      }
+      __syncthreads();
     }
-    __syncthreads();
   }
 }
 
@@ -1546,6 +1557,12 @@ __device__ __forceinline__ void product_sum(
 #endif
 #ifndef OXH_RING32
 #define OXH_RING32 1  // ... and in the 32 x 32 tiles'
+#endif
+#ifndef OXH_RING8
+#define OXH_RING8 2  // ... and in the 8 x 8 split tiles'
+#endif
+#ifndef OXH_RING_SERIAL
+#define OXH_RING_SERIAL 1  // ... and in the serial tiles' sums
 #endif
 #ifndef OXH_TILE32_MFMA
 #define OXH_TILE32_MFMA 1  // 1: the 32 x 32 tiles' fused-multiply-add sums on the matrix cores
@@ -1578,12 +1595,12 @@ __device__ __forceinline__ void product_sum_mfma(const ProductArgs &g, uint32_t 
   // slabs earlier (each slab's global loads take about a memory round trip)
   float va[D][kLoads], vb[D][kLoads];
 #pragma unroll
-  for (int d = 0; d < D; ++d) {
-    const uint32_t k0 = kb + d * kSlab;
+  for (int slot = 0; slot < D; ++slot) {
+    const uint32_t k0 = kb + slot * kSlab;
     if (k0 < ke) {
       const uint32_t kc = min(ke - k0, static_cast<uint32_t>(kSlab));
-      la.fetch(g.a, k0, kc, va[d]);
-      lb.fetch(g.b, k0, kc, vb[d]);
+      la.fetch(g.a, k0, kc, va[slot]);
+      lb.fetch(g.b, k0, kc, vb[slot]);
     }
   }
   const int w = t / 64, lane = t % 64;
@@ -1591,21 +1608,21 @@ __device__ __forceinline__ void product_sum_mfma(const ProductArgs &g, uint32_t 
   const int q = lane / 16;
   for (uint32_t s0 = 0; s0 < slabs; s0 += D) {
 #pragma unroll
-    for (int d = 0; d < D; ++d) {
-      const uint32_t s = s0 + d;
+    for (int slot = 0; slot < D; ++slot) {
+      const uint32_t s = s0 + slot;
       if (s >= slabs) break;  // block-uniform
       const uint32_t k0 = kb + s * kSlab;
       const uint32_t kc = k0 < ke ? min(ke - k0, static_cast<uint32_t>(kSlab)) : 0;
       if (kc > 0) {
-        la.stage(va[d], as);
-        lb.stage(vb[d], bs);
+        la.stage(va[slot], as);
+        lb.stage(vb[slot], bs);
       }
       __syncthreads();
       const uint32_t k1 = k0 + D * kSlab;
       if (k1 < ke) {
         const uint32_t kc1 = min(ke - k1, static_cast<uint32_t>(kSlab));
-        la.fetch(g.a, k1, kc1, va[d]);
-        lb.fetch(g.b, k1, kc1, vb[d]);
+        la.fetch(g.a, k1, kc1, va[slot]);
+        lb.fetch(g.b, k1, kc1, vb[slot]);
       }
       for (uint32_t kk = 0; kk < kc; kk += 16) {
         float4 a = *reinterpret_cast<const float4 *>(&as[ia][kk + 4 * q]);
@@ -1640,7 +1657,7 @@ __device__ __forceinline__ void product_sum_mfma(const ProductArgs &g, uint32_t 
 // accesses and issues four MFMAs, the c-th with component c (k + 4p + c).  k at or past the
 // slab's count are zeroed in both operands.  acc[i] of lane 4 b + j: phase p's sum for output
 // (4 (d / 2) + i, 4 (d % 2) + j) of the tile.
-template <bool AKFast, bool BKFast>
+template <bool AKFast, bool BKFast, int D = 1>
 __device__ __forceinline__ void product_sum_mfma8(const ProductArgs &g, uint32_t m0, uint32_t n0,
                                                   uint32_t kb, uint32_t ke, uint32_t slabs,
                                                   int t, f32x4_t &acc,
@@ -1651,44 +1668,55 @@ __device__ __forceinline__ void product_sum_mfma8(const ProductArgs &g, uint32_t
   static_assert(kSlab % 16 == 0 && kSlab + 4 <= ProductRow<8, 64>::value, "mfma slab");
   const SlabLoader<8, 64, AKFast> la(g.a, m0, g.M, t);
   const SlabLoader<8, 64, BKFast> lb(g.b, n0, g.N, t);
-  float va[kLoads], vb[kLoads];
-  if (kb < ke) {
-    const uint32_t kc = min(ke - kb, static_cast<uint32_t>(kSlab));
-    la.fetch(g.a, kb, kc, va);
-    lb.fetch(g.b, kb, kc, vb);
+  // a ring of D register slabs: slab s is staged from set s % D, whose loads were issued D
+  // slabs earlier
+  float va[D][kLoads], vb[D][kLoads];
+#pragma unroll
+  for (int slot = 0; slot < D; ++slot) {
+    const uint32_t k0 = kb + slot * kSlab;
+    if (k0 < ke) {
+      const uint32_t kc = min(ke - k0, static_cast<uint32_t>(kSlab));
+      la.fetch(g.a, k0, kc, va[slot]);
+      lb.fetch(g.b, k0, kc, vb[slot]);
+    }
   }
   const int d = t / 16, p = (t / 4) % 4, i = t % 4;
   const int ra = 4 * (d / 2) + i, rb = 4 * (d % 2) + i;
-  for (uint32_t s = 0; s < slabs; ++s) {
-    const uint32_t k0 = kb + s * kSlab;
-    const uint32_t kc = k0 < ke ? min(ke - k0, static_cast<uint32_t>(kSlab)) : 0;
-    if (kc > 0) {
-      la.stage(va, as);
-      lb.stage(vb, bs);
-    }
-    __syncthreads();
-    const uint32_t k1 = k0 + kSlab;
-    if (k1 < ke) {
-      const uint32_t kc1 = min(ke - k1, static_cast<uint32_t>(kSlab));
-      la.fetch(g.a, k1, kc1, va);
-      lb.fetch(g.b, k1, kc1, vb);
-    }
-    for (uint32_t kk = 0; kk < kc; kk += 16) {
-      float4 a = *reinterpret_cast<const float4 *>(&as[ra][kk + 4 * p]);
-      float4 b = *reinterpret_cast<const float4 *>(&bs[rb][kk + 4 * p]);
-      if (kk + 16 > kc) {
-        const uint32_t k = kk + 4 * static_cast<uint32_t>(p);
-        if (k >= kc) a.x = b.x = 0.0f;
-        if (k + 1 >= kc) a.y = b.y = 0.0f;
-        if (k + 2 >= kc) a.z = b.z = 0.0f;
-        if (k + 3 >= kc) a.w = b.w = 0.0f;
+  for (uint32_t s0 = 0; s0 < slabs; s0 += D) {
+#pragma unroll
+    for (int slot = 0; slot < D; ++slot) {
+      const uint32_t s = s0 + slot;
+      if (s >= slabs) break;  // block-uniform
+      const uint32_t k0 = kb + s * kSlab;
+      const uint32_t kc = k0 < ke ? min(ke - k0, static_cast<uint32_t>(kSlab)) : 0;
+      if (kc > 0) {
+        la.stage(va[slot], as);
+        lb.stage(vb[slot], bs);
       }
-      acc = __builtin_amdgcn_mfma_f32_4x4x1f32(a.x, b.x, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_4x4x1f32(a.y, b.y, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_4x4x1f32(a.z, b.z, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_4x4x1f32(a.w, b.w, acc, 0, 0, 0);
+      __syncthreads();
+      const uint32_t k1 = k0 + D * kSlab;
+      if (k1 < ke) {
+        const uint32_t kc1 = min(ke - k1, static_cast<uint32_t>(kSlab));
+        la.fetch(g.a, k1, kc1, va[slot]);
+        lb.fetch(g.b, k1, kc1, vb[slot]);
+      }
+      for (uint32_t kk = 0; kk < kc; kk += 16) {
+        float4 a = *reinterpret_cast<const float4 *>(&as[ra][kk + 4 * p]);
+        float4 b = *reinterpret_cast<const float4 *>(&bs[rb][kk + 4 * p]);
+        if (kk + 16 > kc) {
+          const uint32_t k = kk + 4 * static_cast<uint32_t>(p);
+          if (k >= kc) a.x = b.x = 0.0f;
+          if (k + 1 >= kc) a.y = b.y = 0.0f;
+          if (k + 2 >= kc) a.z = b.z = 0.0f;
+          if (k + 3 >= kc) a.w = b.w = 0.0f;
+        }
+        acc = __builtin_amdgcn_mfma_f32_4x4x1f32(a.x, b.x, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_4x4x1f32(a.y, b.y, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_4x4x1f32(a.z, b.z, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_4x4x1f32(a.w, b.w, acc, 0, 0, 0);
+      }
+      __syncthreads();
     }
-    __syncthreads();
   }
 }
 
@@ -1757,7 +1785,8 @@ __device__ __forceinline__ void product_tile(const ProductArgs &g, uint32_t bx, 
                         : 0.0f;
     }
   const uint32_t slabs = kb < ke ? (ke - kb + S::kSlab - 1) / S::kSlab : 0;
-  product_sum<Tile, Threads, AKFast, BKFast, Fma>(g, m0, n0, kb, ke, slabs, t, acc, as, bs);
+  product_sum<Tile, Threads, AKFast, BKFast, Fma, OXH_RING_SERIAL>(g, m0, n0, kb, ke, slabs, t,
+                                                                   acc, as, bs);
 #pragma unroll
   for (int i = 0; i < kMicro; ++i)
 #pragma unroll
@@ -1806,7 +1835,8 @@ __device__ __forceinline__ void split_tile(const ProductArgs &g, uint32_t bx, ui
                             ? g.addend[axis_offset(g.cm, m) + axis_offset(g.cn, n)]
                             : 0.0f;
     f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    product_sum_mfma8<AKFast, BKFast>(g, m0, n0, wb, we, slabs, t, acc, lds.as[w], lds.bs[w]);
+    product_sum_mfma8<AKFast, BKFast, OXH_RING8>(g, m0, n0, wb, we, slabs, t, acc, lds.as[w],
+                                                 lds.bs[w]);
     // the four k phases of a quadrant (lanes 16 d + 4 p + j, p = 0 .. 3), added as
     // (p0 + p1) + (p2 + p3); lanes of phase 0 then hold the wave's part of the quadrant
 #pragma unroll
