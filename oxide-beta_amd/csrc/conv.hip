@@ -801,6 +801,141 @@ __global__ __launch_bounds__(256) void conv2d_input_backward_s2_kernel(
   }
 }
 
+// The stride-2 input gradient of an ungrouped K x K convolution on the matrix cores.  Input
+// position (iy, ix) of phase (py, px) = ((iy + pad) & 1, (ix + pad) & 1) receives the taps
+// ky = py, py + 2, ... < K (kx likewise) from output (oy, ox) = ((iy + pad - ky) / 2,
+// (ix + pad - kx) / 2): per image and phase an implicit GEMM of the phase's positions by the
+// input channels over k = (tap, output channel), a tolerance-bar sum (the MFMA's fused
+// roundings) in place of the phase-blocked kernel's serial one.  Block (16-channel input tile,
+// image) stages the image's output gradient channel-innermost around a zero halo,
+// gl[((oy + lo_y) * owp + ox + lo_x) * ocs + oc] (zero past out_c), and the tile's weights as
+// wl[(t * ocp + oc) * 16 + icl] (zero past the channels); jobs (phase, 16-position tile) go to
+// the waves in turn.  Per tap and step of 4 output channels, v_mfma_f32_16x16x4_f32 with lane
+// (i, q) supplying A[i][q] = the gradient of channel oc + q at position 16 mt + i's output for
+// the tap (positions past the phase read position 0 and are not stored) and B[q][i] =
+// W[oc + q][ic0 + i][t]; D[4 q + r][i] is the input gradient of channel ic0 + i at phase
+// position 16 mt + 4 q + r, stored plus the addend.
+struct MfmaIg {
+  uint32_t lo_y, lo_x, ohp, owp, ocs, ocp;
+};
+
+template <int K>
+__global__ __launch_bounds__(256) void conv2d_input_backward_mfma_kernel(
+    ConvGeom g, MfmaIg f, const float *__restrict__ grad, const float *__restrict__ wt,
+    const float *addend, float *dx) {
+  extern __shared__ float lds[];
+  constexpr int T = K * K;
+  const oxh::BlockTile bt = oxh::xcd_block();
+  const uint32_t n = bt.y, ic0 = bt.x * 16;
+  const uint32_t ocp = f.ocp, ocs = f.ocs, oplane = g.oh * g.ow;
+  const uint32_t gcount = f.ohp * f.owp * ocs;  // a multiple of 4
+  float *gl = lds, *wl = lds + gcount;
+  {  // the gradient's halo and channels past out_c are zero
+    float4 *l4 = reinterpret_cast<float4 *>(gl);
+    const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (uint32_t i = threadIdx.x; i < gcount / 4; i += blockDim.x) l4[i] = z;
+  }
+  __syncthreads();
+  const oxh::FastDiv oplane_div = oxh::make_fastdiv(oplane);
+  stage(gl, grad + static_cast<uint64_t>(n) * g.out_c * oplane, g.out_c * oplane, same_index,
+        [&](uint32_t e) {
+          const uint32_t oc = fdiv(e, oplane_div), opos = e - oc * oplane;
+          const uint32_t oy = fdiv(opos, g.ow_div), ox = opos - oy * g.ow;
+          return ((oy + f.lo_y) * f.owp + ox + f.lo_x) * ocs + oc;
+        });
+  // weights: element e = (oc * T + t) * 4 + quad, four input channels per 128-bit store
+  const uint32_t wtotal = ocp * T * 4, crow = g.in_c * T;
+  constexpr int UW = 8;
+  for (uint32_t b0 = threadIdx.x; b0 < wtotal; b0 += blockDim.x * UW) {
+    float v[UW][4];
+#pragma unroll
+    for (int u = 0; u < UW; ++u) {
+      const uint32_t e = b0 + u * blockDim.x, ec = e < wtotal ? e : 0;
+      const uint32_t rest = ec / 4, quad = ec - rest * 4, oc = rest / T, t = rest - oc * T;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const uint32_t ic = ic0 + 4 * quad + c;
+        const bool ok = oc < g.out_c && ic < g.in_c;
+        v[u][c] = tap_operand(wt[ok ? oc * crow + ic * T + t : 0], tap_mask(ok));
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < UW; ++u) {
+      const uint32_t e = b0 + u * blockDim.x;
+      if (e < wtotal) {
+        const uint32_t rest = e / 4, quad = e - rest * 4, oc = rest / T, t = rest - oc * T;
+        *reinterpret_cast<float4 *>(wl + (t * ocp + oc) * 16 + 4 * quad) =
+            make_float4(v[u][0], v[u][1], v[u][2], v[u][3]);
+      }
+    }
+  }
+  __syncthreads();
+  // phases p = 2 py + px: first position (iy0, ix0), extent na x nb, 16-position tiles
+  uint32_t na[2], nb[2], tiles[4], first[5];
+#pragma unroll
+  for (int ph = 0; ph < 2; ++ph) {
+    const uint32_t iy0 = (ph + g.pad) & 1u;
+    na[ph] = g.h > iy0 ? (g.h - iy0 + 1) / 2 : 0;
+    nb[ph] = g.w > iy0 ? (g.w - iy0 + 1) / 2 : 0;
+  }
+  first[0] = 0;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    tiles[p] = (na[p >> 1] * nb[p & 1] + 15) / 16;
+    first[p + 1] = first[p] + tiles[p];
+  }
+  const uint32_t lane = threadIdx.x % 64, i = lane % 16, q = lane / 16;
+  const uint32_t waves = blockDim.x / 64, steps = ocp / 4;
+  for (uint32_t job = threadIdx.x / 64; job < first[4]; job += waves) {
+    uint32_t p = 0;
+#pragma unroll
+    for (int u = 1; u < 4; ++u) p += job >= first[u] ? 1u : 0u;
+    const uint32_t py = p >> 1, px = p & 1, mt = job - first[p];
+    const uint32_t iy0 = (py + g.pad) & 1u, ix0 = (px + g.pad) & 1u;
+    const uint32_t mcount = na[py] * nb[px];
+    const uint32_t m = mt * 16 + i, mc = m < mcount ? m : 0;
+    const uint32_t a = mc / nb[px], b = mc - a * nb[px];
+    f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t ky = py; ky < static_cast<uint32_t>(K); ky += 2) {
+      // oy = (iy0 + pad - ky) / 2 + a, exact (same parity); lo_y keeps the row inside the halo
+      const uint32_t row = static_cast<uint32_t>(
+          (static_cast<int>(iy0 + g.pad) - static_cast<int>(ky)) / 2 + static_cast<int>(a + f.lo_y));
+      for (uint32_t kx = px; kx < static_cast<uint32_t>(K); kx += 2) {
+        const uint32_t col = static_cast<uint32_t>(
+            (static_cast<int>(ix0 + g.pad) - static_cast<int>(kx)) / 2 + static_cast<int>(b + f.lo_x));
+        const float *ap = gl + (row * f.owp + col) * ocs + q;
+        const float *bp = wl + ((ky * K + kx) * ocp + q) * 16 + i;
+        uint32_t s = 0;
+        for (; s + 4 <= steps; s += 4) {  // four steps' operands read, then their MFMAs
+          float av[4], bv[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            av[u] = ap[4 * (s + u)];
+            bv[u] = bp[64 * (s + u)];
+          }
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u], bv[u], acc, 0, 0, 0);
+        }
+        for (; s < steps; ++s)
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ap[4 * s], bp[64 * s], acc, 0, 0, 0);
+      }
+    }
+    const uint32_t ic = ic0 + i;
+    if (ic < g.in_c) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const uint32_t mo = mt * 16 + 4 * q + r;
+        if (mo >= mcount) continue;
+        const uint32_t ao = mo / nb[px], bo = mo - ao * nb[px];
+        const uint32_t iy = iy0 + 2 * ao, ix = ix0 + 2 * bo;
+        const uint64_t o = ((static_cast<uint64_t>(n) * g.in_c + ic) * g.h + iy) * g.w + ix;
+        dx[o] = addend != nullptr ? acc[r] + addend[o] : acc[r];
+      }
+    }
+  }
+}
+
 // The weight gradient of an ungrouped K x K convolution on the matrix cores:
 // dW[oc][ic][t] = sum over images n and output positions p of G[n][oc][p] *
 // X[n][ic][iy(p, t)][ix(p, t)], a GEMM of M = out_c rows, N = in_c * K * K columns (ic, t) and
@@ -2269,6 +2404,46 @@ MfmaForwardPlan forward_mfma_plan(const ConvGeom &g) {
   return p;
 }
 
+// The matrix-core stride-2 input gradient: ungrouped K x K convolutions whose halo-padded
+// output gradient and 16-channel weight tile fit the LDS budget.  The halo (lo, the padded
+// extents) covers every output position any tap of any input position reads, found by
+// enumerating them.  lds_bytes == 0: not taken.
+#ifndef OXH_IG_MFMA
+#define OXH_IG_MFMA 1  // 0: stride-2 input gradients keep the serial phase-blocked kernel
+#endif
+struct MfmaIgPlan {
+  MfmaIg f{};
+  uint32_t tiles = 0, lds_bytes = 0;
+};
+MfmaIgPlan input_backward_mfma_plan(const ConvGeom &g) {
+  MfmaIgPlan p;
+  if (!OXH_IG_MFMA || !lds_eligible(g) || g.stride != 2) return p;
+  const int K = static_cast<int>(g.kh), pad = static_cast<int>(g.pad);
+  auto extent = [&](uint32_t size, uint32_t out, uint32_t &lo, uint32_t &padded) {
+    int mn = 0, mx = static_cast<int>(out) - 1;
+    for (int i = 0; i < static_cast<int>(size); ++i)
+      for (int k = 0; k < K; ++k)
+        if (((i + pad - k) & 1) == 0) {
+          const int o = (i + pad - k) / 2;
+          mn = o < mn ? o : mn;
+          mx = o > mx ? o : mx;
+        }
+    lo = static_cast<uint32_t>(-mn);
+    padded = static_cast<uint32_t>(mx - mn + 1);
+  };
+  MfmaIg &f = p.f;
+  extent(g.h, g.oh, f.lo_y, f.ohp);
+  extent(g.w, g.ow, f.lo_x, f.owp);
+  f.ocp = round4(g.out_c);
+  f.ocs = (f.ocp / 4) % 2 == 0 ? f.ocp + 4 : f.ocp;
+  const uint64_t floats = static_cast<uint64_t>(f.ohp) * f.owp * f.ocs +
+                          static_cast<uint64_t>(g.kh) * g.kw * f.ocp * 16;
+  if (floats > kLdsFloats) return p;
+  p.tiles = (g.in_c + 15) / 16;
+  p.lds_bytes = static_cast<uint32_t>(floats * 4);
+  return p;
+}
+
 LdsPlan input_backward_lds_plan(const ConvGeom &g) {
   if (!lds_eligible(g)) return LdsPlan{};
   const uint64_t taps = g.kh * g.kw;
@@ -2818,6 +2993,17 @@ oxh_status input_backward_impl(const char *name, oxh_stream stream,
     const ProductArgs x = input_product(g, gradient, weight, addend, input_gradient);
     return launch_product(name, s, x, 1, input_splits(x) != 0);
   }
+  const MfmaIgPlan mp = input_backward_mfma_plan(g);
+  if (mp.lds_bytes > 0) {
+    const dim3 mgrid(mp.tiles, g.batch), mblock(256);
+    if (g.kh == 3)
+      oxh::launch(conv2d_input_backward_mfma_kernel<3>, mgrid, mblock, mp.lds_bytes, s, g, mp.f,
+                  gradient, weight, addend, input_gradient);
+    else
+      oxh::launch(conv2d_input_backward_mfma_kernel<5>, mgrid, mblock, mp.lds_bytes, s, g, mp.f,
+                  gradient, weight, addend, input_gradient);
+    return oxh::launched(name);
+  }
   const PhasePlan pp = input_backward_s2_plan(g);
   if (pp.lds_bytes > 0) {
     const dim3 pgrid(pp.tiles, g.batch), pblock(pp.threads);
@@ -2982,7 +3168,7 @@ oxh_status oxh_conv2d_output_size(const oxh_conv2d_shape *shape, uint64_t *out_h
 int oxh_conv2d_input_backward_serial(const oxh_conv2d_shape *shape) {
   ConvGeom g;
   if (make_conv_geom("oxh_conv2d_input_backward_serial", shape, g) != OXH_OK) return -1;
-  if (!pointwise(g)) return 1;
+  if (!pointwise(g)) return input_backward_mfma_plan(g).lds_bytes > 0 ? 0 : 1;
   return input_splits(input_product(g, nullptr, nullptr, nullptr, nullptr)) != 0 ? 0 : 1;
 }
 

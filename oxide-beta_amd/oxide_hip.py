@@ -423,7 +423,8 @@ def conv2d_output_size(shape: Conv2dShape) -> tuple[int, int]:
 
 def conv2d_forward_serial(shape: Conv2dShape) -> bool:
     """True when oxh_conv2d_forward sums each output in the CPU path's order (bit-identical),
-    False when in four ordered parts over the input channels."""
+    False when in another fixed order (four ordered parts over the input channels, or
+    matrix-core sums) within 1e-5 * sum|terms| of it."""
     v = lib().oxh_conv2d_forward_serial(ctypes.byref(shape))
     if v < 0:
         raise OxideError(INVALID_SHAPE, "invalid conv2d shape")
@@ -432,7 +433,8 @@ def conv2d_forward_serial(shape: Conv2dShape) -> bool:
 
 def conv2d_input_backward_serial(shape: Conv2dShape) -> bool:
     """True when the input gradient sums each value in the CPU path's order (bit-identical),
-    False when in four ordered parts over the output channels."""
+    False when in another fixed order (four ordered parts over the output channels, or
+    matrix-core sums) within 1e-5 * sum|terms| of it."""
     v = lib().oxh_conv2d_input_backward_serial(ctypes.byref(shape))
     if v < 0:
         raise OxideError(INVALID_SHAPE, "invalid conv2d shape")

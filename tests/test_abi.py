@@ -283,8 +283,9 @@ def test_conv_forward_order_query():
 def test_conv_input_gradient_order_query():
     """oxh_conv2d_input_backward_serial: a pointwise input gradient over at least 256 output
     channels on a grid that leaves the chip waiting on its serial chains (the MNIST
-    MobileNetV4's head, its 1x1-plane expands and the 960-channel conv) sums four ordered parts;
-    short channel sums, large grids and the K x K kernels stay serial."""
+    MobileNetV4's head, its 1x1-plane expands and the 960-channel conv) sums four ordered parts,
+    and a stride-2 K x K one (the fused blocks') sums on the matrix cores; short channel sums,
+    large grids, stride-1 and grouped K x K kernels stay serial."""
     sh = ox.conv2d_shape
     assert not ox.conv2d_input_backward_serial(sh(128, 960, 1, 1, 1280, 1, 1, 0, 1))  # head
     assert not ox.conv2d_input_backward_serial(sh(128, 128, 1, 1, 960, 1, 1, 0, 1))
@@ -292,7 +293,9 @@ def test_conv_input_gradient_order_query():
     assert ox.conv2d_input_backward_serial(sh(128, 512, 1, 1, 128, 1, 1, 0, 1))       # project
     assert ox.conv2d_input_backward_serial(sh(128, 1280, 1, 1, 10, 1, 1, 0, 1))       # classifier
     assert ox.conv2d_input_backward_serial(sh(128, 64, 8, 8, 256, 1, 1, 0, 1))        # large grid
-    assert ox.conv2d_input_backward_serial(sh(128, 32, 7, 7, 96, 3, 2, 1, 1))         # K x K
+    assert not ox.conv2d_input_backward_serial(sh(128, 32, 7, 7, 96, 3, 2, 1, 1))     # stride 2
+    assert ox.conv2d_input_backward_serial(sh(2, 18, 6, 6, 20, 3, 1, 1, 1))           # stride 1
+    assert ox.conv2d_input_backward_serial(sh(2, 8, 5, 5, 8, 3, 2, 1, 8))             # grouped
     with pytest.raises(ox.OxideError):
         ox.conv2d_input_backward_serial(sh(1, 1, 1, 1, 1, 3, 1, 0, 1))
 
