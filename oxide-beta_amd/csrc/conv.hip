@@ -820,13 +820,12 @@ struct MfmaIg {
 };
 
 template <int K>
-__global__ __launch_bounds__(256) void conv2d_input_backward_mfma_kernel(
-    ConvGeom g, MfmaIg f, const float *__restrict__ grad, const float *__restrict__ wt,
-    const float *addend, float *dx) {
-  extern __shared__ float lds[];
+__device__ __forceinline__ void input_backward_mfma_block(
+    const ConvGeom &g, const MfmaIg &f, uint32_t tile, uint32_t n, float *lds,
+    const float *__restrict__ grad, const float *__restrict__ wt, const float *addend,
+    float *dx) {
   constexpr int T = K * K;
-  const oxh::BlockTile bt = oxh::xcd_block();
-  const uint32_t n = bt.y, ic0 = bt.x * 16;
+  const uint32_t ic0 = tile * 16;
   const uint32_t ocp = f.ocp, ocs = f.ocs, oplane = g.oh * g.ow;
   const uint32_t gcount = f.ohp * f.owp * ocs;  // a multiple of 4
   float *gl = lds, *wl = lds + gcount;
@@ -936,6 +935,15 @@ __global__ __launch_bounds__(256) void conv2d_input_backward_mfma_kernel(
   }
 }
 
+template <int K>
+__global__ __launch_bounds__(256) void conv2d_input_backward_mfma_kernel(
+    ConvGeom g, MfmaIg f, const float *__restrict__ grad, const float *__restrict__ wt,
+    const float *addend, float *dx) {
+  extern __shared__ float lds[];
+  const oxh::BlockTile bt = oxh::xcd_block();
+  input_backward_mfma_block<K>(g, f, bt.x, bt.y, lds, grad, wt, addend, dx);
+}
+
 // The weight gradient of an ungrouped K x K convolution on the matrix cores:
 // dW[oc][ic][t] = sum over images n and output positions p of G[n][oc][p] *
 // X[n][ic][iy(p, t)][ix(p, t)], a GEMM of M = out_c rows, N = in_c * K * K columns (ic, t) and
@@ -957,12 +965,13 @@ struct MfmaWeight {
 };
 
 template <int K, int S, int NG>
-__global__ __launch_bounds__(256) void conv2d_weight_mfma_kernel(
-    ConvGeom g, MfmaWeight f, const float *__restrict__ grad, const float *__restrict__ x,
-    float *__restrict__ out) {
-  extern __shared__ float lds[];
+__device__ __forceinline__ void weight_mfma_block(const ConvGeom &g, const MfmaWeight &f,
+                                                  uint32_t group, uint32_t chunk, float *lds,
+                                                  const float *__restrict__ grad,
+                                                  const float *__restrict__ x,
+                                                  float *__restrict__ out) {
   constexpr int T = K * K;
-  const uint32_t chunk = blockIdx.y, n0 = chunk * f.ipc;
+  const uint32_t n0 = chunk * f.ipc;
   const uint32_t imgs = min(f.ipc, g.batch - n0);
   const uint32_t C = g.in_c, M = g.out_c, plane = g.h * g.w, P = g.oh * g.ow;
   const uint32_t xcount = round4(f.ipc * C * f.cs), gcount = f.mtiles * 16 * f.kpad;
@@ -1024,7 +1033,7 @@ __global__ __launch_bounds__(256) void conv2d_weight_mfma_kernel(
     }
   }
   __syncthreads();
-  const uint32_t job = blockIdx.x * 4 + threadIdx.x / 64;
+  const uint32_t job = group * 4 + threadIdx.x / 64;
   if (job >= f.jobs) return;  // no barrier follows
   const uint32_t lane = threadIdx.x % 64, i = lane % 16, q = lane / 16;
   const uint32_t mt = job / f.ngroups, nt0 = (job - mt * f.ngroups) * f.ng;
@@ -1085,6 +1094,37 @@ __global__ __launch_bounds__(256) void conv2d_weight_mfma_kernel(
       const uint32_t oc = mt * 16 + 4 * q + r;
       if (oc < M) oc_out[oc * cols + col] = acc[u][r];
     }
+  }
+}
+
+template <int K, int S, int NG>
+__global__ __launch_bounds__(256) void conv2d_weight_mfma_kernel(
+    ConvGeom g, MfmaWeight f, const float *__restrict__ grad, const float *__restrict__ x,
+    float *__restrict__ out) {
+  extern __shared__ float lds[];
+  weight_mfma_block<K, S, NG>(g, f, blockIdx.x, blockIdx.y, lds, grad, x, out);
+}
+
+// A stride-2 K x K convolution's input gradient (blocks [0, ig_blocks): tile, image) and weight
+// gradient partials (the rest: job group, chunk) on the matrix cores in one launch, each block
+// computing exactly what its own kernel's block computes; each part's blocks remapped over the
+// XCDs on their own.
+struct MfmaDual {
+  uint32_t ig_tiles, ig_blocks, wg_groups, wg_blocks;
+};
+template <int K, int NG>
+__global__ __launch_bounds__(256) void conv2d_backward_mfma_kernel(
+    ConvGeom g, MfmaIg fi, MfmaWeight fw, MfmaDual d, const float *__restrict__ grad,
+    const float *__restrict__ wt, const float *__restrict__ x, const float *addend, float *dx,
+    float *__restrict__ out) {
+  extern __shared__ float lds[];
+  const uint32_t b = blockIdx.x;
+  if (b < d.ig_blocks) {
+    const uint32_t r = oxh::xcd_contiguous(b, d.ig_blocks);
+    input_backward_mfma_block<K>(g, fi, r % d.ig_tiles, r / d.ig_tiles, lds, grad, wt, addend, dx);
+  } else {
+    const uint32_t r = oxh::xcd_contiguous(b - d.ig_blocks, d.wg_blocks, d.ig_blocks);
+    weight_mfma_block<K, 2, NG>(g, fw, r % d.wg_groups, r / d.wg_groups, lds, grad, x, out);
   }
 }
 
@@ -3373,6 +3413,47 @@ oxh_status oxh_conv2d_backward(oxh_stream stream, const oxh_conv2d_shape *shape,
       const uint32_t count = g.out_c * g.in_c;
       launch_sum_chunks(s, count, split.chunks, partial, weight_gradient);
       return oxh::launched(name);
+    }
+  }
+  // a stride-2 K x K convolution whose two gradients both take the matrix-core kernels: one
+  // launch (then the chunk sums and the bias launch)
+  if (!pointwise(g) && input_gradient != nullptr && oxh::aligned16(gradient) &&
+      oxh::aligned16(input)) {
+    const MfmaIgPlan ip = input_backward_mfma_plan(g);
+    const MfmaWeightPlan wp = ip.lds_bytes > 0 ? weight_mfma_plan(g) : MfmaWeightPlan{};
+    if (ip.lds_bytes > 0 && wp.lds_bytes > 0) {
+      float *partial = static_cast<float *>(workspace);
+      float *out = wp.chunks > 1 ? partial : weight_gradient;
+      const MfmaDual d{ip.tiles, ip.tiles * g.batch, wp.blocks, wp.blocks * wp.chunks};
+      const uint32_t lds_bytes = ip.lds_bytes > wp.lds_bytes ? ip.lds_bytes : wp.lds_bytes;
+      const dim3 grid(d.ig_blocks + d.wg_blocks), block(256);
+#define OXH_KK_DUAL(KK)                                                                     \
+  do {                                                                                      \
+    if (wp.f.ng == 9)                                                                       \
+      oxh::launch(conv2d_backward_mfma_kernel<KK, 9>, grid, block, lds_bytes, s, g, ip.f,    \
+                  wp.f, d, gradient, weight, input, addend, input_gradient, out);           \
+    else if (wp.f.ng == 6)                                                                  \
+      oxh::launch(conv2d_backward_mfma_kernel<KK, 6>, grid, block, lds_bytes, s, g, ip.f,    \
+                  wp.f, d, gradient, weight, input, addend, input_gradient, out);           \
+    else                                                                                    \
+      oxh::launch(conv2d_backward_mfma_kernel<KK, 3>, grid, block, lds_bytes, s, g, ip.f,    \
+                  wp.f, d, gradient, weight, input, addend, input_gradient, out);           \
+  } while (0)
+      if (g.kh == 3)
+        OXH_KK_DUAL(3);
+      else
+        OXH_KK_DUAL(5);
+#undef OXH_KK_DUAL
+      st = oxh::launched(name);
+      if (st != OXH_OK) return st;
+      if (wp.chunks > 1) {
+        launch_sum_chunks(s, static_cast<uint32_t>(weight_elems(g)), wp.chunks, partial,
+                          weight_gradient);
+        st = oxh::launched(name);
+        if (st != OXH_OK) return st;
+      }
+      if (bias_gradient == nullptr) return oxh::ok();
+      return oxh_conv2d_bias_backward(stream, shape, gradient, bias_gradient, nullptr, 0);
     }
   }
   // parameter gradients only: the bias sums ride in the weight gradient's launches where its
