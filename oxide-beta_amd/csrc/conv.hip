@@ -961,6 +961,9 @@ __global__ __launch_bounds__(256) void conv2d_input_backward_mfma_kernel(
 // out_c * oh * ow multiples of 4.
 struct MfmaWeight {
   uint32_t hp, wp, cs, ipc, kpad, mtiles, ntiles, ng, ngroups, jobs;
+  uint32_t bias;    // 1: column in_c * K * K is the bias gradient (operand 1)
+  uint32_t stride;  // floats per chunk: the weights, then (bias) out_c bias sums
+  uint32_t kparts;  // > 1 (jobs <= 2): the block's waves split each job's k steps
   oxh::FastDiv plane_div, oplane_div, m_div;
 };
 
@@ -969,7 +972,8 @@ __device__ __forceinline__ void weight_mfma_block(const ConvGeom &g, const MfmaW
                                                   uint32_t group, uint32_t chunk, float *lds,
                                                   const float *__restrict__ grad,
                                                   const float *__restrict__ x,
-                                                  float *__restrict__ out) {
+                                                  float *__restrict__ out_w,
+                                                  float *__restrict__ out_b) {
   constexpr int T = K * K;
   const uint32_t n0 = chunk * f.ipc;
   const uint32_t imgs = min(f.ipc, g.batch - n0);
@@ -1033,25 +1037,34 @@ __device__ __forceinline__ void weight_mfma_block(const ConvGeom &g, const MfmaW
     }
   }
   __syncthreads();
-  const uint32_t job = group * 4 + threadIdx.x / 64;
-  if (job >= f.jobs) return;  // no barrier follows
+  // wave w: job w % jobs of the group's four (or, with kparts parts, of the chunk's jobs),
+  // steps part w / jobs
+  const uint32_t w = threadIdx.x / 64;
+  const uint32_t job = f.kparts > 1 ? w % f.jobs : group * 4 + w;
+  const uint32_t kp = f.kparts > 1 ? w / f.jobs : 0;
+  if (job >= f.jobs || kp >= f.kparts) return;  // no barrier follows (kparts 1)
   const uint32_t lane = threadIdx.x % 64, i = lane % 16, q = lane / 16;
   const uint32_t mt = job / f.ngroups, nt0 = (job - mt * f.ngroups) * f.ng;
   const uint32_t cols = C * T;
-  // NG N tiles per job (tiles past the last one read in-range values and are not stored)
-  uint32_t boff[NG];
+  // NG N tiles per job (tiles past the last one read in-range values and are not stored); the
+  // bias column's operand is 1 (the loaded value's bits replaced)
+  uint32_t boff[NG], keep[NG], one[NG];
 #pragma unroll
   for (int u = 0; u < NG; ++u) {
     const uint32_t col = (nt0 + u) * 16 + i;
     const uint32_t ic = col / T, t = col - ic * T;
     boff[u] = col < cols ? ic * f.cs + (t / K) * f.wp + (t % K) : 0;
+    const bool bias_col = f.bias != 0 && col == cols;
+    keep[u] = bias_col ? 0u : 0xFFFFFFFFu;
+    one[u] = bias_col ? 0x3F800000u : 0u;
   }
   f32x4_t acc[NG];
 #pragma unroll
   for (int u = 0; u < NG; ++u) acc[u] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   // per step of 4 k: lane k = 4 s + q's image offset formed in registers
   const float *ga = gl + (mt * 16 + i) * f.kpad + q;
-  const uint32_t steps = f.kpad / 4, kc = imgs * P;
+  const uint32_t kc = imgs * P, per = (f.kpad / 4 + f.kparts - 1) / f.kparts;
+  const uint32_t s0 = min(kp * per, f.kpad / 4), s1 = min(s0 + per, f.kpad / 4);
   auto image_offset = [&](uint32_t k) {
     const uint32_t img = fdiv(k, f.oplane_div), p = k - img * P;
     const uint32_t oy = fdiv(p, g.ow_div), ox = p - oy * g.ow;
@@ -1063,7 +1076,8 @@ __device__ __forceinline__ void weight_mfma_block(const ConvGeom &g, const MfmaW
     av = ga[4 * st];
     const uint32_t base = image_offset(4 * st + q);
 #pragma unroll
-    for (int u = 0; u < NG; ++u) bv[u] = xl[base + boff[u]];
+    for (int u = 0; u < NG; ++u)
+      bv[u] = __uint_as_float((__float_as_uint(xl[base + boff[u]]) & keep[u]) | one[u]);
   };
   auto step = [&](float av, const float (&bv)[NG]) {
 #pragma unroll
@@ -1071,28 +1085,53 @@ __device__ __forceinline__ void weight_mfma_block(const ConvGeom &g, const MfmaW
       acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[u], acc[u], 0, 0, 0);
   };
   float a0, a1, b0[NG], b1[NG];
-  load(0, a0, b0);
-  uint32_t s4 = 0;
-  for (; s4 + 1 < steps; s4 += 2) {  // sched_barrier: the loads stay ahead of the MFMAs
-    load(s4 + 1, a1, b1);
-    __builtin_amdgcn_sched_barrier(0);
-    step(a0, b0);
-    __builtin_amdgcn_sched_barrier(0);
-    load(s4 + 2 < steps ? s4 + 2 : s4 + 1, a0, b0);
-    __builtin_amdgcn_sched_barrier(0);
-    step(a1, b1);
-    __builtin_amdgcn_sched_barrier(0);
+  if (s0 < s1) {
+    load(s0, a0, b0);
+    uint32_t s4 = s0;
+    for (; s4 + 1 < s1; s4 += 2) {  // sched_barrier: the loads stay ahead of the MFMAs
+      load(s4 + 1, a1, b1);
+      __builtin_amdgcn_sched_barrier(0);
+      step(a0, b0);
+      __builtin_amdgcn_sched_barrier(0);
+      load(s4 + 2 < s1 ? s4 + 2 : s4 + 1, a0, b0);
+      __builtin_amdgcn_sched_barrier(0);
+      step(a1, b1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (s4 < s1) step(a0, b0);
   }
-  if (s4 < steps) step(a0, b0);
-  float *oc_out = out + static_cast<uint64_t>(chunk) * M * cols;
+  if (f.kparts > 1) {  // the parts added in order by the part-0 waves (every wave is here)
+    float *red = gl + gcount;  // red[(((kp - 1) * jobs + job) * NG + u) * 256 + r * 64 + lane]
+    if (kp > 0) {
+#pragma unroll
+      for (int u = 0; u < NG; ++u)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          red[(((kp - 1) * f.jobs + job) * NG + u) * 256 + r * 64 + lane] = acc[u][r];
+    }
+    __syncthreads();
+    if (kp > 0) return;
+    for (uint32_t k = 1; k < f.kparts; ++k)
+#pragma unroll
+      for (int u = 0; u < NG; ++u)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          acc[u][r] += red[(((k - 1) * f.jobs + job) * NG + u) * 256 + r * 64 + lane];
+  }
+  float *ow = out_w + static_cast<uint64_t>(chunk) * f.stride;
+  float *ob = out_b + static_cast<uint64_t>(chunk) * f.stride;
 #pragma unroll
   for (int u = 0; u < NG; ++u) {
     const uint32_t col = (nt0 + u) * 16 + i;
-    if (col >= cols) continue;
+    if (col > cols || (col == cols && f.bias == 0)) continue;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const uint32_t oc = mt * 16 + 4 * q + r;
-      if (oc < M) oc_out[oc * cols + col] = acc[u][r];
+      if (oc >= M) continue;
+      if (col < cols)
+        ow[oc * cols + col] = acc[u][r];
+      else
+        ob[oc] = acc[u][r];
     }
   }
 }
@@ -1100,9 +1139,9 @@ __device__ __forceinline__ void weight_mfma_block(const ConvGeom &g, const MfmaW
 template <int K, int S, int NG>
 __global__ __launch_bounds__(256) void conv2d_weight_mfma_kernel(
     ConvGeom g, MfmaWeight f, const float *__restrict__ grad, const float *__restrict__ x,
-    float *__restrict__ out) {
+    float *__restrict__ out_w, float *__restrict__ out_b) {
   extern __shared__ float lds[];
-  weight_mfma_block<K, S, NG>(g, f, blockIdx.x, blockIdx.y, lds, grad, x, out);
+  weight_mfma_block<K, S, NG>(g, f, blockIdx.x, blockIdx.y, lds, grad, x, out_w, out_b);
 }
 
 // A stride-2 K x K convolution's input gradient (blocks [0, ig_blocks): tile, image) and weight
@@ -1124,7 +1163,8 @@ __global__ __launch_bounds__(256) void conv2d_backward_mfma_kernel(
     input_backward_mfma_block<K>(g, fi, r % d.ig_tiles, r / d.ig_tiles, lds, grad, wt, addend, dx);
   } else {
     const uint32_t r = oxh::xcd_contiguous(b - d.ig_blocks, d.wg_blocks, d.ig_blocks);
-    weight_mfma_block<K, 2, NG>(g, fw, r % d.wg_groups, r / d.wg_groups, lds, grad, x, out);
+    weight_mfma_block<K, 2, NG>(g, fw, r % d.wg_groups, r / d.wg_groups, lds, grad, x, out,
+                                out);
   }
 }
 
@@ -2573,9 +2613,9 @@ LdsPlan weight_lds_plan(const ConvGeom &g, bool bias = false) {
 
 // The matrix-core weight gradient: ungrouped K x K convolutions whose image and gradient runs
 // allow 16-byte loads (C * h * w and out_c * oh * ow multiples of 4) and whose chunk of ipc
-// images (at least 32 positions) holds at most 64 positions; N tiles per job for about
-// OXH_WGT_JOB_MFMA MFMAs per wave; the images, the gradient and nothing else in LDS.
-// lds_bytes == 0: not taken.
+// images (at least 32 positions) holds at most 256 positions; N tiles per job (1, 3, 6 or 9)
+// for about OXH_WGT_JOB_MFMA MFMAs per wave; the images, the gradient and nothing else in LDS.
+// bias: one more column, the bias gradient.  lds_bytes == 0: not taken.
 #ifndef OXH_WGT_MFMA
 #define OXH_WGT_MFMA 1  // 0: K x K weight gradients keep the LDS fused-multiply-add kernel
 #endif
@@ -2586,11 +2626,11 @@ struct MfmaWeightPlan {
   MfmaWeight f{};
   uint32_t chunks = 0, blocks = 0, lds_bytes = 0;
 };
-MfmaWeightPlan weight_mfma_plan(const ConvGeom &g) {
+MfmaWeightPlan weight_mfma_plan(const ConvGeom &g, bool bias = false) {
   MfmaWeightPlan p;
   const uint64_t plane = static_cast<uint64_t>(g.h) * g.w, P = static_cast<uint64_t>(g.oh) * g.ow;
   if (!OXH_WGT_MFMA || !lds_eligible(g) || (g.in_c * plane) % 4 != 0 || (g.out_c * P) % 4 != 0 ||
-      P > 64)
+      P > 256)
     return p;
   MfmaWeight &f = p.f;
   f.hp = (g.oh - 1) * g.stride + g.kh;
@@ -2600,24 +2640,29 @@ MfmaWeightPlan weight_mfma_plan(const ConvGeom &g) {
   if (ipc > g.batch) ipc = g.batch;
   f.ipc = static_cast<uint32_t>(ipc);
   f.kpad = static_cast<uint32_t>(round4(static_cast<uint32_t>(ipc * P)));
-  if (f.kpad > 64) return p;
+  if (f.kpad > 256) return p;
   const uint32_t steps = f.kpad / 4;
+  const uint32_t weights = g.in_c * g.kh * g.kw;
+  f.bias = bias ? 1u : 0u;
+  f.stride = static_cast<uint32_t>(weight_elems(g)) + (bias ? g.out_c : 0u);
   f.mtiles = (g.out_c + 15) / 16;
-  f.ntiles = (g.in_c * g.kh * g.kw + 15) / 16;
-  // N tiles per job: 3, 6 or 9 (the kernel's instantiations), about OXH_WGT_JOB_MFMA MFMAs
+  f.ntiles = (weights + f.bias + 15) / 16;
+  // N tiles per job: 1, 3, 6 or 9 (the kernel's instantiations), about OXH_WGT_JOB_MFMA MFMAs
   const uint32_t want = OXH_WGT_JOB_MFMA / steps;
-  f.ng = want >= 9 ? 9 : want >= 6 ? 6 : 3;
+  f.ng = f.ntiles == 1 ? 1 : want >= 9 ? 9 : want >= 6 ? 6 : 3;
   if (f.ng > 3 && (f.ntiles + 2) / 3 * 3 <= f.ng) f.ng = (f.ntiles + 2) / 3 * 3;  // small N
   f.ngroups = (f.ntiles + f.ng - 1) / f.ng;
   f.jobs = f.mtiles * f.ngroups;
+  f.kparts = f.jobs <= 2 ? 4 / f.jobs : 1;
   const uint64_t floats = round4(static_cast<uint32_t>(ipc * g.in_c * f.cs)) +
-                          static_cast<uint64_t>(f.mtiles) * 16 * f.kpad;
+                          static_cast<uint64_t>(f.mtiles) * 16 * f.kpad +
+                          static_cast<uint64_t>(f.kparts - 1) * f.jobs * f.ng * 256;
   if (floats > kLdsFloats) return p;
   f.plane_div = oxh::make_fastdiv(static_cast<uint32_t>(plane));
   f.oplane_div = oxh::make_fastdiv(static_cast<uint32_t>(P));
   f.m_div = oxh::make_fastdiv(g.out_c);
   p.chunks = static_cast<uint32_t>((g.batch + ipc - 1) / ipc);
-  if (p.chunks > 1 && static_cast<uint64_t>(p.chunks) * weight_elems(g) >= kMaxElems) return p;
+  if (p.chunks > 1 && static_cast<uint64_t>(p.chunks) * f.stride >= kMaxElems) return p;
   p.blocks = (f.jobs + 3) / 4;
   p.lds_bytes = static_cast<uint32_t>(floats * 4);
   return p;
@@ -2818,8 +2863,8 @@ uint64_t weight_partial_bytes(const ConvGeom &g) {
   // the matrix-core kernel's chunks, or the LDS kernel's with room for the bias sums of a
   // parameter-only oxh_conv2d_backward after each chunk's weights, or (operands the matrix-core
   // kernel does not take) the generic kernel's
-  const MfmaWeightPlan mp = weight_mfma_plan(g);
-  const uint64_t mbytes = mp.lds_bytes > 0 && mp.chunks > 1 ? mp.chunks * weight_elems(g) * 4 : 0;
+  const MfmaWeightPlan mp = weight_mfma_plan(g, true);
+  const uint64_t mbytes = mp.lds_bytes > 0 && mp.chunks > 1 ? mp.chunks * mp.f.stride * 4ull : 0;
   const LdsPlan lp = weight_lds_plan(g);
   if (lp.tile > 0) {
     const uint64_t lbytes = lp.chunks > 1 ? lp.chunks * (weight_elems(g) + g.out_c) * 4 : 0;
@@ -3114,22 +3159,27 @@ oxh_status weight_backward_impl(const char *name, hipStream_t s, const ConvGeom 
                   oplane_div, gradient, input, weight_gradient);
     return oxh::launched(name);
   }
-  // the matrix-core kernel where it takes the shape (the caller then forms the bias)
-  const MfmaWeightPlan mp = weight_mfma_plan(g);
+  // the matrix-core kernel where it takes the shape, the bias gradient as one more column
+  const MfmaWeightPlan mp = weight_mfma_plan(g, bias_gradient != nullptr);
   if (mp.lds_bytes > 0 && oxh::aligned16(gradient) && oxh::aligned16(input)) {
-    float *out = mp.chunks > 1 ? partial : weight_gradient;
+    const bool chunked = mp.chunks > 1;
+    float *ow = chunked ? partial : weight_gradient;
+    float *ob = !mp.f.bias ? ow : chunked ? partial + weight_elems(g) : bias_gradient;
     const dim3 mgrid(mp.blocks, mp.chunks), mblock(256);
-#define OXH_WGT_MFMA_LAUNCH(KK, SS)                                                           \
-  do {                                                                                      \
-    if (mp.f.ng == 9)                                                                       \
-      oxh::launch(conv2d_weight_mfma_kernel<KK, SS, 9>, mgrid, mblock, mp.lds_bytes, s, g,  \
-                  mp.f, gradient, input, out);                                              \
-    else if (mp.f.ng == 6)                                                                  \
-      oxh::launch(conv2d_weight_mfma_kernel<KK, SS, 6>, mgrid, mblock, mp.lds_bytes, s, g,  \
-                  mp.f, gradient, input, out);                                              \
-    else                                                                                    \
-      oxh::launch(conv2d_weight_mfma_kernel<KK, SS, 3>, mgrid, mblock, mp.lds_bytes, s, g,  \
-                  mp.f, gradient, input, out);                                              \
+#define OXH_WGT_MFMA_LAUNCH(KK, SS)                                                            \
+  do {                                                                                       \
+    if (mp.f.ng == 9)                                                                        \
+      oxh::launch(conv2d_weight_mfma_kernel<KK, SS, 9>, mgrid, mblock, mp.lds_bytes, s, g,   \
+                  mp.f, gradient, input, ow, ob);                                            \
+    else if (mp.f.ng == 6)                                                                   \
+      oxh::launch(conv2d_weight_mfma_kernel<KK, SS, 6>, mgrid, mblock, mp.lds_bytes, s, g,   \
+                  mp.f, gradient, input, ow, ob);                                            \
+    else if (mp.f.ng == 3)                                                                   \
+      oxh::launch(conv2d_weight_mfma_kernel<KK, SS, 3>, mgrid, mblock, mp.lds_bytes, s, g,   \
+                  mp.f, gradient, input, ow, ob);                                            \
+    else                                                                                     \
+      oxh::launch(conv2d_weight_mfma_kernel<KK, SS, 1>, mgrid, mblock, mp.lds_bytes, s, g,   \
+                  mp.f, gradient, input, ow, ob);                                            \
   } while (0)
     switch (tap_kernel(g)) {
       case 31: OXH_WGT_MFMA_LAUNCH(3, 1); break;
@@ -3139,9 +3189,12 @@ oxh_status weight_backward_impl(const char *name, hipStream_t s, const ConvGeom 
     }
 #undef OXH_WGT_MFMA_LAUNCH
     oxh_status st = oxh::launched(name);
-    if (st != OXH_OK || mp.chunks == 1) return st;
-    launch_sum_chunks(s, static_cast<uint32_t>(weight_elems(g)), mp.chunks, partial,
-                      weight_gradient);
+    if (st != OXH_OK) return st;
+    bias_done = mp.f.bias != 0;
+    if (!chunked) return st;
+    const uint32_t weights = static_cast<uint32_t>(weight_elems(g));
+    launch_sum_chunks(s, mp.f.stride, mp.chunks, partial, weight_gradient, weights,
+                      mp.f.bias ? bias_gradient : nullptr);
     return oxh::launched(name);
   }
   // the bias sums ride along where their threads fit; else the caller forms the bias
@@ -3435,8 +3488,11 @@ oxh_status oxh_conv2d_backward(oxh_stream stream, const oxh_conv2d_shape *shape,
     else if (wp.f.ng == 6)                                                                  \
       oxh::launch(conv2d_backward_mfma_kernel<KK, 6>, grid, block, lds_bytes, s, g, ip.f,    \
                   wp.f, d, gradient, weight, input, addend, input_gradient, out);           \
-    else                                                                                    \
+    else if (wp.f.ng == 3)                                                                  \
       oxh::launch(conv2d_backward_mfma_kernel<KK, 3>, grid, block, lds_bytes, s, g, ip.f,    \
+                  wp.f, d, gradient, weight, input, addend, input_gradient, out);           \
+    else                                                                                    \
+      oxh::launch(conv2d_backward_mfma_kernel<KK, 1>, grid, block, lds_bytes, s, g, ip.f,    \
                   wp.f, d, gradient, weight, input, addend, input_gradient, out);           \
   } while (0)
       if (g.kh == 3)
