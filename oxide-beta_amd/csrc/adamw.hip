@@ -16,6 +16,7 @@
 #include <cstring>
 #include <string>
 
+#include "chunk_sum.h"
 #include "common.h"
 
 namespace {
@@ -156,6 +157,33 @@ __host__ __device__ inline float powi_f32(float a, int32_t b) {
 }
 
 __global__ void increment_step_kernel(int32_t *step) { *step += 1; }
+
+// Up to kChunkSumsPerLaunch weight-gradient chunk sums in one launch: block b serves the last
+// sum whose first block is <= b, as block b - first of that sum's own launch would
+// (oxh::sum_chunks_block); with `step` not null, thread 0 of block 0 also advances the
+// optimizer step counter (the AdamW table launch after it reads the new value).
+struct ChunkSumJob {
+  const float *partial;
+  float *out, *out2;
+  uint32_t count, chunks, lanes, split, first_block;
+};
+struct ChunkSumTable {
+  ChunkSumJob job[oxh::kChunkSumsPerLaunch];
+  uint32_t jobs;
+  int32_t *step;
+};
+
+__global__ __launch_bounds__(256) void sum_chunks_table_kernel(ChunkSumTable t) {
+  __shared__ float part[256];
+  const uint32_t b = blockIdx.x;
+  if (t.step != nullptr && b == 0 && threadIdx.x == 0) *t.step += 1;
+  if (t.jobs == 0) return;
+  uint32_t j = 0;
+  while (j + 1 < t.jobs && t.job[j + 1].first_block <= b) ++j;  // block-uniform
+  const ChunkSumJob &c = t.job[j];
+  oxh::sum_chunks_block(b - c.first_block, c.count, c.chunks, c.lanes, c.partial, c.out,
+                        c.split, c.out2, part);
+}
 
 // step != null: the bias corrections come from the device step counter (optim.rs:113-114).
 __global__ __launch_bounds__(oxh::kBlock) void adamw_multi_kernel(Hyper h, TensorTable table,
@@ -335,6 +363,49 @@ oxh_status oxh_adamw_multi_tensor_table_step(oxh_stream stream, float learning_r
 }
 
 }  // extern "C"
+
+oxh_status oxh::adamw_table_step_advanced(hipStream_t s, float learning_rate, float weight_decay,
+                                          float beta1, float beta2, float epsilon,
+                                          const int32_t *step,
+                                          const oxh_adamw_tensor *device_tensors,
+                                          const uint32_t *device_chunk_starts, uint32_t count,
+                                          uint64_t total_chunks) {
+  const char *name = "adamw_table_step_advanced";
+  OXH_REQUIRE(step != nullptr && device_tensors != nullptr && device_chunk_starts != nullptr,
+              OXH_INVALID_SHAPE, std::string(name) + ": null pointer");
+  OXH_REQUIRE(count > 0 && total_chunks > 0 && total_chunks < (1ull << 31), OXH_INVALID_SHAPE,
+              std::string(name) + ": empty table or more than 2^31 chunks");
+  const Hyper h{learning_rate, weight_decay, beta1, beta2, 1.0f, 1.0f, epsilon};
+  OXH_REQUIRE(finite_hyper(h), OXH_INVALID_SHAPE,
+              std::string(name) + ": non-finite hyper-parameter");
+  oxh::launch(adamw_table_kernel, dim3(static_cast<uint32_t>(total_chunks)), dim3(oxh::kBlock),
+              0, s, h, device_tensors, device_chunk_starts, count, step);
+  return oxh::launched(name);
+}
+
+oxh_status oxh::launch_chunk_sums(hipStream_t s, const std::vector<ChunkSum> &sums,
+                                  int32_t *step) {
+  size_t k = 0;
+  do {
+    ChunkSumTable t{};
+    t.step = k == 0 ? step : nullptr;
+    uint32_t blocks = 0;
+    for (; k < sums.size() && t.jobs < kChunkSumsPerLaunch; ++k, ++t.jobs) {
+      const ChunkSum &c = sums[k];
+      OXH_REQUIRE(c.partial != nullptr && c.out != nullptr && c.count > 0 && c.chunks > 0 &&
+                      c.split <= c.count && (c.split == c.count || c.out2 != nullptr),
+                  OXH_INVALID_SHAPE, "launch_chunk_sums: malformed sum");
+      const uint32_t lanes = chunk_sum_lanes(c.chunks), per_block = 256 / lanes;
+      t.job[t.jobs] = ChunkSumJob{c.partial, c.out,   c.out2, c.count,
+                                  c.chunks,  lanes,   c.split, blocks};
+      blocks += (c.count + per_block - 1) / per_block;
+    }
+    oxh::launch(sum_chunks_table_kernel, dim3(blocks > 0 ? blocks : 1), dim3(256), 0, s, t);
+    oxh_status st = oxh::launched("launch_chunk_sums");
+    if (st != OXH_OK) return st;
+  } while (k < sums.size());
+  return oxh::ok();
+}
 
 namespace {
 oxh_status adamw_multi(const char *name, oxh_stream stream, const Hyper &h, const int32_t *step,

@@ -10,6 +10,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <string>
+#include <vector>
 
 #include "oxide_hip.h"
 
@@ -22,6 +23,40 @@ oxh_status bn_scratch_init(int device);
 // Whether a training BatchNorm of this shape runs one block per channel (its backward then
 // sums the input gradient per channel in passing: a preceding convolution's bias gradient).
 bool batch_norm_single_launch(uint64_t batch, uint64_t channels, uint64_t spatial);
+
+// One weight-gradient chunk sum: out[e] (e < split) or out2[e - split] (split <= e < count)
+// = the fixed-order sum over `chunks` of partial[chunk * count + e].
+struct ChunkSum {
+  const float *partial;
+  float *out, *out2;
+  uint32_t count, chunks, split;
+};
+
+// oxh_conv2d_backward (same arguments and checks) with its weight-gradient chunk sums, if it
+// has any, appended to `deferred` in place of launched: the weight (and bias) gradient holds
+// its value only once the caller has run them (launch_chunk_sums), and the workspace must stay
+// untouched until then.
+oxh_status conv2d_backward_deferred(oxh_stream stream, const oxh_conv2d_shape *shape,
+                                    const float *gradient, const float *input,
+                                    const float *weight, const float *addend,
+                                    float *input_gradient, float *weight_gradient,
+                                    float *bias_gradient, void *workspace,
+                                    uint64_t workspace_bytes, std::vector<ChunkSum> &deferred);
+
+// Every sum of `sums` (each element the same sum as the convolution's own launch forms) in one
+// launch per kChunkSumsPerLaunch sums (at least one launch); with `step` not null, the first
+// launch also advances the optimizer step counter (*step += 1).
+constexpr uint32_t kChunkSumsPerLaunch = 16;
+oxh_status launch_chunk_sums(hipStream_t stream, const std::vector<ChunkSum> &sums,
+                             int32_t *step);
+
+// oxh_adamw_multi_tensor_table_step without its step counter advance (the caller has
+// advanced it, e.g. by launch_chunk_sums).
+oxh_status adamw_table_step_advanced(hipStream_t stream, float learning_rate,
+                                     float weight_decay, float beta1, float beta2, float epsilon,
+                                     const int32_t *step, const oxh_adamw_tensor *device_tensors,
+                                     const uint32_t *device_chunk_starts, uint32_t count,
+                                     uint64_t total_chunks);
 
 // Records `message` as the calling thread's last error and returns `status`.
 oxh_status fail(oxh_status status, const std::string &message);

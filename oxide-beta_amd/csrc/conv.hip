@@ -39,6 +39,7 @@
 #include <string>
 #include <type_traits>
 
+#include "chunk_sum.h"
 #include "common.h"
 
 namespace {
@@ -1439,44 +1440,15 @@ BiasArgs bias_args(const ConvGeom &g, const float *gradient, float *bias_gradien
                   oxh::make_fastdiv(g.oh * g.ow)};
 }
 
-// Weight gradient, phase 2: out[e] = sum over chunks of partial[chunk][e] in a fixed order.
-// `lanes` threads share an element (a block serves 256 / lanes elements; thread t takes lane
-// t / (256 / lanes) of element t % (256 / lanes), so each lane's loads are contiguous across
-// elements): lane l sums the l-th contiguous part of the chunks serially (loads issued in
-// groups of 8 ahead of the adds), and the lane sums are then added in lane order.  A chain of
-// chunks / lanes loads per thread in place of chunks.
-// Elements e >= split go to out2[e - split] (a second output sharing the chunks' layout).
+// Weight gradient, phase 2: out[e] = sum over chunks of partial[chunk][e] in a fixed order
+// (oxh::sum_chunks_block); elements e >= split go to out2[e - split].
 __global__ __launch_bounds__(256) void sum_chunks_kernel(uint32_t count, uint32_t chunks,
                                                          uint32_t lanes,
                                                          const float *__restrict__ partial,
                                                          float *__restrict__ out, uint32_t split,
                                                          float *__restrict__ out2) {
   __shared__ float part[256];
-  const uint32_t per_block = 256 / lanes;
-  const uint32_t l = threadIdx.x / per_block, j = threadIdx.x - l * per_block;
-  const uint32_t e = blockIdx.x * per_block + j;
-  float acc = 0.0f;
-  if (e < count) {
-    const uint32_t c1 = (l + 1) * chunks / lanes;
-    uint32_t c = l * chunks / lanes;
-    for (; c + 8 <= c1; c += 8) {
-      float v[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = partial[static_cast<uint64_t>(c + u) * count + e];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) acc += v[u];
-    }
-    for (; c < c1; ++c) acc += partial[static_cast<uint64_t>(c) * count + e];
-  }
-  if (lanes == 1) {
-    if (e < count) (e < split ? out[e] : out2[e - split]) = acc;
-    return;
-  }
-  part[threadIdx.x] = acc;
-  __syncthreads();
-  if (l != 0 || e >= count) return;
-  for (uint32_t r = 1; r < lanes; ++r) acc += part[r * per_block + j];
-  (e < split ? out[e] : out2[e - split]) = acc;
+  oxh::sum_chunks_block(blockIdx.x, count, chunks, lanes, partial, out, split, out2, part);
 }
 
 
@@ -2295,17 +2267,24 @@ uint32_t grid_for(uint64_t items) {
   return static_cast<uint32_t>(g);
 }
 
-// Lanes per element for sum_chunks_kernel: a power of two up to 16 leaving at most 8 chunks
-// per lane.
+// The chunk sums of a convolution backward whose caller takes them over (a training program
+// launching every convolution's sums at once): while set, launch_sum_chunks records its sum
+// here in place of launching it.
+thread_local std::vector<oxh::ChunkSum> *deferred_sums = nullptr;
+
 // Elements at or past `split` (default: none) go to out2.
 void launch_sum_chunks(hipStream_t s, uint32_t count, uint32_t chunks, const void *partial,
                        float *out, uint32_t split = UINT32_MAX, float *out2 = nullptr) {
-  uint32_t lanes = 1;
-  while (lanes < 16 && chunks > 8 * lanes) lanes *= 2;
+  if (split > count) split = count;
+  if (deferred_sums != nullptr) {
+    deferred_sums->push_back(
+        oxh::ChunkSum{static_cast<const float *>(partial), out, out2, count, chunks, split});
+    return;
+  }
+  const uint32_t lanes = oxh::chunk_sum_lanes(chunks);
   const uint32_t per_block = 256 / lanes;
   oxh::launch(sum_chunks_kernel, dim3((count + per_block - 1) / per_block), dim3(256), 0, s,
-              count, chunks, lanes, static_cast<const float *>(partial), out,
-              split < count ? split : count, out2);
+              count, chunks, lanes, static_cast<const float *>(partial), out, split, out2);
 }
 
 uint64_t input_elems(const ConvGeom &g) {
@@ -3527,6 +3506,25 @@ oxh_status oxh_conv2d_backward(oxh_stream stream, const oxh_conv2d_shape *shape,
   if (input_gradient == nullptr) return oxh::ok();
   return input_backward_impl(name, stream, shape, gradient, weight, addend, input_gradient);
 }
+
+}  // extern "C"
+
+oxh_status oxh::conv2d_backward_deferred(oxh_stream stream, const oxh_conv2d_shape *shape,
+                                         const float *gradient, const float *input,
+                                         const float *weight, const float *addend,
+                                         float *input_gradient, float *weight_gradient,
+                                         float *bias_gradient, void *workspace,
+                                         uint64_t workspace_bytes,
+                                         std::vector<ChunkSum> &deferred) {
+  struct Restore {
+    ~Restore() { deferred_sums = nullptr; }
+  } restore;
+  deferred_sums = &deferred;
+  return oxh_conv2d_backward(stream, shape, gradient, input, weight, addend, input_gradient,
+                             weight_gradient, bias_gradient, workspace, workspace_bytes);
+}
+
+extern "C" {
 
 oxh_status oxh_avg_pool2d_forward(oxh_stream stream, const oxh_pool2d_shape *shape,
                                   const float *input, float *output) {

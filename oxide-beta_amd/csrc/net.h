@@ -122,6 +122,11 @@ struct OpRec {
   std::vector<TensorRef> tensors;
   std::vector<std::pair<std::string, double>> attrs;
   std::function<oxh_status(hipStream_t)> launch;
+  // Where set, what the whole program runs (run, capture) in place of `launch`: the same
+  // values, with work moved to a later group of the program (a convolution's weight-gradient
+  // chunk sums, run with every other convolution's before the optimizer step).  `launch` alone
+  // (oxh_program_run_op) always leaves every output of the group formed.
+  std::function<oxh_status(hipStream_t)> program_launch;
   // C views of the above, built once
   std::vector<oxh_op_tensor> c_tensors;
   std::vector<oxh_op_attr> c_attrs;
@@ -152,6 +157,8 @@ struct oxh_program {
   uint64_t adam_chunks = 0;
   int32_t *step = nullptr;
   uint32_t *error_flag = nullptr;  // raised by a cross entropy with an invalid target
+  // chunk sums the program's convolutions leave to the optimizer group, recorded by each run
+  std::vector<oxh::ChunkSum> deferred_sums;
 
   oxh_status finalize();
   oxh_status run();

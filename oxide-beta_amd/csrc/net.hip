@@ -742,6 +742,27 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
   oxh_status st = plan_workspace(g, active, ws_bytes);
   if (st != OXH_OK) return st;
   const uint64_t ws_off = a.reserve(ws_bytes);
+  // A convolution whose parameters feed it alone takes a workspace of its own when the program
+  // ends with AdamW: its weight-gradient chunk partials then stay put until the optimizer
+  // group, which sums every such convolution's in one launch (with the step counter advance).
+  std::vector<int64_t> defer_off(n, -1);
+  std::vector<uint64_t> defer_bytes(n, 0);
+  if (adam != nullptr) {
+    for (size_t i = 0; i < n; ++i) {
+      const Node &x = g.nodes[i];
+      if (!active[i] || x.op != Op::Conv || !want(x.in[1])) continue;
+      bool alone = true;  // trainable parameters read by this convolution only
+      for (size_t k = 1; k < x.in.size(); ++k)
+        alone = alone && g.nodes[x.in[k]].op == Op::Param && consumers[x.in[k]] == 1;
+      const oxh_conv2d_shape cs = conv_shape(g, x);
+      uint64_t b = 0;
+      st = oxh_conv2d_weight_backward_workspace_size(&cs, &b);
+      if (st != OXH_OK) return st;
+      if (!alone || b == 0) continue;
+      defer_off[i] = static_cast<int64_t>(a.reserve(b));
+      defer_bytes[i] = b;
+    }
+  }
   st = a.allocate();  // zero-filled: moments, step counter, error flag start at 0
   if (st != OXH_OK) return st;
 
@@ -780,6 +801,7 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
   p.adam_table = a.at<oxh_adamw_tensor>(table_off);
   p.adam_starts = a.at<uint32_t>(starts_off);
   p.root = root;
+  oxh_program *self = &p;
   void *ws = a.at<void>(ws_off);
   const uint64_t wsb = ws_bytes;
   const float one_value = 1.0f;
@@ -859,6 +881,7 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
   };
   auto attach_sides = [&](OpRec &op) {
     if (side_adds.empty()) return;
+    op.program_launch = nullptr;  // a side add reads its part right after the launch
     std::vector<SideAdd> adds;
     adds.swap(side_adds);
     for (const SideAdd &sa : adds)
@@ -874,20 +897,24 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
       return e;
     };
   };
+  // program_body: set for a group the whole program runs another way (OpRec::program_launch)
   auto emit = [&](OpRec op, float *acc, const Node &target,
-                  std::function<oxh_status(hipStream_t)> body) {
-    if (acc == nullptr) {
-      op.launch = std::move(body);
-    } else {
+                  std::function<oxh_status(hipStream_t)> body,
+                  std::function<oxh_status(hipStream_t)> program_body = nullptr) {
+    using Body = std::function<oxh_status(hipStream_t)>;
+    auto then_accumulate = [&](Body b) -> Body {
+      if (acc == nullptr || !b) return b;
       float *part = scratch;
       const uint64_t cnt = target.numel();
-      op.tensors.push_back(ref("accumulate_into", acc, target, 2));
-      op.launch = [body, acc, part, cnt](hipStream_t s) {
-        oxh_status e = body(s);
+      return [b, acc, part, cnt](hipStream_t s) {
+        oxh_status e = b(s);
         if (e != OXH_OK) return e;
         return oxh_accumulate(s, acc, part, acc, cnt);
       };
-    }
+    };
+    if (acc != nullptr) op.tensors.push_back(ref("accumulate_into", acc, target, 2));
+    op.launch = then_accumulate(std::move(body));
+    op.program_launch = then_accumulate(std::move(program_body));
     attach_sides(op);
     ops.push_back(std::move(op));
   };
@@ -1464,10 +1491,20 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
           if (bias_here) op.tensors.push_back(ref("bias_gradient", db, g.nodes[x.in[2]], 1));
           op.tensors.push_back(ref("contribution", dst, g.nodes[xin], 1));
           op.attrs = conv_attrs(x);
+          std::function<oxh_status(hipStream_t)> deferred;
+          if (defer_off[r] >= 0) {
+            void *own = a.at<void>(static_cast<uint64_t>(defer_off[r]));
+            const uint64_t own_bytes = defer_bytes[r];
+            deferred = [s, gr, xi, w, addend, dst, dw, db, own, own_bytes, self](hipStream_t st) {
+              return oxh::conv2d_backward_deferred(st, &s, gr, xi, w, addend, dst, dw, db, own,
+                                                   own_bytes, self->deferred_sums);
+            };
+          }
           emit(std::move(op), acc, g.nodes[xin],
                [s, gr, xi, w, addend, dst, dw, db, ws, wsb](hipStream_t st) {
                  return oxh_conv2d_backward(st, &s, gr, xi, w, addend, dst, dw, db, ws, wsb);
-               });
+               },
+               std::move(deferred));
           break;
         }
         if (weight_here || bias_here) {
@@ -1487,6 +1524,14 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
             if (dw != nullptr) return oxh_conv2d_weight_backward(st, &s, gr, xi, dw, ws, wsb);
             return oxh_conv2d_bias_backward(st, &s, gr, db, ws, wsb);
           };
+          if (defer_off[r] >= 0 && dw != nullptr) {  // the same launches, sums left to AdamW
+            void *own = a.at<void>(static_cast<uint64_t>(defer_off[r]));
+            const uint64_t own_bytes = defer_bytes[r];
+            pr.program_launch = [s, gr, xi, w, dw, db, own, own_bytes, self](hipStream_t st) {
+              return oxh::conv2d_backward_deferred(st, &s, gr, xi, w, nullptr, nullptr, dw, db,
+                                                   own, own_bytes, self->deferred_sums);
+            };
+          }
           attach_sides(pr);
           ops.push_back(std::move(pr));
         }
@@ -1553,7 +1598,6 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
                             hipMemcpyHostToDevice));
     OXH_HIP_CHECK(hipMemcpy(p.adam_starts, starts.data(), (count + 1) * 4,
                             hipMemcpyHostToDevice));
-    oxh_program *self = &p;
     op.launch = [self](hipStream_t s) {
       const AdamConfig &c = self->adam_config;
       return oxh_adamw_multi_tensor_table_step(
@@ -1561,6 +1605,18 @@ oxh_status build_training(const Graph &g, int root, const AdamConfig *adam, oxh_
           self->adam_table, self->adam_starts,
           static_cast<uint32_t>(self->adam.size()), self->adam_chunks);
     };
+    bool deferring = false;
+    for (const OpRec &o : ops) deferring = deferring || static_cast<bool>(o.program_launch);
+    if (deferring)  // the convolutions' chunk sums and the step advance in one launch first
+      op.program_launch = [self](hipStream_t s) {
+        oxh_status e = oxh::launch_chunk_sums(s, self->deferred_sums, self->step);
+        if (e != OXH_OK) return e;
+        const AdamConfig &c = self->adam_config;
+        return oxh::adamw_table_step_advanced(
+            s, c.learning_rate, c.weight_decay, c.beta1, c.beta2, c.epsilon, self->step,
+            self->adam_table, self->adam_starts, static_cast<uint32_t>(self->adam.size()),
+            self->adam_chunks);
+      };
     ops.push_back(std::move(op));
   }
   return p.finalize();
@@ -1595,8 +1651,9 @@ oxh_status oxh_program::finalize() {
 }
 
 oxh_status oxh_program::run() {
+  deferred_sums.clear();
   for (oxh::net::OpRec &op : ops) {
-    oxh_status st = op.launch(stream);
+    oxh_status st = op.program_launch ? op.program_launch(stream) : op.launch(stream);
     if (st != OXH_OK) return st;
   }
   return oxh::ok();

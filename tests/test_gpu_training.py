@@ -126,14 +126,16 @@ def _state(step):
 
 def test_graph_replay_matches_eager_bitwise():
     """The captured step replayed 3 times leaves parameters, moments, running statistics and
-    loss bit-identical to 3 eager steps (every kernel sums in a fixed order)."""
+    loss bit-identical to 3 eager steps launched group by group (every kernel sums in a fixed
+    order).  Group by group, each convolution sums its own weight-gradient chunks; the whole
+    program (run or captured) sums them all in one launch before AdamW: the same values."""
     r = np.random.default_rng(17)
     batch = _mnist_batch(r, 128)
     eager = T.TrainingStep(T.MobileNetV4ConvSmall.mnist(), 128)
     eager.set_batch(*batch)
     eager_losses = []
     for _ in range(3):
-        eager.run_eager()
+        eager.run_eager(after=lambda op: None)  # oxh_program_run_op per group
         eager_losses.append(eager.loss_value())
     graph = T.TrainingStep(T.MobileNetV4ConvSmall.mnist(), 128)
     graph.set_batch(*batch)
@@ -147,6 +149,18 @@ def test_graph_replay_matches_eager_bitwise():
     assert graph.steps_taken() == 3
     for i, (a, b) in enumerate(zip(_state(eager), _state(graph))):
         assert_bitexact(b, a, f"state tensor {i}")
+    # the whole program run eagerly (oxh_program_run: the deferred sums too) from the graph's
+    # state equals one more group-by-group step
+    eager.run_eager(after=lambda op: None)
+    graph.run_eager()
+    assert graph.loss_value() == eager.loss_value()
+    assert graph.steps_taken() == 4
+    for i, (a, b) in enumerate(zip(_state(eager), _state(graph))):
+        assert_bitexact(b, a, f"state tensor {i} (program run)")
+    grads = [op.by_role["gradient"] for s in (eager, graph) for op in s.ops if op.kind == "adamw"]
+    assert len(grads) == 2 and len(grads[0]) == 186
+    for i, (a, b) in enumerate(zip(*grads)):
+        assert_bitexact(host(b), host(a), f"parameter gradient {i}")
 
 
 def test_loss_decreases_on_a_fixed_batch():
