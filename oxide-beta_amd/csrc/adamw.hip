@@ -204,31 +204,55 @@ __global__ __launch_bounds__(oxh::kBlock) void adamw_multi_kernel(Hyper h, Tenso
 }
 
 // Device-table variant: the tensor descriptors and each tensor's first chunk live in device
-// memory (any number of tensors, one launch); block b finds its tensor among the chunk starts
-// with a block-parallel search: each round the block's threads probe kBlock evenly spaced
-// starts at once, and the probes at or below b form a prefix (starts never decrease), whose
-// length a barrier count gives -- one round for up to kBlock tensors.  Every block reads the
-// step count t = *step, which the one-thread launch before it has advanced (a "last block
-// stores t" ticket would serialise one atomic per block on a single address: about 7 us over
-// config 5's 1360 blocks, against about 2 us for the extra launch).
+// memory (any number of tensors, one launch).  Up to kBlock tensors: thread i loads tensor i's
+// chunk range [starts[i], starts[i + 1]) and descriptor together, and the one thread whose
+// range holds b hands its descriptor to the block through LDS (one memory round trip and one
+// barrier before the data loads).  More tensors: a block-parallel search -- each round the
+// block's threads probe kBlock evenly spaced starts at once, the probes at or below b form a
+// prefix (starts never decrease) whose length a barrier count gives -- then the descriptor's
+// load.  Every block reads the step count t = *step, which the launch before it has advanced
+// (a "last block stores t" ticket would serialise one atomic per block on a single address:
+// about 7 us over config 5's 1360 blocks, against about 2 us for the extra launch).
 __global__ __launch_bounds__(oxh::kBlock) void adamw_table_kernel(
     Hyper h, const oxh_adamw_tensor *__restrict__ table, const uint32_t *__restrict__ starts,
     uint32_t count, const int32_t *step) {
+  __shared__ oxh_adamw_tensor mine;
+  __shared__ uint32_t mine_start;
   const int32_t t = *step;
   h.c1 = 1.0f - powi_f32(h.b1, t);
   h.c2 = 1.0f - powi_f32(h.b2, t);
   const uint32_t b = blockIdx.x;
-  uint32_t lo = 0, hi = count;  // the last tensor index with starts[i] <= b is in [lo, hi)
-  while (hi - lo > 1) {          // block-uniform
-    const uint32_t spacing = (hi - lo + oxh::kBlock - 1) / oxh::kBlock;
-    const uint32_t probe = lo + threadIdx.x * spacing;
-    const int at_or_below = __syncthreads_count(probe < hi && starts[probe] <= b);
-    const uint32_t first = lo + static_cast<uint32_t>(at_or_below - 1) * spacing;  // >= lo
-    hi = first + spacing < hi ? first + spacing : hi;
-    lo = first;
+  oxh_adamw_tensor d;
+  uint32_t first;
+  if (count <= oxh::kBlock) {
+    const uint32_t i = threadIdx.x;
+    if (i < count) {
+      const uint32_t lo = starts[i], hi = starts[i + 1];
+      const oxh_adamw_tensor own = table[i];
+      // exactly one thread: the ranges tile [0, starts[count]) (the first and last tensors
+      // also take blocks outside it, which then find no elements of theirs)
+      if ((lo <= b || i == 0) && (b < hi || i + 1 == count)) {
+        mine = own;
+        mine_start = lo;
+      }
+    }
+    __syncthreads();
+    d = mine;
+    first = mine_start;
+  } else {
+    uint32_t lo = 0, hi = count;  // the last tensor index with starts[i] <= b is in [lo, hi)
+    while (hi - lo > 1) {          // block-uniform
+      const uint32_t spacing = (hi - lo + oxh::kBlock - 1) / oxh::kBlock;
+      const uint32_t probe = lo + threadIdx.x * spacing;
+      const int at_or_below = __syncthreads_count(probe < hi && starts[probe] <= b);
+      const uint32_t f = lo + static_cast<uint32_t>(at_or_below - 1) * spacing;  // >= lo
+      hi = f + spacing < hi ? f + spacing : hi;
+      lo = f;
+    }
+    d = table[lo];
+    first = starts[lo];
   }
-  const oxh_adamw_tensor d = table[lo];
-  const uint64_t begin = static_cast<uint64_t>(b - starts[lo]) * kChunk;
+  const uint64_t begin = static_cast<uint64_t>(b - first) * kChunk;
   const uint64_t end = begin + kChunk < d.n ? begin + kChunk : d.n;
   const bool vec = ((reinterpret_cast<uintptr_t>(d.parameter) |
                      reinterpret_cast<uintptr_t>(d.gradient) |

@@ -109,17 +109,18 @@ def test_adamw_first_step_closed_form(module, dev, rng):
 CONFIG5_SIZES = [864, 32, 32, 32, 288, 32, 1024, 32, 32, 32] * 18 + [12800, 10, 1280, 10, 5, 7]
 
 
-@pytest.mark.parametrize("table", ["config5", "many"])
+@pytest.mark.parametrize("table", ["config5", "block", "many"])
 def test_adamw_table_step_matches_multi_tensor_step(module, dev, rng, table):
     """The one-launch device-table update equals the step-counting multi-tensor update bit for
-    bit over three steps (186 tensors as in config 5, more than one 48-tensor launch of the
-    latter; and 700 tensors of 1 to 5000 values, whose chunk search takes two rounds of the
-    block's 256 probes); the step counter advances once per call."""
+    bit over three steps: 186 tensors as in config 5 (more than one 48-tensor launch of the
+    latter) and 256 tensors of 1 to 5000 values (each block's tensor found by one thread per
+    tensor), and 700 such tensors (the chunk search then takes two rounds of the block's 256
+    probes); the step counter advances once per call."""
     if table == "config5":
         sizes = CONFIG5_SIZES
         assert len(sizes) == 186
     else:
-        sizes = [int(v) for v in rng.integers(1, 5001, 700)]
+        sizes = [int(v) for v in rng.integers(1, 5001, 256 if table == "block" else 700)]
     state = [_state(rng, n) for n in sizes]
     a = [tuple(to_dev(x, dev) for x in s) for s in state]
     b = [tuple(to_dev(x, dev) for x in s) for s in state]
