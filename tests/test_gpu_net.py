@@ -372,3 +372,60 @@ def test_mobilenet_through_generic_builder_matches_native_trainer():
     prog.replay()
     compare("graph replay")
     assert prog.steps() == native.steps_taken() == 3
+
+
+def test_whole_program_step_equals_group_by_group_step():
+    """A training program with AdamW run whole (oxh_program_run, then captured and replayed)
+    against the same program's groups launched one by one (oxh_program_run_op), from the same
+    parameters: loss, parameters and parameter gradients bit-identical after every step.  The
+    whole program moves the chunk sums of the weight gradients of convolutions whose parameters
+    feed them alone (here the strided 3x3 convolution: 512 output positions, more than one
+    chunk) into the optimizer group; the 1x1 weight the two later convolutions share keeps its
+    sums (its second use adds into the first's gradient).  The 3x3 shape's weight-gradient
+    workspace is not empty (its partials are chunked)."""
+    r = np.random.default_rng(59)
+    n, c, h, w, o = 8, 16, 16, 16, 32
+    xv = r.standard_normal((n, c, h, w)).astype(np.float32)
+    kv = (r.standard_normal((o, c, 3, 3)) * 0.2).astype(np.float32)
+    kb = r.standard_normal(o).astype(np.float32) * 0.1
+    pv = (r.standard_normal((o, o, 1, 1)) * 0.3).astype(np.float32)
+    pbv = r.standard_normal(o).astype(np.float32) * 0.1
+    gam, bet = r.uniform(0.5, 1.5, o).astype(np.float32), r.uniform(-0.2, 0.2, o).astype(np.float32)
+    targets = r.integers(0, o, n).astype(np.float32)
+    assert ox.conv2d_workspace_size(ox.conv2d_shape(n, c, h, w, o, 3, 2, 1, 1)) > 0
+
+    def build():
+        x, t = tn.input((n, c, h, w)), tn.input((n,))
+        params = [nn.Parameter(v) for v in (kv, kb, pv, pbv, gam, bet)]
+        k, b, p, pb, g, be = (q.tensor() for q in params)
+        y = x.conv2d(k, b, 2, 1, 1).batch_norm2d(g, be, tn.BatchNormState(o), True, 0.1, 1e-5)
+        y = y.relu().conv2d(p, pb, 1, 0, 1).relu().conv2d(p, pb, 1, 0, 1)
+        loss = y.avg_pool2d((8, 8), (8, 8)).reshape((n, o)).cross_entropy(t)
+        prog = tn.training_program(loss, nn.AdamW(1e-2, 1e-4))
+        prog.feed(x, xv)
+        prog.feed(t, targets)
+        return prog, loss, params
+
+    groups, whole = build(), build()
+
+    def compare(when):
+        torch.cuda.synchronize()
+        (pa, la, qa), (pb, lb, qb) = groups, whole
+        assert_bitexact(pb.value(lb).host(), pa.value(la).host(), f"{when}: loss")
+        for i, (u, v) in enumerate(zip(qa, qb)):
+            assert_bitexact(v.host(), u.host(), f"{when}: parameter {i}")
+            assert_bitexact(pb.gradient(v.tensor()).host(), pa.gradient(u.tensor()).host(),
+                            f"{when}: gradient {i}")
+
+    for step in range(2):
+        for op in groups[0].ops:
+            op.launch()
+        whole[0].run()
+        compare(f"step {step}")
+    whole[0].capture()
+    for step in range(2):
+        for op in groups[0].ops:
+            op.launch()
+        whole[0].replay()
+        compare(f"replay {step}")
+    assert groups[0].steps() == whole[0].steps() == 4
