@@ -101,6 +101,47 @@ __host__ __device__ inline bool centre_only(uint32_t h, uint32_t w, uint32_t oh,
   return h == 1 && w == 1 && oh == 1 && ow == 1;
 }
 
+// Input planes of 4 x 4 with pad K / 2 (config 5's first UIB layers, where the backward's
+// per-value input-gradient loop spends most of its instructions on indices and on taps outside
+// the plane): one thread per image forms all of the image's input-gradient sums from registers,
+// with every index known at compile time.  Each sum adds exactly the terms the per-value loop
+// adds, in its order; the candidates outside the plane, which that loop adds as -0.0f, change
+// no sum and are skipped.  (The same form for the forward's outputs was slower.)
+template <int K, int S>
+struct Plane4 {
+  static constexpr int H = 4, P = K / 2, OH = (H + 2 * P - K) / S + 1, M = (K + S - 1) / S;
+  __device__ __forceinline__ static bool takes(const DwGeom &g) {
+    return g.h == H && g.w == H && g.pad == static_cast<uint32_t>(P) &&
+           g.oh == static_cast<uint32_t>(OH) && g.ow == static_cast<uint32_t>(OH) &&
+           g.in_samples <= kDwMaxOut;
+  }
+  // image n's input-gradient sums (the candidate outputs in input_sum's order) from its output
+  // gradient gp[OH * OH] and the weights wp[K * K]; out(p, value) for input position p
+  template <typename Out>
+  __device__ __forceinline__ static void input(const float *gp, const float *wp, Out out) {
+    float gv[OH * OH], wv[K * K];
+#pragma unroll
+    for (int i = 0; i < OH * OH; ++i) gv[i] = gp[i];
+#pragma unroll
+    for (int t = 0; t < K * K; ++t) wv[t] = wp[t];
+#pragma unroll
+    for (int iy = 0; iy < H; ++iy)
+#pragma unroll
+      for (int ix = 0; ix < H; ++ix) {
+        const int ty = iy + P, tx = ix + P;
+        float a = 0.0f;
+#pragma unroll
+        for (int t = 0; t < M * M; ++t) {
+          const int oy = ty / S - (M - 1) + t / M, ox = tx / S - (M - 1) + t % M;
+          const int ky = ty - oy * S, kx = tx - ox * S;
+          if (oy >= 0 && oy < OH && ky < K && ox >= 0 && ox < OH && kx < K)
+            a += gv[oy * OH + ox] * wv[ky * K + kx];
+        }
+        out(iy * H + ix, a);
+      }
+  }
+};
+
 template <int K, int S, bool Relu, int Pre, bool C = false, int T = 256>
 __global__ __launch_bounds__(T) void dw_bn_forward_kernel(
     DwGeom g, const float *__restrict__ x, const float *__restrict__ conv_weight,
@@ -342,12 +383,19 @@ __global__ __launch_bounds__(T) void dw_bn_backward_kernel(
     // gradient, stored to dx when given; its relu output is the staged convolution input),
     // exactly as its channel backward forms it; its dx sum is the feeding convolution's bias
     // gradient
+    const bool p4 = !C && Plane4<K, S>::takes(g);
+    float *isum = xs + kDwMaxOut;  // past the staged input (at most kDwMaxOut values then)
+    if (p4) {  // the image sums through LDS (read by the value's thread below)
+      for (uint32_t n = threadIdx.x; n * 16 < g.in_samples; n += T)
+        Plane4<K, S>::input(gs + n * oplane, wts, [&](int p, float a) { isum[n * 16 + p] = a; });
+      __syncthreads();
+    }
     float kg[kChannelKeep], kn[kChannelKeep], d[kChannelKeep];
 #pragma unroll
     for (int u = 0; u < kChannelKeep; ++u) {
       const uint32_t i = threadIdx.x + u * T;
       if (i >= g.in_samples) break;
-      float a = input_sum(i);
+      float a = p4 ? isum[i] : input_sum(i);
       if (addend != nullptr) a = a + addv[u];
       if (dx != nullptr) dx[pat[u]] = a;
       kg[u] = Pre == kPreBnRelu ? oxh::relu_masked(a, xs[i]) : a;

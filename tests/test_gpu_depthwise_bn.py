@@ -34,6 +34,7 @@ SHAPES = [
     (3, 5, 7, 6, 3, 2, 1),       # ragged, output 4 x 3
     (2, 3, 9, 9, 5, 1, 2),
     (16, 4, 4, 4, 3, 1, 0),      # no padding
+    (8, 6, 4, 4, 3, 2, 1),       # 4x4 planes, 3x3 stride 2 (one thread per image)
     (2, 1, 1, 1, 3, 1, 1),       # two values per channel (the minimum)
     (128, 3, 4, 4, 5, 1, 2),     # 2048 output values per channel (the maximum)
     (32, 130, 16, 16, 3, 2, 1),  # 8192 input values per channel (the maximum), 8x8 output
@@ -206,10 +207,15 @@ def test_unsupported_shapes_are_rejected(module, dev):
 
 
 # (batch, channels, height, width, kernel, stride, padding) of depthwise layers fed by a
-# BatchNorm (+ ReLU): the MNIST MobileNetV4's expand BatchNorms before their middle depthwise
-# layers, then ragged and minimal shapes (at most 2048 input values per channel)
+# BatchNorm (+ ReLU): the MNIST MobileNetV4's first UIB start and expand BatchNorms before their
+# depthwise layers, 4x4 planes under 3x3 kernels (the backward of a 4x4 plane forms its input
+# gradient with one thread per image), then ragged and minimal shapes (at most 2048 input
+# values per channel)
 PRE_SHAPES = [
+    (128, 64, 4, 4, 5, 1, 2),
     (128, 192, 4, 4, 5, 2, 2),
+    (8, 6, 4, 4, 3, 1, 1),
+    (8, 6, 4, 4, 3, 2, 1),
     (128, 192, 2, 2, 3, 1, 1),
     (128, 576, 2, 2, 3, 2, 1),
     (128, 512, 1, 1, 5, 1, 2),
