@@ -60,7 +60,7 @@ using oxh::write_forward_outputs;
 
 // Launch-shape constants (overridable at build time for tuning sweeps).
 #ifndef OXH_BN_RED_BLOCKS_PER_CU
-#define OXH_BN_RED_BLOCKS_PER_CU 8  // reduce grid: target blocks per CU over all channels
+#define OXH_BN_RED_BLOCKS_PER_CU 32  // reduce grid: target blocks per CU over all channels
 #endif
 #ifndef OXH_BN_RED_UNROLL
 #define OXH_BN_RED_UNROLL 4  // float4 loads in flight per thread per stream in a reduce pass
