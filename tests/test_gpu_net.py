@@ -429,3 +429,52 @@ def test_whole_program_step_equals_group_by_group_step():
         whole[0].replay()
         compare(f"replay {step}")
     assert groups[0].steps() == whole[0].steps() == 4
+
+
+def test_whole_program_sums_more_convolutions_than_one_launch_takes():
+    """Eighteen chained 3x3 convolutions, each with parameters of its own and a chunked weight
+    gradient (2048 output positions): the optimizer group sums their chunks in more than one
+    launch (at most 16 sums per launch, the step counter advanced by the first).  One whole
+    program run and one replay against group-by-group steps: loss, parameters and gradients
+    bit for bit, and the step counter advanced once per step."""
+    r = np.random.default_rng(61)
+    n, c, h, w, depth = 8, 8, 16, 16, 18
+    xv = r.standard_normal((n, c, h, w)).astype(np.float32)
+    ws = [(r.standard_normal((c, c, 3, 3)) * 0.25).astype(np.float32) for _ in range(depth)]
+    bs = [(r.standard_normal(c) * 0.1).astype(np.float32) for _ in range(depth)]
+    targets = r.integers(0, c, n).astype(np.float32)
+    assert ox.conv2d_workspace_size(ox.conv2d_shape(n, c, h, w, c, 3, 1, 1, 1)) > 0
+
+    def build():
+        x, t = tn.input((n, c, h, w)), tn.input((n,))
+        params = [nn.Parameter(v) for pair in zip(ws, bs) for v in pair]
+        y = x
+        for i in range(depth):
+            y = y.conv2d(params[2 * i].tensor(), params[2 * i + 1].tensor(), 1, 1, 1)
+        loss = y.avg_pool2d((h, w), (h, w)).reshape((n, c)).cross_entropy(t)
+        prog = tn.training_program(loss, nn.AdamW(1e-3, 1e-4))
+        prog.feed(x, xv)
+        prog.feed(t, targets)
+        return prog, loss, params
+
+    groups, whole = build(), build()
+
+    def compare(when):
+        torch.cuda.synchronize()
+        (pa, la, qa), (pb, lb, qb) = groups, whole
+        assert_bitexact(pb.value(lb).host(), pa.value(la).host(), f"{when}: loss")
+        for i, (u, v) in enumerate(zip(qa, qb)):
+            assert_bitexact(v.host(), u.host(), f"{when}: parameter {i}")
+            assert_bitexact(pb.gradient(v.tensor()).host(), pa.gradient(u.tensor()).host(),
+                            f"{when}: gradient {i}")
+
+    for op in groups[0].ops:
+        op.launch()
+    whole[0].run()
+    compare("run")
+    whole[0].capture()
+    for op in groups[0].ops:
+        op.launch()
+    whole[0].replay()
+    compare("replay")
+    assert groups[0].steps() == whole[0].steps() == 2
