@@ -9,8 +9,12 @@
 //   p'     = p - lr*((first/c1) / (sqrt(second/c2) + eps) + wd*p)
 // built with -ffp-contract=off and IEEE (correctly rounded) division and square root, so the
 // result is bit-identical to the CPU path.  Traffic: 4 reads + 3 writes of 4 bytes per element,
-// all as 128-bit accesses with the non-temporal hint (every byte is touched once per step;
-// measured on MI355X: 5.93 TB/s with the hint on loads and stores, 5.40 TB/s without).
+// all as 128-bit accesses.  The one-tensor kernel streams them with the non-temporal hint (every
+// byte is touched once per step; measured on MI355X: 5.93 TB/s with the hint on loads and
+// stores, 5.40 TB/s without).  The multi-tensor and table kernels update a model's parameters,
+// which the next step's layers read again: they keep the default cache policy, so the updated
+// parameters (and the moments) stay in the caches (config 5: 846 -> 824 us per step against
+// the non-temporal hint on both, 841 us with it on the loads only).
 #include <hip/hip_runtime.h>
 
 #include <cstring>
@@ -29,12 +33,16 @@ namespace {
 #endif
 constexpr int kUnroll = OXH_ADAMW_UNROLL;
 
+// Stream: the one-tensor kernel's accesses (non-temporal per OXH_ADAMW_NT); else the default
+// cache policy.
+template <bool Stream>
 __device__ __forceinline__ float4 ld(const float4 *p) {
-  if constexpr ((OXH_ADAMW_NT & 1) != 0) return oxh::load_nt(p);
+  if constexpr (Stream && (OXH_ADAMW_NT & 1) != 0) return oxh::load_nt(p);
   else return *p;
 }
+template <bool Stream>
 __device__ __forceinline__ void st(float4 *p, const float4 &v) {
-  if constexpr ((OXH_ADAMW_NT & 2) != 0) oxh::store_nt(p, v);
+  if constexpr (Stream && (OXH_ADAMW_NT & 2) != 0) oxh::store_nt(p, v);
   else *p = v;
 }
 
@@ -68,6 +76,7 @@ struct Streams {
 
 // Elements [begin, end) of one tensor, processed by one block.  Vector accesses when all seven
 // pointers are 16-byte aligned and begin is a multiple of 4.
+template <bool Stream>
 __device__ __forceinline__ void adamw_range(const Hyper &h, const Streams &s, uint64_t begin,
                                             uint64_t end, bool vec) {
   if (vec) {
@@ -84,26 +93,27 @@ __device__ __forceinline__ void adamw_range(const Hyper &h, const Streams &s, ui
       float4 p[kUnroll], g[kUnroll], m[kUnroll], v[kUnroll];
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
-        p[u] = ld(&p4[i + u * oxh::kBlock]);
-        g[u] = ld(&g4[i + u * oxh::kBlock]);
-        m[u] = ld(&m4[i + u * oxh::kBlock]);
-        v[u] = ld(&v4[i + u * oxh::kBlock]);
+        p[u] = ld<Stream>(&p4[i + u * oxh::kBlock]);
+        g[u] = ld<Stream>(&g4[i + u * oxh::kBlock]);
+        m[u] = ld<Stream>(&m4[i + u * oxh::kBlock]);
+        v[u] = ld<Stream>(&v4[i + u * oxh::kBlock]);
       }
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
         float4 po, mo, vo;
         adamw_vec(h, p[u], g[u], m[u], v[u], po, mo, vo);
-        st(&po4[i + u * oxh::kBlock], po);
-        st(&mo4[i + u * oxh::kBlock], mo);
-        st(&vo4[i + u * oxh::kBlock], vo);
+        st<Stream>(&po4[i + u * oxh::kBlock], po);
+        st<Stream>(&mo4[i + u * oxh::kBlock], mo);
+        st<Stream>(&vo4[i + u * oxh::kBlock], vo);
       }
     }
     for (; i < e4; i += oxh::kBlock) {
       float4 po, mo, vo;
-      adamw_vec(h, ld(&p4[i]), ld(&g4[i]), ld(&m4[i]), ld(&v4[i]), po, mo, vo);
-      st(&po4[i], po);
-      st(&mo4[i], mo);
-      st(&vo4[i], vo);
+      adamw_vec(h, ld<Stream>(&p4[i]), ld<Stream>(&g4[i]), ld<Stream>(&m4[i]),
+                ld<Stream>(&v4[i]), po, mo, vo);
+      st<Stream>(&po4[i], po);
+      st<Stream>(&mo4[i], mo);
+      st<Stream>(&vo4[i], vo);
     }
     begin = e4 * 4;
   }
@@ -126,7 +136,7 @@ __global__ __launch_bounds__(oxh::kBlock) void adamw_kernel(Hyper h, Streams s, 
   for (uint64_t c = blockIdx.x; c < chunks; c += gridDim.x) {
     const uint64_t begin = c * kChunk;
     const uint64_t end = begin + kChunk < n ? begin + kChunk : n;
-    adamw_range(h, s, begin, end, vec);
+    adamw_range<true>(h, s, begin, end, vec);
   }
 }
 
@@ -200,7 +210,7 @@ __global__ __launch_bounds__(oxh::kBlock) void adamw_multi_kernel(Hyper h, Tenso
   const uint64_t n = table.n[t];
   const uint64_t end = begin + kChunk < n ? begin + kChunk : n;
   const bool vec = t < 32 ? ((table.vec_mask_lo >> t) & 1u) : ((table.vec_mask_hi >> (t - 32)) & 1u);
-  adamw_range(h, table.s[t], begin, end, vec);
+  adamw_range<false>(h, table.s[t], begin, end, vec);
 }
 
 // Device-table variant: the tensor descriptors and each tensor's first chunk live in device
@@ -258,7 +268,7 @@ __global__ __launch_bounds__(oxh::kBlock) void adamw_table_kernel(
                      reinterpret_cast<uintptr_t>(d.gradient) |
                      reinterpret_cast<uintptr_t>(d.first_moment) |
                      reinterpret_cast<uintptr_t>(d.second_moment)) & 15u) == 0;
-  adamw_range(h,
+  adamw_range<false>(h,
               Streams{d.parameter, d.gradient, d.first_moment, d.second_moment, d.parameter,
                       d.first_moment, d.second_moment},
               begin, end, vec);
