@@ -49,7 +49,7 @@ constexpr int kMinW16 = OXH_CE_MINW16, kMinW32 = OXH_CE_MINW32;
 #define OXH_CE_PIPE_BLOCK 512  // pipelined path: lanes per row block (0: path off)
 #endif
 #ifndef OXH_CE_PIPE_GRID
-#define OXH_CE_PIPE_GRID 256  // pipelined path: blocks (one per CU)
+#define OXH_CE_PIPE_GRID 512  // pipelined path: blocks (two per CU)
 #endif
 
 // The pipelined path serves rows of 4 * kPipeBlock * kPipeV classes (32 768 at 512 lanes).
@@ -255,10 +255,12 @@ __global__ __launch_bounds__(BLOCK, MINW) void ce_row_kernel(CeArgs a) {
 // a block keeps two rows in VGPRs and walks rows blockIdx.x, blockIdx.x + gridDim.x, ...; the
 // next row's loads are issued before the current row's reductions, exp and gradient stores, so
 // a CU's memory pipe stays busy through the compute phases (barriers wait only on LDS, never on
-// outstanding global loads).  One 512-lane block per CU (~240 VGPRs).  Measured at [8192, 32768]
-// fused: 375 us against 378-412 us for two independent row blocks per CU (whose load, compute
-// and store phases fall into step); a forward alone (reads only) is faster with the two
-// independent blocks (160 against 225 us), so it keeps them.  The logits and the gradient move
+// outstanding global loads).  Two 512-lane blocks per CU (227 VGPRs: two waves per SIMD), four
+// rows in flight per CU: 357-358 against 366 us with one block per CU in the same call (384
+// blocks, one or two per CU: 422 us).  Measured at [8192, 32768] fused, one block per CU: 375 us
+// against 378-412 us for two independent row blocks per CU (whose load, compute and store
+// phases fall into step); a forward alone (reads only) is faster with the two independent
+// blocks (160 against 225 us), so it keeps them.  The logits and the gradient move
 // through non-temporal buffer loads and stores on a per-row resource (the lane's offset in a
 // VGPR, the part's offset k * BLOCK * 16 in a scalar): 364 against 373 us with 64-bit lane
 // addresses.  The same launch copying the rows without the softmax takes as long (366 us), so

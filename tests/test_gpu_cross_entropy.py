@@ -124,11 +124,11 @@ def test_cross_entropy_exp_accuracy_within_rows(module, dev):
         assert spread < 5e-7, (row, spread)
 
 
-@pytest.mark.parametrize("rows", [512, 513, 600, 1024 + 37])
+@pytest.mark.parametrize("rows", [1024, 1025, 1200, 2048 + 37])
 @pytest.mark.parametrize("mode", ["fused", "separate"])
 def test_cross_entropy_pipelined_rows(module, dev, rows, mode):
-    """Rows of 32 768 classes from 512 rows up take the two-rows-in-flight path (a block walks
-    rows b, b + 256, ...): every block count parity and ragged tail, with invalid targets in
+    """Rows of 32 768 classes from 1024 rows up take the two-rows-in-flight path (a block walks
+    rows b, b + 512, ...): every block count parity and ragged tail, with invalid targets in
     the middle and at the end (NaN rows, NaN loss, flag) and the valid rows against the
     oracle."""
     k = 32768
