@@ -49,7 +49,7 @@ constexpr int kMinW16 = OXH_CE_MINW16, kMinW32 = OXH_CE_MINW32;
 #define OXH_CE_PIPE_BLOCK 512  // pipelined path: lanes per row block (0: path off)
 #endif
 #ifndef OXH_CE_PIPE_GRID
-#define OXH_CE_PIPE_GRID 512  // pipelined path: blocks (two per CU)
+#define OXH_CE_PIPE_GRID 512  // pipelined path: blocks (two rounds of one block per CU)
 #endif
 
 // The pipelined path serves rows of 4 * kPipeBlock * kPipeV classes (32 768 at 512 lanes).
@@ -255,9 +255,11 @@ __global__ __launch_bounds__(BLOCK, MINW) void ce_row_kernel(CeArgs a) {
 // a block keeps two rows in VGPRs and walks rows blockIdx.x, blockIdx.x + gridDim.x, ...; the
 // next row's loads are issued before the current row's reductions, exp and gradient stores, so
 // a CU's memory pipe stays busy through the compute phases (barriers wait only on LDS, never on
-// outstanding global loads).  Two 512-lane blocks per CU (227 VGPRs: two waves per SIMD), four
-// rows in flight per CU: 357-358 against 366 us with one block per CU in the same call (384
-// blocks, one or two per CU: 422 us).  Measured at [8192, 32768] fused, one block per CU: 375 us
+// outstanding global loads).  At 227 VGPRs (two waves per SIMD) one 512-lane block fills a CU,
+// so the 512-block grid runs as two rounds of 16-row blocks per CU, the second round filling in
+// as CUs finish: 357 us, against 366 us for one 32-row block per CU, 367 us for three rounds
+// (768 blocks), 373-377 us for four or more (1024, 2048) and 422 us for 384 blocks (half the
+// CUs idle in the second round).  Measured at [8192, 32768] fused, one block per CU: 375 us
 // against 378-412 us for two independent row blocks per CU (whose load, compute and store
 // phases fall into step); a forward alone (reads only) is faster with the two independent
 // blocks (160 against 225 us), so it keeps them.  The logits and the gradient move
